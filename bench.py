@@ -1,0 +1,188 @@
+"""Benchmark of ts5's batch-1 token loop on one MI355X (BASELINE.json cfg2).
+
+A Llama-style 8B (32 layers, hidden 4096, FFN 14336, 32/8 heads of 128,
+vocab 128256) with random-init Q4_K weights (Q6_K head) and fp32 norms is
+generated in HBM; a 4096-token prompt of uniform ids is prefilled into the q8
+KV cache; then --steps greedy decode steps run at batch 1, each token the
+argmax of the previous step's logits, one HIP graph replay per token. The
+timed region is exactly those steps, bracketed by device synchronisation.
+
+Beside the decode rate it reports:
+  roofline      the dominant kernel (fused gate/up + SiLU, 45 % of a token's
+                bytes) timed with HIP events on the library's stream over
+                launches that rotate through > 256 MB of weights (so the
+                Infinity Cache cannot serve them), against 8 TB/s.
+  cpu_baseline  the CPU oracle (a restatement of ts5's CPU backend,
+                engine/src/cpu_backend.cpp) decoding a few tokens of the same
+                model shape at ~4k keys on the host cores.
+
+    python bench.py [--steps 256] [--warmup 8] [--gpus 1]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from tokenstation5_amd import synth, ts5hip  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+PROMPT = 4096
+SEED = 20241201
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def model_tensor_specs(hp: dict):
+    """(name, type, ne0, ne1) of every tensor (engine/src/model.cpp:89-119 names)."""
+    E, F, H, HKV, HD, V = (hp[k] for k in ("n_embd", "n_ff", "n_head", "n_head_kv", "head_dim", "n_vocab"))
+    wt = hp["wtype"]
+    yield "token_embd.weight", hp["embd_type"], E, V
+    yield "output_norm.weight", synth.F32, E, 1
+    if hp.get("head_type") is not None:
+        yield "output.weight", hp["head_type"], E, V
+    for i in range(hp["n_layer"]):
+        p = f"blk.{i}."
+        yield p + "attn_norm.weight", synth.F32, E, 1
+        yield p + "ffn_norm.weight", synth.F32, E, 1
+        yield p + "attn_q.weight", wt, E, H * HD
+        yield p + "attn_k.weight", wt, E, HKV * HD
+        yield p + "attn_v.weight", wt, E, HKV * HD
+        yield p + "attn_output.weight", wt, H * HD, E
+        yield p + "ffn_gate.weight", wt, E, F
+        yield p + "ffn_up.weight", wt, E, F
+        yield p + "ffn_down.weight", hp.get("down_type", wt), F, E
+
+
+def decode_bench(ctx, hp, steps: int, warmup: int):
+    n_ctx = PROMPT + max(steps, warmup) + 8
+    m = ts5hip.Model(ctx, hp, n_ctx)
+    t0 = time.time()
+    for name, t, ne0, ne1 in model_tensor_specs(hp):
+        m.synth_tensor(name, t, ne0, ne1, SEED)
+    ctx.sync()
+    log(f"weights generated in HBM ({time.time() - t0:.1f} s)")
+    prompt = np.random.default_rng(SEED).integers(0, hp["n_vocab"], PROMPT).astype(np.int32)
+    t0 = time.time()
+    m.forward(prompt[:-1], 0, logits=False)
+    first = int(m.generate_greedy(int(prompt[-1]), PROMPT - 1, 1)[0])
+    log(f"prefill of {PROMPT} tokens: {time.time() - t0:.1f} s (one token per graph replay)")
+    if warmup:
+        m.generate_greedy(first, PROMPT, warmup)
+    ctx.sync()
+    ctx.timer_begin()
+    ids = m.generate_greedy(first, PROMPT, steps)
+    ms = ctx.timer_end()
+    log(f"{steps} decode steps: {ms:.2f} ms ({steps / ms * 1e3:.1f} tok/s); ids[:8] {list(ids[:8])}")
+    m.close()
+    return ms, ids
+
+
+def glu_roofline(ctx, hp, launches: int = 200):
+    """Fused gate/up + SiLU (k_mv_glu) alone on the library's stream, HIP events
+    around `launches` launches cycling through copies that exceed 256 MB."""
+    E, F = hp["n_embd"], hp["n_ff"]
+    wb = ctx.weight_bytes(synth.Q4_K, E, F)
+    copies = max(2, -(-(320 << 20) // (2 * wb)))
+    gates = [ctx.weight_synth(synth.Q4_K, E, F, 100 + i) for i in range(copies)]
+    ups = [ctx.weight_synth(synth.Q4_K, E, F, 200 + i) for i in range(copies)]
+    x = np.random.default_rng(1).standard_normal(E).astype(np.float32)
+    act = ctx.alloc(ctx.act_bytes(E))
+    ctx.act_quantize(ctx.to_device(x), None, 0.0, E, 1, act)
+    out = ctx.alloc(ctx.act_bytes(F))
+    for i in range(copies):
+        ctx.matvec_glu(synth.Q4_K, gates[i], ups[i], E, F, act, None, out)
+    ctx.sync()
+    ctx.timer_begin()
+    for i in range(launches):
+        ctx.matvec_glu(synth.Q4_K, gates[i % copies], ups[i % copies], E, F, act, None, out)
+    ms = ctx.timer_end()
+    avg_us = ms * 1e3 / launches
+    algo = 2 * E // 256 * F * 144 + ctx.act_bytes(E) + ctx.act_bytes(F)
+    achieved = algo / (avg_us * 1e-6) / 1e9
+    for b in gates + ups:
+        b.free()
+    return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                kernel="k_mv_glu<Q4K,4,8> (ffn gate+up+SiLU, 14336x4096 x2)", avg_us=round(avg_us, 2),
+                algorithmic_bytes=int(algo))
+
+
+def cpu_baseline(hp, steps: int = 3, keys: int = PROMPT):
+    """The CPU oracle decoding `steps` tokens of the same model shape at
+    `keys` cached positions (KV seeded with random q8-rounded values)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle  # test infrastructure: the checker, timed only as the CPU baseline
+
+    threads = min(os.cpu_count() or 1, 16)
+    t0 = time.time()
+    tensors = synth.model_tensors(hp, SEED)
+    log(f"cpu baseline: host weights generated ({time.time() - t0:.1f} s)")
+    m = oracle.Model(hp, tensors, keys + steps + 1, 2, threads=threads)
+    rng = np.random.default_rng(3)
+    for layer in range(hp["n_layer"]):
+        for which in (0, 1):
+            kv = m.kv(which, layer)
+            kv[:keys] = oracle.round_kv(2, rng.standard_normal(kv[:keys].size).astype(np.float32)).reshape(keys, -1)
+    tok = np.array([1], np.int32)
+    m.forward(tok, keys)  # warm
+    t0 = time.time()
+    for i in range(steps):
+        lg = m.forward(tok, keys + 1 + i)
+        tok = np.array([int(np.argmax(lg[0]))], np.int32)
+    dt = time.time() - t0
+    return dict(value=round(steps / dt, 4), unit="tok/s", cores=threads, kind="port",
+                sample=f"{steps} greedy decode steps of the cfg2 8B shape at {keys} seeded q8 keys, "
+                       f"oracle/cpu_forward.cpp (fp64 dots, rows over {threads} threads)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this backend runs ts5's token loop on one GPU (batch 1); "
+              "there is no multi-GPU path to measure.", file=sys.stderr)
+        sys.exit(2)
+    hp = dict(synth.LLAMA_8B)
+    ctx = ts5hip.Context(0)
+    log(f"device {ctx.arch}, {ctx.n_cu} CUs, {ctx.hbm / 2**30:.0f} GiB")
+    ms, ids = decode_bench(ctx, hp, args.steps, args.warmup)
+    roof = glu_roofline(ctx, hp)
+    log(f"roofline: {roof}")
+    ctx.close()
+    cpu = None if args.no_cpu else cpu_baseline(hp)
+    if cpu:
+        log(f"cpu baseline: {cpu}")
+    value = args.steps / (ms / 1e3)
+    wb = synth.weight_bytes(hp)
+    token_bytes = wb["layers"] + wb["head"] + wb["norms"] + wb["embd_row"] + \
+        (hp["n_layer"]) * (PROMPT + args.steps / 2) * hp["n_head_kv"] * hp["head_dim"] * 2 * (1 + 2 / 32)
+    print(json.dumps({
+        "metric": "decode tok/s (8B Q4_K, bs1, 4k ctx, 1 GPU)",
+        "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "q4_k/q6_k weights, int8 x int16 dot, fp32 accum",
+        "data": "synthetic (random-init weights generated in HBM, uniform prompt ids)",
+        "config": {"workload": "cfg2: Llama-style 8B decode, 4096-token prompt, greedy, q8 KV",
+                   "global_batch": 1, "seq_len": PROMPT, "parallelism": "none (1 GPU)",
+                   "decode_hbm_gbs": round(token_bytes * value / 1e9, 1),
+                   "decode_roofline_frac": round(token_bytes * value / 1e9 / HBM_PEAK_GBS, 4)},
+        "roofline": roof, "cpu_baseline": cpu,
+    }), flush=True)
+
+
+if __name__ == "__main__":
+    main()

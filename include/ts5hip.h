@@ -1,0 +1,175 @@
+/* ts5hip.h: the C ABI of ts5's MI355X (gfx950) backend, libts5hip.so.
+ *
+ * This is the thin layer the C++ host engine calls in place of the Vulkan
+ * backend (engine/src/vk_backend.cpp). Plain C types only: opaque handles,
+ * pointers and sizes. Every entry point returns TS5HIP_OK (0) or a negative
+ * TS5HIP_ERR_* code, with the message at ts5hip_last_error(ctx). A context
+ * owns one HIP stream; calls on one context are not thread-safe (the
+ * reference's Backend is not re-entrant either, engine/src/server.h:17-18).
+ * The library owns device memory; callers own host buffers.
+ *
+ * Citations name the reference interface each entry point replaces
+ * (paths under ThatRetiredDude/TokenStation5).
+ */
+#ifndef TS5HIP_H
+#define TS5HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TS5HIP_OK 0
+#define TS5HIP_ERR_ARG (-1)          /* invalid argument or shape */
+#define TS5HIP_ERR_HIP (-2)          /* HIP runtime error */
+#define TS5HIP_ERR_UNSUPPORTED (-3)  /* type / shape this backend has no kernel for */
+#define TS5HIP_ERR_CONTEXT_FULL (-4) /* "context full" (engine/src/vk_backend.cpp:271) */
+#define TS5HIP_ERR_STATE (-5)        /* missing tensor, model not complete */
+
+/* GGML type ids (engine/src/gguf.h:12-16) with kernels here. */
+enum { TS5HIP_F32 = 0, TS5HIP_F16 = 1, TS5HIP_Q8_0 = 8, TS5HIP_Q4_K = 12, TS5HIP_Q6_K = 14 };
+/* KvType (engine/src/backend.h:13). Only Q8 is implemented on the GPU. */
+enum { TS5HIP_KV_F32 = 0, TS5HIP_KV_F16 = 1, TS5HIP_KV_Q8 = 2 };
+
+typedef struct ts5hip_ctx ts5hip_ctx;
+typedef struct ts5hip_model ts5hip_model;
+typedef struct ts5hip_sampler ts5hip_sampler;
+
+/* ---- device and context (replaces VkContext, engine/src/vk_context.h:14-36) ---- */
+
+/* The last error on ctx, or of the calling thread when ctx is null. */
+const char *ts5hip_last_error(const ts5hip_ctx *ctx);
+/* Opens HIP device `device` and a stream on it. Fails unless it is gfx950. */
+int ts5hip_init(int device, ts5hip_ctx **out);
+void ts5hip_destroy(ts5hip_ctx *ctx);
+/* Compute units, the gfx architecture name, and HBM bytes of the device. */
+int ts5hip_device_info(ts5hip_ctx *ctx, int *n_cu, char *arch, int arch_len, int64_t *hbm_bytes);
+
+/* ---- device memory and timing (test and benchmark plumbing) ---- */
+int ts5hip_alloc(ts5hip_ctx *ctx, size_t bytes, void **dptr);
+int ts5hip_free(ts5hip_ctx *ctx, void *dptr);
+int ts5hip_upload(ts5hip_ctx *ctx, void *dst, const void *src, size_t bytes);   /* host -> device, synchronous */
+int ts5hip_download(ts5hip_ctx *ctx, void *dst, const void *src, size_t bytes); /* device -> host, synchronous */
+int ts5hip_memset(ts5hip_ctx *ctx, void *dst, int value, size_t bytes);
+int ts5hip_sync(ts5hip_ctx *ctx);
+/* HIP events on the context's stream around the work enqueued between them. */
+int ts5hip_timer_begin(ts5hip_ctx *ctx);
+int ts5hip_timer_end(ts5hip_ctx *ctx, float *ms);
+
+/* ---- weights (replaces VkBackend::upload_weights, engine/src/vk_backend.cpp:531-600) ---- */
+
+/* Whether a matrix of this GGML type has GPU kernels (vk_supports_type, engine/src/backend.h:89). */
+int ts5hip_supports_type(uint32_t type);
+/* Bytes of a (ne1 rows x ne0 values) tensor in its HBM layout; -1 if unsupported. */
+int64_t ts5hip_weight_bytes(uint32_t type, int64_t ne0, int64_t ne1);
+/* GGUF bytes on the host (engine/src/model.h:44-53 Weight::data) -> HBM layout at dst. */
+int ts5hip_weight_upload(ts5hip_ctx *ctx, uint32_t type, int64_t ne0, int64_t ne1, const void *gguf, void *dst);
+/* Seeded random-init weights written straight into HBM layout (benchmark inputs). */
+int ts5hip_weight_synth(ts5hip_ctx *ctx, uint32_t type, int64_t ne0, int64_t ne1, uint64_t seed, int centered,
+                        void *dst);
+
+/* ---- per-op entry points: device pointers, asynchronous on the context's stream ---- */
+
+/* dequantize_row (engine/src/quants.h:11) of `rows` rows in HBM layout -> fp32, bit-exact. */
+int ts5hip_dequantize(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0, int64_t rows, float *y);
+/* Bytes of one token's quantized activation of n values (the matvec input form). */
+int64_t ts5hip_act_bytes(int64_t n);
+/* x [ntok][n] fp32 -> ntok activations; with norm_w, rmsnorm first (engine/src/cpu_backend.cpp:48-53). */
+int ts5hip_act_quantize(ts5hip_ctx *ctx, const float *x, const float *norm_w, float eps, int64_t n, int ntok,
+                        void *act);
+/* rmsnorm (engine/src/cpu_backend.cpp:48-53): y = x / rms(x) * w per token. */
+int ts5hip_rmsnorm(ts5hip_ctx *ctx, const float *x, const float *w, float eps, int64_t n, int ntok, float *y);
+/* One-token matvec y (+)= W act (engine/src/cpu_backend.cpp:18-37 at n = 1; mv16_q4_k /
+ * mv16_q6_k / matmul_q8_0 in engine/src/vk_backend.cpp:863-880). W: ne1 rows of ne0. */
+int ts5hip_matvec(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0, int64_t ne1, const void *act, float *y,
+                  int accumulate);
+/* Fused gate/up + SiLU (mv16_glu_q4_k, engine/src/vk_backend.cpp:1009-1021; CPU
+ * engine/src/cpu_backend.cpp:253-261): out = silu(Wg act) * (Wu act), as fp32 y (may be
+ * null) and as the activation act_out of the down projection. ne1 % 32 == 0. */
+int ts5hip_matvec_glu(ts5hip_ctx *ctx, uint32_t type, const void *w_gate, const void *w_up, int64_t ne0,
+                      int64_t ne1, const void *act, float *y, void *act_out);
+/* RoPE angles as engine/src/cpu_backend.cpp:59-61 computes them, for positions
+ * [0, n_pos): dst gets [n_pos][n_rot/2] (cos, sin) float pairs. freqs: n_rot/2 divisors or null. */
+int ts5hip_rope_table(ts5hip_ctx *ctx, int n_rot, int n_pos, float base, float scale, const float *freqs_host,
+                      float *dst);
+/* The q/k/v rows of ntok tokens at positions *pos0_dev.. (qkv: [ntok][(H + 2 HKV) HD]):
+ * bias, optional per-head norm, RoPE, then K and V rounded to q8 and stored at their slots
+ * (qkv_post_q8, engine/src/vk_backend.cpp:1145-1164; round_kv, engine/src/cpu_backend.cpp:78-90).
+ * Cache: k8/v8 int8 [n_head_kv][n_ctx][head_dim], ks/vs f16 [n_head_kv][n_ctx][head_dim/32].
+ * q_out: [ntok][H HD] fp32. bias ([(H + 2 HKV) HD]), q_norm, k_norm ([HD]) may be null. */
+int ts5hip_rope_kv_append(ts5hip_ctx *ctx, const float *qkv, int ntok, const int32_t *pos0_dev, int n_head,
+                          int n_head_kv, int head_dim, int n_rot, int neox, const float *rope_cs, int n_ctx,
+                          const float *bias, const float *q_norm, const float *k_norm, float eps, float *q_out,
+                          void *k8, void *ks, void *v8, void *vs);
+/* Split-K flash decode over the q8 cache (attn_q8 + attn_merge, engine/src/vk_backend.cpp:937-995;
+ * CPU engine/src/cpu_backend.cpp:222-248). q: [B][H HD]. kv_per_batch = 1: query b reads
+ * sequence b's cache (B caches of n_ctx slots back to back) over n_keys_dev[b] keys;
+ * kv_per_batch = 0: one cache, query b reads n_keys_dev[0] + b + 1 keys (n_keys_dev[0] =
+ * the batch's first position). out [B][H HD] fp32 and/or act_out (B activations) may be null.
+ * n_split <= 0 picks a split count that fills the GPU. */
+int ts5hip_attn_decode(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n_head_kv, int head_dim,
+                       const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx,
+                       const int32_t *n_keys_dev, int kv_per_batch, float scale, int n_split, float *out,
+                       void *act_out);
+/* Greedy token per row: the first maximum of each row of n logits (engine/src/engine.cpp:17). */
+int ts5hip_argmax(ts5hip_ctx *ctx, const float *x, int n, int rows, int32_t *out_dev);
+/* The k (<= 64) largest of n logits, descending, ties by ascending id (the candidate set
+ * of engine/src/engine.cpp:19-33). */
+int ts5hip_topk(ts5hip_ctx *ctx, const float *x, int n, int k, float *vals_dev, int32_t *ids_dev);
+
+/* ---- the sampler: Engine::sample (engine/src/engine.cpp:16-46) on host, std::mt19937_64 ---- */
+ts5hip_sampler *ts5hip_sampler_new(uint64_t seed);
+void ts5hip_sampler_free(ts5hip_sampler *s);
+/* Draw from candidates sorted by descending logit: weights exp((l - l0) / T) in double, the
+ * shortest prefix reaching top_p, std::discrete_distribution. */
+int32_t ts5hip_sampler_draw(ts5hip_sampler *s, const int32_t *ids, const float *logits, int k, float temperature,
+                            float top_p);
+
+/* ---- model: Backend (engine/src/backend.h:16-44) over HIP ---- */
+
+/* HParams (engine/src/model.h:14-42), the fields the token loop reads. */
+typedef struct {
+    int32_t n_vocab, n_embd, n_layer, n_ff, n_head, n_head_kv, head_dim, rope_dims, rope_neox;
+    float rms_eps, rope_base, attn_scale, rope_scale;
+} ts5hip_hparams;
+
+/* make_vk_backend (engine/src/backend.h:82) for HIP: a model of these hyperparameters with a
+ * KV cache of n_ctx positions. Tensors are then set by GGUF name (engine/src/model.cpp:89-119). */
+int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, int kv_type, ts5hip_model **out);
+void ts5hip_model_destroy(ts5hip_model *m);
+/* A tensor from its GGUF bytes on the host. */
+int ts5hip_model_set_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, int64_t ne1,
+                            const void *gguf);
+/* A tensor generated in HBM (ts5hip_weight_synth). */
+int ts5hip_model_synth_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, int64_t ne1,
+                              uint64_t seed, int centered);
+/* Backend::forward (engine/src/backend.h:21-24): tokens at positions pos0..pos0+n-1; logits of
+ * the last token, or of all n when all_logits, into logits ([n or 1][n_vocab]); logits null:
+ * fill the KV cache only. */
+int ts5hip_forward(ts5hip_model *m, const int32_t *tokens, int n, int pos0, float *logits, int all_logits);
+/* Backend::forward_in_place / logits_view (engine/src/backend.h:25-33): logits stay in pinned
+ * host memory at ts5hip_logits_view (room for 256 rows). */
+int ts5hip_forward_in_place(ts5hip_model *m, const int32_t *tokens, int n, int pos0, int all_logits);
+const float *ts5hip_logits_view(const ts5hip_model *m);
+/* Backend::n_ctx / kv_type (engine/src/backend.h:34-39). */
+int ts5hip_n_ctx(const ts5hip_model *m);
+int ts5hip_kv_type(const ts5hip_model *m);
+/* Top-k of the last forward's logits row `row` on the GPU and the host draw (Engine::sample). */
+int32_t ts5hip_model_sample(ts5hip_model *m, ts5hip_sampler *s, int row, float temperature, float top_p,
+                            int top_k);
+/* Greedy decode kept on the device (run_bench's generation loop, engine/src/checks.cpp:195-199,
+ * with argmax feedback): `token` at `pos`, then n_steps tokens, each the argmax of the previous
+ * step's logits; ids_out gets those n_steps ids. One HIP graph replay per token. */
+int ts5hip_generate_greedy(ts5hip_model *m, int32_t token, int pos, int n_steps, int32_t *ids_out);
+/* K (which 0) or V (1) of `layer` at positions [pos0, pos0+n), dequantized to fp32
+ * [n][n_head_kv * head_dim] (the CPU cache's layout, engine/src/cpu_backend.cpp:95-97). */
+int ts5hip_kv_read(ts5hip_model *m, int layer, int which, int pos0, int n, float *out);
+/* Backend::take_profile (engine/src/backend.h:40-43): text since the last call. */
+int ts5hip_take_profile(ts5hip_model *m, char *buf, int len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TS5HIP_H */

@@ -1,0 +1,141 @@
+"""The HIP backend's token forward against ts5's own CPU backend (golden
+logits and greedy ids made by tests/golden/make_golden.py from
+engine/src/cpu_backend.cpp and engine/src/engine.cpp), through the C ABI.
+
+Bars: the reference's own GPU-vs-CPU checks for a q8 cache (engine/src/
+checks.cpp:145-159: max|diff| / max|ref| <= 2e-2; engine/tests/compare.py:51-55:
+cosine > 0.999 per row), and 100 % greedy agreement over 64 tokens."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import make_golden
+import oracle
+from tokenstation5_amd import synth, ts5hip
+
+pytestmark = pytest.mark.gpu
+G = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+MODELS = json.load(open(os.path.join(G, "models.json")))
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = ts5hip.Context(0)
+    yield c
+    c.close()
+
+
+def load(ctx, name, n_ctx):
+    hp = dict(MODELS[name]["hparams"])
+    tensors = synth.model_tensors(hp, make_golden.MODEL_SEED)
+    m = ts5hip.Model(ctx, hp, n_ctx)
+    m.set_tensors(tensors)
+    return hp, tensors, m
+
+
+def check_rows(got, want, tol=2e-2):
+    for r in range(want.shape[0]):
+        d = np.abs(got[r].astype(np.float64) - want[r]).max() / np.abs(want[r]).max()
+        cos = float(np.dot(got[r], want[r]) / (np.linalg.norm(got[r]) * np.linalg.norm(want[r])))
+        assert d <= tol and cos > 0.999, (r, d, cos)
+
+
+@pytest.mark.parametrize("name", ["tiny_llama", "tiny_draft", "tiny_llama_c", "tiny_draft_c"])
+def test_check_schedule_logits(ctx, name):
+    """ts5 check's order (engine/src/checks.cpp:119-124): n-4 tokens in one
+    call with every position's logits, then 4 single-token calls."""
+    hp, _, m = load(ctx, name, 64)
+    g = np.load(os.path.join(G, f"model_{name}.npz"))
+    toks, want = g["kv2_tokens"], g["kv2_logits"]
+    n = toks.size
+    batch = n - 4
+    got = np.empty_like(want)
+    got[:batch] = m.forward(toks[:batch], 0, all_logits=True)
+    for i in range(batch, n):
+        got[i] = m.forward(toks[i:i + 1], i)[0]
+    check_rows(got, want)
+    top = np.mean(np.argmax(got, 1) == np.argmax(want, 1))
+    print(f"{name}: top-1 agreement {top:.3f}")
+
+
+@pytest.mark.parametrize("name", ["tiny_llama_c", "tiny_draft_c"])
+def test_greedy_64_tokens_match_reference(ctx, name):
+    """100 % argmax agreement over the first 64 generated tokens, with the
+    device-resident greedy loop (argmax feeding the next step)."""
+    hp, _, m = load(ctx, name, 128)
+    g = np.load(os.path.join(G, f"model_{name}.npz"))
+    prompt = g["greedy_prompt"]
+    want = list(g["greedy_q8_ids"])
+    m.forward(prompt[:-1], 0, logits=False)
+    got = list(m.generate_greedy(int(prompt[-1]), prompt.size - 1, 64))
+    div = next((i for i in range(64) if got[i] != want[i]), None)
+    assert div is None, f"first divergence at token {div}: {got[div]} vs {want[div]}"
+
+
+def test_greedy_host_loop_equals_device_loop(ctx):
+    hp, _, m = load(ctx, "tiny_llama_c", 128)
+    prompt = np.array([(17 + 31 * i) % hp["n_vocab"] for i in range(8)], np.int32)
+    lg = m.forward(prompt, 0)[0]
+    host = []
+    for i in range(24):
+        host.append(int(np.argmax(lg)))
+        lg = m.forward(np.array([host[-1]], np.int32), prompt.size + i)[0]
+    dev = m.generate_greedy(int(prompt[-1]), prompt.size - 1, 25)
+    assert list(dev[:24]) == host
+
+
+def test_kv_cache_matches_oracle(ctx):
+    """K/V rows in the cache equal the oracle's q8-rounded values, except where
+    an fp32 difference upstream crosses a rounding boundary (one q step)."""
+    hp, tensors, m = load(ctx, "tiny_llama_c", 64)
+    ref = oracle.Model(hp, tensors, 64, 2)
+    toks = np.array([(5 + 11 * i) % hp["n_vocab"] for i in range(20)], np.int32)
+    m.forward(toks, 0, logits=False)
+    ref.forward(toks, 0, logits=False)
+    for layer in range(hp["n_layer"]):
+        for which in (0, 1):
+            got = m.kv(layer, which, 0, 20)
+            want = ref.kv(which, layer)[:20]
+            same = np.mean(got == want)
+            step = np.abs(want).reshape(20, -1, 32).max(2, keepdims=True) / 127
+            assert same > 0.98, (layer, which, same)
+            assert np.all(np.abs(got - want).reshape(20, -1, 32) <= step * 1.01 + 1e-30)
+
+
+def test_forward_in_place_and_sampling(ctx):
+    hp, _, m = load(ctx, "tiny_llama_c", 64)
+    toks = np.array([3, 1, 4, 1, 5, 9, 2, 6], np.int32)
+    view = m.forward_in_place(toks, 0, all_logits=True).copy()
+    assert view.shape == (8, hp["n_vocab"])
+    direct = m.forward(toks, 0, all_logits=True)
+    assert np.array_equal(view, direct)
+    s1, s2 = ts5hip.Sampler(7), oracle.Sampler(7)
+    for r in range(8):
+        got = m.sample(s1, r, 0.7, 0.9, 40)
+        want = s2.sample(direct[r], 0.7, 0.9, 40)
+        assert got == want, r
+        assert m.sample(s1, r, 0.0, 0.9, 40) == int(np.argmax(direct[r]))
+
+
+def test_context_full_and_bad_tokens(ctx):
+    hp, _, m = load(ctx, "tiny_llama", 16)
+    with pytest.raises(ts5hip.Ts5HipError) as e:
+        m.forward(np.zeros(17, np.int32), 0)
+    assert e.value.code == ts5hip.ERR_CONTEXT_FULL
+    with pytest.raises(ts5hip.Ts5HipError) as e:
+        m.forward(np.array([hp["n_vocab"]], np.int32), 0)
+    assert e.value.code == ts5hip.ERR_ARG
+    m.forward(np.array([1, 2], np.int32), 14)  # the last two slots are fine
+
+
+def test_missing_tensor_is_reported(ctx):
+    hp = dict(MODELS["tiny_llama"]["hparams"])
+    m = ts5hip.Model(ctx, hp, 16)
+    tensors = synth.model_tensors(hp, make_golden.MODEL_SEED)
+    del tensors["blk.1.ffn_up.weight"]
+    m.set_tensors(tensors)
+    with pytest.raises(ts5hip.Ts5HipError) as e:
+        m.forward(np.array([1], np.int32), 0)
+    assert e.value.code == ts5hip.ERR_STATE and "blk.1.ffn_up" in str(e.value)

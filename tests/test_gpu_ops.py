@@ -1,0 +1,352 @@
+"""Per-op parity of the HIP kernels with the CPU oracle (a restatement of
+ts5's engine/src/cpu_backend.cpp and quants.cpp, pinned to the reference's own
+outputs by tests/test_oracle.py), through the C ABI.
+
+Bars: unpack and q8 KV rounding bit-exact; matvec and attention relative L2
+error <= 1e-3 against the oracle's fp64-accumulated results."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from tokenstation5_amd import synth, ts5hip
+
+pytestmark = pytest.mark.gpu
+G = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+REL_L2 = 1e-3
+
+
+def rel_l2(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = ts5hip.Context(0)
+    assert c.arch.startswith("gfx950"), c.arch
+    yield c
+    c.close()
+
+
+# ---- unpack -------------------------------------------------------------------------
+
+@pytest.mark.parametrize("t", [synth.Q4_K, synth.Q6_K, synth.Q8_0])
+def test_dequantize_bit_exact_golden(ctx, t):
+    """HBM-layout unpack == the reference's dequantize_row (golden blocks,
+    including zero, subnormal, negative and large f16 scales)."""
+    q = np.load(os.path.join(G, "quants.npz"))
+    blocks, want = q[f"t{t}_blocks"], q[f"t{t}_values"]
+    bv = synth.BLOCK[t][0]
+    rows = blocks.shape[0] if bv == 32 else blocks.shape[0]
+    ne0 = bv
+    w = ctx.weight(t, ne0, rows, blocks.reshape(rows, -1))
+    y = ctx.alloc(want.nbytes)
+    ctx.dequantize(t, w, ne0, rows, y)
+    got = y.download(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_f16_unpack_every_half(ctx):
+    h = np.arange(65536, dtype=np.uint16)
+    w = ctx.to_device(h)
+    y = ctx.alloc(65536 * 4)
+    ctx.dequantize(synth.F16, w, 65536, 1, y)
+    got = y.download(np.float32).view(np.uint32)
+    want = np.array([oracle.lib().ts5o_fp16_to_fp32(int(v)) for v in h], np.float32).view(np.uint32)
+    finite = np.isfinite(h.view(np.float16))
+    assert np.array_equal(got[finite], want[finite])
+    assert np.all(np.isnan(got[~finite].view(np.float32)) == np.isnan(want[~finite].view(np.float32)))
+
+
+@pytest.mark.parametrize("t,ne0,rows", [(synth.Q4_K, 4096, 64), (synth.Q6_K, 4096, 32), (synth.Q8_0, 896, 50),
+                                        (synth.Q4_K, 14336, 3)])
+def test_dequantize_bit_exact_random(ctx, t, ne0, rows):
+    W = synth.tensor(t, ne0, rows, 11, f"deq{t}")
+    w = ctx.weight(t, ne0, rows, W)
+    y = ctx.alloc(ne0 * rows * 4)
+    ctx.dequantize(t, w, ne0, rows, y)
+    got = y.download(np.float32).reshape(rows, ne0)
+    want = np.stack([oracle.dequantize(t, W[r], ne0) for r in range(rows)])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+# ---- activations ----------------------------------------------------------------------
+
+def act_unpack(buf, n, ntok=1):
+    """(x16 values, scale, sum, isum) of ntok activations from the device."""
+    ab = ts5hip.Context.act_bytes(n)
+    raw = buf.download(np.uint8)[:ab * ntok].reshape(ntok, ab)
+    al = lambda v: -(-v // 256) * 256  # noqa: E731
+    hi = raw[:, :n].view(np.int8).astype(np.int32)
+    lo = raw[:, al(n):al(n) + n].view(np.int8).astype(np.int32)
+    o = 2 * al(n)
+    sc = raw[:, o:o + n // 32 * 4].copy().view(np.float32)
+    o += al(n // 32 * 4)
+    sm = raw[:, o:o + n // 32 * 4].copy().view(np.float32)
+    o += al(n // 32 * 4)
+    isum = raw[:, o:o + n // 16 * 4].copy().view(np.int32)
+    return 256 * hi + lo, sc, sm, isum
+
+
+@pytest.mark.parametrize("n,norm", [(4096, True), (14336, False), (896, True)])
+def test_act_quantize(ctx, n, norm):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * rng.choice([1e-3, 1.0, 1e4], n)).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+    dx, dw = ctx.to_device(x), ctx.to_device(w)
+    act = ctx.alloc(ctx.act_bytes(n))
+    ctx.act_quantize(dx, dw if norm else None, 1e-5, n, 1, act)
+    x16, sc, sm, isum = act_unpack(act, n)
+    ref = oracle.rmsnorm(x, w, 1e-5) if norm else x
+    rb = ref.reshape(-1, 32)
+    assert np.abs(x16).max() <= 16383
+    # Per sub-block the scale is max|x| / 16383 and every value within half a step.
+    assert np.allclose(sc[0], np.abs(rb).max(1) / 16383, rtol=1e-5)
+    err = np.abs(x16[0].reshape(-1, 32) * sc[0][:, None] - rb)
+    assert np.all(err <= 0.5 * sc[0][:, None] * (1 + 1e-4) + 1e-30)
+    assert np.allclose(sm[0], rb.astype(np.float64).sum(1), rtol=1e-4, atol=1e-6 * np.abs(rb).max())
+    assert np.array_equal(isum[0], x16[0].reshape(-1, 16).sum(1))
+
+
+def test_rmsnorm(ctx):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((3, 4096)) * 1e6).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(4096)).astype(np.float32)
+    y = ctx.alloc(x.nbytes)
+    ctx.rmsnorm(ctx.to_device(x), ctx.to_device(w), 1e-5, 4096, 3, y)
+    got = y.download(np.float32, (3, 4096))
+    want = np.stack([oracle.rmsnorm(x[t], w, 1e-5) for t in range(3)])
+    assert rel_l2(got, want) < 1e-6
+
+
+# ---- matvec -----------------------------------------------------------------------------
+
+def run_matvec(ctx, t, W, ne0, rows, x, accumulate=None):
+    w = ctx.weight(t, ne0, rows, W)
+    act = ctx.alloc(ctx.act_bytes(ne0))
+    ctx.act_quantize(ctx.to_device(x), None, 0.0, ne0, 1, act)
+    y = ctx.to_device(accumulate if accumulate is not None else np.zeros(rows, np.float32))
+    ctx.matvec(t, w, ne0, rows, act, y, accumulate is not None)
+    return y.download(np.float32)
+
+
+@pytest.mark.parametrize("t,ne0,rows", [
+    (synth.Q4_K, 4096, 4096),     # cfg1
+    (synth.Q4_K, 4096, 1024),     # wk/wv
+    (synth.Q4_K, 14336, 4096),    # ffn_down
+    (synth.Q4_K, 4864, 896),      # the draft's ffn_down (19 blocks per row)
+    (synth.Q4_K, 256, 37),        # one block, ragged rows
+    (synth.Q6_K, 4096, 4096),
+    (synth.Q6_K, 512, 1000),
+    (synth.Q8_0, 896, 896),       # the draft's 896-wide matrices
+    (synth.Q8_0, 896, 4864),
+    (synth.Q8_0, 32, 5),
+])
+def test_matvec_vs_oracle(ctx, t, ne0, rows):
+    W = synth.tensor(t, ne0, rows, 1, f"mv{t}_{ne0}_{rows}")
+    x = np.random.default_rng(ne0 + rows).standard_normal(ne0).astype(np.float32)
+    got = run_matvec(ctx, t, W, ne0, rows, x)
+    want = oracle.matmul(t, W, ne0, x)[0]
+    assert rel_l2(got, want) <= REL_L2, rel_l2(got, want)
+
+
+def test_matvec_centered_weights(ctx):
+    """Zero-mean Q4_K weights (outputs not dominated by the weight mean)."""
+    W = synth.tensor(synth.Q4_K, 4096, 512, 2, "centered", centered=True)
+    x = np.random.default_rng(9).standard_normal(4096).astype(np.float32)
+    got = run_matvec(ctx, synth.Q4_K, W, 4096, 512, x)
+    want = oracle.matmul(synth.Q4_K, W, 4096, x)[0]
+    assert rel_l2(got, want) <= REL_L2
+
+
+def test_matvec_accumulate_and_scales(ctx):
+    W = synth.tensor(synth.Q4_K, 1024, 256, 3, "acc")
+    rng = np.random.default_rng(4)
+    for scale in (1e-6, 1.0, 1e7):
+        x = (rng.standard_normal(1024) * scale).astype(np.float32)
+        y0 = rng.standard_normal(256).astype(np.float32) * 1e3
+        got = run_matvec(ctx, synth.Q4_K, W, 1024, 256, x, accumulate=y0.copy())
+        want = oracle.matmul(synth.Q4_K, W, 1024, x)[0]
+        assert rel_l2(got - y0, want) <= REL_L2, scale
+
+
+def test_matvec_zero_input(ctx):
+    W = synth.tensor(synth.Q6_K, 256, 64, 5, "zero")
+    got = run_matvec(ctx, synth.Q6_K, W, 256, 64, np.zeros(256, np.float32))
+    assert np.array_equal(got, np.zeros(64, np.float32))
+
+
+@pytest.mark.parametrize("t,ne0,rows", [(synth.Q4_K, 4096, 14336), (synth.Q8_0, 896, 4864), (synth.Q4_K, 512, 64)])
+def test_glu_vs_oracle(ctx, t, ne0, rows):
+    Wg = synth.tensor(t, ne0, rows, 6, "gate")
+    Wu = synth.tensor(t, ne0, rows, 6, "up")
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(ne0).astype(np.float32)
+    wg, wu = ctx.weight(t, ne0, rows, Wg), ctx.weight(t, ne0, rows, Wu)
+    act = ctx.alloc(ctx.act_bytes(ne0))
+    ctx.act_quantize(ctx.to_device(x), None, 0.0, ne0, 1, act)
+    y = ctx.alloc(rows * 4)
+    act_out = ctx.alloc(ctx.act_bytes(rows))
+    ctx.matvec_glu(t, wg, wu, ne0, rows, act, y, act_out)
+    got = y.download(np.float32)
+    g = oracle.matmul(t, Wg, ne0, x)[0]
+    u = oracle.matmul(t, Wu, ne0, x)[0]
+    want = oracle.swiglu(g, u)
+    assert rel_l2(got, want) <= REL_L2
+    # act_out is the activation of `got`.
+    x16, sc, _, _ = act_unpack(act_out, rows)
+    assert rel_l2(x16[0].reshape(-1, 32) * sc[0][:, None], got.reshape(-1, 32)) < 1e-4
+
+
+# ---- RoPE + q8 KV append, attention ---------------------------------------------------------
+
+@pytest.mark.parametrize("H,HKV,HD,neox,ntok,pos0", [(32, 8, 128, False, 1, 4095), (14, 2, 64, True, 3, 17),
+                                                     (4, 1, 128, False, 5, 0)])
+def test_rope_kv_append(ctx, H, HKV, HD, neox, ntok, pos0):
+    """q rotated and K/V rounded to q8 exactly as the CPU path does it."""
+    n_ctx = pos0 + ntok + 3
+    rng = np.random.default_rng(H + pos0)
+    R = (H + 2 * HKV) * HD
+    qkv = (rng.standard_normal((ntok, R)) * rng.choice([1.0, 300.0], (ntok, R))).astype(np.float32)
+    bias = (rng.standard_normal(R) * 0.1).astype(np.float32) if neox else None
+    rope = ctx.rope_table(HD, n_ctx, 1e6 if neox else 500000.0)
+    pos = ctx.to_device(np.array([pos0], np.int32))
+    q_out = ctx.alloc(ntok * H * HD * 4)
+    k8, v8 = ctx.alloc(HKV * n_ctx * HD).zero(), ctx.alloc(HKV * n_ctx * HD).zero()
+    ks, vs = ctx.alloc(HKV * n_ctx * HD // 16).zero(), ctx.alloc(HKV * n_ctx * HD // 16).zero()
+    ctx.rope_kv_append(ctx.to_device(qkv), ntok, pos, H, HKV, HD, HD, neox, rope, n_ctx, q_out, k8, ks, v8, vs,
+                       bias=None if bias is None else ctx.to_device(bias))
+    q = q_out.download(np.float32, (ntok, H, HD))
+    K8 = k8.download(np.int8, (HKV, n_ctx, HD)).astype(np.float32)
+    V8 = v8.download(np.int8, (HKV, n_ctx, HD)).astype(np.float32)
+    KS = ks.download(np.float16, (HKV, n_ctx, HD // 32)).astype(np.float32)
+    VS = vs.download(np.float16, (HKV, n_ctx, HD // 32)).astype(np.float32)
+    base = 1e6 if neox else 500000.0
+    for t in range(ntok):
+        v = qkv[t] + (bias if bias is not None else 0)
+        p = pos0 + t
+        for h in range(H):
+            want = oracle.rope(v[h * HD:(h + 1) * HD], HD, p, base, neox)
+            assert np.array_equal(q[t, h].view(np.uint32), want.view(np.uint32)), (t, h)
+        for h in range(HKV):
+            kw = oracle.round_kv(2, oracle.rope(v[(H + h) * HD:(H + h + 1) * HD], HD, p, base, neox))
+            vw = oracle.round_kv(2, v[(H + HKV + h) * HD:(H + HKV + h + 1) * HD])
+            kg = (K8[h, p].reshape(-1, 32) * KS[h, p][:, None]).ravel()
+            vg = (V8[h, p].reshape(-1, 32) * VS[h, p][:, None]).ravel()
+            assert np.array_equal(kg, kw), (t, h)
+            assert np.array_equal(vg, vw), (t, h)
+
+
+def q8_cache(rng, B, HKV, n_ctx, HD):
+    """K/V ~ N(0,1) rounded by the q8 rule: (int8, f16 scale) and fp32 values."""
+    vals = rng.standard_normal((B, HKV, n_ctx, HD)).astype(np.float32)
+    blocks = vals.reshape(-1, 32)
+    amax = np.abs(blocks).max(1)
+    sc = (amax / np.float32(127)).astype(np.float16)
+    scf = sc.astype(np.float32)
+    q = np.clip(np.rint(blocks / scf[:, None]), -127, 127).astype(np.int8)
+    deq = (q.astype(np.float32) * scf[:, None]).reshape(vals.shape)
+    return q.reshape(vals.shape), sc.reshape(B, HKV, n_ctx, HD // 32), deq
+
+
+@pytest.mark.parametrize("B,ctxlen,H,HKV,HD", [(1, 8192, 32, 8, 128), (4, 8192, 32, 8, 128), (1, 1000, 32, 8, 128),
+                                               (2, 33, 14, 2, 64), (3, 1, 32, 8, 128), (4, 32768, 32, 8, 128)])
+def test_attention_vs_oracle(ctx, B, ctxlen, H, HKV, HD):
+    """cfg3: one query per sequence over its q8 cache, full context, scale 1/sqrt(HD)."""
+    rng = np.random.default_rng(B * 7 + ctxlen)
+    q8, sc, deq = q8_cache(rng, B, HKV, ctxlen, HD)
+    v8, vsc, vdeq = q8_cache(rng, B, HKV, ctxlen, HD)
+    q = rng.standard_normal((B, H * HD)).astype(np.float32)
+    scale = float(np.float32(1) / np.sqrt(np.float32(HD)))
+    out = ctx.alloc(q.nbytes)
+    act = ctx.alloc(ctx.act_bytes(H * HD) * B)
+    nk = ctx.to_device(np.full(B, ctxlen, np.int32))
+    ctx.attn_decode(ctx.to_device(q), B, H, HKV, HD, ctx.to_device(q8), ctx.to_device(sc), ctx.to_device(v8),
+                    ctx.to_device(vsc), ctxlen, nk, 1, scale, 0, out, act)
+    got = out.download(np.float32, (B, H * HD))
+    for b in range(B):
+        kc = deq[b].transpose(1, 0, 2).reshape(ctxlen, HKV * HD)
+        vc = vdeq[b].transpose(1, 0, 2).reshape(ctxlen, HKV * HD)
+        want = oracle.attention(q[b], kc, vc, H, HKV, HD, ctxlen - 1, scale)
+        assert rel_l2(got[b], want) <= REL_L2, (b, rel_l2(got[b], want))
+    x16, s, _, _ = act_unpack(act, H * HD, B)
+    assert rel_l2(x16.reshape(B, -1, 32) * s[:, :, None], got.reshape(B, -1, 32)) < 1e-4
+
+
+def test_attention_splits_agree(ctx):
+    """Any split count gives the same softmax (merge of partials)."""
+    rng = np.random.default_rng(5)
+    B, H, HKV, HD, n = 1, 32, 8, 128, 3000
+    q8, sc, _ = q8_cache(rng, B, HKV, n, HD)
+    v8, vsc, _ = q8_cache(rng, B, HKV, n, HD)
+    q = ctx.to_device(rng.standard_normal((B, H * HD)).astype(np.float32))
+    dq8, dsc, dv8, dvs = ctx.to_device(q8), ctx.to_device(sc), ctx.to_device(v8), ctx.to_device(vsc)
+    nk = ctx.to_device(np.array([n], np.int32))
+    outs = []
+    for split in (1, 7, 47, 64):
+        out = ctx.alloc(H * HD * 4)
+        ctx.attn_decode(q, B, H, HKV, HD, dq8, dsc, dv8, dvs, n, nk, 1, 0.0883883, split, out, None)
+        outs.append(out.download(np.float32))
+    for o in outs[1:]:
+        assert rel_l2(o, outs[0]) < 1e-5
+
+
+def test_attention_causal_batch(ctx):
+    """kv_per_batch = 0: query b at position p0 + b sees keys 0..p0+b."""
+    rng = np.random.default_rng(6)
+    H, HKV, HD, n_ctx, p0, B = 8, 2, 64, 200, 150, 4
+    q8, sc, deq = q8_cache(rng, 1, HKV, n_ctx, HD)
+    v8, vsc, vdeq = q8_cache(rng, 1, HKV, n_ctx, HD)
+    q = rng.standard_normal((B, H * HD)).astype(np.float32)
+    out = ctx.alloc(q.nbytes)
+    ctx.attn_decode(ctx.to_device(q), B, H, HKV, HD, ctx.to_device(q8), ctx.to_device(sc), ctx.to_device(v8),
+                    ctx.to_device(vsc), n_ctx, ctx.to_device(np.array([p0], np.int32)), 0, 0.125, 0, out, None)
+    got = out.download(np.float32, (B, H * HD))
+    kc = deq[0].transpose(1, 0, 2).reshape(n_ctx, HKV * HD)
+    vc = vdeq[0].transpose(1, 0, 2).reshape(n_ctx, HKV * HD)
+    for b in range(B):
+        want = oracle.attention(q[b], kc, vc, H, HKV, HD, p0 + b, 0.125)
+        assert rel_l2(got[b], want) <= REL_L2
+
+
+# ---- sampling reductions ------------------------------------------------------------------------
+
+def test_argmax_first_maximum(ctx):
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((3, 128256)).astype(np.float32)
+    x[1, 777] = x[1, 99999] = 50.0   # a tie: the lower id wins (std::max_element)
+    x[2, :] = 1.0                    # all equal: id 0
+    out = ctx.alloc(12)
+    ctx.argmax(ctx.to_device(x), 128256, 3, out)
+    got = out.download(np.int32)
+    assert list(got) == [int(np.argmax(x[0])), 777, 0]
+
+
+@pytest.mark.parametrize("n,k", [(128256, 40), (151936, 64), (1000, 5), (128256, 1)])
+def test_topk(ctx, n, k):
+    rng = np.random.default_rng(n + k)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    x[10] = x[20] = x.max() + 1  # tie at the top: ascending id
+    vals, ids = ctx.alloc(k * 4), ctx.alloc(k * 4)
+    ctx.topk(ctx.to_device(x), n, k, vals, ids)
+    want = np.argsort(-x, kind="stable")[:k]
+    assert list(ids.download(np.int32)) == list(want)
+    assert np.array_equal(vals.download(np.float32), x[want])
+
+
+def test_sampling_cfg4_matches_reference_draws(ctx):
+    """cfg4's sampling step: GPU top-40 then the host draw (T 0.7, p 0.9) gives
+    the reference engine's ids on the golden logit table."""
+    import make_golden
+    s = np.load(os.path.join(G, "sampler.npz"))
+    table = make_golden.sampler_table(int(s["table_seed"]), int(s["rows"]), int(s["n_vocab"]))
+    T, p, k = make_golden.SAMPLER_CASES[0]
+    smp = ts5hip.Sampler(42)
+    vals, ids = ctx.alloc(k * 4), ctx.alloc(k * 4)
+    got = []
+    for r in range(table.shape[0]):
+        ctx.topk(ctx.to_device(table[r]), table.shape[1], k, vals, ids)
+        got.append(smp.draw(ids.download(np.int32), vals.download(np.float32), T, p))
+    assert got == list(s["ids0"])

@@ -1,0 +1,65 @@
+// RMSNorm (engine/src/cpu_backend.cpp:48-53) and the quantized-activation
+// form every matvec reads (see Act in common.h).
+#include "common.h"
+#include "kernels.h"
+
+namespace ts5hip {
+
+// Block-wide sum over a 256-thread block (4 waves).
+__device__ inline float block_sum256(float v, float *red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    v = red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
+    return v;
+}
+
+// 1 / sqrt(mean(x^2) + eps) of one token's n values (the reference keeps
+// the sum in double; fp32 over <= 16384 values is within 1e-6 relative).
+__device__ inline float rms_scale(const float *x, int n, float eps, float *red) {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ss += x[i] * x[i];
+    ss = block_sum256(ss, red);
+    return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+// y = x * s * w per token (blockIdx.x); 256 threads.
+__global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, float eps,
+                                                 int n, float *__restrict__ y) {
+    __shared__ float red[4];
+    const float *xt = x + (int64_t)blockIdx.x * n;
+    float *yt = y + (int64_t)blockIdx.x * n;
+    const float s = rms_scale(xt, n, eps, red);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) yt[i] = xt[i] * s * w[i];
+}
+
+// Act of x (optionally rms-normalised by w first) per token (blockIdx.x).
+__global__ __launch_bounds__(256) void k_act_quant(const float *__restrict__ x, int64_t xstride,
+                                                   const float *__restrict__ w, float eps, int n,
+                                                   uint8_t *__restrict__ act, int64_t act_stride) {
+    __shared__ float red[4];
+    const float *xt = x + (int64_t)blockIdx.x * xstride;
+    const Act a = act_view(act + (int64_t)blockIdx.x * act_stride, n);
+    const float s = w ? rms_scale(xt, n, eps, red) : 1.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = xt[i];
+        if (w) v = v * s * w[i];
+        quant32(v, threadIdx.x & 31, a, i / 32);
+    }
+}
+
+hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int ntok, float *y, hipStream_t s) {
+    hipLaunchKernelGGL(k_rmsnorm, dim3(ntok), dim3(256), 0, s, x, w, eps, n, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_act_quant(const float *x, int64_t xstride, const float *w, float eps, int n, int ntok, void *act,
+                            hipStream_t s) {
+    hipLaunchKernelGGL(k_act_quant, dim3(ntok), dim3(256), 0, s, x, xstride, w, eps, n, (uint8_t *)act,
+                       (int64_t)act_bytes(n));
+    return hipGetLastError();
+}
+
+}  // namespace ts5hip

@@ -1,0 +1,182 @@
+// Shared definitions of the HIP library: GGML block formats as they sit in
+// HBM, the quantized-activation format every matvec reads, and small device
+// helpers. Everything here is gfx950 (CDNA4, wave64) code.
+#pragma once
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#else
+#include <hip/hip_runtime_api.h>  // host-only translation units (g++)
+#endif
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ts5hip {
+
+// GGML type ids (engine/src/gguf.h:12-16).
+enum : uint32_t { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+// KvType (engine/src/backend.h:13).
+enum : int { KV_F32 = 0, KV_F16 = 1, KV_Q8 = 2 };
+
+constexpr int WAVE = 64;
+
+__host__ __device__ constexpr inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// ---------------------------------------------------------------------------
+// Weight layouts in HBM (per tensor of ne1 rows of ne0 values, row-major).
+//
+//  Q4_K  unchanged GGUF bytes, 144 B per 256 values: d, dmin (f16), 12 bytes
+//        of packed 6-bit scales/mins, 128 bytes of nibbles. 144 = 9 x 16, so
+//        every block starts on a 16-byte boundary and loads as dwordx4.
+//  Q6_K  GGUF blocks are 210 B (2-byte aligned). Split at upload into a body
+//        array of 208 B per block (ql[128] qh[64] scales[16], 13 x 16 B) and
+//        an f16 d array behind it, so bodies load as dwordx4.
+//  Q8_0  GGUF blocks are 34 B. Split into 32 B of int8 quants per block and
+//        an f16 d array behind them.
+//  F32 / F16 unchanged.
+// ---------------------------------------------------------------------------
+constexpr int Q4K_BYTES = 144;
+constexpr int Q6K_BODY = 208;
+constexpr int Q8_BODY = 32;
+
+__host__ __device__ inline int block_values(uint32_t t) {
+    return t == T_Q4_K || t == T_Q6_K ? 256 : t == T_Q8_0 ? 32 : (t == T_F32 || t == T_F16) ? 1 : 0;
+}
+// Bytes of one GGUF block (engine/src/gguf.cpp:34-48).
+__host__ __device__ inline int gguf_block_bytes(uint32_t t) {
+    return t == T_Q4_K ? 144 : t == T_Q6_K ? 210 : t == T_Q8_0 ? 34 : t == T_F32 ? 4 : t == T_F16 ? 2 : 0;
+}
+// Offset of the f16 scale array of a split layout of nblocks blocks.
+__host__ __device__ inline size_t split_scale_offset(uint32_t t, int64_t nblocks) {
+    return align_up((size_t)nblocks * (t == T_Q6_K ? Q6K_BODY : Q8_BODY), 256);
+}
+// Bytes of a tensor in its HBM layout; 0 if unsupported.
+__host__ __device__ inline size_t device_bytes(uint32_t t, int64_t ne0, int64_t ne1) {
+    const int bv = block_values(t);
+    if (bv == 0 || ne0 % bv) return 0;
+    const int64_t nb = ne0 / bv * ne1;
+    if (t == T_Q6_K || t == T_Q8_0) return split_scale_offset(t, nb) + align_up((size_t)nb * 2, 256);
+    return (size_t)nb * gguf_block_bytes(t);
+}
+
+// ---------------------------------------------------------------------------
+// Quantized activations ("act"): the form in which every matvec reads its
+// input vector x of n values (n a multiple of 32). Per 32-value sub-block s:
+//   scale[s] = max|x| / 16383, x16 = rint(x / scale[s]) in [-16383, 16383],
+//   x16 = 256 * hi + lo with lo in [-128, 127] and hi in [-64, 64],
+//   sum[s]  = sum of x over the sub-block (fp32, the unquantized values),
+// and per 16-value run r: isum[r] = sum of x16 over the run (exact).
+// The two int8 planes feed v_dot4_i32_i8 directly against int8/uint4
+// weights: sum(q * x16) = 256 * dot4(q, hi) + dot4(q, lo), exact in int32.
+// The relative rounding error per value is at most 1/32766 of the
+// sub-block's largest magnitude.
+// ---------------------------------------------------------------------------
+struct Act {
+    int8_t *hi, *lo;
+    float *scale, *sum;
+    int32_t *isum;
+};
+struct CAct {
+    const int8_t *hi, *lo;
+    const float *scale, *sum;
+    const int32_t *isum;
+};
+
+__host__ __device__ inline size_t act_bytes(int64_t n) {
+    return 2 * align_up((size_t)n, 256) + 2 * align_up((size_t)n / 32 * 4, 256) + align_up((size_t)n / 16 * 4, 256);
+}
+__host__ __device__ inline Act act_view(void *base, int64_t n) {
+    uint8_t *p = (uint8_t *)base;
+    Act a;
+    a.hi = (int8_t *)p;
+    p += align_up((size_t)n, 256);
+    a.lo = (int8_t *)p;
+    p += align_up((size_t)n, 256);
+    a.scale = (float *)p;
+    p += align_up((size_t)n / 32 * 4, 256);
+    a.sum = (float *)p;
+    p += align_up((size_t)n / 32 * 4, 256);
+    a.isum = (int32_t *)p;
+    return a;
+}
+__host__ __device__ inline CAct cact_view(const void *base, int64_t n) {
+    Act a = act_view(const_cast<void *>(base), n);
+    return CAct{a.hi, a.lo, a.scale, a.sum, a.isum};
+}
+
+#if defined(__HIPCC__)
+// ---------------------------------------------------------------------------
+// Device helpers.
+// ---------------------------------------------------------------------------
+// f16 bits to fp32: v_cvt_f32_f16 is exact for every half, subnormals
+// included (f16 denormals are not flushed on gfx9).
+__device__ inline float h2f(uint32_t bits16) {
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
+    return (float)h;
+}
+// fp32 to f16 bits, round to nearest even (v_cvt_f16_f32).
+__device__ inline uint16_t f2h(float f) {
+    _Float16 h = (_Float16)f;
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ inline int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+template <typename T>
+__device__ inline T wave_sum(T v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+
+// Quantizes 32 values held one per lane of a 32-lane segment (lane32 =
+// 0..31, all 32 lanes active) into sub-block `group` of an Act.
+__device__ inline void quant32(float v, int lane32, const Act &a, int64_t group) {
+    float amax = fabsf(v), s = v;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+        s += __shfl_xor(s, o, 32);
+    }
+    int x16 = 0;
+    if (amax > 0.f) x16 = max(-16383, min(16383, (int)rintf(v * (16383.0f / amax))));
+    const int lo = (int)(int8_t)(x16 & 255);
+    const int hi = (x16 - lo) >> 8;
+    a.hi[group * 32 + lane32] = (int8_t)hi;
+    a.lo[group * 32 + lane32] = (int8_t)lo;
+    int is = x16;
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) is += __shfl_xor(is, o, 16);
+    if (lane32 == 0) {
+        a.scale[group] = amax / 16383.0f;
+        a.sum[group] = s;
+        a.isum[2 * group] = is;
+    } else if (lane32 == 16) {
+        a.isum[2 * group + 1] = is;
+    }
+}
+
+// The 6-bit scale and min of sub-block j (0..7) of a K-quant block, from its
+// 12 packed bytes held as three little-endian dwords a (bytes 0-3),
+// b (4-7), c (8-11): sub-blocks 0-3 keep theirs in the low 6 bits of bytes j
+// and j+4; 4-7 take their low 4 bits from byte j+4's low/high nibble and
+// their top 2 bits from the top of bytes j-4 and j
+// (engine/src/quants.cpp:64-72).
+__device__ inline void kq_scale_min(int j, uint32_t a, uint32_t b, uint32_t c, int &sc, int &m) {
+    if (j < 4) {
+        sc = (a >> (8 * j)) & 63;
+        m = (b >> (8 * j)) & 63;
+    } else {
+        const int s = 8 * (j - 4);
+        sc = ((c >> s) & 15) | (((a >> (s + 6)) & 3) << 4);
+        m = ((c >> (s + 4)) & 15) | (((b >> (s + 6)) & 3) << 4);
+    }
+}
+
+#endif  // __HIPCC__
+
+}  // namespace ts5hip

@@ -1,0 +1,61 @@
+// Host-side launchers of the library's kernels (internal to libts5hip.so).
+#pragma once
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+namespace ts5hip {
+
+// One layer's q8 KV cache (layout in attention.hip).
+struct KvLayer {
+    int8_t *k;
+    uint16_t *ks;
+    int8_t *v;
+    uint16_t *vs;
+};
+
+// quant.hip
+hipError_t launch_dequant(uint32_t t, const void *w, int64_t ne0, int64_t rows, float *y, hipStream_t s);
+// x[t] = row ids[*pos + t] of the embedding (pos null: ids[t]).
+hipError_t launch_embed(uint32_t t, const void *w, int64_t ne0, int64_t n_rows, const int32_t *ids, const int32_t *pos,
+                        int ntok, float *x, hipStream_t s);
+// Split layouts (Q6_K, Q8_0): nblocks GGUF blocks in HBM -> bodies and f16 scales.
+hipError_t launch_repack(uint32_t t, int64_t nblocks, const void *gguf, void *body, void *scales, hipStream_t s);
+// nrows random-init rows of ne0 values (scales: the split layout's f16 array, else unused).
+hipError_t launch_synth(uint32_t t, int64_t ne0, int64_t nrows, uint64_t seed, int centered, void *body, void *scales,
+                        hipStream_t s);
+
+// act.hip
+hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int ntok, float *y, hipStream_t s);
+hipError_t launch_act_quant(const float *x, int64_t xstride, const float *w, float eps, int n, int ntok, void *act,
+                            hipStream_t s);
+
+// matvec.hip
+hipError_t launch_matvec(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const void *act, float *y, int add,
+                         hipStream_t s);
+hipError_t launch_matvec_glu(uint32_t t, const void *wg, const void *wu, int64_t ne0, int64_t ne1, const void *act,
+                             float *y, void *act_out, hipStream_t s);
+
+// attention.hip
+hipError_t launch_rope_kv(const float *qkv, int64_t qkv_stride, const float *bias, const float *q_norm,
+                          const float *k_norm, float eps, const float *rope_cs, int n_rot, int neox,
+                          const int32_t *pos0, int H, int HKV, int HD, int n_ctx, int ntok, float *q_out, KvLayer kv,
+                          hipStream_t s);
+bool attn_supported(int H, int HKV, int HD);
+hipError_t launch_attn_decode(const float *q, KvLayer kv, int kv_per_batch, const int32_t *n_keys, int B, int H,
+                              int HKV, int HD, int n_ctx, int n_split, float scale, float *part, float *out, void *act,
+                              hipStream_t s);
+
+hipError_t launch_kv_read(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, float *out, hipStream_t s);
+
+// sample.hip
+size_t argmax_scratch_bytes(int rows);
+// out[r] = argmax of row r; with seq (one row): seq[*pos + 1] = id, ++*pos.
+hipError_t launch_argmax(const float *x, int n, int rows, void *scratch, int32_t *out, int32_t *seq, int32_t *pos,
+                         hipStream_t s);
+hipError_t launch_advance(int32_t *pos, hipStream_t s);
+size_t topk_scratch_bytes();
+int topk_max();
+int topk_max_n();
+hipError_t launch_topk(const float *x, int n, int k, void *scratch, float *vals, int32_t *ids, hipStream_t s);
+
+}  // namespace ts5hip

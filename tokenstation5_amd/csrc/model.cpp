@@ -1,0 +1,617 @@
+// The model behind the C ABI: tensors by GGUF name, the q8 KV cache, and the
+// token forward of ts5's Backend (engine/src/backend.h:16-44) as a sequence
+// of HIP kernels captured once into HIP graphs and replayed per token (the
+// counterpart of VkBackend::record / record-ahead,
+// engine/src/vk_backend.cpp:1049-1199).
+//
+// One token at position p (state[0] = p, its id at seq[p]):
+//   embed -> per layer: act(rmsnorm x) -> QKV matvec -> RoPE + q8 KV append
+//   -> split-K flash decode + merge (act) -> O matvec (x +=) -> act(rmsnorm x)
+//   -> gate/up + SiLU (act) -> down matvec (x +=)
+//   -> act(rmsnorm x) -> head matvec -> logits [-> argmax -> seq[p+1]], p++.
+// The token id and position live in device memory, so one graph serves every
+// step, and greedy decoding never returns to the host between tokens.
+#include <algorithm>
+#include <chrono>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "common_host.h"
+#include "kernels.h"
+#include "runtime.h"
+
+using namespace ts5hip;
+
+namespace {
+
+struct DevT {
+    uint32_t type = 0;
+    int64_t ne0 = 0, ne1 = 0;
+    void *d = nullptr;
+    bool set = false;
+};
+
+struct LayerDev {
+    DevT attn_norm, ffn_norm, q_norm, k_norm;
+    DevT qkv;                    // [q; k; v] rows of one type
+    DevT part[3];                // a q/k/v matrix whose type differs from qkv's
+    bool in_qkv[3] = {false, false, false};
+    DevT wo, gate, up, down;
+};
+
+enum Graph { G_KV = 0, G_LOGITS = 1, G_GREEDY = 2, N_GRAPHS = 3 };
+
+}  // namespace
+
+struct ts5hip_model {
+    ts5hip_ctx *ctx = nullptr;
+    ts5hip_hparams hp{};
+    int n_ctx = 0, kv_type = KV_Q8, n_split = 1;
+    DevT tok_embd, out_norm, output;
+    std::vector<float> freqs;
+    std::vector<LayerDev> layers;
+    float *bias = nullptr;  // [n_layer][(H + 2 HKV) HD], zero where absent
+    std::vector<bool> has_bias;
+    // KV cache (all layers) and RoPE table.
+    int8_t *k8 = nullptr, *v8 = nullptr;
+    uint16_t *ks = nullptr, *vs = nullptr;
+    float *rope_cs = nullptr;
+    bool rope_ready = false;
+    // Activations and scratch.
+    float *x = nullptr, *qkv = nullptr, *q_rot = nullptr, *logits = nullptr, *part = nullptr;
+    uint8_t *act_e = nullptr, *act_att = nullptr, *act_f = nullptr;
+    void *amax = nullptr, *topk = nullptr;
+    float *topk_v = nullptr;
+    int32_t *topk_i = nullptr;
+    int32_t *seq = nullptr;    // [n_ctx + 1] token id at each position
+    int32_t *state = nullptr;  // [0] position, [1] last argmax
+    // Logits rows of the last forward: on the device, and in pinned host memory.
+    float *dev_rows = nullptr, *host_rows = nullptr;
+    int rows_cap = 0, rows_valid = 0;
+    int32_t *pinned_ids = nullptr;  // [n_ctx + 1]
+    hipGraphExec_t graph[N_GRAPHS] = {nullptr, nullptr, nullptr};
+    bool graphs_stale = true;
+    // Profile (TS5HIP_PROFILE set): GPU time per forward call.
+    bool profile = false;
+    double prof_ms = 0;
+    int prof_calls = 0, prof_tokens = 0;
+    std::vector<void *> allocs;
+
+    int qkv_rows() const { return (hp.n_head + 2 * hp.n_head_kv) * hp.head_dim; }
+    int64_t kv_head_elems() const { return (int64_t)n_ctx * hp.head_dim; }
+    KvLayer kv_layer(int l) const {
+        const int64_t per = (int64_t)hp.n_head_kv * n_ctx * hp.head_dim;
+        const int64_t per_s = per / 32;
+        return KvLayer{k8 + l * per, ks + l * per_s, v8 + l * per, vs + l * per_s};
+    }
+};
+
+namespace {
+
+int alloc(ts5hip_model *m, size_t bytes, void **p) {
+    TS5_HIP(m->ctx, hipMalloc(p, bytes ? bytes : 1));
+    m->allocs.push_back(*p);
+    return TS5HIP_OK;
+}
+
+template <typename T>
+int alloc_t(ts5hip_model *m, size_t count, T **p) {
+    void *v = nullptr;
+    if (int rc = alloc(m, count * sizeof(T), &v)) return rc;
+    *p = (T *)v;
+    return TS5HIP_OK;
+}
+
+// A vector tensor (norm weight, bias, rope freqs) as floats on the host.
+int host_floats(ts5hip_ctx *ctx, uint32_t type, int64_t n, const void *src, std::vector<float> &out) {
+    out.resize((size_t)n);
+    if (type == T_F32) {
+        std::memcpy(out.data(), src, (size_t)n * 4);
+    } else if (type == T_F16) {
+        const uint16_t *h = (const uint16_t *)src;
+        for (int64_t i = 0; i < n; i++) {
+            const uint32_t s = (uint32_t)(h[i] >> 15) << 31;
+            uint32_t e = (h[i] >> 10) & 31u, f = h[i] & 0x3ffu, bits;
+            if (e == 31) bits = s | 0x7f800000u | (f << 13);
+            else if (e) bits = s | ((e + 112u) << 23) | (f << 13);
+            else if (!f) bits = s;
+            else {
+                int sh = 0;
+                while (!(f & 0x400u)) f <<= 1, sh++;
+                bits = s | ((uint32_t)(113 - sh) << 23) | ((f & 0x3ffu) << 13);
+            }
+            std::memcpy(&out[i], &bits, 4);
+        }
+    } else {
+        return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "vector tensor of type %u", type);
+    }
+    return TS5HIP_OK;
+}
+
+// Allocates t (once) for a matrix of this shape and type.
+int matrix_slot(ts5hip_model *m, DevT &t, uint32_t type, int64_t ne0, int64_t ne1) {
+    if (ts5hip_weight_bytes(type, ne0, ne1) < 0 || !ts5hip_supports_type(type))
+        return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "matrix of type %u, %lld x %lld", type, (long long)ne1,
+                    (long long)ne0);
+    if (t.d && (t.type != type || t.ne0 != ne0 || t.ne1 != ne1)) return fail(m->ctx, TS5HIP_ERR_ARG, "tensor reshaped");
+    if (!t.d) {
+        if (int rc = alloc(m, device_bytes(type, ne0, ne1), &t.d)) return rc;
+        t.type = type, t.ne0 = ne0, t.ne1 = ne1;
+    }
+    return TS5HIP_OK;
+}
+
+// Source of a tensor's bytes: GGUF on the host, or a synthesis seed.
+struct Source {
+    const void *gguf;
+    uint64_t seed;
+    int centered;
+};
+
+int fill_rows(ts5hip_model *m, const DevT &t, int64_t row0, int64_t nrows, const Source &src) {
+    if (src.gguf) return upload_weight(m->ctx, t.type, t.ne0, nrows, src.gguf, t.d, row0, t.ne1);
+    const SplitDst d = split_dst(t.type, t.ne0, t.ne1, t.d, row0);
+    TS5_HIP(m->ctx, launch_synth(t.type, t.ne0, nrows, src.seed, src.centered, d.body, d.scales, m->ctx->stream));
+    return TS5HIP_OK;
+}
+
+int set_matrix(ts5hip_model *m, DevT &t, uint32_t type, int64_t ne0, int64_t ne1, int64_t want0, int64_t want1,
+               const Source &src, const char *name) {
+    if (ne0 != want0 || ne1 != want1)
+        return fail(m->ctx, TS5HIP_ERR_ARG, "%s is %lld x %lld, expected %lld x %lld", name, (long long)ne0,
+                    (long long)ne1, (long long)want0, (long long)want1);
+    if (int rc = matrix_slot(m, t, type, ne0, ne1)) return rc;
+    if (int rc = fill_rows(m, t, 0, ne1, src)) return rc;
+    t.set = true;
+    return TS5HIP_OK;
+}
+
+// Synthesised vectors: N(1, 0.02) generated on the device.
+int set_vector(ts5hip_model *m, DevT &t, uint32_t type, int64_t n, int64_t want, const Source &src,
+               const char *name) {
+    if (n != want) return fail(m->ctx, TS5HIP_ERR_ARG, "%s has %lld values, expected %lld", name, (long long)n,
+                               (long long)want);
+    if (!t.d) {
+        if (int rc = alloc(m, (size_t)n * 4, &t.d)) return rc;
+        t.type = T_F32, t.ne0 = n, t.ne1 = 1;
+    }
+    if (src.gguf) {
+        std::vector<float> f;
+        if (int rc = host_floats(m->ctx, type, n, src.gguf, f)) return rc;
+        if (int rc = ts5hip_upload(m->ctx, t.d, f.data(), (size_t)n * 4)) return rc;
+    } else {
+        TS5_HIP(m->ctx, launch_synth(T_F32, n, 1, src.seed, 0, t.d, nullptr, m->ctx->stream));
+    }
+    t.set = true;
+    return TS5HIP_OK;
+}
+
+int set_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, int64_t ne1, const Source &src) {
+    const ts5hip_hparams &hp = m->hp;
+    const int64_t E = hp.n_embd, F = hp.n_ff, HD = hp.head_dim, H = hp.n_head, HKV = hp.n_head_kv;
+    m->graphs_stale = true;
+    const std::string n(name);
+    if (n == "token_embd.weight") {
+        if (type != T_F32 && type != T_F16 && !ts5hip_supports_type(type))
+            return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "token_embd of type %u", type);
+        if (ne0 != E || ne1 != hp.n_vocab) return fail(m->ctx, TS5HIP_ERR_ARG, "token_embd shape");
+        if (!m->tok_embd.d) {
+            const size_t bytes = (type == T_F32 || type == T_F16) ? (size_t)ne0 * ne1 * (type == T_F32 ? 4 : 2)
+                                                                  : device_bytes(type, ne0, ne1);
+            if (int rc = alloc(m, bytes, &m->tok_embd.d)) return rc;
+            m->tok_embd.type = type, m->tok_embd.ne0 = ne0, m->tok_embd.ne1 = ne1;
+        }
+        if (type == T_F32 || type == T_F16) {
+            if (!src.gguf) return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "synthetic float embeddings");
+            if (int rc = ts5hip_upload(m->ctx, m->tok_embd.d, src.gguf, (size_t)ne0 * ne1 * (type == T_F32 ? 4 : 2)))
+                return rc;
+        } else if (int rc = fill_rows(m, m->tok_embd, 0, ne1, src)) {
+            return rc;
+        }
+        m->tok_embd.set = true;
+        return TS5HIP_OK;
+    }
+    if (n == "output_norm.weight") return set_vector(m, m->out_norm, type, ne0 * ne1, E, src, name);
+    if (n == "output.weight") return set_matrix(m, m->output, type, ne0, ne1, E, hp.n_vocab, src, name);
+    if (n == "rope_freqs.weight") {
+        if (!src.gguf) return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "synthetic rope_freqs");
+        if (ne0 * ne1 != hp.rope_dims / 2) return fail(m->ctx, TS5HIP_ERR_ARG, "rope_freqs has %lld values", (long long)(ne0 * ne1));
+        m->rope_ready = false;
+        return host_floats(m->ctx, type, ne0 * ne1, src.gguf, m->freqs);
+    }
+    int l = -1, used = 0;
+    char rest[96] = {0};
+    if (std::sscanf(name, "blk.%d.%95s%n", &l, rest, &used) != 2 || l < 0 || l >= hp.n_layer)
+        return fail(m->ctx, TS5HIP_ERR_ARG, "unknown tensor %s", name);
+    LayerDev &L = m->layers[l];
+    const std::string r(rest);
+    if (r == "attn_norm.weight") return set_vector(m, L.attn_norm, type, ne0 * ne1, E, src, name);
+    if (r == "ffn_norm.weight") return set_vector(m, L.ffn_norm, type, ne0 * ne1, E, src, name);
+    if (r == "attn_q_norm.weight") return set_vector(m, L.q_norm, type, ne0 * ne1, HD, src, name);
+    if (r == "attn_k_norm.weight") return set_vector(m, L.k_norm, type, ne0 * ne1, HD, src, name);
+    if (r == "attn_output.weight") return set_matrix(m, L.wo, type, ne0, ne1, H * HD, E, src, name);
+    if (r == "ffn_gate.weight") return set_matrix(m, L.gate, type, ne0, ne1, E, F, src, name);
+    if (r == "ffn_up.weight") return set_matrix(m, L.up, type, ne0, ne1, E, F, src, name);
+    if (r == "ffn_down.weight") return set_matrix(m, L.down, type, ne0, ne1, F, E, src, name);
+    const char *parts[3] = {"attn_q", "attn_k", "attn_v"};
+    const int64_t rows[3] = {H * HD, HKV * HD, HKV * HD}, row0[3] = {0, H * HD, (H + HKV) * HD};
+    for (int p = 0; p < 3; p++) {
+        if (r == std::string(parts[p]) + ".weight") {
+            if (ne0 != E || ne1 != rows[p]) return fail(m->ctx, TS5HIP_ERR_ARG, "%s shape", name);
+            if (!L.qkv.d || L.qkv.type == type) {
+                if (int rc = matrix_slot(m, L.qkv, type, E, m->qkv_rows())) return rc;
+                if (int rc = fill_rows(m, L.qkv, row0[p], rows[p], src)) return rc;
+                L.in_qkv[p] = true;
+                L.part[p].set = false;
+            } else {
+                if (int rc = set_matrix(m, L.part[p], type, ne0, ne1, E, rows[p], src, name)) return rc;
+                L.in_qkv[p] = false;
+            }
+            return TS5HIP_OK;
+        }
+        if (r == std::string(parts[p]) + ".bias") {
+            if (!src.gguf) return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "synthetic bias");
+            if (ne0 * ne1 != rows[p]) return fail(m->ctx, TS5HIP_ERR_ARG, "%s shape", name);
+            std::vector<float> f;
+            if (int rc = host_floats(m->ctx, type, rows[p], src.gguf, f)) return rc;
+            m->has_bias[l] = true;
+            return ts5hip_upload(m->ctx, m->bias + (int64_t)l * m->qkv_rows() + row0[p], f.data(), f.size() * 4);
+        }
+    }
+    return fail(m->ctx, TS5HIP_ERR_ARG, "unknown tensor %s", name);
+}
+
+int check_complete(ts5hip_model *m) {
+    auto need = [&](const DevT &t, const char *what, int l) {
+        if (t.set) return TS5HIP_OK;
+        return l < 0 ? fail(m->ctx, TS5HIP_ERR_STATE, "tensor %s not set", what)
+                     : fail(m->ctx, TS5HIP_ERR_STATE, "tensor blk.%d.%s not set", l, what);
+    };
+    if (int rc = need(m->tok_embd, "token_embd.weight", -1)) return rc;
+    if (int rc = need(m->out_norm, "output_norm.weight", -1)) return rc;
+    if (!m->output.set && !ts5hip_supports_type(m->tok_embd.type))
+        return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "tied output head of type %u", m->tok_embd.type);
+    for (int l = 0; l < m->hp.n_layer; l++) {
+        const LayerDev &L = m->layers[l];
+        if (int rc = need(L.attn_norm, "attn_norm.weight", l)) return rc;
+        if (int rc = need(L.ffn_norm, "ffn_norm.weight", l)) return rc;
+        const char *parts[3] = {"attn_q.weight", "attn_k.weight", "attn_v.weight"};
+        for (int p = 0; p < 3; p++)
+            if (!L.in_qkv[p])
+                if (int rc = need(L.part[p], parts[p], l)) return rc;
+        if (int rc = need(L.wo, "attn_output.weight", l)) return rc;
+        if (int rc = need(L.gate, "ffn_gate.weight", l)) return rc;
+        if (int rc = need(L.up, "ffn_up.weight", l)) return rc;
+        if (int rc = need(L.down, "ffn_down.weight", l)) return rc;
+        if (L.gate.type != L.up.type) return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "gate and up of different types");
+    }
+    if (!m->rope_ready) {
+        std::vector<float> t;
+        rope_table_host(m->hp.rope_dims, m->n_ctx, m->hp.rope_base, m->hp.rope_scale,
+                        m->freqs.empty() ? nullptr : m->freqs.data(), t);
+        if (int rc = ts5hip_upload(m->ctx, m->rope_cs, t.data(), t.size() * 4)) return rc;
+        m->rope_ready = true;
+    }
+    return TS5HIP_OK;
+}
+
+// The kernels of one token at position state[0] (see the file comment).
+// tail: 0 = advance the position, 1 = argmax into seq[p+1] and advance.
+int enqueue_token(ts5hip_model *m, bool head, int tail) {
+    ts5hip_ctx *ctx = m->ctx;
+    const hipStream_t s = ctx->stream;
+    const ts5hip_hparams &hp = m->hp;
+    const int E = hp.n_embd, H = hp.n_head, HKV = hp.n_head_kv, HD = hp.head_dim, F = hp.n_ff;
+    const int QR = m->qkv_rows();
+    TS5_HIP(ctx, launch_embed(m->tok_embd.type, m->tok_embd.d, E, hp.n_vocab, m->seq, m->state, 1, m->x, s));
+    for (int l = 0; l < hp.n_layer; l++) {
+        const LayerDev &L = m->layers[l];
+        TS5_HIP(ctx, launch_act_quant(m->x, E, (const float *)L.attn_norm.d, hp.rms_eps, E, 1, m->act_e, s));
+        if (L.in_qkv[0] && L.in_qkv[1] && L.in_qkv[2]) {
+            TS5_HIP(ctx, launch_matvec(L.qkv.type, L.qkv.d, E, QR, m->act_e, m->qkv, 0, s));
+        } else {
+            // Rows kept in the fused buffer are a sub-tensor only for layouts
+            // without a separate scale array (Q4_K); split layouts go per part.
+            const int64_t rows[3] = {(int64_t)H * HD, (int64_t)HKV * HD, (int64_t)HKV * HD};
+            int64_t r0 = 0;
+            for (int p = 0; p < 3; p++) {
+                if (L.in_qkv[p]) {
+                    if (L.qkv.type == T_Q6_K || L.qkv.type == T_Q8_0)
+                        return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "mixed q/k/v types with a split layout");
+                    const SplitDst d = split_dst(L.qkv.type, E, QR, L.qkv.d, r0);
+                    TS5_HIP(ctx, launch_matvec(L.qkv.type, d.body, E, rows[p], m->act_e, m->qkv + r0, 0, s));
+                } else {
+                    TS5_HIP(ctx, launch_matvec(L.part[p].type, L.part[p].d, E, rows[p], m->act_e, m->qkv + r0, 0, s));
+                }
+                r0 += rows[p];
+            }
+        }
+        const KvLayer kv = m->kv_layer(l);
+        TS5_HIP(ctx, launch_rope_kv(m->qkv, QR, m->has_bias[l] ? m->bias + (int64_t)l * QR : nullptr,
+                                    L.q_norm.set ? (const float *)L.q_norm.d : nullptr,
+                                    L.k_norm.set ? (const float *)L.k_norm.d : nullptr, hp.rms_eps, m->rope_cs,
+                                    hp.rope_dims, hp.rope_neox, m->state, H, HKV, HD, m->n_ctx, 1, m->q_rot, kv, s));
+        TS5_HIP(ctx, launch_attn_decode(m->q_rot, kv, 0, m->state, 1, H, HKV, HD, m->n_ctx, m->n_split, hp.attn_scale,
+                                        m->part, nullptr, m->act_att, s));
+        TS5_HIP(ctx, launch_matvec(L.wo.type, L.wo.d, (int64_t)H * HD, E, m->act_att, m->x, 1, s));
+        TS5_HIP(ctx, launch_act_quant(m->x, E, (const float *)L.ffn_norm.d, hp.rms_eps, E, 1, m->act_e, s));
+        TS5_HIP(ctx, launch_matvec_glu(L.gate.type, L.gate.d, L.up.d, E, F, m->act_e, nullptr, m->act_f, s));
+        TS5_HIP(ctx, launch_matvec(L.down.type, L.down.d, F, E, m->act_f, m->x, 1, s));
+    }
+    if (head) {
+        const DevT &out = m->output.set ? m->output : m->tok_embd;
+        TS5_HIP(ctx, launch_act_quant(m->x, E, (const float *)m->out_norm.d, hp.rms_eps, E, 1, m->act_e, s));
+        TS5_HIP(ctx, launch_matvec(out.type, out.d, E, hp.n_vocab, m->act_e, m->logits, 0, s));
+    }
+    if (tail == 1) {
+        TS5_HIP(ctx, launch_argmax(m->logits, hp.n_vocab, 1, m->amax, m->state + 1, m->seq, m->state, s));
+    } else {
+        TS5_HIP(ctx, launch_advance(m->state, s));
+    }
+    return TS5HIP_OK;
+}
+
+int build_graphs(ts5hip_model *m) {
+    if (!m->graphs_stale) return TS5HIP_OK;
+    if (int rc = check_complete(m)) return rc;
+    ts5hip_ctx *ctx = m->ctx;
+    TS5_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (int g = 0; g < N_GRAPHS; g++) {
+        if (m->graph[g]) {
+            (void)hipGraphExecDestroy(m->graph[g]);
+            m->graph[g] = nullptr;
+        }
+        hipGraph_t graph = nullptr;
+        TS5_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        const int rc = enqueue_token(m, g != G_KV, g == G_GREEDY ? 1 : 0);
+        const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+        if (rc) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return rc;
+        }
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamEndCapture");
+        const hipError_t ei = hipGraphInstantiate(&m->graph[g], graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (ei != hipSuccess) return hip_fail(ctx, ei, "hipGraphInstantiate");
+    }
+    m->graphs_stale = false;
+    return TS5HIP_OK;
+}
+
+int ensure_rows(ts5hip_model *m, int rows) {
+    if (rows <= m->rows_cap) return TS5HIP_OK;
+    ts5hip_ctx *ctx = m->ctx;
+    TS5_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (m->dev_rows) TS5_HIP(ctx, hipFree(m->dev_rows));
+    if (m->host_rows) TS5_HIP(ctx, hipHostFree(m->host_rows));
+    m->dev_rows = nullptr, m->host_rows = nullptr, m->rows_cap = 0, m->rows_valid = 0;
+    const int cap = std::max(rows, 8);
+    const size_t bytes = (size_t)cap * m->hp.n_vocab * 4;
+    TS5_HIP(ctx, hipMalloc((void **)&m->dev_rows, bytes));
+    TS5_HIP(ctx, hipHostMalloc((void **)&m->host_rows, bytes, hipHostMallocDefault));
+    m->rows_cap = cap;
+    return TS5HIP_OK;
+}
+
+// Positions pos0.. of n tokens; logits rows (all or the last) left at
+// dev_rows / host_rows when want_logits.
+int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool want_logits, bool all) {
+    ts5hip_ctx *ctx = m->ctx;
+    if (!tokens || n <= 0 || pos0 < 0) return fail(ctx, TS5HIP_ERR_ARG, "bad tokens/n/pos0");
+    if ((int64_t)pos0 + n > m->n_ctx) return fail(ctx, TS5HIP_ERR_CONTEXT_FULL, "context full");
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->hp.n_vocab)
+            return fail(ctx, TS5HIP_ERR_ARG, "token %d out of range", tokens[i]);
+    if (int rc = build_graphs(m)) return rc;
+    const int rows = want_logits ? (all ? n : 1) : 0;
+    if (rows)
+        if (int rc = ensure_rows(m, rows)) return rc;
+    const hipStream_t s = ctx->stream;
+    std::memcpy(m->pinned_ids, tokens, (size_t)n * 4);
+    m->pinned_ids[n] = pos0;
+    TS5_HIP(ctx, hipMemcpyAsync(m->seq + pos0, m->pinned_ids, (size_t)n * 4, hipMemcpyHostToDevice, s));
+    TS5_HIP(ctx, hipMemcpyAsync(m->state, m->pinned_ids + n, 4, hipMemcpyHostToDevice, s));
+    if (m->profile) TS5_HIP(ctx, hipEventRecord(ctx->ev0, s));
+    const size_t row_bytes = (size_t)m->hp.n_vocab * 4;
+    for (int t = 0; t < n; t++) {
+        const bool lg = want_logits && (all || t == n - 1);
+        TS5_HIP(ctx, hipGraphLaunch(m->graph[lg ? G_LOGITS : G_KV], s));
+        if (lg) {
+            const int r = all ? t : 0;
+            TS5_HIP(ctx, hipMemcpyAsync(m->dev_rows + (size_t)r * m->hp.n_vocab, m->logits, row_bytes,
+                                        hipMemcpyDeviceToDevice, s));
+        }
+    }
+    if (rows) {
+        TS5_HIP(ctx, hipMemcpyAsync(m->host_rows, m->dev_rows, rows * row_bytes, hipMemcpyDeviceToHost, s));
+    }
+    if (m->profile) TS5_HIP(ctx, hipEventRecord(ctx->ev1, s));
+    TS5_HIP(ctx, hipStreamSynchronize(s));
+    if (m->profile) {
+        float ms = 0;
+        TS5_HIP(ctx, hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
+        m->prof_ms += ms, m->prof_calls++, m->prof_tokens += n;
+    }
+    m->rows_valid = rows;
+    return TS5HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, int kv_type, ts5hip_model **out) {
+    if (!ctx || !hp || !out) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
+    *out = nullptr;
+    if (kv_type != KV_Q8) return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "KV type %d (the GPU cache is q8)", kv_type);
+    // Rows are whole 32-value blocks (Q8_0; Q4_K/Q6_K tensors also check ne0 % 256).
+    if (hp->n_embd <= 0 || hp->n_embd % 32 || hp->n_ff <= 0 || hp->n_ff % 32 || hp->n_layer <= 0 ||
+        hp->n_vocab <= 0 || n_ctx <= 0 || hp->rope_dims <= 0 || hp->rope_dims > hp->head_dim || hp->rope_dims % 2)
+        return fail(ctx, TS5HIP_ERR_ARG, "bad hyperparameters");
+    if (!attn_supported(hp->n_head, hp->n_head_kv, hp->head_dim))
+        return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "attention for %d/%d heads of %d", hp->n_head, hp->n_head_kv,
+                    hp->head_dim);
+    ts5hip_model *m = new ts5hip_model();
+    m->ctx = ctx;
+    m->hp = *hp;
+    m->n_ctx = n_ctx;
+    m->kv_type = kv_type;
+    m->layers.resize(hp->n_layer);
+    m->has_bias.assign(hp->n_layer, false);
+    m->n_split = attn_splits(1, hp->n_head_kv);
+    const char *prof = std::getenv("TS5HIP_PROFILE");
+    m->profile = prof && *prof && std::strcmp(prof, "0") != 0;
+    const int64_t E = hp->n_embd, F = hp->n_ff, HD = hp->head_dim, H = hp->n_head, HKV = hp->n_head_kv;
+    const int64_t kv_elems = (int64_t)hp->n_layer * HKV * n_ctx * HD;
+    int rc = 0;
+    if ((rc = alloc_t(m, kv_elems, &m->k8)) || (rc = alloc_t(m, kv_elems, &m->v8)) ||
+        (rc = alloc_t(m, kv_elems / 32, &m->ks)) || (rc = alloc_t(m, kv_elems / 32, &m->vs)) ||
+        (rc = alloc_t(m, (size_t)n_ctx * hp->rope_dims, &m->rope_cs)) ||
+        (rc = alloc_t(m, (size_t)hp->n_layer * m->qkv_rows(), &m->bias)) || (rc = alloc_t(m, E, &m->x)) ||
+        (rc = alloc_t(m, m->qkv_rows(), &m->qkv)) || (rc = alloc_t(m, H * HD, &m->q_rot)) ||
+        (rc = alloc_t(m, hp->n_vocab, &m->logits)) ||
+        (rc = alloc_t(m, attn_partial_bytes(1, m->n_split, H, HD) / 4, &m->part)) ||
+        (rc = alloc_t(m, act_bytes(std::max(E, H * HD)), &m->act_e)) ||
+        (rc = alloc_t(m, act_bytes(H * HD), &m->act_att)) || (rc = alloc_t(m, act_bytes(F), &m->act_f)) ||
+        (rc = alloc(m, argmax_scratch_bytes(1), &m->amax)) || (rc = alloc(m, topk_scratch_bytes(), &m->topk)) ||
+        (rc = alloc_t(m, 64, &m->topk_v)) || (rc = alloc_t(m, 64, &m->topk_i)) ||
+        (rc = alloc_t(m, (size_t)n_ctx + 1, &m->seq)) || (rc = alloc_t(m, 4, &m->state))) {
+        ts5hip_model_destroy(m);
+        return rc;
+    }
+    hipError_t e;
+    if ((e = hipMemsetAsync(m->bias, 0, (size_t)hp->n_layer * m->qkv_rows() * 4, ctx->stream)) != hipSuccess ||
+        (e = hipMemsetAsync(m->seq, 0, ((size_t)n_ctx + 1) * 4, ctx->stream)) != hipSuccess ||
+        (e = hipMemsetAsync(m->k8, 0, kv_elems, ctx->stream)) != hipSuccess ||
+        (e = hipMemsetAsync(m->v8, 0, kv_elems, ctx->stream)) != hipSuccess ||
+        (e = hipMemsetAsync(m->ks, 0, kv_elems / 32 * 2, ctx->stream)) != hipSuccess ||
+        (e = hipMemsetAsync(m->vs, 0, kv_elems / 32 * 2, ctx->stream)) != hipSuccess ||
+        (e = hipHostMalloc((void **)&m->pinned_ids, ((size_t)n_ctx + 2) * 4, hipHostMallocDefault)) != hipSuccess ||
+        (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) {
+        hip_fail(ctx, e, "model buffers");
+        ts5hip_model_destroy(m);
+        return TS5HIP_ERR_HIP;
+    }
+    *out = m;
+    return TS5HIP_OK;
+}
+
+void ts5hip_model_destroy(ts5hip_model *m) {
+    if (!m) return;
+    (void)hipStreamSynchronize(m->ctx->stream);
+    for (auto &g : m->graph)
+        if (g) (void)hipGraphExecDestroy(g);
+    for (void *p : m->allocs) (void)hipFree(p);
+    if (m->dev_rows) (void)hipFree(m->dev_rows);
+    if (m->host_rows) (void)hipHostFree(m->host_rows);
+    if (m->pinned_ids) (void)hipHostFree(m->pinned_ids);
+    delete m;
+}
+
+int ts5hip_model_set_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, int64_t ne1,
+                            const void *gguf) {
+    if (!m || !name || !gguf) return fail(m ? m->ctx : nullptr, TS5HIP_ERR_ARG, "null argument");
+    return set_tensor(m, name, type, ne0, ne1, Source{gguf, 0, 0});
+}
+
+int ts5hip_model_synth_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, int64_t ne1,
+                              uint64_t seed, int centered) {
+    if (!m || !name) return fail(m ? m->ctx : nullptr, TS5HIP_ERR_ARG, "null argument");
+    // One stream per tensor name: FNV-1a of the name mixed into the seed.
+    uint64_t h = 1469598103934665603ull;
+    for (const char *c = name; *c; c++) h = (h ^ (uint8_t)*c) * 1099511628211ull;
+    return set_tensor(m, name, type, ne0, ne1, Source{nullptr, seed ^ h, centered});
+}
+
+int ts5hip_forward(ts5hip_model *m, const int32_t *tokens, int n, int pos0, float *logits, int all_logits) {
+    if (!m) return fail(nullptr, TS5HIP_ERR_ARG, "null model");
+    if (int rc = run_tokens(m, tokens, n, pos0, logits != nullptr, all_logits != 0)) return rc;
+    if (logits) std::memcpy(logits, m->host_rows, (size_t)m->rows_valid * m->hp.n_vocab * 4);
+    return TS5HIP_OK;
+}
+
+int ts5hip_forward_in_place(ts5hip_model *m, const int32_t *tokens, int n, int pos0, int all_logits) {
+    if (!m) return fail(nullptr, TS5HIP_ERR_ARG, "null model");
+    return run_tokens(m, tokens, n, pos0, true, all_logits != 0);
+}
+
+const float *ts5hip_logits_view(const ts5hip_model *m) { return m && m->rows_valid ? m->host_rows : nullptr; }
+int ts5hip_n_ctx(const ts5hip_model *m) { return m ? m->n_ctx : 0; }
+int ts5hip_kv_type(const ts5hip_model *m) { return m ? m->kv_type : -1; }
+
+int32_t ts5hip_model_sample(ts5hip_model *m, ts5hip_sampler *s, int row, float temperature, float top_p, int top_k) {
+    if (!m || !s) return fail(m ? m->ctx : nullptr, TS5HIP_ERR_ARG, "null argument");
+    ts5hip_ctx *ctx = m->ctx;
+    if (row < 0 || row >= m->rows_valid) return fail(ctx, TS5HIP_ERR_ARG, "row %d of %d", row, m->rows_valid);
+    const int nv = m->hp.n_vocab;
+    const float *dl = m->dev_rows + (size_t)row * nv;
+    if (temperature <= 0) {
+        TS5_HIP(ctx, launch_argmax(dl, nv, 1, m->amax, m->state + 1, nullptr, nullptr, ctx->stream));
+        int32_t id = 0;
+        if (int rc = ts5hip_download(ctx, &id, m->state + 1, 4)) return rc;
+        return id;
+    }
+    if (top_k > 0 && top_k <= topk_max() && nv <= topk_max_n()) {
+        TS5_HIP(ctx, launch_topk(dl, nv, top_k, m->topk, m->topk_v, m->topk_i, ctx->stream));
+        float v[64];
+        int32_t id[64];
+        if (int rc = ts5hip_download(ctx, v, m->topk_v, (size_t)top_k * 4)) return rc;
+        if (int rc = ts5hip_download(ctx, id, m->topk_i, (size_t)top_k * 4)) return rc;
+        return ts5hip_sampler_draw(s, id, v, top_k, temperature, top_p);
+    }
+    // No top-k, or a k beyond the GPU reduction: the whole row, on the host.
+    return sample_host_row(s, m->host_rows + (size_t)row * nv, nv, temperature, top_p, top_k);
+}
+
+int ts5hip_generate_greedy(ts5hip_model *m, int32_t token, int pos, int n_steps, int32_t *ids_out) {
+    if (!m) return fail(nullptr, TS5HIP_ERR_ARG, "null model");
+    ts5hip_ctx *ctx = m->ctx;
+    if (n_steps <= 0 || pos < 0 || token < 0 || token >= m->hp.n_vocab) return fail(ctx, TS5HIP_ERR_ARG, "bad arguments");
+    if ((int64_t)pos + n_steps > m->n_ctx) return fail(ctx, TS5HIP_ERR_CONTEXT_FULL, "context full");
+    if (int rc = build_graphs(m)) return rc;
+    const hipStream_t s = ctx->stream;
+    m->pinned_ids[0] = token;
+    m->pinned_ids[1] = pos;
+    TS5_HIP(ctx, hipMemcpyAsync(m->seq + pos, m->pinned_ids, 4, hipMemcpyHostToDevice, s));
+    TS5_HIP(ctx, hipMemcpyAsync(m->state, m->pinned_ids + 1, 4, hipMemcpyHostToDevice, s));
+    for (int i = 0; i < n_steps; i++) TS5_HIP(ctx, hipGraphLaunch(m->graph[G_GREEDY], s));
+    TS5_HIP(ctx, hipMemcpyAsync(m->pinned_ids, m->seq + pos + 1, (size_t)n_steps * 4, hipMemcpyDeviceToHost, s));
+    TS5_HIP(ctx, hipStreamSynchronize(s));
+    if (ids_out) std::memcpy(ids_out, m->pinned_ids, (size_t)n_steps * 4);
+    m->rows_valid = 0;
+    return TS5HIP_OK;
+}
+
+int ts5hip_kv_read(ts5hip_model *m, int layer, int which, int pos0, int n, float *out) {
+    if (!m || !out) return fail(m ? m->ctx : nullptr, TS5HIP_ERR_ARG, "null argument");
+    ts5hip_ctx *ctx = m->ctx;
+    if (layer < 0 || layer >= m->hp.n_layer || pos0 < 0 || n <= 0 || pos0 + n > m->n_ctx)
+        return fail(ctx, TS5HIP_ERR_ARG, "bad layer/range");
+    const int64_t w = (int64_t)m->hp.n_head_kv * m->hp.head_dim;
+    float *d = nullptr;
+    TS5_HIP(ctx, hipMalloc((void **)&d, (size_t)n * w * 4));
+    hipError_t e = launch_kv_read(m->kv_layer(layer), which, m->hp.n_head_kv, m->hp.head_dim, m->n_ctx, pos0, n, d,
+                                  ctx->stream);
+    int rc = e == hipSuccess ? ts5hip_download(ctx, out, d, (size_t)n * w * 4) : hip_fail(ctx, e, "kv_read");
+    (void)hipFree(d);
+    return rc;
+}
+
+int ts5hip_take_profile(ts5hip_model *m, char *buf, int len) {
+    if (!m || !buf || len <= 0) return fail(m ? m->ctx : nullptr, TS5HIP_ERR_ARG, "bad argument");
+    std::string s;
+    if (m->profile && m->prof_calls) {
+        char line[256];
+        std::snprintf(line, sizeof line, "hip: %d forward calls, %d tokens, %.3f ms GPU (%.3f ms/token)\n",
+                      m->prof_calls, m->prof_tokens, m->prof_ms, m->prof_ms / std::max(1, m->prof_tokens));
+        s = line;
+    }
+    m->prof_ms = 0, m->prof_calls = 0, m->prof_tokens = 0;
+    std::strncpy(buf, s.c_str(), (size_t)len - 1);
+    buf[len - 1] = 0;
+    return TS5HIP_OK;
+}
+
+}  // extern "C"

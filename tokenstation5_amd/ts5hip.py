@@ -1,0 +1,354 @@
+"""ctypes binding of libts5hip.so (include/ts5hip.h) for tests and benchmarks.
+
+Everything calls through the C ABI; there is no Python fallback: if the
+library is not built, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libts5hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "ts5hip.h")
+
+OK, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED, ERR_CONTEXT_FULL, ERR_STATE = 0, -1, -2, -3, -4, -5
+F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
+KV_Q8 = 2
+
+_vp, _i64, _i32, _u32, _u64, _f32 = C.c_void_p, C.c_int64, C.c_int, C.c_uint32, C.c_uint64, C.c_float
+
+
+class HParams(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("n_vocab", "n_embd", "n_layer", "n_ff", "n_head", "n_head_kv",
+                                          "head_dim", "rope_dims", "rope_neox")] + \
+               [(n, C.c_float) for n in ("rms_eps", "rope_base", "attn_scale", "rope_scale")]
+
+
+_SIGS = {
+    "ts5hip_last_error": (C.c_char_p, [_vp]),
+    "ts5hip_init": (_i32, [_i32, C.POINTER(_vp)]),
+    "ts5hip_destroy": (None, [_vp]),
+    "ts5hip_device_info": (_i32, [_vp, C.POINTER(_i32), C.c_char_p, _i32, C.POINTER(_i64)]),
+    "ts5hip_alloc": (_i32, [_vp, C.c_size_t, C.POINTER(_vp)]),
+    "ts5hip_free": (_i32, [_vp, _vp]),
+    "ts5hip_upload": (_i32, [_vp, _vp, _vp, C.c_size_t]),
+    "ts5hip_download": (_i32, [_vp, _vp, _vp, C.c_size_t]),
+    "ts5hip_memset": (_i32, [_vp, _vp, _i32, C.c_size_t]),
+    "ts5hip_sync": (_i32, [_vp]),
+    "ts5hip_timer_begin": (_i32, [_vp]),
+    "ts5hip_timer_end": (_i32, [_vp, C.POINTER(_f32)]),
+    "ts5hip_supports_type": (_i32, [_u32]),
+    "ts5hip_weight_bytes": (_i64, [_u32, _i64, _i64]),
+    "ts5hip_weight_upload": (_i32, [_vp, _u32, _i64, _i64, _vp, _vp]),
+    "ts5hip_weight_synth": (_i32, [_vp, _u32, _i64, _i64, _u64, _i32, _vp]),
+    "ts5hip_dequantize": (_i32, [_vp, _u32, _vp, _i64, _i64, _vp]),
+    "ts5hip_act_bytes": (_i64, [_i64]),
+    "ts5hip_act_quantize": (_i32, [_vp, _vp, _vp, _f32, _i64, _i32, _vp]),
+    "ts5hip_rmsnorm": (_i32, [_vp, _vp, _vp, _f32, _i64, _i32, _vp]),
+    "ts5hip_matvec": (_i32, [_vp, _u32, _vp, _i64, _i64, _vp, _vp, _i32]),
+    "ts5hip_matvec_glu": (_i32, [_vp, _u32, _vp, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "ts5hip_rope_table": (_i32, [_vp, _i32, _i32, _f32, _f32, _vp, _vp]),
+    "ts5hip_rope_kv_append": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp,
+                                     _f32, _vp, _vp, _vp, _vp, _vp]),
+    "ts5hip_attn_decode": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _f32, _i32,
+                                  _vp, _vp]),
+    "ts5hip_argmax": (_i32, [_vp, _vp, _i32, _i32, _vp]),
+    "ts5hip_topk": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp]),
+    "ts5hip_sampler_new": (_vp, [_u64]),
+    "ts5hip_sampler_free": (None, [_vp]),
+    "ts5hip_sampler_draw": (C.c_int32, [_vp, _vp, _vp, _i32, _f32, _f32]),
+    "ts5hip_model_create": (_i32, [_vp, C.POINTER(HParams), _i32, _i32, C.POINTER(_vp)]),
+    "ts5hip_model_destroy": (None, [_vp]),
+    "ts5hip_model_set_tensor": (_i32, [_vp, C.c_char_p, _u32, _i64, _i64, _vp]),
+    "ts5hip_model_synth_tensor": (_i32, [_vp, C.c_char_p, _u32, _i64, _i64, _u64, _i32]),
+    "ts5hip_forward": (_i32, [_vp, _vp, _i32, _i32, _vp, _i32]),
+    "ts5hip_forward_in_place": (_i32, [_vp, _vp, _i32, _i32, _i32]),
+    "ts5hip_logits_view": (C.POINTER(C.c_float), [_vp]),
+    "ts5hip_n_ctx": (_i32, [_vp]),
+    "ts5hip_kv_type": (_i32, [_vp]),
+    "ts5hip_model_sample": (C.c_int32, [_vp, _vp, _i32, _f32, _f32, _i32]),
+    "ts5hip_generate_greedy": (_i32, [_vp, C.c_int32, _i32, _i32, _vp]),
+    "ts5hip_kv_read": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
+    "ts5hip_take_profile": (_i32, [_vp, C.c_char_p, _i32]),
+}
+
+_lib = None
+
+
+def header_symbols() -> list[str]:
+    """Every function include/ts5hip.h declares."""
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(ts5hip_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build() (no CPU fallback exists)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+class Ts5HipError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"ts5hip error {code}: {msg}")
+        self.code = code
+
+
+def _ptr(a) -> int | None:
+    if a is None:
+        return None
+    if isinstance(a, DeviceBuffer):
+        return a.ptr
+    if isinstance(a, np.ndarray):
+        assert a.flags["C_CONTIGUOUS"]
+        return a.ctypes.data
+    return int(a)
+
+
+class DeviceBuffer:
+    def __init__(self, ctx: "Context", nbytes: int):
+        self.ctx, self.nbytes = ctx, int(nbytes)
+        p = _vp()
+        ctx.check(lib().ts5hip_alloc(ctx.h, self.nbytes, C.byref(p)))
+        self.ptr = p.value
+
+    def free(self):
+        if self.ptr:
+            self.ctx.check(lib().ts5hip_free(self.ctx.h, self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and self.ctx.h:
+                lib().ts5hip_free(self.ctx.h, self.ptr)
+        except Exception:
+            pass
+
+    def upload(self, a: np.ndarray):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes, (a.nbytes, self.nbytes)
+        self.ctx.check(lib().ts5hip_upload(self.ctx.h, self.ptr, a.ctypes.data, a.nbytes))
+        return self
+
+    def download(self, dtype, shape=None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        count = (self.nbytes - offset) // dtype.itemsize if shape is None else int(np.prod(shape))
+        out = np.empty(count, dtype)
+        self.ctx.check(lib().ts5hip_download(self.ctx.h, out.ctypes.data, self.ptr + offset, out.nbytes))
+        return out if shape is None else out.reshape(shape)
+
+    def zero(self):
+        self.ctx.check(lib().ts5hip_memset(self.ctx.h, self.ptr, 0, self.nbytes))
+        return self
+
+
+class Context:
+    def __init__(self, device: int = 0):
+        self.h = None
+        h = _vp()
+        rc = lib().ts5hip_init(device, C.byref(h))
+        if rc != OK:
+            raise Ts5HipError(rc, lib().ts5hip_last_error(None).decode())
+        self.h = h.value
+        n_cu, hbm = _i32(), _i64()
+        arch = C.create_string_buffer(64)
+        self.check(lib().ts5hip_device_info(self.h, C.byref(n_cu), arch, 64, C.byref(hbm)))
+        self.n_cu, self.arch, self.hbm = n_cu.value, arch.value.decode(), hbm.value
+
+    def close(self):
+        if self.h:
+            lib().ts5hip_destroy(self.h)
+            self.h = None
+
+    def check(self, rc: int):
+        if rc != OK:
+            raise Ts5HipError(rc, lib().ts5hip_last_error(self.h).decode())
+        return rc
+
+    # -- memory ------------------------------------------------------------------
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def to_device(self, a: np.ndarray) -> DeviceBuffer:
+        a = np.ascontiguousarray(a)
+        return DeviceBuffer(self, max(a.nbytes, 1)).upload(a)
+
+    def sync(self):
+        self.check(lib().ts5hip_sync(self.h))
+
+    def timer_begin(self):
+        self.check(lib().ts5hip_timer_begin(self.h))
+
+    def timer_end(self) -> float:
+        ms = _f32()
+        self.check(lib().ts5hip_timer_end(self.h, C.byref(ms)))
+        return ms.value
+
+    # -- weights -----------------------------------------------------------------
+    @staticmethod
+    def weight_bytes(t: int, ne0: int, ne1: int) -> int:
+        return lib().ts5hip_weight_bytes(t, ne0, ne1)
+
+    def weight(self, t: int, ne0: int, ne1: int, gguf: np.ndarray) -> DeviceBuffer:
+        """GGUF bytes (ne1, row_bytes) uint8 -> a device buffer in HBM layout."""
+        n = self.weight_bytes(t, ne0, ne1)
+        if n < 0:
+            raise Ts5HipError(ERR_UNSUPPORTED, f"type {t} {ne1}x{ne0}")
+        d = DeviceBuffer(self, n)
+        g = np.ascontiguousarray(gguf, np.uint8)
+        self.check(lib().ts5hip_weight_upload(self.h, t, ne0, ne1, g.ctypes.data, d.ptr))
+        return d
+
+    def weight_synth(self, t: int, ne0: int, ne1: int, seed: int, centered: bool = False) -> DeviceBuffer:
+        d = DeviceBuffer(self, self.weight_bytes(t, ne0, ne1))
+        self.check(lib().ts5hip_weight_synth(self.h, t, ne0, ne1, seed, int(centered), d.ptr))
+        return d
+
+    # -- ops (device buffers in and out) --------------------------------------------
+    def dequantize(self, t, w, ne0, rows, y):
+        self.check(lib().ts5hip_dequantize(self.h, t, _ptr(w), ne0, rows, _ptr(y)))
+
+    @staticmethod
+    def act_bytes(n: int) -> int:
+        return lib().ts5hip_act_bytes(n)
+
+    def act_quantize(self, x, norm_w, eps, n, ntok, act):
+        self.check(lib().ts5hip_act_quantize(self.h, _ptr(x), _ptr(norm_w), eps, n, ntok, _ptr(act)))
+
+    def rmsnorm(self, x, w, eps, n, ntok, y):
+        self.check(lib().ts5hip_rmsnorm(self.h, _ptr(x), _ptr(w), eps, n, ntok, _ptr(y)))
+
+    def matvec(self, t, w, ne0, ne1, act, y, accumulate=False):
+        self.check(lib().ts5hip_matvec(self.h, t, _ptr(w), ne0, ne1, _ptr(act), _ptr(y), int(accumulate)))
+
+    def matvec_glu(self, t, wg, wu, ne0, ne1, act, y, act_out):
+        self.check(lib().ts5hip_matvec_glu(self.h, t, _ptr(wg), _ptr(wu), ne0, ne1, _ptr(act), _ptr(y),
+                                           _ptr(act_out)))
+
+    def rope_table(self, n_rot, n_pos, base, scale=1.0, freqs=None) -> DeviceBuffer:
+        d = DeviceBuffer(self, n_pos * n_rot * 4)
+        f = None if freqs is None else np.ascontiguousarray(freqs, np.float32)
+        self.check(lib().ts5hip_rope_table(self.h, n_rot, n_pos, base, scale, _ptr(f), d.ptr))
+        return d
+
+    def rope_kv_append(self, qkv, ntok, pos0_dev, H, HKV, HD, n_rot, neox, rope_cs, n_ctx, q_out, k8, ks, v8, vs,
+                       bias=None, q_norm=None, k_norm=None, eps=1e-6):
+        self.check(lib().ts5hip_rope_kv_append(self.h, _ptr(qkv), ntok, _ptr(pos0_dev), H, HKV, HD, n_rot, int(neox),
+                                               _ptr(rope_cs), n_ctx, _ptr(bias), _ptr(q_norm), _ptr(k_norm), eps,
+                                               _ptr(q_out), _ptr(k8), _ptr(ks), _ptr(v8), _ptr(vs)))
+
+    def attn_decode(self, q, B, H, HKV, HD, k8, ks, v8, vs, n_ctx, n_keys_dev, kv_per_batch, scale, n_split=0,
+                    out=None, act_out=None):
+        self.check(lib().ts5hip_attn_decode(self.h, _ptr(q), B, H, HKV, HD, _ptr(k8), _ptr(ks), _ptr(v8), _ptr(vs),
+                                            n_ctx, _ptr(n_keys_dev), int(kv_per_batch), scale, n_split, _ptr(out),
+                                            _ptr(act_out)))
+
+    def argmax(self, x, n, rows, out):
+        self.check(lib().ts5hip_argmax(self.h, _ptr(x), n, rows, _ptr(out)))
+
+    def topk(self, x, n, k, vals, ids):
+        self.check(lib().ts5hip_topk(self.h, _ptr(x), n, k, _ptr(vals), _ptr(ids)))
+
+
+class Sampler:
+    def __init__(self, seed: int):
+        self.h = lib().ts5hip_sampler_new(seed)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().ts5hip_sampler_free(self.h)
+            self.h = None
+
+    def draw(self, ids, logits, temperature, top_p) -> int:
+        ids = np.ascontiguousarray(ids, np.int32)
+        lg = np.ascontiguousarray(logits, np.float32)
+        return int(lib().ts5hip_sampler_draw(self.h, ids.ctypes.data, lg.ctypes.data, ids.size, temperature, top_p))
+
+
+def hparams(hp: dict) -> HParams:
+    """HParams of a synth.py model dict (engine/src/model.cpp:13-68 derivations)."""
+    return HParams(n_vocab=hp["n_vocab"], n_embd=hp["n_embd"], n_layer=hp["n_layer"], n_ff=hp["n_ff"],
+                   n_head=hp["n_head"], n_head_kv=hp["n_head_kv"], head_dim=hp["head_dim"],
+                   rope_dims=hp.get("rope_dims", hp["head_dim"]),
+                   rope_neox=int(hp["arch"] in ("qwen2", "qwen3", "gemma3")),
+                   rms_eps=hp["rms_eps"], rope_base=hp["rope_base"],
+                   attn_scale=float(np.float32(1.0) / np.sqrt(np.float32(hp["head_dim"]))), rope_scale=1.0)
+
+
+class Model:
+    """Backend (engine/src/backend.h:16-44) over libts5hip.so."""
+
+    def __init__(self, ctx: Context, hp: dict, n_ctx: int, kv: int = KV_Q8):
+        self.ctx, self.hp, self.h = ctx, hp, None
+        self._hp = hparams(hp)
+        h = _vp()
+        ctx.check(lib().ts5hip_model_create(ctx.h, C.byref(self._hp), n_ctx, kv, C.byref(h)))
+        self.h = h.value
+        self.n_vocab = hp["n_vocab"]
+
+    def close(self):
+        if self.h:
+            lib().ts5hip_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_tensors(self, tensors: dict):
+        """{name: (type, ne0, ne1, gguf uint8 array)} (synth.model_tensors)."""
+        for name, (t, ne0, ne1, data) in tensors.items():
+            d = np.ascontiguousarray(data, np.uint8)
+            self.ctx.check(lib().ts5hip_model_set_tensor(self.h, name.encode(), t, ne0, ne1, d.ctypes.data))
+
+    def synth_tensor(self, name: str, t: int, ne0: int, ne1: int, seed: int, centered: bool = False):
+        self.ctx.check(lib().ts5hip_model_synth_tensor(self.h, name.encode(), t, ne0, ne1, seed, int(centered)))
+
+    def forward(self, tokens, pos0: int, logits: bool = True, all_logits: bool = False):
+        tok = np.ascontiguousarray(tokens, np.int32)
+        n = tok.size
+        out = np.empty(((n if all_logits else 1), self.n_vocab), np.float32) if logits else None
+        self.ctx.check(lib().ts5hip_forward(self.h, tok.ctypes.data, n, pos0, _ptr(out), int(all_logits)))
+        return out
+
+    def forward_in_place(self, tokens, pos0: int, all_logits: bool = False) -> np.ndarray:
+        tok = np.ascontiguousarray(tokens, np.int32)
+        self.ctx.check(lib().ts5hip_forward_in_place(self.h, tok.ctypes.data, tok.size, pos0, int(all_logits)))
+        rows = tok.size if all_logits else 1
+        p = lib().ts5hip_logits_view(self.h)
+        return np.ctypeslib.as_array(p, shape=(rows, self.n_vocab))
+
+    def sample(self, sampler: Sampler, row: int, temperature: float, top_p: float, top_k: int) -> int:
+        r = lib().ts5hip_model_sample(self.h, sampler.h, row, temperature, top_p, top_k)
+        if r < 0:
+            self.ctx.check(r)
+        return int(r)
+
+    def generate_greedy(self, token: int, pos: int, n_steps: int) -> np.ndarray:
+        out = np.empty(n_steps, np.int32)
+        self.ctx.check(lib().ts5hip_generate_greedy(self.h, token, pos, n_steps, out.ctypes.data))
+        return out
+
+    def kv(self, layer: int, which: int, pos0: int, n: int) -> np.ndarray:
+        w = self.hp["n_head_kv"] * self.hp["head_dim"]
+        out = np.empty((n, w), np.float32)
+        self.ctx.check(lib().ts5hip_kv_read(self.h, layer, which, pos0, n, out.ctypes.data))
+        return out
+
+    def take_profile(self) -> str:
+        buf = C.create_string_buffer(4096)
+        self.ctx.check(lib().ts5hip_take_profile(self.h, buf, 4096))
+        return buf.value.decode()

@@ -63,24 +63,24 @@ def model_tensor_specs(hp: dict):
         yield p + "ffn_down.weight", hp.get("down_type", wt), F, E
 
 
-def decode_bench(ctx, hp, steps: int, warmup: int):
-    n_ctx = PROMPT + max(steps, warmup) + 8
+def decode_bench(ctx, hp, steps: int, warmup: int, prompt_len: int = PROMPT):
+    n_ctx = prompt_len + max(steps, warmup) + 8
     m = ts5hip.Model(ctx, hp, n_ctx)
     t0 = time.time()
     for name, t, ne0, ne1 in model_tensor_specs(hp):
         m.synth_tensor(name, t, ne0, ne1, SEED)
     ctx.sync()
     log(f"weights generated in HBM ({time.time() - t0:.1f} s)")
-    prompt = np.random.default_rng(SEED).integers(0, hp["n_vocab"], PROMPT).astype(np.int32)
+    prompt = np.random.default_rng(SEED).integers(0, hp["n_vocab"], prompt_len).astype(np.int32)
     t0 = time.time()
     m.forward(prompt[:-1], 0, logits=False)
-    first = int(m.generate_greedy(int(prompt[-1]), PROMPT - 1, 1)[0])
-    log(f"prefill of {PROMPT} tokens: {time.time() - t0:.1f} s (one token per graph replay)")
+    first = int(m.generate_greedy(int(prompt[-1]), prompt_len - 1, 1)[0])
+    log(f"prefill of {prompt_len} tokens: {time.time() - t0:.1f} s (one token per graph replay)")
     if warmup:
-        m.generate_greedy(first, PROMPT, warmup)
+        m.generate_greedy(first, prompt_len, warmup)
     ctx.sync()
     ctx.timer_begin()
-    ids = m.generate_greedy(first, PROMPT, steps)
+    ids = m.generate_greedy(first, prompt_len, steps)
     ms = ctx.timer_end()
     log(f"{steps} decode steps: {ms:.2f} ms ({steps / ms * 1e3:.1f} tok/s); ids[:8] {list(ids[:8])}")
     m.close()
@@ -95,25 +95,26 @@ def glu_roofline(ctx, hp, launches: int = 200):
     copies = max(2, -(-(320 << 20) // (2 * wb)))
     gates = [ctx.weight_synth(synth.Q4_K, E, F, 100 + i) for i in range(copies)]
     ups = [ctx.weight_synth(synth.Q4_K, E, F, 200 + i) for i in range(copies)]
-    x = np.random.default_rng(1).standard_normal(E).astype(np.float32)
-    act = ctx.alloc(ctx.act_bytes(E))
-    ctx.act_quantize(ctx.to_device(x), None, 0.0, E, 1, act)
-    out = ctx.alloc(ctx.act_bytes(F))
+    rng = np.random.default_rng(1)
+    x = ctx.to_device((rng.standard_normal(E) * 100).astype(np.float32))
+    nw = ctx.to_device((1 + 0.02 * rng.standard_normal(E)).astype(np.float32))
+    out = ctx.alloc(F * 4)
     for i in range(copies):
-        ctx.matvec_glu(synth.Q4_K, gates[i], ups[i], E, F, act, None, out)
+        ctx.matvec_glu(synth.Q4_K, gates[i], ups[i], E, F, x, out, norm_w=nw, eps=1e-5)
     ctx.sync()
     ctx.timer_begin()
     for i in range(launches):
-        ctx.matvec_glu(synth.Q4_K, gates[i % copies], ups[i % copies], E, F, act, None, out)
+        ctx.matvec_glu(synth.Q4_K, gates[i % copies], ups[i % copies], E, F, x, out, norm_w=nw, eps=1e-5)
     ms = ctx.timer_end()
     avg_us = ms * 1e3 / launches
-    algo = 2 * E // 256 * F * 144 + ctx.act_bytes(E) + ctx.act_bytes(F)
+    # Weights, the fp32 input and norm weight, the fp32 output.
+    algo = 2 * E // 256 * F * 144 + 2 * 4 * E + 4 * F
     achieved = algo / (avg_us * 1e-6) / 1e9
     for b in gates + ups:
         b.free()
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
-                kernel="k_mv_glu<Q4K,4,8> (ffn gate+up+SiLU, 14336x4096 x2)", avg_us=round(avg_us, 2),
+                kernel="k_mv<Q4K,2,4,MV_GLU> (ffn rmsnorm+gate+up+SiLU, 14336x4096 x2)", avg_us=round(avg_us, 2),
                 algorithmic_bytes=int(algo))
 
 
@@ -151,6 +152,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--prompt", type=int, default=PROMPT, help="prompt length (cfg2: 4096)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this backend runs ts5's token loop on one GPU (batch 1); "
@@ -159,7 +161,7 @@ def main():
     hp = dict(synth.LLAMA_8B)
     ctx = ts5hip.Context(0)
     log(f"device {ctx.arch}, {ctx.n_cu} CUs, {ctx.hbm / 2**30:.0f} GiB")
-    ms, ids = decode_bench(ctx, hp, args.steps, args.warmup)
+    ms, ids = decode_bench(ctx, hp, args.steps, args.warmup, args.prompt)
     roof = glu_roofline(ctx, hp)
     log(f"roofline: {roof}")
     ctx.close()
@@ -169,7 +171,7 @@ def main():
     value = args.steps / (ms / 1e3)
     wb = synth.weight_bytes(hp)
     token_bytes = wb["layers"] + wb["head"] + wb["norms"] + wb["embd_row"] + \
-        (hp["n_layer"]) * (PROMPT + args.steps / 2) * hp["n_head_kv"] * hp["head_dim"] * 2 * (1 + 2 / 32)
+        (hp["n_layer"]) * (args.prompt + args.steps / 2) * hp["n_head_kv"] * hp["head_dim"] * 2 * (1 + 2 / 32)
     print(json.dumps({
         "metric": "decode tok/s (8B Q4_K, bs1, 4k ctx, 1 GPU)",
         "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -177,7 +179,7 @@ def main():
         "vs_baseline": None, "dtype": "q4_k/q6_k weights, int8 x int16 dot, fp32 accum",
         "data": "synthetic (random-init weights generated in HBM, uniform prompt ids)",
         "config": {"workload": "cfg2: Llama-style 8B decode, 4096-token prompt, greedy, q8 KV",
-                   "global_batch": 1, "seq_len": PROMPT, "parallelism": "none (1 GPU)",
+                   "global_batch": 1, "seq_len": args.prompt, "parallelism": "none (1 GPU)",
                    "decode_hbm_gbs": round(token_bytes * value / 1e9, 1),
                    "decode_roofline_frac": round(token_bytes * value / 1e9 / HBM_PEAK_GBS, 4)},
         "roofline": roof, "cpu_baseline": cpu,

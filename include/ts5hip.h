@@ -81,15 +81,20 @@ int ts5hip_act_quantize(ts5hip_ctx *ctx, const float *x, const float *norm_w, fl
                         void *act);
 /* rmsnorm (engine/src/cpu_backend.cpp:48-53): y = x / rms(x) * w per token. */
 int ts5hip_rmsnorm(ts5hip_ctx *ctx, const float *x, const float *w, float eps, int64_t n, int ntok, float *y);
-/* One-token matvec y (+)= W act (engine/src/cpu_backend.cpp:18-37 at n = 1; mv16_q4_k /
- * mv16_q6_k / matmul_q8_0 in engine/src/vk_backend.cpp:863-880). W: ne1 rows of ne0. */
-int ts5hip_matvec(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0, int64_t ne1, const void *act, float *y,
-                  int accumulate);
+/* One-token matvec y (+)= W x (engine/src/cpu_backend.cpp:18-37 at n = 1; mv16_q4_k /
+ * mv16_q6_k / matmul_q8_0 in engine/src/vk_backend.cpp:863-880). W: ne1 rows of ne0 in HBM
+ * layout; x: ne0 fp32, rms-normalised by norm_w first when norm_w is not null (the norm
+ * before every projection, engine/src/cpu_backend.cpp:193, :252). */
+int ts5hip_matvec(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0, int64_t ne1, const float *x,
+                  const float *norm_w, float eps, float *y, int accumulate);
 /* Fused gate/up + SiLU (mv16_glu_q4_k, engine/src/vk_backend.cpp:1009-1021; CPU
- * engine/src/cpu_backend.cpp:253-261): out = silu(Wg act) * (Wu act), as fp32 y (may be
- * null) and as the activation act_out of the down projection. ne1 % 32 == 0. */
+ * engine/src/cpu_backend.cpp:253-261): y = silu(Wg x') * (Wu x'), x' = x or rmsnorm(x). */
 int ts5hip_matvec_glu(ts5hip_ctx *ctx, uint32_t type, const void *w_gate, const void *w_up, int64_t ne0,
-                      int64_t ne1, const void *act, float *y, void *act_out);
+                      int64_t ne1, const float *x, const float *norm_w, float eps, float *y);
+/* The output head and the greedy pick in one pass (engine/src/cpu_backend.cpp:270-285 then
+ * engine/src/engine.cpp:17): y = W x' and out_dev[0] = the first index of max(y). */
+int ts5hip_matvec_argmax(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0, int64_t ne1, const float *x,
+                         const float *norm_w, float eps, float *y, int32_t *out_dev);
 /* RoPE angles as engine/src/cpu_backend.cpp:59-61 computes them, for positions
  * [0, n_pos): dst gets [n_pos][n_rot/2] (cos, sin) float pairs. freqs: n_rot/2 divisors or null. */
 int ts5hip_rope_table(ts5hip_ctx *ctx, int n_rot, int n_pos, float base, float scale, const float *freqs_host,
@@ -107,12 +112,11 @@ int ts5hip_rope_kv_append(ts5hip_ctx *ctx, const float *qkv, int ntok, const int
  * CPU engine/src/cpu_backend.cpp:222-248). q: [B][H HD]. kv_per_batch = 1: query b reads
  * sequence b's cache (B caches of n_ctx slots back to back) over n_keys_dev[b] keys;
  * kv_per_batch = 0: one cache, query b reads n_keys_dev[0] + b + 1 keys (n_keys_dev[0] =
- * the batch's first position). out [B][H HD] fp32 and/or act_out (B activations) may be null.
- * n_split <= 0 picks a split count that fills the GPU. */
+ * the batch's first position). out: [B][H HD] fp32. n_split <= 0 picks a split count that
+ * fills the GPU. */
 int ts5hip_attn_decode(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n_head_kv, int head_dim,
                        const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx,
-                       const int32_t *n_keys_dev, int kv_per_batch, float scale, int n_split, float *out,
-                       void *act_out);
+                       const int32_t *n_keys_dev, int kv_per_batch, float scale, int n_split, float *out);
 /* Greedy token per row: the first maximum of each row of n logits (engine/src/engine.cpp:17). */
 int ts5hip_argmax(ts5hip_ctx *ctx, const float *x, int n, int rows, int32_t *out_dev);
 /* The k (<= 64) largest of n logits, descending, ties by ascending id (the candidate set

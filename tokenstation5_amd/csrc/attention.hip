@@ -4,12 +4,14 @@
 //                 (engine/src/cpu_backend.cpp:57-68, :198-221), then for K and
 //                 V heads the q8 rounding of round_kv (:78-90) written as int8
 //                 quants + f16 scales (the split layout of qkv_post.glsl:29-41).
-//  k_attn_split   split-K flash decode: per (key slice, KV head) one
+//                 (kept for batches of tokens: their K/V must all be in the
+//                 cache before any of them attends).
+//  k_attn         split-K flash decode: per (key slice, KV head) one
 //                 workgroup scores its G = H/HKV query heads against 64-key
-//                 tiles and keeps an online softmax (attn.glsl:54-162).
-//  k_attn_merge   O = sum_s e^(m_s-M) O_s / sum_s e^(m_s-M) l_s
-//                 (attn_merge.comp:18-47), written as fp32 and as the Act of
-//                 the output projection.
+//                 tiles with an online softmax (attn.glsl:54-162); for one
+//                 decode token it also does that token's RoPE and q8 append,
+//                 and the last workgroup per KV head merges the splits
+//                 (attn_merge.comp:18-47).
 //
 // Cache layout per layer: K8/V8 int8 [seq][kv_head][slot][head_dim] and
 // Ks/Vs f16 [seq][kv_head][slot][head_dim/32]: one KV head's keys are
@@ -95,53 +97,163 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float *__restrict__ qkv, i
 }
 
 // ---------------------------------------------------------------------------
-// Split-K flash decode. grid (n_split, HKV, B), 256 threads. Query b reads
-// keys [0, n_keys[b]) of sequence b (kv_per_batch), or of the one sequence
-// keys [0, n_keys[0] + b + 1) (a batch of consecutive positions starting at
-// n_keys[0]). Writes the unnormalised partial (sum p*v, m, l) per
-// (b, split, head) to part.
+// Split-K flash decode with the token's own preparation and the merge fused
+// in. grid (n_split, HKV, B), 256 threads; query b is at position nk - 1
+// and reads keys [0, nk):
+//   nk = n_keys[b] (kv_per_batch: B independent caches), or
+//   nk = n_keys[0] + b + 1 (one cache, a batch of consecutive positions).
+// 1. The G query heads of this KV head: q (+ bias, per-head norm, RoPE
+//    when `rope`) -> LDS.
+// 2. `append` (B == 1): the workgroup whose key slice holds the new key
+//    rounds that token's K (RoPE'd) and V to q8, stores them at their slot,
+//    and keeps a copy in LDS that it reads instead of the cache.
+// 3. 64-key tiles: scores (4 lanes per key), online softmax per head, p*v.
+// 4. The unnormalised partial (sum p*v, m, l) per head goes to `part`; the
+//    last workgroup of a (b, KV head) to finish (an atomic counter, reset by
+//    that workgroup for the next launch) merges the splits:
+//    O = sum_s e^(m_s - M) O_s / sum_s e^(m_s - M) l_s (attn_merge.comp:18-47).
 // ---------------------------------------------------------------------------
+struct AttnArgs {
+    const float *q;  // query rows [B][q_stride]; with rope: raw q, k, v rows of each token
+    int64_t q_stride;
+    const float *bias, *q_norm, *k_norm;
+    float eps;
+    const float2 *rope_cs;
+    int n_rot, neox, rope, append;
+    KvLayer kv;
+    int kv_per_batch, n_ctx, H, HKV;
+    const int32_t *n_keys;
+    float scale;
+    float *part;    // [B][n_split][H][HD + 2]
+    int *counters;  // [B * HKV], zero between launches
+    float *out;     // [B][H * HD]
+};
+
+__device__ inline void rope_inplace(float *v, int n_rot, int neox, const float2 *cs, int i) {
+    const int a = neox ? i : 2 * i, b = neox ? i + n_rot / 2 : 2 * i + 1;
+    float x0 = v[a], x1 = v[b];
+    rope_pair(x0, x1, cs[i].x, cs[i].y);
+    v[a] = x0;
+    v[b] = x1;
+}
+
 template <int HD, int G>
-__global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ q, KvLayer kv, int kv_per_batch,
-                                                    const int32_t *__restrict__ n_keys, int H, int HKV, int n_ctx,
-                                                    float scale, float *__restrict__ part) {
+__global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
     constexpr int TILE = 64, NQ = HD / 4, NPAIR = G * HD / 2, PPT = (NPAIR + 255) / 256;
     __shared__ float q_s[G][HD];
     __shared__ float p_s[G][TILE];
-    __shared__ float alpha_s[G], m_s[G], l_s[G];
+    __shared__ float alpha_s[G], m_s[G], l_s[G], red[G];
+    __shared__ float kv_s[2][HD];                 // the new token's K and V before rounding
+    __shared__ __align__(16) int8_t new8[2][HD];  // ... and after, as int8
+    __shared__ uint16_t new_sc[2][HD / 32];       // ... with their f16 scales
+    __shared__ int last;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, n_split = gridDim.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nk = kv_per_batch ? n_keys[b] : n_keys[0] + b + 1;
+    const int nk = a.kv_per_batch ? a.n_keys[b] : a.n_keys[0] + b + 1;
+    const int pq = nk - 1;  // the query's position
     int chunk = (nk + n_split - 1) / n_split;
     chunk = (chunk + TILE - 1) / TILE * TILE;
     const int p0 = split * chunk, p1 = min(nk, p0 + chunk);
-    const int seq = kv_per_batch ? b : 0;
-    const int64_t head_base = ((int64_t)seq * HKV + kvh) * n_ctx;  // slot index of key 0
-    const float *qb = q + ((int64_t)b * H + (int64_t)kvh * G) * HD;
-    for (int j = tid; j < G * HD; j += 256) q_s[j / HD][j % HD] = qb[j];
+    const int seq = a.kv_per_batch ? b : 0;
+    const int64_t head_base = ((int64_t)seq * a.HKV + kvh) * a.n_ctx;  // slot of key 0
+    const float *row = a.q + (int64_t)b * a.q_stride;
+    const bool has_new = a.append && pq >= p0 && pq < p1;
+
+    // 1. Query heads (and the new K/V rows) into LDS.
+    for (int j = tid; j < G * HD; j += 256) {
+        const int64_t e = (int64_t)(kvh * G + j / HD) * HD + j % HD;
+        q_s[j / HD][j % HD] = row[e] + (a.rope && a.bias ? a.bias[e] : 0.f);
+    }
+    if (has_new) {
+        for (int j = tid; j < 2 * HD; j += 256) {
+            const int64_t e = (int64_t)((j < HD ? a.H : a.H + a.HKV) + kvh) * HD + j % HD;
+            kv_s[j / HD][j % HD] = row[e] + (a.bias ? a.bias[e] : 0.f);
+        }
+    }
     if (tid < G) {
         m_s[tid] = -INFINITY;
         l_s[tid] = 0.f;
     }
+    __syncthreads();
+    if (a.rope) {
+        // Per-head RMSNorm (qwen3's q_norm / k_norm), then RoPE.
+        if (a.q_norm || (has_new && a.k_norm)) {
+            for (int g = wave; g < G + 1; g += 4) {
+                const float *nw = g < G ? a.q_norm : (has_new ? a.k_norm : nullptr);
+                if (!nw) continue;
+                float *v = g < G ? q_s[g] : kv_s[0];
+                float ss = 0.f;
+                for (int j = lane; j < HD; j += 64) ss += v[j] * v[j];
+                ss = wave_sum(ss);
+                const float sc = 1.0f / sqrtf(ss / (float)HD + a.eps);
+                for (int j = lane; j < HD; j += 64) v[j] = v[j] * sc * nw[j];
+            }
+            __syncthreads();
+        }
+        const float2 *cs = a.rope_cs + (int64_t)pq * (a.n_rot / 2);
+        for (int j = tid; j < (G + 1) * (HD / 2); j += 256) {
+            const int g = j / (HD / 2), i = j % (HD / 2);
+            if (i >= a.n_rot / 2) continue;
+            if (g < G) rope_inplace(q_s[g], a.n_rot, a.neox, cs, i);
+            else if (has_new) rope_inplace(kv_s[0], a.n_rot, a.neox, cs, i);
+        }
+        __syncthreads();
+    }
+    if (has_new && tid < 128) {
+        // q8 (engine/src/cpu_backend.cpp:78-90): per 32 values sc = f16(amax / 127),
+        // q = clamp(rint(v / sc), +-127). Wave 0 rounds K, wave 1 V, a pair per lane.
+        const int which = tid >> 6, i = tid & 63;
+        if (2 * i < HD) {
+            const float a0 = kv_s[which][2 * i], a1 = kv_s[which][2 * i + 1];
+            float amax = fmaxf(fabsf(a0), fabsf(a1));
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+            const uint16_t sh = f2h(amax / 127.0f);
+            const float sc = h2f(sh);
+            int q0 = 0, q1 = 0;
+            if (sc > 0.f) {
+                q0 = (int)fminf(127.f, fmaxf(-127.f, rintf(a0 / sc)));
+                q1 = (int)fminf(127.f, fmaxf(-127.f, rintf(a1 / sc)));
+            }
+            const uint16_t packed = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
+            const int64_t slot = head_base + pq;
+            *(uint16_t *)(new8[which] + 2 * i) = packed;
+            *(uint16_t *)((which ? a.kv.v : a.kv.k) + slot * HD + 2 * i) = packed;
+            if ((i & 15) == 0) {
+                new_sc[which][i / 16] = sh;
+                (which ? a.kv.vs : a.kv.ks)[slot * (HD / 32) + i / 16] = sh;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 3. Tiles of 64 keys.
     float o[PPT][2];
 #pragma unroll
     for (int k = 0; k < PPT; k++) o[k][0] = o[k][1] = 0.f;
-    __syncthreads();
-
     for (int t0 = p0; t0 < p1; t0 += TILE) {
-        // Scores: 4 lanes per key, NQ dims each.
-        {
+        {   // Scores: 4 lanes per key, NQ dims each.
             const int kk = tid >> 2, qq = tid & 3, p = t0 + kk;
             float acc[G];
 #pragma unroll
             for (int g = 0; g < G; g++) acc[g] = 0.f;
             if (p < p1) {
-                const int8_t *kp = kv.k + (head_base + p) * HD + qq * NQ;
-                const float ks = h2f(kv.ks[(head_base + p) * (HD / 32) + (qq * NQ) / 32]);
+                const bool mine = has_new && p == pq;
+                uint4 w[NQ / 16];
+                float ks;
+                if (mine) {
+#pragma unroll
+                    for (int c = 0; c < NQ / 16; c++) w[c] = *(const uint4 *)(new8[0] + qq * NQ + 16 * c);
+                    ks = h2f(new_sc[0][(qq * NQ) / 32]);
+                } else {
+                    const int8_t *kp = a.kv.k + (head_base + p) * HD + qq * NQ;
+#pragma unroll
+                    for (int c = 0; c < NQ / 16; c++) w[c] = *(const uint4 *)(kp + 16 * c);
+                    ks = h2f(a.kv.ks[(head_base + p) * (HD / 32) + (qq * NQ) / 32]);
+                }
 #pragma unroll
                 for (int c = 0; c < NQ / 16; c++) {
-                    const uint4 w = *(const uint4 *)(kp + 16 * c);
-                    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+                    const uint32_t ws[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
 #pragma unroll
                     for (int e = 0; e < 16; e++) {
                         const float kf = (float)(int8_t)((ws[e >> 2] >> (8 * (e & 3))) & 0xff) * ks;
@@ -158,17 +270,17 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ q,
             }
             if (qq == 0) {
 #pragma unroll
-                for (int g = 0; g < G; g++) p_s[g][kk] = p < p1 ? acc[g] * scale : -INFINITY;
+                for (int g = 0; g < G; g++) p_s[g][kk] = p < p1 ? acc[g] * a.scale : -INFINITY;
             }
         }
         __syncthreads();
         // Online softmax per head: wave w takes heads w, w+4.
         for (int g = wave; g < G; g += 4) {
-            const float s = p_s[g][lane];
-            const float mt = wave_max(s);
+            const float sv = p_s[g][lane];
+            const float mt = wave_max(sv);
             const float mo = m_s[g];
             const float mn = fmaxf(mo, mt);
-            const float p = s == -INFINITY ? 0.f : expf(s - mn);
+            const float p = sv == -INFINITY ? 0.f : expf(sv - mn);
             const float ls = wave_sum(p);
             p_s[g][lane] = p;
             if (lane == 0) {
@@ -179,8 +291,10 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ q,
             }
         }
         __syncthreads();
-        // o = o * alpha + sum_k p_k * v_k.
+        // o = o * alpha + sum_k p_k * v_k (the new key's V from LDS).
         const int nt = min(TILE, p1 - t0);
+        const bool new_here = has_new && pq >= t0 && pq < t0 + nt;
+        const int nc = new_here ? pq - t0 : nt;  // keys of this tile read from the cache
 #pragma unroll
         for (int k = 0; k < PPT; k++) {
             const int pp = tid + 256 * k;
@@ -188,11 +302,17 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ q,
                 const int g = (2 * pp) / HD, d = (2 * pp) % HD;
                 const float al = alpha_s[g];
                 float o0 = o[k][0] * al, o1 = o[k][1] * al;
-                const int8_t *vp = kv.v + (head_base + t0) * HD + d;
-                const uint16_t *vsp = kv.vs + (head_base + t0) * (HD / 32) + d / 32;
-                for (int kk = 0; kk < nt; kk++) {
+                const int8_t *vp = a.kv.v + (head_base + t0) * HD + d;
+                const uint16_t *vsp = a.kv.vs + (head_base + t0) * (HD / 32) + d / 32;
+                for (int kk = 0; kk < nc; kk++) {
                     const uint16_t v2 = *(const uint16_t *)(vp + (int64_t)kk * HD);
                     const float w = p_s[g][kk] * h2f(vsp[(int64_t)kk * (HD / 32)]);
+                    o0 += w * (float)(int8_t)(v2 & 0xff);
+                    o1 += w * (float)(int8_t)(v2 >> 8);
+                }
+                if (new_here) {
+                    const uint16_t v2 = *(const uint16_t *)(new8[1] + d);
+                    const float w = p_s[g][nc] * h2f(new_sc[1][d / 32]);
                     o0 += w * (float)(int8_t)(v2 & 0xff);
                     o1 += w * (float)(int8_t)(v2 >> 8);
                 }
@@ -202,42 +322,54 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ q,
         }
         __syncthreads();
     }
-    // Partial record per head: [HD values][m][l].
-    float *pb = part + (((int64_t)b * n_split + split) * H + (int64_t)kvh * G) * (HD + 2);
+
+    // 4. Partial record per head: [HD values][m][l]; the last workgroup merges.
+    const int64_t rec = HD + 2;
+    float *pb = a.part + (((int64_t)b * n_split + split) * a.H + (int64_t)kvh * G) * rec;
 #pragma unroll
     for (int k = 0; k < PPT; k++) {
         const int pp = tid + 256 * k;
         if (pp < NPAIR) {
             const int g = (2 * pp) / HD, d = (2 * pp) % HD;
-            pb[g * (HD + 2) + d] = o[k][0];
-            pb[g * (HD + 2) + d + 1] = o[k][1];
+            pb[g * rec + d] = o[k][0];
+            pb[g * rec + d + 1] = o[k][1];
         }
     }
     if (tid < G) {
-        pb[tid * (HD + 2) + HD] = m_s[tid];
-        pb[tid * (HD + 2) + HD + 1] = l_s[tid];
+        pb[tid * rec + HD] = m_s[tid];
+        pb[tid * rec + HD + 1] = l_s[tid];
     }
-}
-
-// grid (H, B), HD threads.
-__global__ __launch_bounds__(128) void k_attn_merge(const float *__restrict__ part, int n_split, int H, int HD,
-                                                    float *__restrict__ out, uint8_t *__restrict__ act) {
-    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-    const float *pb = part + ((int64_t)b * n_split * H + h) * (HD + 2);
-    const int64_t stride = (int64_t)H * (HD + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < n_split; s++) M = fmaxf(M, pb[s * stride + HD]);
-    float L = 0.f, acc = 0.f;
-    for (int s = 0; s < n_split; s++) {
-        const float m = pb[s * stride + HD];
-        const float w = m == -INFINITY ? 0.f : expf(m - M);
-        L += w * pb[s * stride + HD + 1];
-        acc += w * pb[s * stride + d];
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last = atomicAdd(a.counters + b * a.HKV + kvh, 1) == n_split - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    const float *p_all = a.part + ((int64_t)b * n_split * a.H + (int64_t)kvh * G) * rec;
+    const int64_t sstride = (int64_t)a.H * rec;
+    if (tid < G) {
+        float M = -INFINITY;
+        for (int sp = 0; sp < n_split; sp++) M = fmaxf(M, p_all[sp * sstride + tid * rec + HD]);
+        float L = 0.f;
+        for (int sp = 0; sp < n_split; sp++) {
+            const float m = p_all[sp * sstride + tid * rec + HD];
+            L += (m == -INFINITY ? 0.f : expf(m - M)) * p_all[sp * sstride + tid * rec + HD + 1];
+        }
+        m_s[tid] = M;
+        red[tid] = L;
     }
-    const float v = acc / L;
-    const int64_t n = (int64_t)H * HD;
-    if (out) out[(int64_t)b * n + (int64_t)h * HD + d] = v;
-    if (act) quant32(v, d & 31, act_view(act + (int64_t)b * act_bytes(n), n), ((int64_t)h * HD + d) / 32);
+    __syncthreads();
+    for (int j = tid; j < G * HD; j += 256) {
+        const int g = j / HD, d = j % HD;
+        const float M = m_s[g];
+        float acc = 0.f;
+        for (int sp = 0; sp < n_split; sp++) {
+            const float m = p_all[sp * sstride + g * rec + HD];
+            if (m != -INFINITY) acc += expf(m - M) * p_all[sp * sstride + g * rec + d];
+        }
+        a.out[(int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d] = acc / red[g];
+    }
+    if (tid == 0) a.counters[b * a.HKV + kvh] = 0;  // ready for the next launch
 }
 
 // K (which 0) or V (1) at positions [pos0, pos0 + n) dequantized to fp32
@@ -268,23 +400,21 @@ hipError_t launch_rope_kv(const float *qkv, int64_t qkv_stride, const float *bia
 }
 
 template <int HD>
-static hipError_t split_launch(int G, dim3 grid, const float *q, KvLayer kv, int kv_per_batch, const int32_t *n_keys,
-                               int H, int HKV, int n_ctx, float scale, float *part, hipStream_t s) {
-#define TS5_SPLIT(GG)                                                                                             \
-    case GG:                                                                                                      \
-        hipLaunchKernelGGL((k_attn_split<HD, GG>), grid, dim3(256), 0, s, q, kv, kv_per_batch, n_keys, H, HKV, \
-                           n_ctx, scale, part);                                                                   \
+static hipError_t attn_launch(int G, dim3 grid, const AttnArgs &a, hipStream_t s) {
+#define TS5_ATTN(GG)                                                      \
+    case GG:                                                              \
+        hipLaunchKernelGGL((k_attn<HD, GG>), grid, dim3(256), 0, s, a); \
         break;
     switch (G) {
-        TS5_SPLIT(1)
-        TS5_SPLIT(2)
-        TS5_SPLIT(4)
-        TS5_SPLIT(5)
-        TS5_SPLIT(7)
-        TS5_SPLIT(8)
+        TS5_ATTN(1)
+        TS5_ATTN(2)
+        TS5_ATTN(4)
+        TS5_ATTN(5)
+        TS5_ATTN(7)
+        TS5_ATTN(8)
     default: return hipErrorInvalidValue;
     }
-#undef TS5_SPLIT
+#undef TS5_ATTN
     return hipGetLastError();
 }
 
@@ -294,17 +424,15 @@ bool attn_supported(int H, int HKV, int HD) {
     return (HD == 64 || HD == 128) && (G == 1 || G == 2 || G == 4 || G == 5 || G == 7 || G == 8);
 }
 
-hipError_t launch_attn_decode(const float *q, KvLayer kv, int kv_per_batch, const int32_t *n_keys, int B, int H,
-                              int HKV, int HD, int n_ctx, int n_split, float scale, float *part, float *out, void *act,
-                              hipStream_t s) {
-    const dim3 grid(n_split, HKV, B);
-    hipError_t e = HD == 128 ? split_launch<128>(H / HKV, grid, q, kv, kv_per_batch, n_keys, H, HKV, n_ctx, scale,
-                                                 part, s)
-                             : split_launch<64>(H / HKV, grid, q, kv, kv_per_batch, n_keys, H, HKV, n_ctx, scale,
-                                                part, s);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_merge, dim3(H, B), dim3(HD), 0, s, part, n_split, H, HD, out, (uint8_t *)act);
-    return hipGetLastError();
+hipError_t launch_attn(const AttnIO &io, hipStream_t s) {
+    AttnArgs a{};
+    a.q = io.q, a.q_stride = io.q_stride, a.bias = io.bias, a.q_norm = io.q_norm, a.k_norm = io.k_norm;
+    a.eps = io.eps, a.rope_cs = (const float2 *)io.rope_cs, a.n_rot = io.n_rot, a.neox = io.neox;
+    a.rope = io.rope, a.append = io.append, a.kv = io.kv, a.kv_per_batch = io.kv_per_batch, a.n_ctx = io.n_ctx;
+    a.H = io.H, a.HKV = io.HKV, a.n_keys = io.n_keys, a.scale = io.scale, a.part = io.part;
+    a.counters = io.counters, a.out = io.out;
+    const dim3 grid(io.n_split, io.HKV, io.B);
+    return io.HD == 128 ? attn_launch<128>(io.H / io.HKV, grid, a, s) : attn_launch<64>(io.H / io.HKV, grid, a, s);
 }
 
 }  // namespace ts5hip

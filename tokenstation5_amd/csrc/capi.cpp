@@ -88,8 +88,11 @@ int ts5hip_init(int device, ts5hip_ctx **out) {
     c->n_cu = p.multiProcessorCount;
     c->arch = p.gcnArchName;
     c->hbm = (int64_t)p.totalGlobalMem;
+    set_cu_count(c->n_cu);
     if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess ||
-        (e = hipEventCreate(&c->ev0)) != hipSuccess || (e = hipEventCreate(&c->ev1)) != hipSuccess) {
+        (e = hipEventCreate(&c->ev0)) != hipSuccess || (e = hipEventCreate(&c->ev1)) != hipSuccess ||
+        (e = hipMalloc((void **)&c->counters, 4160 * sizeof(int))) != hipSuccess ||
+        (e = hipMemset(c->counters, 0, 4160 * sizeof(int))) != hipSuccess) {
         hip_fail(nullptr, e, "stream/event creation");
         ts5hip_destroy(c);
         return TS5HIP_ERR_HIP;
@@ -103,6 +106,7 @@ void ts5hip_destroy(ts5hip_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
     if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -219,22 +223,37 @@ int ts5hip_rmsnorm(ts5hip_ctx *ctx, const float *x, const float *w, float eps, i
     return TS5HIP_OK;
 }
 
-int ts5hip_matvec(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0, int64_t ne1, const void *act, float *y,
-                  int accumulate) {
-    if (!ctx || !w || !act || !y) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
+static int check_matrix(ts5hip_ctx *ctx, uint32_t type, int64_t ne0, int64_t ne1) {
     if (!ts5hip_supports_type(type) || ts5hip_weight_bytes(type, ne0, ne1) < 0)
         return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "matvec of type %u, %lld x %lld", type, (long long)ne1,
                     (long long)ne0);
-    TS5_HIP(ctx, launch_matvec(type, w, ne0, ne1, act, y, accumulate, ctx->stream));
+    if (ne0 > 16384) return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "input of %lld values (at most 16384)", (long long)ne0);
+    return TS5HIP_OK;
+}
+
+int ts5hip_matvec(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0, int64_t ne1, const float *x,
+                  const float *norm_w, float eps, float *y, int accumulate) {
+    if (!ctx || !w || !x || !y) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
+    if (int rc = check_matrix(ctx, type, ne0, ne1)) return rc;
+    TS5_HIP(ctx, launch_matvec(type, w, ne0, ne1, x, norm_w, eps, y, accumulate, ctx->stream));
     return TS5HIP_OK;
 }
 
 int ts5hip_matvec_glu(ts5hip_ctx *ctx, uint32_t type, const void *w_gate, const void *w_up, int64_t ne0, int64_t ne1,
-                      const void *act, float *y, void *act_out) {
-    if (!ctx || !w_gate || !w_up || !act || !act_out) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
-    if (!ts5hip_supports_type(type) || ts5hip_weight_bytes(type, ne0, ne1) < 0 || ne1 % 32)
-        return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "glu of type %u, %lld x %lld", type, (long long)ne1, (long long)ne0);
-    TS5_HIP(ctx, launch_matvec_glu(type, w_gate, w_up, ne0, ne1, act, y, act_out, ctx->stream));
+                      const float *x, const float *norm_w, float eps, float *y) {
+    if (!ctx || !w_gate || !w_up || !x || !y) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
+    if (int rc = check_matrix(ctx, type, ne0, ne1)) return rc;
+    TS5_HIP(ctx, launch_matvec_glu(type, w_gate, w_up, ne0, ne1, x, norm_w, eps, y, ctx->stream));
+    return TS5HIP_OK;
+}
+
+int ts5hip_matvec_argmax(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0, int64_t ne1, const float *x,
+                         const float *norm_w, float eps, float *y, int32_t *out_dev) {
+    if (!ctx || !w || !x || !y || !out_dev) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
+    if (int rc = check_matrix(ctx, type, ne0, ne1)) return rc;
+    if (int rc = ensure_scratch(ctx, matvec_argmax_scratch_bytes())) return rc;
+    TS5_HIP(ctx, launch_matvec_argmax(type, w, ne0, ne1, x, norm_w, eps, y, ctx->scratch, ctx->counters + 4096,
+                                      out_dev, nullptr, nullptr, ctx->stream));
     return TS5HIP_OK;
 }
 
@@ -265,18 +284,21 @@ int ts5hip_rope_kv_append(ts5hip_ctx *ctx, const float *qkv, int ntok, const int
 
 int ts5hip_attn_decode(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n_head_kv, int head_dim,
                        const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx,
-                       const int32_t *n_keys_dev, int kv_per_batch, float scale, int n_split, float *out,
-                       void *act_out) {
-    if (!ctx || !q || !k8 || !ks || !v8 || !vs || !n_keys_dev) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
+                       const int32_t *n_keys_dev, int kv_per_batch, float scale, int n_split, float *out) {
+    if (!ctx || !q || !k8 || !ks || !v8 || !vs || !n_keys_dev || !out) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
     if (B <= 0 || n_ctx <= 0 || !attn_supported(n_head, n_head_kv, head_dim))
         return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "attention for %d/%d heads of %d", n_head, n_head_kv, head_dim);
+    if (B * n_head_kv > 4096) return fail(ctx, TS5HIP_ERR_ARG, "batch of %d x %d KV heads", B, n_head_kv);
     if (n_split <= 0) n_split = attn_splits(B, n_head_kv);
     if (n_split > 1024) return fail(ctx, TS5HIP_ERR_ARG, "n_split %d", n_split);
-    const size_t part = attn_partial_bytes(B, n_split, n_head, head_dim);
-    if (int rc = ensure_scratch(ctx, part)) return rc;
-    const KvLayer kv{(int8_t *)k8, (uint16_t *)ks, (int8_t *)v8, (uint16_t *)vs};
-    TS5_HIP(ctx, launch_attn_decode(q, kv, kv_per_batch, n_keys_dev, B, n_head, n_head_kv, head_dim, n_ctx, n_split,
-                                    scale, (float *)ctx->scratch, out, act_out, ctx->stream));
+    if (int rc = ensure_scratch(ctx, attn_partial_bytes(B, n_split, n_head, head_dim))) return rc;
+    AttnIO io{};
+    io.q = q, io.q_stride = (int64_t)n_head * head_dim, io.rope = 0, io.append = 0;
+    io.kv = KvLayer{(int8_t *)k8, (uint16_t *)ks, (int8_t *)v8, (uint16_t *)vs};
+    io.kv_per_batch = kv_per_batch, io.n_ctx = n_ctx, io.n_keys = n_keys_dev;
+    io.B = B, io.H = n_head, io.HKV = n_head_kv, io.HD = head_dim, io.n_split = n_split, io.scale = scale;
+    io.part = (float *)ctx->scratch, io.counters = ctx->counters, io.out = out;
+    TS5_HIP(ctx, launch_attn(io, ctx->stream));
     return TS5HIP_OK;
 }
 

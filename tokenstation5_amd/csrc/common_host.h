@@ -49,9 +49,9 @@ inline void rope_table_host(int n_rot, int n_pos, float base, float scale, const
     }
 }
 
-// Split count of the flash decode: about 512 workgroups in all.
-inline int attn_splits(int B, int n_head_kv) {
-    const int s = (512 + B * n_head_kv - 1) / (B * n_head_kv);
+// Split count of the flash decode: about `target` workgroups in all.
+inline int attn_splits(int B, int n_head_kv, int target = 512) {
+    const int s = (target + B * n_head_kv - 1) / (B * n_head_kv);
     return s < 1 ? 1 : (s > 64 ? 64 : s);
 }
 inline size_t attn_partial_bytes(int B, int n_split, int H, int HD) {

@@ -29,11 +29,19 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int 
 hipError_t launch_act_quant(const float *x, int64_t xstride, const float *w, float eps, int n, int ntok, void *act,
                             hipStream_t s);
 
-// matvec.hip
-hipError_t launch_matvec(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const void *act, float *y, int add,
-                         hipStream_t s);
-hipError_t launch_matvec_glu(uint32_t t, const void *wg, const void *wu, int64_t ne0, int64_t ne1, const void *act,
-                             float *y, void *act_out, hipStream_t s);
+// matvec.hip: y (=|+=) W x for fp32 x, rms-normalised by norm_w first when given.
+void set_cu_count(int n);
+hipError_t launch_matvec(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const float *x, const float *norm_w,
+                         float eps, float *y, int add, hipStream_t s);
+// y = silu(Wg x) * (Wu x).
+hipError_t launch_matvec_glu(uint32_t t, const void *wg, const void *wu, int64_t ne0, int64_t ne1, const float *x,
+                             const float *norm_w, float eps, float *y, hipStream_t s);
+// y = W x and out[0] = the first argmax of y; with seq: seq[*pos + 1] = it, ++*pos.
+// scratch: matvec_argmax_scratch_bytes(); *counter zero before (and after) the launch.
+size_t matvec_argmax_scratch_bytes();
+hipError_t launch_matvec_argmax(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const float *x,
+                                const float *norm_w, float eps, float *y, void *scratch, int *counter, int32_t *out,
+                                int32_t *seq, int32_t *pos, hipStream_t s);
 
 // attention.hip
 hipError_t launch_rope_kv(const float *qkv, int64_t qkv_stride, const float *bias, const float *q_norm,
@@ -41,10 +49,27 @@ hipError_t launch_rope_kv(const float *qkv, int64_t qkv_stride, const float *bia
                           const int32_t *pos0, int H, int HKV, int HD, int n_ctx, int ntok, float *q_out, KvLayer kv,
                           hipStream_t s);
 bool attn_supported(int H, int HKV, int HD);
-hipError_t launch_attn_decode(const float *q, KvLayer kv, int kv_per_batch, const int32_t *n_keys, int B, int H,
-                              int HKV, int HD, int n_ctx, int n_split, float scale, float *part, float *out, void *act,
-                              hipStream_t s);
-
+// Flash decode (attention.hip: k_attn). q rows of B queries; with rope each
+// row holds the token's raw q, k, v ((H + 2 HKV) HD values), and q (with
+// append, B == 1, also the token's K/V) gets bias / norm / RoPE here.
+struct AttnIO {
+    const float *q;
+    int64_t q_stride;
+    int rope, append;
+    const float *bias, *q_norm, *k_norm;
+    float eps;
+    const float *rope_cs;
+    int n_rot, neox;
+    KvLayer kv;
+    int kv_per_batch, n_ctx;
+    const int32_t *n_keys;
+    int B, H, HKV, HD, n_split;
+    float scale;
+    float *part;    // B * n_split * H * (HD + 2) floats
+    int *counters;  // B * HKV ints, zero before the first launch (kept zero after)
+    float *out;     // [B][H * HD]
+};
+hipError_t launch_attn(const AttnIO &io, hipStream_t s);
 hipError_t launch_kv_read(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, float *out, hipStream_t s);
 
 // sample.hip

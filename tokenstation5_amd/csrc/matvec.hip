@@ -1,28 +1,34 @@
-// One-token k-quant matvecs y = W x for Q4_K, Q6_K and Q8_0 weights, and the
-// fused gate/up + SiLU variant, against a quantized activation (Act).
+// One-token k-quant matvecs y = W x for Q4_K, Q6_K and Q8_0 weights: plain,
+// accumulating into a residual, fused gate/up + SiLU, and the output head with
+// a fused greedy argmax.
 //
 // The reference computes y[r] = sum_i deq(W[r,i]) * x[i] with fp64
 // accumulation (engine/src/cpu_backend.cpp:18-37); its GPU path reads 8
 // lanes per Q4_K super-block with 16-byte loads (mv16_q4_k.glsl:64-113).
-// Here the weights stay packed in registers: each lane takes whole 32-value
-// sub-blocks, multiplies the raw quants with the activation's two int8 planes
-// on v_dot4_i32_i8 (exact int32), and applies the block scales once per
-// sub-block in fp32:
-//   Q4_K: y += d*sc*(xs*sum q*x16) - dmin*m*(sum x)      (quants.cpp:140-157)
-//   Q6_K: y += d*sc*xs*(sum q*x16 - 32*sum x16)          (quants.cpp:179-202)
-//   Q8_0: y += d*xs*(sum q*x16)                          (quants.cpp:133-139)
-// Bandwidth-bound: every weight byte is read once with dwordx4 loads; the
-// activation (<= 36 KB) is re-read from L2 by every wave and reused across
-// the R rows a wave owns. No MFMA.
+// Here:
+//  * Each workgroup first turns the fp32 input (rms-normalised when a norm
+//    weight is given, engine/src/cpu_backend.cpp:48-53) into the quantized
+//    activation of common.h in LDS: x16 = 256*hi + lo per value, a scale per
+//    32. The weights are the only HBM stream; the input is read from L2.
+//  * Weights stay packed in registers. A lane takes whole 32-value
+//    sub-blocks, multiplies raw quants with the activation's two int8 planes
+//    on v_dot4_i32_i8 (exact int32) and applies the block scales once per
+//    sub-block in fp32:
+//      Q4_K: y += d*sc*(xs*sum q*x16) - dmin*m*(sum x)   (quants.cpp:140-157)
+//      Q6_K: y += d*sc*xs*(sum q*x16 - 32*sum x16)       (quants.cpp:179-202)
+//      Q8_0: y += d*xs*(sum q*x16)                       (quants.cpp:133-139)
+//  * Persistent row groups: a workgroup walks its groups (R rows per wave)
+//    as a flat sequence of steps (one 64-lane sweep of 64/LPB blocks each)
+//    and always has the next step's weight loads in flight while it computes
+//    the current one. Every weight byte is read once with dwordx4 loads.
+// Bandwidth-bound: no MFMA.
+#include <climits>
+
 #include "common.h"
 #include "kernels.h"
 
 namespace ts5hip {
 
-// ---------------------------------------------------------------------------
-// Formats. Each lane owns `sub` (0..LPB-1) of every block it visits; a wave
-// covers BPI = 64 / LPB consecutive blocks of a row per iteration.
-// ---------------------------------------------------------------------------
 struct WPtr {
     const uint8_t *body;     // blocks (Q4_K: whole blocks; Q6_K/Q8_0: bodies)
     const uint16_t *dscale;  // f16 block scales of split layouts
@@ -37,12 +43,17 @@ __device__ inline WPtr wptr(uint32_t t, const void *w, int64_t nblocks) {
 
 __device__ inline uint4 ld16(const void *p) { return *(const uint4 *)p; }
 
+// ---------------------------------------------------------------------------
+// Formats. Each lane owns `sub` (0..LPB-1) of every block it visits; a wave
+// covers BPI = 64 / LPB consecutive blocks of a row per step.
+// ---------------------------------------------------------------------------
+
 // Q4_K: 4 lanes per block, lane `sub` = nibble group g: sub-blocks 2g (low
 // nibbles) and 2g+1 (high nibbles), 64 values.
 struct Q4K {
     static constexpr int LPB = 4;
     struct X {
-        uint4 h[4], l[4];
+        uint32_t h0[8], h1[8], l0[8], l1[8];
         float s0, s1, m0, m1;
     };
     struct W {
@@ -51,10 +62,22 @@ struct Q4K {
     __device__ static X load_x(const CAct &x, int b, int sub) {
         X r;
         const int base = b * 256 + 64 * sub;
+        uint4 v[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            r.h[k] = ld16(x.hi + base + 16 * k);
-            r.l[k] = ld16(x.lo + base + 16 * k);
+        for (int k = 0; k < 4; k++) v[k] = ld16(x.hi + base + 16 * k);
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            r.h0[4 * k] = v[k].x, r.h0[4 * k + 1] = v[k].y, r.h0[4 * k + 2] = v[k].z, r.h0[4 * k + 3] = v[k].w;
+            r.h1[4 * k] = v[k + 2].x, r.h1[4 * k + 1] = v[k + 2].y, r.h1[4 * k + 2] = v[k + 2].z,
+                     r.h1[4 * k + 3] = v[k + 2].w;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = ld16(x.lo + base + 16 * k);
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            r.l0[4 * k] = v[k].x, r.l0[4 * k + 1] = v[k].y, r.l0[4 * k + 2] = v[k].z, r.l0[4 * k + 3] = v[k].w;
+            r.l1[4 * k] = v[k + 2].x, r.l1[4 * k + 1] = v[k + 2].y, r.l1[4 * k + 2] = v[k + 2].z,
+                     r.l1[4 * k + 3] = v[k + 2].w;
         }
         const int s = b * 8 + 2 * sub;
         r.s0 = x.scale[s];
@@ -73,18 +96,14 @@ struct Q4K {
     }
     __device__ static float dot(const W &w, const X &x, int sub) {
         const uint32_t q[8] = {w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w};
-        const uint32_t xh0[8] = {x.h[0].x, x.h[0].y, x.h[0].z, x.h[0].w, x.h[1].x, x.h[1].y, x.h[1].z, x.h[1].w};
-        const uint32_t xh1[8] = {x.h[2].x, x.h[2].y, x.h[2].z, x.h[2].w, x.h[3].x, x.h[3].y, x.h[3].z, x.h[3].w};
-        const uint32_t xl0[8] = {x.l[0].x, x.l[0].y, x.l[0].z, x.l[0].w, x.l[1].x, x.l[1].y, x.l[1].z, x.l[1].w};
-        const uint32_t xl1[8] = {x.l[2].x, x.l[2].y, x.l[2].z, x.l[2].w, x.l[3].x, x.l[3].y, x.l[3].z, x.l[3].w};
         int ah0 = 0, al0 = 0, ah1 = 0, al1 = 0;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const int lo = (int)(q[k] & 0x0F0F0F0Fu), hi = (int)((q[k] >> 4) & 0x0F0F0F0Fu);
-            ah0 = dot4(lo, (int)xh0[k], ah0);
-            al0 = dot4(lo, (int)xl0[k], al0);
-            ah1 = dot4(hi, (int)xh1[k], ah1);
-            al1 = dot4(hi, (int)xl1[k], al1);
+            ah0 = dot4(lo, (int)x.h0[k], ah0);
+            al0 = dot4(lo, (int)x.l0[k], al0);
+            ah1 = dot4(hi, (int)x.h1[k], ah1);
+            al1 = dot4(hi, (int)x.l1[k], al1);
         }
         int sc0, m0, sc1, m1;
         kq_scale_min(2 * sub, w.hdr.y, w.hdr.z, w.hdr.w, sc0, m0);
@@ -210,129 +229,315 @@ struct Q80 {
 };
 
 // ---------------------------------------------------------------------------
-// y[r] (=|+=) W[r] . x for the R rows of each wave. The last wave's surplus
-// rows re-read the final row (in bounds) and are not written.
+// The activation prologue: x (n values, optionally rms-normalised by norm_w)
+// -> Act in LDS. One thread per 32-value sub-block.
 // ---------------------------------------------------------------------------
-enum { EPI_STORE = 0, EPI_ADD = 1 };
-
-template <class F, int R>
-__device__ inline void mv_rows(const WPtr &w, int64_t row0, int64_t nrows, int nb, const CAct &x, float (&acc)[R]) {
-    constexpr int BPI = WAVE / F::LPB;
-    const int lane = threadIdx.x & 63, bsub = lane / F::LPB, sub = lane % F::LPB;
+__device__ inline void quant_group_lds(const float *v, const Act &a, int g) {
+    float amax = 0.f, s = 0.f;
 #pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = 0.f;
-    for (int b = bsub; b < nb; b += BPI) {
-        const typename F::X xf = F::load_x(x, b, sub);
-        typename F::W wf[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) wf[r] = F::load_w(w, min(row0 + r, nrows - 1), nb, b, sub);
-#pragma unroll
-        for (int r = 0; r < R; r++) acc[r] += F::dot(wf[r], xf, sub);
+    for (int i = 0; i < 32; i++) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        s += v[i];
     }
+    const float inv = amax > 0.f ? 16383.0f / amax : 0.f;
+    uint32_t hw[8], lw[8];
+    int is0 = 0, is1 = 0;
 #pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+    for (int k = 0; k < 8; k++) {
+        uint32_t h = 0, l = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int i = 4 * k + e;
+            const int x16 = max(-16383, min(16383, (int)rintf(v[i] * inv)));
+            const int lo = (int)(int8_t)(x16 & 255);
+            const int hi = (x16 - lo) >> 8;
+            h |= (uint32_t)(hi & 255) << (8 * e);
+            l |= (uint32_t)(lo & 255) << (8 * e);
+            if (i < 16) is0 += x16;
+            else is1 += x16;
+        }
+        hw[k] = h, lw[k] = l;
+    }
+    uint4 *ph = (uint4 *)(a.hi + 32 * g), *pl = (uint4 *)(a.lo + 32 * g);
+    ph[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    ph[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+    pl[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    pl[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+    a.scale[g] = amax / 16383.0f;
+    a.sum[g] = s;
+    a.isum[2 * g] = is0;
+    a.isum[2 * g + 1] = is1;
 }
 
-template <class F, int R, int WAVES, int EPI>
-__global__ __launch_bounds__(WAVES *WAVE) void k_mv(uint32_t t, const void *__restrict__ W, int64_t nrows, int nb,
-                                                    const uint8_t *__restrict__ actp, int n_in, float *__restrict__ y) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t row0 = ((int64_t)blockIdx.x * WAVES + wave) * R;
-    if (row0 >= nrows) return;
-    const WPtr w = wptr(t, W, (int64_t)nb * nrows);
-    const CAct x = cact_view(actp, n_in);
-    float acc[R];
-    mv_rows<F, R>(w, row0, nrows, nb, x, acc);
-    if (lane < R && row0 + lane < nrows) {
-        float v = acc[0];
+template <int NT>
+__device__ inline void build_act(const float *__restrict__ x, const float *__restrict__ norm_w, float eps, int n,
+                                 const Act &a, float *red) {
+    float s = 1.0f;
+    if (norm_w) {
+        float ss = 0.f;
+        for (int i = 4 * threadIdx.x; i < n; i += 4 * NT) {
+            const float4 v = *(const float4 *)(x + i);
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ss = wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        ss = 0.f;
 #pragma unroll
-        for (int r = 1; r < R; r++)
-            if (lane == r) v = acc[r];
-        if (EPI == EPI_ADD)
-            y[row0 + lane] += v;
-        else
-            y[row0 + lane] = v;
+        for (int w = 0; w < NT / 64; w++) ss += red[w];
+        s = 1.0f / sqrtf(ss / (float)n + eps);
     }
-}
-
-// Fused gate/up: out[r] = silu(gate[r] . x) * (up[r] . x) (the reference's
-// float expression g / (1 + exp(-g)) * u, engine/src/cpu_backend.cpp:260-261),
-// written as fp32 (optional) and as the Act of the next matvec (one 32-row
-// sub-block per workgroup, so R * WAVES == 32).
-template <class F, int R, int WAVES>
-__global__ __launch_bounds__(WAVES *WAVE) void k_mv_glu(uint32_t t, const void *__restrict__ Wg,
-                                                        const void *__restrict__ Wu, int64_t nrows, int nb,
-                                                        const uint8_t *__restrict__ actp, int n_in,
-                                                        float *__restrict__ y, uint8_t *__restrict__ act_out) {
-    static_assert(R * WAVES == 32, "one 32-row sub-block per workgroup");
-    __shared__ float outv[32];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t row0 = ((int64_t)blockIdx.x * WAVES + wave) * R;
-    const WPtr wg = wptr(t, Wg, (int64_t)nb * nrows), wu = wptr(t, Wu, (int64_t)nb * nrows);
-    const CAct x = cact_view(actp, n_in);
-    float g[R], u[R];
-    mv_rows<F, R>(wg, row0, nrows, nb, x, g);
-    mv_rows<F, R>(wu, row0, nrows, nb, x, u);
-    if (lane == 0) {
+    for (int g = threadIdx.x; g < n / 32; g += NT) {
+        float v[32];
 #pragma unroll
-        for (int r = 0; r < R; r++) outv[wave * R + r] = g[r] / (1.0f + expf(-g[r])) * u[r];
+        for (int k = 0; k < 8; k++) {
+            const float4 f = *(const float4 *)(x + 32 * g + 4 * k);
+            v[4 * k] = f.x, v[4 * k + 1] = f.y, v[4 * k + 2] = f.z, v[4 * k + 3] = f.w;
+        }
+        if (norm_w) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const float4 w = *(const float4 *)(norm_w + 32 * g + 4 * k);
+                v[4 * k] = v[4 * k] * s * w.x;
+                v[4 * k + 1] = v[4 * k + 1] * s * w.y;
+                v[4 * k + 2] = v[4 * k + 2] * s * w.z;
+                v[4 * k + 3] = v[4 * k + 3] * s * w.w;
+            }
+        }
+        quant_group_lds(v, a, g);
     }
     __syncthreads();
-    if (threadIdx.x < 32) {
-        const float v = outv[threadIdx.x];
-        const int64_t row = (int64_t)blockIdx.x * 32 + threadIdx.x;
-        if (y) y[row] = v;
-        quant32(v, threadIdx.x, act_view(act_out, nrows), blockIdx.x);
+}
+
+// ---------------------------------------------------------------------------
+// The persistent matvec.
+// ---------------------------------------------------------------------------
+enum { MV_STORE = 0, MV_ADD = 1, MV_GLU = 2, MV_ARGMAX = 3 };
+
+struct MvArgs {
+    uint32_t t;
+    const void *w, *w2;  // w2: the up projection of MV_GLU
+    int64_t nrows;
+    int nb, n_in;
+    const float *x, *norm_w;
+    float eps;
+    float *y;
+    // MV_ARGMAX: per-workgroup best (value, row), the last workgroup's counter,
+    // and where the winning id goes: out[0], and seq[*pos + 1] with ++*pos
+    // when seq is given.
+    float *best_v;
+    int *best_i, *counter;
+    int32_t *out, *seq, *pos;
+};
+
+template <class F, int R>
+__device__ inline void load_rows(const WPtr &w, int64_t row0, int64_t nrows, int nb, int b, int sub,
+                                 typename F::W (&wf)[R]) {
+    const int bb = min(b, nb - 1);  // lanes past the row's end re-read its last block (in bounds), not used
+#pragma unroll
+    for (int r = 0; r < R; r++) wf[r] = F::load_w(w, min(row0 + r, nrows - 1), nb, bb, sub);
+}
+
+template <class F, int R, int WAVES, int MODE>
+__global__ __launch_bounds__(WAVES *WAVE) void k_mv(MvArgs a) {
+    constexpr int NT = WAVES * WAVE, BPI = WAVE / F::LPB, NW = MODE == MV_GLU ? 2 : 1;
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ float red[NT / 64];
+    __shared__ float best_vs[WAVES];
+    __shared__ int best_is[WAVES];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, bsub = lane / F::LPB, sub = lane % F::LPB;
+    const int64_t rpg = (int64_t)R * WAVES;
+    const int64_t ngroups = (a.nrows + rpg - 1) / rpg;
+    const int spg = (a.nb + BPI - 1) / BPI;  // steps per row group
+    const int64_t nblocks = (int64_t)a.nb * a.nrows;
+    const WPtr w1 = wptr(a.t, a.w, nblocks), w2 = wptr(a.t, MODE == MV_GLU ? a.w2 : a.w, nblocks);
+    float best_v = -INFINITY;
+    int best_i = INT_MAX;
+
+    int64_t g = blockIdx.x;
+    int it = 0;
+    typename F::W cur[NW][R], nxt[NW][R];
+    if (g < ngroups) {
+        const int64_t row0 = g * rpg + (int64_t)wave * R;
+        load_rows<F, R>(w1, row0, a.nrows, a.nb, bsub, sub, cur[0]);
+        if (MODE == MV_GLU) load_rows<F, R>(w2, row0, a.nrows, a.nb, bsub, sub, cur[NW - 1]);
+    }
+    const Act xa = act_view(lds, a.n_in);
+    build_act<NT>(a.x, a.norm_w, a.eps, a.n_in, xa, red);
+    const CAct x{xa.hi, xa.lo, xa.scale, xa.sum, xa.isum};
+
+    float acc[NW][R];
+#pragma unroll
+    for (int k = 0; k < NW; k++)
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[k][r] = 0.f;
+    while (g < ngroups) {
+        int64_t gn = g;
+        int itn = it + 1;
+        if (itn == spg) itn = 0, gn = g + gridDim.x;
+        const bool more = gn < ngroups;
+        if (more) {
+            const int64_t row0n = gn * rpg + (int64_t)wave * R;
+            load_rows<F, R>(w1, row0n, a.nrows, a.nb, itn * BPI + bsub, sub, nxt[0]);
+            if (MODE == MV_GLU) load_rows<F, R>(w2, row0n, a.nrows, a.nb, itn * BPI + bsub, sub, nxt[NW - 1]);
+        }
+        const int b = it * BPI + bsub;
+        if (b < a.nb) {
+            const typename F::X xf = F::load_x(x, b, sub);
+#pragma unroll
+            for (int k = 0; k < NW; k++)
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[k][r] += F::dot(cur[k][r], xf, sub);
+        }
+        if (it == spg - 1) {
+            const int64_t row0 = g * rpg + (int64_t)wave * R;
+#pragma unroll
+            for (int k = 0; k < NW; k++)
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[k][r] = wave_sum(acc[k][r]);
+            if (lane < R && row0 + lane < a.nrows) {
+                float v = acc[0][0], u = acc[NW - 1][0];
+#pragma unroll
+                for (int r = 1; r < R; r++)
+                    if (lane == r) v = acc[0][r], u = acc[NW - 1][r];
+                const int64_t row = row0 + lane;
+                if (MODE == MV_ADD) {
+                    a.y[row] += v;
+                } else if (MODE == MV_GLU) {
+                    a.y[row] = v / (1.0f + expf(-v)) * u;  // engine/src/cpu_backend.cpp:260-261
+                } else {
+                    a.y[row] = v;
+                    if (MODE == MV_ARGMAX && (v > best_v || (v == best_v && row < best_i))) best_v = v, best_i = (int)row;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < NW; k++)
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[k][r] = 0.f;
+        }
+        if (!more) break;
+#pragma unroll
+        for (int k = 0; k < NW; k++)
+#pragma unroll
+            for (int r = 0; r < R; r++) cur[k][r] = nxt[k][r];
+        g = gn, it = itn;
+    }
+    if (MODE == MV_ARGMAX) {
+        // The first maximum wins (std::max_element): larger value, then lower row.
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float v = __shfl_xor(best_v, o, WAVE);
+            const int i = __shfl_xor(best_i, o, WAVE);
+            if (v > best_v || (v == best_v && i < best_i)) best_v = v, best_i = i;
+        }
+        if (lane == 0) best_vs[wave] = best_v, best_is[wave] = best_i;
+        __syncthreads();
+        __shared__ int last;
+        if (threadIdx.x == 0) {
+            for (int k = 1; k < WAVES; k++)
+                if (best_vs[k] > best_v || (best_vs[k] == best_v && best_is[k] < best_i)) best_v = best_vs[k], best_i = best_is[k];
+            a.best_v[blockIdx.x] = best_v;
+            a.best_i[blockIdx.x] = best_i;
+            __threadfence();
+            last = atomicAdd(a.counter, 1) == (int)gridDim.x - 1;
+        }
+        __syncthreads();
+        if (last) {
+            __threadfence();
+            best_v = -INFINITY, best_i = INT_MAX;
+            for (int k = threadIdx.x; k < (int)gridDim.x; k += NT) {
+                const float v = __hip_atomic_load(a.best_v + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const int i = __hip_atomic_load(a.best_i + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (v > best_v || (v == best_v && i < best_i)) best_v = v, best_i = i;
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float v = __shfl_xor(best_v, o, WAVE);
+                const int i = __shfl_xor(best_i, o, WAVE);
+                if (v > best_v || (v == best_v && i < best_i)) best_v = v, best_i = i;
+            }
+            __syncthreads();
+            if (lane == 0) best_vs[wave] = best_v, best_is[wave] = best_i;
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                for (int k = 1; k < WAVES; k++)
+                    if (best_vs[k] > best_v || (best_vs[k] == best_v && best_is[k] < best_i))
+                        best_v = best_vs[k], best_i = best_is[k];
+                if (best_i == INT_MAX) best_i = 0;  // every logit NaN
+                a.out[0] = best_i;
+                if (a.seq) {
+                    const int p = *a.pos;
+                    a.seq[p + 1] = best_i;
+                    *a.pos = p + 1;
+                }
+                *a.counter = 0;  // ready for the next launch (graph replays)
+            }
+        }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Launchers. Shapes are checked by the caller (capi.cpp).
+// Launch shapes. Rows per group = R * WAVES; the grid is capped at two
+// workgroups per CU, so large matrices loop over their groups with the next
+// step's weights in flight.
 // ---------------------------------------------------------------------------
-template <class F, int R, int WAVES>
-static hipError_t mv_launch(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const void *act, float *y, int add,
-                            hipStream_t s) {
-    const int nb = (int)(ne0 / block_values(t));
-    const int64_t rows_per_wg = (int64_t)R * WAVES;
-    const dim3 grid((unsigned)((ne1 + rows_per_wg - 1) / rows_per_wg));
-    if (add)
-        hipLaunchKernelGGL((k_mv<F, R, WAVES, EPI_ADD>), grid, dim3(WAVES * WAVE), 0, s, t, w, ne1, nb,
-                           (const uint8_t *)act, (int)ne0, y);
-    else
-        hipLaunchKernelGGL((k_mv<F, R, WAVES, EPI_STORE>), grid, dim3(WAVES * WAVE), 0, s, t, w, ne1, nb,
-                           (const uint8_t *)act, (int)ne0, y);
+static int g_n_cu = 256;
+void set_cu_count(int n) { g_n_cu = n > 0 ? n : 256; }
+
+template <class F, int R, int WAVES, int MODE>
+static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
+    const int64_t rpg = (int64_t)R * WAVES;
+    const int64_t ngroups = (a.nrows + rpg - 1) / rpg;
+    const int64_t cap = 2LL * g_n_cu;
+    const int64_t per = (ngroups + cap - 1) / cap;  // groups per workgroup
+    const unsigned grid = (unsigned)((ngroups + per - 1) / per);
+    hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE>), dim3(grid), dim3(WAVES * WAVE), act_bytes(a.n_in), s, a);
     return hipGetLastError();
 }
 
-hipError_t launch_matvec(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const void *act, float *y, int add,
-                         hipStream_t s) {
-    switch (t) {
-    case T_Q4_K: return mv_launch<Q4K, 4, 4>(t, w, ne0, ne1, act, y, add, s);
-    case T_Q6_K: return mv_launch<Q6K, 4, 4>(t, w, ne0, ne1, act, y, add, s);
-    case T_Q8_0: return mv_launch<Q80, 4, 4>(t, w, ne0, ne1, act, y, add, s);
+template <int MODE>
+static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
+    switch (a.t) {
+    case T_Q4_K: return MODE == MV_GLU ? mv_go<Q4K, 2, 4, MODE>(a, s) : mv_go<Q4K, 4, 4, MODE>(a, s);
+    case T_Q6_K: return MODE == MV_GLU ? mv_go<Q6K, 2, 4, MODE>(a, s) : mv_go<Q6K, 4, 4, MODE>(a, s);
+    case T_Q8_0: return MODE == MV_GLU ? mv_go<Q80, 2, 4, MODE>(a, s) : mv_go<Q80, 4, 4, MODE>(a, s);
     }
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_matvec_glu(uint32_t t, const void *wg, const void *wu, int64_t ne0, int64_t ne1, const void *act,
-                             float *y, void *act_out, hipStream_t s) {
-    const int nb = (int)(ne0 / block_values(t));
-    const dim3 grid((unsigned)(ne1 / 32));
-    switch (t) {
-    case T_Q4_K:
-        hipLaunchKernelGGL((k_mv_glu<Q4K, 4, 8>), grid, dim3(8 * WAVE), 0, s, t, wg, wu, ne1, nb, (const uint8_t *)act,
-                           (int)ne0, y, (uint8_t *)act_out);
-        return hipGetLastError();
-    case T_Q6_K:
-        hipLaunchKernelGGL((k_mv_glu<Q6K, 4, 8>), grid, dim3(8 * WAVE), 0, s, t, wg, wu, ne1, nb, (const uint8_t *)act,
-                           (int)ne0, y, (uint8_t *)act_out);
-        return hipGetLastError();
-    case T_Q8_0:
-        hipLaunchKernelGGL((k_mv_glu<Q80, 4, 8>), grid, dim3(8 * WAVE), 0, s, t, wg, wu, ne1, nb, (const uint8_t *)act,
-                           (int)ne0, y, (uint8_t *)act_out);
-        return hipGetLastError();
-    }
-    return hipErrorInvalidValue;
+static MvArgs mv_args(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const float *x, const float *norm_w,
+                      float eps, float *y) {
+    MvArgs a{};
+    a.t = t, a.w = w, a.w2 = nullptr, a.nrows = ne1, a.nb = (int)(ne0 / block_values(t)), a.n_in = (int)ne0;
+    a.x = x, a.norm_w = norm_w, a.eps = eps, a.y = y;
+    return a;
+}
+
+hipError_t launch_matvec(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const float *x, const float *norm_w,
+                         float eps, float *y, int add, hipStream_t s) {
+    const MvArgs a = mv_args(t, w, ne0, ne1, x, norm_w, eps, y);
+    return add ? mv_dispatch<MV_ADD>(a, s) : mv_dispatch<MV_STORE>(a, s);
+}
+
+hipError_t launch_matvec_glu(uint32_t t, const void *wg, const void *wu, int64_t ne0, int64_t ne1, const float *x,
+                             const float *norm_w, float eps, float *y, hipStream_t s) {
+    MvArgs a = mv_args(t, wg, ne0, ne1, x, norm_w, eps, y);
+    a.w2 = wu;
+    return mv_dispatch<MV_GLU>(a, s);
+}
+
+// Per-workgroup partials of the argmax epilogue: best values then best rows.
+size_t matvec_argmax_scratch_bytes() { return 8 * (size_t)(2 * g_n_cu + 64); }
+
+hipError_t launch_matvec_argmax(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const float *x,
+                                const float *norm_w, float eps, float *y, void *scratch, int *counter, int32_t *out,
+                                int32_t *seq, int32_t *pos, hipStream_t s) {
+    MvArgs a = mv_args(t, w, ne0, ne1, x, norm_w, eps, y);
+    a.counter = counter;
+    a.best_v = (float *)scratch;
+    a.best_i = (int *)((uint8_t *)scratch + 4 * (size_t)(2 * g_n_cu + 64));
+    a.out = out, a.seq = seq, a.pos = pos;
+    return mv_dispatch<MV_ARGMAX>(a, s);
 }
 
 }  // namespace ts5hip

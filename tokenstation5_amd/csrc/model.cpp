@@ -60,8 +60,8 @@ struct ts5hip_model {
     float *rope_cs = nullptr;
     bool rope_ready = false;
     // Activations and scratch.
-    float *x = nullptr, *qkv = nullptr, *q_rot = nullptr, *logits = nullptr, *part = nullptr;
-    uint8_t *act_e = nullptr, *act_att = nullptr, *act_f = nullptr;
+    float *x = nullptr, *qkv = nullptr, *att = nullptr, *ffn = nullptr, *logits = nullptr, *part = nullptr;
+    int *counters = nullptr;  // [HKV] attention merges, [HKV] head argmax; zero between launches
     void *amax = nullptr, *topk = nullptr;
     float *topk_v = nullptr;
     int32_t *topk_i = nullptr;
@@ -73,6 +73,7 @@ struct ts5hip_model {
     int32_t *pinned_ids = nullptr;  // [n_ctx + 1]
     hipGraphExec_t graph[N_GRAPHS] = {nullptr, nullptr, nullptr};
     bool graphs_stale = true;
+    bool use_graphs = true;  // TS5HIP_GRAPHS=0: launch each token's kernels directly (profilers)
     // Profile (TS5HIP_PROFILE set): GPU time per forward call.
     bool profile = false;
     double prof_ms = 0;
@@ -308,9 +309,9 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
     TS5_HIP(ctx, launch_embed(m->tok_embd.type, m->tok_embd.d, E, hp.n_vocab, m->seq, m->state, 1, m->x, s));
     for (int l = 0; l < hp.n_layer; l++) {
         const LayerDev &L = m->layers[l];
-        TS5_HIP(ctx, launch_act_quant(m->x, E, (const float *)L.attn_norm.d, hp.rms_eps, E, 1, m->act_e, s));
+        const float *an = (const float *)L.attn_norm.d;
         if (L.in_qkv[0] && L.in_qkv[1] && L.in_qkv[2]) {
-            TS5_HIP(ctx, launch_matvec(L.qkv.type, L.qkv.d, E, QR, m->act_e, m->qkv, 0, s));
+            TS5_HIP(ctx, launch_matvec(L.qkv.type, L.qkv.d, E, QR, m->x, an, hp.rms_eps, m->qkv, 0, s));
         } else {
             // Rows kept in the fused buffer are a sub-tensor only for layouts
             // without a separate scale array (Q4_K); split layouts go per part.
@@ -321,41 +322,50 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
                     if (L.qkv.type == T_Q6_K || L.qkv.type == T_Q8_0)
                         return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "mixed q/k/v types with a split layout");
                     const SplitDst d = split_dst(L.qkv.type, E, QR, L.qkv.d, r0);
-                    TS5_HIP(ctx, launch_matvec(L.qkv.type, d.body, E, rows[p], m->act_e, m->qkv + r0, 0, s));
+                    TS5_HIP(ctx, launch_matvec(L.qkv.type, d.body, E, rows[p], m->x, an, hp.rms_eps, m->qkv + r0, 0, s));
                 } else {
-                    TS5_HIP(ctx, launch_matvec(L.part[p].type, L.part[p].d, E, rows[p], m->act_e, m->qkv + r0, 0, s));
+                    TS5_HIP(ctx, launch_matvec(L.part[p].type, L.part[p].d, E, rows[p], m->x, an, hp.rms_eps,
+                                               m->qkv + r0, 0, s));
                 }
                 r0 += rows[p];
             }
         }
-        const KvLayer kv = m->kv_layer(l);
-        TS5_HIP(ctx, launch_rope_kv(m->qkv, QR, m->has_bias[l] ? m->bias + (int64_t)l * QR : nullptr,
-                                    L.q_norm.set ? (const float *)L.q_norm.d : nullptr,
-                                    L.k_norm.set ? (const float *)L.k_norm.d : nullptr, hp.rms_eps, m->rope_cs,
-                                    hp.rope_dims, hp.rope_neox, m->state, H, HKV, HD, m->n_ctx, 1, m->q_rot, kv, s));
-        TS5_HIP(ctx, launch_attn_decode(m->q_rot, kv, 0, m->state, 1, H, HKV, HD, m->n_ctx, m->n_split, hp.attn_scale,
-                                        m->part, nullptr, m->act_att, s));
-        TS5_HIP(ctx, launch_matvec(L.wo.type, L.wo.d, (int64_t)H * HD, E, m->act_att, m->x, 1, s));
-        TS5_HIP(ctx, launch_act_quant(m->x, E, (const float *)L.ffn_norm.d, hp.rms_eps, E, 1, m->act_e, s));
-        TS5_HIP(ctx, launch_matvec_glu(L.gate.type, L.gate.d, L.up.d, E, F, m->act_e, nullptr, m->act_f, s));
-        TS5_HIP(ctx, launch_matvec(L.down.type, L.down.d, F, E, m->act_f, m->x, 1, s));
+        AttnIO io{};
+        io.q = m->qkv, io.q_stride = QR, io.rope = 1, io.append = 1;
+        io.bias = m->has_bias[l] ? m->bias + (int64_t)l * QR : nullptr;
+        io.q_norm = L.q_norm.set ? (const float *)L.q_norm.d : nullptr;
+        io.k_norm = L.k_norm.set ? (const float *)L.k_norm.d : nullptr;
+        io.eps = hp.rms_eps, io.rope_cs = m->rope_cs, io.n_rot = hp.rope_dims, io.neox = hp.rope_neox;
+        io.kv = m->kv_layer(l), io.kv_per_batch = 0, io.n_ctx = m->n_ctx, io.n_keys = m->state;
+        io.B = 1, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = m->n_split, io.scale = hp.attn_scale;
+        io.part = m->part, io.counters = m->counters, io.out = m->att;
+        TS5_HIP(ctx, launch_attn(io, s));
+        TS5_HIP(ctx, launch_matvec(L.wo.type, L.wo.d, (int64_t)H * HD, E, m->att, nullptr, 0.f, m->x, 1, s));
+        TS5_HIP(ctx, launch_matvec_glu(L.gate.type, L.gate.d, L.up.d, E, F, m->x, (const float *)L.ffn_norm.d,
+                                       hp.rms_eps, m->ffn, s));
+        TS5_HIP(ctx, launch_matvec(L.down.type, L.down.d, F, E, m->ffn, nullptr, 0.f, m->x, 1, s));
     }
     if (head) {
         const DevT &out = m->output.set ? m->output : m->tok_embd;
-        TS5_HIP(ctx, launch_act_quant(m->x, E, (const float *)m->out_norm.d, hp.rms_eps, E, 1, m->act_e, s));
-        TS5_HIP(ctx, launch_matvec(out.type, out.d, E, hp.n_vocab, m->act_e, m->logits, 0, s));
+        const float *on = (const float *)m->out_norm.d;
+        if (tail == 1) {
+            TS5_HIP(ctx, launch_matvec_argmax(out.type, out.d, E, hp.n_vocab, m->x, on, hp.rms_eps, m->logits, m->amax,
+                                              m->counters + HKV, m->state + 1, m->seq, m->state, s));
+            return TS5HIP_OK;
+        }
+        TS5_HIP(ctx, launch_matvec(out.type, out.d, E, hp.n_vocab, m->x, on, hp.rms_eps, m->logits, 0, s));
     }
-    if (tail == 1) {
-        TS5_HIP(ctx, launch_argmax(m->logits, hp.n_vocab, 1, m->amax, m->state + 1, m->seq, m->state, s));
-    } else {
-        TS5_HIP(ctx, launch_advance(m->state, s));
-    }
+    TS5_HIP(ctx, launch_advance(m->state, s));
     return TS5HIP_OK;
 }
 
 int build_graphs(ts5hip_model *m) {
     if (!m->graphs_stale) return TS5HIP_OK;
     if (int rc = check_complete(m)) return rc;
+    if (!m->use_graphs) {
+        m->graphs_stale = false;
+        return TS5HIP_OK;
+    }
     ts5hip_ctx *ctx = m->ctx;
     TS5_HIP(ctx, hipStreamSynchronize(ctx->stream));
     for (int g = 0; g < N_GRAPHS; g++) {
@@ -377,6 +387,13 @@ int build_graphs(ts5hip_model *m) {
         if (ei != hipSuccess) return hip_fail(ctx, ei, "hipGraphInstantiate");
     }
     m->graphs_stale = false;
+    return TS5HIP_OK;
+}
+
+// One token's kernels: a replay of the captured graph, or direct launches.
+int launch_token(ts5hip_model *m, int g) {
+    if (!m->use_graphs) return enqueue_token(m, g != G_KV, g == G_GREEDY ? 1 : 0);
+    TS5_HIP(m->ctx, hipGraphLaunch(m->graph[g], m->ctx->stream));
     return TS5HIP_OK;
 }
 
@@ -417,7 +434,7 @@ int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool wan
     const size_t row_bytes = (size_t)m->hp.n_vocab * 4;
     for (int t = 0; t < n; t++) {
         const bool lg = want_logits && (all || t == n - 1);
-        TS5_HIP(ctx, hipGraphLaunch(m->graph[lg ? G_LOGITS : G_KV], s));
+        if (int rc = launch_token(m, lg ? G_LOGITS : G_KV)) return rc;
         if (lg) {
             const int r = all ? t : 0;
             TS5_HIP(ctx, hipMemcpyAsync(m->dev_rows + (size_t)r * m->hp.n_vocab, m->logits, row_bytes,
@@ -460,9 +477,11 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
     m->kv_type = kv_type;
     m->layers.resize(hp->n_layer);
     m->has_bias.assign(hp->n_layer, false);
-    m->n_split = attn_splits(1, hp->n_head_kv);
+    m->n_split = attn_splits(1, hp->n_head_kv, 256);
     const char *prof = std::getenv("TS5HIP_PROFILE");
     m->profile = prof && *prof && std::strcmp(prof, "0") != 0;
+    const char *graphs = std::getenv("TS5HIP_GRAPHS");
+    m->use_graphs = !(graphs && std::strcmp(graphs, "0") == 0);
     const int64_t E = hp->n_embd, F = hp->n_ff, HD = hp->head_dim, H = hp->n_head, HKV = hp->n_head_kv;
     const int64_t kv_elems = (int64_t)hp->n_layer * HKV * n_ctx * HD;
     int rc = 0;
@@ -470,12 +489,11 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
         (rc = alloc_t(m, kv_elems / 32, &m->ks)) || (rc = alloc_t(m, kv_elems / 32, &m->vs)) ||
         (rc = alloc_t(m, (size_t)n_ctx * hp->rope_dims, &m->rope_cs)) ||
         (rc = alloc_t(m, (size_t)hp->n_layer * m->qkv_rows(), &m->bias)) || (rc = alloc_t(m, E, &m->x)) ||
-        (rc = alloc_t(m, m->qkv_rows(), &m->qkv)) || (rc = alloc_t(m, H * HD, &m->q_rot)) ||
-        (rc = alloc_t(m, hp->n_vocab, &m->logits)) ||
+        (rc = alloc_t(m, m->qkv_rows(), &m->qkv)) || (rc = alloc_t(m, H * HD, &m->att)) ||
+        (rc = alloc_t(m, F, &m->ffn)) || (rc = alloc_t(m, hp->n_vocab, &m->logits)) ||
         (rc = alloc_t(m, attn_partial_bytes(1, m->n_split, H, HD) / 4, &m->part)) ||
-        (rc = alloc_t(m, act_bytes(std::max(E, H * HD)), &m->act_e)) ||
-        (rc = alloc_t(m, act_bytes(H * HD), &m->act_att)) || (rc = alloc_t(m, act_bytes(F), &m->act_f)) ||
-        (rc = alloc(m, argmax_scratch_bytes(1), &m->amax)) || (rc = alloc(m, topk_scratch_bytes(), &m->topk)) ||
+        (rc = alloc_t(m, 2 * HKV + 64, &m->counters)) ||
+        (rc = alloc(m, matvec_argmax_scratch_bytes(), &m->amax)) || (rc = alloc(m, topk_scratch_bytes(), &m->topk)) ||
         (rc = alloc_t(m, 64, &m->topk_v)) || (rc = alloc_t(m, 64, &m->topk_i)) ||
         (rc = alloc_t(m, (size_t)n_ctx + 1, &m->seq)) || (rc = alloc_t(m, 4, &m->state))) {
         ts5hip_model_destroy(m);
@@ -484,6 +502,7 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
     hipError_t e;
     if ((e = hipMemsetAsync(m->bias, 0, (size_t)hp->n_layer * m->qkv_rows() * 4, ctx->stream)) != hipSuccess ||
         (e = hipMemsetAsync(m->seq, 0, ((size_t)n_ctx + 1) * 4, ctx->stream)) != hipSuccess ||
+        (e = hipMemsetAsync(m->counters, 0, (2 * (size_t)HKV + 64) * 4, ctx->stream)) != hipSuccess ||
         (e = hipMemsetAsync(m->k8, 0, kv_elems, ctx->stream)) != hipSuccess ||
         (e = hipMemsetAsync(m->v8, 0, kv_elems, ctx->stream)) != hipSuccess ||
         (e = hipMemsetAsync(m->ks, 0, kv_elems / 32 * 2, ctx->stream)) != hipSuccess ||
@@ -576,7 +595,8 @@ int ts5hip_generate_greedy(ts5hip_model *m, int32_t token, int pos, int n_steps,
     m->pinned_ids[1] = pos;
     TS5_HIP(ctx, hipMemcpyAsync(m->seq + pos, m->pinned_ids, 4, hipMemcpyHostToDevice, s));
     TS5_HIP(ctx, hipMemcpyAsync(m->state, m->pinned_ids + 1, 4, hipMemcpyHostToDevice, s));
-    for (int i = 0; i < n_steps; i++) TS5_HIP(ctx, hipGraphLaunch(m->graph[G_GREEDY], s));
+    for (int i = 0; i < n_steps; i++)
+        if (int rc = launch_token(m, G_GREEDY)) return rc;
     TS5_HIP(ctx, hipMemcpyAsync(m->pinned_ids, m->seq + pos + 1, (size_t)n_steps * 4, hipMemcpyDeviceToHost, s));
     TS5_HIP(ctx, hipStreamSynchronize(s));
     if (ids_out) std::memcpy(ids_out, m->pinned_ids, (size_t)n_steps * 4);

@@ -20,6 +20,8 @@ struct ts5hip_ctx {
     // grown on demand outside any graph capture.
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
+    // Zeroed once; kernels that count finished workgroups leave them zero.
+    int *counters = nullptr;  // [0, 4096): attention, [4096]: head argmax
 };
 
 namespace ts5hip {

@@ -49,13 +49,14 @@ _SIGS = {
     "ts5hip_act_bytes": (_i64, [_i64]),
     "ts5hip_act_quantize": (_i32, [_vp, _vp, _vp, _f32, _i64, _i32, _vp]),
     "ts5hip_rmsnorm": (_i32, [_vp, _vp, _vp, _f32, _i64, _i32, _vp]),
-    "ts5hip_matvec": (_i32, [_vp, _u32, _vp, _i64, _i64, _vp, _vp, _i32]),
-    "ts5hip_matvec_glu": (_i32, [_vp, _u32, _vp, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "ts5hip_matvec": (_i32, [_vp, _u32, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _i32]),
+    "ts5hip_matvec_glu": (_i32, [_vp, _u32, _vp, _vp, _i64, _i64, _vp, _vp, _f32, _vp]),
+    "ts5hip_matvec_argmax": (_i32, [_vp, _u32, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _vp]),
     "ts5hip_rope_table": (_i32, [_vp, _i32, _i32, _f32, _f32, _vp, _vp]),
     "ts5hip_rope_kv_append": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp,
                                      _f32, _vp, _vp, _vp, _vp, _vp]),
     "ts5hip_attn_decode": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _f32, _i32,
-                                  _vp, _vp]),
+                                  _vp]),
     "ts5hip_argmax": (_i32, [_vp, _vp, _i32, _i32, _vp]),
     "ts5hip_topk": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp]),
     "ts5hip_sampler_new": (_vp, [_u64]),
@@ -229,12 +230,17 @@ class Context:
     def rmsnorm(self, x, w, eps, n, ntok, y):
         self.check(lib().ts5hip_rmsnorm(self.h, _ptr(x), _ptr(w), eps, n, ntok, _ptr(y)))
 
-    def matvec(self, t, w, ne0, ne1, act, y, accumulate=False):
-        self.check(lib().ts5hip_matvec(self.h, t, _ptr(w), ne0, ne1, _ptr(act), _ptr(y), int(accumulate)))
+    def matvec(self, t, w, ne0, ne1, x, y, norm_w=None, eps=0.0, accumulate=False):
+        self.check(lib().ts5hip_matvec(self.h, t, _ptr(w), ne0, ne1, _ptr(x), _ptr(norm_w), eps, _ptr(y),
+                                       int(accumulate)))
 
-    def matvec_glu(self, t, wg, wu, ne0, ne1, act, y, act_out):
-        self.check(lib().ts5hip_matvec_glu(self.h, t, _ptr(wg), _ptr(wu), ne0, ne1, _ptr(act), _ptr(y),
-                                           _ptr(act_out)))
+    def matvec_glu(self, t, wg, wu, ne0, ne1, x, y, norm_w=None, eps=0.0):
+        self.check(lib().ts5hip_matvec_glu(self.h, t, _ptr(wg), _ptr(wu), ne0, ne1, _ptr(x), _ptr(norm_w), eps,
+                                           _ptr(y)))
+
+    def matvec_argmax(self, t, w, ne0, ne1, x, y, out, norm_w=None, eps=0.0):
+        self.check(lib().ts5hip_matvec_argmax(self.h, t, _ptr(w), ne0, ne1, _ptr(x), _ptr(norm_w), eps, _ptr(y),
+                                              _ptr(out)))
 
     def rope_table(self, n_rot, n_pos, base, scale=1.0, freqs=None) -> DeviceBuffer:
         d = DeviceBuffer(self, n_pos * n_rot * 4)
@@ -248,11 +254,10 @@ class Context:
                                                _ptr(rope_cs), n_ctx, _ptr(bias), _ptr(q_norm), _ptr(k_norm), eps,
                                                _ptr(q_out), _ptr(k8), _ptr(ks), _ptr(v8), _ptr(vs)))
 
-    def attn_decode(self, q, B, H, HKV, HD, k8, ks, v8, vs, n_ctx, n_keys_dev, kv_per_batch, scale, n_split=0,
-                    out=None, act_out=None):
+    def attn_decode(self, q, B, H, HKV, HD, k8, ks, v8, vs, n_ctx, n_keys_dev, kv_per_batch, scale, out,
+                    n_split=0):
         self.check(lib().ts5hip_attn_decode(self.h, _ptr(q), B, H, HKV, HD, _ptr(k8), _ptr(ks), _ptr(v8), _ptr(vs),
-                                            n_ctx, _ptr(n_keys_dev), int(kv_per_batch), scale, n_split, _ptr(out),
-                                            _ptr(act_out)))
+                                            n_ctx, _ptr(n_keys_dev), int(kv_per_batch), scale, n_split, _ptr(out)))
 
     def argmax(self, x, n, rows, out):
         self.check(lib().ts5hip_argmax(self.h, _ptr(x), n, rows, _ptr(out)))

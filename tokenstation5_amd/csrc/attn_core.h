@@ -1,0 +1,320 @@
+// Device core of split-K flash decode over the q8 KV cache, shared by the
+// standalone kernel (attention.hip) and the whole-token persistent kernel
+// (decode.hip).
+#pragma once
+#include "common.h"
+#include "kernels.h"
+
+namespace ts5hip {
+
+// x0*c - x1*s and x0*s + x1*c with separate roundings, as the reference's
+// scalar float code computes them (engine/src/cpu_backend.cpp:63-64).
+__device__ inline void rope_pair(float &x0, float &x1, float c, float s) {
+#pragma clang fp contract(off)
+    const float a = x0 * c - x1 * s;
+    const float b = x0 * s + x1 * c;
+    x0 = a;
+    x1 = b;
+}
+
+// ---------------------------------------------------------------------------
+// Split-K flash decode with the token's own preparation and the merge fused
+// in. grid (n_split, HKV, B), 256 threads; query b is at position nk - 1
+// and reads keys [0, nk):
+//   nk = n_keys[b] (kv_per_batch: B independent caches), or
+//   nk = n_keys[0] + b + 1 (one cache, a batch of consecutive positions).
+// 1. The G query heads of this KV head: q (+ bias, per-head norm, RoPE
+//    when `rope`) -> LDS.
+// 2. `append` (B == 1): the workgroup whose key slice holds the new key
+//    rounds that token's K (RoPE'd) and V to q8, stores them at their slot,
+//    and keeps a copy in LDS that it reads instead of the cache.
+// 3. 64-key tiles: scores (4 lanes per key), online softmax per head, p*v.
+// 4. The unnormalised partial (sum p*v, m, l) per head goes to `part`; the
+//    last workgroup of a (b, KV head) to finish (an atomic counter, reset by
+//    that workgroup for the next launch) merges the splits:
+//    O = sum_s e^(m_s - M) O_s / sum_s e^(m_s - M) l_s (attn_merge.comp:18-47).
+// ---------------------------------------------------------------------------
+struct AttnArgs {
+    const float *q;  // query rows [B][q_stride]; with rope: raw q, k, v rows of each token
+    int64_t q_stride;
+    const float *bias, *q_norm, *k_norm;
+    float eps;
+    const float2 *rope_cs;
+    int n_rot, neox, rope, append;
+    KvLayer kv;
+    int kv_per_batch, n_ctx, H, HKV;
+    const int32_t *n_keys;
+    float scale;
+    float *part;    // [B][n_split][H][HD + 2]
+    int *counters;  // [B * HKV], zero between launches
+    float *out;     // [B][H * HD]
+};
+
+__device__ inline void rope_inplace(float *v, int n_rot, int neox, const float2 *cs, int i) {
+    const int a = neox ? i : 2 * i, b = neox ? i + n_rot / 2 : 2 * i + 1;
+    float x0 = v[a], x1 = v[b];
+    rope_pair(x0, x1, cs[i].x, cs[i].y);
+    v[a] = x0;
+    v[b] = x1;
+}
+
+constexpr int ATTN_MAX_SPLIT = 64;
+
+template <int HD, int G>
+struct AttnLds {
+    float q_s[G][HD];
+    float p_s[G][64];
+    float alpha_s[G], m_s[G], l_s[G], red[G];
+    float kv_s[2][HD];                 // the new token's K and V before rounding
+    __align__(16) int8_t new8[2][HD];  // ... and after, as int8
+    uint16_t new_sc[2][HD / 32];       // ... with their f16 scales
+    float mw[ATTN_MAX_SPLIT][G], lw[ATTN_MAX_SPLIT][G];  // the merge's (m, l), then weights
+    int last;
+};
+
+// One work item (split, KV head kvh, query b) of n_split; 256 threads.
+template <int HD, int G>
+__device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, int n_split, AttnLds<HD, G> &S) {
+    constexpr int TILE = 64, NQ = HD / 4, NPAIR = G * HD / 2, PPT = (NPAIR + 255) / 256;
+    auto &q_s = S.q_s;
+    auto &p_s = S.p_s;
+    auto &alpha_s = S.alpha_s;
+    auto &m_s = S.m_s;
+    auto &l_s = S.l_s;
+    auto &red = S.red;
+    auto &kv_s = S.kv_s;
+    auto &new8 = S.new8;
+    auto &new_sc = S.new_sc;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nk = a.kv_per_batch ? a.n_keys[b] : a.n_keys[0] + b + 1;
+    const int pq = nk - 1;  // the query's position
+    int chunk = (nk + n_split - 1) / n_split;
+    chunk = (chunk + TILE - 1) / TILE * TILE;
+    const int p0 = split * chunk, p1 = min(nk, p0 + chunk);
+    const int seq = a.kv_per_batch ? b : 0;
+    const int64_t head_base = ((int64_t)seq * a.HKV + kvh) * a.n_ctx;  // slot of key 0
+    const float *row = a.q + (int64_t)b * a.q_stride;
+    const bool has_new = a.append && pq >= p0 && pq < p1;
+
+    // 1. Query heads (and the new K/V rows) into LDS.
+    for (int j = tid; j < G * HD; j += 256) {
+        const int64_t e = (int64_t)(kvh * G + j / HD) * HD + j % HD;
+        q_s[j / HD][j % HD] = row[e] + (a.rope && a.bias ? a.bias[e] : 0.f);
+    }
+    if (has_new) {
+        for (int j = tid; j < 2 * HD; j += 256) {
+            const int64_t e = (int64_t)((j < HD ? a.H : a.H + a.HKV) + kvh) * HD + j % HD;
+            kv_s[j / HD][j % HD] = row[e] + (a.bias ? a.bias[e] : 0.f);
+        }
+    }
+    if (tid < G) {
+        m_s[tid] = -INFINITY;
+        l_s[tid] = 0.f;
+    }
+    __syncthreads();
+    if (a.rope) {
+        // Per-head RMSNorm (qwen3's q_norm / k_norm), then RoPE.
+        if (a.q_norm || (has_new && a.k_norm)) {
+            for (int g = wave; g < G + 1; g += 4) {
+                const float *nw = g < G ? a.q_norm : (has_new ? a.k_norm : nullptr);
+                if (!nw) continue;
+                float *v = g < G ? q_s[g] : kv_s[0];
+                float ss = 0.f;
+                for (int j = lane; j < HD; j += 64) ss += v[j] * v[j];
+                ss = wave_sum(ss);
+                const float sc = 1.0f / sqrtf(ss / (float)HD + a.eps);
+                for (int j = lane; j < HD; j += 64) v[j] = v[j] * sc * nw[j];
+            }
+            __syncthreads();
+        }
+        const float2 *cs = a.rope_cs + (int64_t)pq * (a.n_rot / 2);
+        for (int j = tid; j < (G + 1) * (HD / 2); j += 256) {
+            const int g = j / (HD / 2), i = j % (HD / 2);
+            if (i >= a.n_rot / 2) continue;
+            if (g < G) rope_inplace(q_s[g], a.n_rot, a.neox, cs, i);
+            else if (has_new) rope_inplace(kv_s[0], a.n_rot, a.neox, cs, i);
+        }
+        __syncthreads();
+    }
+    if (has_new && tid < 128) {
+        // q8 (engine/src/cpu_backend.cpp:78-90): per 32 values sc = f16(amax / 127),
+        // q = clamp(rint(v / sc), +-127). Wave 0 rounds K, wave 1 V, a pair per lane.
+        const int which = tid >> 6, i = tid & 63;
+        if (2 * i < HD) {
+            const float a0 = kv_s[which][2 * i], a1 = kv_s[which][2 * i + 1];
+            float amax = fmaxf(fabsf(a0), fabsf(a1));
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+            const uint16_t sh = f2h(amax / 127.0f);
+            const float sc = h2f(sh);
+            int q0 = 0, q1 = 0;
+            if (sc > 0.f) {
+                q0 = (int)fminf(127.f, fmaxf(-127.f, rintf(a0 / sc)));
+                q1 = (int)fminf(127.f, fmaxf(-127.f, rintf(a1 / sc)));
+            }
+            const uint16_t packed = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
+            const int64_t slot = head_base + pq;
+            *(uint16_t *)(new8[which] + 2 * i) = packed;
+            *(uint16_t *)((which ? a.kv.v : a.kv.k) + slot * HD + 2 * i) = packed;
+            if ((i & 15) == 0) {
+                new_sc[which][i / 16] = sh;
+                (which ? a.kv.vs : a.kv.ks)[slot * (HD / 32) + i / 16] = sh;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 3. Tiles of 64 keys.
+    float o[PPT][2];
+#pragma unroll
+    for (int k = 0; k < PPT; k++) o[k][0] = o[k][1] = 0.f;
+    for (int t0 = p0; t0 < p1; t0 += TILE) {
+        {   // Scores: 4 lanes per key, NQ dims each.
+            const int kk = tid >> 2, qq = tid & 3, p = t0 + kk;
+            float acc[G];
+#pragma unroll
+            for (int g = 0; g < G; g++) acc[g] = 0.f;
+            if (p < p1) {
+                const bool mine = has_new && p == pq;
+                uint4 w[NQ / 16];
+                float ks;
+                if (mine) {
+#pragma unroll
+                    for (int c = 0; c < NQ / 16; c++) w[c] = *(const uint4 *)(new8[0] + qq * NQ + 16 * c);
+                    ks = h2f(new_sc[0][(qq * NQ) / 32]);
+                } else {
+                    const int8_t *kp = a.kv.k + (head_base + p) * HD + qq * NQ;
+#pragma unroll
+                    for (int c = 0; c < NQ / 16; c++) w[c] = *(const uint4 *)(kp + 16 * c);
+                    ks = h2f(a.kv.ks[(head_base + p) * (HD / 32) + (qq * NQ) / 32]);
+                }
+#pragma unroll
+                for (int c = 0; c < NQ / 16; c++) {
+                    const uint32_t ws[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const float kf = (float)(int8_t)((ws[e >> 2] >> (8 * (e & 3))) & 0xff) * ks;
+                        const int d = qq * NQ + 16 * c + e;
+#pragma unroll
+                        for (int g = 0; g < G; g++) acc[g] += q_s[g][d] * kf;
+                    }
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                acc[g] += __shfl_xor(acc[g], 1, WAVE);
+                acc[g] += __shfl_xor(acc[g], 2, WAVE);
+            }
+            if (qq == 0) {
+#pragma unroll
+                for (int g = 0; g < G; g++) p_s[g][kk] = p < p1 ? acc[g] * a.scale : -INFINITY;
+            }
+        }
+        __syncthreads();
+        // Online softmax per head: wave w takes heads w, w+4.
+        for (int g = wave; g < G; g += 4) {
+            const float sv = p_s[g][lane];
+            const float mt = wave_max(sv);
+            const float mo = m_s[g];
+            const float mn = fmaxf(mo, mt);
+            const float p = sv == -INFINITY ? 0.f : expf(sv - mn);
+            const float ls = wave_sum(p);
+            p_s[g][lane] = p;
+            if (lane == 0) {
+                const float al = mo == -INFINITY ? 0.f : expf(mo - mn);
+                alpha_s[g] = al;
+                m_s[g] = mn;
+                l_s[g] = l_s[g] * al + ls;
+            }
+        }
+        __syncthreads();
+        // o = o * alpha + sum_k p_k * v_k (the new key's V from LDS).
+        const int nt = min(TILE, p1 - t0);
+        const bool new_here = has_new && pq >= t0 && pq < t0 + nt;
+        const int nc = new_here ? pq - t0 : nt;  // keys of this tile read from the cache
+#pragma unroll
+        for (int k = 0; k < PPT; k++) {
+            const int pp = tid + 256 * k;
+            if (pp < NPAIR) {
+                const int g = (2 * pp) / HD, d = (2 * pp) % HD;
+                const float al = alpha_s[g];
+                float o0 = o[k][0] * al, o1 = o[k][1] * al;
+                const int8_t *vp = a.kv.v + (head_base + t0) * HD + d;
+                const uint16_t *vsp = a.kv.vs + (head_base + t0) * (HD / 32) + d / 32;
+                for (int kk = 0; kk < nc; kk++) {
+                    const uint16_t v2 = *(const uint16_t *)(vp + (int64_t)kk * HD);
+                    const float w = p_s[g][kk] * h2f(vsp[(int64_t)kk * (HD / 32)]);
+                    o0 += w * (float)(int8_t)(v2 & 0xff);
+                    o1 += w * (float)(int8_t)(v2 >> 8);
+                }
+                if (new_here) {
+                    const uint16_t v2 = *(const uint16_t *)(new8[1] + d);
+                    const float w = p_s[g][nc] * h2f(new_sc[1][d / 32]);
+                    o0 += w * (float)(int8_t)(v2 & 0xff);
+                    o1 += w * (float)(int8_t)(v2 >> 8);
+                }
+                o[k][0] = o0;
+                o[k][1] = o1;
+            }
+        }
+        __syncthreads();
+    }
+
+    // 4. Partial record per head: [HD values][m][l]; the last workgroup merges.
+    const int64_t rec = HD + 2;
+    float *pb = a.part + (((int64_t)b * n_split + split) * a.H + (int64_t)kvh * G) * rec;
+#pragma unroll
+    for (int k = 0; k < PPT; k++) {
+        const int pp = tid + 256 * k;
+        if (pp < NPAIR) {
+            const int g = (2 * pp) / HD, d = (2 * pp) % HD;
+            pb[g * rec + d] = o[k][0];
+            pb[g * rec + d + 1] = o[k][1];
+        }
+    }
+    if (tid < G) {
+        pb[tid * rec + HD] = m_s[tid];
+        pb[tid * rec + HD + 1] = l_s[tid];
+    }
+    __syncthreads();
+    if (tid == 0) {
+        __threadfence();
+        S.last = atomicAdd(a.counters + b * a.HKV + kvh, 1) == n_split - 1;
+    }
+    __syncthreads();
+    if (!S.last) return;
+    __threadfence();
+    const float *p_all = a.part + ((int64_t)b * n_split * a.H + (int64_t)kvh * G) * rec;
+    const int64_t sstride = (int64_t)a.H * rec;
+    // Every split's (m, l) in one round of loads, then the weights e^(m_s - M).
+    for (int j = tid; j < n_split * G; j += 256) {
+        const int sp = j / G, g = j % G;
+        S.mw[sp][g] = p_all[sp * sstride + g * rec + HD];
+        S.lw[sp][g] = p_all[sp * sstride + g * rec + HD + 1];
+    }
+    __syncthreads();
+    if (tid < G) {
+        float M = -INFINITY;
+        for (int sp = 0; sp < n_split; sp++) M = fmaxf(M, S.mw[sp][tid]);
+        float L = 0.f;
+        for (int sp = 0; sp < n_split; sp++) {
+            const float m = S.mw[sp][tid];
+            const float w = m == -INFINITY ? 0.f : expf(m - M);
+            S.mw[sp][tid] = w;
+            L += w * S.lw[sp][tid];
+        }
+        red[tid] = L;
+    }
+    __syncthreads();
+    for (int j = tid; j < G * HD; j += 256) {
+        const int g = j / HD, d = j % HD;
+        const float *pd = p_all + g * rec + d;
+        float acc = 0.f;
+#pragma unroll 8
+        for (int sp = 0; sp < n_split; sp++) acc += S.mw[sp][g] * pd[sp * sstride];
+        a.out[(int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d] = acc / red[g];
+    }
+    if (tid == 0) a.counters[b * a.HKV + kvh] = 0;  // ready for the next launch
+}
+
+}  // namespace ts5hip

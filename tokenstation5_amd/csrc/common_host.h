@@ -52,7 +52,7 @@ inline void rope_table_host(int n_rot, int n_pos, float base, float scale, const
 // Split count of the flash decode: about `target` workgroups in all.
 inline int attn_splits(int B, int n_head_kv, int target = 512) {
     const int s = (target + B * n_head_kv - 1) / (B * n_head_kv);
-    return s < 1 ? 1 : (s > 64 ? 64 : s);
+    return s < 1 ? 1 : (s > 64 ? 64 : s);  // at most 64 (the merge's table)
 }
 inline size_t attn_partial_bytes(int B, int n_split, int H, int HD) {
     return (size_t)B * n_split * H * (HD + 2) * sizeof(float);

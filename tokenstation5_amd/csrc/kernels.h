@@ -70,6 +70,36 @@ struct AttnIO {
     float *out;     // [B][H * HD]
 };
 hipError_t launch_attn(const AttnIO &io, hipStream_t s);
+// decode.hip: one token as one persistent kernel (cooperative launch).
+struct DecodeLayerIn {
+    const void *qkv, *wo, *gate, *up, *down;
+    uint32_t t_qkv, t_wo, t_gu, t_down;
+    const float *attn_norm, *ffn_norm, *bias, *q_norm, *k_norm;
+    KvLayer kv;
+};
+struct DecodeIn {
+    int E, F, H, HKV, HD, V, n_layer, n_ctx, n_rot, neox, n_split;
+    float eps, scale;
+    const void *layers;  // device array of n_layer records (fill_decode_layer)
+    uint32_t t_embd, t_head;
+    const void *embd, *head;
+    const float *out_norm, *rope;
+    float *x, *qkv, *att, *ffn, *logits, *part;
+    int *counters;         // [HKV], zero
+    int32_t *seq, *state;  // state[0] position, state[1] greedy id
+    int head_mode;         // 0: none, 1: logits, 2: logits + greedy argmax into seq[p + 1]
+    void *bar;             // decode_bar_bytes(), zeroed once
+    float *best_v;
+    int *best_i;  // grid entries each
+    int grid;
+    size_t lds_bytes;
+};
+size_t decode_layer_bytes();
+size_t decode_bar_bytes();
+int decode_grid(int HD, int G, int n_cu, size_t lds_bytes);
+hipError_t fill_decode_layer(void *dst_host, const DecodeLayerIn &in);
+hipError_t launch_decode(const DecodeIn &in, hipStream_t s);
+
 hipError_t launch_kv_read(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, float *out, hipStream_t s);
 
 // sample.hip

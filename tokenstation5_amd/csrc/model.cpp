@@ -74,6 +74,14 @@ struct ts5hip_model {
     hipGraphExec_t graph[N_GRAPHS] = {nullptr, nullptr, nullptr};
     bool graphs_stale = true;
     bool use_graphs = true;  // TS5HIP_GRAPHS=0: launch each token's kernels directly (profilers)
+    // The whole-token persistent kernel (decode.hip), used for single-token
+    // steps when every tensor fits it; TS5HIP_DECODE=0 turns it off.
+    bool want_decode = true, use_decode = false;
+    int dec_grid = 0, dec_split = 32;
+    size_t dec_lds = 0;
+    void *dec_layers = nullptr, *bar = nullptr;
+    float *dec_best_v = nullptr;
+    int *dec_best_i = nullptr;
     // Profile (TS5HIP_PROFILE set): GPU time per forward call.
     bool profile = false;
     double prof_ms = 0;
@@ -359,9 +367,78 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
     return TS5HIP_OK;
 }
 
+// Sets up the persistent whole-token kernel when every tensor fits it.
+int prepare_decode(ts5hip_model *m) {
+    m->use_decode = false;
+    if (!m->want_decode) return TS5HIP_OK;
+    const ts5hip_hparams &hp = m->hp;
+    auto ok_type = [](uint32_t t) { return t == T_Q4_K || t == T_Q6_K || t == T_Q8_0; };
+    const DevT &out = m->output.set ? m->output : m->tok_embd;
+    if (!ok_type(out.type) || hp.n_embd > 16384 || hp.n_ff > 16384 || hp.n_head * hp.head_dim > 16384) return TS5HIP_OK;
+    std::vector<uint8_t> host((size_t)hp.n_layer * decode_layer_bytes());
+    for (int l = 0; l < hp.n_layer; l++) {
+        const LayerDev &L = m->layers[l];
+        if (!(L.in_qkv[0] && L.in_qkv[1] && L.in_qkv[2]) || !ok_type(L.qkv.type) || !ok_type(L.wo.type) ||
+            !ok_type(L.gate.type) || !ok_type(L.down.type))
+            return TS5HIP_OK;
+        DecodeLayerIn in{};
+        in.qkv = L.qkv.d, in.wo = L.wo.d, in.gate = L.gate.d, in.up = L.up.d, in.down = L.down.d;
+        in.t_qkv = L.qkv.type, in.t_wo = L.wo.type, in.t_gu = L.gate.type, in.t_down = L.down.type;
+        in.attn_norm = (const float *)L.attn_norm.d, in.ffn_norm = (const float *)L.ffn_norm.d;
+        in.bias = m->has_bias[l] ? m->bias + (int64_t)l * m->qkv_rows() : nullptr;
+        in.q_norm = L.q_norm.set ? (const float *)L.q_norm.d : nullptr;
+        in.k_norm = L.k_norm.set ? (const float *)L.k_norm.d : nullptr;
+        in.kv = m->kv_layer(l);
+        TS5_HIP(m->ctx, fill_decode_layer(host.data() + (size_t)l * decode_layer_bytes(), in));
+    }
+    const size_t lds = act_bytes(std::max({hp.n_embd, hp.n_ff, hp.n_head * hp.head_dim}));
+    const int grid = decode_grid(hp.head_dim, hp.n_head / hp.n_head_kv, m->ctx->n_cu, lds);
+    if (grid < m->ctx->n_cu) return TS5HIP_OK;
+    if (!m->dec_layers && alloc(m, host.size(), &m->dec_layers)) return TS5HIP_ERR_HIP;
+    if (!m->bar) {
+        if (int rc = alloc(m, decode_bar_bytes(), &m->bar)) return rc;
+        TS5_HIP(m->ctx, hipMemsetAsync(m->bar, 0, decode_bar_bytes(), m->ctx->stream));
+    }
+    if (!m->dec_best_v) {
+        if (int rc = alloc_t(m, (size_t)grid, &m->dec_best_v)) return rc;
+        if (int rc = alloc_t(m, (size_t)grid, &m->dec_best_i)) return rc;
+    }
+    if (int rc = ts5hip_upload(m->ctx, m->dec_layers, host.data(), host.size())) return rc;
+    m->dec_grid = grid, m->dec_lds = lds;
+    m->dec_split = std::min(64, std::max(1, 256 / hp.n_head_kv));
+    m->use_decode = true;
+    return TS5HIP_OK;
+}
+
+int launch_decode_token(ts5hip_model *m, int head_mode) {
+    const ts5hip_hparams &hp = m->hp;
+    const DevT &out = m->output.set ? m->output : m->tok_embd;
+    DecodeIn in{};
+    in.E = hp.n_embd, in.F = hp.n_ff, in.H = hp.n_head, in.HKV = hp.n_head_kv, in.HD = hp.head_dim;
+    in.V = hp.n_vocab, in.n_layer = hp.n_layer, in.n_ctx = m->n_ctx, in.n_rot = hp.rope_dims;
+    in.neox = hp.rope_neox, in.n_split = m->dec_split, in.eps = hp.rms_eps, in.scale = hp.attn_scale;
+    in.layers = m->dec_layers, in.t_embd = m->tok_embd.type, in.t_head = out.type, in.embd = m->tok_embd.d;
+    in.head = out.d, in.out_norm = (const float *)m->out_norm.d, in.rope = m->rope_cs, in.x = m->x;
+    in.qkv = m->qkv, in.att = m->att, in.ffn = m->ffn, in.logits = m->logits, in.part = m->part;
+    in.counters = m->counters, in.seq = m->seq, in.state = m->state, in.head_mode = head_mode, in.bar = m->bar;
+    in.best_v = m->dec_best_v, in.best_i = m->dec_best_i, in.grid = m->dec_grid, in.lds_bytes = m->dec_lds;
+    TS5_HIP(m->ctx, launch_decode(in, m->ctx->stream));
+    return TS5HIP_OK;
+}
+
+// After a synchronisation: a persistent-kernel barrier that gave up waiting.
+int check_decode(ts5hip_model *m) {
+    if (!m->use_decode) return TS5HIP_OK;
+    int err[3] = {0, 0, 0};
+    TS5_HIP(m->ctx, hipMemcpy(err, m->bar, sizeof err, hipMemcpyDeviceToHost));
+    if (err[2]) return fail(m->ctx, TS5HIP_ERR_HIP, "decode kernel: a grid barrier timed out");
+    return TS5HIP_OK;
+}
+
 int build_graphs(ts5hip_model *m) {
     if (!m->graphs_stale) return TS5HIP_OK;
     if (int rc = check_complete(m)) return rc;
+    if (int rc = prepare_decode(m)) return rc;
     if (!m->use_graphs) {
         m->graphs_stale = false;
         return TS5HIP_OK;
@@ -390,8 +467,10 @@ int build_graphs(ts5hip_model *m) {
     return TS5HIP_OK;
 }
 
-// One token's kernels: a replay of the captured graph, or direct launches.
+// One token's kernels: the persistent kernel, a replay of the captured
+// graph, or direct launches.
 int launch_token(ts5hip_model *m, int g) {
+    if (m->use_decode) return launch_decode_token(m, g == G_KV ? 0 : g == G_LOGITS ? 1 : 2);
     if (!m->use_graphs) return enqueue_token(m, g != G_KV, g == G_GREEDY ? 1 : 0);
     TS5_HIP(m->ctx, hipGraphLaunch(m->graph[g], m->ctx->stream));
     return TS5HIP_OK;
@@ -446,6 +525,7 @@ int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool wan
     }
     if (m->profile) TS5_HIP(ctx, hipEventRecord(ctx->ev1, s));
     TS5_HIP(ctx, hipStreamSynchronize(s));
+    if (int rc = check_decode(m)) return rc;
     if (m->profile) {
         float ms = 0;
         TS5_HIP(ctx, hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
@@ -482,6 +562,8 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
     m->profile = prof && *prof && std::strcmp(prof, "0") != 0;
     const char *graphs = std::getenv("TS5HIP_GRAPHS");
     m->use_graphs = !(graphs && std::strcmp(graphs, "0") == 0);
+    const char *dec = std::getenv("TS5HIP_DECODE");
+    m->want_decode = !(dec && std::strcmp(dec, "0") == 0);
     const int64_t E = hp->n_embd, F = hp->n_ff, HD = hp->head_dim, H = hp->n_head, HKV = hp->n_head_kv;
     const int64_t kv_elems = (int64_t)hp->n_layer * HKV * n_ctx * HD;
     int rc = 0;
@@ -491,7 +573,7 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
         (rc = alloc_t(m, (size_t)hp->n_layer * m->qkv_rows(), &m->bias)) || (rc = alloc_t(m, E, &m->x)) ||
         (rc = alloc_t(m, m->qkv_rows(), &m->qkv)) || (rc = alloc_t(m, H * HD, &m->att)) ||
         (rc = alloc_t(m, F, &m->ffn)) || (rc = alloc_t(m, hp->n_vocab, &m->logits)) ||
-        (rc = alloc_t(m, attn_partial_bytes(1, m->n_split, H, HD) / 4, &m->part)) ||
+        (rc = alloc_t(m, attn_partial_bytes(1, 64, H, HD) / 4, &m->part)) ||
         (rc = alloc_t(m, 2 * HKV + 64, &m->counters)) ||
         (rc = alloc(m, matvec_argmax_scratch_bytes(), &m->amax)) || (rc = alloc(m, topk_scratch_bytes(), &m->topk)) ||
         (rc = alloc_t(m, 64, &m->topk_v)) || (rc = alloc_t(m, 64, &m->topk_i)) ||
@@ -599,6 +681,7 @@ int ts5hip_generate_greedy(ts5hip_model *m, int32_t token, int pos, int n_steps,
         if (int rc = launch_token(m, G_GREEDY)) return rc;
     TS5_HIP(ctx, hipMemcpyAsync(m->pinned_ids, m->seq + pos + 1, (size_t)n_steps * 4, hipMemcpyDeviceToHost, s));
     TS5_HIP(ctx, hipStreamSynchronize(s));
+    if (int rc = check_decode(m)) return rc;
     if (ids_out) std::memcpy(ids_out, m->pinned_ids, (size_t)n_steps * 4);
     m->rows_valid = 0;
     return TS5HIP_OK;

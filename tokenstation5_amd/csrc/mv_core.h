@@ -1,0 +1,456 @@
+// Device core of the one-token k-quant matvec, shared by the standalone
+// kernels (matvec.hip) and the whole-token persistent kernel (decode.hip).
+//
+// The reference computes y[r] = sum_i deq(W[r,i]) * x[i] with fp64
+// accumulation (engine/src/cpu_backend.cpp:18-37); its GPU path reads 8
+// lanes per Q4_K super-block with 16-byte loads (mv16_q4_k.glsl:64-113).
+// Here:
+//  * A workgroup first turns the fp32 input (rms-normalised when a norm
+//    weight is given, engine/src/cpu_backend.cpp:48-53) into the quantized
+//    activation of common.h in LDS: x16 = 256*hi + lo per value, a scale per
+//    32. The weights are the only HBM stream; the input is read from L2.
+//  * Weights stay packed in registers. A lane takes whole 32-value
+//    sub-blocks, multiplies raw quants with the activation's two int8 planes
+//    on v_dot4_i32_i8 (exact int32) and applies the block scales once per
+//    sub-block in fp32:
+//      Q4_K: y += d*sc*(xs*sum q*x16) - dmin*m*(sum x)   (quants.cpp:140-157)
+//      Q6_K: y += d*sc*xs*(sum q*x16 - 32*sum x16)       (quants.cpp:179-202)
+//      Q8_0: y += d*xs*(sum q*x16)                       (quants.cpp:133-139)
+//  * Persistent row groups: a workgroup walks its groups (R rows per wave)
+//    as a flat sequence of steps (one 64-lane sweep of 64/LPB blocks each)
+//    and always has the next step's weight loads in flight while it computes
+//    the current one. The first step's loads are issued before the
+//    activation is built (and, in the persistent kernel, before the grid
+//    barrier that precedes it). Every weight byte is read once.
+// Bandwidth-bound: no MFMA.
+#pragma once
+#include <climits>
+
+#include "common.h"
+
+namespace ts5hip {
+
+struct WPtr {
+    const uint8_t *body;     // blocks (Q4_K: whole blocks; Q6_K/Q8_0: bodies)
+    const uint16_t *dscale;  // f16 block scales of split layouts
+};
+
+__device__ inline WPtr wptr(uint32_t t, const void *w, int64_t nblocks) {
+    WPtr p;
+    p.body = (const uint8_t *)w;
+    p.dscale = (t == T_Q6_K || t == T_Q8_0) ? (const uint16_t *)(p.body + split_scale_offset(t, nblocks)) : nullptr;
+    return p;
+}
+
+__device__ inline uint4 ld16(const void *p) { return *(const uint4 *)p; }
+
+// ---------------------------------------------------------------------------
+// Formats. Each lane owns `sub` (0..LPB-1) of every block it visits; a wave
+// covers BPI = 64 / LPB consecutive blocks of a row per step.
+// ---------------------------------------------------------------------------
+
+// Q4_K: 4 lanes per block, lane `sub` = nibble group g: sub-blocks 2g (low
+// nibbles) and 2g+1 (high nibbles), 64 values.
+struct Q4K {
+    static constexpr int LPB = 4;
+    struct X {
+        uint32_t h0[8], h1[8], l0[8], l1[8];
+        float s0, s1, m0, m1;
+    };
+    struct W {
+        uint4 hdr, qa, qb;
+    };
+    __device__ static X load_x(const CAct &x, int b, int sub) {
+        X r;
+        const int base = b * 256 + 64 * sub;
+        uint4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = ld16(x.hi + base + 16 * k);
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            r.h0[4 * k] = v[k].x, r.h0[4 * k + 1] = v[k].y, r.h0[4 * k + 2] = v[k].z, r.h0[4 * k + 3] = v[k].w;
+            r.h1[4 * k] = v[k + 2].x, r.h1[4 * k + 1] = v[k + 2].y, r.h1[4 * k + 2] = v[k + 2].z,
+                     r.h1[4 * k + 3] = v[k + 2].w;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = ld16(x.lo + base + 16 * k);
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            r.l0[4 * k] = v[k].x, r.l0[4 * k + 1] = v[k].y, r.l0[4 * k + 2] = v[k].z, r.l0[4 * k + 3] = v[k].w;
+            r.l1[4 * k] = v[k + 2].x, r.l1[4 * k + 1] = v[k + 2].y, r.l1[4 * k + 2] = v[k + 2].z,
+                     r.l1[4 * k + 3] = v[k + 2].w;
+        }
+        const int s = b * 8 + 2 * sub;
+        r.s0 = x.scale[s];
+        r.s1 = x.scale[s + 1];
+        r.m0 = x.sum[s];
+        r.m1 = x.sum[s + 1];
+        return r;
+    }
+    __device__ static W load_w(const WPtr &w, int64_t row, int nb, int b, int sub) {
+        const uint8_t *blk = w.body + ((size_t)row * nb + b) * Q4K_BYTES;
+        W r;
+        r.hdr = ld16(blk);
+        r.qa = ld16(blk + 16 + 32 * sub);
+        r.qb = ld16(blk + 32 + 32 * sub);
+        return r;
+    }
+    __device__ static float dot(const W &w, const X &x, int sub) {
+        const uint32_t q[8] = {w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w};
+        int ah0 = 0, al0 = 0, ah1 = 0, al1 = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int lo = (int)(q[k] & 0x0F0F0F0Fu), hi = (int)((q[k] >> 4) & 0x0F0F0F0Fu);
+            ah0 = dot4(lo, (int)x.h0[k], ah0);
+            al0 = dot4(lo, (int)x.l0[k], al0);
+            ah1 = dot4(hi, (int)x.h1[k], ah1);
+            al1 = dot4(hi, (int)x.l1[k], al1);
+        }
+        int sc0, m0, sc1, m1;
+        kq_scale_min(2 * sub, w.hdr.y, w.hdr.z, w.hdr.w, sc0, m0);
+        kq_scale_min(2 * sub + 1, w.hdr.y, w.hdr.z, w.hdr.w, sc1, m1);
+        const float d = h2f(w.hdr.x & 0xffff), dmin = h2f(w.hdr.x >> 16);
+        const float p = (float)sc0 * x.s0 * (float)(ah0 * 256 + al0) + (float)sc1 * x.s1 * (float)(ah1 * 256 + al1);
+        return d * p - dmin * ((float)m0 * x.m0 + (float)m1 * x.m1);
+    }
+};
+
+// Q6_K: 4 lanes per block, lane `sub` = (half h = sub/2, i0 = 16*(sub%2)):
+// the four 16-value runs at 128h + 32c + i0 (c = 0..3), 64 values.
+struct Q6K {
+    static constexpr int LPB = 4;
+    struct X {
+        uint32_t h[4][4], l[4][4];  // [run c][dword]
+        float s[4];
+        int is[4];
+    };
+    struct W {
+        uint4 qla, qlb, qh, sc;
+        float d;
+    };
+    __device__ static X load_x(const CAct &x, int b, int sub) {
+        X r;
+        const int h = sub >> 1, i0 = (sub & 1) * 16;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int base = b * 256 + 128 * h + 32 * c + i0;
+            const uint4 vh = ld16(x.hi + base), vl = ld16(x.lo + base);
+            r.h[c][0] = vh.x, r.h[c][1] = vh.y, r.h[c][2] = vh.z, r.h[c][3] = vh.w;
+            r.l[c][0] = vl.x, r.l[c][1] = vl.y, r.l[c][2] = vl.z, r.l[c][3] = vl.w;
+            r.s[c] = x.scale[base / 32];
+            r.is[c] = x.isum[base / 16];
+        }
+        return r;
+    }
+    __device__ static W load_w(const WPtr &w, int64_t row, int nb, int b, int sub) {
+        const size_t blk = (size_t)row * nb + b;
+        const uint8_t *body = w.body + blk * Q6K_BODY;
+        const int h = sub >> 1, i0 = (sub & 1) * 16;
+        W r;
+        r.qla = ld16(body + 64 * h + i0);
+        r.qlb = ld16(body + 64 * h + 32 + i0);
+        r.qh = ld16(body + 128 + 32 * h + i0);
+        r.sc = ld16(body + 192);
+        r.d = h2f(w.dscale[blk]);
+        return r;
+    }
+    __device__ static float dot(const W &w, const X &x, int sub) {
+        const uint32_t qa[4] = {w.qla.x, w.qla.y, w.qla.z, w.qla.w};
+        const uint32_t qb[4] = {w.qlb.x, w.qlb.y, w.qlb.z, w.qlb.w};
+        const uint32_t qh[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+        int ah[4] = {0, 0, 0, 0}, al[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t q0 = (qa[k] & 0x0F0F0F0Fu) | ((qh[k] << 4) & 0x30303030u);
+            const uint32_t q1 = (qb[k] & 0x0F0F0F0Fu) | ((qh[k] << 2) & 0x30303030u);
+            const uint32_t q2 = ((qa[k] >> 4) & 0x0F0F0F0Fu) | (qh[k] & 0x30303030u);
+            const uint32_t q3 = ((qb[k] >> 4) & 0x0F0F0F0Fu) | ((qh[k] >> 2) & 0x30303030u);
+            ah[0] = dot4((int)q0, (int)x.h[0][k], ah[0]);
+            al[0] = dot4((int)q0, (int)x.l[0][k], al[0]);
+            ah[1] = dot4((int)q1, (int)x.h[1][k], ah[1]);
+            al[1] = dot4((int)q1, (int)x.l[1][k], al[1]);
+            ah[2] = dot4((int)q2, (int)x.h[2][k], ah[2]);
+            al[2] = dot4((int)q2, (int)x.l[2][k], al[2]);
+            ah[3] = dot4((int)q3, (int)x.h[3][k], ah[3]);
+            al[3] = dot4((int)q3, (int)x.l[3][k], al[3]);
+        }
+        // Run c's scale is byte 8h + sub%2 + 2c of the 16: dword 2h (c < 2)
+        // or 2h + 1 (c >= 2), byte sub%2 + 2(c%2).
+        const uint32_t s01 = (sub >> 1) ? w.sc.z : w.sc.x, s23 = (sub >> 1) ? w.sc.w : w.sc.y;
+        const int sh = 8 * (sub & 1);
+        float p = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t word = c < 2 ? s01 : s23;
+            const int sc = (int)(int8_t)((word >> (sh + 16 * (c & 1))) & 0xff);
+            const int v = ah[c] * 256 + al[c] - 32 * x.is[c];
+            p += (float)sc * x.s[c] * (float)v;
+        }
+        return w.d * p;
+    }
+};
+
+// Q8_0: 2 lanes per 32-value block, 16 values each.
+struct Q80 {
+    static constexpr int LPB = 2;
+    struct X {
+        uint4 h, l;
+        float s;
+    };
+    struct W {
+        uint4 q;
+        float d;
+    };
+    __device__ static X load_x(const CAct &x, int b, int sub) {
+        X r;
+        r.h = ld16(x.hi + b * 32 + 16 * sub);
+        r.l = ld16(x.lo + b * 32 + 16 * sub);
+        r.s = x.scale[b];
+        return r;
+    }
+    __device__ static W load_w(const WPtr &w, int64_t row, int nb, int b, int sub) {
+        const size_t blk = (size_t)row * nb + b;
+        W r;
+        r.q = ld16(w.body + blk * Q8_BODY + 16 * sub);
+        r.d = h2f(w.dscale[blk]);
+        return r;
+    }
+    __device__ static float dot(const W &w, const X &x, int) {
+        int ah = 0, al = 0;
+        ah = dot4((int)w.q.x, (int)x.h.x, ah);
+        ah = dot4((int)w.q.y, (int)x.h.y, ah);
+        ah = dot4((int)w.q.z, (int)x.h.z, ah);
+        ah = dot4((int)w.q.w, (int)x.h.w, ah);
+        al = dot4((int)w.q.x, (int)x.l.x, al);
+        al = dot4((int)w.q.y, (int)x.l.y, al);
+        al = dot4((int)w.q.z, (int)x.l.z, al);
+        al = dot4((int)w.q.w, (int)x.l.w, al);
+        return w.d * x.s * (float)(ah * 256 + al);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// The activation prologue: x (n values, optionally rms-normalised by norm_w)
+// -> Act in LDS. One thread per 32-value sub-block.
+// ---------------------------------------------------------------------------
+__device__ inline void quant_group_lds(const float *v, const Act &a, int g) {
+    float amax = 0.f, s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        s += v[i];
+    }
+    const float inv = amax > 0.f ? 16383.0f / amax : 0.f;
+    uint32_t hw[8], lw[8];
+    int is0 = 0, is1 = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        uint32_t h = 0, l = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int i = 4 * k + e;
+            const int x16 = max(-16383, min(16383, (int)rintf(v[i] * inv)));
+            const int lo = (int)(int8_t)(x16 & 255);
+            const int hi = (x16 - lo) >> 8;
+            h |= (uint32_t)(hi & 255) << (8 * e);
+            l |= (uint32_t)(lo & 255) << (8 * e);
+            if (i < 16) is0 += x16;
+            else is1 += x16;
+        }
+        hw[k] = h, lw[k] = l;
+    }
+    uint4 *ph = (uint4 *)(a.hi + 32 * g), *pl = (uint4 *)(a.lo + 32 * g);
+    ph[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    ph[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+    pl[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    pl[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+    a.scale[g] = amax / 16383.0f;
+    a.sum[g] = s;
+    a.isum[2 * g] = is0;
+    a.isum[2 * g + 1] = is1;
+}
+
+template <int NT>
+__device__ inline void build_act(const float *__restrict__ x, const float *__restrict__ norm_w, float eps, int n,
+                                 const Act &a, float *red) {
+    float s = 1.0f;
+    if (norm_w) {
+        float ss = 0.f;
+        for (int i = 4 * threadIdx.x; i < n; i += 4 * NT) {
+            const float4 v = *(const float4 *)(x + i);
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ss = wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        ss = 0.f;
+#pragma unroll
+        for (int w = 0; w < NT / 64; w++) ss += red[w];
+        s = 1.0f / sqrtf(ss / (float)n + eps);
+    }
+    for (int g = threadIdx.x; g < n / 32; g += NT) {
+        float v[32];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 f = *(const float4 *)(x + 32 * g + 4 * k);
+            v[4 * k] = f.x, v[4 * k + 1] = f.y, v[4 * k + 2] = f.z, v[4 * k + 3] = f.w;
+        }
+        if (norm_w) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const float4 w = *(const float4 *)(norm_w + 32 * g + 4 * k);
+                v[4 * k] = v[4 * k] * s * w.x;
+                v[4 * k + 1] = v[4 * k + 1] * s * w.y;
+                v[4 * k + 2] = v[4 * k + 2] * s * w.z;
+                v[4 * k + 3] = v[4 * k + 3] * s * w.w;
+            }
+        }
+        quant_group_lds(v, a, g);
+    }
+    __syncthreads();
+}
+
+enum { MV_STORE = 0, MV_ADD = 1, MV_GLU = 2, MV_ARGMAX = 3 };
+
+struct MvArgs {
+    uint32_t t;
+    const void *w, *w2;  // w2: the up projection of MV_GLU
+    int64_t nrows;
+    int nb, n_in;
+    const float *x, *norm_w;
+    float eps;
+    float *y;
+    // MV_ARGMAX: per-workgroup best (value, row), the last workgroup's counter,
+    // and where the winning id goes: out[0], and seq[*pos + 1] with ++*pos
+    // when seq is given.
+    float *best_v;
+    int *best_i, *counter;
+    int32_t *out, *seq, *pos;
+};
+
+template <class F, int R>
+__device__ inline void load_rows(const WPtr &w, int64_t row0, int64_t nrows, int nb, int b, int sub,
+                                 typename F::W (&wf)[R]) {
+    const int bb = min(b, nb - 1);  // lanes past the row's end re-read its last block (in bounds), not used
+#pragma unroll
+    for (int r = 0; r < R; r++) wf[r] = F::load_w(w, min(row0 + r, nrows - 1), nb, bb, sub);
+}
+
+
+// (v, i) across the wave: larger value, then lower index.
+__device__ inline void best_pick_wave(float &v, int &i) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float w = __shfl_xor(v, o, WAVE);
+        const int j = __shfl_xor(i, o, WAVE);
+        if (w > v || (w == v && j < i)) v = w, i = j;
+    }
+}
+
+// The workgroup `wg` of `nwg` computes its row groups of a.  before_act()
+// runs after the first weight loads are issued and before the activation is
+// built (the persistent kernel's grid barrier). lds: act_bytes(a.n_in)
+// bytes; red: NT/64 floats. MV_ARGMAX returns this workgroup's best
+// (value, row) in best_v / best_i (every thread).
+template <class F, int R, int WAVES, int MODE, class Hook>
+__device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, float *red, Hook before_act,
+                              float &best_v, int &best_i) {
+    constexpr int NT = WAVES * WAVE, BPI = WAVE / F::LPB, NW = MODE == MV_GLU ? 2 : 1;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, bsub = lane / F::LPB, sub = lane % F::LPB;
+    const int64_t rpg = (int64_t)R * WAVES;
+    const int64_t ngroups = (a.nrows + rpg - 1) / rpg;
+    const int spg = (a.nb + BPI - 1) / BPI;  // steps per row group
+    const int64_t nblocks = (int64_t)a.nb * a.nrows;
+    const WPtr w1 = wptr(a.t, a.w, nblocks), w2 = wptr(a.t, MODE == MV_GLU ? a.w2 : a.w, nblocks);
+    best_v = -INFINITY;
+    best_i = INT_MAX;
+
+    int64_t g = wg;
+    int it = 0;
+    typename F::W cur[NW][R], nxt[NW][R];
+    if (g < ngroups) {
+        const int64_t row0 = g * rpg + (int64_t)wave * R;
+        load_rows<F, R>(w1, row0, a.nrows, a.nb, bsub, sub, cur[0]);
+        if (MODE == MV_GLU) load_rows<F, R>(w2, row0, a.nrows, a.nb, bsub, sub, cur[NW - 1]);
+    }
+    before_act();
+    const Act xa = act_view(lds, a.n_in);
+    if (g < ngroups) build_act<NT>(a.x, a.norm_w, a.eps, a.n_in, xa, red);
+    const CAct x{xa.hi, xa.lo, xa.scale, xa.sum, xa.isum};
+
+    float acc[NW][R];
+#pragma unroll
+    for (int k = 0; k < NW; k++)
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[k][r] = 0.f;
+    while (g < ngroups) {
+        int64_t gn = g;
+        int itn = it + 1;
+        if (itn == spg) itn = 0, gn = g + nwg;
+        const bool more = gn < ngroups;
+        if (more) {
+            const int64_t row0n = gn * rpg + (int64_t)wave * R;
+            load_rows<F, R>(w1, row0n, a.nrows, a.nb, itn * BPI + bsub, sub, nxt[0]);
+            if (MODE == MV_GLU) load_rows<F, R>(w2, row0n, a.nrows, a.nb, itn * BPI + bsub, sub, nxt[NW - 1]);
+        }
+        const int b = it * BPI + bsub;
+        if (b < a.nb) {
+            const typename F::X xf = F::load_x(x, b, sub);
+#pragma unroll
+            for (int k = 0; k < NW; k++)
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[k][r] += F::dot(cur[k][r], xf, sub);
+        }
+        if (it == spg - 1) {
+            const int64_t row0 = g * rpg + (int64_t)wave * R;
+#pragma unroll
+            for (int k = 0; k < NW; k++)
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[k][r] = wave_sum(acc[k][r]);
+            if (lane < R && row0 + lane < a.nrows) {
+                float v = acc[0][0], u = acc[NW - 1][0];
+#pragma unroll
+                for (int r = 1; r < R; r++)
+                    if (lane == r) v = acc[0][r], u = acc[NW - 1][r];
+                const int64_t row = row0 + lane;
+                if (MODE == MV_ADD) {
+                    a.y[row] += v;
+                } else if (MODE == MV_GLU) {
+                    a.y[row] = v / (1.0f + expf(-v)) * u;  // engine/src/cpu_backend.cpp:260-261
+                } else {
+                    a.y[row] = v;
+                    if (MODE == MV_ARGMAX && (v > best_v || (v == best_v && row < best_i))) best_v = v, best_i = (int)row;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < NW; k++)
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[k][r] = 0.f;
+        }
+        if (!more) break;
+#pragma unroll
+        for (int k = 0; k < NW; k++)
+#pragma unroll
+            for (int r = 0; r < R; r++) cur[k][r] = nxt[k][r];
+        g = gn, it = itn;
+    }
+    if (MODE == MV_ARGMAX) {
+        // The first maximum wins (std::max_element): larger value, then lower row.
+        best_pick_wave(best_v, best_i);
+        __syncthreads();
+        if (lane == 0) red[wave] = best_v, red[WAVES + wave] = __int_as_float(best_i);
+        __syncthreads();
+        for (int k = 0; k < WAVES; k++) {
+            const float v = red[k];
+            const int i = __float_as_int(red[WAVES + k]);
+            if (v > best_v || (v == best_v && i < best_i)) best_v = v, best_i = i;
+        }
+        __syncthreads();
+    }
+}
+
+struct NoHook {
+    __device__ void operator()() const {}
+};
+
+}  // namespace ts5hip

@@ -10,49 +10,6 @@
 
 namespace ts5hip {
 
-// ---------------------------------------------------------------------------
-// Value i of row `row` in the HBM layout of a tensor with nb blocks per row
-// (bit-exact with dequantize_row).
-// ---------------------------------------------------------------------------
-__device__ inline float unpack_value(uint32_t t, const uint8_t *base, int64_t nblocks, int64_t row, int nb,
-                                     int64_t i) {
-    switch (t) {
-    case T_F32:
-        return ((const float *)base)[row * nb + i];
-    case T_F16:
-        return h2f(((const uint16_t *)base)[row * nb + i]);
-    case T_Q8_0: {
-        const int64_t blk = row * nb + i / 32;
-        const uint16_t *ds = (const uint16_t *)(base + split_scale_offset(T_Q8_0, nblocks));
-        return (float)((const int8_t *)base)[blk * Q8_BODY + (i & 31)] * h2f(ds[blk]);
-    }
-    case T_Q4_K: {
-        const uint8_t *b = base + (row * nb + i / 256) * Q4K_BYTES;
-        const int j = (int)(i & 255), s = j / 32, pos = j & 31;
-        const uint32_t *w = (const uint32_t *)b;
-        int sc, m;
-        kq_scale_min(s, w[1], w[2], w[3], sc, m);
-        const float d = h2f(w[0] & 0xffff), dmin = h2f(w[0] >> 16);
-        const float dl = d * (float)sc, ml = dmin * (float)m;
-        const uint8_t q = b[16 + 32 * (s / 2) + pos];
-        const int qv = (s & 1) ? (q >> 4) : (q & 15);
-        return dl * (float)qv - ml;
-    }
-    case T_Q6_K: {
-        const int64_t blk = row * nb + i / 256;
-        const uint8_t *b = base + blk * Q6K_BODY;
-        const uint16_t *ds = (const uint16_t *)(base + split_scale_offset(T_Q6_K, nblocks));
-        const int j = (int)(i & 255), half = j / 128, c = (j & 127) / 32, ii = j & 31;
-        const uint8_t ql = b[64 * half + ii + 32 * (c & 1)];
-        const uint8_t qh = b[128 + 32 * half + ii];
-        const int q = (int)(((c >> 1) ? (ql >> 4) : (ql & 15)) | (((qh >> (2 * c)) & 3) << 4)) - 32;
-        const int8_t sc = (int8_t)b[192 + 8 * half + ii / 16 + 2 * c];
-        return h2f(ds[blk]) * (float)sc * (float)q;
-    }
-    }
-    return 0.f;
-}
-
 __global__ void k_dequant(uint32_t t, const uint8_t *__restrict__ w, int64_t ne0, int64_t rows, float *__restrict__ y) {
     const int bv = block_values(t);
     const int nb = (int)(ne0 / bv);

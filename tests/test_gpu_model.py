@@ -27,6 +27,14 @@ def ctx():
     c.close()
 
 
+# The two token paths: the whole-token persistent kernel, and the same kernels
+# launched one per phase from a replayed HIP graph (TS5HIP_DECODE=0).
+@pytest.fixture(params=["persistent", "graphs"], autouse=True)
+def token_path(request, monkeypatch):
+    monkeypatch.setenv("TS5HIP_DECODE", "1" if request.param == "persistent" else "0")
+    return request.param
+
+
 def load(ctx, name, n_ctx):
     hp = dict(MODELS[name]["hparams"])
     tensors = synth.model_tensors(hp, make_golden.MODEL_SEED)

@@ -268,22 +268,19 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
         const int pp = tid + 256 * k;
         if (pp < NPAIR) {
             const int g = (2 * pp) / HD, d = (2 * pp) % HD;
-            pb[g * rec + d] = o[k][0];
-            pb[g * rec + d + 1] = o[k][1];
+            st_dev(pb + g * rec + d, o[k][0]);
+            st_dev(pb + g * rec + d + 1, o[k][1]);
         }
     }
     if (tid < G) {
-        pb[tid * rec + HD] = m_s[tid];
-        pb[tid * rec + HD + 1] = l_s[tid];
+        st_dev(pb + tid * rec + HD, m_s[tid]);
+        st_dev(pb + tid * rec + HD + 1, l_s[tid]);
     }
+    wait_stores();
     __syncthreads();
-    if (tid == 0) {
-        __threadfence();
-        S.last = atomicAdd(a.counters + b * a.HKV + kvh, 1) == n_split - 1;
-    }
+    if (tid == 0) S.last = atomicAdd(a.counters + b * a.HKV + kvh, 1) == n_split - 1;
     __syncthreads();
     if (!S.last) return;
-    __threadfence();
     const float *p_all = a.part + ((int64_t)b * n_split * a.H + (int64_t)kvh * G) * rec;
     const int64_t sstride = (int64_t)a.H * rec;
     // Every split's (m, l) in one round of loads, then the weights e^(m_s - M).
@@ -312,9 +309,9 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
         float acc = 0.f;
 #pragma unroll 8
         for (int sp = 0; sp < n_split; sp++) acc += S.mw[sp][g] * pd[sp * sstride];
-        a.out[(int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d] = acc / red[g];
+        st_dev(a.out + (int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d, acc / red[g]);
     }
-    if (tid == 0) a.counters[b * a.HKV + kvh] = 0;  // ready for the next launch
+    if (tid == 0) st_dev(a.counters + b * a.HKV + kvh, 0);  // ready for the next use
 }
 
 }  // namespace ts5hip

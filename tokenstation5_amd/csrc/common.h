@@ -121,6 +121,17 @@ __device__ inline uint16_t f2h(float f) {
 
 __device__ inline int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// Cross-workgroup data. A store another workgroup will read goes out
+// device-coherent (global_store ... sc1, written through past this XCD's L2);
+// the writer waits for its stores (s_waitcnt vmcnt(0): __syncthreads does not
+// on gfx950) before signalling, with a relaxed atomic, that they are done.
+// Readers use ordinary cached loads of addresses that were not read earlier in
+// the same kernel, so no stale copy can sit in their L1/L2. None of this needs
+// buffer_wbl2 / buffer_inv, which __threadfence() would emit.
+__device__ inline void st_dev(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ inline void st_dev(int *p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ inline void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
 template <typename T>
 __device__ inline T wave_sum(T v) {
 #pragma unroll

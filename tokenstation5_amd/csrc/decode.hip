@@ -32,28 +32,36 @@ struct GridBar {
 
 constexpr unsigned BAR_SPIN_LIMIT = 1u << 22;  // ~seconds of waiting
 
+__device__ inline unsigned ld_rlx(unsigned *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+// Every workgroup of the grid arrives (its stores performed) before any leaves.
+// Relaxed device-scope atomics only: the data handoff is by coherent stores
+// into buffers no reader has cached (common.h), so no cache maintenance.
 __device__ inline void grid_barrier(GridBar *bar, unsigned nwg, int *lds_flag) {
+    wait_stores();
     __syncthreads();
     if (threadIdx.x == 0) {
-        int err = __hip_atomic_load(&bar->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int err = __hip_atomic_load(&bar->err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (!err) {
-            const unsigned g = __hip_atomic_load(&bar->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __threadfence();
-            const unsigned arrived = __hip_atomic_fetch_add(&bar->count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned g = ld_rlx(&bar->gen);
+            const unsigned arrived = __hip_atomic_fetch_add(&bar->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (arrived == nwg - 1) {
-                __hip_atomic_store(&bar->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(&bar->gen, g + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                // Reset the count before publishing the new generation: the
+                // generation stored depends on the exchange's result, so it
+                // cannot be issued first.
+                const unsigned old = __hip_atomic_exchange(&bar->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&bar->gen, g + 1 + (old == 0xffffffffu ? 1u : 0u), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             } else {
                 unsigned spins = 0;
-                while (__hip_atomic_load(&bar->gen, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == g) {
-                    __builtin_amdgcn_s_sleep(2);
+                while (ld_rlx(&bar->gen) == g) {
+                    __builtin_amdgcn_s_sleep(1);
                     if (++spins > BAR_SPIN_LIMIT) {
                         __hip_atomic_store(&bar->err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         break;
                     }
                 }
             }
-            __threadfence();
         }
         *lds_flag = err;
     }
@@ -74,7 +82,11 @@ struct DecParams {
     uint32_t t_embd, t_head;
     const void *embd, *head;
     const float *out_norm, *rope;
-    float *x, *qkv, *att, *ffn, *logits, *part;
+    // The token's arena: every phase writes buffers of its own (x: 2 L + 1
+    // versions of the residual), strides in floats, 256-byte aligned.
+    float *x, *qkv, *att, *ffn, *part;
+    int64_t sx, sqkv, satt, sffn, spart;
+    float *logits;
     int *counters;  // [HKV] attention merges
     int32_t *seq, *state;
     int head_mode;  // 0: none, 1: logits, 2: logits + greedy argmax into seq[p + 1]
@@ -95,10 +107,10 @@ __device__ inline void mv_phase(const MvArgs &a, int wg, int nwg, uint8_t *lds, 
 }
 
 __device__ inline MvArgs mv_of(uint32_t t, const void *w, const void *w2, int64_t rows, int n_in, const float *x,
-                               const float *norm_w, float eps, float *y) {
+                               const float *norm_w, float eps, float *y, const float *y_in = nullptr) {
     MvArgs a{};
     a.t = t, a.w = w, a.w2 = w2, a.nrows = rows, a.nb = n_in / block_values(t), a.n_in = n_in;
-    a.x = x, a.norm_w = norm_w, a.eps = eps, a.y = y;
+    a.x = x, a.norm_w = norm_w, a.eps = eps, a.y = y, a.y_in = y_in;
     return a;
 }
 
@@ -123,28 +135,30 @@ __global__ __launch_bounds__(256) void k_decode(DecParams p) {
         const int chunk = (p.E + nwg - 1) / nwg;
         const int i0 = wg * chunk, i1 = min(p.E, i0 + chunk);
         for (int i = i0 + threadIdx.x; i < i1; i += 256)
-            p.x[i] = unpack_value(p.t_embd, (const uint8_t *)p.embd, (int64_t)nb * p.V, row, nb, i);
+            st_dev(p.x + i, unpack_value(p.t_embd, (const uint8_t *)p.embd, (int64_t)nb * p.V, row, nb, i));
     }
 
     AttnArgs at{};
     at.q_stride = p.QR, at.rope = 1, at.append = 1, at.eps = p.eps, at.rope_cs = (const float2 *)p.rope;
     at.n_rot = p.n_rot, at.neox = p.neox, at.kv_per_batch = 0, at.n_ctx = p.n_ctx, at.H = p.H, at.HKV = p.HKV;
-    at.n_keys = p.state, at.scale = p.scale, at.part = p.part, at.counters = p.counters;
-    at.q = p.qkv, at.out = p.att;
+    at.n_keys = p.state, at.scale = p.scale, at.counters = p.counters;
 
     for (int l = 0; l < p.n_layer; l++) {
         const DecLayer &L = p.layers[l];
-        mv_phase<MV_STORE>(mv_of(L.t_qkv, L.qkv, nullptr, p.QR, p.E, p.x, L.attn_norm, p.eps, p.qkv), wg, nwg, lds,
-                           red, barrier, bv, bi);
+        float *x0 = p.x + 2 * l * p.sx, *x1 = x0 + p.sx, *x2 = x1 + p.sx;
+        float *qkv = p.qkv + l * p.sqkv, *att = p.att + l * p.satt, *ffn = p.ffn + l * p.sffn;
+        mv_phase<MV_STORE>(mv_of(L.t_qkv, L.qkv, nullptr, p.QR, p.E, x0, L.attn_norm, p.eps, qkv), wg, nwg, lds, red,
+                           barrier, bv, bi);
         barrier();
         at.kv = L.kv, at.bias = L.bias, at.q_norm = L.q_norm, at.k_norm = L.k_norm;
+        at.q = qkv, at.out = att, at.part = p.part + l * p.spart;
         for (int item = wg; item < p.HKV * p.n_split; item += nwg)
             attn_item<HD, G>(at, item / p.HKV, item % p.HKV, 0, p.n_split, S);
-        mv_phase<MV_ADD>(mv_of(L.t_wo, L.wo, nullptr, p.E, p.H * HD, p.att, nullptr, 0.f, p.x), wg, nwg, lds, red,
+        mv_phase<MV_ADD>(mv_of(L.t_wo, L.wo, nullptr, p.E, p.H * HD, att, nullptr, 0.f, x1, x0), wg, nwg, lds, red,
                          barrier, bv, bi);
-        mv_phase<MV_GLU>(mv_of(L.t_gu, L.gate, L.up, p.F, p.E, p.x, L.ffn_norm, p.eps, p.ffn), wg, nwg, lds, red,
+        mv_phase<MV_GLU>(mv_of(L.t_gu, L.gate, L.up, p.F, p.E, x1, L.ffn_norm, p.eps, ffn), wg, nwg, lds, red,
                          barrier, bv, bi);
-        mv_phase<MV_ADD>(mv_of(L.t_down, L.down, nullptr, p.E, p.F, p.ffn, nullptr, 0.f, p.x), wg, nwg, lds, red,
+        mv_phase<MV_ADD>(mv_of(L.t_down, L.down, nullptr, p.E, p.F, ffn, nullptr, 0.f, x2, x1), wg, nwg, lds, red,
                          barrier, bv, bi);
     }
     if (p.head_mode == 0) {
@@ -152,7 +166,8 @@ __global__ __launch_bounds__(256) void k_decode(DecParams p) {
         if (wg == 0 && threadIdx.x == 0) p.state[0] = pos + 1;
         return;
     }
-    const MvArgs ha = mv_of(p.t_head, p.head, nullptr, p.V, p.E, p.x, p.out_norm, p.eps, p.logits);
+    const MvArgs ha = mv_of(p.t_head, p.head, nullptr, p.V, p.E, p.x + 2 * p.n_layer * p.sx, p.out_norm, p.eps,
+                            p.logits);
     if (p.head_mode == 1) {
         mv_phase<MV_STORE>(ha, wg, nwg, lds, red, barrier, bv, bi);
         barrier();
@@ -161,8 +176,8 @@ __global__ __launch_bounds__(256) void k_decode(DecParams p) {
     }
     mv_phase<MV_ARGMAX>(ha, wg, nwg, lds, red, barrier, bv, bi);
     if (threadIdx.x == 0) {
-        p.best_v[wg] = bv;
-        p.best_i[wg] = bi;
+        st_dev(p.best_v + wg, bv);
+        st_dev(p.best_i + wg, bi);
     }
     barrier();
     if (wg != 0) return;
@@ -235,7 +250,8 @@ hipError_t launch_decode(const DecodeIn &in, hipStream_t s) {
     p.n_split = in.n_split, p.eps = in.eps, p.scale = in.scale, p.layers = (const DecLayer *)in.layers;
     p.t_embd = in.t_embd, p.t_head = in.t_head, p.embd = in.embd, p.head = in.head, p.out_norm = in.out_norm;
     p.rope = in.rope, p.x = in.x, p.qkv = in.qkv, p.att = in.att, p.ffn = in.ffn, p.logits = in.logits;
-    p.part = in.part, p.counters = in.counters, p.seq = in.seq, p.state = in.state, p.head_mode = in.head_mode;
+    p.part = in.part, p.sx = in.sx, p.sqkv = in.sqkv, p.satt = in.satt, p.sffn = in.sffn, p.spart = in.spart;
+    p.counters = in.counters, p.seq = in.seq, p.state = in.state, p.head_mode = in.head_mode;
     p.bar = (GridBar *)in.bar, p.best_v = in.best_v, p.best_i = in.best_i;
     void *args[] = {&p};
     return hipLaunchCooperativeKernel(f, dim3(in.grid), dim3(256), args, in.lds_bytes, s);

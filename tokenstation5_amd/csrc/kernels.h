@@ -84,7 +84,11 @@ struct DecodeIn {
     uint32_t t_embd, t_head;
     const void *embd, *head;
     const float *out_norm, *rope;
-    float *x, *qkv, *att, *ffn, *logits, *part;
+    // Arena: x [2 n_layer + 1][sx], qkv [n_layer][sqkv], att [n_layer][satt],
+    // ffn [n_layer][sffn], part [n_layer][spart] (floats, 256-byte aligned rows).
+    float *x, *qkv, *att, *ffn, *part;
+    int64_t sx, sqkv, satt, sffn, spart;
+    float *logits;
     int *counters;         // [HKV], zero
     int32_t *seq, *state;  // state[0] position, state[1] greedy id
     int head_mode;         // 0: none, 1: logits, 2: logits + greedy argmax into seq[p + 1]

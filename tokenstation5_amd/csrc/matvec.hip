@@ -17,18 +17,17 @@ __global__ __launch_bounds__(WAVES *WAVE) void k_mv(MvArgs a) {
     if (MODE != MV_ARGMAX) return;
     // Each workgroup's best, then the last workgroup to finish picks the winner.
     if (threadIdx.x == 0) {
-        a.best_v[blockIdx.x] = best_v;
-        a.best_i[blockIdx.x] = best_i;
-        __threadfence();
+        st_dev(a.best_v + blockIdx.x, best_v);
+        st_dev(a.best_i + blockIdx.x, best_i);
+        wait_stores();
         last = atomicAdd(a.counter, 1) == (int)gridDim.x - 1;
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();
     best_v = -INFINITY, best_i = INT_MAX;
     for (int k = threadIdx.x; k < (int)gridDim.x; k += WAVES * WAVE) {
-        const float v = __hip_atomic_load(a.best_v + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int i = __hip_atomic_load(a.best_i + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float v = a.best_v[k];
+        const int i = a.best_i[k];
         if (v > best_v || (v == best_v && i < best_i)) best_v = v, best_i = i;
     }
     best_pick_wave(best_v, best_i);
@@ -48,7 +47,7 @@ __global__ __launch_bounds__(WAVES *WAVE) void k_mv(MvArgs a) {
             a.seq[p + 1] = best_i;
             *a.pos = p + 1;
         }
-        *a.counter = 0;  // ready for the next launch (graph replays)
+        st_dev(a.counter, 0);  // ready for the next launch (graph replays)
     }
 }
 
@@ -85,7 +84,7 @@ static MvArgs mv_args(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const
                       float eps, float *y) {
     MvArgs a{};
     a.t = t, a.w = w, a.w2 = nullptr, a.nrows = ne1, a.nb = (int)(ne0 / block_values(t)), a.n_in = (int)ne0;
-    a.x = x, a.norm_w = norm_w, a.eps = eps, a.y = y;
+    a.x = x, a.norm_w = norm_w, a.eps = eps, a.y = y, a.y_in = y;
     return a;
 }
 

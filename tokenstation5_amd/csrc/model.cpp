@@ -80,6 +80,8 @@ struct ts5hip_model {
     int dec_grid = 0, dec_split = 32;
     size_t dec_lds = 0;
     void *dec_layers = nullptr, *bar = nullptr;
+    float *arena = nullptr;  // the persistent kernel's per-phase buffers
+    int64_t a_sx = 0, a_sqkv = 0, a_satt = 0, a_sffn = 0, a_spart = 0;
     float *dec_best_v = nullptr;
     int *dec_best_i = nullptr;
     // Profile (TS5HIP_PROFILE set): GPU time per forward call.
@@ -400,12 +402,21 @@ int prepare_decode(ts5hip_model *m) {
         TS5_HIP(m->ctx, hipMemsetAsync(m->bar, 0, decode_bar_bytes(), m->ctx->stream));
     }
     if (!m->dec_best_v) {
-        if (int rc = alloc_t(m, (size_t)grid, &m->dec_best_v)) return rc;
-        if (int rc = alloc_t(m, (size_t)grid, &m->dec_best_i)) return rc;
+        if (int rc = alloc_t(m, align_up((size_t)grid, 64), &m->dec_best_v)) return rc;
+        if (int rc = alloc_t(m, align_up((size_t)grid, 64), &m->dec_best_i)) return rc;
+    }
+    const int split = std::min(64, std::max(1, 256 / hp.n_head_kv));
+    if (!m->arena) {
+        auto row = [](int64_t n) { return (int64_t)align_up((size_t)n, 64); };  // 256-byte rows
+        m->a_sx = row(hp.n_embd), m->a_sqkv = row(m->qkv_rows()), m->a_satt = row((int64_t)hp.n_head * hp.head_dim);
+        m->a_sffn = row(hp.n_ff), m->a_spart = row((int64_t)split * hp.n_head * (hp.head_dim + 2));
+        const int64_t L = hp.n_layer;
+        const size_t n = (size_t)((2 * L + 1) * m->a_sx + L * (m->a_sqkv + m->a_satt + m->a_sffn + m->a_spart));
+        if (int rc = alloc_t(m, n, &m->arena)) return rc;
     }
     if (int rc = ts5hip_upload(m->ctx, m->dec_layers, host.data(), host.size())) return rc;
     m->dec_grid = grid, m->dec_lds = lds;
-    m->dec_split = std::min(64, std::max(1, 256 / hp.n_head_kv));
+    m->dec_split = split;
     m->use_decode = true;
     return TS5HIP_OK;
 }
@@ -418,8 +429,12 @@ int launch_decode_token(ts5hip_model *m, int head_mode) {
     in.V = hp.n_vocab, in.n_layer = hp.n_layer, in.n_ctx = m->n_ctx, in.n_rot = hp.rope_dims;
     in.neox = hp.rope_neox, in.n_split = m->dec_split, in.eps = hp.rms_eps, in.scale = hp.attn_scale;
     in.layers = m->dec_layers, in.t_embd = m->tok_embd.type, in.t_head = out.type, in.embd = m->tok_embd.d;
-    in.head = out.d, in.out_norm = (const float *)m->out_norm.d, in.rope = m->rope_cs, in.x = m->x;
-    in.qkv = m->qkv, in.att = m->att, in.ffn = m->ffn, in.logits = m->logits, in.part = m->part;
+    in.head = out.d, in.out_norm = (const float *)m->out_norm.d, in.rope = m->rope_cs;
+    const int64_t L = hp.n_layer;
+    in.x = m->arena, in.qkv = in.x + (2 * L + 1) * m->a_sx, in.att = in.qkv + L * m->a_sqkv;
+    in.ffn = in.att + L * m->a_satt, in.part = in.ffn + L * m->a_sffn;
+    in.sx = m->a_sx, in.sqkv = m->a_sqkv, in.satt = m->a_satt, in.sffn = m->a_sffn, in.spart = m->a_spart;
+    in.logits = m->logits;
     in.counters = m->counters, in.seq = m->seq, in.state = m->state, in.head_mode = head_mode, in.bar = m->bar;
     in.best_v = m->dec_best_v, in.best_i = m->dec_best_i, in.grid = m->dec_grid, in.lds_bytes = m->dec_lds;
     TS5_HIP(m->ctx, launch_decode(in, m->ctx->stream));

@@ -320,6 +320,7 @@ struct MvArgs {
     const float *x, *norm_w;
     float eps;
     float *y;
+    const float *y_in;  // MV_ADD: y[r] = y_in[r] + W x (y_in may be y)
     // MV_ARGMAX: per-workgroup best (value, row), the last workgroup's counter,
     // and where the winning id goes: out[0], and seq[*pos + 1] with ++*pos
     // when seq is given.
@@ -414,11 +415,11 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
                     if (lane == r) v = acc[0][r], u = acc[NW - 1][r];
                 const int64_t row = row0 + lane;
                 if (MODE == MV_ADD) {
-                    a.y[row] += v;
+                    st_dev(a.y + row, a.y_in[row] + v);
                 } else if (MODE == MV_GLU) {
-                    a.y[row] = v / (1.0f + expf(-v)) * u;  // engine/src/cpu_backend.cpp:260-261
+                    st_dev(a.y + row, v / (1.0f + expf(-v)) * u);  // engine/src/cpu_backend.cpp:260-261
                 } else {
-                    a.y[row] = v;
+                    st_dev(a.y + row, v);
                     if (MODE == MV_ARGMAX && (v > best_v || (v == best_v && row < best_i))) best_v = v, best_i = (int)row;
                 }
             }

@@ -97,7 +97,10 @@ struct DecodeIn {
     int *best_i;  // grid entries each
     int grid;
     size_t lds_bytes;
+    uint64_t *trace;  // optional phase timestamps (decode_trace_len() entries)
 };
+// Phase timestamps one token records: start, each barrier, the end.
+inline int decode_trace_len(int n_layer) { return 2 + 5 * n_layer + 3; }
 size_t decode_layer_bytes();
 size_t decode_bar_bytes();
 int decode_grid(int HD, int G, int n_cu, size_t lds_bytes);

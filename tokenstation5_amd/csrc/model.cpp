@@ -81,6 +81,10 @@ struct ts5hip_model {
     size_t dec_lds = 0;
     void *dec_layers = nullptr, *bar = nullptr;
     float *arena = nullptr;  // the persistent kernel's per-phase buffers
+    uint64_t *trace = nullptr;           // phase timestamps (profile mode)
+    std::vector<uint64_t> trace_host;
+    double phase_us[8] = {0};            // embed qkv attn wo glu down head final
+    int phase_tokens = 0;
     int64_t a_sx = 0, a_sqkv = 0, a_satt = 0, a_sffn = 0, a_spart = 0;
     float *dec_best_v = nullptr;
     int *dec_best_i = nullptr;
@@ -415,6 +419,10 @@ int prepare_decode(ts5hip_model *m) {
         if (int rc = alloc_t(m, n, &m->arena)) return rc;
     }
     if (int rc = ts5hip_upload(m->ctx, m->dec_layers, host.data(), host.size())) return rc;
+    if (m->profile && !m->trace) {
+        if (int rc = alloc_t(m, (size_t)decode_trace_len(hp.n_layer), &m->trace)) return rc;
+        m->trace_host.assign((size_t)decode_trace_len(hp.n_layer), 0);
+    }
     m->dec_grid = grid, m->dec_lds = lds;
     m->dec_split = split;
     m->use_decode = true;
@@ -437,7 +445,23 @@ int launch_decode_token(ts5hip_model *m, int head_mode) {
     in.logits = m->logits;
     in.counters = m->counters, in.seq = m->seq, in.state = m->state, in.head_mode = head_mode, in.bar = m->bar;
     in.best_v = m->dec_best_v, in.best_i = m->dec_best_i, in.grid = m->dec_grid, in.lds_bytes = m->dec_lds;
+    in.trace = m->profile ? m->trace : nullptr;
     TS5_HIP(m->ctx, launch_decode(in, m->ctx->stream));
+    if (m->profile) {
+        // Workgroup 0's timestamps at each phase start (100 MHz): per-phase time
+        // including the barrier that ends the phase.
+        const int n = 1 + 5 * hp.n_layer + (head_mode == 2 ? 3 : head_mode == 1 ? 2 : 1);
+        TS5_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+        TS5_HIP(m->ctx, hipMemcpy(m->trace_host.data(), m->trace, (size_t)n * 8, hipMemcpyDeviceToHost));
+        const uint64_t *t = m->trace_host.data();
+        auto us = [&](int k) { return (double)(t[k + 1] - t[k]) / 100.0; };
+        m->phase_us[0] += us(0);
+        for (int l = 0; l < hp.n_layer; l++)
+            for (int ph = 0; ph < 5; ph++) m->phase_us[1 + ph] += us(1 + 5 * l + ph);
+        if (head_mode >= 1) m->phase_us[6] += us(5 * hp.n_layer);
+        if (head_mode == 2) m->phase_us[7] += us(5 * hp.n_layer + 1);
+        m->phase_tokens++;
+    }
     return TS5HIP_OK;
 }
 
@@ -726,7 +750,22 @@ int ts5hip_take_profile(ts5hip_model *m, char *buf, int len) {
                       m->prof_calls, m->prof_tokens, m->prof_ms, m->prof_ms / std::max(1, m->prof_tokens));
         s = line;
     }
+    if (m->profile && m->phase_tokens) {
+        static const char *names[8] = {"embed", "qkv", "attn", "wo", "ffn_glu", "ffn_down", "head", "argmax"};
+        const double n = m->phase_tokens, L = m->hp.n_layer;
+        s += "persistent kernel, us per token (per layer where it repeats):";
+        for (int k = 0; k < 8; k++) {
+            char part[96];
+            const bool per_layer = k >= 1 && k <= 5;
+            std::snprintf(part, sizeof part, " %s %.2f%s", names[k], m->phase_us[k] / n / (per_layer ? L : 1.0),
+                          per_layer ? "/layer" : "");
+            s += part;
+        }
+        s += "\n";
+    }
     m->prof_ms = 0, m->prof_calls = 0, m->prof_tokens = 0;
+    for (double &v : m->phase_us) v = 0;
+    m->phase_tokens = 0;
     std::strncpy(buf, s.c_str(), (size_t)len - 1);
     buf[len - 1] = 0;
     return TS5HIP_OK;

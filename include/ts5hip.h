@@ -43,6 +43,7 @@ typedef struct ts5hip_sampler ts5hip_sampler;
 const char *ts5hip_last_error(const ts5hip_ctx *ctx);
 /* Opens HIP device `device` and a stream on it. Fails unless it is gfx950. */
 int ts5hip_init(int device, ts5hip_ctx **out);
+/* Destroy every model of the context first (ts5hip_model_destroy uses it). */
 void ts5hip_destroy(ts5hip_ctx *ctx);
 /* Compute units, the gfx architecture name, and HBM bytes of the device. */
 int ts5hip_device_info(ts5hip_ctx *ctx, int *n_cu, char *arch, int arch_len, int64_t *hbm_bytes);

@@ -8,6 +8,7 @@ from __future__ import annotations
 import ctypes as C
 import os
 import re
+import weakref
 
 import numpy as np
 
@@ -157,6 +158,7 @@ class DeviceBuffer:
 class Context:
     def __init__(self, device: int = 0):
         self.h = None
+        self._models = weakref.WeakSet()  # destroyed before the context
         h = _vp()
         rc = lib().ts5hip_init(device, C.byref(h))
         if rc != OK:
@@ -169,6 +171,8 @@ class Context:
 
     def close(self):
         if self.h:
+            for m in list(self._models):
+                m.close()
             lib().ts5hip_destroy(self.h)
             self.h = None
 
@@ -300,12 +304,15 @@ class Model:
         h = _vp()
         ctx.check(lib().ts5hip_model_create(ctx.h, C.byref(self._hp), n_ctx, kv, C.byref(h)))
         self.h = h.value
+        ctx._models.add(self)
         self.n_vocab = hp["n_vocab"]
 
     def close(self):
-        if self.h:
+        # A model lives inside its context: after the context is gone there is
+        # nothing left to free (ts5hip_destroy must not precede model_destroy).
+        if self.h and self.ctx.h:
             lib().ts5hip_model_destroy(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):
         try:

@@ -19,7 +19,7 @@ __device__ inline void rope_pair(float &x0, float &x1, float c, float s) {
 
 // ---------------------------------------------------------------------------
 // Split-K flash decode with the token's own preparation and the merge fused
-// in. grid (n_split, HKV, B), 256 threads; query b is at position nk - 1
+// in. grid (n_split, HKV, B), NT threads; query b is at position nk - 1
 // and reads keys [0, nk):
 //   nk = n_keys[b] (kv_per_batch: B independent caches), or
 //   nk = n_keys[0] + b + 1 (one cache, a batch of consecutive positions).
@@ -28,7 +28,8 @@ __device__ inline void rope_pair(float &x0, float &x1, float c, float s) {
 // 2. `append` (B == 1): the workgroup whose key slice holds the new key
 //    rounds that token's K (RoPE'd) and V to q8, stores them at their slot,
 //    and keeps a copy in LDS that it reads instead of the cache.
-// 3. 64-key tiles: scores (4 lanes per key), online softmax per head, p*v.
+// 3. 64-key tiles: scores (NT/64 lanes per key), online softmax per head,
+//    p*v with the tile's V staged in LDS.
 // 4. The unnormalised partial (sum p*v, m, l) per head goes to `part`; the
 //    last workgroup of a (b, KV head) to finish (an atomic counter, reset by
 //    that workgroup for the next launch) merges the splits:
@@ -59,29 +60,56 @@ __device__ inline void rope_inplace(float *v, int n_rot, int neox, const float2 
 }
 
 constexpr int ATTN_MAX_SPLIT = 64;
+constexpr int ATTN_TILE = 64;
 
 template <int HD, int G>
 struct AttnLds {
     float q_s[G][HD];
-    float p_s[G][64];
+    float p_s[G][ATTN_TILE];
     float alpha_s[G], m_s[G], l_s[G], red[G];
-    float kv_s[2][HD];                 // the new token's K and V before rounding
-    __align__(16) int8_t new8[2][HD];  // ... and after, as int8
-    uint16_t new_sc[2][HD / 32];       // ... with their f16 scales
+    float kv_s[2][HD];                         // the new token's K and V before rounding
+    __align__(16) int8_t new8[2][HD];          // ... and after, as int8
+    uint16_t new_sc[2][HD / 32];               // ... with their f16 scales
+    __align__(16) int8_t vt[ATTN_TILE][HD];    // the tile's V rows
+    uint16_t vsc[ATTN_TILE][HD / 32];          // ... and their scales
     float mw[ATTN_MAX_SPLIT][G], lw[ATTN_MAX_SPLIT][G];  // the merge's (m, l), then weights
     int last;
 };
 
-// One work item (split, KV head kvh, query b) of n_split; 256 threads.
-template <int HD, int G>
+// K bytes per lane of a key's score: NQ = HD / (NT / 64) lanes' worth.
+template <int NQ>
+struct KRow {
+    uint32_t w[NQ / 4];
+};
+template <int NQ>
+__device__ inline KRow<NQ> load_krow(const int8_t *p) {
+    KRow<NQ> r;
+    if constexpr (NQ % 16 == 0) {
+#pragma unroll
+        for (int c = 0; c < NQ / 16; c++) {
+            const uint4 v = *(const uint4 *)(p + 16 * c);
+            r.w[4 * c] = v.x, r.w[4 * c + 1] = v.y, r.w[4 * c + 2] = v.z, r.w[4 * c + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < NQ / 8; c++) {
+            const uint2 v = *(const uint2 *)(p + 8 * c);
+            r.w[2 * c] = v.x, r.w[2 * c + 1] = v.y;
+        }
+    }
+    return r;
+}
+
+// One work item (split, KV head kvh, query b) of n_split; NT threads.
+template <int HD, int G, int NT>
 __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, int n_split, AttnLds<HD, G> &S) {
-    constexpr int TILE = 64, NQ = HD / 4, NPAIR = G * HD / 2, PPT = (NPAIR + 255) / 256;
+    constexpr int TILE = ATTN_TILE, NWV = NT / 64, LPK = NT / TILE, NQ = HD / LPK;
+    constexpr int NPAIR = G * HD / 2, PPT = (NPAIR + NT - 1) / NT;
+    constexpr int VP = TILE * HD / 16, VPT = (VP + NT - 1) / NT;  // 16-byte V pieces per tile, per thread
+    constexpr int NSC = TILE * (HD / 32);                          // V scales per tile
+    static_assert(NT % 64 == 0 && NQ % 8 == 0, "attention tile shape");
     auto &q_s = S.q_s;
     auto &p_s = S.p_s;
-    auto &alpha_s = S.alpha_s;
-    auto &m_s = S.m_s;
-    auto &l_s = S.l_s;
-    auto &red = S.red;
     auto &kv_s = S.kv_s;
     auto &new8 = S.new8;
     auto &new_sc = S.new_sc;
@@ -97,25 +125,25 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
     const bool has_new = a.append && pq >= p0 && pq < p1;
 
     // 1. Query heads (and the new K/V rows) into LDS.
-    for (int j = tid; j < G * HD; j += 256) {
+    for (int j = tid; j < G * HD; j += NT) {
         const int64_t e = (int64_t)(kvh * G + j / HD) * HD + j % HD;
         q_s[j / HD][j % HD] = row[e] + (a.rope && a.bias ? a.bias[e] : 0.f);
     }
     if (has_new) {
-        for (int j = tid; j < 2 * HD; j += 256) {
+        for (int j = tid; j < 2 * HD; j += NT) {
             const int64_t e = (int64_t)((j < HD ? a.H : a.H + a.HKV) + kvh) * HD + j % HD;
             kv_s[j / HD][j % HD] = row[e] + (a.bias ? a.bias[e] : 0.f);
         }
     }
     if (tid < G) {
-        m_s[tid] = -INFINITY;
-        l_s[tid] = 0.f;
+        S.m_s[tid] = -INFINITY;
+        S.l_s[tid] = 0.f;
     }
     __syncthreads();
     if (a.rope) {
         // Per-head RMSNorm (qwen3's q_norm / k_norm), then RoPE.
         if (a.q_norm || (has_new && a.k_norm)) {
-            for (int g = wave; g < G + 1; g += 4) {
+            for (int g = wave; g < G + 1; g += NWV) {
                 const float *nw = g < G ? a.q_norm : (has_new ? a.k_norm : nullptr);
                 if (!nw) continue;
                 float *v = g < G ? q_s[g] : kv_s[0];
@@ -128,7 +156,7 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
             __syncthreads();
         }
         const float2 *cs = a.rope_cs + (int64_t)pq * (a.n_rot / 2);
-        for (int j = tid; j < (G + 1) * (HD / 2); j += 256) {
+        for (int j = tid; j < (G + 1) * (HD / 2); j += NT) {
             const int g = j / (HD / 2), i = j % (HD / 2);
             if (i >= a.n_rot / 2) continue;
             if (g < G) rope_inplace(q_s[g], a.n_rot, a.neox, cs, i);
@@ -164,92 +192,103 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
     }
     __syncthreads();
 
-    // 3. Tiles of 64 keys.
+    // 2. Tiles of 64 keys: the tile's K (to registers, LPK lanes per key) and
+    //    V (to registers, then LDS) are requested together; scores; online
+    //    softmax per head; o = o * alpha + sum_k p_k v_k from LDS. The new key
+    //    comes from LDS, never from the cache it was just written to.
     float o[PPT][2];
 #pragma unroll
     for (int k = 0; k < PPT; k++) o[k][0] = o[k][1] = 0.f;
     for (int t0 = p0; t0 < p1; t0 += TILE) {
-        {   // Scores: 4 lanes per key, NQ dims each.
-            const int kk = tid >> 2, qq = tid & 3, p = t0 + kk;
+        const int nt = min(TILE, p1 - t0);
+        const int kk = tid / LPK, qq = tid % LPK, p = t0 + kk;
+        const bool kin = kk < nt, kmine = has_new && p == pq;
+        KRow<NQ> kr;
+        float ks = 0.f;
+        if (kin && !kmine) {
+            kr = load_krow<NQ>(a.kv.k + (head_base + p) * HD + qq * NQ);
+            ks = h2f(a.kv.ks[(head_base + p) * (HD / 32) + (qq * NQ) / 32]);
+        }
+        uint4 vr[VPT];
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            const int pc = tid + NT * k, key = pc / (HD / 16);
+            if (pc < VP && key < nt) vr[k] = *(const uint4 *)(a.kv.v + (head_base + t0 + key) * HD + 16 * (pc % (HD / 16)));
+        }
+        uint16_t vs[(NSC + NT - 1) / NT];
+#pragma unroll
+        for (int k = 0; k < (NSC + NT - 1) / NT; k++) {
+            const int j = tid + NT * k;
+            if (j < NSC && j / (HD / 32) < nt) vs[k] = a.kv.vs[(head_base + t0) * (HD / 32) + j];
+        }
+        {   // Scores.
             float acc[G];
 #pragma unroll
             for (int g = 0; g < G; g++) acc[g] = 0.f;
-            if (p < p1) {
-                const bool mine = has_new && p == pq;
-                uint4 w[NQ / 16];
-                float ks;
-                if (mine) {
+            if (kin) {
+                if (kmine) {
 #pragma unroll
-                    for (int c = 0; c < NQ / 16; c++) w[c] = *(const uint4 *)(new8[0] + qq * NQ + 16 * c);
+                    for (int c = 0; c < NQ / 4; c++) kr.w[c] = *(const uint32_t *)(new8[0] + qq * NQ + 4 * c);
                     ks = h2f(new_sc[0][(qq * NQ) / 32]);
-                } else {
-                    const int8_t *kp = a.kv.k + (head_base + p) * HD + qq * NQ;
-#pragma unroll
-                    for (int c = 0; c < NQ / 16; c++) w[c] = *(const uint4 *)(kp + 16 * c);
-                    ks = h2f(a.kv.ks[(head_base + p) * (HD / 32) + (qq * NQ) / 32]);
                 }
 #pragma unroll
-                for (int c = 0; c < NQ / 16; c++) {
-                    const uint32_t ws[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+                for (int e = 0; e < NQ; e++) {
+                    const float kf = (float)(int8_t)((kr.w[e >> 2] >> (8 * (e & 3))) & 0xff) * ks;
+                    const int d = qq * NQ + e;
 #pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        const float kf = (float)(int8_t)((ws[e >> 2] >> (8 * (e & 3))) & 0xff) * ks;
-                        const int d = qq * NQ + 16 * c + e;
-#pragma unroll
-                        for (int g = 0; g < G; g++) acc[g] += q_s[g][d] * kf;
-                    }
+                    for (int g = 0; g < G; g++) acc[g] += q_s[g][d] * kf;
                 }
             }
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                acc[g] += __shfl_xor(acc[g], 1, WAVE);
-                acc[g] += __shfl_xor(acc[g], 2, WAVE);
-            }
+            for (int g = 0; g < G; g++)
+#pragma unroll
+                for (int o2 = 1; o2 < LPK; o2 <<= 1) acc[g] += __shfl_xor(acc[g], o2, WAVE);
             if (qq == 0) {
 #pragma unroll
-                for (int g = 0; g < G; g++) p_s[g][kk] = p < p1 ? acc[g] * a.scale : -INFINITY;
+                for (int g = 0; g < G; g++) p_s[g][kk] = kin ? acc[g] * a.scale : -INFINITY;
             }
         }
+        // The tile's V rows into LDS (the new key's from its rounded copy).
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            const int pc = tid + NT * k, key = pc / (HD / 16), off = 16 * (pc % (HD / 16));
+            if (pc < VP && key < nt)
+                *(uint4 *)(&S.vt[key][off]) =
+                    (has_new && t0 + key == pq) ? *(const uint4 *)(new8[1] + off) : vr[k];
+        }
+#pragma unroll
+        for (int k = 0; k < (NSC + NT - 1) / NT; k++) {
+            const int j = tid + NT * k, key = j / (HD / 32);
+            if (j < NSC && key < nt) S.vsc[key][j % (HD / 32)] = (has_new && t0 + key == pq) ? new_sc[1][j % (HD / 32)] : vs[k];
+        }
         __syncthreads();
-        // Online softmax per head: wave w takes heads w, w+4.
-        for (int g = wave; g < G; g += 4) {
+        // Online softmax per head: wave w takes heads w, w + NT/64, ...
+        for (int g = wave; g < G; g += NWV) {
             const float sv = p_s[g][lane];
             const float mt = wave_max(sv);
-            const float mo = m_s[g];
+            const float mo = S.m_s[g];
             const float mn = fmaxf(mo, mt);
-            const float p = sv == -INFINITY ? 0.f : expf(sv - mn);
-            const float ls = wave_sum(p);
-            p_s[g][lane] = p;
+            const float pe = sv == -INFINITY ? 0.f : expf(sv - mn);
+            const float ls = wave_sum(pe);
+            p_s[g][lane] = pe;
             if (lane == 0) {
                 const float al = mo == -INFINITY ? 0.f : expf(mo - mn);
-                alpha_s[g] = al;
-                m_s[g] = mn;
-                l_s[g] = l_s[g] * al + ls;
+                S.alpha_s[g] = al;
+                S.m_s[g] = mn;
+                S.l_s[g] = S.l_s[g] * al + ls;
             }
         }
         __syncthreads();
-        // o = o * alpha + sum_k p_k * v_k (the new key's V from LDS).
-        const int nt = min(TILE, p1 - t0);
-        const bool new_here = has_new && pq >= t0 && pq < t0 + nt;
-        const int nc = new_here ? pq - t0 : nt;  // keys of this tile read from the cache
 #pragma unroll
         for (int k = 0; k < PPT; k++) {
-            const int pp = tid + 256 * k;
+            const int pp = tid + NT * k;
             if (pp < NPAIR) {
                 const int g = (2 * pp) / HD, d = (2 * pp) % HD;
-                const float al = alpha_s[g];
+                const float al = S.alpha_s[g];
                 float o0 = o[k][0] * al, o1 = o[k][1] * al;
-                const int8_t *vp = a.kv.v + (head_base + t0) * HD + d;
-                const uint16_t *vsp = a.kv.vs + (head_base + t0) * (HD / 32) + d / 32;
-                for (int kk = 0; kk < nc; kk++) {
-                    const uint16_t v2 = *(const uint16_t *)(vp + (int64_t)kk * HD);
-                    const float w = p_s[g][kk] * h2f(vsp[(int64_t)kk * (HD / 32)]);
-                    o0 += w * (float)(int8_t)(v2 & 0xff);
-                    o1 += w * (float)(int8_t)(v2 >> 8);
-                }
-                if (new_here) {
-                    const uint16_t v2 = *(const uint16_t *)(new8[1] + d);
-                    const float w = p_s[g][nc] * h2f(new_sc[1][d / 32]);
+                for (int j = 0; j < nt; j++) {
+                    const uint16_t v2 = *(const uint16_t *)(&S.vt[j][d]);
+                    const float w = p_s[g][j] * h2f(S.vsc[j][d / 32]);
                     o0 += w * (float)(int8_t)(v2 & 0xff);
                     o1 += w * (float)(int8_t)(v2 >> 8);
                 }
@@ -260,12 +299,12 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
         __syncthreads();
     }
 
-    // 4. Partial record per head: [HD values][m][l]; the last workgroup merges.
+    // 3. Partial record per head: [HD values][m][l]; the last workgroup merges.
     const int64_t rec = HD + 2;
     float *pb = a.part + (((int64_t)b * n_split + split) * a.H + (int64_t)kvh * G) * rec;
 #pragma unroll
     for (int k = 0; k < PPT; k++) {
-        const int pp = tid + 256 * k;
+        const int pp = tid + NT * k;
         if (pp < NPAIR) {
             const int g = (2 * pp) / HD, d = (2 * pp) % HD;
             st_dev(pb + g * rec + d, o[k][0]);
@@ -273,8 +312,8 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
         }
     }
     if (tid < G) {
-        st_dev(pb + tid * rec + HD, m_s[tid]);
-        st_dev(pb + tid * rec + HD + 1, l_s[tid]);
+        st_dev(pb + tid * rec + HD, S.m_s[tid]);
+        st_dev(pb + tid * rec + HD + 1, S.l_s[tid]);
     }
     wait_stores();
     __syncthreads();
@@ -284,7 +323,7 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
     const float *p_all = a.part + ((int64_t)b * n_split * a.H + (int64_t)kvh * G) * rec;
     const int64_t sstride = (int64_t)a.H * rec;
     // Every split's (m, l) in one round of loads, then the weights e^(m_s - M).
-    for (int j = tid; j < n_split * G; j += 256) {
+    for (int j = tid; j < n_split * G; j += NT) {
         const int sp = j / G, g = j % G;
         S.mw[sp][g] = p_all[sp * sstride + g * rec + HD];
         S.lw[sp][g] = p_all[sp * sstride + g * rec + HD + 1];
@@ -300,16 +339,16 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
             S.mw[sp][tid] = w;
             L += w * S.lw[sp][tid];
         }
-        red[tid] = L;
+        S.red[tid] = L;
     }
     __syncthreads();
-    for (int j = tid; j < G * HD; j += 256) {
+    for (int j = tid; j < G * HD; j += NT) {
         const int g = j / HD, d = j % HD;
         const float *pd = p_all + g * rec + d;
         float acc = 0.f;
 #pragma unroll 8
         for (int sp = 0; sp < n_split; sp++) acc += S.mw[sp][g] * pd[sp * sstride];
-        st_dev(a.out + (int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d, acc / red[g]);
+        st_dev(a.out + (int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d, acc / S.red[g]);
     }
     if (tid == 0) st_dev(a.counters + b * a.HKV + kvh, 0);  // ready for the next use
 }

@@ -131,10 +131,13 @@ struct DecParams {
 template <int MODE, class Hook>
 __device__ inline void mv_phase(const MvArgs &a, int wg, int nwg, uint8_t *lds, float *red, Hook hook, float &bv,
                                 int &bi) {
+    // One row per wave: the kernel's register budget (two workgroups per CU)
+    // holds the weights of one step and the next.
+    constexpr int R = 1;
     switch (a.t) {
-    case T_Q4_K: mv_run<Q4K, 1, 4, MODE>(a, wg, nwg, lds, red, hook, bv, bi); break;
-    case T_Q6_K: mv_run<Q6K, 1, 4, MODE>(a, wg, nwg, lds, red, hook, bv, bi); break;
-    default: mv_run<Q80, 1, 4, MODE>(a, wg, nwg, lds, red, hook, bv, bi); break;
+    case T_Q4_K: mv_run<Q4K, R, 4, MODE>(a, wg, nwg, lds, red, hook, bv, bi); break;
+    case T_Q6_K: mv_run<Q6K, R, 4, MODE>(a, wg, nwg, lds, red, hook, bv, bi); break;
+    default: mv_run<Q80, R, 4, MODE>(a, wg, nwg, lds, red, hook, bv, bi); break;
     }
 }
 
@@ -193,7 +196,7 @@ __global__ __launch_bounds__(256) void k_decode(DecParams p) {
         at.kv = L.kv, at.bias = L.bias, at.q_norm = L.q_norm, at.k_norm = L.k_norm;
         at.q = qkv, at.out = att, at.part = p.part + l * p.spart;
         for (int item = wg; item < p.HKV * p.n_split; item += nwg)
-            attn_item<HD, G>(at, item / p.HKV, item % p.HKV, 0, p.n_split, S);
+            attn_item<HD, G, 256>(at, item / p.HKV, item % p.HKV, 0, p.n_split, S);
         mv_phase<MV_ADD>(mv_of(L.t_wo, L.wo, nullptr, p.E, p.H * HD, att, nullptr, 0.f, x1, x0), wg, nwg, lds, red,
                          barrier, bv, bi);
         mv_phase<MV_GLU>(mv_of(L.t_gu, L.gate, L.up, p.F, p.E, x1, L.ffn_norm, p.eps, ffn), wg, nwg, lds, red,

@@ -450,7 +450,7 @@ int launch_decode_token(ts5hip_model *m, int head_mode) {
     if (m->profile) {
         // Workgroup 0's timestamps at each phase start (100 MHz): per-phase time
         // including the barrier that ends the phase.
-        const int n = 1 + 5 * hp.n_layer + (head_mode == 2 ? 3 : head_mode == 1 ? 2 : 1);
+        const int n = 2 + 5 * hp.n_layer + (head_mode == 2 ? 2 : head_mode == 1 ? 1 : 0);
         TS5_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
         TS5_HIP(m->ctx, hipMemcpy(m->trace_host.data(), m->trace, (size_t)n * 8, hipMemcpyDeviceToHost));
         const uint64_t *t = m->trace_host.data();
@@ -458,8 +458,8 @@ int launch_decode_token(ts5hip_model *m, int head_mode) {
         m->phase_us[0] += us(0);
         for (int l = 0; l < hp.n_layer; l++)
             for (int ph = 0; ph < 5; ph++) m->phase_us[1 + ph] += us(1 + 5 * l + ph);
-        if (head_mode >= 1) m->phase_us[6] += us(5 * hp.n_layer);
-        if (head_mode == 2) m->phase_us[7] += us(5 * hp.n_layer + 1);
+        if (head_mode >= 1) m->phase_us[6] += us(1 + 5 * hp.n_layer);
+        if (head_mode == 2) m->phase_us[7] += us(2 + 5 * hp.n_layer);
         m->phase_tokens++;
     }
     return TS5HIP_OK;

@@ -231,48 +231,13 @@ struct Q80 {
 
 // ---------------------------------------------------------------------------
 // The activation prologue: x (n values, optionally rms-normalised by norm_w)
-// -> Act in LDS. One thread per 32-value sub-block.
+// -> Act in LDS.
 // ---------------------------------------------------------------------------
-__device__ inline void quant_group_lds(const float *v, const Act &a, int g) {
-    float amax = 0.f, s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-        amax = fmaxf(amax, fabsf(v[i]));
-        s += v[i];
-    }
-    const float inv = amax > 0.f ? 16383.0f / amax : 0.f;
-    uint32_t hw[8], lw[8];
-    int is0 = 0, is1 = 0;
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        uint32_t h = 0, l = 0;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int i = 4 * k + e;
-            const int x16 = max(-16383, min(16383, (int)rintf(v[i] * inv)));
-            const int lo = (int)(int8_t)(x16 & 255);
-            const int hi = (x16 - lo) >> 8;
-            h |= (uint32_t)(hi & 255) << (8 * e);
-            l |= (uint32_t)(lo & 255) << (8 * e);
-            if (i < 16) is0 += x16;
-            else is1 += x16;
-        }
-        hw[k] = h, lw[k] = l;
-    }
-    uint4 *ph = (uint4 *)(a.hi + 32 * g), *pl = (uint4 *)(a.lo + 32 * g);
-    ph[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    ph[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-    pl[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-    pl[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
-    a.scale[g] = amax / 16383.0f;
-    a.sum[g] = s;
-    a.isum[2 * g] = is0;
-    a.isum[2 * g + 1] = is1;
-}
-
 template <int NT>
 __device__ inline void build_act(const float *__restrict__ x, const float *__restrict__ norm_w, float eps, int n,
                                  const Act &a, float *red) {
+    // Two threads per 32-value sub-block, 16 values each, every thread busy:
+    // the pair exchanges its max and sum once; each thread owns one 16-run.
     float s = 1.0f;
     if (norm_w) {
         float ss = 0.f;
@@ -288,24 +253,57 @@ __device__ inline void build_act(const float *__restrict__ x, const float *__res
         for (int w = 0; w < NT / 64; w++) ss += red[w];
         s = 1.0f / sqrtf(ss / (float)n + eps);
     }
-    for (int g = threadIdx.x; g < n / 32; g += NT) {
-        float v[32];
+    for (int r = threadIdx.x; r < n / 16; r += NT) {  // 16-run r, half (r & 1) of sub-block r / 2
+        float v[16];
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const float4 f = *(const float4 *)(x + 32 * g + 4 * k);
+        for (int k = 0; k < 4; k++) {
+            const float4 f = *(const float4 *)(x + 16 * r + 4 * k);
             v[4 * k] = f.x, v[4 * k + 1] = f.y, v[4 * k + 2] = f.z, v[4 * k + 3] = f.w;
         }
         if (norm_w) {
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const float4 w = *(const float4 *)(norm_w + 32 * g + 4 * k);
+            for (int k = 0; k < 4; k++) {
+                const float4 w = *(const float4 *)(norm_w + 16 * r + 4 * k);
                 v[4 * k] = v[4 * k] * s * w.x;
                 v[4 * k + 1] = v[4 * k + 1] * s * w.y;
                 v[4 * k + 2] = v[4 * k + 2] * s * w.z;
                 v[4 * k + 3] = v[4 * k + 3] * s * w.w;
             }
         }
-        quant_group_lds(v, a, g);
+        float amax = 0.f, sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            amax = fmaxf(amax, fabsf(v[i]));
+            sum += v[i];
+        }
+        // Runs 2g and 2g+1 sit in adjacent lanes (NT is a multiple of 64 and
+        // n / 16 is even, so both are in the loop together).
+        amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
+        sum += __shfl_xor(sum, 1, WAVE);
+        const float inv = amax > 0.f ? 16383.0f / amax : 0.f;
+        uint32_t hw[4], lw[4];
+        int is = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            uint32_t h = 0, l = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int x16 = max(-16383, min(16383, (int)rintf(v[4 * k + e] * inv)));
+                const int lo = (int)(int8_t)(x16 & 255);
+                const int hi = (x16 - lo) >> 8;
+                h |= (uint32_t)(hi & 255) << (8 * e);
+                l |= (uint32_t)(lo & 255) << (8 * e);
+                is += x16;
+            }
+            hw[k] = h, lw[k] = l;
+        }
+        *(uint4 *)(a.hi + 16 * r) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        *(uint4 *)(a.lo + 16 * r) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        a.isum[r] = is;
+        if ((r & 1) == 0) {
+            a.scale[r / 2] = amax / 16383.0f;
+            a.sum[r / 2] = sum;
+        }
     }
     __syncthreads();
 }

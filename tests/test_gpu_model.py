@@ -40,6 +40,8 @@ def load(ctx, name, n_ctx):
     tensors = synth.model_tensors(hp, make_golden.MODEL_SEED)
     m = ts5hip.Model(ctx, hp, n_ctx)
     m.set_tensors(tensors)
+    want = "persistent" if os.environ.get("TS5HIP_DECODE") == "1" else "graphs"
+    assert m.token_path() == want  # every test model fits the persistent kernel
     return hp, tensors, m
 
 

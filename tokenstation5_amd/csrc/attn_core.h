@@ -100,39 +100,56 @@ __device__ inline KRow<NQ> load_krow(const int8_t *p) {
     return r;
 }
 
-// One work item (split, KV head kvh, query b) of n_split; NT threads.
+// Where work item (split, kvh, b) of n_split reads keys: [p0, p1) of the nk
+// keys [0, nk) of query b (at position pq = nk - 1), in 64-key tiles.
+struct AttnSpan {
+    int pq, p0, p1;
+    int64_t head_base;  // cache slot of key 0 for this KV head
+    bool has_new;       // the new key (pq) falls in this slice
+};
+template <int TILE = ATTN_TILE>
+__device__ inline AttnSpan attn_span(const AttnArgs &a, int split, int kvh, int b, int n_split) {
+    AttnSpan sp;
+    const int nk = a.kv_per_batch ? a.n_keys[b] : a.n_keys[0] + b + 1;
+    sp.pq = nk - 1;
+    int chunk = (nk + n_split - 1) / n_split;
+    chunk = (chunk + TILE - 1) / TILE * TILE;
+    sp.p0 = split * chunk;
+    sp.p1 = min(nk, sp.p0 + chunk);
+    const int seq = a.kv_per_batch ? b : 0;
+    sp.head_base = ((int64_t)seq * a.HKV + kvh) * a.n_ctx;
+    sp.has_new = a.append && sp.pq >= sp.p0 && sp.pq < sp.p1;
+    return sp;
+}
+
 template <int HD, int G, int NT>
-__device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, int n_split, AttnLds<HD, G> &S) {
-    constexpr int TILE = ATTN_TILE, NWV = NT / 64, LPK = NT / TILE, NQ = HD / LPK;
-    constexpr int NPAIR = G * HD / 2, PPT = (NPAIR + NT - 1) / NT;
-    constexpr int VP = TILE * HD / 16, VPT = (VP + NT - 1) / NT;  // 16-byte V pieces per tile, per thread
-    constexpr int NSC = TILE * (HD / 32);                          // V scales per tile
-    static_assert(NT % 64 == 0 && NQ % 8 == 0, "attention tile shape");
+struct AttnShape {
+    static constexpr int NPAIR = G * HD / 2, PPT = (NPAIR + NT - 1) / NT;
+};
+
+// 1. The G query heads of KV head kvh (and, when the slice holds the new key,
+//    that token's K and V) into LDS, from q(e) = element e of the token's
+//    q|k|v row; bias, per-head norm and RoPE when a.rope; the new K and V
+//    rounded to q8 and stored at their cache slot.
+template <int HD, int G, int NT, class QLoad>
+__device__ inline void attn_prepare(const AttnArgs &a, int kvh, const AttnSpan &sp, AttnLds<HD, G> &S,
+                                    QLoad qload) {
+    constexpr int NWV = NT / 64;
     auto &q_s = S.q_s;
-    auto &p_s = S.p_s;
     auto &kv_s = S.kv_s;
     auto &new8 = S.new8;
     auto &new_sc = S.new_sc;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nk = a.kv_per_batch ? a.n_keys[b] : a.n_keys[0] + b + 1;
-    const int pq = nk - 1;  // the query's position
-    int chunk = (nk + n_split - 1) / n_split;
-    chunk = (chunk + TILE - 1) / TILE * TILE;
-    const int p0 = split * chunk, p1 = min(nk, p0 + chunk);
-    const int seq = a.kv_per_batch ? b : 0;
-    const int64_t head_base = ((int64_t)seq * a.HKV + kvh) * a.n_ctx;  // slot of key 0
-    const float *row = a.q + (int64_t)b * a.q_stride;
-    const bool has_new = a.append && pq >= p0 && pq < p1;
-
-    // 1. Query heads (and the new K/V rows) into LDS.
+    const int pq = sp.pq;
+    const bool has_new = sp.has_new;
     for (int j = tid; j < G * HD; j += NT) {
         const int64_t e = (int64_t)(kvh * G + j / HD) * HD + j % HD;
-        q_s[j / HD][j % HD] = row[e] + (a.rope && a.bias ? a.bias[e] : 0.f);
+        q_s[j / HD][j % HD] = qload(e) + (a.rope && a.bias ? a.bias[e] : 0.f);
     }
     if (has_new) {
         for (int j = tid; j < 2 * HD; j += NT) {
             const int64_t e = (int64_t)((j < HD ? a.H : a.H + a.HKV) + kvh) * HD + j % HD;
-            kv_s[j / HD][j % HD] = row[e] + (a.bias ? a.bias[e] : 0.f);
+            kv_s[j / HD][j % HD] = qload(e) + (a.bias ? a.bias[e] : 0.f);
         }
     }
     if (tid < G) {
@@ -181,7 +198,7 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
                 q1 = (int)fminf(127.f, fmaxf(-127.f, rintf(a1 / sc)));
             }
             const uint16_t packed = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
-            const int64_t slot = head_base + pq;
+            const int64_t slot = sp.head_base + pq;
             *(uint16_t *)(new8[which] + 2 * i) = packed;
             *(uint16_t *)((which ? a.kv.v : a.kv.k) + slot * HD + 2 * i) = packed;
             if ((i & 15) == 0) {
@@ -191,12 +208,29 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
         }
     }
     __syncthreads();
+}
 
-    // 2. Tiles of 64 keys: the tile's K (to registers, LPK lanes per key) and
-    //    V (to registers, then LDS) are requested together; scores; online
-    //    softmax per head; o = o * alpha + sum_k p_k v_k from LDS. The new key
-    //    comes from LDS, never from the cache it was just written to.
-    float o[PPT][2];
+// 2. Tiles of 64 keys over [p0, p1): the tile's K (to registers, NT/64 lanes
+//    per key) and V (to registers, then LDS) are requested together; scores;
+//    online softmax per head; o = o * alpha + sum_k p_k v_k from LDS. The new
+//    key comes from LDS, never from the cache it was just written to. o holds
+//    this thread's (head, dim pair) entries of the unnormalised output.
+template <int HD, int G, int NT>
+__device__ inline void attn_tiles(const AttnArgs &a, const AttnSpan &sp, AttnLds<HD, G> &S,
+                                  float (&o)[AttnShape<HD, G, NT>::PPT][2]) {
+    constexpr int TILE = ATTN_TILE, NWV = NT / 64, LPK = NT / TILE, NQ = HD / LPK;
+    constexpr int NPAIR = G * HD / 2, PPT = AttnShape<HD, G, NT>::PPT;
+    constexpr int VP = TILE * HD / 16, VPT = (VP + NT - 1) / NT;  // 16-byte V pieces per tile, per thread
+    constexpr int NSC = TILE * (HD / 32);                          // V scales per tile
+    static_assert(NT % 64 == 0 && NQ % 8 == 0, "attention tile shape");
+    auto &q_s = S.q_s;
+    auto &p_s = S.p_s;
+    auto &new8 = S.new8;
+    auto &new_sc = S.new_sc;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pq = sp.pq, p0 = sp.p0, p1 = sp.p1;
+    const int64_t head_base = sp.head_base;
+    const bool has_new = sp.has_new;
 #pragma unroll
     for (int k = 0; k < PPT; k++) o[k][0] = o[k][1] = 0.f;
     for (int t0 = p0; t0 < p1; t0 += TILE) {
@@ -298,6 +332,19 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
         }
         __syncthreads();
     }
+
+}
+
+// One work item (split, KV head kvh, query b) of n_split; NT threads.
+template <int HD, int G, int NT>
+__device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, int n_split, AttnLds<HD, G> &S) {
+    constexpr int NPAIR = G * HD / 2, PPT = AttnShape<HD, G, NT>::PPT;
+    const int tid = threadIdx.x;
+    const AttnSpan sp = attn_span(a, split, kvh, b, n_split);
+    const float *row = a.q + (int64_t)b * a.q_stride;
+    attn_prepare<HD, G, NT>(a, kvh, sp, S, [&](int64_t e) { return row[e]; });
+    float o[PPT][2];
+    attn_tiles<HD, G, NT>(a, sp, S, o);
 
     // 3. Partial record per head: [HD values][m][l]; the last workgroup merges.
     const int64_t rec = HD + 2;

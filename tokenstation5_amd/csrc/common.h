@@ -138,6 +138,23 @@ __device__ inline T wave_sum(T v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
     return v;
 }
+// Sum over the wave in registers: DPP steps (quad swaps, half-row and row
+// mirrors, then the row broadcasts of lanes 15 and 31) leave the total in lane
+// 63, which is read out to every lane. Six VALU ops, where a butterfly of
+// __shfl_xor is six dependent LDS-crossbar round trips.
+template <int CTRL, int ROW_MASK, bool BOUND>
+__device__ inline float dpp_add(float x) {
+    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, BOUND));
+}
+__device__ inline float wave_sum_dpp(float v) {
+    v = dpp_add<0xB1, 0xF, true>(v);    // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E, 0xF, true>(v);    // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xF, true>(v);   // row_half_mirror: 8-lane sums
+    v = dpp_add<0x140, 0xF, true>(v);   // row_mirror: 16-lane sums
+    v = dpp_add<0x142, 0xA, false>(v);  // row_bcast:15 into rows 1 and 3
+    v = dpp_add<0x143, 0xC, false>(v);  // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
 __device__ inline float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
@@ -186,6 +203,21 @@ __device__ inline void kq_scale_min(int j, uint32_t a, uint32_t b, uint32_t c, i
         sc = ((c >> s) & 15) | (((a >> (s + 6)) & 3) << 4);
         m = ((c >> (s + 4)) & 15) | (((b >> (s + 6)) & 3) << 4);
     }
+}
+
+// The same for the pair j = 2*sub, 2*sub + 1 that one matvec lane owns,
+// without branches: bytes 2*(sub & 1) and +1 of each dword, the 6-bit form
+// for sub < 2 and the split form (low 4 bits from c, top 2 from a or b) for
+// sub >= 2.
+__device__ inline void kq_scale_min_pair(int sub, uint32_t a, uint32_t b, uint32_t c, int &sc0, int &m0, int &sc1,
+                                         int &m1) {
+    const int s = 16 * (sub & 1);
+    const uint32_t A = a >> s, B = b >> s, C = c >> s;
+    const bool split = sub >= 2;
+    const uint32_t scw = split ? (C & 0x0F0Fu) | ((A >> 2) & 0x3030u) : A & 0x3F3Fu;
+    const uint32_t mw = split ? ((C >> 4) & 0x0F0Fu) | ((B >> 2) & 0x3030u) : B & 0x3F3Fu;
+    sc0 = (int)(scw & 0xFF), sc1 = (int)((scw >> 8) & 0xFF);
+    m0 = (int)(mw & 0xFF), m1 = (int)((mw >> 8) & 0xFF);
 }
 
 // ---------------------------------------------------------------------------

@@ -70,41 +70,46 @@ struct AttnIO {
     float *out;     // [B][H * HD]
 };
 hipError_t launch_attn(const AttnIO &io, hipStream_t s);
-// decode.hip: one token as one persistent kernel (cooperative launch).
-struct DecodeLayerIn {
-    const void *qkv, *wo, *gate, *up, *down;
-    uint32_t t_qkv, t_wo, t_gu, t_down;
-    const float *attn_norm, *ffn_norm, *bias, *q_norm, *k_norm;
-    KvLayer kv;
+// decode.hip: one token as one persistent kernel (cooperative launch) that
+// streams the weights through LDS and hands values between workgroups as
+// tagged 64-bit words (value bits, launch tag).
+enum { DPH_MV = 0, DPH_ADD = 1, DPH_GLU = 2, DPH_LOGITS = 3, DPH_ARGMAX = 4, DPH_ATTN = 5 };
+struct DecodePhaseIn {
+    int kind;
+    uint32_t t;  // weight type (matrix phases)
+    int ne0, nrows;
+    const void *w, *w2;        // GLU: gate, up
+    const void *x;             // tagged input words
+    const float *norm_w;       // fused rmsnorm, or null
+    void *y;                   // tagged output words
+    const void *y_in;          // ADD: tagged residual words
+    float *logits;             // LOGITS: plain fp32
+    KvLayer kv;                // ATTN: the layer's cache
+    const float *bias, *q_norm, *k_norm;
+    void *part;                // ATTN: n_split * H * (HD + 2) tagged words
 };
 struct DecodeIn {
-    int E, F, H, HKV, HD, V, n_layer, n_ctx, n_rot, neox, n_split;
+    int E, H, HKV, HD, V, n_ctx, n_rot, neox, n_split, max_in;
     float eps, scale;
-    const void *layers;  // device array of n_layer records (fill_decode_layer)
-    uint32_t t_embd, t_head;
-    const void *embd, *head;
-    const float *out_norm, *rope;
-    // Arena: x [2 n_layer + 1][sx], qkv [n_layer][sqkv], att [n_layer][satt],
-    // ffn [n_layer][sffn], part [n_layer][spart] (floats, 256-byte aligned rows).
-    float *x, *qkv, *att, *ffn, *part;
-    int64_t sx, sqkv, satt, sffn, spart;
-    float *logits;
-    int *counters;         // [HKV], zero
+    const void *phases;  // device array of fill_decode_phase records
+    int n_phases;
+    uint32_t t_embd;
+    const void *embd;
+    const float *rope;
+    void *x0;              // tagged embedding output (the first phase's input)
     int32_t *seq, *state;  // state[0] position, state[1] greedy id
-    int head_mode;         // 0: none, 1: logits, 2: logits + greedy argmax into seq[p + 1]
-    void *bar;             // decode_bar_bytes(), zeroed once
-    float *best_v;
-    int *best_i;  // grid entries each
+    int head_mode;         // 0: no head phase, 1: logits, 2: logits + greedy argmax into seq[p + 1]
+    void *best;            // 2 * grid tagged words
+    void *sync;            // decode_sync_bytes(), zeroed with the arena
     int grid;
     size_t lds_bytes;
-    uint64_t *trace;  // optional phase timestamps (decode_trace_len() entries)
+    uint64_t *trace;  // optional: grid * (n_phases + 2) * 4 timestamps
 };
-// Phase timestamps one token records: start, each barrier, the end.
-inline int decode_trace_len(int n_layer) { return 2 + 5 * n_layer + 3; }
-size_t decode_layer_bytes();
-size_t decode_bar_bytes();
+size_t decode_phase_bytes();
+size_t decode_sync_bytes();
+size_t decode_lds_bytes(int HD, int G, int max_in);
 int decode_grid(int HD, int G, int n_cu, size_t lds_bytes);
-hipError_t fill_decode_layer(void *dst_host, const DecodeLayerIn &in);
+int fill_decode_phase(void *dst_host, const DecodePhaseIn &in, int grid);  // 0, or -1: not streamable
 hipError_t launch_decode(const DecodeIn &in, hipStream_t s);
 
 hipError_t launch_kv_read(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, float *out, hipStream_t s);

@@ -95,6 +95,16 @@ struct Q4K {
         r.qb = ld16(blk + 32 + 32 * sub);
         return r;
     }
+    // The same from a row of blocks staged in LDS (scales unused: Q4_K keeps
+    // its own in the block).
+    __device__ static W load_w_lds(const uint8_t *row, const uint8_t *, int b, int sub) {
+        const uint8_t *blk = row + b * Q4K_BYTES;
+        W r;
+        r.hdr = ld16(blk);
+        r.qa = ld16(blk + 16 + 32 * sub);
+        r.qb = ld16(blk + 32 + 32 * sub);
+        return r;
+    }
     __device__ static float dot(const W &w, const X &x, int sub) {
         const uint32_t q[8] = {w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w};
         int ah0 = 0, al0 = 0, ah1 = 0, al1 = 0;
@@ -107,8 +117,7 @@ struct Q4K {
             al1 = dot4(hi, (int)x.l1[k], al1);
         }
         int sc0, m0, sc1, m1;
-        kq_scale_min(2 * sub, w.hdr.y, w.hdr.z, w.hdr.w, sc0, m0);
-        kq_scale_min(2 * sub + 1, w.hdr.y, w.hdr.z, w.hdr.w, sc1, m1);
+        kq_scale_min_pair(sub, w.hdr.y, w.hdr.z, w.hdr.w, sc0, m0, sc1, m1);
         const float d = h2f(w.hdr.x & 0xffff), dmin = h2f(w.hdr.x >> 16);
         const float p = (float)sc0 * x.s0 * (float)(ah0 * 256 + al0) + (float)sc1 * x.s1 * (float)(ah1 * 256 + al1);
         return d * p - dmin * ((float)m0 * x.m0 + (float)m1 * x.m1);
@@ -152,6 +161,18 @@ struct Q6K {
         r.qh = ld16(body + 128 + 32 * h + i0);
         r.sc = ld16(body + 192);
         r.d = h2f(w.dscale[blk]);
+        return r;
+    }
+    // The same from a row of bodies staged in LDS, its f16 scales at sc.
+    __device__ static W load_w_lds(const uint8_t *row, const uint8_t *sc, int b, int sub) {
+        const uint8_t *body = row + b * Q6K_BODY;
+        const int h = sub >> 1, i0 = (sub & 1) * 16;
+        W r;
+        r.qla = ld16(body + 64 * h + i0);
+        r.qlb = ld16(body + 64 * h + 32 + i0);
+        r.qh = ld16(body + 128 + 32 * h + i0);
+        r.sc = ld16(body + 192);
+        r.d = h2f(*(const uint16_t *)(sc + 2 * b));
         return r;
     }
     __device__ static float dot(const W &w, const X &x, int sub) {
@@ -213,6 +234,12 @@ struct Q80 {
         W r;
         r.q = ld16(w.body + blk * Q8_BODY + 16 * sub);
         r.d = h2f(w.dscale[blk]);
+        return r;
+    }
+    __device__ static W load_w_lds(const uint8_t *row, const uint8_t *sc, int b, int sub) {
+        W r;
+        r.q = ld16(row + b * Q8_BODY + 16 * sub);
+        r.d = h2f(*(const uint16_t *)(sc + 2 * b));
         return r;
     }
     __device__ static float dot(const W &w, const X &x, int) {
@@ -405,7 +432,7 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
 #pragma unroll
             for (int k = 0; k < NW; k++)
 #pragma unroll
-                for (int r = 0; r < R; r++) acc[k][r] = wave_sum(acc[k][r]);
+                for (int r = 0; r < R; r++) acc[k][r] = wave_sum_dpp(acc[k][r]);
             if (lane < R && row0 + lane < a.nrows) {
                 float v = acc[0][0], u = acc[NW - 1][0];
 #pragma unroll

@@ -72,6 +72,7 @@ _SIGS = {
     "ts5hip_logits_view": (C.POINTER(C.c_float), [_vp]),
     "ts5hip_n_ctx": (_i32, [_vp]),
     "ts5hip_kv_type": (_i32, [_vp]),
+    "ts5hip_token_path": (_i32, [_vp]),
     "ts5hip_model_sample": (C.c_int32, [_vp, _vp, _i32, _f32, _f32, _i32]),
     "ts5hip_generate_greedy": (_i32, [_vp, C.c_int32, _i32, _i32, _vp]),
     "ts5hip_kv_read": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
@@ -359,6 +360,12 @@ class Model:
         out = np.empty((n, w), np.float32)
         self.ctx.check(lib().ts5hip_kv_read(self.h, layer, which, pos0, n, out.ctypes.data))
         return out
+
+    def token_path(self) -> str:
+        """How single-token steps run: "persistent", "graphs" or "direct"."""
+        rc = lib().ts5hip_token_path(self.h)
+        self.ctx.check(min(rc, 0))
+        return ("direct", "graphs", "persistent")[rc]
 
     def take_profile(self) -> str:
         buf = C.create_string_buffer(4096)

@@ -10,8 +10,8 @@ timed region is exactly those steps, bracketed by device synchronisation.
 Beside the decode rate it reports:
   roofline      the dominant kernel (fused gate/up + SiLU, 45 % of a token's
                 bytes) timed with HIP events on the library's stream over
-                launches that rotate through > 256 MB of weights (so the
-                Infinity Cache cannot serve them), against 8 TB/s.
+                launches that rotate through > 1 GiB of weights (so the
+                256 MB Infinity Cache cannot serve them), against 8 TB/s.
   cpu_baseline  the CPU oracle (a restatement of ts5's CPU backend,
                 engine/src/cpu_backend.cpp) decoding a few tokens of the same
                 model shape at ~4k keys on the host cores.
@@ -89,10 +89,14 @@ def decode_bench(ctx, hp, steps: int, warmup: int, prompt_len: int = PROMPT):
 
 def glu_roofline(ctx, hp, launches: int = 200):
     """Fused gate/up + SiLU (k_mv_glu) alone on the library's stream, HIP events
-    around `launches` launches cycling through copies that exceed 256 MB."""
+    around `launches` launches cycling through > 1 GiB of weight copies: a
+    token sweeps 4.3 GB of weights, so none of its matrices is still in the
+    256 MB Infinity Cache when it comes round again, and with a rotation of
+    only ~330 MB half of each launch's weights were still found there
+    (rocprofv3 FETCH_SIZE)."""
     E, F = hp["n_embd"], hp["n_ff"]
     wb = ctx.weight_bytes(synth.Q4_K, E, F)
-    copies = max(2, -(-(320 << 20) // (2 * wb)))
+    copies = max(2, -(-(1100 << 20) // (2 * wb)))
     gates = [ctx.weight_synth(synth.Q4_K, E, F, 100 + i) for i in range(copies)]
     ups = [ctx.weight_synth(synth.Q4_K, E, F, 200 + i) for i in range(copies)]
     rng = np.random.default_rng(1)
@@ -116,6 +120,25 @@ def glu_roofline(ctx, hp, launches: int = 200):
                 frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
                 kernel="k_mv<Q4K,2,4,MV_GLU> (ffn rmsnorm+gate+up+SiLU, 14336x4096 x2)", avg_us=round(avg_us, 2),
                 algorithmic_bytes=int(algo))
+
+
+def roofline_only(hp):
+    """The roofline kernel's launches alone, then one RMSNorm over 256 MiB
+    (k_rmsnorm: reads 256 MiB once, writes 256 MiB once): the known-size
+    stream that scales the hardware counters (FETCH_SIZE, WRITE_SIZE) of a
+    rocprofv3 --pmc run of this mode."""
+    ctx = ts5hip.Context(0)
+    roof = glu_roofline(ctx, hp, launches=40)
+    n, rows = 4096, 16384
+    x = ctx.alloc(n * rows * 4)
+    y = ctx.alloc(n * rows * 4)
+    x.zero()
+    w = ctx.to_device(np.ones(n, np.float32))
+    ctx.rmsnorm(x, w, 1e-5, n, rows, y)
+    ctx.sync()
+    ctx.close()
+    print(json.dumps({"roofline": roof, "stream_kernel": "k_rmsnorm", "stream_read_bytes": n * rows * 4,
+                      "stream_write_bytes": n * rows * 4}), flush=True)
 
 
 def cpu_baseline(hp, steps: int = 3, keys: int = PROMPT):
@@ -153,12 +176,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--prompt", type=int, default=PROMPT, help="prompt length (cfg2: 4096)")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the roofline kernel's launches and a 256 MiB device copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this backend runs ts5's token loop on one GPU (batch 1); "
               "there is no multi-GPU path to measure.", file=sys.stderr)
         sys.exit(2)
     hp = dict(synth.LLAMA_8B)
+    if args.roofline_only:
+        roofline_only(hp)
+        return
     ctx = ts5hip.Context(0)
     log(f"device {ctx.arch}, {ctx.n_cu} CUs, {ctx.hbm / 2**30:.0f} GiB")
     ms, ids = decode_bench(ctx, hp, args.steps, args.warmup, args.prompt)

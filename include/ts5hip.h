@@ -96,6 +96,16 @@ int ts5hip_matvec_glu(ts5hip_ctx *ctx, uint32_t type, const void *w_gate, const 
  * engine/src/engine.cpp:17): y = W x' and out_dev[0] = the first index of max(y). */
 int ts5hip_matvec_argmax(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0, int64_t ne1, const float *x,
                          const float *norm_w, float eps, float *y, int32_t *out_dev);
+/* The projections of ntok tokens at once, each weight read once per call
+ * (engine/src/cpu_backend.cpp:18-41 at n > 1; the reference's GPU path uses mvt_q4_k / mvt_q6_k
+ * for 2..8 tokens and matmul_big for prompts, engine/src/vk_backend.cpp:835-918):
+ * y[t] (+)= W x'_t for t < ntok (1..4096), x' = x_t or rmsnorm(x_t) by norm_w.
+ * x: [ntok][ne0] fp32, y: [ntok][ne1] fp32. Matrix cores; the numerics of ts5hip_matvec. */
+int ts5hip_matmul(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0, int64_t ne1, const float *x, int ntok,
+                  const float *norm_w, float eps, float *y, int accumulate);
+/* The same for gate/up + SiLU (engine/src/cpu_backend.cpp:253-261): y[t] = silu(Wg x'_t) * (Wu x'_t). */
+int ts5hip_matmul_glu(ts5hip_ctx *ctx, uint32_t type, const void *w_gate, const void *w_up, int64_t ne0,
+                      int64_t ne1, const float *x, int ntok, const float *norm_w, float eps, float *y);
 /* RoPE angles as engine/src/cpu_backend.cpp:59-61 computes them, for positions
  * [0, n_pos): dst gets [n_pos][n_rot/2] (cos, sin) float pairs. freqs: n_rot/2 divisors or null. */
 int ts5hip_rope_table(ts5hip_ctx *ctx, int n_rot, int n_pos, float base, float scale, const float *freqs_host,

@@ -88,6 +88,7 @@ int ts5hip_init(int device, ts5hip_ctx **out) {
     c->n_cu = p.multiProcessorCount;
     c->arch = p.gcnArchName;
     c->hbm = (int64_t)p.totalGlobalMem;
+    set_gemm_cu_count(c->n_cu);
     set_cu_count(c->n_cu);
     if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess ||
         (e = hipEventCreate(&c->ev0)) != hipSuccess || (e = hipEventCreate(&c->ev1)) != hipSuccess ||
@@ -245,6 +246,31 @@ int ts5hip_matvec_glu(ts5hip_ctx *ctx, uint32_t type, const void *w_gate, const 
     if (int rc = check_matrix(ctx, type, ne0, ne1)) return rc;
     TS5_HIP(ctx, launch_matvec_glu(type, w_gate, w_up, ne0, ne1, x, norm_w, eps, y, ctx->stream));
     return TS5HIP_OK;
+}
+
+// Several tokens: their activations, then the matrix-core matmul.
+static int matmul_any(ts5hip_ctx *ctx, uint32_t type, const void *w, const void *w2, int64_t ne0, int64_t ne1,
+                      const float *x, int ntok, const float *norm_w, float eps, float *y, int mode) {
+    if (!ctx || !w || !x || !y || (mode == 2 && !w2)) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
+    if (ntok < 1 || ntok > 4096) return fail(ctx, TS5HIP_ERR_ARG, "ntok %d outside 1..4096", ntok);
+    if (int rc = check_matrix(ctx, type, ne0, ne1)) return rc;
+    const size_t act = align_up((size_t)ntok * act_bytes(ne0), 256);
+    const size_t part = gemm_scratch_bytes(ne1, ntok, (int)(ne0 / block_values(type)));
+    if (int rc = ensure_scratch(ctx, act + part)) return rc;
+    uint8_t *base = (uint8_t *)ctx->scratch;
+    TS5_HIP(ctx, launch_act_quant(x, ne0, norm_w, eps, (int)ne0, ntok, base, ctx->stream));
+    TS5_HIP(ctx, launch_gemm(type, w, w2, ne0, ne1, base, ntok, mode, y, y, ne1, base + act, ctx->stream));
+    return TS5HIP_OK;
+}
+
+int ts5hip_matmul(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0, int64_t ne1, const float *x, int ntok,
+                  const float *norm_w, float eps, float *y, int accumulate) {
+    return matmul_any(ctx, type, w, nullptr, ne0, ne1, x, ntok, norm_w, eps, y, accumulate ? 1 : 0);
+}
+
+int ts5hip_matmul_glu(ts5hip_ctx *ctx, uint32_t type, const void *w_gate, const void *w_up, int64_t ne0, int64_t ne1,
+                      const float *x, int ntok, const float *norm_w, float eps, float *y) {
+    return matmul_any(ctx, type, w_gate, w_up, ne0, ne1, x, ntok, norm_w, eps, y, 2);
 }
 
 int ts5hip_matvec_argmax(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0, int64_t ne1, const float *x,

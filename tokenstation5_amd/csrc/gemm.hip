@@ -1,0 +1,329 @@
+// The k-quant matmul of several tokens: Y[t] = W x_t for t < M, reading each
+// weight once per M tokens (engine/src/cpu_backend.cpp:18-41 at n > 1; the
+// reference's GPU path uses mvt_q4_k / mvt_q6_k for 2..8 tokens and
+// matmul_big for prompts, engine/src/vk_backend.cpp:835-918).
+//
+// Matrix cores. The activations are the same quantized form the one-token
+// matvec reads (common.h Act: x16 = 256*hi + lo, a scale per 32 values), so
+// every product is exact in int32 and only the per-sub-block scaling runs in
+// fp32. One v_mfma_i32_16x16x32_i8 multiplies 16 rows x 32 weights (A: the raw
+// quants, 0..15 or 0..63 or int8) by 32 values of 16 tokens' hi plane (B), a
+// second by their lo plane; 256*C_hi + C_lo is then sum q * x16 for each
+// (row, token) of the sub-block, and
+//   Q4_K: y += d*sc * xs * (sum q x16) - dmin*m * (sum x)       per 32 values
+//   Q6_K: y += d*sc * xs * (sum q x16 - 32 * sum x16)          per 16 values
+//   Q8_0: y += d * xs * (sum q x16)                             per 32 values
+// (engine/src/quants.cpp:133-202). Q6_K's 16-value groups each get an MFMA of
+// their own, the other half of the 32-value A operand zeroed.
+//
+// Lane layout of the 16x16x32 int8 MFMA (checked on the device): A lane l =
+// row l%16, k 8*(l/16)..+7; B lane l = column l%16, same k; D lane l holds
+// rows 4*(l/16)+i (i = 0..3) of column l%16. A lane therefore loads 8 bytes
+// of a row's quants and 8 bytes of a token's activation per sub-block, and
+// needs the block scales of rows 4*(l/16)..+3, which lanes exchange through
+// LDS (each lane decodes the scales of its own row and k-range).
+//
+// Workgroup: 4 waves, each 16 rows x 16*TN tokens; grid (rows/64, tokens /
+// (16 TN), KS). With KS > 1 the blocks of a row are split over KS workgroups
+// whose partial sums a second kernel adds in a fixed order.
+#include <algorithm>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace ts5hip {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct GemmArgs {
+    uint32_t t;
+    const uint8_t *w, *w2;    // block bodies (w2: GLU's up projection)
+    const uint16_t *s, *s2;   // split layouts' f16 block scales
+    int nrows, nb, n_in, M, ks;
+    const uint8_t *act;       // M activation records of act_bytes(n_in)
+    int64_t act_stride;
+    float *out;               // ks == 1: y [M][ldy]; ks > 1: partials [ks][2][M][nrows]
+    const float *y_in;        // MODE_ADD: residual [M][ldy] (may be out)
+    int64_t ldy;
+};
+
+enum { G_STORE = 0, G_ADD = 1, G_GLU = 2 };
+
+__device__ inline uint64_t ld8(const void *p) { return *(const uint64_t *)p; }
+__device__ inline uint4 ld16(const void *p) { return *(const uint4 *)p; }
+__device__ inline v4i mfma(uint64_t a, uint64_t b) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)a, (long)b, v4i{0, 0, 0, 0}, 0, 0, 0);
+}
+
+// Per-wave LDS for the scale exchange: [sub-block or group][row] (scale, min).
+struct GemmLds {
+    __align__(16) float2 scl[2][16][16];  // [matrix][sub-block / group][row]
+};
+
+constexpr int F_Q4K = 0, F_Q6K = 1, F_Q80 = 2;
+
+// Activation fragments of token group tg for 32-value chunk c of the row
+// (sub-block index in Act units), and the token's scale, sum.
+struct AFrag {
+    uint64_t hi, lo;
+    float xs, xsum;
+};
+__device__ inline AFrag act_frag(const GemmArgs &a, int tok, int chunk, int kq) {
+    AFrag f{0, 0, 0.f, 0.f};
+    if (tok < a.M) {
+        const CAct x = cact_view(a.act + (int64_t)tok * a.act_stride, a.n_in);
+        f.hi = ld8(x.hi + 32 * chunk + 8 * kq);
+        f.lo = ld8(x.lo + 32 * chunk + 8 * kq);
+        f.xs = x.scale[chunk];
+        f.xsum = x.sum[chunk];
+    }
+    return f;
+}
+
+template <int FMT, int MODE, int TN>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
+    __shared__ GemmLds L[4];
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, kq = l >> 4, rl = l & 15;
+    GemmLds &S = L[wave];
+    const int r0 = blockIdx.x * 64 + wave * 16;
+    const int t0 = blockIdx.y * 16 * TN;
+    const int row = r0 + rl;                    // the row this lane loads quants / scales of
+    const bool rin = row < a.nrows;
+    const int bpk = (a.nb + a.ks - 1) / a.ks;  // blocks per split
+    const int b0 = blockIdx.z * bpk, b1 = min(a.nb, b0 + bpk);
+    constexpr int NW = MODE == G_GLU ? 2 : 1;
+    float acc[NW][TN][4];
+#pragma unroll
+    for (int m = 0; m < NW; m++)
+#pragma unroll
+        for (int g = 0; g < TN; g++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[m][g][i] = 0.f;
+
+    for (int b = b0; b < b1; b++) {
+        __builtin_amdgcn_wave_barrier();  // this wave's reads of the last block's scales are issued
+        if constexpr (FMT == F_Q4K) {
+            uint64_t q[NW][4];
+#pragma unroll
+            for (int m = 0; m < NW; m++) {
+                const uint8_t *blk = (m ? a.w2 : a.w) + ((int64_t)(rin ? row : 0) * a.nb + b) * Q4K_BYTES;
+                uint4 hdr = ld16(blk);
+                if (!rin) hdr = make_uint4(0, 0, 0, 0);
+#pragma unroll
+                for (int g = 0; g < 4; g++) q[m][g] = rin ? ld8(blk + 16 + 32 * g + 8 * kq) : 0;
+                int sc0, m0, sc1, m1;
+                kq_scale_min_pair(kq, hdr.y, hdr.z, hdr.w, sc0, m0, sc1, m1);
+                const float d = h2f(hdr.x & 0xffff), dmin = h2f(hdr.x >> 16);
+                S.scl[m][2 * kq][rl] = make_float2(d * (float)sc0, dmin * (float)m0);
+                S.scl[m][2 * kq + 1][rl] = make_float2(d * (float)sc1, dmin * (float)m1);
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                AFrag x[TN];
+#pragma unroll
+                for (int g = 0; g < TN; g++) x[g] = act_frag(a, t0 + 16 * g + rl, b * 8 + s, kq);
+#pragma unroll
+                for (int m = 0; m < NW; m++) {
+                    const uint64_t qa = (s & 1) ? (q[m][s >> 1] >> 4) & 0x0F0F0F0F0F0F0F0Full
+                                                : q[m][s >> 1] & 0x0F0F0F0F0F0F0F0Full;
+                    const float4 sA = *(const float4 *)&S.scl[m][s][4 * kq];
+                    const float4 sB = *(const float4 *)&S.scl[m][s][4 * kq + 2];
+                    const float dsc[4] = {sA.x, sA.z, sB.x, sB.z}, dm[4] = {sA.y, sA.w, sB.y, sB.w};
+#pragma unroll
+                    for (int g = 0; g < TN; g++) {
+                        const v4i ch = mfma(qa, x[g].hi), cl = mfma(qa, x[g].lo);
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            acc[m][g][i] += dsc[i] * x[g].xs * (float)(ch[i] * 256 + cl[i]) - dm[i] * x[g].xsum;
+                    }
+                }
+            }
+        } else if constexpr (FMT == F_Q80) {
+            uint64_t q[NW];
+#pragma unroll
+            for (int m = 0; m < NW; m++) {
+                const int64_t blk = (int64_t)(rin ? row : 0) * a.nb + b;
+                q[m] = rin ? ld8((m ? a.w2 : a.w) + blk * Q8_BODY + 8 * kq) : 0;
+                if (kq == 0) S.scl[m][0][rl] = make_float2(rin ? h2f((m ? a.s2 : a.s)[blk]) : 0.f, 0.f);
+            }
+            __builtin_amdgcn_wave_barrier();
+            AFrag x[TN];
+#pragma unroll
+            for (int g = 0; g < TN; g++) x[g] = act_frag(a, t0 + 16 * g + rl, b, kq);
+#pragma unroll
+            for (int m = 0; m < NW; m++) {
+                const float4 sA = *(const float4 *)&S.scl[m][0][4 * kq];
+                const float4 sB = *(const float4 *)&S.scl[m][0][4 * kq + 2];
+                const float d[4] = {sA.x, sA.z, sB.x, sB.z};
+#pragma unroll
+                for (int g = 0; g < TN; g++) {
+                    const v4i ch = mfma(q[m], x[g].hi), cl = mfma(q[m], x[g].lo);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[m][g][i] += d[i] * x[g].xs * (float)(ch[i] * 256 + cl[i]);
+                }
+            }
+        } else {  // Q6_K
+            uint64_t ql[NW][4], qh[NW][2];
+#pragma unroll
+            for (int m = 0; m < NW; m++) {
+                const int64_t blk = (int64_t)(rin ? row : 0) * a.nb + b;
+                const uint8_t *body = (m ? a.w2 : a.w) + blk * Q6K_BODY;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    ql[m][2 * h] = rin ? ld8(body + 64 * h + 8 * kq) : 0;
+                    ql[m][2 * h + 1] = rin ? ld8(body + 64 * h + 32 + 8 * kq) : 0;
+                    qh[m][h] = rin ? ld8(body + 128 + 32 * h + 8 * kq) : 0;
+                }
+                const float d = rin ? h2f((m ? a.s2 : a.s)[blk]) : 0.f;
+                const uint32_t scw = rin ? *(const uint32_t *)(body + 192 + 4 * kq) : 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    S.scl[m][4 * kq + j][rl] = make_float2(d * (float)(int8_t)((scw >> (8 * j)) & 0xff), 0.f);
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int c32 = 0; c32 < 8; c32++) {  // 32-value chunk: half h = c32/4, quarter c = c32%4
+                const int h = c32 >> 2, c = c32 & 3;
+                AFrag x[TN];
+                int is0[TN], is1[TN];
+#pragma unroll
+                for (int g = 0; g < TN; g++) {
+                    const int tok = t0 + 16 * g + rl;
+                    x[g] = act_frag(a, tok, b * 8 + c32, kq);
+                    is0[g] = is1[g] = 0;
+                    if (tok < a.M) {
+                        const CAct xa = cact_view(a.act + (int64_t)tok * a.act_stride, a.n_in);
+                        is0[g] = xa.isum[b * 16 + 2 * c32];
+                        is1[g] = xa.isum[b * 16 + 2 * c32 + 1];
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < NW; m++) {
+                    const uint64_t lo4 = (ql[m][2 * h + (c & 1)] >> (4 * (c >> 1))) & 0x0F0F0F0F0F0F0F0Full;
+                    const uint64_t hi2 = ((qh[m][h] >> (2 * c)) & 0x0303030303030303ull) << 4;
+                    const uint64_t q = lo4 | hi2;  // 0..63
+                    const uint64_t qa0 = kq < 2 ? q : 0, qa1 = kq < 2 ? 0 : q;
+                    const int g0 = 2 * c32, g1 = 2 * c32 + 1;  // the block's 16-value groups
+                    const float4 s0A = *(const float4 *)&S.scl[m][g0][4 * kq];
+                    const float4 s0B = *(const float4 *)&S.scl[m][g0][4 * kq + 2];
+                    const float4 s1A = *(const float4 *)&S.scl[m][g1][4 * kq];
+                    const float4 s1B = *(const float4 *)&S.scl[m][g1][4 * kq + 2];
+                    const float e0[4] = {s0A.x, s0A.z, s0B.x, s0B.z}, e1[4] = {s1A.x, s1A.z, s1B.x, s1B.z};
+#pragma unroll
+                    for (int g = 0; g < TN; g++) {
+                        const v4i h0 = mfma(qa0, x[g].hi), l0 = mfma(qa0, x[g].lo);
+                        const v4i h1 = mfma(qa1, x[g].hi), l1 = mfma(qa1, x[g].lo);
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            acc[m][g][i] += x[g].xs * (e0[i] * (float)(h0[i] * 256 + l0[i] - 32 * is0[g]) +
+                                                       e1[i] * (float)(h1[i] * 256 + l1[i] - 32 * is1[g]));
+                    }
+                }
+            }
+        }
+    }
+
+    // Results: rows r0 + 4*kq + i, tokens t0 + 16*g + rl.
+#pragma unroll
+    for (int g = 0; g < TN; g++) {
+        const int tok = t0 + 16 * g + rl;
+        if (tok >= a.M) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = r0 + 4 * kq + i;
+            if (r >= a.nrows) continue;
+            if (a.ks > 1) {
+                float *p = a.out + (((int64_t)blockIdx.z * 2) * a.M + tok) * a.nrows + r;
+                p[0] = acc[0][g][i];
+                if (MODE == G_GLU) p[(int64_t)a.M * a.nrows] = acc[NW - 1][g][i];
+            } else {
+                const int64_t o = (int64_t)tok * a.ldy + r;
+                const float v = acc[0][g][i];
+                if (MODE == G_ADD) a.out[o] = a.y_in[o] + v;
+                else if (MODE == G_GLU) a.out[o] = v / (1.0f + expf(-v)) * acc[NW - 1][g][i];  // cpu_backend.cpp:260-261
+                else a.out[o] = v;
+            }
+        }
+    }
+}
+
+// Split-K: y[t][r] = (y_in +) sum over splits in order (GLU: silu(g) * u).
+__global__ void k_gemm_reduce(const float *__restrict__ part, int ks, int M, int nrows, int mode, float *y,
+                              const float *y_in, int64_t ldy) {
+    const int64_t n = (int64_t)M * nrows;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+        float g = 0.f, u = 0.f;
+        for (int k = 0; k < ks; k++) {
+            g += part[(int64_t)k * 2 * n + e];
+            if (mode == G_GLU) u += part[(int64_t)k * 2 * n + n + e];
+        }
+        const int tok = (int)(e / nrows), r = (int)(e % nrows);
+        const int64_t o = (int64_t)tok * ldy + r;
+        if (mode == G_ADD) y[o] = y_in[o] + g;
+        else if (mode == G_GLU) y[o] = g / (1.0f + expf(-g)) * u;
+        else y[o] = g;
+    }
+}
+
+// ---------------------------------------------------------------------------
+template <int FMT, int MODE>
+static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
+    if (tn == 4) hipLaunchKernelGGL((k_gemm<FMT, MODE, 4>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_gemm<FMT, MODE, 1>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int MODE>
+static hipError_t gemm_fmt(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
+    switch (a.t) {
+    case T_Q4_K: return gemm_go<F_Q4K, MODE>(a, grid, tn, s);
+    case T_Q6_K: return gemm_go<F_Q6K, MODE>(a, grid, tn, s);
+    case T_Q8_0: return gemm_go<F_Q80, MODE>(a, grid, tn, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+static int g_gemm_cu = 256;
+void set_gemm_cu_count(int n) { g_gemm_cu = n > 0 ? n : 256; }
+
+// Splits of K that give the launch about four workgroups per CU when the
+// tokens alone do not (small M: the matmul is a weight stream).
+static int gemm_splits(int64_t rows, int M, int nb, int tn) {
+    const int64_t wgs = ((rows + 63) / 64) * ((M + 16 * tn - 1) / (16 * tn));
+    int ks = (int)std::min<int64_t>(16, std::max<int64_t>(1, (4 * g_gemm_cu + wgs - 1) / wgs));
+    return std::min(ks, nb);
+}
+
+size_t gemm_scratch_bytes(int64_t rows, int M, int nb) {
+    const int tn = M > 16 ? 4 : 1;
+    const int ks = gemm_splits(rows, M, nb, tn);
+    return ks > 1 ? (size_t)ks * 2 * M * rows * 4 : 0;
+}
+
+hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, int64_t ne1, const void *act, int M,
+                       int mode, float *y, const float *y_in, int64_t ldy, void *scratch, hipStream_t s) {
+    GemmArgs a{};
+    a.t = t, a.w = (const uint8_t *)w, a.w2 = (const uint8_t *)w2, a.nrows = (int)ne1;
+    a.nb = (int)(ne0 / block_values(t)), a.n_in = (int)ne0, a.M = M, a.act = (const uint8_t *)act;
+    a.act_stride = (int64_t)act_bytes(ne0), a.y_in = y_in, a.ldy = ldy;
+    if (t == T_Q6_K || t == T_Q8_0) {
+        const int64_t nblocks = (int64_t)a.nb * ne1;
+        a.s = (const uint16_t *)(a.w + split_scale_offset(t, nblocks));
+        a.s2 = w2 ? (const uint16_t *)(a.w2 + split_scale_offset(t, nblocks)) : nullptr;
+    }
+    const int tn = M > 16 ? 4 : 1;
+    a.ks = gemm_splits(ne1, M, a.nb, tn);
+    a.out = a.ks > 1 ? (float *)scratch : y;
+    const dim3 grid((unsigned)((ne1 + 63) / 64), (unsigned)((M + 16 * tn - 1) / (16 * tn)), (unsigned)a.ks);
+    hipError_t e = mode == G_ADD ? gemm_fmt<G_ADD>(a, grid, tn, s)
+                   : mode == G_GLU ? gemm_fmt<G_GLU>(a, grid, tn, s)
+                                   : gemm_fmt<G_STORE>(a, grid, tn, s);
+    if (e != hipSuccess || a.ks == 1) return e;
+    const int64_t n = (int64_t)M * ne1;
+    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)std::min<int64_t>(4096, (n + 255) / 256)), dim3(256), 0, s,
+                       (const float *)scratch, a.ks, M, (int)ne1, mode, y, y_in, ldy);
+    return hipGetLastError();
+}
+
+}  // namespace ts5hip

@@ -24,6 +24,15 @@ hipError_t launch_repack(uint32_t t, int64_t nblocks, const void *gguf, void *bo
 hipError_t launch_synth(uint32_t t, int64_t ne0, int64_t nrows, uint64_t seed, int centered, void *body, void *scales,
                         hipStream_t s);
 
+// gemm.hip: Y[t] = W x_t for M tokens on the matrix cores; act: M records of
+// act_bytes(ne0) (launch_act_quant); mode 0 store, 1 add (y = y_in + ...),
+// 2 GLU (w2 = up: y = silu(W x) * (W2 x)); y [M][ldy]; scratch:
+// gemm_scratch_bytes(ne1, M, blocks per row) bytes.
+void set_gemm_cu_count(int n);
+size_t gemm_scratch_bytes(int64_t rows, int M, int nb);
+hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, int64_t ne1, const void *act, int M,
+                       int mode, float *y, const float *y_in, int64_t ldy, void *scratch, hipStream_t s);
+
 // act.hip
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int ntok, float *y, hipStream_t s);
 hipError_t launch_act_quant(const float *x, int64_t xstride, const float *w, float eps, int n, int ntok, void *act,
@@ -120,6 +129,7 @@ size_t argmax_scratch_bytes(int rows);
 hipError_t launch_argmax(const float *x, int n, int rows, void *scratch, int32_t *out, int32_t *seq, int32_t *pos,
                          hipStream_t s);
 hipError_t launch_advance(int32_t *pos, hipStream_t s);
+hipError_t launch_set_pos(int32_t *pos, int32_t v, hipStream_t s);
 size_t topk_scratch_bytes();
 int topk_max();
 int topk_max_n();

@@ -95,6 +95,12 @@ struct ts5hip_model {
     double ph_wait[7] = {0};  // ... of which waiting for weight slots
     int ph_count[7] = {0};
     int phase_tokens = 0;
+    // Several tokens per call (prompt chunks, speculative verification): the
+    // chunk's activations [CHUNK][...], its quantized activations, the
+    // matmul's split-K partials, attention partials and merge counters.
+    float *bx = nullptr, *bqkv = nullptr, *bq = nullptr, *batt = nullptr, *bffn = nullptr, *bpart = nullptr;
+    void *bact = nullptr, *bgemm = nullptr;
+    int *bcounters = nullptr;
     // Profile (TS5HIP_PROFILE set): GPU time per forward call.
     bool profile = false;
     double prof_ms = 0;
@@ -578,6 +584,109 @@ int ensure_rows(ts5hip_model *m, int rows) {
 
 // Positions pos0.. of n tokens; logits rows (all or the last) left at
 // dev_rows / host_rows when want_logits.
+// Tokens per batched pass: the reference chunks prompts at 256 tokens
+// (engine/src/vk_backend.cpp:272-277), and logits_view holds 256 rows.
+constexpr int CHUNK = 256;
+
+int ensure_batch(ts5hip_model *m) {
+    if (m->bx) return TS5HIP_OK;
+    const ts5hip_hparams &hp = m->hp;
+    const int64_t E = hp.n_embd, F = hp.n_ff, AH = (int64_t)hp.n_head * hp.head_dim, QR = m->qkv_rows();
+    const int64_t wide = std::max({E, F, AH});
+    size_t gemm = 0, part = 0;
+    const DevT &out = m->output.set ? m->output : m->tok_embd;
+    for (int M = 1; M <= CHUNK; M++) {
+        auto g = [&](int64_t rows, int64_t ne0, uint32_t t) {
+            const int bv = block_values(t) ? block_values(t) : 32;
+            gemm = std::max(gemm, gemm_scratch_bytes(rows, M, (int)(ne0 / bv)));
+        };
+        for (const LayerDev &L : m->layers) {
+            g(QR, E, L.qkv.type), g(E, AH, L.wo.type), g(F, E, L.gate.type), g(E, F, L.down.type);
+            for (int p = 0; p < 3; p++)
+                if (L.part[p].set) g(QR, E, L.part[p].type);
+        }
+        g(hp.n_vocab, E, out.type);
+        part = std::max(part, attn_partial_bytes(M, attn_splits(M, hp.n_head_kv, 512), hp.n_head, hp.head_dim));
+    }
+    int rc = 0;
+    if ((rc = alloc_t(m, CHUNK * E, &m->bx)) || (rc = alloc_t(m, CHUNK * QR, &m->bqkv)) ||
+        (rc = alloc_t(m, CHUNK * AH, &m->bq)) || (rc = alloc_t(m, CHUNK * AH, &m->batt)) ||
+        (rc = alloc_t(m, CHUNK * F, &m->bffn)) || (rc = alloc(m, CHUNK * act_bytes(wide), &m->bact)) ||
+        (rc = alloc(m, std::max<size_t>(gemm, 256), &m->bgemm)) || (rc = alloc(m, part, (void **)&m->bpart)) ||
+        (rc = alloc_t(m, (size_t)CHUNK * hp.n_head_kv, &m->bcounters)))
+        return rc;
+    TS5_HIP(m->ctx, hipMemsetAsync(m->bcounters, 0, (size_t)CHUNK * hp.n_head_kv * 4, m->ctx->stream));
+    return TS5HIP_OK;
+}
+
+// nc tokens (ids at seq[p0..]) at positions p0..p0+nc-1 in one pass per
+// layer: every projection a matmul over the chunk, attention a causal batch
+// over the cache. Logits (rows: 0, 1 = the last token's, nc = all) go to
+// `logits` ([rows][n_vocab]).
+int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
+    ts5hip_ctx *ctx = m->ctx;
+    const hipStream_t s = ctx->stream;
+    const ts5hip_hparams &hp = m->hp;
+    const int E = hp.n_embd, H = hp.n_head, HKV = hp.n_head_kv, HD = hp.head_dim, F = hp.n_ff, AH = H * HD;
+    const int QR = m->qkv_rows();
+    const float eps = hp.rms_eps;
+    auto proj = [&](uint32_t t, const void *w, const void *w2, int64_t ne0, int64_t ne1, const float *x,
+                    int64_t xstride, const float *norm, int ntok, int mode, float *y, int64_t ldy) -> int {
+        TS5_HIP(ctx, launch_act_quant(x, xstride, norm, eps, (int)ne0, ntok, m->bact, s));
+        TS5_HIP(ctx, launch_gemm(t, w, w2, ne0, ne1, m->bact, ntok, mode, y, y, ldy, m->bgemm, s));
+        return TS5HIP_OK;
+    };
+    TS5_HIP(ctx, launch_set_pos(m->state, p0, s));
+    TS5_HIP(ctx, launch_embed(m->tok_embd.type, m->tok_embd.d, E, hp.n_vocab, m->seq, m->state, nc, m->bx, s));
+    for (int l = 0; l < hp.n_layer; l++) {
+        const LayerDev &L = m->layers[l];
+        const float *an = (const float *)L.attn_norm.d;
+        if (L.in_qkv[0] && L.in_qkv[1] && L.in_qkv[2]) {
+            if (int rc = proj(L.qkv.type, L.qkv.d, nullptr, E, QR, m->bx, E, an, nc, 0, m->bqkv, QR)) return rc;
+        } else {
+            const int64_t prow[3] = {(int64_t)AH, (int64_t)HKV * HD, (int64_t)HKV * HD};
+            int64_t r0 = 0;
+            for (int p = 0; p < 3; p++) {
+                if (L.in_qkv[p]) {
+                    if (L.qkv.type == T_Q6_K || L.qkv.type == T_Q8_0)
+                        return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "mixed q/k/v types with a split layout");
+                    const SplitDst d = split_dst(L.qkv.type, E, QR, L.qkv.d, r0);
+                    if (int rc = proj(L.qkv.type, d.body, nullptr, E, prow[p], m->bx, E, an, nc, 0, m->bqkv + r0, QR))
+                        return rc;
+                } else {
+                    if (int rc = proj(L.part[p].type, L.part[p].d, nullptr, E, prow[p], m->bx, E, an, nc, 0,
+                                      m->bqkv + r0, QR))
+                        return rc;
+                }
+                r0 += prow[p];
+            }
+        }
+        const float *bias = m->has_bias[l] ? m->bias + (int64_t)l * QR : nullptr;
+        const float *qn = L.q_norm.set ? (const float *)L.q_norm.d : nullptr;
+        const float *kn = L.k_norm.set ? (const float *)L.k_norm.d : nullptr;
+        TS5_HIP(ctx, launch_rope_kv(m->bqkv, QR, bias, qn, kn, eps, m->rope_cs, hp.rope_dims, hp.rope_neox, m->state,
+                                    H, HKV, HD, m->n_ctx, nc, m->bq, m->kv_layer(l), s));
+        AttnIO io{};
+        io.q = m->bq, io.q_stride = AH, io.rope = 0, io.append = 0;
+        io.kv = m->kv_layer(l), io.kv_per_batch = 0, io.n_ctx = m->n_ctx, io.n_keys = m->state;
+        io.B = nc, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = attn_splits(nc, HKV, 512);
+        io.scale = hp.attn_scale, io.part = m->bpart, io.counters = m->bcounters, io.out = m->batt;
+        TS5_HIP(ctx, launch_attn(io, s));
+        if (int rc = proj(L.wo.type, L.wo.d, nullptr, AH, E, m->batt, AH, nullptr, nc, 1, m->bx, E)) return rc;
+        if (int rc = proj(L.gate.type, L.gate.d, L.up.d, E, F, m->bx, E, (const float *)L.ffn_norm.d, nc, 2, m->bffn, F))
+            return rc;
+        if (int rc = proj(L.down.type, L.down.d, nullptr, F, E, m->bffn, F, nullptr, nc, 1, m->bx, E)) return rc;
+    }
+    if (rows) {
+        const DevT &out = m->output.set ? m->output : m->tok_embd;
+        const float *x = rows == nc ? m->bx : m->bx + (int64_t)(nc - 1) * E;
+        if (int rc = proj(out.type, out.d, nullptr, E, hp.n_vocab, x, E, (const float *)m->out_norm.d, rows, 0, logits,
+                          hp.n_vocab))
+            return rc;
+    }
+    return TS5HIP_OK;
+}
+
 int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool want_logits, bool all) {
     ts5hip_ctx *ctx = m->ctx;
     if (!tokens || n <= 0 || pos0 < 0) return fail(ctx, TS5HIP_ERR_ARG, "bad tokens/n/pos0");
@@ -596,14 +705,20 @@ int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool wan
     TS5_HIP(ctx, hipMemcpyAsync(m->state, m->pinned_ids + n, 4, hipMemcpyHostToDevice, s));
     if (m->profile) TS5_HIP(ctx, hipEventRecord(ctx->ev0, s));
     const size_t row_bytes = (size_t)m->hp.n_vocab * 4;
-    for (int t = 0; t < n; t++) {
-        const bool lg = want_logits && (all || t == n - 1);
-        if (int rc = launch_token(m, lg ? G_LOGITS : G_KV)) return rc;
-        if (lg) {
-            const int r = all ? t : 0;
-            TS5_HIP(ctx, hipMemcpyAsync(m->dev_rows + (size_t)r * m->hp.n_vocab, m->logits, row_bytes,
-                                        hipMemcpyDeviceToDevice, s));
+    if (n == 1) {
+        if (int rc = launch_token(m, want_logits ? G_LOGITS : G_KV)) return rc;
+        if (want_logits)
+            TS5_HIP(ctx, hipMemcpyAsync(m->dev_rows, m->logits, row_bytes, hipMemcpyDeviceToDevice, s));
+    } else {
+        if (int rc = ensure_batch(m)) return rc;
+        for (int c0 = 0; c0 < n; c0 += CHUNK) {
+            const int nc = std::min(CHUNK, n - c0);
+            const bool last = c0 + nc == n;
+            const int r = !want_logits ? 0 : all ? nc : last ? 1 : 0;
+            if (int rc = enqueue_batch(m, nc, pos0 + c0, r, m->dev_rows + (all ? (size_t)c0 * m->hp.n_vocab : 0)))
+                return rc;
         }
+        TS5_HIP(ctx, launch_set_pos(m->state, pos0 + n, s));
     }
     if (rows) {
         TS5_HIP(ctx, hipMemcpyAsync(m->host_rows, m->dev_rows, rows * row_bytes, hipMemcpyDeviceToHost, s));

@@ -158,9 +158,15 @@ hipError_t launch_argmax(const float *x, int n, int rows, void *scratch, int32_t
 }
 
 __global__ void k_advance(int32_t *pos) { *pos += 1; }
+__global__ void k_set_pos(int32_t *pos, int32_t v) { *pos = v; }
 
 hipError_t launch_advance(int32_t *pos, hipStream_t s) {
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, s, pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_set_pos(int32_t *pos, int32_t v, hipStream_t s) {
+    hipLaunchKernelGGL(k_set_pos, dim3(1), dim3(1), 0, s, pos, v);
     return hipGetLastError();
 }
 

@@ -53,6 +53,8 @@ _SIGS = {
     "ts5hip_matvec": (_i32, [_vp, _u32, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _i32]),
     "ts5hip_matvec_glu": (_i32, [_vp, _u32, _vp, _vp, _i64, _i64, _vp, _vp, _f32, _vp]),
     "ts5hip_matvec_argmax": (_i32, [_vp, _u32, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _vp]),
+    "ts5hip_matmul": (_i32, [_vp, C.c_uint32, _vp, C.c_int64, C.c_int64, _vp, _i32, _vp, _f32, _vp, _i32]),
+    "ts5hip_matmul_glu": (_i32, [_vp, C.c_uint32, _vp, _vp, C.c_int64, C.c_int64, _vp, _i32, _vp, _f32, _vp]),
     "ts5hip_rope_table": (_i32, [_vp, _i32, _i32, _f32, _f32, _vp, _vp]),
     "ts5hip_rope_kv_append": (_i32, [_vp, _vp, _i32, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _i32, _vp, _vp, _vp,
                                      _f32, _vp, _vp, _vp, _vp, _vp]),
@@ -234,6 +236,14 @@ class Context:
 
     def rmsnorm(self, x, w, eps, n, ntok, y):
         self.check(lib().ts5hip_rmsnorm(self.h, _ptr(x), _ptr(w), eps, n, ntok, _ptr(y)))
+
+    def matmul(self, t, w, ne0, ne1, x, ntok, y, norm_w=None, eps=0.0, accumulate=False):
+        self.check(lib().ts5hip_matmul(self.h, t, _ptr(w), ne0, ne1, _ptr(x), ntok, _ptr(norm_w), eps, _ptr(y),
+                                       int(accumulate)))
+
+    def matmul_glu(self, t, wg, wu, ne0, ne1, x, ntok, y, norm_w=None, eps=0.0):
+        self.check(lib().ts5hip_matmul_glu(self.h, t, _ptr(wg), _ptr(wu), ne0, ne1, _ptr(x), ntok, _ptr(norm_w), eps,
+                                           _ptr(y)))
 
     def matvec(self, t, w, ne0, ne1, x, y, norm_w=None, eps=0.0, accumulate=False):
         self.check(lib().ts5hip_matvec(self.h, t, _ptr(w), ne0, ne1, _ptr(x), _ptr(norm_w), eps, _ptr(y),

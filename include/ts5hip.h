@@ -188,6 +188,35 @@ int ts5hip_kv_read(ts5hip_model *m, int layer, int which, int pos0, int n, float
 /* Backend::take_profile (engine/src/backend.h:40-43): text since the last call. */
 int ts5hip_take_profile(ts5hip_model *m, char *buf, int len);
 
+/* ---- the decode driver: Engine (engine/src/engine.h:33-66) over this backend ---- */
+
+typedef struct ts5hip_engine ts5hip_engine;
+/* SampleParams (engine/src/engine.h:16-23). draft < 0: 7 drafted tokens per step; 0: none.
+ * adapt: the adaptive draft length (TS5_ADAPT, engine/src/engine.cpp:225-228). seed 0 keeps the
+ * generator's state (std::mt19937_64, default-seeded when the engine is made). */
+typedef struct {
+    float temperature, top_p;
+    int32_t top_k, max_tokens;
+    uint64_t seed;
+    int32_t draft, adapt;
+} ts5hip_sample_params;
+/* Engine(Model, Backend, Tokenizer): generation over model m, which must outlive it. */
+int ts5hip_engine_new(ts5hip_model *m, ts5hip_engine **out);
+void ts5hip_engine_free(ts5hip_engine *e);
+/* Engine::set_drafter (engine/src/engine.cpp:59-68): dm's greedy continuations become the
+ * drafts where prompt lookup finds none (null: none). dm is not owned and must outlive e;
+ * its token ids must be the target's. */
+int ts5hip_engine_set_drafter(ts5hip_engine *e, ts5hip_model *dm);
+/* Engine::generate (engine/src/engine.cpp:149-292) with the tokens as ids instead of text:
+ * the prompt in 256-token chunks after the prefix already cached, then per step the next token
+ * and up to `draft` drafts (prompt lookup, engine.cpp:134-147, else the draft model,
+ * engine.cpp:75-129) forwarded as one batch, each draft kept while the sample at its position
+ * equals it. eog: n_eog end-of-generation ids. out: the generated ids (at most max_tokens);
+ * returns their count, or a negative error. stats (6): prompt tokens, prompt tokens evaluated,
+ * generated, drafted, accepted drafts, 1 if an end-of-generation id stopped it. */
+int ts5hip_engine_generate(ts5hip_engine *e, const int32_t *prompt, int n_prompt, const ts5hip_sample_params *p,
+                           const int32_t *eog, int n_eog, int32_t *out, int32_t *stats);
+
 #ifdef __cplusplus
 }
 #endif

@@ -369,6 +369,8 @@ int32_t ts5hip_sampler_draw(ts5hip_sampler *s, const int32_t *ids, const float *
 
 namespace ts5hip {
 
+void sampler_reseed(ts5hip_sampler *s, uint64_t seed) { s->rng.seed(seed); }
+
 // Engine::sample (engine/src/engine.cpp:16-46) over a host row of n logits.
 int32_t sample_host_row(ts5hip_sampler *s, const float *lg, int n, float temperature, float top_p, int top_k) {
     if (temperature <= 0) return (int32_t)(std::max_element(lg, lg + n) - lg);

@@ -83,5 +83,10 @@ inline int32_t sampler_draw(std::mt19937_64 &rng, std::vector<double> &w, const 
 
 // Engine::sample over a host row of logits (capi.cpp).
 int32_t sample_host_row(ts5hip_sampler *s, const float *lg, int n, float temperature, float top_p, int top_k);
+// Engine::generate's rng_.seed(seed) (capi.cpp).
+void sampler_reseed(ts5hip_sampler *s, uint64_t seed);
+// The model's vocabulary and context handle (model.cpp), for the decode driver.
+int model_vocab(const ts5hip_model *m);
+ts5hip_ctx *model_ctx(const ts5hip_model *m);
 
 }  // namespace ts5hip

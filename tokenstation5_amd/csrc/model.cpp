@@ -737,6 +737,11 @@ int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool wan
 
 }  // namespace
 
+namespace ts5hip {
+int model_vocab(const ts5hip_model *m) { return m->hp.n_vocab; }
+ts5hip_ctx *model_ctx(const ts5hip_model *m) { return m->ctx; }
+}  // namespace ts5hip
+
 extern "C" {
 
 int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, int kv_type, ts5hip_model **out) {

@@ -29,6 +29,12 @@ class HParams(C.Structure):
                [(n, C.c_float) for n in ("rms_eps", "rope_base", "attn_scale", "rope_scale")]
 
 
+class SampleParams(C.Structure):
+    """ts5hip_sample_params: SampleParams (engine/src/engine.h:16-23)."""
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int32), ("max_tokens", C.c_int32),
+                ("seed", C.c_uint64), ("draft", C.c_int32), ("adapt", C.c_int32)]
+
+
 _SIGS = {
     "ts5hip_last_error": (C.c_char_p, [_vp]),
     "ts5hip_init": (_i32, [_i32, C.POINTER(_vp)]),
@@ -79,6 +85,10 @@ _SIGS = {
     "ts5hip_generate_greedy": (_i32, [_vp, C.c_int32, _i32, _i32, _vp]),
     "ts5hip_kv_read": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
     "ts5hip_take_profile": (_i32, [_vp, C.c_char_p, _i32]),
+    "ts5hip_engine_new": (_i32, [_vp, C.POINTER(_vp)]),
+    "ts5hip_engine_free": (None, [_vp]),
+    "ts5hip_engine_set_drafter": (_i32, [_vp, _vp]),
+    "ts5hip_engine_generate": (_i32, [_vp, _vp, _i32, C.POINTER(SampleParams), _vp, _i32, _vp, _vp]),
 }
 
 _lib = None
@@ -381,3 +391,43 @@ class Model:
         buf = C.create_string_buffer(4096)
         self.ctx.check(lib().ts5hip_take_profile(self.h, buf, 4096))
         return buf.value.decode()
+
+
+class Engine:
+    """Engine (engine/src/engine.h:33-66): generation with prompt-lookup and
+    draft-model speculation over a Model."""
+
+    def __init__(self, model: Model):
+        self.model = model
+        h = _vp()
+        model.ctx.check(lib().ts5hip_engine_new(model.h, C.byref(h)))
+        self.h = h.value
+
+    def set_drafter(self, dm: "Model | None"):
+        self.drafter = dm
+        self.model.ctx.check(lib().ts5hip_engine_set_drafter(self.h, dm.h if dm else None))
+
+    def generate(self, prompt, temperature=0.0, top_p=0.95, top_k=40, max_tokens=64, seed=0, draft=-1, adapt=True,
+                 eog=()):
+        """(ids, stats): stats = prompt, evaluated, generated, drafted, accepted, stopped."""
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        eog = np.ascontiguousarray(eog, np.int32)
+        out = np.empty(max(max_tokens, 1), np.int32)
+        stats = np.zeros(6, np.int32)
+        p = SampleParams(temperature, top_p, top_k, max_tokens, seed, draft, int(adapt))
+        n = lib().ts5hip_engine_generate(self.h, prompt.ctypes.data, prompt.size, C.byref(p),
+                                         eog.ctypes.data if eog.size else None, eog.size, out.ctypes.data,
+                                         stats.ctypes.data)
+        self.model.ctx.check(min(n, 0))
+        return out[:n], stats
+
+    def close(self):
+        if self.h:
+            lib().ts5hip_engine_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

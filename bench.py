@@ -64,7 +64,9 @@ def model_tensor_specs(hp: dict):
 
 
 def decode_bench(ctx, hp, steps: int, warmup: int, prompt_len: int = PROMPT):
-    n_ctx = prompt_len + max(steps, warmup) + 8
+    """The timed decode; also the prompt's prefill rate and the cost of a
+    5-token verify batch (one token + 4 drafts, all logits) against one step."""
+    n_ctx = prompt_len + max(steps, warmup) + 16
     m = ts5hip.Model(ctx, hp, n_ctx)
     t0 = time.time()
     for name, t, ne0, ne1 in model_tensor_specs(hp):
@@ -72,10 +74,13 @@ def decode_bench(ctx, hp, steps: int, warmup: int, prompt_len: int = PROMPT):
     ctx.sync()
     log(f"weights generated in HBM ({time.time() - t0:.1f} s)")
     prompt = np.random.default_rng(SEED).integers(0, hp["n_vocab"], prompt_len).astype(np.int32)
+    m.forward(prompt[:256], 0, logits=False)  # first use: graphs, batch buffers
     t0 = time.time()
     m.forward(prompt[:-1], 0, logits=False)
+    prefill_s = time.time() - t0
     first = int(m.generate_greedy(int(prompt[-1]), prompt_len - 1, 1)[0])
-    log(f"prefill of {prompt_len} tokens: {time.time() - t0:.1f} s (one token per graph replay)")
+    log(f"prefill of {prompt_len - 1} tokens: {prefill_s:.2f} s ({(prompt_len - 1) / prefill_s:.0f} tok/s, "
+        f"256-token batches)")
     if warmup:
         m.generate_greedy(first, prompt_len, warmup)
     ctx.sync()
@@ -83,8 +88,21 @@ def decode_bench(ctx, hp, steps: int, warmup: int, prompt_len: int = PROMPT):
     ids = m.generate_greedy(first, prompt_len, steps)
     ms = ctx.timer_end()
     log(f"{steps} decode steps: {ms:.2f} ms ({steps / ms * 1e3:.1f} tok/s); ids[:8] {list(ids[:8])}")
+    # Speculative verification at the end of the context: 5 tokens with every
+    # position's logits, against a single step, both end to end (host logits).
+    pos = prompt_len + steps
+    batch = np.array(ids[-5:], np.int32)
+    times = {}
+    for n in (1, 5, 1, 5):
+        t0 = time.time()
+        for _ in range(10):
+            m.forward(batch[:n], pos, all_logits=n > 1)
+        times[n] = (time.time() - t0) / 10 * 1e3
+    log(f"verify: 1 token {times[1]:.3f} ms, 5 tokens {times[5]:.3f} ms ({times[5] / times[1]:.2f}x)")
     m.close()
-    return ms, ids
+    extra = dict(prefill_tok_s=round((prompt_len - 1) / prefill_s, 1), step_ms_host=round(times[1], 3),
+                 verify5_ms_host=round(times[5], 3), verify5_over_step=round(times[5] / times[1], 3))
+    return ms, ids, extra
 
 
 def glu_roofline(ctx, hp, launches: int = 200):
@@ -189,7 +207,7 @@ def main():
         return
     ctx = ts5hip.Context(0)
     log(f"device {ctx.arch}, {ctx.n_cu} CUs, {ctx.hbm / 2**30:.0f} GiB")
-    ms, ids = decode_bench(ctx, hp, args.steps, args.warmup, args.prompt)
+    ms, ids, extra = decode_bench(ctx, hp, args.steps, args.warmup, args.prompt)
     roof = glu_roofline(ctx, hp)
     log(f"roofline: {roof}")
     ctx.close()
@@ -209,7 +227,7 @@ def main():
         "config": {"workload": "cfg2: Llama-style 8B decode, 4096-token prompt, greedy, q8 KV",
                    "global_batch": 1, "seq_len": args.prompt, "parallelism": "none (1 GPU)",
                    "decode_hbm_gbs": round(token_bytes * value / 1e9, 1),
-                   "decode_roofline_frac": round(token_bytes * value / 1e9 / HBM_PEAK_GBS, 4)},
+                   "decode_roofline_frac": round(token_bytes * value / 1e9 / HBM_PEAK_GBS, 4), **extra},
         "roofline": roof, "cpu_baseline": cpu,
     }), flush=True)
 

@@ -2,6 +2,7 @@
 // form every matvec reads (see Act in common.h).
 #include "common.h"
 #include "kernels.h"
+#include "mv_core.h"
 
 namespace ts5hip {
 
@@ -35,19 +36,18 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
     for (int i = threadIdx.x; i < n; i += blockDim.x) yt[i] = xt[i] * s * w[i];
 }
 
-// Act of x (optionally rms-normalised by w first) per token (blockIdx.x).
+// Act of x (optionally rms-normalised by w first): token blockIdx.x, 16-runs
+// 256*blockIdx.y .. +255 (one per thread; the norm's sum over the whole row
+// is taken by every slice).
 __global__ __launch_bounds__(256) void k_act_quant(const float *__restrict__ x, int64_t xstride,
                                                    const float *__restrict__ w, float eps, int n,
                                                    uint8_t *__restrict__ act, int64_t act_stride) {
     __shared__ float red[4];
     const float *xt = x + (int64_t)blockIdx.x * xstride;
     const Act a = act_view(act + (int64_t)blockIdx.x * act_stride, n);
-    const float s = w ? rms_scale(xt, n, eps, red) : 1.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float v = xt[i];
-        if (w) v = v * s * w[i];
-        quant32(v, threadIdx.x & 31, a, i / 32);
-    }
+    const float s = act_rms<256>(xt, w, eps, n, red);
+    const int r0 = 256 * blockIdx.y;
+    act_runs<256>(xt, w, s, r0, min(n / 16, r0 + 256), a);
 }
 
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int ntok, float *y, hipStream_t s) {
@@ -57,7 +57,8 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int 
 
 hipError_t launch_act_quant(const float *x, int64_t xstride, const float *w, float eps, int n, int ntok, void *act,
                             hipStream_t s) {
-    hipLaunchKernelGGL(k_act_quant, dim3(ntok), dim3(256), 0, s, x, xstride, w, eps, n, (uint8_t *)act,
+    hipLaunchKernelGGL(k_act_quant, dim3(ntok, (n / 16 + 255) / 256), dim3(256), 0, s, x, xstride, w, eps, n,
+                       (uint8_t *)act,
                        (int64_t)act_bytes(n));
     return hipGetLastError();
 }

@@ -88,8 +88,8 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float *__restrict__ qkv, i
 
 template <int HD, int G>
 __global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
-    __shared__ AttnLds<HD, G> S;
-    attn_item<HD, G, 256>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x, S);
+    __shared__ SliceLds<HD, G> S;
+    attn_slice<HD, G>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x, S);
 }
 
 // K (which 0) or V (1) at positions [pos0, pos0 + n) dequantized to fp32

@@ -131,9 +131,8 @@ struct AttnShape {
 //    that token's K and V) into LDS, from q(e) = element e of the token's
 //    q|k|v row; bias, per-head norm and RoPE when a.rope; the new K and V
 //    rounded to q8 and stored at their cache slot.
-template <int HD, int G, int NT, class QLoad>
-__device__ inline void attn_prepare(const AttnArgs &a, int kvh, const AttnSpan &sp, AttnLds<HD, G> &S,
-                                    QLoad qload) {
+template <int HD, int G, int NT, class QLoad, class Lds>
+__device__ inline void attn_prepare(const AttnArgs &a, int kvh, const AttnSpan &sp, Lds &S, QLoad qload) {
     constexpr int NWV = NT / 64;
     auto &q_s = S.q_s;
     auto &kv_s = S.kv_s;
@@ -395,6 +394,239 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
         float acc = 0.f;
 #pragma unroll 8
         for (int sp = 0; sp < n_split; sp++) acc += S.mw[sp][g] * pd[sp * sstride];
+        st_dev(a.out + (int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d, acc / S.red[g]);
+    }
+    if (tid == 0) st_dev(a.counters + b * a.HKV + kvh, 0);  // ready for the next use
+}
+
+// ---------------------------------------------------------------------------
+// One work item (split, KV head kvh, query b) of n_split over its whole key
+// slice, in passes of up to ATTN_KT keys: every K and V byte of a pass is
+// requested before the query's preparation and held in registers, so the
+// slice costs one memory round trip rather than one per 64-key tile.
+//   scores   4 lanes per key (HD/4 dims each), 64 keys per sweep of the
+//            workgroup, q from LDS, the 4 partial sums added by DPP;
+//   softmax  a wave per head over the pass, online across passes;
+//   p * v    8 dims per lane straight from the V rows in registers, G heads
+//            per V value; the lanes and waves that took other keys of the
+//            same dims are added at the end (shuffles, then LDS).
+// Then the partial record and the merge of attn_item.
+// ---------------------------------------------------------------------------
+constexpr int ATTN_KT = 256;
+
+template <int HD, int G>
+struct SliceLds {
+    float q_s[G][HD];
+    __align__(16) float p_s[ATTN_KT][G];  // scores, then probabilities
+    float alpha_s[G], m_s[G], l_s[G], red[G];
+    float kv_s[2][HD];                    // the new token's K and V before rounding
+    __align__(16) int8_t new8[2][HD];     // ... and after, as int8
+    uint16_t new_sc[2][HD / 32];          // ... with their f16 scales
+    __align__(16) float o_s[4][G * HD];   // each wave's p * v sums
+    float mw[ATTN_MAX_SPLIT][G], lw[ATTN_MAX_SPLIT][G];
+    int last;
+};
+
+template <int HD, int G>
+struct SliceShape {
+    static constexpr int NT = 256, LPK = 4, NQ = HD / LPK, NPASS = ATTN_KT / 64;
+    static constexpr int DPL = 8, LPV = HD / DPL, KPW = 64 / LPV, KPS = 4 * KPW, NVS = ATTN_KT / KPS;
+    static_assert(NQ % 8 == 0 && LPV <= 64 && 64 % LPV == 0, "attention slice shape");
+};
+
+template <int HD, int G>
+__device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, int n_split, SliceLds<HD, G> &S) {
+    using SH = SliceShape<HD, G>;
+    constexpr int NT = SH::NT, NQ = SH::NQ, NPASS = SH::NPASS, LPV = SH::LPV, KPW = SH::KPW, KPS = SH::KPS,
+                  NVS = SH::NVS;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kk = tid >> 2, qq = tid & 3;              // scores: key kk of a sweep, quarter qq of the dims
+    const int vk = lane / LPV, vc = lane % LPV;         // p * v: key vk of a wave's step, dims 8 vc ..
+    const AttnSpan sp = attn_span<16>(a, split, kvh, b, n_split);
+    const int8_t *kb = a.kv.k + sp.head_base * HD, *vb = a.kv.v + sp.head_base * HD;
+    const uint16_t *ksb = a.kv.ks + sp.head_base * (HD / 32), *vsb = a.kv.vs + sp.head_base * (HD / 32);
+    float o[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[g][e] = 0.f;
+    bool prepared = false;
+    for (int t0 = sp.p0; t0 < sp.p1 || !prepared; t0 += ATTN_KT) {
+        const int nt = max(0, min(ATTN_KT, sp.p1 - t0));
+        const int kmax = max(sp.p1 - 1, 0);  // loads past the slice read its last key (zero weight)
+        KRow<NQ> kr[NPASS];
+        uint16_t ksr[NPASS];
+#pragma unroll
+        for (int j = 0; j < NPASS; j++) {
+            const int key = min(t0 + 64 * j + kk, kmax);
+            kr[j] = load_krow<NQ>(kb + (int64_t)key * HD + qq * NQ);
+            ksr[j] = ksb[(int64_t)key * (HD / 32) + (qq * NQ) / 32];
+        }
+        uint2 vr[NVS];
+        uint16_t vsr[NVS];
+#pragma unroll
+        for (int s2 = 0; s2 < NVS; s2++) {
+            const int key = min(t0 + s2 * KPS + wave * KPW + vk, kmax);
+            vr[s2] = *(const uint2 *)(vb + (int64_t)key * HD + 8 * vc);
+            vsr[s2] = vsb[(int64_t)key * (HD / 32) + (8 * vc) / 32];
+        }
+        if (!prepared) {
+            const float *row = a.q + (int64_t)b * a.q_stride;
+            attn_prepare<HD, G, NT>(a, kvh, sp, S, [&](int64_t e) { return row[e]; });
+            prepared = true;
+            if (nt == 0) break;
+        }
+        // Scores of the pass.
+#pragma unroll
+        for (int j = 0; j < NPASS; j++) {
+            if (64 * j >= nt) break;
+            const int idx = 64 * j + kk, key = t0 + idx;
+            float ks = h2f(ksr[j]);
+            if (sp.has_new && key == sp.pq) {
+#pragma unroll
+                for (int c = 0; c < NQ / 4; c++) kr[j].w[c] = *(const uint32_t *)(S.new8[0] + qq * NQ + 4 * c);
+                ks = h2f(S.new_sc[0][(qq * NQ) / 32]);
+            }
+            float acc[G];
+#pragma unroll
+            for (int g = 0; g < G; g++) acc[g] = 0.f;
+#pragma unroll
+            for (int e4 = 0; e4 < NQ / 4; e4++) {
+                const uint32_t w = kr[j].w[e4];
+                float kf[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) kf[i] = (float)(int8_t)((w >> (8 * i)) & 0xff) * ks;
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    const float4 qv = *(const float4 *)&S.q_s[g][qq * NQ + 4 * e4];
+                    acc[g] += qv.x * kf[0] + qv.y * kf[1] + qv.z * kf[2] + qv.w * kf[3];
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                acc[g] = dpp_add<0xB1, 0xF, true>(acc[g]);  // quad_perm [1,0,3,2]
+                acc[g] = dpp_add<0x4E, 0xF, true>(acc[g]);  // quad_perm [2,3,0,1]
+            }
+            if (qq == 0) {
+#pragma unroll
+                for (int g = 0; g < G; g++) S.p_s[idx][g] = idx < nt ? acc[g] * a.scale : -INFINITY;
+            }
+        }
+        __syncthreads();
+        // Online softmax per head over the pass.
+        for (int g = wave; g < G; g += NT / 64) {
+            float v[NPASS];
+            float mt = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < NPASS; i++) {
+                v[i] = 64 * i + lane < nt ? S.p_s[64 * i + lane][g] : -INFINITY;
+                mt = fmaxf(mt, v[i]);
+            }
+            mt = wave_max(mt);
+            const float mo = S.m_s[g], mn = fmaxf(mo, mt);
+            float ls = 0.f;
+#pragma unroll
+            for (int i = 0; i < NPASS; i++) {
+                const float pe = v[i] == -INFINITY ? 0.f : expf(v[i] - mn);
+                if (64 * i < nt) S.p_s[64 * i + lane][g] = pe;
+                ls += pe;
+            }
+            ls = wave_sum(ls);
+            if (lane == 0) {
+                const float al = mo == -INFINITY ? 0.f : expf(mo - mn);
+                S.alpha_s[g] = al;
+                S.m_s[g] = mn;
+                S.l_s[g] = S.l_s[g] * al + ls;
+            }
+        }
+        __syncthreads();
+        // o = o * alpha + sum over the pass's keys of p * v.
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float al = S.alpha_s[g];
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[g][e] *= al;
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < NVS; s2++) {
+            if (s2 * KPS >= nt) break;
+            const int idx = s2 * KPS + wave * KPW + vk, key = t0 + idx;
+            uint2 v8 = vr[s2];
+            float vs = h2f(vsr[s2]);
+            if (sp.has_new && key == sp.pq) {
+                v8 = *(const uint2 *)(S.new8[1] + 8 * vc);
+                vs = h2f(S.new_sc[1][(8 * vc) / 32]);
+            }
+            float w[G];
+#pragma unroll
+            for (int g = 0; g < G; g++) w[g] = S.p_s[idx][g] * vs;  // idx < 64 * ceil(nt / 64): a written row
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float vf = (float)(int8_t)((((e < 4) ? v8.x : v8.y) >> (8 * (e & 3))) & 0xff);
+#pragma unroll
+                for (int g = 0; g < G; g++) o[g][e] += w[g] * vf;
+            }
+        }
+        __syncthreads();  // p_s is rewritten by the next pass
+    }
+    // The wave's KPW key groups of the same dims, then the 4 waves.
+#pragma unroll
+    for (int m = LPV; m < 64; m <<= 1)
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[g][e] += __shfl_xor(o[g][e], m, WAVE);
+    if (vk == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            *(float4 *)&S.o_s[wave][g * HD + 8 * vc] = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+            *(float4 *)&S.o_s[wave][g * HD + 8 * vc + 4] = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
+        }
+    }
+    __syncthreads();
+
+    const int64_t rec = HD + 2;
+    float *pb = a.part + (((int64_t)b * n_split + split) * a.H + (int64_t)kvh * G) * rec;
+    for (int j = tid; j < G * HD; j += NT) {
+        const int g = j / HD, d = j % HD;
+        st_dev(pb + g * rec + d, S.o_s[0][j] + S.o_s[1][j] + S.o_s[2][j] + S.o_s[3][j]);
+    }
+    if (tid < G) {
+        st_dev(pb + tid * rec + HD, S.m_s[tid]);
+        st_dev(pb + tid * rec + HD + 1, S.l_s[tid]);
+    }
+    wait_stores();
+    __syncthreads();
+    if (tid == 0) S.last = atomicAdd(a.counters + b * a.HKV + kvh, 1) == n_split - 1;
+    __syncthreads();
+    if (!S.last) return;
+    const float *p_all = a.part + ((int64_t)b * n_split * a.H + (int64_t)kvh * G) * rec;
+    const int64_t sstride = (int64_t)a.H * rec;
+    for (int j = tid; j < n_split * G; j += NT) {
+        const int s2 = j / G, g = j % G;
+        S.mw[s2][g] = p_all[s2 * sstride + g * rec + HD];
+        S.lw[s2][g] = p_all[s2 * sstride + g * rec + HD + 1];
+    }
+    __syncthreads();
+    if (tid < G) {
+        float M = -INFINITY;
+        for (int s2 = 0; s2 < n_split; s2++) M = fmaxf(M, S.mw[s2][tid]);
+        float L = 0.f;
+        for (int s2 = 0; s2 < n_split; s2++) {
+            const float m = S.mw[s2][tid];
+            const float w = m == -INFINITY ? 0.f : expf(m - M);
+            S.mw[s2][tid] = w;
+            L += w * S.lw[s2][tid];
+        }
+        S.red[tid] = L;
+    }
+    __syncthreads();
+    for (int j = tid; j < G * HD; j += NT) {
+        const int g = j / HD, d = j % HD;
+        const float *pd = p_all + g * rec + d;
+        float acc = 0.f;
+#pragma unroll 16
+        for (int s2 = 0; s2 < n_split; s2++) acc += S.mw[s2][g] * pd[s2 * sstride];
         st_dev(a.out + (int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d, acc / S.red[g]);
     }
     if (tid == 0) st_dev(a.counters + b * a.HKV + kvh, 0);  // ready for the next use

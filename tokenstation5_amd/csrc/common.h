@@ -213,9 +213,9 @@ __device__ inline void kq_scale_min_pair(int sub, uint32_t a, uint32_t b, uint32
                                          int &m1) {
     const int s = 16 * (sub & 1);
     const uint32_t A = a >> s, B = b >> s, C = c >> s;
-    const bool split = sub >= 2;
-    const uint32_t scw = split ? (C & 0x0F0Fu) | ((A >> 2) & 0x3030u) : A & 0x3F3Fu;
-    const uint32_t mw = split ? ((C >> 4) & 0x0F0Fu) | ((B >> 2) & 0x3030u) : B & 0x3F3Fu;
+    const uint32_t split = 0u - (uint32_t)(sub >> 1);  // all ones for sub-blocks 2, 3: a bit select, no branch
+    const uint32_t scw = (((C & 0x0F0Fu) | ((A >> 2) & 0x3030u)) & split) | (A & 0x3F3Fu & ~split);
+    const uint32_t mw = ((((C >> 4) & 0x0F0Fu) | ((B >> 2) & 0x3030u)) & split) | (B & 0x3F3Fu & ~split);
     sc0 = (int)(scw & 0xFF), sc1 = (int)((scw >> 8) & 0xFF);
     m0 = (int)(mw & 0xFF), m1 = (int)((mw >> 8) & 0xFF);
 }

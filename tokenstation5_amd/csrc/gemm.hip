@@ -248,6 +248,230 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Up to 16 tokens (the speculative verify batch): the matmul is a weight
+// stream. A workgroup takes 16 rows; its 4 waves each take a quarter of the
+// row's blocks and keep the next block's quants, header and activation
+// fragments in flight while they compute the current one; the quarters' sums
+// meet in LDS and are added in a fixed order.
+// ---------------------------------------------------------------------------
+template <int FMT, int NW>
+struct WBlk {  // one block of the lane's row (rl) and k-group (kq), per matrix
+    uint4 hdr[NW];     // Q4_K header
+    uint64_t q[NW][4]; // Q4_K: the 4 nibble groups' 8 bytes; Q8_0: q[m][0]; Q6_K: ql (4)
+    uint64_t qh[NW][2];
+    uint32_t scw[NW];  // Q6_K: the 4 int8 scales of this k-group
+    float d[NW];       // Q6_K / Q8_0 block scale
+};
+
+// Loads are unconditional (a row or token past the end reads the last one,
+// then its scale is zeroed), so no branch separates a load from its use and
+// the next block's loads stay in flight across the current block's compute.
+template <int FMT, int NW>
+__device__ inline WBlk<FMT, NW> load_wblk(const GemmArgs &a, int row, bool rin, int kq, int b) {
+    WBlk<FMT, NW> w;
+    const int64_t blk = (int64_t)min(row, a.nrows - 1) * a.nb + b;
+#pragma unroll
+    for (int m = 0; m < NW; m++) {
+        const uint8_t *base = m ? a.w2 : a.w;
+        if constexpr (FMT == F_Q4K) {
+            const uint8_t *p = base + blk * Q4K_BYTES;
+            w.hdr[m] = ld16(p);
+#pragma unroll
+            for (int g = 0; g < 4; g++) w.q[m][g] = ld8(p + 16 + 32 * g + 8 * kq);
+        } else if constexpr (FMT == F_Q80) {
+            w.q[m][0] = ld8(base + blk * Q8_BODY + 8 * kq);
+            w.d[m] = h2f((m ? a.s2 : a.s)[blk]);
+        } else {
+            const uint8_t *body = base + blk * Q6K_BODY;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                w.q[m][2 * h] = ld8(body + 64 * h + 8 * kq);
+                w.q[m][2 * h + 1] = ld8(body + 64 * h + 32 + 8 * kq);
+                w.qh[m][h] = ld8(body + 128 + 32 * h + 8 * kq);
+            }
+            w.scw[m] = *(const uint32_t *)(body + 192 + 4 * kq);
+            w.d[m] = h2f((m ? a.s2 : a.s)[blk]);
+        }
+    }
+    return w;
+}
+
+template <int FMT, int NW>
+__device__ inline void mask_wblk(WBlk<FMT, NW> &w, bool rin) {
+#pragma unroll
+    for (int m = 0; m < NW; m++) {
+        if constexpr (FMT == F_Q4K) w.hdr[m].x = rin ? w.hdr[m].x : 0u;  // d = dmin = 0
+        else w.d[m] = rin ? w.d[m] : 0.f;
+    }
+}
+
+// Activation fragments of one block for the lane's token and k-group.
+template <int FMT>
+struct ABlk {
+    static constexpr int C = FMT == F_Q80 ? 1 : 8;  // 32-value chunks per block
+    uint64_t hi[C], lo[C];
+    float xs[C], xsum[C];
+    int is[FMT == F_Q6K ? 16 : 1];
+};
+
+template <int FMT>
+__device__ inline ABlk<FMT> load_ablk(const GemmArgs &a, int tok, int kq, int b) {
+    ABlk<FMT> x;
+    const CAct xa = cact_view(a.act + (int64_t)min(tok, a.M - 1) * a.act_stride, a.n_in);
+#pragma unroll
+    for (int c = 0; c < ABlk<FMT>::C; c++) {
+        const int ch = b * ABlk<FMT>::C + c;
+        x.hi[c] = ld8(xa.hi + 32 * ch + 8 * kq);
+        x.lo[c] = ld8(xa.lo + 32 * ch + 8 * kq);
+        x.xs[c] = xa.scale[ch];
+        x.xsum[c] = xa.sum[ch];
+    }
+    if constexpr (FMT == F_Q6K) {
+#pragma unroll
+        for (int g = 0; g < 16; g++) x.is[g] = xa.isum[b * 16 + g];
+    }
+    return x;
+}
+
+template <int FMT>
+__device__ inline void mask_ablk(ABlk<FMT> &x, bool tin) {
+#pragma unroll
+    for (int c = 0; c < ABlk<FMT>::C; c++) {
+        x.xs[c] = tin ? x.xs[c] : 0.f;
+        x.xsum[c] = tin ? x.xsum[c] : 0.f;
+    }
+}
+
+// acc[m][i] += block b's products for rows 4*kq+i of the tile and token rl.
+template <int FMT, int NW>
+__device__ inline void compute_blk(GemmLds &S, const WBlk<FMT, NW> &w, const ABlk<FMT> &x, int kq, int rl,
+                                   float (&acc)[NW][4]) {
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int m = 0; m < NW; m++) {
+        if constexpr (FMT == F_Q4K) {
+            int sc0, m0, sc1, m1;
+            kq_scale_min_pair(kq, w.hdr[m].y, w.hdr[m].z, w.hdr[m].w, sc0, m0, sc1, m1);
+            const float d = h2f(w.hdr[m].x & 0xffff), dmin = h2f(w.hdr[m].x >> 16);
+            S.scl[m][2 * kq][rl] = make_float2(d * (float)sc0, dmin * (float)m0);
+            S.scl[m][2 * kq + 1][rl] = make_float2(d * (float)sc1, dmin * (float)m1);
+        } else if constexpr (FMT == F_Q80) {
+            if (kq == 0) S.scl[m][0][rl] = make_float2(w.d[m], 0.f);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                S.scl[m][4 * kq + j][rl] = make_float2(w.d[m] * (float)(int8_t)((w.scw[m] >> (8 * j)) & 0xff), 0.f);
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int m = 0; m < NW; m++) {
+        if constexpr (FMT == F_Q4K) {
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                const uint64_t qa = (s & 1) ? (w.q[m][s >> 1] >> 4) & 0x0F0F0F0F0F0F0F0Full
+                                            : w.q[m][s >> 1] & 0x0F0F0F0F0F0F0F0Full;
+                const float4 sA = *(const float4 *)&S.scl[m][s][4 * kq];
+                const float4 sB = *(const float4 *)&S.scl[m][s][4 * kq + 2];
+                const float dsc[4] = {sA.x, sA.z, sB.x, sB.z}, dm[4] = {sA.y, sA.w, sB.y, sB.w};
+                const v4i ch = mfma(qa, x.hi[s]), cl = mfma(qa, x.lo[s]);
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    acc[m][i] += dsc[i] * x.xs[s] * (float)(ch[i] * 256 + cl[i]) - dm[i] * x.xsum[s];
+            }
+        } else if constexpr (FMT == F_Q80) {
+            const float4 sA = *(const float4 *)&S.scl[m][0][4 * kq];
+            const float4 sB = *(const float4 *)&S.scl[m][0][4 * kq + 2];
+            const float d[4] = {sA.x, sA.z, sB.x, sB.z};
+            const v4i ch = mfma(w.q[m][0], x.hi[0]), cl = mfma(w.q[m][0], x.lo[0]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[m][i] += d[i] * x.xs[0] * (float)(ch[i] * 256 + cl[i]);
+        } else {
+#pragma unroll
+            for (int c32 = 0; c32 < 8; c32++) {
+                const int h = c32 >> 2, c = c32 & 3;
+                const uint64_t lo4 = (w.q[m][2 * h + (c & 1)] >> (4 * (c >> 1))) & 0x0F0F0F0F0F0F0F0Full;
+                const uint64_t hi2 = ((w.qh[m][h] >> (2 * c)) & 0x0303030303030303ull) << 4;
+                const uint64_t q = lo4 | hi2;
+                const uint64_t qa0 = kq < 2 ? q : 0, qa1 = kq < 2 ? 0 : q;
+                const float4 s0A = *(const float4 *)&S.scl[m][2 * c32][4 * kq];
+                const float4 s0B = *(const float4 *)&S.scl[m][2 * c32][4 * kq + 2];
+                const float4 s1A = *(const float4 *)&S.scl[m][2 * c32 + 1][4 * kq];
+                const float4 s1B = *(const float4 *)&S.scl[m][2 * c32 + 1][4 * kq + 2];
+                const float e0[4] = {s0A.x, s0A.z, s0B.x, s0B.z}, e1[4] = {s1A.x, s1A.z, s1B.x, s1B.z};
+                const v4i h0 = mfma(qa0, x.hi[c32]), l0 = mfma(qa0, x.lo[c32]);
+                const v4i h1 = mfma(qa1, x.hi[c32]), l1 = mfma(qa1, x.lo[c32]);
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    acc[m][i] += x.xs[c32] * (e0[i] * (float)(h0[i] * 256 + l0[i] - 32 * x.is[2 * c32]) +
+                                                e1[i] * (float)(h1[i] * 256 + l1[i] - 32 * x.is[2 * c32 + 1]));
+            }
+        }
+    }
+}
+
+template <int FMT, int MODE>
+__global__ __launch_bounds__(256) void k_gemm_small(GemmArgs a) {
+    constexpr int NW = MODE == G_GLU ? 2 : 1;
+    __shared__ GemmLds L[4];
+    __shared__ float red[3][NW][64][4];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: a scalar block loop
+    const int l = threadIdx.x & 63, kq = l >> 4, rl = l & 15;
+    GemmLds &S = L[wave];
+    const int r0 = blockIdx.x * 16, row = r0 + rl;
+    const bool rin = row < a.nrows;
+    const int bpq = (a.nb + 3) / 4, b0 = wave * bpq, b1 = min(a.nb, b0 + bpq);
+    float acc[NW][4];
+#pragma unroll
+    for (int m = 0; m < NW; m++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[m][i] = 0.f;
+    const bool tin = rl < a.M;
+    if (b0 < b1) {  // ping-pong buffers: no register copy waits on a load in flight
+        WBlk<FMT, NW> wA = load_wblk<FMT, NW>(a, row, rin, kq, b0), wB;
+        ABlk<FMT> xA = load_ablk<FMT>(a, rl, kq, b0), xB;
+        for (int b = b0;;) {
+            wB = load_wblk<FMT, NW>(a, row, rin, kq, min(b + 1, b1 - 1));
+            xB = load_ablk<FMT>(a, rl, kq, min(b + 1, b1 - 1));
+            mask_wblk(wA, rin), mask_ablk(xA, tin);
+            compute_blk<FMT, NW>(S, wA, xA, kq, rl, acc);
+            if (++b >= b1) break;
+            wA = load_wblk<FMT, NW>(a, row, rin, kq, min(b + 1, b1 - 1));
+            xA = load_ablk<FMT>(a, rl, kq, min(b + 1, b1 - 1));
+            mask_wblk(wB, rin), mask_ablk(xB, tin);
+            compute_blk<FMT, NW>(S, wB, xB, kq, rl, acc);
+            if (++b >= b1) break;
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int m = 0; m < NW; m++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) red[wave - 1][m][l][i] = acc[m][i];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int q = 0; q < 3; q++)
+#pragma unroll
+        for (int m = 0; m < NW; m++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[m][i] += red[q][m][l][i];
+    const int tok = rl;
+    if (tok >= a.M) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = r0 + 4 * kq + i;
+        if (r >= a.nrows) continue;
+        const int64_t o = (int64_t)tok * a.ldy + r;
+        const float v = acc[0][i];
+        if (MODE == G_ADD) a.out[o] = a.y_in[o] + v;
+        else if (MODE == G_GLU) a.out[o] = v / (1.0f + expf(-v)) * acc[NW - 1][i];  // cpu_backend.cpp:260-261
+        else a.out[o] = v;
+    }
+}
+
 // Split-K: y[t][r] = (y_in +) sum over splits in order (GLU: silu(g) * u).
 __global__ void k_gemm_reduce(const float *__restrict__ part, int ks, int M, int nrows, int mode, float *y,
                               const float *y_in, int64_t ldy) {
@@ -269,7 +493,8 @@ __global__ void k_gemm_reduce(const float *__restrict__ part, int ks, int M, int
 // ---------------------------------------------------------------------------
 template <int FMT, int MODE>
 static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
-    if (tn == 4) hipLaunchKernelGGL((k_gemm<FMT, MODE, 4>), grid, dim3(256), 0, s, a);
+    if (a.M <= 16) hipLaunchKernelGGL((k_gemm_small<FMT, MODE>), dim3((a.nrows + 15) / 16), dim3(256), 0, s, a);
+    else if (tn == 4) hipLaunchKernelGGL((k_gemm<FMT, MODE, 4>), grid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL((k_gemm<FMT, MODE, 1>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
@@ -290,6 +515,7 @@ void set_gemm_cu_count(int n) { g_gemm_cu = n > 0 ? n : 256; }
 // Splits of K that give the launch about four workgroups per CU when the
 // tokens alone do not (small M: the matmul is a weight stream).
 static int gemm_splits(int64_t rows, int M, int nb, int tn) {
+    if (M <= 16) return 1;  // k_gemm_small splits the blocks inside the workgroup
     const int64_t wgs = ((rows + 63) / 64) * ((M + 16 * tn - 1) / (16 * tn));
     int ks = (int)std::min<int64_t>(16, std::max<int64_t>(1, (4 * g_gemm_cu + wgs - 1) / wgs));
     return std::min(ks, nb);

@@ -260,27 +260,32 @@ struct Q80 {
 // The activation prologue: x (n values, optionally rms-normalised by norm_w)
 // -> Act in LDS.
 // ---------------------------------------------------------------------------
+// 1 / sqrt(mean(x^2) + eps) over the n values (1 without norm weights).
 template <int NT>
-__device__ inline void build_act(const float *__restrict__ x, const float *__restrict__ norm_w, float eps, int n,
-                                 const Act &a, float *red) {
-    // Two threads per 32-value sub-block, 16 values each, every thread busy:
-    // the pair exchanges its max and sum once; each thread owns one 16-run.
-    float s = 1.0f;
-    if (norm_w) {
-        float ss = 0.f;
-        for (int i = 4 * threadIdx.x; i < n; i += 4 * NT) {
-            const float4 v = *(const float4 *)(x + i);
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-        }
-        ss = wave_sum(ss);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-        __syncthreads();
-        ss = 0.f;
-#pragma unroll
-        for (int w = 0; w < NT / 64; w++) ss += red[w];
-        s = 1.0f / sqrtf(ss / (float)n + eps);
+__device__ inline float act_rms(const float *__restrict__ x, const float *__restrict__ norm_w, float eps, int n,
+                                float *red) {
+    if (!norm_w) return 1.0f;
+    float ss = 0.f;
+    for (int i = 4 * threadIdx.x; i < n; i += 4 * NT) {
+        const float4 v = *(const float4 *)(x + i);
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
     }
-    for (int r = threadIdx.x; r < n / 16; r += NT) {  // 16-run r, half (r & 1) of sub-block r / 2
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = 0.f;
+#pragma unroll
+    for (int w = 0; w < NT / 64; w++) ss += red[w];
+    return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+// The 16-runs r0 + threadIdx.x, r0 + threadIdx.x + NT, ... below r1 of Act a.
+// Two threads per 32-value sub-block, 16 values each, every thread busy: the
+// pair exchanges its max and sum once; each thread owns one 16-run.
+template <int NT>
+__device__ inline void act_runs(const float *__restrict__ x, const float *__restrict__ norm_w, float s, int r0,
+                                int r1, const Act &a) {
+    for (int r = r0 + threadIdx.x; r < r1; r += NT) {  // 16-run r, half (r & 1) of sub-block r / 2
         float v[16];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -332,6 +337,12 @@ __device__ inline void build_act(const float *__restrict__ x, const float *__res
             a.sum[r / 2] = sum;
         }
     }
+}
+
+template <int NT>
+__device__ inline void build_act(const float *__restrict__ x, const float *__restrict__ norm_w, float eps, int n,
+                                 const Act &a, float *red) {
+    act_runs<NT>(x, norm_w, act_rms<NT>(x, norm_w, eps, n, red), 0, n / 16, a);
     __syncthreads();
 }
 

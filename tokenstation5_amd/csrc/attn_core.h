@@ -522,7 +522,7 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
                 v[i] = 64 * i + lane < nt ? S.p_s[64 * i + lane][g] : -INFINITY;
                 mt = fmaxf(mt, v[i]);
             }
-            mt = wave_max(mt);
+            mt = wave_max_dpp(mt);
             const float mo = S.m_s[g], mn = fmaxf(mo, mt);
             float ls = 0.f;
 #pragma unroll
@@ -531,7 +531,7 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
                 if (64 * i < nt) S.p_s[64 * i + lane][g] = pe;
                 ls += pe;
             }
-            ls = wave_sum(ls);
+            ls = wave_sum_dpp(ls);
             if (lane == 0) {
                 const float al = mo == -INFINITY ? 0.f : expf(mo - mn);
                 S.alpha_s[g] = al;
@@ -569,13 +569,17 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
         }
         __syncthreads();  // p_s is rewritten by the next pass
     }
-    // The wave's KPW key groups of the same dims, then the 4 waves.
+    // The wave's KPW key groups of the same dims (lanes i ^ 8, ^ 16, ^ 32),
+    // then the 4 waves.
 #pragma unroll
-    for (int m = LPV; m < 64; m <<= 1)
+    for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) o[g][e] += __shfl_xor(o[g][e], m, WAVE);
+        for (int e = 0; e < 8; e++) {
+            float v = o[g][e];
+            if constexpr (LPV <= 8) v = dpp_add<0x128, 0xF, true>(v);  // row_ror:8 within 16-lane rows
+            if constexpr (LPV <= 16) v = add_xor16(v);
+            o[g][e] = add_xor32(v);
+        }
     if (vk == 0) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -600,34 +604,55 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
     if (tid == 0) S.last = atomicAdd(a.counters + b * a.HKV + kvh, 1) == n_split - 1;
     __syncthreads();
     if (!S.last) return;
+    // The merge: this thread's outputs of every split (up to 32 at a time)
+    // and every split's (m, l) are requested together; a wave per head turns
+    // the (m, l) into weights, a lane per split.
     const float *p_all = a.part + ((int64_t)b * n_split * a.H + (int64_t)kvh * G) * rec;
     const int64_t sstride = (int64_t)a.H * rec;
-    for (int j = tid; j < n_split * G; j += NT) {
-        const int s2 = j / G, g = j % G;
-        S.mw[s2][g] = p_all[s2 * sstride + g * rec + HD];
-        S.lw[s2][g] = p_all[s2 * sstride + g * rec + HD + 1];
-    }
-    __syncthreads();
-    if (tid < G) {
-        float M = -INFINITY;
-        for (int s2 = 0; s2 < n_split; s2++) M = fmaxf(M, S.mw[s2][tid]);
-        float L = 0.f;
-        for (int s2 = 0; s2 < n_split; s2++) {
-            const float m = S.mw[s2][tid];
-            const float w = m == -INFINITY ? 0.f : expf(m - M);
-            S.mw[s2][tid] = w;
-            L += w * S.lw[s2][tid];
+    constexpr int OPT = (G * HD + NT - 1) / NT, MC = 32;
+    float acc[OPT];
+#pragma unroll
+    for (int k = 0; k < OPT; k++) acc[k] = 0.f;
+    for (int s0 = 0; s0 < n_split; s0 += MC) {
+        const int nc = min(MC, n_split - s0);
+        float ov[OPT][MC];
+#pragma unroll
+        for (int k = 0; k < OPT; k++) {
+            const int j = min(tid + NT * k, G * HD - 1), g = j / HD, d = j % HD;
+#pragma unroll
+            for (int i = 0; i < MC; i++) ov[k][i] = p_all[(int64_t)(s0 + min(i, nc - 1)) * sstride + g * rec + d];
         }
-        S.red[tid] = L;
+        if (s0 == 0) {
+            for (int g = wave; g < G; g += NT / 64) {
+                const int sl = min(lane, n_split - 1);
+                const float m0 = p_all[(int64_t)sl * sstride + g * rec + HD];
+                const float l0 = p_all[(int64_t)sl * sstride + g * rec + HD + 1];
+                const float m = lane < n_split ? m0 : -INFINITY;
+                const float M = wave_max_dpp(m);
+                const float w = m == -INFINITY ? 0.f : expf(m - M);
+                const float L = wave_sum_dpp(w * (lane < n_split ? l0 : 0.f));
+                if (lane < n_split) S.mw[lane][g] = w;
+                if (lane == 0) S.red[g] = L;
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int k = 0; k < OPT; k++) {
+            const int j = min(tid + NT * k, G * HD - 1), g = j / HD;
+            float v = acc[k];
+#pragma unroll
+            for (int i = 0; i < MC; i++)
+                if (i < nc) v += S.mw[s0 + i][g] * ov[k][i];
+            acc[k] = v;
+        }
     }
-    __syncthreads();
-    for (int j = tid; j < G * HD; j += NT) {
-        const int g = j / HD, d = j % HD;
-        const float *pd = p_all + g * rec + d;
-        float acc = 0.f;
-#pragma unroll 16
-        for (int s2 = 0; s2 < n_split; s2++) acc += S.mw[s2][g] * pd[s2 * sstride];
-        st_dev(a.out + (int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d, acc / S.red[g]);
+#pragma unroll
+    for (int k = 0; k < OPT; k++) {
+        const int j = tid + NT * k;
+        if (j < G * HD) {
+            const int g = j / HD, d = j % HD;
+            st_dev(a.out + (int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d, acc[k] / S.red[g]);
+        }
     }
     if (tid == 0) st_dev(a.counters + b * a.HKV + kvh, 0);  // ready for the next use
 }

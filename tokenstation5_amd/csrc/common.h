@@ -155,6 +155,31 @@ __device__ inline float wave_sum_dpp(float v) {
     v = dpp_add<0x143, 0xC, false>(v);  // row_bcast:31 into rows 2 and 3
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+// Max over the wave by the same DPP steps (disabled rows keep their own value).
+template <int CTRL, int ROW_MASK, bool BOUND>
+__device__ inline float dpp_max(float x) {
+    return fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), CTRL, ROW_MASK,
+                                                               0xF, BOUND)));
+}
+__device__ inline float wave_max_dpp(float v) {
+    v = dpp_max<0xB1, 0xF, true>(v);
+    v = dpp_max<0x4E, 0xF, true>(v);
+    v = dpp_max<0x141, 0xF, true>(v);
+    v = dpp_max<0x140, 0xF, true>(v);
+    v = dpp_max<0x142, 0xA, false>(v);
+    v = dpp_max<0x143, 0xC, false>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// v + the value of lane i ^ 16 (v_permlane16_swap), of lane i ^ 32
+// (v_permlane32_swap): VALU lane exchanges across 16-lane rows and wave halves.
+__device__ inline float add_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float add_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 __device__ inline float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));

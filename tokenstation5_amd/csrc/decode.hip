@@ -136,12 +136,10 @@ __device__ inline float ld_tagf(const uint64_t *p, uint32_t tag, int *err) {
 // ---------------------------------------------------------------------------
 // The weight ring.
 // ---------------------------------------------------------------------------
-// 64 lanes x 16 bytes from per-lane global addresses to LDS [base, base+1024).
-// Inline asm keeps the compiler from waiting for these loads (it would wait for
-// every LDS DMA before any LDS read); the stream's waits are explicit.
-__device__ inline void dma16(const void *g, uint32_t lds_base) {
-    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_base) : "memory");
-}
+// dma16 (mv_core.h): 64 lanes x 16 bytes from per-lane global addresses to
+// LDS [base, base+1024), by inline asm so that the compiler does not wait for
+// these loads (it would wait for every LDS DMA before any LDS read); the
+// stream's waits are explicit.
 // Workgroup barrier that also completes this wave's LDS reads before it.
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 // Stores through inline asm, so that each is exactly one instruction in the

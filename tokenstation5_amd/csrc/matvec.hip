@@ -1,6 +1,8 @@
 // One-token k-quant matvec kernels (plain, accumulating into a residual,
 // fused gate/up + SiLU, and the output head with the greedy argmax) over the
 // device core in mv_core.h.
+#include <algorithm>
+
 #include "kernels.h"
 #include "mv_core.h"
 
@@ -51,29 +53,79 @@ __global__ __launch_bounds__(WAVES *WAVE) void k_mv(MvArgs a) {
     }
 }
 
+// Q4_K plain / accumulate / gate-up matvecs through the per-wave LDS ring
+// (mv_run_dma): one workgroup of 4 waves per CU.
+template <class F, int R, int MODE, int NS>
+__global__ __launch_bounds__(256) void k_mv_ring(MvArgs a) {
+    extern __shared__ __align__(1024) uint8_t lds[];
+    __shared__ float red[4];
+    mv_run_dma<F, R, MODE, NS>(a, lds, red);
+}
+
 // ---------------------------------------------------------------------------
 // Launch shapes. Rows per group = R * WAVES; the grid is capped at two
 // workgroups per CU, so large matrices loop over their groups with the next
 // step's weights in flight.
 // ---------------------------------------------------------------------------
+#ifndef TS5_MV_WG_PER_CU
+#define TS5_MV_WG_PER_CU 2
+#endif
+#ifndef TS5_MV_GLU_WAVES
+#define TS5_MV_GLU_WAVES 4
+#endif
+#ifndef TS5_MV_GLU_R
+#define TS5_MV_GLU_R 2
+#endif
+#ifndef TS5_MV_R
+#define TS5_MV_R 4
+#endif
 static int g_n_cu = 256;
 void set_cu_count(int n) { g_n_cu = n > 0 ? n : 256; }
+// The grid cap, and so the most per-workgroup (value, row) pairs of the
+// head's argmax.
+static size_t mv_max_grid() { return (size_t)TS5_MV_WG_PER_CU * g_n_cu; }
 
 template <class F, int R, int WAVES, int MODE>
 static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
     const int64_t rpg = (int64_t)R * WAVES;
     const int64_t ngroups = (a.nrows + rpg - 1) / rpg;
-    const int64_t cap = 2LL * g_n_cu;
+    const int64_t cap = (int64_t)mv_max_grid();
     const int64_t per = (ngroups + cap - 1) / cap;  // groups per workgroup
     const unsigned grid = (unsigned)((ngroups + per - 1) / per);
     hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE>), dim3(grid), dim3(WAVES * WAVE), act_bytes(a.n_in), s, a);
     return hipGetLastError();
 }
 
+// Off by default: on the 8B decode shapes the ring kernel measured 5% slower
+// than k_mv (fused gate/up 20.4 us against 19.4 us), with twice k_mv's DRAM
+// credit stalls at the same bytes. Build with -DTS5_MV_RING=1 to use it.
+#ifndef TS5_MV_RING
+#define TS5_MV_RING 0
+#endif
+// The ring kernel when its LDS fits (160 KB per workgroup), else false.
+template <class F, int R, int MODE, int NS>
+static bool mv_ring_go(const MvArgs &a, hipStream_t s, hipError_t &e) {
+    const size_t lds = MvRing<F, R, MODE, NS>::lds_bytes(a.n_in);
+    if (!TS5_MV_RING || lds > 160 * 1024) return false;
+    const int64_t ngroups = (a.nrows + 4 * R - 1) / (4 * R);
+    const unsigned grid = (unsigned)std::min<int64_t>(ngroups, g_n_cu);
+    hipLaunchKernelGGL((k_mv_ring<F, R, MODE, NS>), dim3(grid), dim3(256), lds, s, a);
+    e = hipGetLastError();
+    return true;
+}
+
 template <int MODE>
 static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
+    if constexpr (MODE != MV_ARGMAX) {
+        hipError_t e = hipSuccess;
+        if (a.t == T_Q4_K &&
+            (MODE == MV_GLU ? mv_ring_go<Q4K, 2, MODE, 3>(a, s, e) : mv_ring_go<Q4K, 2, MODE, 4>(a, s, e)))
+            return e;
+    }
     switch (a.t) {
-    case T_Q4_K: return MODE == MV_GLU ? mv_go<Q4K, 2, 4, MODE>(a, s) : mv_go<Q4K, 4, 4, MODE>(a, s);
+    case T_Q4_K:
+        return MODE == MV_GLU ? mv_go<Q4K, TS5_MV_GLU_R, TS5_MV_GLU_WAVES, MODE>(a, s)
+                              : mv_go<Q4K, TS5_MV_R, 4, MODE>(a, s);
     case T_Q6_K: return MODE == MV_GLU ? mv_go<Q6K, 2, 4, MODE>(a, s) : mv_go<Q6K, 4, 4, MODE>(a, s);
     case T_Q8_0: return MODE == MV_GLU ? mv_go<Q80, 2, 4, MODE>(a, s) : mv_go<Q80, 4, 4, MODE>(a, s);
     }
@@ -102,7 +154,7 @@ hipError_t launch_matvec_glu(uint32_t t, const void *wg, const void *wu, int64_t
 }
 
 // Per-workgroup partials of the argmax epilogue: best values then best rows.
-size_t matvec_argmax_scratch_bytes() { return 8 * (size_t)(2 * g_n_cu + 64); }
+size_t matvec_argmax_scratch_bytes() { return 8 * mv_max_grid(); }
 
 hipError_t launch_matvec_argmax(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const float *x,
                                 const float *norm_w, float eps, float *y, void *scratch, int *counter, int32_t *out,
@@ -110,7 +162,7 @@ hipError_t launch_matvec_argmax(uint32_t t, const void *w, int64_t ne0, int64_t 
     MvArgs a = mv_args(t, w, ne0, ne1, x, norm_w, eps, y);
     a.counter = counter;
     a.best_v = (float *)scratch;
-    a.best_i = (int *)((uint8_t *)scratch + 4 * (size_t)(2 * g_n_cu + 64));
+    a.best_i = (int *)((uint8_t *)scratch + 4 * mv_max_grid());
     a.out = out, a.seq = seq, a.pos = pos;
     return mv_dispatch<MV_ARGMAX>(a, s);
 }

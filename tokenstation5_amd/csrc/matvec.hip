@@ -8,14 +8,14 @@
 
 namespace ts5hip {
 
-template <class F, int R, int WAVES, int MODE>
+template <class F, int R, int WAVES, int MODE, int RUNS, bool NORM>
 __global__ __launch_bounds__(WAVES *WAVE) void k_mv(MvArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[2 * WAVES];
     __shared__ int last;
     float best_v;
     int best_i;
-    mv_run<F, R, WAVES, MODE>(a, blockIdx.x, gridDim.x, lds, red, NoHook{}, best_v, best_i);
+    mv_run<F, R, WAVES, MODE, RUNS, NORM>(a, blockIdx.x, gridDim.x, lds, red, NoHook{}, best_v, best_i);
     if (MODE != MV_ARGMAX) return;
     // Each workgroup's best, then the last workgroup to finish picks the winner.
     if (threadIdx.x == 0) {
@@ -92,7 +92,18 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
     const int64_t cap = (int64_t)mv_max_grid();
     const int64_t per = (ngroups + cap - 1) / cap;  // groups per workgroup
     const unsigned grid = (unsigned)((ngroups + per - 1) / per);
-    hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE>), dim3(grid), dim3(WAVES * WAVE), act_bytes(a.n_in), s, a);
+    // The prologue's inputs in registers (runs per thread, norm weights) when
+    // they fit: up to 2 runs with the norm, 4 without; else the two-pass one.
+    const int nr = a.n_in / 16, nt = WAVES * WAVE;
+    const bool norm = a.norm_w != nullptr;
+    const dim3 g(grid), b(WAVES * WAVE);
+    const size_t lds = act_bytes(a.n_in);
+    if (nr <= nt && norm) hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, 1, true>), g, b, lds, s, a);
+    else if (nr <= nt) hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, 1, false>), g, b, lds, s, a);
+    else if (nr <= 2 * nt && norm) hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, 2, true>), g, b, lds, s, a);
+    else if (nr <= 2 * nt) hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, 2, false>), g, b, lds, s, a);
+    else if (nr <= 4 * nt && !norm) hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, 4, false>), g, b, lds, s, a);
+    else hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, 0, false>), g, b, lds, s, a);
     return hipGetLastError();
 }
 

@@ -294,13 +294,51 @@ __device__ inline float act_rms(const float *__restrict__ x, const float *__rest
     return 1.0f / sqrtf(ss / (float)n + eps);
 }
 
-// The 16-runs r0 + threadIdx.x, r0 + threadIdx.x + NT, ... below r1 of Act a.
-// Two threads per 32-value sub-block, 16 values each, every thread busy: the
-// pair exchanges its max and sum once; each thread owns one 16-run.
+// 16-run r of Act a (half r & 1 of sub-block r / 2) from its 16 values. Two
+// threads per 32-value sub-block, in adjacent lanes, exchange their max and
+// sum once (both call this together).
+__device__ inline void quant_run(const float (&v)[16], int r, const Act &a) {
+    float amax = 0.f, sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        sum += v[i];
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
+    sum += __shfl_xor(sum, 1, WAVE);
+    const float inv = amax > 0.f ? 16383.0f / amax : 0.f;
+    uint32_t hw[4], lw[4];
+    int is = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        uint32_t h = 0, l = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int x16 = max(-16383, min(16383, (int)rintf(v[4 * k + e] * inv)));
+            const int lo = (int)(int8_t)(x16 & 255);
+            const int hi = (x16 - lo) >> 8;
+            h |= (uint32_t)(hi & 255) << (8 * e);
+            l |= (uint32_t)(lo & 255) << (8 * e);
+            is += x16;
+        }
+        hw[k] = h, lw[k] = l;
+    }
+    *(uint4 *)(a.hi + 16 * r) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *(uint4 *)(a.lo + 16 * r) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    a.isum[r] = is;
+    if ((r & 1) == 0) {
+        a.scale[r / 2] = amax / 16383.0f;
+        a.sum[r / 2] = sum;
+    }
+}
+
+// The 16-runs r0 + threadIdx.x, r0 + threadIdx.x + NT, ... below r1 of Act a
+// (runs 2g and 2g+1 sit in adjacent lanes: NT is a multiple of 64 and r0, r1
+// are even, so both are in the loop together).
 template <int NT>
 __device__ inline void act_runs(const float *__restrict__ x, const float *__restrict__ norm_w, float s, int r0,
                                 int r1, const Act &a) {
-    for (int r = r0 + threadIdx.x; r < r1; r += NT) {  // 16-run r, half (r & 1) of sub-block r / 2
+    for (int r = r0 + threadIdx.x; r < r1; r += NT) {
         float v[16];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -317,40 +355,7 @@ __device__ inline void act_runs(const float *__restrict__ x, const float *__rest
                 v[4 * k + 3] = v[4 * k + 3] * s * w.w;
             }
         }
-        float amax = 0.f, sum = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            amax = fmaxf(amax, fabsf(v[i]));
-            sum += v[i];
-        }
-        // Runs 2g and 2g+1 sit in adjacent lanes (NT is a multiple of 64 and
-        // n / 16 is even, so both are in the loop together).
-        amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
-        sum += __shfl_xor(sum, 1, WAVE);
-        const float inv = amax > 0.f ? 16383.0f / amax : 0.f;
-        uint32_t hw[4], lw[4];
-        int is = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            uint32_t h = 0, l = 0;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int x16 = max(-16383, min(16383, (int)rintf(v[4 * k + e] * inv)));
-                const int lo = (int)(int8_t)(x16 & 255);
-                const int hi = (x16 - lo) >> 8;
-                h |= (uint32_t)(hi & 255) << (8 * e);
-                l |= (uint32_t)(lo & 255) << (8 * e);
-                is += x16;
-            }
-            hw[k] = h, lw[k] = l;
-        }
-        *(uint4 *)(a.hi + 16 * r) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        *(uint4 *)(a.lo + 16 * r) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-        a.isum[r] = is;
-        if ((r & 1) == 0) {
-            a.scale[r / 2] = amax / 16383.0f;
-            a.sum[r / 2] = sum;
-        }
+        quant_run(v, r, a);
     }
 }
 
@@ -358,6 +363,75 @@ template <int NT>
 __device__ inline void build_act(const float *__restrict__ x, const float *__restrict__ norm_w, float eps, int n,
                                  const Act &a, float *red) {
     act_runs<NT>(x, norm_w, act_rms<NT>(x, norm_w, eps, n, red), 0, n / 16, a);
+    __syncthreads();
+}
+
+// The same prologue with its inputs requested up front: thread t's runs
+// t, t + NT, ... (at most RUNS) of x, and of the norm weights with NORM, go to
+// registers before the weight loads are issued, so they come back first
+// (loads complete in order) and the norm's sum and the quantization need no
+// second pass over memory.
+template <int NT, int RUNS, bool NORM>
+struct ActIn {
+    float4 x[RUNS][4];
+    float4 w[NORM ? RUNS : 1][4];
+};
+template <int NT, int RUNS, bool NORM>
+__device__ inline void act_in_load(ActIn<NT, RUNS, NORM> &in, const float *__restrict__ x,
+                                   const float *__restrict__ norm_w, int n) {
+    const int nr = n / 16;
+#pragma unroll
+    for (int k = 0; k < RUNS; k++) {
+        const int r = min((int)threadIdx.x + NT * k, nr - 1);  // past the end: a valid run, not used
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            in.x[k][j] = *(const float4 *)(x + 16 * r + 4 * j);
+            if constexpr (NORM) in.w[k][j] = *(const float4 *)(norm_w + 16 * r + 4 * j);
+        }
+    }
+}
+template <int NT, int RUNS, bool NORM>
+__device__ inline void act_in_build(const ActIn<NT, RUNS, NORM> &in, float eps, int n, const Act &a, float *red) {
+    const int nr = n / 16;
+    float s = 1.0f;
+    if constexpr (NORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < RUNS; k++) {
+            if ((int)threadIdx.x + NT * k >= nr) continue;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float4 v = in.x[k][j];
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+        }
+        ss = wave_sum_dpp(ss);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        ss = 0.f;
+#pragma unroll
+        for (int w = 0; w < NT / 64; w++) ss += red[w];
+        s = 1.0f / sqrtf(ss / (float)n + eps);
+    }
+#pragma unroll
+    for (int k = 0; k < RUNS; k++) {
+        const int r = (int)threadIdx.x + NT * k;
+        if (r >= nr) continue;
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float4 f = in.x[k][j];
+            v[4 * j] = f.x, v[4 * j + 1] = f.y, v[4 * j + 2] = f.z, v[4 * j + 3] = f.w;
+            if constexpr (NORM) {
+                const float4 w = in.w[k][j];
+                v[4 * j] = v[4 * j] * s * w.x;
+                v[4 * j + 1] = v[4 * j + 1] * s * w.y;
+                v[4 * j + 2] = v[4 * j + 2] * s * w.z;
+                v[4 * j + 3] = v[4 * j + 3] * s * w.w;
+            }
+        }
+        quant_run(v, r, a);
+    }
     __syncthreads();
 }
 
@@ -404,7 +478,7 @@ __device__ inline void best_pick_wave(float &v, int &i) {
 // built (the persistent kernel's grid barrier). lds: act_bytes(a.n_in)
 // bytes; red: NT/64 floats. MV_ARGMAX returns this workgroup's best
 // (value, row) in best_v / best_i (every thread).
-template <class F, int R, int WAVES, int MODE, class Hook>
+template <class F, int R, int WAVES, int MODE, int RUNS, bool NORM, class Hook>
 __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, float *red, Hook before_act,
                               float &best_v, int &best_i) {
     constexpr int NT = WAVES * WAVE, BPI = WAVE / F::LPB, NW = MODE == MV_GLU ? 2 : 1;
@@ -419,6 +493,8 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
 
     int64_t g = wg;
     int it = 0;
+    ActIn<NT, RUNS ? RUNS : 1, NORM> ain;
+    if constexpr (RUNS > 0) act_in_load<NT, RUNS, NORM>(ain, a.x, a.norm_w, a.n_in);
     typename F::W cur[NW][R], nxt[NW][R];
     if (g < ngroups) {
         const int64_t row0 = g * rpg + (int64_t)wave * R;
@@ -427,7 +503,8 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
     }
     before_act();
     const Act xa = act_view(lds, a.n_in);
-    if (g < ngroups) build_act<NT>(a.x, a.norm_w, a.eps, a.n_in, xa, red);
+    if constexpr (RUNS > 0) act_in_build<NT, RUNS, NORM>(ain, a.eps, a.n_in, xa, red);
+    else if (g < ngroups) build_act<NT>(a.x, a.norm_w, a.eps, a.n_in, xa, red);
     const CAct x{xa.hi, xa.lo, xa.scale, xa.sum, xa.isum};
 
     float acc[NW][R];

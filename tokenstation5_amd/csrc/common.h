@@ -121,6 +121,7 @@ __device__ inline uint16_t f2h(float f) {
 
 __device__ inline int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+
 // Cross-workgroup data. A store another workgroup will read goes out
 // device-coherent (global_store ... sc1, written through past this XCD's L2);
 // the writer waits for its stores (s_waitcnt vmcnt(0): __syncthreads does not

@@ -2,20 +2,49 @@
 // fused gate/up + SiLU, and the output head with the greedy argmax) over the
 // device core in mv_core.h.
 #include <algorithm>
+#include <climits>
 
 #include "kernels.h"
 #include "mv_core.h"
 
 namespace ts5hip {
 
+// The arguments only some modes need, passed after the others.
+struct MvTail {
+    uint32_t t;
+    int nb;
+    const float *y_in;
+    float *best_v;
+    int *best_i, *counter;
+    int32_t *out, *seq, *pos;
+};
+
+// The arguments every mode needs come first and one by one: 14 dwords the
+// command processor preloads into SGPRs at wave launch (the matvec file builds
+// with -amdgpu-kernarg-preload-count=16; two of the 16 user SGPRs hold the
+// argument pointer), so a launch does not start with a round trip to its
+// argument buffer. nwg is the grid size.
 template <class F, int R, int WAVES, int MODE, int RUNS, bool NORM>
-__global__ __launch_bounds__(WAVES *WAVE) void k_mv(MvArgs a) {
+__global__ __launch_bounds__(WAVES *WAVE) void k_mv(const void *w, const void *w2, const float *x,
+                                                    const float *norm_w, float *y, int nrows, int n_in, int nwg,
+                                                    float eps, MvTail tail) {
+    MvArgs a;
+    a.t = tail.t, a.w = w, a.w2 = w2, a.nrows = nrows, a.nb = tail.nb, a.n_in = n_in, a.x = x, a.norm_w = norm_w;
+    a.eps = eps, a.y = y, a.y_in = tail.y_in;
+    a.best_v = tail.best_v, a.best_i = tail.best_i, a.counter = tail.counter, a.out = tail.out, a.seq = tail.seq;
+    a.pos = tail.pos;
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[2 * WAVES];
     __shared__ int last;
     float best_v;
     int best_i;
-    mv_run<F, R, WAVES, MODE, RUNS, NORM>(a, blockIdx.x, gridDim.x, lds, red, NoHook{}, best_v, best_i);
+    // The type and block count are compile-time facts of F and n_in; only the
+    // residual pointer of MV_ADD is fetched, once the first loads are out.
+    a.nb = n_in / F::VALUES;
+    auto fetch_tail = [&]() {
+        if constexpr (MODE == MV_ADD) asm volatile("" ::"s"(a.y_in));
+    };
+    mv_run<F, R, WAVES, MODE, RUNS, NORM>(a, blockIdx.x, nwg, lds, red, fetch_tail, best_v, best_i);
     if (MODE != MV_ARGMAX) return;
     // Each workgroup's best, then the last workgroup to finish picks the winner.
     if (threadIdx.x == 0) {
@@ -87,6 +116,7 @@ static size_t mv_max_grid() { return (size_t)TS5_MV_WG_PER_CU * g_n_cu; }
 
 template <class F, int R, int WAVES, int MODE>
 static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
+    if (a.nrows > INT32_MAX) return hipErrorInvalidValue;  // the kernel takes a 32-bit row count
     const int64_t rpg = (int64_t)R * WAVES;
     const int64_t ngroups = (a.nrows + rpg - 1) / rpg;
     const int64_t cap = (int64_t)mv_max_grid();
@@ -98,12 +128,17 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
     const bool norm = a.norm_w != nullptr;
     const dim3 g(grid), b(WAVES * WAVE);
     const size_t lds = act_bytes(a.n_in);
-    if (nr <= nt && norm) hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, 1, true>), g, b, lds, s, a);
-    else if (nr <= nt) hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, 1, false>), g, b, lds, s, a);
-    else if (nr <= 2 * nt && norm) hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, 2, true>), g, b, lds, s, a);
-    else if (nr <= 2 * nt) hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, 2, false>), g, b, lds, s, a);
-    else if (nr <= 4 * nt && !norm) hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, 4, false>), g, b, lds, s, a);
-    else hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, 0, false>), g, b, lds, s, a);
+    const MvTail tail{a.t, a.nb, a.y_in, a.best_v, a.best_i, a.counter, a.out, a.seq, a.pos};
+#define TS5_MV_LAUNCH(RUNS, NORM)                                                                                 \
+    hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, RUNS, NORM>), g, b, lds, s, a.w, a.w2, a.x, a.norm_w, a.y,        \
+                       (int)a.nrows, a.n_in, (int)grid, a.eps, tail)
+    if (nr <= nt && norm) TS5_MV_LAUNCH(1, true);
+    else if (nr <= nt) TS5_MV_LAUNCH(1, false);
+    else if (nr <= 2 * nt && norm) TS5_MV_LAUNCH(2, true);
+    else if (nr <= 2 * nt) TS5_MV_LAUNCH(2, false);
+    else if (nr <= 4 * nt && !norm) TS5_MV_LAUNCH(4, false);
+    else TS5_MV_LAUNCH(0, false);
+#undef TS5_MV_LAUNCH
     return hipGetLastError();
 }
 

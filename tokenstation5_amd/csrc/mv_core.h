@@ -52,7 +52,7 @@ __device__ inline uint4 ld16(const void *p) { return *(const uint4 *)p; }
 // Q4_K: 4 lanes per block, lane `sub` = nibble group g: sub-blocks 2g (low
 // nibbles) and 2g+1 (high nibbles), 64 values.
 struct Q4K {
-    static constexpr int LPB = 4;
+    static constexpr int LPB = 4, VALUES = 256;  // lanes per block, values per block
     struct X {
         uint32_t h0[8], h1[8], l0[8], l1[8];
         float s0, s1, m0, m1;
@@ -142,7 +142,7 @@ struct Q4K {
 // Q6_K: 4 lanes per block, lane `sub` = (half h = sub/2, i0 = 16*(sub%2)):
 // the four 16-value runs at 128h + 32c + i0 (c = 0..3), 64 values.
 struct Q6K {
-    static constexpr int LPB = 4;
+    static constexpr int LPB = 4, VALUES = 256;
     struct X {
         uint32_t h[4][4], l[4][4];  // [run c][dword]
         float s[4];
@@ -228,7 +228,7 @@ struct Q6K {
 
 // Q8_0: 2 lanes per 32-value block, 16 values each.
 struct Q80 {
-    static constexpr int LPB = 2;
+    static constexpr int LPB = 2, VALUES = 32;
     struct X {
         uint4 h, l;
         float s;
@@ -491,12 +491,17 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
     best_v = -INFINITY;
     best_i = INT_MAX;
 
+    // Every argument the prologue and the first loads need, fetched together
+    // (the compiler would fetch each where first used: a round trip apiece).
+    asm volatile("" ::"s"(a.w), "s"(a.w2), "s"(a.x), "s"(a.norm_w), "s"(a.y), "s"(a.nrows), "s"(a.nb), "s"(a.n_in),
+                 "s"(a.eps), "s"(nwg));
     int64_t g = wg;
     int it = 0;
     ActIn<NT, RUNS ? RUNS : 1, NORM> ain;
     if constexpr (RUNS > 0) act_in_load<NT, RUNS, NORM>(ain, a.x, a.norm_w, a.n_in);
     typename F::W cur[NW][R], nxt[NW][R];
-    if (g < ngroups) {
+    {  // unconditional (rows are clamped; every launch has wg < ngroups), so no
+       // branch makes the compiler's waits for the activation cover these
         const int64_t row0 = g * rpg + (int64_t)wave * R;
         load_rows<F, R>(w1, row0, a.nrows, a.nb, bsub, sub, cur[0]);
         if (MODE == MV_GLU) load_rows<F, R>(w2, row0, a.nrows, a.nb, bsub, sub, cur[NW - 1]);

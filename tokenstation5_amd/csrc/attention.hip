@@ -86,10 +86,22 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float *__restrict__ qkv, i
     }
 }
 
+// What the work item needs before its first loads (where its keys are) comes
+// first and one by one, 14 dwords preloaded into SGPRs at wave launch (this
+// file builds with -amdgpu-kernarg-preload-count=16); the rest of AttnArgs
+// (query, RoPE, norms, partials, output) follows in `tail`. flags: 1
+// kv_per_batch, 2 append, 4 rope.
 template <int HD, int G>
-__global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
+__global__ __launch_bounds__(256) void k_attn(const int8_t *k8, const uint16_t *ks, const int8_t *v8,
+                                              const uint16_t *vs, const int32_t *n_keys, int n_ctx, int HKV,
+                                              int flags, int n_split, AttnArgs tail) {
     __shared__ SliceLds<HD, G> S;
-    attn_slice<HD, G>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x, S);
+    AttnArgs a = tail;
+    a.kv = KvLayer{const_cast<int8_t *>(k8), const_cast<uint16_t *>(ks), const_cast<int8_t *>(v8),
+                   const_cast<uint16_t *>(vs)};
+    a.n_keys = n_keys, a.n_ctx = n_ctx, a.HKV = HKV;
+    a.kv_per_batch = flags & 1, a.append = (flags >> 1) & 1, a.rope = (flags >> 2) & 1;
+    attn_slice<HD, G>(a, blockIdx.x, blockIdx.y, blockIdx.z, n_split, S);
 }
 
 // K (which 0) or V (1) at positions [pos0, pos0 + n) dequantized to fp32
@@ -121,9 +133,12 @@ hipError_t launch_rope_kv(const float *qkv, int64_t qkv_stride, const float *bia
 
 template <int HD>
 static hipError_t attn_launch(int G, dim3 grid, const AttnArgs &a, hipStream_t s) {
-#define TS5_ATTN(GG)                                                      \
-    case GG:                                                              \
-        hipLaunchKernelGGL((k_attn<HD, GG>), grid, dim3(256), 0, s, a); \
+    const int flags = (a.kv_per_batch ? 1 : 0) | (a.append ? 2 : 0) | (a.rope ? 4 : 0);
+#define TS5_ATTN(GG)                                                                                          \
+    case GG:                                                                                                  \
+        hipLaunchKernelGGL((k_attn<HD, GG>), grid, dim3(256), 0, s, (const int8_t *)a.kv.k,                   \
+                           (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs, a.n_keys, \
+                           a.n_ctx, a.HKV, flags, (int)grid.x, a);                                           \
         break;
     switch (G) {
         TS5_ATTN(1)

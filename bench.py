@@ -34,6 +34,13 @@ sys.path.insert(0, ROOT)
 from tokenstation5_amd import synth, ts5hip  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the roofline kernel, from rocprofv3 --pmc runs of
+# `bench.py --roofline-only` (profiles/glu_roofline_counters.md): FETCH_SIZE
+# 32,438.2 KiB and WRITE_SIZE 224 KiB per dispatch, scaled by what the same
+# counters read for the one-pass RMSNorm stream of 256 MiB in and 256 MiB out
+# (131,220.6 and 262,144 KiB: factors 1.9977 and 1.0). 1.007 x the algorithmic
+# bytes.
+GLU_TRAFFIC_BYTES = 66587577
 PROMPT = 4096
 SEED = 20241201
 
@@ -135,16 +142,17 @@ def glu_roofline(ctx, hp, launches: int = 200):
     for b in gates + ups:
         b.free()
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=GLU_TRAFFIC_BYTES,
                 kernel="k_mv<Q4K,2,4,MV_GLU> (ffn rmsnorm+gate+up+SiLU, 14336x4096 x2)", avg_us=round(avg_us, 2),
                 algorithmic_bytes=int(algo))
 
 
 def roofline_only(hp):
     """The roofline kernel's launches alone, then one RMSNorm over 256 MiB
-    (k_rmsnorm: reads 256 MiB once, writes 256 MiB once): the known-size
-    stream that scales the hardware counters (FETCH_SIZE, WRITE_SIZE) of a
-    rocprofv3 --pmc run of this mode."""
+    (k_rmsnorm_reg: 16384 rows of 4096 values, each row held in registers
+    between its sum and its write, so it reads 256 MiB once and writes 256 MiB
+    once): the known-size stream that scales the hardware counters
+    (FETCH_SIZE, WRITE_SIZE) of a rocprofv3 --pmc run of this mode."""
     ctx = ts5hip.Context(0)
     roof = glu_roofline(ctx, hp, launches=40)
     n, rows = 4096, 16384

@@ -111,13 +111,14 @@ def test_act_quantize(ctx, n, norm):
     assert np.array_equal(isum[0], x16[0].reshape(-1, 16).sum(1))
 
 
-def test_rmsnorm(ctx):
+@pytest.mark.parametrize("n", [4096, 1000, 8192])  # one pass in registers up to 4096, else two passes
+def test_rmsnorm(ctx, n):
     rng = np.random.default_rng(3)
-    x = (rng.standard_normal((3, 4096)) * 1e6).astype(np.float32)
-    w = (1 + 0.02 * rng.standard_normal(4096)).astype(np.float32)
+    x = (rng.standard_normal((3, n)) * 1e6).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(n)).astype(np.float32)
     y = ctx.alloc(x.nbytes)
-    ctx.rmsnorm(ctx.to_device(x), ctx.to_device(w), 1e-5, 4096, 3, y)
-    got = y.download(np.float32, (3, 4096))
+    ctx.rmsnorm(ctx.to_device(x), ctx.to_device(w), 1e-5, n, 3, y)
+    got = y.download(np.float32, (3, n))
     want = np.stack([oracle.rmsnorm(x[t], w, 1e-5) for t in range(3)])
     assert rel_l2(got, want) < 1e-6
 

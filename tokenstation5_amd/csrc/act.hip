@@ -50,8 +50,33 @@ __global__ __launch_bounds__(256) void k_act_quant(const float *__restrict__ x, 
     act_runs<256>(xt, w, s, r0, min(n / 16, r0 + 256), a);
 }
 
+// The same in one pass over x for rows of at most 256 * PER values: thread t
+// holds values t, t + 256, ... in registers between the norm's sum and the
+// scaled write, so each row is read from memory once.
+template <int PER>
+__global__ __launch_bounds__(256) void k_rmsnorm_reg(const float *__restrict__ x, const float *__restrict__ w,
+                                                     float eps, int n, float *__restrict__ y) {
+    __shared__ float red[4];
+    const float *xt = x + (int64_t)blockIdx.x * n;
+    float *yt = y + (int64_t)blockIdx.x * n;
+    float v[PER], ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int i = threadIdx.x + 256 * k;
+        v[k] = i < n ? xt[i] : 0.f;
+        ss += v[k] * v[k];
+    }
+    const float s = 1.0f / sqrtf(block_sum256(ss, red) / (float)n + eps);
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < n) yt[i] = v[k] * s * w[i];
+    }
+}
+
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int ntok, float *y, hipStream_t s) {
-    hipLaunchKernelGGL(k_rmsnorm, dim3(ntok), dim3(256), 0, s, x, w, eps, n, y);
+    if (n <= 256 * 16) hipLaunchKernelGGL(k_rmsnorm_reg<16>, dim3(ntok), dim3(256), 0, s, x, w, eps, n, y);
+    else hipLaunchKernelGGL(k_rmsnorm, dim3(ntok), dim3(256), 0, s, x, w, eps, n, y);
     return hipGetLastError();
 }
 

@@ -423,7 +423,7 @@ struct SliceLds {
     __align__(16) int8_t new8[2][HD];     // ... and after, as int8
     uint16_t new_sc[2][HD / 32];          // ... with their f16 scales
     __align__(16) float o_s[4][G * HD];   // each wave's p * v sums
-    float mw[ATTN_MAX_SPLIT][G], lw[ATTN_MAX_SPLIT][G];
+    __align__(16) float wts[G][ATTN_MAX_SPLIT];  // the merge's weight per (head, split), 0 past n_split
     int last;
 };
 
@@ -631,7 +631,7 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
                 const float M = wave_max_dpp(m);
                 const float w = m == -INFINITY ? 0.f : expf(m - M);
                 const float L = wave_sum_dpp(w * (lane < n_split ? l0 : 0.f));
-                if (lane < n_split) S.mw[lane][g] = w;
+                S.wts[g][lane] = w;  // lanes past n_split: 0
                 if (lane == 0) S.red[g] = L;
             }
             __syncthreads();
@@ -641,8 +641,10 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
             const int j = min(tid + NT * k, G * HD - 1), g = j / HD;
             float v = acc[k];
 #pragma unroll
-            for (int i = 0; i < MC; i++)
-                if (i < nc) v += S.mw[s0 + i][g] * ov[k][i];
+            for (int i4 = 0; i4 < MC / 4; i4++) {  // weights past n_split are 0 (their o: a valid split's)
+                const float4 w = *(const float4 *)&S.wts[g][s0 + 4 * i4];
+                v += w.x * ov[k][4 * i4] + w.y * ov[k][4 * i4 + 1] + w.z * ov[k][4 * i4 + 2] + w.w * ov[k][4 * i4 + 3];
+            }
             acc[k] = v;
         }
     }

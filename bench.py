@@ -114,11 +114,13 @@ def decode_bench(ctx, hp, steps: int, warmup: int, prompt_len: int = PROMPT):
 
 def glu_roofline(ctx, hp, launches: int = 200):
     """Fused gate/up + SiLU (k_mv_glu) alone on the library's stream, HIP events
-    around `launches` launches cycling through > 1 GiB of weight copies: a
+    around `launches` launches cycling through > 1 GiB of weight copies (a
     token sweeps 4.3 GB of weights, so none of its matrices is still in the
-    256 MB Infinity Cache when it comes round again, and with a rotation of
-    only ~330 MB half of each launch's weights were still found there
-    (rocprofv3 FETCH_SIZE)."""
+    256 MB Infinity Cache when it comes round again). The stream is first
+    given other work first (RMSNorm over 1 GiB, ~0.4 ms, once per 10 timed
+    launches), during which the host queues every timed launch: the events
+    then time kernels back to back, not the host's launch rate (which a
+    profiler slows to ~40 us a launch)."""
     E, F = hp["n_embd"], hp["n_ff"]
     wb = ctx.weight_bytes(synth.Q4_K, E, F)
     copies = max(2, -(-(1100 << 20) // (2 * wb)))
@@ -130,7 +132,13 @@ def glu_roofline(ctx, hp, launches: int = 200):
     out = ctx.alloc(F * 4)
     for i in range(copies):
         ctx.matvec_glu(synth.Q4_K, gates[i], ups[i], E, F, x, out, norm_w=nw, eps=1e-5)
+    busy_n, busy_rows = 4096, 65536
+    bx, by = ctx.alloc(busy_n * busy_rows * 4), ctx.alloc(busy_n * busy_rows * 4)
+    ones = ctx.to_device(np.ones(busy_n, np.float32))
+    bx.zero()
     ctx.sync()
+    for _ in range(max(2, launches // 10)):
+        ctx.rmsnorm(bx, ones, 1e-5, busy_n, busy_rows, by)
     ctx.timer_begin()
     for i in range(launches):
         ctx.matvec_glu(synth.Q4_K, gates[i % copies], ups[i % copies], E, F, x, out, norm_w=nw, eps=1e-5)
@@ -139,7 +147,7 @@ def glu_roofline(ctx, hp, launches: int = 200):
     # Weights, the fp32 input and norm weight, the fp32 output.
     algo = 2 * E // 256 * F * 144 + 2 * 4 * E + 4 * F
     achieved = algo / (avg_us * 1e-6) / 1e9
-    for b in gates + ups:
+    for b in gates + ups + [bx, by]:
         b.free()
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(achieved / HBM_PEAK_GBS, 4), traffic=GLU_TRAFFIC_BYTES,

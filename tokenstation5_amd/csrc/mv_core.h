@@ -608,13 +608,13 @@ __device__ inline uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
-template <class F, int R, int MODE, int NS>
+template <class F, int R, int MODE, int NS, int WAVES = 4>
 struct MvRing {
     static constexpr int NW = MODE == MV_GLU ? 2 : 1;
     static constexpr int PIECES = NW * R * F::NPIECE;           // 1 KB DMAs per step
     static constexpr int PER_STEP = PIECES + (MODE == MV_ADD);  // DMA instructions per step
     static constexpr int SLOT = PIECES * 1024 + (MODE == MV_ADD ? 256 : 0);
-    static constexpr size_t lds_bytes(int n_in) { return align_up(act_bytes(n_in), 1024) + (size_t)4 * NS * SLOT; }
+    static constexpr size_t lds_bytes(int n_in) { return align_up(act_bytes(n_in), 1024) + (size_t)WAVES * NS * SLOT; }
 };
 
 // vmcnt(PER_STEP * newer) for newer = 0 .. NS-1 (wave-uniform).
@@ -629,11 +629,11 @@ __device__ inline void wait_steps(int newer) {
     }
 }
 
-template <class F, int R, int MODE, int NS>
+template <class F, int R, int MODE, int NS, int WAVES = 4>
 __device__ inline void mv_run_dma(const MvArgs &a, uint8_t *lds, float *red) {
     static_assert(MODE != MV_ARGMAX && NS >= 2 && NS <= 5, "ring matvec shape");
-    using RG = MvRing<F, R, MODE, NS>;
-    constexpr int WAVES = 4, NT = WAVES * WAVE, BPI = WAVE / F::LPB, NW = RG::NW;
+    using RG = MvRing<F, R, MODE, NS, WAVES>;
+    constexpr int NT = WAVES * WAVE, BPI = WAVE / F::LPB, NW = RG::NW;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int bsub = lane / F::LPB, sub = lane % F::LPB;
     const int64_t rpg = (int64_t)R * WAVES;

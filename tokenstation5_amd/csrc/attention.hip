@@ -91,17 +91,22 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float *__restrict__ qkv, i
 // file builds with -amdgpu-kernarg-preload-count=16); the rest of AttnArgs
 // (query, RoPE, norms, partials, output) follows in `tail`. flags: 1
 // kv_per_batch, 2 append, 4 rope.
+#ifndef TS5_ATTN_NT
+#define TS5_ATTN_NT 512
+#endif
+constexpr int ATTN_NT = TS5_ATTN_NT;  // threads per work item: 8 waves, two per SIMD
+
 template <int HD, int G>
-__global__ __launch_bounds__(256) void k_attn(const int8_t *k8, const uint16_t *ks, const int8_t *v8,
-                                              const uint16_t *vs, const int32_t *n_keys, int n_ctx, int HKV,
-                                              int flags, int n_split, AttnArgs tail) {
-    __shared__ SliceLds<HD, G> S;
+__global__ __launch_bounds__(ATTN_NT) void k_attn(const int8_t *k8, const uint16_t *ks, const int8_t *v8,
+                                                  const uint16_t *vs, const int32_t *n_keys, int n_ctx, int HKV,
+                                                  int flags, int n_split, AttnArgs tail) {
+    __shared__ SliceLds<HD, G, ATTN_NT> S;
     AttnArgs a = tail;
     a.kv = KvLayer{const_cast<int8_t *>(k8), const_cast<uint16_t *>(ks), const_cast<int8_t *>(v8),
                    const_cast<uint16_t *>(vs)};
     a.n_keys = n_keys, a.n_ctx = n_ctx, a.HKV = HKV;
     a.kv_per_batch = flags & 1, a.append = (flags >> 1) & 1, a.rope = (flags >> 2) & 1;
-    attn_slice<HD, G>(a, blockIdx.x, blockIdx.y, blockIdx.z, n_split, S);
+    attn_slice<HD, G, ATTN_NT>(a, blockIdx.x, blockIdx.y, blockIdx.z, n_split, S);
 }
 
 // K (which 0) or V (1) at positions [pos0, pos0 + n) dequantized to fp32
@@ -136,7 +141,7 @@ static hipError_t attn_launch(int G, dim3 grid, const AttnArgs &a, hipStream_t s
     const int flags = (a.kv_per_batch ? 1 : 0) | (a.append ? 2 : 0) | (a.rope ? 4 : 0);
 #define TS5_ATTN(GG)                                                                                          \
     case GG:                                                                                                  \
-        hipLaunchKernelGGL((k_attn<HD, GG>), grid, dim3(256), 0, s, (const int8_t *)a.kv.k,                   \
+        hipLaunchKernelGGL((k_attn<HD, GG>), grid, dim3(ATTN_NT), 0, s, (const int8_t *)a.kv.k,               \
                            (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs, a.n_keys, \
                            a.n_ctx, a.HKV, flags, (int)grid.x, a);                                           \
         break;

@@ -414,7 +414,7 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
 // ---------------------------------------------------------------------------
 constexpr int ATTN_KT = 256;
 
-template <int HD, int G>
+template <int HD, int G, int NT = 256>
 struct SliceLds {
     float q_s[G][HD];
     __align__(16) float p_s[ATTN_KT][G];  // scores, then probabilities
@@ -422,23 +422,27 @@ struct SliceLds {
     float kv_s[2][HD];                    // the new token's K and V before rounding
     __align__(16) int8_t new8[2][HD];     // ... and after, as int8
     uint16_t new_sc[2][HD / 32];          // ... with their f16 scales
-    __align__(16) float o_s[4][G * HD];   // each wave's p * v sums
+    __align__(16) float o_s[NT / 64][G * HD];  // each wave's p * v sums
     __align__(16) float wts[G][ATTN_MAX_SPLIT];  // the merge's weight per (head, split), 0 past n_split
     int last;
 };
 
-template <int HD, int G>
+template <int HD, int G, int NT>
 struct SliceShape {
-    static constexpr int NT = 256, LPK = 4, NQ = HD / LPK, NPASS = ATTN_KT / 64;
-    static constexpr int DPL = 8, LPV = HD / DPL, KPW = 64 / LPV, KPS = 4 * KPW, NVS = ATTN_KT / KPS;
-    static_assert(NQ % 8 == 0 && LPV <= 64 && 64 % LPV == 0, "attention slice shape");
+    // Scores: LPK lanes a key, KS keys a sweep of the workgroup, NPASS sweeps a
+    // pass. p * v: DPL dims a lane, KPW keys a wave, KPS keys a step, NVS steps.
+    static constexpr int NW = NT / 64, LPK = 4, NQ = HD / LPK, KS = NT / LPK, NPASS = ATTN_KT / KS;
+    static constexpr int DPL = 8, LPV = HD / DPL, KPW = 64 / LPV, KPS = NW * KPW, NVS = ATTN_KT / KPS;
+    static_assert(NQ % 8 == 0 && LPV <= 64 && 64 % LPV == 0 && 64 % KPS == 0 && ATTN_KT % KS == 0,
+                  "attention slice shape");
 };
 
-template <int HD, int G>
-__device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, int n_split, SliceLds<HD, G> &S) {
-    using SH = SliceShape<HD, G>;
-    constexpr int NT = SH::NT, NQ = SH::NQ, NPASS = SH::NPASS, LPV = SH::LPV, KPW = SH::KPW, KPS = SH::KPS,
-                  NVS = SH::NVS;
+template <int HD, int G, int NT>
+__device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, int n_split,
+                                  SliceLds<HD, G, NT> &S) {
+    using SH = SliceShape<HD, G, NT>;
+    constexpr int NW = SH::NW, NQ = SH::NQ, KS = SH::KS, NPASS = SH::NPASS, LPV = SH::LPV, KPW = SH::KPW,
+                  KPS = SH::KPS, NVS = SH::NVS, SMX = ATTN_KT / 64;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kk = tid >> 2, qq = tid & 3;              // scores: key kk of a sweep, quarter qq of the dims
     const int vk = lane / LPV, vc = lane % LPV;         // p * v: key vk of a wave's step, dims 8 vc ..
@@ -458,7 +462,7 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
         uint16_t ksr[NPASS];
 #pragma unroll
         for (int j = 0; j < NPASS; j++) {
-            const int key = min(t0 + 64 * j + kk, kmax);
+            const int key = min(t0 + KS * j + kk, kmax);
             kr[j] = load_krow<NQ>(kb + (int64_t)key * HD + qq * NQ);
             ksr[j] = ksb[(int64_t)key * (HD / 32) + (qq * NQ) / 32];
         }
@@ -479,8 +483,8 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
         // Scores of the pass.
 #pragma unroll
         for (int j = 0; j < NPASS; j++) {
-            if (64 * j >= nt) break;
-            const int idx = 64 * j + kk, key = t0 + idx;
+            if (KS * j >= nt) break;
+            const int idx = KS * j + kk, key = t0 + idx;
             float ks = h2f(ksr[j]);
             if (sp.has_new && key == sp.pq) {
 #pragma unroll
@@ -515,10 +519,10 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
         __syncthreads();
         // Online softmax per head over the pass.
         for (int g = wave; g < G; g += NT / 64) {
-            float v[NPASS];
+            float v[SMX];
             float mt = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < NPASS; i++) {
+            for (int i = 0; i < SMX; i++) {
                 v[i] = 64 * i + lane < nt ? S.p_s[64 * i + lane][g] : -INFINITY;
                 mt = fmaxf(mt, v[i]);
             }
@@ -526,7 +530,7 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
             const float mo = S.m_s[g], mn = fmaxf(mo, mt);
             float ls = 0.f;
 #pragma unroll
-            for (int i = 0; i < NPASS; i++) {
+            for (int i = 0; i < SMX; i++) {
                 const float pe = v[i] == -INFINITY ? 0.f : expf(v[i] - mn);
                 if (64 * i < nt) S.p_s[64 * i + lane][g] = pe;
                 ls += pe;
@@ -593,7 +597,10 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
     float *pb = a.part + (((int64_t)b * n_split + split) * a.H + (int64_t)kvh * G) * rec;
     for (int j = tid; j < G * HD; j += NT) {
         const int g = j / HD, d = j % HD;
-        st_dev(pb + g * rec + d, S.o_s[0][j] + S.o_s[1][j] + S.o_s[2][j] + S.o_s[3][j]);
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) v += S.o_s[w][j];
+        st_dev(pb + g * rec + d, v);
     }
     if (tid < G) {
         st_dev(pb + tid * rec + HD, S.m_s[tid]);

@@ -74,6 +74,48 @@ __global__ __launch_bounds__(256) void k_rmsnorm_reg(const float *__restrict__ x
     }
 }
 
+// The matmul layout (MAct) of x, optionally rms-normalised: token blockIdx.x,
+// 16-runs 256*blockIdx.y .. +255 (one per thread).
+__global__ __launch_bounds__(256) void k_act_quant_m(const float *__restrict__ x, int64_t xstride,
+                                                     const float *__restrict__ w, float eps, int n,
+                                                     uint8_t *__restrict__ act, int64_t act_stride) {
+    __shared__ float red[4];
+    const float *xt = x + (int64_t)blockIdx.x * xstride;
+    uint8_t *m = act + (int64_t)blockIdx.x * act_stride;
+    const float s = act_rms<256>(xt, w, eps, n, red);
+    const int r = 256 * blockIdx.y + threadIdx.x;  // runs 2g, 2g+1 in adjacent lanes, both in or out
+    if (r >= n / 16) return;
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float4 f = *(const float4 *)(xt + 16 * r + 4 * k);
+        v[4 * k] = f.x, v[4 * k + 1] = f.y, v[4 * k + 2] = f.z, v[4 * k + 3] = f.w;
+    }
+    if (w) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float4 g = *(const float4 *)(w + 16 * r + 4 * k);
+            v[4 * k] = v[4 * k] * s * g.x;
+            v[4 * k + 1] = v[4 * k + 1] * s * g.y;
+            v[4 * k + 2] = v[4 * k + 2] * s * g.z;
+            v[4 * k + 3] = v[4 * k + 3] * s * g.w;
+        }
+    }
+    quant_run_m(v, r, m);
+}
+
+size_t gemm_act_bytes(uint32_t t, int64_t n) {
+    return (t == T_Q8_0 || n % 256) ? act_bytes(n) : mact_bytes(n);
+}
+
+hipError_t launch_gemm_act(uint32_t t, const float *x, int64_t xstride, const float *w, float eps, int n, int ntok,
+                           void *act, hipStream_t s) {
+    if (t == T_Q8_0 || n % 256) return launch_act_quant(x, xstride, w, eps, n, ntok, act, s);
+    hipLaunchKernelGGL(k_act_quant_m, dim3(ntok, (n / 16 + 255) / 256), dim3(256), 0, s, x, xstride, w, eps, n,
+                       (uint8_t *)act, (int64_t)mact_bytes(n));
+    return hipGetLastError();
+}
+
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int ntok, float *y, hipStream_t s) {
     if (n <= 256 * 16) hipLaunchKernelGGL(k_rmsnorm_reg<16>, dim3(ntok), dim3(256), 0, s, x, w, eps, n, y);
     else hipLaunchKernelGGL(k_rmsnorm, dim3(ntok), dim3(256), 0, s, x, w, eps, n, y);

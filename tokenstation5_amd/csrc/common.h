@@ -84,6 +84,18 @@ struct CAct {
 __host__ __device__ inline size_t act_bytes(int64_t n) {
     return 2 * align_up((size_t)n, 256) + 2 * align_up((size_t)n / 32 * 4, 256) + align_up((size_t)n / 16 * 4, 256);
 }
+// The matrix-core matmuls' activation for Q4_K / Q6_K rows (n a multiple of
+// 256): the same x16 = 256 hi + lo values, scales and sums as Act, ordered per
+// 256-value block so that a lane feeding k-group kq of the MFMA finds its 8
+// bytes of all 8 chunks side by side:
+//   hi[4][8][8]   k-group kq, chunk c, the chunk's bytes 8 kq .. 8 kq + 7
+//   lo[4][8][8]
+//   scale[8], sum[8] (f32 per chunk), isum[16] (i32 per 16 values)
+// 640 bytes a block.
+constexpr int MACT_BLOCK = 640;
+constexpr int MACT_LO = 256, MACT_SCALE = 512, MACT_SUM = 544, MACT_ISUM = 576;
+__host__ __device__ inline size_t mact_bytes(int64_t n) { return align_up((size_t)(n / 256) * MACT_BLOCK, 256); }
+
 __host__ __device__ inline Act act_view(void *base, int64_t n) {
     uint8_t *p = (uint8_t *)base;
     Act a;

@@ -40,7 +40,7 @@ struct GemmArgs {
     const uint8_t *w, *w2;    // block bodies (w2: GLU's up projection)
     const uint16_t *s, *s2;   // split layouts' f16 block scales
     int nrows, nb, n_in, M, ks;
-    const uint8_t *act;       // M activation records of act_bytes(n_in)
+    const uint8_t *act;       // M activation records of gemm_act_bytes(t, n_in)
     int64_t act_stride;
     float *out;               // ks == 1: y [M][ldy]; ks > 1: partials [ks][2][M][nrows]
     const float *y_in;        // MODE_ADD: residual [M][ldy] (may be out)
@@ -62,20 +62,34 @@ struct GemmLds {
 
 constexpr int F_Q4K = 0, F_Q6K = 1, F_Q80 = 2;
 
-// Activation fragments of token group tg for 32-value chunk c of the row
-// (sub-block index in Act units), and the token's scale, sum.
+// Activation fragments of token tok for 32-value chunk s of block b, k-group
+// kq, and the chunk's scale and sum: Q4_K / Q6_K rows read the matmul layout
+// (MACT_*), Q8_0 rows Act (its block is one chunk, s = 0).
 struct AFrag {
     uint64_t hi, lo;
     float xs, xsum;
 };
-__device__ inline AFrag act_frag(const GemmArgs &a, int tok, int chunk, int kq) {
+template <int FMT>
+__device__ inline const uint8_t *mact_blk(const GemmArgs &a, int tok, int b) {
+    return a.act + (int64_t)tok * a.act_stride + (int64_t)b * MACT_BLOCK;
+}
+template <int FMT>
+__device__ inline AFrag act_frag(const GemmArgs &a, int tok, int b, int s, int kq) {
     AFrag f{0, 0, 0.f, 0.f};
     if (tok < a.M) {
-        const CAct x = cact_view(a.act + (int64_t)tok * a.act_stride, a.n_in);
-        f.hi = ld8(x.hi + 32 * chunk + 8 * kq);
-        f.lo = ld8(x.lo + 32 * chunk + 8 * kq);
-        f.xs = x.scale[chunk];
-        f.xsum = x.sum[chunk];
+        if constexpr (FMT == F_Q80) {
+            const CAct x = cact_view(a.act + (int64_t)tok * a.act_stride, a.n_in);
+            f.hi = ld8(x.hi + 32 * b + 8 * kq);
+            f.lo = ld8(x.lo + 32 * b + 8 * kq);
+            f.xs = x.scale[b];
+            f.xsum = x.sum[b];
+        } else {
+            const uint8_t *blk = mact_blk<FMT>(a, tok, b);
+            f.hi = ld8(blk + 64 * kq + 8 * s);
+            f.lo = ld8(blk + MACT_LO + 64 * kq + 8 * s);
+            f.xs = ((const float *)(blk + MACT_SCALE))[s];
+            f.xsum = ((const float *)(blk + MACT_SUM))[s];
+        }
     }
     return f;
 }
@@ -122,7 +136,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
             for (int s = 0; s < 8; s++) {
                 AFrag x[TN];
 #pragma unroll
-                for (int g = 0; g < TN; g++) x[g] = act_frag(a, t0 + 16 * g + rl, b * 8 + s, kq);
+                for (int g = 0; g < TN; g++) x[g] = act_frag<FMT>(a, t0 + 16 * g + rl, b, s, kq);
 #pragma unroll
                 for (int m = 0; m < NW; m++) {
                     const uint64_t qa = (s & 1) ? (q[m][s >> 1] >> 4) & 0x0F0F0F0F0F0F0F0Full
@@ -138,6 +152,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
                             acc[m][g][i] += dsc[i] * x[g].xs * (float)(ch[i] * 256 + cl[i]) - dm[i] * x[g].xsum;
                     }
                 }
+                if constexpr (TN > 1) __builtin_amdgcn_sched_barrier(0);  // one chunk's loads at a time
             }
         } else if constexpr (FMT == F_Q80) {
             uint64_t q[NW];
@@ -150,7 +165,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
             __builtin_amdgcn_wave_barrier();
             AFrag x[TN];
 #pragma unroll
-            for (int g = 0; g < TN; g++) x[g] = act_frag(a, t0 + 16 * g + rl, b, kq);
+            for (int g = 0; g < TN; g++) x[g] = act_frag<FMT>(a, t0 + 16 * g + rl, b, 0, kq);
 #pragma unroll
             for (int m = 0; m < NW; m++) {
                 const float4 sA = *(const float4 *)&S.scl[m][0][4 * kq];
@@ -190,12 +205,12 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 #pragma unroll
                 for (int g = 0; g < TN; g++) {
                     const int tok = t0 + 16 * g + rl;
-                    x[g] = act_frag(a, tok, b * 8 + c32, kq);
+                    x[g] = act_frag<FMT>(a, tok, b, c32, kq);
                     is0[g] = is1[g] = 0;
                     if (tok < a.M) {
-                        const CAct xa = cact_view(a.act + (int64_t)tok * a.act_stride, a.n_in);
-                        is0[g] = xa.isum[b * 16 + 2 * c32];
-                        is1[g] = xa.isum[b * 16 + 2 * c32 + 1];
+                        const int *isum = (const int *)(mact_blk<FMT>(a, tok, b) + MACT_ISUM);
+                        is0[g] = isum[2 * c32];
+                        is1[g] = isum[2 * c32 + 1];
                     }
                 }
 #pragma unroll
@@ -220,6 +235,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
                                                        e1[i] * (float)(h1[i] * 256 + l1[i] - 32 * is1[g]));
                     }
                 }
+                if constexpr (TN > 1) __builtin_amdgcn_sched_barrier(0);  // one chunk's loads at a time
             }
         }
     }
@@ -318,18 +334,35 @@ struct ABlk {
 template <int FMT>
 __device__ inline ABlk<FMT> load_ablk(const GemmArgs &a, int tok, int kq, int b) {
     ABlk<FMT> x;
-    const CAct xa = cact_view(a.act + (int64_t)min(tok, a.M - 1) * a.act_stride, a.n_in);
+    tok = min(tok, a.M - 1);
+    if constexpr (FMT == F_Q80) {
+        const CAct xa = cact_view(a.act + (int64_t)tok * a.act_stride, a.n_in);
+        x.hi[0] = ld8(xa.hi + 32 * b + 8 * kq);
+        x.lo[0] = ld8(xa.lo + 32 * b + 8 * kq);
+        x.xs[0] = xa.scale[b];
+        x.xsum[0] = xa.sum[b];
+    } else {  // the lane's 8 bytes of every chunk, side by side: 16-byte loads
+        const uint8_t *blk = mact_blk<FMT>(a, tok, b);
 #pragma unroll
-    for (int c = 0; c < ABlk<FMT>::C; c++) {
-        const int ch = b * ABlk<FMT>::C + c;
-        x.hi[c] = ld8(xa.hi + 32 * ch + 8 * kq);
-        x.lo[c] = ld8(xa.lo + 32 * ch + 8 * kq);
-        x.xs[c] = xa.scale[ch];
-        x.xsum[c] = xa.sum[ch];
-    }
-    if constexpr (FMT == F_Q6K) {
+        for (int c = 0; c < 8; c += 2) {
+            const uint4 h = ld16(blk + 64 * kq + 8 * c), l = ld16(blk + MACT_LO + 64 * kq + 8 * c);
+            x.hi[c] = ((uint64_t)h.y << 32) | h.x, x.hi[c + 1] = ((uint64_t)h.w << 32) | h.z;
+            x.lo[c] = ((uint64_t)l.y << 32) | l.x, x.lo[c + 1] = ((uint64_t)l.w << 32) | l.z;
+        }
 #pragma unroll
-        for (int g = 0; g < 16; g++) x.is[g] = xa.isum[b * 16 + g];
+        for (int c = 0; c < 8; c += 4) {
+            const float4 sc = *(const float4 *)(blk + MACT_SCALE + 4 * c);
+            const float4 su = *(const float4 *)(blk + MACT_SUM + 4 * c);
+            x.xs[c] = sc.x, x.xs[c + 1] = sc.y, x.xs[c + 2] = sc.z, x.xs[c + 3] = sc.w;
+            x.xsum[c] = su.x, x.xsum[c + 1] = su.y, x.xsum[c + 2] = su.z, x.xsum[c + 3] = su.w;
+        }
+        if constexpr (FMT == F_Q6K) {
+#pragma unroll
+            for (int g = 0; g < 16; g += 4) {
+                const int4 v = *(const int4 *)(blk + MACT_ISUM + 4 * g);
+                x.is[g] = v.x, x.is[g + 1] = v.y, x.is[g + 2] = v.z, x.is[g + 3] = v.w;
+            }
+        }
     }
     return x;
 }
@@ -494,7 +527,10 @@ __global__ void k_gemm_reduce(const float *__restrict__ part, int ks, int M, int
 template <int FMT, int MODE>
 static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
     if (a.M <= 16) hipLaunchKernelGGL((k_gemm_small<FMT, MODE>), dim3((a.nrows + 15) / 16), dim3(256), 0, s, a);
-    else if (tn == 4) hipLaunchKernelGGL((k_gemm<FMT, MODE, 4>), grid, dim3(256), 0, s, a);
+    else if constexpr (FMT != F_Q6K) {
+        if (tn == 4) hipLaunchKernelGGL((k_gemm<FMT, MODE, 4>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm<FMT, MODE, 1>), grid, dim3(256), 0, s, a);
+    }
     else hipLaunchKernelGGL((k_gemm<FMT, MODE, 1>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
@@ -509,6 +545,10 @@ static hipError_t gemm_fmt(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) 
     return hipErrorInvalidValue;
 }
 
+// Token groups of 16 per wave: 4 for batches past 16 tokens (Q6_K rows keep
+// 1: its 4-group kernel does not fit the register file).
+static int gemm_tn(uint32_t t, int M) { return M > 16 && t != T_Q6_K ? 4 : 1; }
+
 static int g_gemm_cu = 256;
 void set_gemm_cu_count(int n) { g_gemm_cu = n > 0 ? n : 256; }
 
@@ -521,7 +561,7 @@ static int gemm_splits(int64_t rows, int M, int nb, int tn) {
     return std::min(ks, nb);
 }
 
-size_t gemm_scratch_bytes(int64_t rows, int M, int nb) {
+size_t gemm_scratch_bytes(int64_t rows, int M, int nb) {  // 4 groups split the most: the bound for every type
     const int tn = M > 16 ? 4 : 1;
     const int ks = gemm_splits(rows, M, nb, tn);
     return ks > 1 ? (size_t)ks * 2 * M * rows * 4 : 0;
@@ -532,13 +572,13 @@ hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, i
     GemmArgs a{};
     a.t = t, a.w = (const uint8_t *)w, a.w2 = (const uint8_t *)w2, a.nrows = (int)ne1;
     a.nb = (int)(ne0 / block_values(t)), a.n_in = (int)ne0, a.M = M, a.act = (const uint8_t *)act;
-    a.act_stride = (int64_t)act_bytes(ne0), a.y_in = y_in, a.ldy = ldy;
+    a.act_stride = (int64_t)gemm_act_bytes(t, ne0), a.y_in = y_in, a.ldy = ldy;
     if (t == T_Q6_K || t == T_Q8_0) {
         const int64_t nblocks = (int64_t)a.nb * ne1;
         a.s = (const uint16_t *)(a.w + split_scale_offset(t, nblocks));
         a.s2 = w2 ? (const uint16_t *)(a.w2 + split_scale_offset(t, nblocks)) : nullptr;
     }
-    const int tn = M > 16 ? 4 : 1;
+    const int tn = gemm_tn(t, M);
     a.ks = gemm_splits(ne1, M, a.nb, tn);
     a.out = a.ks > 1 ? (float *)scratch : y;
     const dim3 grid((unsigned)((ne1 + 63) / 64), (unsigned)((M + 16 * tn - 1) / (16 * tn)), (unsigned)a.ks);

@@ -35,6 +35,11 @@ hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, i
 
 // act.hip
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int ntok, float *y, hipStream_t s);
+// The activation records launch_gemm reads for type t (the matmul layout for
+// Q4_K / Q6_K rows, Act for Q8_0), gemm_act_bytes(t, n) per token.
+size_t gemm_act_bytes(uint32_t t, int64_t n);
+hipError_t launch_gemm_act(uint32_t t, const float *x, int64_t xstride, const float *w, float eps, int n, int ntok,
+                           void *act, hipStream_t s);
 hipError_t launch_act_quant(const float *x, int64_t xstride, const float *w, float eps, int n, int ntok, void *act,
                             hipStream_t s);
 

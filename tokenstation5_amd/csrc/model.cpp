@@ -611,7 +611,8 @@ int ensure_batch(ts5hip_model *m) {
     int rc = 0;
     if ((rc = alloc_t(m, CHUNK * E, &m->bx)) || (rc = alloc_t(m, CHUNK * QR, &m->bqkv)) ||
         (rc = alloc_t(m, CHUNK * AH, &m->bq)) || (rc = alloc_t(m, CHUNK * AH, &m->batt)) ||
-        (rc = alloc_t(m, CHUNK * F, &m->bffn)) || (rc = alloc(m, CHUNK * act_bytes(wide), &m->bact)) ||
+        (rc = alloc_t(m, CHUNK * F, &m->bffn)) ||
+        (rc = alloc(m, CHUNK * std::max(act_bytes(wide), mact_bytes(wide)), &m->bact)) ||
         (rc = alloc(m, std::max<size_t>(gemm, 256), &m->bgemm)) || (rc = alloc(m, part, (void **)&m->bpart)) ||
         (rc = alloc_t(m, (size_t)CHUNK * hp.n_head_kv, &m->bcounters)))
         return rc;
@@ -632,7 +633,7 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
     const float eps = hp.rms_eps;
     auto proj = [&](uint32_t t, const void *w, const void *w2, int64_t ne0, int64_t ne1, const float *x,
                     int64_t xstride, const float *norm, int ntok, int mode, float *y, int64_t ldy) -> int {
-        TS5_HIP(ctx, launch_act_quant(x, xstride, norm, eps, (int)ne0, ntok, m->bact, s));
+        TS5_HIP(ctx, launch_gemm_act(t, x, xstride, norm, eps, (int)ne0, ntok, m->bact, s));
         TS5_HIP(ctx, launch_gemm(t, w, w2, ne0, ne1, m->bact, ntok, mode, y, y, ldy, m->bgemm, s));
         return TS5HIP_OK;
     };

@@ -297,6 +297,58 @@ __device__ inline float act_rms(const float *__restrict__ x, const float *__rest
 // 16-run r of Act a (half r & 1 of sub-block r / 2) from its 16 values. Two
 // threads per 32-value sub-block, in adjacent lanes, exchange their max and
 // sum once (both call this together).
+struct Run16 {
+    uint32_t hw[4], lw[4];  // hi and lo bytes of the 16 values
+    int isum;
+    float scale, sum;       // of the 32-value chunk (both threads of the pair)
+};
+__device__ inline Run16 quant16(const float (&v)[16]) {
+    Run16 q;
+    float amax = 0.f, sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        sum += v[i];
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
+    sum += __shfl_xor(sum, 1, WAVE);
+    const float inv = amax > 0.f ? 16383.0f / amax : 0.f;
+    int is = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        uint32_t h = 0, l = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int x16 = max(-16383, min(16383, (int)rintf(v[4 * k + e] * inv)));
+            const int lo = (int)(int8_t)(x16 & 255);
+            const int hi = (x16 - lo) >> 8;
+            h |= (uint32_t)(hi & 255) << (8 * e);
+            l |= (uint32_t)(lo & 255) << (8 * e);
+            is += x16;
+        }
+        q.hw[k] = h, q.lw[k] = l;
+    }
+    q.isum = is, q.scale = amax / 16383.0f, q.sum = sum;
+    return q;
+}
+// Run r into the matmul layout at `m` (the token's MAct): block r / 16, chunk
+// (r % 16) / 2, bytes 16 (r & 1) .. +15 of the chunk, i.e. k-groups
+// 2 (r & 1) and 2 (r & 1) + 1.
+__device__ inline void quant_run_m(const float (&v)[16], int r, uint8_t *m) {
+    const Run16 q = quant16(v);
+    uint8_t *blk = m + (size_t)(r / 16) * MACT_BLOCK;
+    const int c = (r % 16) / 2, kq = 2 * (r & 1);
+    *(uint2 *)(blk + kq * 64 + 8 * c) = make_uint2(q.hw[0], q.hw[1]);
+    *(uint2 *)(blk + (kq + 1) * 64 + 8 * c) = make_uint2(q.hw[2], q.hw[3]);
+    *(uint2 *)(blk + MACT_LO + kq * 64 + 8 * c) = make_uint2(q.lw[0], q.lw[1]);
+    *(uint2 *)(blk + MACT_LO + (kq + 1) * 64 + 8 * c) = make_uint2(q.lw[2], q.lw[3]);
+    ((int *)(blk + MACT_ISUM))[r % 16] = q.isum;
+    if ((r & 1) == 0) {
+        ((float *)(blk + MACT_SCALE))[c] = q.scale;
+        ((float *)(blk + MACT_SUM))[c] = q.sum;
+    }
+}
+
 __device__ inline void quant_run(const float (&v)[16], int r, const Act &a) {
     float amax = 0.f, sum = 0.f;
 #pragma unroll

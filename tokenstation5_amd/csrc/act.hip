@@ -104,15 +104,80 @@ __global__ __launch_bounds__(256) void k_act_quant_m(const float *__restrict__ x
     quant_run_m(v, r, m);
 }
 
-size_t gemm_act_bytes(uint32_t t, int64_t n) {
-    return (t == T_Q8_0 || n % 256) ? act_bytes(n) : mact_bytes(n);
+// The prompt matmuls' fp16 pair form (hact_*) of x, optionally
+// rms-normalised: token blockIdx.x; the largest |value| sets the token's power
+// of two, then each thread writes 32-value chunks (hi, lo and their sum).
+__global__ __launch_bounds__(256) void k_act_half(const float *__restrict__ x, int64_t xstride,
+                                                  const float *__restrict__ w, float eps, int n,
+                                                  uint8_t *__restrict__ act, int64_t act_stride) {
+    __shared__ float red[4], redm[4];
+    const float *xt = x + (int64_t)blockIdx.x * xstride;
+    uint8_t *o = act + (int64_t)blockIdx.x * act_stride;
+    const float s = act_rms<256>(xt, w, eps, n, red);
+    auto value4 = [&](int i) {
+        float4 v = *(const float4 *)(xt + i);
+        if (w) {
+            const float4 g = *(const float4 *)(w + i);
+            v.x = v.x * s * g.x, v.y = v.y * s * g.y, v.z = v.z * s * g.z, v.w = v.w * s * g.w;
+        }
+        return v;
+    };
+    float amax = 0.f;
+    for (int i = 4 * threadIdx.x; i < n; i += 1024) {
+        const float4 v = value4(i);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    amax = wave_max(amax);
+    if ((threadIdx.x & 63) == 0) redm[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
+    const int e = amax > 0.f ? max(ilogbf(amax) - 13, -100) : 0;  // amax 2^-e in [2^13, 2^14)
+    const float scale = ldexpf(1.0f, -e);
+    if (threadIdx.x == 0) *(float *)(o + hact_unscale(n)) = ldexpf(1.0f, e);
+    for (int c = threadIdx.x; c < n / 32; c += 256) {
+        uint32_t hw[16], lw[16];
+        float sum = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 v = value4(32 * c + 4 * k);
+            const float f[4] = {v.x * scale, v.y * scale, v.z * scale, v.w * scale};
+#pragma unroll
+            for (int j = 0; j < 4; j += 2) {
+                const _Float16 h0 = (_Float16)f[j], h1 = (_Float16)f[j + 1];
+                const _Float16 l0 = (_Float16)(f[j] - (float)h0), l1 = (_Float16)(f[j + 1] - (float)h1);
+                hw[2 * k + j / 2] = __builtin_bit_cast(uint16_t, h0) | (uint32_t)__builtin_bit_cast(uint16_t, h1) << 16;
+                lw[2 * k + j / 2] = __builtin_bit_cast(uint16_t, l0) | (uint32_t)__builtin_bit_cast(uint16_t, l1) << 16;
+                sum += f[j] + f[j + 1];
+            }
+        }
+        uint8_t *blk = o + (size_t)(c / 8) * 1024 + (c % 8) * 64;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            ((uint4 *)blk)[k] = make_uint4(hw[4 * k], hw[4 * k + 1], hw[4 * k + 2], hw[4 * k + 3]);
+            ((uint4 *)(blk + 512))[k] = make_uint4(lw[4 * k], lw[4 * k + 1], lw[4 * k + 2], lw[4 * k + 3]);
+        }
+        ((float *)(o + hact_x(n)))[c] = sum;
+    }
+}
+
+size_t gemm_act_bytes(uint32_t t, int64_t n, int ntok) {
+    switch (gemm_act_form(t, n, ntok)) {
+    case GA_HACT: return hact_bytes(n);
+    case GA_MACT: return mact_bytes(n);
+    default: return act_bytes(n);
+    }
 }
 
 hipError_t launch_gemm_act(uint32_t t, const float *x, int64_t xstride, const float *w, float eps, int n, int ntok,
                            void *act, hipStream_t s) {
-    if (t == T_Q8_0 || n % 256) return launch_act_quant(x, xstride, w, eps, n, ntok, act, s);
-    hipLaunchKernelGGL(k_act_quant_m, dim3(ntok, (n / 16 + 255) / 256), dim3(256), 0, s, x, xstride, w, eps, n,
-                       (uint8_t *)act, (int64_t)mact_bytes(n));
+    const int form = gemm_act_form(t, n, ntok);
+    if (form == GA_ACT) return launch_act_quant(x, xstride, w, eps, n, ntok, act, s);
+    if (form == GA_HACT)
+        hipLaunchKernelGGL(k_act_half, dim3(ntok), dim3(256), 0, s, x, xstride, w, eps, n, (uint8_t *)act,
+                           (int64_t)hact_bytes(n));
+    else
+        hipLaunchKernelGGL(k_act_quant_m, dim3(ntok, (n / 16 + 255) / 256), dim3(256), 0, s, x, xstride, w, eps, n,
+                           (uint8_t *)act, (int64_t)mact_bytes(n));
     return hipGetLastError();
 }
 

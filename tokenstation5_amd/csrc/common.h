@@ -95,6 +95,15 @@ __host__ __device__ inline size_t act_bytes(int64_t n) {
 constexpr int MACT_BLOCK = 640;
 constexpr int MACT_LO = 256, MACT_SCALE = 512, MACT_SUM = 544, MACT_ISUM = 576;
 __host__ __device__ inline size_t mact_bytes(int64_t n) { return align_up((size_t)(n / 256) * MACT_BLOCK, 256); }
+// The prompt matmuls' activation (Q4_K rows, batches past 16 tokens; n a
+// multiple of 256): each token's values scaled by a power of two, 2^-e, that
+// puts the largest in [2^13, 2^14), then split into two fp16 planes,
+// x 2^-e = hi + lo to about 22 bits:
+//   per 256-value block: hi[256] f16, lo[256] f16     (1 KB)
+//   then X[n / 32] f32, the 32-value chunk sums of x 2^-e, then 2^e (f32).
+__host__ __device__ inline size_t hact_x(int64_t n) { return (size_t)(n / 256) * 1024; }
+__host__ __device__ inline size_t hact_unscale(int64_t n) { return hact_x(n) + (size_t)(n / 32) * 4; }
+__host__ __device__ inline size_t hact_bytes(int64_t n) { return align_up(hact_unscale(n) + 4, 256); }
 
 __host__ __device__ inline Act act_view(void *base, int64_t n) {
     uint8_t *p = (uint8_t *)base;
@@ -299,6 +308,26 @@ __device__ inline float unpack_value(uint32_t t, const uint8_t *base, int64_t nb
     }
     }
     return 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// LDS DMA (global_load_lds_*): lane l's 16 (4) bytes from g land at LDS
+// address lds_base + 16 l (4 l). The compiler does not see these loads:
+// completion is waited for explicitly with wait_vm_n (vmcnt counts them in
+// issue order with every other vector memory load).
+// ---------------------------------------------------------------------------
+__device__ inline void dma16(const void *g, uint32_t lds_base) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_base) : "memory");
+}
+__device__ inline void dma4(const void *g, uint32_t lds_base) {
+    asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_base) : "memory");
+}
+template <int N>
+__device__ inline void wait_vm_n() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ inline uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
 #endif  // __HIPCC__

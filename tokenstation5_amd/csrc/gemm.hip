@@ -561,9 +561,14 @@ static int gemm_splits(int64_t rows, int M, int nb, int tn) {
     return std::min(ks, nb);
 }
 
-size_t gemm_scratch_bytes(int64_t rows, int M, int nb) {  // 4 groups split the most: the bound for every type
-    const int tn = M > 16 ? 4 : 1;
-    const int ks = gemm_splits(rows, M, nb, tn);
+int gemm_act_form(uint32_t t, int64_t n, int ntok) {
+    if (n % 256) return GA_ACT;
+    if (t == T_Q4_K) return ntok > 16 ? GA_HACT : GA_MACT;
+    return t == T_Q6_K ? GA_MACT : GA_ACT;
+}
+
+size_t gemm_scratch_bytes(int64_t rows, int M, int nb) {  // the bound for every type
+    const int ks = std::max(gemm_splits(rows, M, nb, M > 16 ? 4 : 1), M > 16 ? wide_splits(rows, M, nb, g_gemm_cu) : 1);
     return ks > 1 ? (size_t)ks * 2 * M * rows * 4 : 0;
 }
 
@@ -572,7 +577,16 @@ hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, i
     GemmArgs a{};
     a.t = t, a.w = (const uint8_t *)w, a.w2 = (const uint8_t *)w2, a.nrows = (int)ne1;
     a.nb = (int)(ne0 / block_values(t)), a.n_in = (int)ne0, a.M = M, a.act = (const uint8_t *)act;
-    a.act_stride = (int64_t)gemm_act_bytes(t, ne0), a.y_in = y_in, a.ldy = ldy;
+    if (gemm_act_form(t, ne0, M) == GA_HACT) {
+        const int ks = wide_splits(ne1, M, (int)(ne0 / 256), g_gemm_cu);
+        hipError_t e = launch_gemm_wide(w, w2, ne0, ne1, act, M, mode, y, y_in, ldy, scratch, ks, s);
+        if (e != hipSuccess || ks == 1) return e;
+        const int64_t n = (int64_t)M * ne1;
+        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)std::min<int64_t>(4096, (n + 255) / 256)), dim3(256), 0, s,
+                           (const float *)scratch, ks, M, (int)ne1, mode, y, y_in, ldy);
+        return hipGetLastError();
+    }
+    a.act_stride = (int64_t)gemm_act_bytes(t, ne0, M), a.y_in = y_in, a.ldy = ldy;
     if (t == T_Q6_K || t == T_Q8_0) {
         const int64_t nblocks = (int64_t)a.nb * ne1;
         a.s = (const uint16_t *)(a.w + split_scale_offset(t, nblocks));

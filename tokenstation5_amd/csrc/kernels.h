@@ -29,15 +29,22 @@ hipError_t launch_synth(uint32_t t, int64_t ne0, int64_t nrows, uint64_t seed, i
 // 2 GLU (w2 = up: y = silu(W x) * (W2 x)); y [M][ldy]; scratch:
 // gemm_scratch_bytes(ne1, M, blocks per row) bytes.
 void set_gemm_cu_count(int n);
+// gemm_wide.hip: the Q4_K prompt matmul on hact_* records (launch_gemm picks it).
+int wide_splits(int64_t rows, int M, int nb, int cus);
+hipError_t launch_gemm_wide(const void *w, const void *w2, int64_t ne0, int64_t ne1, const void *act, int M, int mode,
+                            float *y, const float *y_in, int64_t ldy, void *scratch, int ks, hipStream_t s);
 size_t gemm_scratch_bytes(int64_t rows, int M, int nb);
 hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, int64_t ne1, const void *act, int M,
                        int mode, float *y, const float *y_in, int64_t ldy, void *scratch, hipStream_t s);
 
 // act.hip
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int ntok, float *y, hipStream_t s);
-// The activation records launch_gemm reads for type t (the matmul layout for
-// Q4_K / Q6_K rows, Act for Q8_0), gemm_act_bytes(t, n) per token.
-size_t gemm_act_bytes(uint32_t t, int64_t n);
+// The activation records launch_gemm reads for type t and ntok tokens
+// (gemm_act_form: Act, the matmul layout mact_* or the fp16 pair form hact_*),
+// gemm_act_bytes(t, n, ntok) per token.
+enum { GA_ACT = 0, GA_MACT = 1, GA_HACT = 2 };
+int gemm_act_form(uint32_t t, int64_t n, int ntok);
+size_t gemm_act_bytes(uint32_t t, int64_t n, int ntok);
 hipError_t launch_gemm_act(uint32_t t, const float *x, int64_t xstride, const float *w, float eps, int n, int ntok,
                            void *act, hipStream_t s);
 hipError_t launch_act_quant(const float *x, int64_t xstride, const float *w, float eps, int n, int ntok, void *act,

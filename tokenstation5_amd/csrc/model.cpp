@@ -612,7 +612,7 @@ int ensure_batch(ts5hip_model *m) {
     if ((rc = alloc_t(m, CHUNK * E, &m->bx)) || (rc = alloc_t(m, CHUNK * QR, &m->bqkv)) ||
         (rc = alloc_t(m, CHUNK * AH, &m->bq)) || (rc = alloc_t(m, CHUNK * AH, &m->batt)) ||
         (rc = alloc_t(m, CHUNK * F, &m->bffn)) ||
-        (rc = alloc(m, CHUNK * std::max(act_bytes(wide), mact_bytes(wide)), &m->bact)) ||
+        (rc = alloc(m, CHUNK * std::max({act_bytes(wide), mact_bytes(wide), hact_bytes(wide)}), &m->bact)) ||
         (rc = alloc(m, std::max<size_t>(gemm, 256), &m->bgemm)) || (rc = alloc(m, part, (void **)&m->bpart)) ||
         (rc = alloc_t(m, (size_t)CHUNK * hp.n_head_kv, &m->bcounters)))
         return rc;

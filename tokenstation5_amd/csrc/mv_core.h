@@ -646,19 +646,7 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
 // lanes < R), so the epilogue does not wait on a load of its own.
 // One workgroup per CU (the ring is most of the LDS); 4 waves.
 // ---------------------------------------------------------------------------
-__device__ inline void dma16(const void *g, uint32_t lds_base) {
-    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_base) : "memory");
-}
-__device__ inline void dma4(const void *g, uint32_t lds_base) {
-    asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_base) : "memory");
-}
-template <int N>
-__device__ inline void wait_vm_n() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-__device__ inline uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
+// (dma16, dma4, wait_vm_n, lds_addr: common.h)
 
 template <class F, int R, int MODE, int NS, int WAVES = 4>
 struct MvRing {

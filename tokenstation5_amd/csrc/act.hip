@@ -156,7 +156,11 @@ __global__ __launch_bounds__(256) void k_act_half(const float *__restrict__ x, i
             ((uint4 *)blk)[k] = make_uint4(hw[4 * k], hw[4 * k + 1], hw[4 * k + 2], hw[4 * k + 3]);
             ((uint4 *)(blk + 512))[k] = make_uint4(lw[4 * k], lw[4 * k + 1], lw[4 * k + 2], lw[4 * k + 3]);
         }
-        ((float *)(o + hact_x(n)))[c] = sum;
+        const float xs = sum * (1.0f / 32);  // exact; keeps the sums in fp16 range
+        const _Float16 xh = (_Float16)xs, xl = (_Float16)(xs - (float)xh);
+        uint16_t *xq = (uint16_t *)(o + hact_x(n)) + 4 * (c / 2) + (c & 1);  // [quarter][hi pair, lo pair]
+        xq[0] = __builtin_bit_cast(uint16_t, xh);
+        xq[2] = __builtin_bit_cast(uint16_t, xl);
     }
 }
 

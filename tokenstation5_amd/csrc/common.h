@@ -100,7 +100,9 @@ __host__ __device__ inline size_t mact_bytes(int64_t n) { return align_up((size_
 // puts the largest in [2^13, 2^14), then split into two fp16 planes,
 // x 2^-e = hi + lo to about 22 bits:
 //   per 256-value block: hi[256] f16, lo[256] f16     (1 KB)
-//   then X[n / 32] f32, the 32-value chunk sums of x 2^-e, then 2^e (f32).
+//   then per 64-value quarter of a block, the sums X of its two 32-value
+//   chunks (of x 2^-e, divided by 32) as fp16 hi + lo: (hi_0, hi_1) (lo_0, lo_1)
+//   (8 bytes), then 2^e (f32).
 __host__ __device__ inline size_t hact_x(int64_t n) { return (size_t)(n / 256) * 1024; }
 __host__ __device__ inline size_t hact_unscale(int64_t n) { return hact_x(n) + (size_t)(n / 32) * 4; }
 __host__ __device__ inline size_t hact_bytes(int64_t n) { return align_up(hact_unscale(n) + 4, 256); }

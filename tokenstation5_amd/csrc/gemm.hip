@@ -568,7 +568,7 @@ int gemm_act_form(uint32_t t, int64_t n, int ntok) {
 }
 
 size_t gemm_scratch_bytes(int64_t rows, int M, int nb) {  // the bound for every type
-    const int ks = std::max(gemm_splits(rows, M, nb, M > 16 ? 4 : 1), M > 16 ? wide_splits(rows, M, nb, g_gemm_cu) : 1);
+    const int ks = std::max(gemm_splits(rows, M, nb, M > 16 ? 4 : 1), M > 16 ? wide_splits(rows, M, nb, g_gemm_cu, G_ADD) : 1);
     return ks > 1 ? (size_t)ks * 2 * M * rows * 4 : 0;
 }
 
@@ -578,7 +578,7 @@ hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, i
     a.t = t, a.w = (const uint8_t *)w, a.w2 = (const uint8_t *)w2, a.nrows = (int)ne1;
     a.nb = (int)(ne0 / block_values(t)), a.n_in = (int)ne0, a.M = M, a.act = (const uint8_t *)act;
     if (gemm_act_form(t, ne0, M) == GA_HACT) {
-        const int ks = wide_splits(ne1, M, (int)(ne0 / 256), g_gemm_cu);
+        const int ks = wide_splits(ne1, M, (int)(ne0 / 256), g_gemm_cu, mode);
         hipError_t e = launch_gemm_wide(w, w2, ne0, ne1, act, M, mode, y, y_in, ldy, scratch, ks, s);
         if (e != hipSuccess || ks == 1) return e;
         const int64_t n = (int64_t)M * ne1;

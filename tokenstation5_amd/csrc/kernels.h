@@ -30,7 +30,7 @@ hipError_t launch_synth(uint32_t t, int64_t ne0, int64_t nrows, uint64_t seed, i
 // gemm_scratch_bytes(ne1, M, blocks per row) bytes.
 void set_gemm_cu_count(int n);
 // gemm_wide.hip: the Q4_K prompt matmul on hact_* records (launch_gemm picks it).
-int wide_splits(int64_t rows, int M, int nb, int cus);
+int wide_splits(int64_t rows, int M, int nb, int cus, int mode);
 hipError_t launch_gemm_wide(const void *w, const void *w2, int64_t ne0, int64_t ne1, const void *act, int M, int mode,
                             float *y, const float *y_in, int64_t ldy, void *scratch, int ks, hipStream_t s);
 size_t gemm_scratch_bytes(int64_t rows, int M, int nb);

@@ -128,6 +128,14 @@ int ts5hip_rope_kv_append(ts5hip_ctx *ctx, const float *qkv, int ntok, const int
 int ts5hip_attn_decode(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n_head_kv, int head_dim,
                        const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx,
                        const int32_t *n_keys_dev, int kv_per_batch, float scale, int n_split, float *out);
+/* Causal prompt attention on the matrix cores (attn_pf, engine/shaders/attn_pf.glsl with its
+ * policy at engine/src/vk_backend.cpp:954-961; CPU engine/src/cpu_backend.cpp:222-248): nq
+ * queries at positions pos0 .. pos0 + nq - 1 over one q8 cache (the layout above), query t
+ * reading keys 0 .. pos0 + t. q: [nq][H HD]; out: [nq][H HD] fp32. head_dim 128 and
+ * n_head / n_head_kv in {1, 2, 4, 8}; otherwise TS5HIP_ERR_UNSUPPORTED. */
+int ts5hip_attn_prompt(ts5hip_ctx *ctx, const float *q, int nq, int n_head, int n_head_kv, int head_dim,
+                       const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx, int pos0,
+                       float scale, float *out);
 /* Greedy token per row: the first maximum of each row of n logits (engine/src/engine.cpp:17). */
 int ts5hip_argmax(ts5hip_ctx *ctx, const float *x, int n, int rows, int32_t *out_dev);
 /* The k (<= 64) largest of n logits, descending, ties by ascending id (the candidate set

@@ -337,6 +337,57 @@ def test_attention_causal_batch(ctx):
         assert rel_l2(got[b], want) <= REL_L2
 
 
+@pytest.mark.parametrize("nq,p0,n_ctx,H,HKV", [(64, 0, 64, 32, 8), (256, 3840, 4096, 32, 8), (100, 1000, 2048, 8, 2),
+                                             (37, 5, 64, 4, 1), (130, 300, 512, 16, 16), (50, 200, 300, 16, 8),
+                                             (40, 700, 1000, 64, 8), (17, 4079, 4096, 32, 8)])
+def test_attention_prompt_vs_oracle(ctx, nq, p0, n_ctx, H, HKV):
+    """Prompt chunks on the matrix cores: query t at p0 + t over keys 0..p0+t (one split
+    up to 256 keys, then up to 16 merged splits; ragged query blocks; GQA groups 1-8).
+    The path keeps ~22-bit operands, so it is held to 2e-5, not the shared 1e-3."""
+    HD = 128
+    rng = np.random.default_rng(nq + p0 + H)
+    q8, sc, deq = q8_cache(rng, 1, HKV, n_ctx, HD)
+    v8, vsc, vdeq = q8_cache(rng, 1, HKV, n_ctx, HD)
+    q = (rng.standard_normal((nq, H * HD)) * 3).astype(np.float32)
+    scale = float(np.float32(1) / np.sqrt(np.float32(HD)))
+    out = ctx.alloc(q.nbytes)
+    ctx.attn_prompt(ctx.to_device(q), nq, H, HKV, HD, ctx.to_device(q8), ctx.to_device(sc), ctx.to_device(v8),
+                    ctx.to_device(vsc), n_ctx, p0, scale, out)
+    got = out.download(np.float32, (nq, H * HD))
+    kc = deq[0].transpose(1, 0, 2).reshape(n_ctx, HKV * HD)
+    vc = vdeq[0].transpose(1, 0, 2).reshape(n_ctx, HKV * HD)
+    for t in range(nq):
+        want = oracle.attention(q[t], kc, vc, H, HKV, HD, p0 + t, scale)
+        assert rel_l2(got[t], want) <= 2e-5, (t, rel_l2(got[t], want))
+
+
+def test_attention_prompt_large_values_and_bad_shapes(ctx):
+    """Queries of 1e6 (past fp16: each row is scaled by a power of two first), keys of
+    1e3; then shapes the path does not take are refused, not guessed."""
+    H, HKV, HD, n_ctx, p0, nq = 8, 2, 128, 96, 10, 40
+    rng = np.random.default_rng(11)
+    q8, sc, deq = q8_cache(rng, 1, HKV, n_ctx, HD)
+    sc = (sc.astype(np.float32) * 1000).astype(np.float16)
+    deq = (q8.astype(np.float32).reshape(-1, 32) * sc.astype(np.float32).reshape(-1, 1)).reshape(deq.shape)
+    v8, vsc, vdeq = q8_cache(rng, 1, HKV, n_ctx, HD)
+    q = (rng.standard_normal((nq, H * HD)) * 1e6).astype(np.float32)
+    out = ctx.alloc(q.nbytes)
+    ctx.attn_prompt(ctx.to_device(q), nq, H, HKV, HD, ctx.to_device(q8), ctx.to_device(sc), ctx.to_device(v8),
+                    ctx.to_device(vsc), n_ctx, p0, 0.088, out)
+    got = out.download(np.float32, (nq, H * HD))
+    kc = deq[0].transpose(1, 0, 2).reshape(n_ctx, HKV * HD)
+    vc = vdeq[0].transpose(1, 0, 2).reshape(n_ctx, HKV * HD)
+    for t in range(nq):
+        want = oracle.attention(q[t], kc, vc, H, HKV, HD, p0 + t, 0.088)
+        assert rel_l2(got[t], want) <= 2e-5, t
+    with pytest.raises(ts5hip.Ts5HipError):
+        ctx.attn_prompt(ctx.to_device(q), nq, 14, 2, 64, ctx.to_device(q8), ctx.to_device(sc), ctx.to_device(v8),
+                        ctx.to_device(vsc), n_ctx, p0, 0.088, out)
+    with pytest.raises(ts5hip.Ts5HipError):
+        ctx.attn_prompt(ctx.to_device(q), nq, H, HKV, HD, ctx.to_device(q8), ctx.to_device(sc), ctx.to_device(v8),
+                        ctx.to_device(vsc), n_ctx, n_ctx - nq + 1, 0.088, out)
+
+
 # ---- sampling reductions ------------------------------------------------------------------------
 
 def test_argmax_first_maximum(ctx):

@@ -91,6 +91,13 @@ struct AttnIO {
     float *out;     // [B][H * HD]
 };
 hipError_t launch_attn(const AttnIO &io, hipStream_t s);
+// attn_prefill.hip: causal attention of nq consecutive queries (positions p0..,
+// rows q [nq][q_stride]) over one q8 cache on the matrix cores; out [nq][H * HD];
+// part: attn_prefill_partial_bytes(nq, H, HD, p0 + nq) bytes.
+bool attn_prefill_supported(int H, int HKV, int HD);
+size_t attn_prefill_partial_bytes(int nq, int H, int HD, int64_t max_keys);
+hipError_t launch_attn_prefill(const float *q, int64_t q_stride, KvLayer kv, int n_ctx, int H, int HKV, int HD, int p0,
+                               int nq, float scale, float *part, float *out, hipStream_t s);
 // decode.hip: one token as one persistent kernel (cooperative launch) that
 // streams the weights through LDS and hands values between workgroups as
 // tagged 64-bit words (value bits, launch tag).

@@ -608,6 +608,7 @@ int ensure_batch(ts5hip_model *m) {
         g(hp.n_vocab, E, out.type);
         part = std::max(part, attn_partial_bytes(M, attn_splits(M, hp.n_head_kv, 512), hp.n_head, hp.head_dim));
     }
+    part = std::max(part, attn_prefill_partial_bytes(CHUNK, hp.n_head, hp.head_dim, m->n_ctx));
     int rc = 0;
     if ((rc = alloc_t(m, CHUNK * E, &m->bx)) || (rc = alloc_t(m, CHUNK * QR, &m->bqkv)) ||
         (rc = alloc_t(m, CHUNK * AH, &m->bq)) || (rc = alloc_t(m, CHUNK * AH, &m->batt)) ||
@@ -667,12 +668,17 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
         const float *kn = L.k_norm.set ? (const float *)L.k_norm.d : nullptr;
         TS5_HIP(ctx, launch_rope_kv(m->bqkv, QR, bias, qn, kn, eps, m->rope_cs, hp.rope_dims, hp.rope_neox, m->state,
                                     H, HKV, HD, m->n_ctx, nc, m->bq, m->kv_layer(l), s));
-        AttnIO io{};
-        io.q = m->bq, io.q_stride = AH, io.rope = 0, io.append = 0;
-        io.kv = m->kv_layer(l), io.kv_per_batch = 0, io.n_ctx = m->n_ctx, io.n_keys = m->state;
-        io.B = nc, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = attn_splits(nc, HKV, 512);
-        io.scale = hp.attn_scale, io.part = m->bpart, io.counters = m->bcounters, io.out = m->batt;
-        TS5_HIP(ctx, launch_attn(io, s));
+        if (nc > 16 && attn_prefill_supported(H, HKV, HD)) {  // prompt chunks: flash attention on the matrix cores
+            TS5_HIP(ctx, launch_attn_prefill(m->bq, AH, m->kv_layer(l), m->n_ctx, H, HKV, HD, p0, nc, hp.attn_scale,
+                                             m->bpart, m->batt, s));
+        } else {
+            AttnIO io{};
+            io.q = m->bq, io.q_stride = AH, io.rope = 0, io.append = 0;
+            io.kv = m->kv_layer(l), io.kv_per_batch = 0, io.n_ctx = m->n_ctx, io.n_keys = m->state;
+            io.B = nc, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = attn_splits(nc, HKV, 512);
+            io.scale = hp.attn_scale, io.part = m->bpart, io.counters = m->bcounters, io.out = m->batt;
+            TS5_HIP(ctx, launch_attn(io, s));
+        }
         if (int rc = proj(L.wo.type, L.wo.d, nullptr, AH, E, m->batt, AH, nullptr, nc, 1, m->bx, E)) return rc;
         if (int rc = proj(L.gate.type, L.gate.d, L.up.d, E, F, m->bx, E, (const float *)L.ffn_norm.d, nc, 2, m->bffn, F))
             return rc;

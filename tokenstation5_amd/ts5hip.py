@@ -66,6 +66,7 @@ _SIGS = {
                                      _f32, _vp, _vp, _vp, _vp, _vp]),
     "ts5hip_attn_decode": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _f32, _i32,
                                   _vp]),
+    "ts5hip_attn_prompt": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "ts5hip_argmax": (_i32, [_vp, _vp, _i32, _i32, _vp]),
     "ts5hip_topk": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp]),
     "ts5hip_sampler_new": (_vp, [_u64]),
@@ -283,6 +284,10 @@ class Context:
                     n_split=0):
         self.check(lib().ts5hip_attn_decode(self.h, _ptr(q), B, H, HKV, HD, _ptr(k8), _ptr(ks), _ptr(v8), _ptr(vs),
                                             n_ctx, _ptr(n_keys_dev), int(kv_per_batch), scale, n_split, _ptr(out)))
+
+    def attn_prompt(self, q, nq, H, HKV, HD, k8, ks, v8, vs, n_ctx, pos0, scale, out):
+        self.check(lib().ts5hip_attn_prompt(self.h, _ptr(q), nq, H, HKV, HD, _ptr(k8), _ptr(ks), _ptr(v8), _ptr(vs),
+                                            n_ctx, pos0, scale, _ptr(out)))
 
     def argmax(self, x, n, rows, out):
         self.check(lib().ts5hip_argmax(self.h, _ptr(x), n, rows, _ptr(out)))

@@ -175,6 +175,26 @@ def roofline_only(hp):
                       "stream_write_bytes": n * rows * 4}), flush=True)
 
 
+def prefill_only(hp, prompt_len: int = PROMPT):
+    """The prompt alone (for rocprofv3 runs of the prefill kernels): one
+    256-token chunk to warm up, then the prompt's prefill into the q8 cache,
+    timed with HIP events on the library's stream."""
+    ctx = ts5hip.Context(0)
+    m = ts5hip.Model(ctx, hp, prompt_len + 16)
+    for name, t, ne0, ne1 in model_tensor_specs(hp):
+        m.synth_tensor(name, t, ne0, ne1, SEED)
+    prompt = np.random.default_rng(SEED).integers(0, hp["n_vocab"], prompt_len).astype(np.int32)
+    m.forward(prompt[:256], 0, logits=False)
+    ctx.sync()
+    ctx.timer_begin()
+    m.forward(prompt, 0, logits=False)
+    ms = ctx.timer_end()
+    m.close()
+    ctx.close()
+    print(json.dumps({"prefill_tokens": prompt_len, "prefill_ms": round(ms, 2),
+                      "prefill_tok_s": round(prompt_len / ms * 1e3, 1)}), flush=True)
+
+
 def cpu_baseline(hp, steps: int = 3, keys: int = PROMPT):
     """The CPU oracle decoding `steps` tokens of the same model shape at
     `keys` cached positions (KV seeded with random q8-rounded values)."""
@@ -212,6 +232,8 @@ def main():
     ap.add_argument("--prompt", type=int, default=PROMPT, help="prompt length (cfg2: 4096)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the roofline kernel's launches and a 256 MiB device copy (for rocprofv3 --pmc)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the prompt's prefill, timed on the device (for rocprofv3 runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this backend runs ts5's token loop on one GPU (batch 1); "
@@ -220,6 +242,9 @@ def main():
     hp = dict(synth.LLAMA_8B)
     if args.roofline_only:
         roofline_only(hp)
+        return
+    if args.prefill_only:
+        prefill_only(hp, args.prompt)
         return
     ctx = ts5hip.Context(0)
     log(f"device {ctx.arch}, {ctx.n_cu} CUs, {ctx.hbm / 2**30:.0f} GiB")

@@ -164,6 +164,90 @@ __global__ __launch_bounds__(256) void k_act_half(const float *__restrict__ x, i
     }
 }
 
+// The same form from one read of x: thread t holds 16-value runs t, t + 256,
+// ... (at most RUNS) in registers through the norm's sum, the maximum and the
+// writes; the two runs of a 32-value chunk sit in adjacent lanes.
+template <int RUNS>
+__global__ __launch_bounds__(256) void k_act_half_reg(const float *__restrict__ x, int64_t xstride,
+                                                      const float *__restrict__ w, float eps, int n,
+                                                      uint8_t *__restrict__ act, int64_t act_stride) {
+    __shared__ float red[4], redm[4];
+    const float *xt = x + (int64_t)blockIdx.x * xstride;
+    uint8_t *o = act + (int64_t)blockIdx.x * act_stride;
+    const int tid = threadIdx.x, nr = n / 16;
+    float v[RUNS][16];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < RUNS; k++) {
+        const int r = tid + 256 * k;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float4 f = r < nr ? *(const float4 *)(xt + 16 * r + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[k][4 * j] = f.x, v[k][4 * j + 1] = f.y, v[k][4 * j + 2] = f.z, v[k][4 * j + 3] = f.w;
+            ss += f.x * f.x + f.y * f.y + f.z * f.z + f.w * f.w;
+        }
+    }
+    float s = 1.0f;
+    if (w) {  // the same expression as act_rms
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        s = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)n + eps);
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int k = 0; k < RUNS; k++) {
+        const int r = tid + 256 * k;
+        if (w && r < nr) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float4 g = *(const float4 *)(w + 16 * r + 4 * j);
+                v[k][4 * j] = v[k][4 * j] * s * g.x, v[k][4 * j + 1] = v[k][4 * j + 1] * s * g.y;
+                v[k][4 * j + 2] = v[k][4 * j + 2] * s * g.z, v[k][4 * j + 3] = v[k][4 * j + 3] * s * g.w;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[k][i]));
+    }
+    amax = wave_max(amax);
+    if ((tid & 63) == 0) redm[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
+    const int e = amax > 0.f ? max(ilogbf(amax) - 13, -100) : 0;  // amax 2^-e in [2^13, 2^14)
+    const float scale = ldexpf(1.0f, -e);
+    if (tid == 0) *(float *)(o + hact_unscale(n)) = ldexpf(1.0f, e);
+#pragma unroll
+    for (int k = 0; k < RUNS; k++) {
+        const int r = tid + 256 * k;  // runs 2c, 2c + 1 in adjacent lanes, both in or both out
+        uint32_t hw[8], lw[8];
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j += 2) {
+            const float f0 = v[k][j] * scale, f1 = v[k][j + 1] * scale;
+            const _Float16 h0 = (_Float16)f0, h1 = (_Float16)f1;
+            const _Float16 l0 = (_Float16)(f0 - (float)h0), l1 = (_Float16)(f1 - (float)h1);
+            hw[j / 2] = __builtin_bit_cast(uint16_t, h0) | (uint32_t)__builtin_bit_cast(uint16_t, h1) << 16;
+            lw[j / 2] = __builtin_bit_cast(uint16_t, l0) | (uint32_t)__builtin_bit_cast(uint16_t, l1) << 16;
+            sum += f0 + f1;
+        }
+        sum += __shfl_xor(sum, 1, WAVE);
+        if (r >= nr) continue;
+        const int c = r / 2;  // the 32-value chunk
+        uint8_t *blk = o + (size_t)(c / 8) * 1024 + (c % 8) * 64 + (r & 1) * 32;
+        ((uint4 *)blk)[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        ((uint4 *)blk)[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+        ((uint4 *)(blk + 512))[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        ((uint4 *)(blk + 512))[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+        if ((r & 1) == 0) {
+            const float xs = sum * (1.0f / 32);
+            const _Float16 xh = (_Float16)xs, xl = (_Float16)(xs - (float)xh);
+            uint16_t *xq = (uint16_t *)(o + hact_x(n)) + 4 * (c / 2) + (c & 1);
+            xq[0] = __builtin_bit_cast(uint16_t, xh);
+            xq[2] = __builtin_bit_cast(uint16_t, xl);
+        }
+    }
+}
+
 size_t gemm_act_bytes(uint32_t t, int64_t n, int ntok) {
     switch (gemm_act_form(t, n, ntok)) {
     case GA_HACT: return hact_bytes(n);
@@ -176,7 +260,13 @@ hipError_t launch_gemm_act(uint32_t t, const float *x, int64_t xstride, const fl
                            void *act, hipStream_t s) {
     const int form = gemm_act_form(t, n, ntok);
     if (form == GA_ACT) return launch_act_quant(x, xstride, w, eps, n, ntok, act, s);
-    if (form == GA_HACT)
+    if (form == GA_HACT && n <= 256 * 16)
+        hipLaunchKernelGGL(k_act_half_reg<1>, dim3(ntok), dim3(256), 0, s, x, xstride, w, eps, n, (uint8_t *)act,
+                           (int64_t)hact_bytes(n));
+    else if (form == GA_HACT && n <= 256 * 64)
+        hipLaunchKernelGGL(k_act_half_reg<4>, dim3(ntok), dim3(256), 0, s, x, xstride, w, eps, n, (uint8_t *)act,
+                           (int64_t)hact_bytes(n));
+    else if (form == GA_HACT)
         hipLaunchKernelGGL(k_act_half, dim3(ntok), dim3(256), 0, s, x, xstride, w, eps, n, (uint8_t *)act,
                            (int64_t)hact_bytes(n));
     else

@@ -57,10 +57,6 @@ struct WideArgs {
     int nrows, nb, n_in, M, ks;
 };
 
-#ifndef TS5_WIDE_SCHED
-#define TS5_WIDE_SCHED 0
-#endif
-
 enum { W_STORE = 0, W_ADD = 1, W_GLU = 2 };
 constexpr int WG_TOK = 128;
 __host__ __device__ constexpr int wide_rows(int mode) { return mode == W_GLU ? 64 : 128; }
@@ -150,11 +146,6 @@ __device__ inline void wide_stage(const WideStage &S, WideAcc &R, int wave, int 
     for (int p = 0; p < 2; p++) q[p] = *(const uint2 *)((const uint8_t *)&S.wq[wave][16 * p + rl][0] + 8 * kq);
 #pragma unroll
     for (int c = 0; c < 2; c++) {
-#if TS5_WIDE_SCHED == 1
-        __builtin_amdgcn_iglp_opt(0);
-#elif TS5_WIDE_SCHED == 2
-        __builtin_amdgcn_iglp_opt(1);
-#endif
         v8h A[2];
 #pragma unroll
         for (int p = 0; p < 2; p++) A[p] = nib_f16(q[p], c, sc[p][c], off[p][c]);

@@ -330,9 +330,12 @@ bool attn_prefill_supported(int H, int HKV, int HD) {
     return HD == 128 && (G == 1 || G == 2 || G == 4 || G == 8);
 }
 
-// Keys per split: a multiple of 64, at least 256, at most 16 splits.
-static int pf_split_keys(int64_t max_keys) {
-    const int64_t per = std::max<int64_t>(256, (max_keys + 15) / 16);
+// Keys per split: a multiple of 64, at least 256, at most 16 splits, and
+// no more splits than bring the launch to about 512 workgroups (wg: the
+// workgroups of one split); every split adds (m, l, O) partials to merge.
+static int pf_split_keys(int64_t max_keys, int64_t wg) {
+    const int64_t splits = std::max<int64_t>(1, std::min<int64_t>(16, (512 + wg - 1) / wg));
+    const int64_t per = std::max<int64_t>(256, (max_keys + splits - 1) / splits);
     return (int)((per + PF_KB - 1) / PF_KB * PF_KB);
 }
 
@@ -350,7 +353,8 @@ hipError_t launch_attn_prefill(const float *q, int64_t q_stride, KvLayer kv, int
     a.q = q, a.q_stride = q_stride, a.kv = kv, a.n_ctx = n_ctx, a.H = H, a.HKV = HKV, a.p0 = p0, a.nq = nq;
     a.scale = scale, a.part = part, a.out = out;
     const int64_t max_keys = (int64_t)p0 + nq;
-    a.split_keys = pf_split_keys(max_keys);
+    const int qb = PF_ROWS / (H / HKV);
+    a.split_keys = pf_split_keys(max_keys, (int64_t)((nq + qb - 1) / qb) * HKV);
     a.n_split = (int)((max_keys + a.split_keys - 1) / a.split_keys);
     const int G = H / HKV, QB = PF_ROWS / G;
     const dim3 grid((unsigned)((nq + QB - 1) / QB), (unsigned)HKV, (unsigned)a.n_split);

@@ -30,8 +30,10 @@ __global__ void k_embed(uint32_t t, const uint8_t *__restrict__ w, int64_t ne0, 
     int64_t row = ids[(pos ? pos[0] : 0) + (int)blockIdx.x];
     if (row < 0 || row >= n_rows) row = 0;  // ids are checked on the host; never read out of bounds
     float *out = x + (int64_t)blockIdx.x * ne0;
-    for (int64_t i = threadIdx.x; i < ne0; i += blockDim.x)
-        out[i] = unpack_value(t, w, (int64_t)nb * n_rows, row, t == T_F32 || t == T_F16 ? (int)ne0 : nb, i);
+    // One value per thread (grid.y covers the row): every value's loads are
+    // independent, so a token costs one memory round trip, not one per value.
+    const int64_t i = (int64_t)blockIdx.y * blockDim.x + threadIdx.x;
+    if (i < ne0) out[i] = unpack_value(t, w, (int64_t)nb * n_rows, row, t == T_F32 || t == T_F16 ? (int)ne0 : nb, i);
 }
 
 // ---------------------------------------------------------------------------
@@ -141,7 +143,8 @@ hipError_t launch_dequant(uint32_t t, const void *w, int64_t ne0, int64_t rows, 
 
 hipError_t launch_embed(uint32_t t, const void *w, int64_t ne0, int64_t n_rows, const int32_t *ids, const int32_t *pos,
                         int ntok, float *x, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed, dim3(ntok), dim3(256), 0, s, t, (const uint8_t *)w, ne0, n_rows, ids, pos, x);
+    hipLaunchKernelGGL(k_embed, dim3(ntok, (unsigned)((ne0 + 255) / 256)), dim3(256), 0, s, t, (const uint8_t *)w, ne0,
+                       n_rows, ids, pos, x);
     return hipGetLastError();
 }
 

@@ -103,8 +103,22 @@ def test_matmul_norm_and_accumulate(ctx):
     assert np.array_equal(got, np.zeros_like(got))
 
 
+@pytest.mark.parametrize("t,ne0,rows", [(synth.Q6_K, 4096, 515), (synth.Q6_K, 512, 1000), (synth.Q8_0, 896, 300),
+                                         (synth.Q8_0, 4864, 128)])
+@pytest.mark.parametrize("ntok", [130, 256])
+def test_matmul_prompt_chunk_vs_oracle(ctx, t, ne0, rows, ntok):
+    """Q6_K and Q8_0 at prompt-chunk sizes (the int8 matrix-core path in
+    64-token tiles, ragged at 130): the shared bar per token."""
+    W = synth.tensor(t, ne0, rows, 9, f"pc{t}_{ne0}_{rows}")
+    x = np.random.default_rng(ne0 + 5 * rows + ntok).standard_normal((ntok, ne0)).astype(np.float32)
+    got = run_matmul(ctx, t, W, ne0, rows, x)
+    want = oracle.matmul(t, W, ne0, x)
+    for i in range(ntok):
+        assert rel_l2(got[i], want[i]) <= REL_L2, (i, rel_l2(got[i], want[i]))
+
+
 @pytest.mark.parametrize("t,ne0,rows", [(synth.Q4_K, 4096, 1536), (synth.Q8_0, 896, 4864)])
-@pytest.mark.parametrize("ntok", [1, 5, 40])
+@pytest.mark.parametrize("ntok", [1, 5, 40, 256])
 def test_matmul_glu_vs_oracle(ctx, t, ne0, rows, ntok):
     """silu(Wg x') * (Wu x') per token (engine/src/cpu_backend.cpp:253-261)."""
     rng = np.random.default_rng(rows + ntok)

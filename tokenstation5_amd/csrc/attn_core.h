@@ -47,7 +47,7 @@ struct AttnArgs {
     const int32_t *n_keys;
     float scale;
     float *part;    // [B][n_split][H][HD + 2]
-    int *counters;  // [B * HKV], zero between launches
+    int *counters;  // [B * HKV] at CTR_STRIDE ints apart, zero between launches
     float *out;     // [B][H * HD]
 };
 
@@ -363,7 +363,7 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
     }
     wait_stores();
     __syncthreads();
-    if (tid == 0) S.last = atomicAdd(a.counters + b * a.HKV + kvh, 1) == n_split - 1;
+    if (tid == 0) S.last = atomicAdd(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 1) == n_split - 1;
     __syncthreads();
     if (!S.last) return;
     const float *p_all = a.part + ((int64_t)b * n_split * a.H + (int64_t)kvh * G) * rec;
@@ -396,7 +396,7 @@ __device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, i
         for (int sp = 0; sp < n_split; sp++) acc += S.mw[sp][g] * pd[sp * sstride];
         st_dev(a.out + (int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d, acc / S.red[g]);
     }
-    if (tid == 0) st_dev(a.counters + b * a.HKV + kvh, 0);  // ready for the next use
+    if (tid == 0) st_dev(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 0);  // ready for the next use
 }
 
 // ---------------------------------------------------------------------------
@@ -608,7 +608,7 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
     }
     wait_stores();
     __syncthreads();
-    if (tid == 0) S.last = atomicAdd(a.counters + b * a.HKV + kvh, 1) == n_split - 1;
+    if (tid == 0) S.last = atomicAdd(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 1) == n_split - 1;
     __syncthreads();
     if (!S.last) return;
     // The merge: this thread's outputs of every split (up to 32 at a time)
@@ -663,7 +663,7 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
             st_dev(a.out + (int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d, acc[k] / S.red[g]);
         }
     }
-    if (tid == 0) st_dev(a.counters + b * a.HKV + kvh, 0);  // ready for the next use
+    if (tid == 0) st_dev(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 0);  // ready for the next use
 }
 
 }  // namespace ts5hip

@@ -15,6 +15,9 @@ using namespace ts5hip;
 
 namespace {
 thread_local std::string g_thread_err;
+// The per-op entry points' completion counters: up to 4096 (query, KV head)
+// attention merges, then the head argmax's.
+constexpr size_t CTX_COUNTER_INTS = 4096 * CTR_STRIDE + ARGMAX_CTR_INTS;
 }
 
 namespace ts5hip {
@@ -92,8 +95,8 @@ int ts5hip_init(int device, ts5hip_ctx **out) {
     set_cu_count(c->n_cu);
     if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess ||
         (e = hipEventCreate(&c->ev0)) != hipSuccess || (e = hipEventCreate(&c->ev1)) != hipSuccess ||
-        (e = hipMalloc((void **)&c->counters, 4160 * sizeof(int))) != hipSuccess ||
-        (e = hipMemset(c->counters, 0, 4160 * sizeof(int))) != hipSuccess) {
+        (e = hipMalloc((void **)&c->counters, CTX_COUNTER_INTS * sizeof(int))) != hipSuccess ||
+        (e = hipMemset(c->counters, 0, CTX_COUNTER_INTS * sizeof(int))) != hipSuccess) {
         hip_fail(nullptr, e, "stream/event creation");
         ts5hip_destroy(c);
         return TS5HIP_ERR_HIP;
@@ -278,7 +281,7 @@ int ts5hip_matvec_argmax(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t 
     if (!ctx || !w || !x || !y || !out_dev) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
     if (int rc = check_matrix(ctx, type, ne0, ne1)) return rc;
     if (int rc = ensure_scratch(ctx, matvec_argmax_scratch_bytes())) return rc;
-    TS5_HIP(ctx, launch_matvec_argmax(type, w, ne0, ne1, x, norm_w, eps, y, ctx->scratch, ctx->counters + 4096,
+    TS5_HIP(ctx, launch_matvec_argmax(type, w, ne0, ne1, x, norm_w, eps, y, ctx->scratch, ctx->counters + 4096 * CTR_STRIDE,
                                       out_dev, nullptr, nullptr, ctx->stream));
     return TS5HIP_OK;
 }

@@ -58,7 +58,18 @@ hipError_t launch_matvec(uint32_t t, const void *w, int64_t ne0, int64_t ne1, co
 hipError_t launch_matvec_glu(uint32_t t, const void *wg, const void *wu, int64_t ne0, int64_t ne1, const float *x,
                              const float *norm_w, float eps, float *y, hipStream_t s);
 // y = W x and out[0] = the first argmax of y; with seq: seq[*pos + 1] = it, ++*pos.
-// scratch: matvec_argmax_scratch_bytes(); *counter zero before (and after) the launch.
+// Completion counters (a workgroup counts in; the last one to arrive does the
+// epilogue) sit CTR_STRIDE ints apart: atomics from different workgroups to
+// one 64-byte granule are served one after another (about 10 ns each on
+// this chip; 256 of them add 1.7 us to a launch), to different lines in
+// parallel.
+constexpr int CTR_STRIDE = 32;
+// The head's argmax counts its workgroups into ARGMAX_FAN sub-counters, the
+// last arrival at each into a top counter: ARGMAX_CTR_INTS ints.
+constexpr int ARGMAX_FAN = 16;
+constexpr int ARGMAX_CTR_INTS = (1 + ARGMAX_FAN) * CTR_STRIDE;
+// scratch: matvec_argmax_scratch_bytes(); counter: ARGMAX_CTR_INTS ints, zero
+// before (and after) the launch.
 size_t matvec_argmax_scratch_bytes();
 hipError_t launch_matvec_argmax(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const float *x,
                                 const float *norm_w, float eps, float *y, void *scratch, int *counter, int32_t *out,
@@ -87,7 +98,7 @@ struct AttnIO {
     int B, H, HKV, HD, n_split;
     float scale;
     float *part;    // B * n_split * H * (HD + 2) floats
-    int *counters;  // B * HKV ints, zero before the first launch (kept zero after)
+    int *counters;  // B * HKV * CTR_STRIDE ints, zero before the first launch (kept zero after)
     float *out;     // [B][H * HD]
 };
 hipError_t launch_attn(const AttnIO &io, hipStream_t s);

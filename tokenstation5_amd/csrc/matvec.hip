@@ -46,12 +46,20 @@ __global__ __launch_bounds__(WAVES *WAVE) void k_mv(const void *w, const void *w
     };
     mv_run<F, R, WAVES, MODE, RUNS, NORM>(a, blockIdx.x, nwg, lds, red, fetch_tail, best_v, best_i);
     if (MODE != MV_ARGMAX) return;
-    // Each workgroup's best, then the last workgroup to finish picks the winner.
+    // Each workgroup's best, then the last workgroup to finish picks the
+    // winner. Workgroup w counts into sub-counter w % ARGMAX_FAN, the last
+    // arrival there (which zeroes it) into the top counter a.counter[0].
     if (threadIdx.x == 0) {
         st_dev(a.best_v + blockIdx.x, best_v);
         st_dev(a.best_i + blockIdx.x, best_i);
         wait_stores();
-        last = atomicAdd(a.counter, 1) == (int)gridDim.x - 1;
+        const int n = (int)gridDim.x, sub = blockIdx.x % ARGMAX_FAN;
+        int *sc = a.counter + CTR_STRIDE * (1 + sub);
+        last = 0;
+        if (atomicAdd(sc, 1) == (n - sub + ARGMAX_FAN - 1) / ARGMAX_FAN - 1) {
+            st_dev(sc, 0);
+            last = atomicAdd(a.counter, 1) == min(n, ARGMAX_FAN) - 1;
+        }
     }
     __syncthreads();
     if (!last) return;

@@ -61,7 +61,7 @@ struct ts5hip_model {
     bool rope_ready = false;
     // Activations and scratch.
     float *x = nullptr, *qkv = nullptr, *att = nullptr, *ffn = nullptr, *logits = nullptr, *part = nullptr;
-    int *counters = nullptr;  // [HKV] attention merges, [HKV] head argmax; zero between launches
+    int *counters = nullptr;  // HKV attention merges (CTR_STRIDE apart), then the head argmax's; zero between launches
     void *amax = nullptr, *topk = nullptr;
     float *topk_v = nullptr;
     int32_t *topk_i = nullptr;
@@ -377,7 +377,7 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
         const float *on = (const float *)m->out_norm.d;
         if (tail == 1) {
             TS5_HIP(ctx, launch_matvec_argmax(out.type, out.d, E, hp.n_vocab, m->x, on, hp.rms_eps, m->logits, m->amax,
-                                              m->counters + HKV, m->state + 1, m->seq, m->state, s));
+                                              m->counters + HKV * CTR_STRIDE, m->state + 1, m->seq, m->state, s));
             return TS5HIP_OK;
         }
         TS5_HIP(ctx, launch_matvec(out.type, out.d, E, hp.n_vocab, m->x, on, hp.rms_eps, m->logits, 0, s));
@@ -615,9 +615,9 @@ int ensure_batch(ts5hip_model *m) {
         (rc = alloc_t(m, CHUNK * F, &m->bffn)) ||
         (rc = alloc(m, CHUNK * std::max({act_bytes(wide), mact_bytes(wide), hact_bytes(wide)}), &m->bact)) ||
         (rc = alloc(m, std::max<size_t>(gemm, 256), &m->bgemm)) || (rc = alloc(m, part, (void **)&m->bpart)) ||
-        (rc = alloc_t(m, (size_t)CHUNK * hp.n_head_kv, &m->bcounters)))
+        (rc = alloc_t(m, (size_t)CHUNK * hp.n_head_kv * CTR_STRIDE, &m->bcounters)))
         return rc;
-    TS5_HIP(m->ctx, hipMemsetAsync(m->bcounters, 0, (size_t)CHUNK * hp.n_head_kv * 4, m->ctx->stream));
+    TS5_HIP(m->ctx, hipMemsetAsync(m->bcounters, 0, (size_t)CHUNK * hp.n_head_kv * CTR_STRIDE * 4, m->ctx->stream));
     return TS5HIP_OK;
 }
 
@@ -786,7 +786,7 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
         (rc = alloc_t(m, m->qkv_rows(), &m->qkv)) || (rc = alloc_t(m, H * HD, &m->att)) ||
         (rc = alloc_t(m, F, &m->ffn)) || (rc = alloc_t(m, hp->n_vocab, &m->logits)) ||
         (rc = alloc_t(m, attn_partial_bytes(1, 64, H, HD) / 4, &m->part)) ||
-        (rc = alloc_t(m, 2 * HKV + 64, &m->counters)) ||
+        (rc = alloc_t(m, HKV * CTR_STRIDE + ARGMAX_CTR_INTS, &m->counters)) ||
         (rc = alloc(m, matvec_argmax_scratch_bytes(), &m->amax)) || (rc = alloc(m, topk_scratch_bytes(), &m->topk)) ||
         (rc = alloc_t(m, 64, &m->topk_v)) || (rc = alloc_t(m, 64, &m->topk_i)) ||
         (rc = alloc_t(m, (size_t)n_ctx + 1, &m->seq)) || (rc = alloc_t(m, 4, &m->state))) {
@@ -796,7 +796,7 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
     hipError_t e;
     if ((e = hipMemsetAsync(m->bias, 0, (size_t)hp->n_layer * m->qkv_rows() * 4, ctx->stream)) != hipSuccess ||
         (e = hipMemsetAsync(m->seq, 0, ((size_t)n_ctx + 1) * 4, ctx->stream)) != hipSuccess ||
-        (e = hipMemsetAsync(m->counters, 0, (2 * (size_t)HKV + 64) * 4, ctx->stream)) != hipSuccess ||
+        (e = hipMemsetAsync(m->counters, 0, ((size_t)HKV * CTR_STRIDE + ARGMAX_CTR_INTS) * 4, ctx->stream)) != hipSuccess ||
         (e = hipMemsetAsync(m->k8, 0, kv_elems, ctx->stream)) != hipSuccess ||
         (e = hipMemsetAsync(m->v8, 0, kv_elems, ctx->stream)) != hipSuccess ||
         (e = hipMemsetAsync(m->ks, 0, kv_elems / 32 * 2, ctx->stream)) != hipSuccess ||

@@ -21,7 +21,7 @@ struct ts5hip_ctx {
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
     // Zeroed once; kernels that count finished workgroups leave them zero.
-    int *counters = nullptr;  // [0, 4096): attention, [4096]: head argmax
+    int *counters = nullptr;  // 4096 attention counters (CTR_STRIDE apart), then the head argmax's
 };
 
 namespace ts5hip {

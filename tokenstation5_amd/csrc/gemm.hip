@@ -506,21 +506,74 @@ __global__ __launch_bounds__(256) void k_gemm_small(GemmArgs a) {
 }
 
 // Split-K: y[t][r] = (y_in +) sum over splits in order (GLU: silu(g) * u).
-__global__ void k_gemm_reduce(const float *__restrict__ part, int ks, int M, int nrows, int mode, float *y,
-                              const float *y_in, int64_t ldy) {
+// Four consecutive values a thread (rows of one token when nrows % 4 == 0,
+// else one value at a time), every split's partial requested before the
+// first is added; the sums run in split order.
+template <int MODE>
+__device__ inline void gemm_reduce_one(const float *__restrict__ part, int ks, int64_t n, int nrows, int64_t e,
+                                       float *y, const float *y_in, int64_t ldy) {
+    float g = 0.f, u = 0.f;
+    for (int k = 0; k < ks; k++) {
+        g += part[(int64_t)k * 2 * n + e];
+        if (MODE == G_GLU) u += part[(int64_t)k * 2 * n + n + e];
+    }
+    const int tok = (int)(e / nrows), r = (int)(e % nrows);
+    const int64_t o = (int64_t)tok * ldy + r;
+    if (MODE == G_ADD) y[o] = y_in[o] + g;
+    else if (MODE == G_GLU) y[o] = g / (1.0f + expf(-g)) * u;
+    else y[o] = g;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ part, int ks, int M, int nrows, float *y,
+                                                     const float *y_in, int64_t ldy) {
     const int64_t n = (int64_t)M * nrows;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
-        float g = 0.f, u = 0.f;
-        for (int k = 0; k < ks; k++) {
-            g += part[(int64_t)k * 2 * n + e];
-            if (mode == G_GLU) u += part[(int64_t)k * 2 * n + n + e];
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    if (nrows % 4) {
+        for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += stride)
+            gemm_reduce_one<MODE>(part, ks, n, nrows, e, y, y_in, ldy);
+        return;
+    }
+    constexpr int KC = 8;  // splits requested at once
+    for (int64_t e = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x); e < n; e += 4 * stride) {
+        float4 g = make_float4(0.f, 0.f, 0.f, 0.f), u = g;
+        for (int k0 = 0; k0 < ks; k0 += KC) {
+            float4 pg[KC], pu[KC];
+#pragma unroll
+            for (int k = 0; k < KC; k++) {
+                if (k0 + k < ks) {
+                    pg[k] = *(const float4 *)(part + (int64_t)(k0 + k) * 2 * n + e);
+                    if (MODE == G_GLU) pu[k] = *(const float4 *)(part + (int64_t)(k0 + k) * 2 * n + n + e);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < KC; k++) {
+                if (k0 + k < ks) {
+                    g.x += pg[k].x, g.y += pg[k].y, g.z += pg[k].z, g.w += pg[k].w;
+                    if (MODE == G_GLU) u.x += pu[k].x, u.y += pu[k].y, u.z += pu[k].z, u.w += pu[k].w;
+                }
+            }
         }
         const int tok = (int)(e / nrows), r = (int)(e % nrows);
-        const int64_t o = (int64_t)tok * ldy + r;
-        if (mode == G_ADD) y[o] = y_in[o] + g;
-        else if (mode == G_GLU) y[o] = g / (1.0f + expf(-g)) * u;
-        else y[o] = g;
+        float *o = y + (int64_t)tok * ldy + r;
+        const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (MODE == G_ADD) o[j] = y_in[(int64_t)tok * ldy + r + j] + gv[j];
+            else if (MODE == G_GLU) o[j] = gv[j] / (1.0f + expf(-gv[j])) * uv[j];  // cpu_backend.cpp:260-261
+            else o[j] = gv[j];
+        }
     }
+}
+
+static hipError_t launch_gemm_reduce(const float *part, int ks, int M, int nrows, int mode, float *y, const float *y_in,
+                                     int64_t ldy, hipStream_t s) {
+    const int64_t n = (int64_t)M * nrows, per = nrows % 4 ? 1 : 4;
+    const dim3 g((unsigned)std::min<int64_t>(4096, (n / per + 255) / 256)), b(256);
+    if (mode == G_ADD) hipLaunchKernelGGL(k_gemm_reduce<G_ADD>, g, b, 0, s, part, ks, M, nrows, y, y_in, ldy);
+    else if (mode == G_GLU) hipLaunchKernelGGL(k_gemm_reduce<G_GLU>, g, b, 0, s, part, ks, M, nrows, y, y_in, ldy);
+    else hipLaunchKernelGGL(k_gemm_reduce<G_STORE>, g, b, 0, s, part, ks, M, nrows, y, y_in, ldy);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -581,10 +634,7 @@ hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, i
         const int ks = wide_splits(ne1, M, (int)(ne0 / 256), g_gemm_cu, mode);
         hipError_t e = launch_gemm_wide(w, w2, ne0, ne1, act, M, mode, y, y_in, ldy, scratch, ks, s);
         if (e != hipSuccess || ks == 1) return e;
-        const int64_t n = (int64_t)M * ne1;
-        hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)std::min<int64_t>(4096, (n + 255) / 256)), dim3(256), 0, s,
-                           (const float *)scratch, ks, M, (int)ne1, mode, y, y_in, ldy);
-        return hipGetLastError();
+        return launch_gemm_reduce((const float *)scratch, ks, M, (int)ne1, mode, y, y_in, ldy, s);
     }
     a.act_stride = (int64_t)gemm_act_bytes(t, ne0, M), a.y_in = y_in, a.ldy = ldy;
     if (t == T_Q6_K || t == T_Q8_0) {
@@ -600,10 +650,7 @@ hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, i
                    : mode == G_GLU ? gemm_fmt<G_GLU>(a, grid, tn, s)
                                    : gemm_fmt<G_STORE>(a, grid, tn, s);
     if (e != hipSuccess || a.ks == 1) return e;
-    const int64_t n = (int64_t)M * ne1;
-    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)std::min<int64_t>(4096, (n + 255) / 256)), dim3(256), 0, s,
-                       (const float *)scratch, a.ks, M, (int)ne1, mode, y, y_in, ldy);
-    return hipGetLastError();
+    return launch_gemm_reduce((const float *)scratch, a.ks, M, (int)ne1, mode, y, y_in, ldy, s);
 }
 
 }  // namespace ts5hip

@@ -301,6 +301,31 @@ def test_attention_vs_oracle(ctx, B, ctxlen, H, HKV, HD):
         assert rel_l2(got[b], want) <= REL_L2, (b, rel_l2(got[b], want))
 
 
+def test_attention_most_work_items_twice(ctx):
+    """B * HKV = 4096 (the per-op entry point's limit): every (query, KV head)
+    merge counter in use, run twice (the counters must be back at zero), and
+    one more query refused."""
+    rng = np.random.default_rng(11)
+    B, H, HKV, HD, n = 512, 32, 8, 64, 40
+    q8, sc, deq = q8_cache(rng, B, HKV, n, HD)
+    v8, vsc, vdeq = q8_cache(rng, B, HKV, n, HD)
+    q = rng.standard_normal((B, H * HD)).astype(np.float32)
+    args = (ctx.to_device(q8), ctx.to_device(sc), ctx.to_device(v8), ctx.to_device(vsc), n,
+            ctx.to_device(np.full(B, n, np.int32)), 1, 0.125)
+    dq = ctx.to_device(q)
+    for _ in range(2):
+        out = ctx.alloc(q.nbytes)
+        ctx.attn_decode(dq, B, H, HKV, HD, *args, out)
+        got = out.download(np.float32, (B, H * HD))
+        for b in range(0, B, 7):
+            kc = deq[b].transpose(1, 0, 2).reshape(n, HKV * HD)
+            vc = vdeq[b].transpose(1, 0, 2).reshape(n, HKV * HD)
+            assert rel_l2(got[b], oracle.attention(q[b], kc, vc, H, HKV, HD, n - 1, 0.125)) <= REL_L2, b
+    with pytest.raises(ts5hip.Ts5HipError):
+        ctx.attn_decode(ctx.to_device(np.zeros((B + 1, H * HD), np.float32)), B + 1, H, HKV, HD, *args,
+                        ctx.alloc((B + 1) * H * HD * 4))
+
+
 def test_attention_splits_agree(ctx):
     """Any split count gives the same softmax (merge of partials)."""
     rng = np.random.default_rng(5)

@@ -318,7 +318,7 @@ int ts5hip_attn_decode(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n
     if (B <= 0 || n_ctx <= 0 || !attn_supported(n_head, n_head_kv, head_dim))
         return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "attention for %d/%d heads of %d", n_head, n_head_kv, head_dim);
     if (B * n_head_kv > 4096) return fail(ctx, TS5HIP_ERR_ARG, "batch of %d x %d KV heads", B, n_head_kv);
-    if (n_split <= 0) n_split = attn_splits(B, n_head_kv);
+    if (n_split <= 0) n_split = attn_splits(B, n_head_kv, ctx->n_cu);
     if (n_split > 64) return fail(ctx, TS5HIP_ERR_ARG, "n_split %d (at most 64)", n_split);
     if (int rc = ensure_scratch(ctx, attn_partial_bytes(B, n_split, n_head, head_dim))) return rc;
     AttnIO io{};

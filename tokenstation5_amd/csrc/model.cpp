@@ -606,7 +606,7 @@ int ensure_batch(ts5hip_model *m) {
                 if (L.part[p].set) g(QR, E, L.part[p].type);
         }
         g(hp.n_vocab, E, out.type);
-        part = std::max(part, attn_partial_bytes(M, attn_splits(M, hp.n_head_kv, 512), hp.n_head, hp.head_dim));
+        part = std::max(part, attn_partial_bytes(M, attn_splits(M, hp.n_head_kv, m->ctx->n_cu), hp.n_head, hp.head_dim));
     }
     part = std::max(part, attn_prefill_partial_bytes(CHUNK, hp.n_head, hp.head_dim, m->n_ctx));
     int rc = 0;
@@ -675,7 +675,7 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
             AttnIO io{};
             io.q = m->bq, io.q_stride = AH, io.rope = 0, io.append = 0;
             io.kv = m->kv_layer(l), io.kv_per_batch = 0, io.n_ctx = m->n_ctx, io.n_keys = m->state;
-            io.B = nc, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = attn_splits(nc, HKV, 512);
+            io.B = nc, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = attn_splits(nc, HKV, ctx->n_cu);
             io.scale = hp.attn_scale, io.part = m->bpart, io.counters = m->bcounters, io.out = m->batt;
             TS5_HIP(ctx, launch_attn(io, s));
         }
@@ -769,7 +769,7 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
     m->kv_type = kv_type;
     m->layers.resize(hp->n_layer);
     m->has_bias.assign(hp->n_layer, false);
-    m->n_split = attn_splits(1, hp->n_head_kv, 256);
+    m->n_split = attn_splits(1, hp->n_head_kv, ctx->n_cu);
     const char *prof = std::getenv("TS5HIP_PROFILE");
     m->profile = prof && *prof && std::strcmp(prof, "0") != 0;
     const char *graphs = std::getenv("TS5HIP_GRAPHS");

@@ -151,7 +151,7 @@ def glu_roofline(ctx, hp, launches: int = 200):
         b.free()
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(achieved / HBM_PEAK_GBS, 4), traffic=GLU_TRAFFIC_BYTES,
-                kernel="k_mv<Q4K,2,4,MV_GLU> (ffn rmsnorm+gate+up+SiLU, 14336x4096 x2)", avg_us=round(avg_us, 2),
+                kernel="k_mv<Q4K,1,4,MV_GLU> (ffn rmsnorm+gate+up+SiLU, 14336x4096 x2)", avg_us=round(avg_us, 2),
                 algorithmic_bytes=int(algo))
 
 

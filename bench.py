@@ -36,11 +36,11 @@ from tokenstation5_amd import synth, ts5hip  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the roofline kernel, from rocprofv3 --pmc runs of
 # `bench.py --roofline-only` (profiles/glu_roofline_counters.md): FETCH_SIZE
-# 32,465.0 KiB and WRITE_SIZE 224 KiB per dispatch, scaled by what the same
+# 32,442.0 KiB and WRITE_SIZE 448 KiB per dispatch, scaled by what the same
 # counters read for the one-pass RMSNorm stream of 256 MiB in and 256 MiB out
-# (131,219.7 and 262,144 KiB: factors 1.9977 and 1.0). 1.007 x the algorithmic
+# (131,226.9 and 262,144 KiB: factors 1.9976 and 1.0). 1.010 x the algorithmic
 # bytes.
-GLU_TRAFFIC_BYTES = 66642864
+GLU_TRAFFIC_BYTES = 66821554
 PROMPT = 4096
 SEED = 20241201
 

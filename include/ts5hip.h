@@ -179,8 +179,8 @@ const float *ts5hip_logits_view(const ts5hip_model *m);
 /* Backend::n_ctx / kv_type (engine/src/backend.h:34-39). */
 int ts5hip_n_ctx(const ts5hip_model *m);
 int ts5hip_kv_type(const ts5hip_model *m);
-/* How single-token steps run once every tensor is set: 2 the whole-token persistent kernel,
- * 1 HIP graph replays, 0 direct kernel launches; < 0 an error. No counterpart in the
+/* How single-token steps run once every tensor is set: 1 HIP graph replays, 0 direct kernel
+ * launches (TS5HIP_GRAPHS=0 at model creation); < 0 an error. No counterpart in the
  * reference (its Vulkan backend has one path): for tests and profiles. */
 int ts5hip_token_path(ts5hip_model *m);
 /* Top-k of the last forward's logits row `row` on the GPU and the host draw (Engine::sample). */

@@ -27,11 +27,12 @@ def ctx():
     c.close()
 
 
-# The two token paths: the whole-token persistent kernel, and the same kernels
-# launched one per phase from a replayed HIP graph (TS5HIP_DECODE=0).
-@pytest.fixture(params=["persistent", "graphs"], autouse=True)
+# The two ways a single-token step runs: a replay of the token's captured HIP
+# graph, and the same kernels launched one by one (TS5HIP_GRAPHS=0, the form
+# profilers see).
+@pytest.fixture(params=["graphs", "direct"], autouse=True)
 def token_path(request, monkeypatch):
-    monkeypatch.setenv("TS5HIP_DECODE", "1" if request.param == "persistent" else "0")
+    monkeypatch.setenv("TS5HIP_GRAPHS", "1" if request.param == "graphs" else "0")
     return request.param
 
 
@@ -40,8 +41,8 @@ def load(ctx, name, n_ctx):
     tensors = synth.model_tensors(hp, make_golden.MODEL_SEED)
     m = ts5hip.Model(ctx, hp, n_ctx)
     m.set_tensors(tensors)
-    want = "persistent" if os.environ.get("TS5HIP_DECODE") == "1" else "graphs"
-    assert m.token_path() == want  # every test model fits the persistent kernel
+    want = "graphs" if os.environ.get("TS5HIP_GRAPHS") != "0" else "direct"
+    assert m.token_path() == want
     return hp, tensors, m
 
 

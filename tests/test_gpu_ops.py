@@ -270,7 +270,7 @@ def test_rope_kv_append(ctx, H, HKV, HD, neox, ntok, pos0):
 
 def q8_cache(rng, B, HKV, n_ctx, HD):
     """K/V ~ N(0,1) rounded by the q8 rule: (int8, f16 scale) and fp32 values."""
-    vals = rng.standard_normal((B, HKV, n_ctx, HD)).astype(np.float32)
+    vals = rng.standard_normal((B, HKV, n_ctx, HD), dtype=np.float32)
     blocks = vals.reshape(-1, 32)
     amax = np.abs(blocks).max(1)
     sc = (amax / np.float32(127)).astype(np.float16)
@@ -280,10 +280,13 @@ def q8_cache(rng, B, HKV, n_ctx, HD):
     return q.reshape(vals.shape), sc.reshape(B, HKV, n_ctx, HD // 32), deq
 
 
-@pytest.mark.parametrize("B,ctxlen,H,HKV,HD", [(1, 8192, 32, 8, 128), (4, 8192, 32, 8, 128), (1, 1000, 32, 8, 128),
-                                               (2, 33, 14, 2, 64), (3, 1, 32, 8, 128), (4, 32768, 32, 8, 128)])
+@pytest.mark.parametrize("B,ctxlen,H,HKV,HD", [(1, 8192, 32, 8, 128), (4, 8192, 32, 8, 128), (16, 8192, 32, 8, 128),
+                                               (1, 32768, 32, 8, 128), (4, 32768, 32, 8, 128),
+                                               (16, 32768, 32, 8, 128), (1, 1000, 32, 8, 128),
+                                               (2, 33, 14, 2, 64), (3, 1, 32, 8, 128)])
 def test_attention_vs_oracle(ctx, B, ctxlen, H, HKV, HD):
-    """cfg3: one query per sequence over its q8 cache, full context, scale 1/sqrt(HD)."""
+    """cfg3: one query per sequence over its q8 cache, full context, scale 1/sqrt(HD);
+    every cfg3 shape (B 1, 4, 16 x 8192, 32768 keys) with the default split count."""
     rng = np.random.default_rng(B * 7 + ctxlen)
     q8, sc, deq = q8_cache(rng, B, HKV, ctxlen, HD)
     v8, vsc, vdeq = q8_cache(rng, B, HKV, ctxlen, HD)
@@ -302,11 +305,12 @@ def test_attention_vs_oracle(ctx, B, ctxlen, H, HKV, HD):
 
 
 def test_attention_most_work_items_twice(ctx):
-    """B * HKV = 4096 (the per-op entry point's limit): every (query, KV head)
-    merge counter in use, run twice (the counters must be back at zero), and
-    one more query refused."""
+    """B * HKV = 4096 (the per-op entry point's limit) with 8 key splits each:
+    every (query, KV head) merge counter counts 8 workgroups and its last one
+    merges, 32768 workgroups in all; run twice (the counters must be back at
+    zero), and one more query refused."""
     rng = np.random.default_rng(11)
-    B, H, HKV, HD, n = 512, 32, 8, 64, 40
+    B, H, HKV, HD, n = 512, 32, 8, 64, 200
     q8, sc, deq = q8_cache(rng, B, HKV, n, HD)
     v8, vsc, vdeq = q8_cache(rng, B, HKV, n, HD)
     q = rng.standard_normal((B, H * HD)).astype(np.float32)
@@ -315,7 +319,7 @@ def test_attention_most_work_items_twice(ctx):
     dq = ctx.to_device(q)
     for _ in range(2):
         out = ctx.alloc(q.nbytes)
-        ctx.attn_decode(dq, B, H, HKV, HD, *args, out)
+        ctx.attn_decode(dq, B, H, HKV, HD, *args, out, n_split=8)
         got = out.download(np.float32, (B, H * HD))
         for b in range(0, B, 7):
             kc = deq[b].transpose(1, 0, 2).reshape(n, HKV * HD)
@@ -342,6 +346,29 @@ def test_attention_splits_agree(ctx):
         outs.append(out.download(np.float32))
     for o in outs[1:]:
         assert rel_l2(o, outs[0]) < 1e-5
+
+
+@pytest.mark.parametrize("n_split", [0, 32])
+def test_attention_verify_batch(ctx, n_split):
+    """The verify batch of speculative decoding: 5 consecutive queries of one
+    cache at ~4.3k keys (the default split count, then 32 splits: 40 KV-head
+    merges each with many concurrent mergers), against the oracle."""
+    rng = np.random.default_rng(12 + n_split)
+    H, HKV, HD, n_ctx, p0, B = 32, 8, 128, 4400, 4300, 5
+    q8, sc, deq = q8_cache(rng, 1, HKV, n_ctx, HD)
+    v8, vsc, vdeq = q8_cache(rng, 1, HKV, n_ctx, HD)
+    q = rng.standard_normal((B, H * HD)).astype(np.float32)
+    scale = float(np.float32(1) / np.sqrt(np.float32(HD)))
+    out = ctx.alloc(q.nbytes)
+    ctx.attn_decode(ctx.to_device(q), B, H, HKV, HD, ctx.to_device(q8), ctx.to_device(sc), ctx.to_device(v8),
+                    ctx.to_device(vsc), n_ctx, ctx.to_device(np.array([p0], np.int32)), 0, scale, out,
+                    n_split=n_split)
+    got = out.download(np.float32, (B, H * HD))
+    kc = deq[0].transpose(1, 0, 2).reshape(n_ctx, HKV * HD)
+    vc = vdeq[0].transpose(1, 0, 2).reshape(n_ctx, HKV * HD)
+    for b in range(B):
+        want = oracle.attention(q[b], kc, vc, H, HKV, HD, p0 + b, scale)
+        assert rel_l2(got[b], want) <= REL_L2, (b, rel_l2(got[b], want))
 
 
 def test_attention_causal_batch(ctx):

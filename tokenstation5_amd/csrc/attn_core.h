@@ -46,7 +46,7 @@ struct AttnArgs {
     int kv_per_batch, n_ctx, H, HKV;
     const int32_t *n_keys;
     float scale;
-    float *part;    // [B][n_split][H][HD + 2]
+    float *part;    // [B][n_split][HKV] groups of G records [HD + 2], attn_group_floats(G, HD) floats apart
     int *counters;  // [B * HKV] at CTR_STRIDE ints apart, zero between launches
     float *out;     // [B][H * HD]
 };
@@ -61,20 +61,6 @@ __device__ inline void rope_inplace(float *v, int n_rot, int neox, const float2 
 
 constexpr int ATTN_MAX_SPLIT = 64;
 constexpr int ATTN_TILE = 64;
-
-template <int HD, int G>
-struct AttnLds {
-    float q_s[G][HD];
-    float p_s[G][ATTN_TILE];
-    float alpha_s[G], m_s[G], l_s[G], red[G];
-    float kv_s[2][HD];                         // the new token's K and V before rounding
-    __align__(16) int8_t new8[2][HD];          // ... and after, as int8
-    uint16_t new_sc[2][HD / 32];               // ... with their f16 scales
-    __align__(16) int8_t vt[ATTN_TILE][HD];    // the tile's V rows
-    uint16_t vsc[ATTN_TILE][HD / 32];          // ... and their scales
-    float mw[ATTN_MAX_SPLIT][G], lw[ATTN_MAX_SPLIT][G];  // the merge's (m, l), then weights
-    int last;
-};
 
 // K bytes per lane of a key's score: NQ = HD / (NT / 64) lanes' worth.
 template <int NQ>
@@ -121,11 +107,6 @@ __device__ inline AttnSpan attn_span(const AttnArgs &a, int split, int kvh, int 
     sp.has_new = a.append && sp.pq >= sp.p0 && sp.pq < sp.p1;
     return sp;
 }
-
-template <int HD, int G, int NT>
-struct AttnShape {
-    static constexpr int NPAIR = G * HD / 2, PPT = (NPAIR + NT - 1) / NT;
-};
 
 // 1. The G query heads of KV head kvh (and, when the slice holds the new key,
 //    that token's K and V) into LDS, from q(e) = element e of the token's
@@ -207,196 +188,6 @@ __device__ inline void attn_prepare(const AttnArgs &a, int kvh, const AttnSpan &
         }
     }
     __syncthreads();
-}
-
-// 2. Tiles of 64 keys over [p0, p1): the tile's K (to registers, NT/64 lanes
-//    per key) and V (to registers, then LDS) are requested together; scores;
-//    online softmax per head; o = o * alpha + sum_k p_k v_k from LDS. The new
-//    key comes from LDS, never from the cache it was just written to. o holds
-//    this thread's (head, dim pair) entries of the unnormalised output.
-template <int HD, int G, int NT>
-__device__ inline void attn_tiles(const AttnArgs &a, const AttnSpan &sp, AttnLds<HD, G> &S,
-                                  float (&o)[AttnShape<HD, G, NT>::PPT][2]) {
-    constexpr int TILE = ATTN_TILE, NWV = NT / 64, LPK = NT / TILE, NQ = HD / LPK;
-    constexpr int NPAIR = G * HD / 2, PPT = AttnShape<HD, G, NT>::PPT;
-    constexpr int VP = TILE * HD / 16, VPT = (VP + NT - 1) / NT;  // 16-byte V pieces per tile, per thread
-    constexpr int NSC = TILE * (HD / 32);                          // V scales per tile
-    static_assert(NT % 64 == 0 && NQ % 8 == 0, "attention tile shape");
-    auto &q_s = S.q_s;
-    auto &p_s = S.p_s;
-    auto &new8 = S.new8;
-    auto &new_sc = S.new_sc;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int pq = sp.pq, p0 = sp.p0, p1 = sp.p1;
-    const int64_t head_base = sp.head_base;
-    const bool has_new = sp.has_new;
-#pragma unroll
-    for (int k = 0; k < PPT; k++) o[k][0] = o[k][1] = 0.f;
-    for (int t0 = p0; t0 < p1; t0 += TILE) {
-        const int nt = min(TILE, p1 - t0);
-        const int kk = tid / LPK, qq = tid % LPK, p = t0 + kk;
-        const bool kin = kk < nt, kmine = has_new && p == pq;
-        KRow<NQ> kr;
-        float ks = 0.f;
-        if (kin && !kmine) {
-            kr = load_krow<NQ>(a.kv.k + (head_base + p) * HD + qq * NQ);
-            ks = h2f(a.kv.ks[(head_base + p) * (HD / 32) + (qq * NQ) / 32]);
-        }
-        uint4 vr[VPT];
-#pragma unroll
-        for (int k = 0; k < VPT; k++) {
-            const int pc = tid + NT * k, key = pc / (HD / 16);
-            if (pc < VP && key < nt) vr[k] = *(const uint4 *)(a.kv.v + (head_base + t0 + key) * HD + 16 * (pc % (HD / 16)));
-        }
-        uint16_t vs[(NSC + NT - 1) / NT];
-#pragma unroll
-        for (int k = 0; k < (NSC + NT - 1) / NT; k++) {
-            const int j = tid + NT * k;
-            if (j < NSC && j / (HD / 32) < nt) vs[k] = a.kv.vs[(head_base + t0) * (HD / 32) + j];
-        }
-        {   // Scores.
-            float acc[G];
-#pragma unroll
-            for (int g = 0; g < G; g++) acc[g] = 0.f;
-            if (kin) {
-                if (kmine) {
-#pragma unroll
-                    for (int c = 0; c < NQ / 4; c++) kr.w[c] = *(const uint32_t *)(new8[0] + qq * NQ + 4 * c);
-                    ks = h2f(new_sc[0][(qq * NQ) / 32]);
-                }
-#pragma unroll
-                for (int e = 0; e < NQ; e++) {
-                    const float kf = (float)(int8_t)((kr.w[e >> 2] >> (8 * (e & 3))) & 0xff) * ks;
-                    const int d = qq * NQ + e;
-#pragma unroll
-                    for (int g = 0; g < G; g++) acc[g] += q_s[g][d] * kf;
-                }
-            }
-#pragma unroll
-            for (int g = 0; g < G; g++)
-#pragma unroll
-                for (int o2 = 1; o2 < LPK; o2 <<= 1) acc[g] += __shfl_xor(acc[g], o2, WAVE);
-            if (qq == 0) {
-#pragma unroll
-                for (int g = 0; g < G; g++) p_s[g][kk] = kin ? acc[g] * a.scale : -INFINITY;
-            }
-        }
-        // The tile's V rows into LDS (the new key's from its rounded copy).
-#pragma unroll
-        for (int k = 0; k < VPT; k++) {
-            const int pc = tid + NT * k, key = pc / (HD / 16), off = 16 * (pc % (HD / 16));
-            if (pc < VP && key < nt)
-                *(uint4 *)(&S.vt[key][off]) =
-                    (has_new && t0 + key == pq) ? *(const uint4 *)(new8[1] + off) : vr[k];
-        }
-#pragma unroll
-        for (int k = 0; k < (NSC + NT - 1) / NT; k++) {
-            const int j = tid + NT * k, key = j / (HD / 32);
-            if (j < NSC && key < nt) S.vsc[key][j % (HD / 32)] = (has_new && t0 + key == pq) ? new_sc[1][j % (HD / 32)] : vs[k];
-        }
-        __syncthreads();
-        // Online softmax per head: wave w takes heads w, w + NT/64, ...
-        for (int g = wave; g < G; g += NWV) {
-            const float sv = p_s[g][lane];
-            const float mt = wave_max(sv);
-            const float mo = S.m_s[g];
-            const float mn = fmaxf(mo, mt);
-            const float pe = sv == -INFINITY ? 0.f : expf(sv - mn);
-            const float ls = wave_sum(pe);
-            p_s[g][lane] = pe;
-            if (lane == 0) {
-                const float al = mo == -INFINITY ? 0.f : expf(mo - mn);
-                S.alpha_s[g] = al;
-                S.m_s[g] = mn;
-                S.l_s[g] = S.l_s[g] * al + ls;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < PPT; k++) {
-            const int pp = tid + NT * k;
-            if (pp < NPAIR) {
-                const int g = (2 * pp) / HD, d = (2 * pp) % HD;
-                const float al = S.alpha_s[g];
-                float o0 = o[k][0] * al, o1 = o[k][1] * al;
-                for (int j = 0; j < nt; j++) {
-                    const uint16_t v2 = *(const uint16_t *)(&S.vt[j][d]);
-                    const float w = p_s[g][j] * h2f(S.vsc[j][d / 32]);
-                    o0 += w * (float)(int8_t)(v2 & 0xff);
-                    o1 += w * (float)(int8_t)(v2 >> 8);
-                }
-                o[k][0] = o0;
-                o[k][1] = o1;
-            }
-        }
-        __syncthreads();
-    }
-
-}
-
-// One work item (split, KV head kvh, query b) of n_split; NT threads.
-template <int HD, int G, int NT>
-__device__ inline void attn_item(const AttnArgs &a, int split, int kvh, int b, int n_split, AttnLds<HD, G> &S) {
-    constexpr int NPAIR = G * HD / 2, PPT = AttnShape<HD, G, NT>::PPT;
-    const int tid = threadIdx.x;
-    const AttnSpan sp = attn_span(a, split, kvh, b, n_split);
-    const float *row = a.q + (int64_t)b * a.q_stride;
-    attn_prepare<HD, G, NT>(a, kvh, sp, S, [&](int64_t e) { return row[e]; });
-    float o[PPT][2];
-    attn_tiles<HD, G, NT>(a, sp, S, o);
-
-    // 3. Partial record per head: [HD values][m][l]; the last workgroup merges.
-    const int64_t rec = HD + 2;
-    float *pb = a.part + (((int64_t)b * n_split + split) * a.H + (int64_t)kvh * G) * rec;
-#pragma unroll
-    for (int k = 0; k < PPT; k++) {
-        const int pp = tid + NT * k;
-        if (pp < NPAIR) {
-            const int g = (2 * pp) / HD, d = (2 * pp) % HD;
-            st_dev(pb + g * rec + d, o[k][0]);
-            st_dev(pb + g * rec + d + 1, o[k][1]);
-        }
-    }
-    if (tid < G) {
-        st_dev(pb + tid * rec + HD, S.m_s[tid]);
-        st_dev(pb + tid * rec + HD + 1, S.l_s[tid]);
-    }
-    wait_stores();
-    __syncthreads();
-    if (tid == 0) S.last = atomicAdd(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 1) == n_split - 1;
-    __syncthreads();
-    if (!S.last) return;
-    const float *p_all = a.part + ((int64_t)b * n_split * a.H + (int64_t)kvh * G) * rec;
-    const int64_t sstride = (int64_t)a.H * rec;
-    // Every split's (m, l) in one round of loads, then the weights e^(m_s - M).
-    for (int j = tid; j < n_split * G; j += NT) {
-        const int sp = j / G, g = j % G;
-        S.mw[sp][g] = p_all[sp * sstride + g * rec + HD];
-        S.lw[sp][g] = p_all[sp * sstride + g * rec + HD + 1];
-    }
-    __syncthreads();
-    if (tid < G) {
-        float M = -INFINITY;
-        for (int sp = 0; sp < n_split; sp++) M = fmaxf(M, S.mw[sp][tid]);
-        float L = 0.f;
-        for (int sp = 0; sp < n_split; sp++) {
-            const float m = S.mw[sp][tid];
-            const float w = m == -INFINITY ? 0.f : expf(m - M);
-            S.mw[sp][tid] = w;
-            L += w * S.lw[sp][tid];
-        }
-        S.red[tid] = L;
-    }
-    __syncthreads();
-    for (int j = tid; j < G * HD; j += NT) {
-        const int g = j / HD, d = j % HD;
-        const float *pd = p_all + g * rec + d;
-        float acc = 0.f;
-#pragma unroll 8
-        for (int sp = 0; sp < n_split; sp++) acc += S.mw[sp][g] * pd[sp * sstride];
-        st_dev(a.out + (int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d, acc / S.red[g]);
-    }
-    if (tid == 0) st_dev(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 0);  // ready for the next use
 }
 
 // ---------------------------------------------------------------------------
@@ -593,8 +384,8 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
     }
     __syncthreads();
 
-    const int64_t rec = HD + 2;
-    float *pb = a.part + (((int64_t)b * n_split + split) * a.H + (int64_t)kvh * G) * rec;
+    constexpr int64_t rec = HD + 2, grp = attn_group_floats(G, HD);
+    float *pb = a.part + (((int64_t)b * n_split + split) * a.HKV + kvh) * grp;
     for (int j = tid; j < G * HD; j += NT) {
         const int g = j / HD, d = j % HD;
         float v = 0.f;
@@ -614,8 +405,8 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
     // The merge: this thread's outputs of every split (up to 32 at a time)
     // and every split's (m, l) are requested together; a wave per head turns
     // the (m, l) into weights, a lane per split.
-    const float *p_all = a.part + ((int64_t)b * n_split * a.H + (int64_t)kvh * G) * rec;
-    const int64_t sstride = (int64_t)a.H * rec;
+    const float *p_all = a.part + ((int64_t)b * n_split * a.HKV + kvh) * grp;
+    const int64_t sstride = (int64_t)a.HKV * grp;
     constexpr int OPT = (G * HD + NT - 1) / NT, MC = 32;
     float acc[OPT];
 #pragma unroll
@@ -627,13 +418,13 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
         for (int k = 0; k < OPT; k++) {
             const int j = min(tid + NT * k, G * HD - 1), g = j / HD, d = j % HD;
 #pragma unroll
-            for (int i = 0; i < MC; i++) ov[k][i] = p_all[(int64_t)(s0 + min(i, nc - 1)) * sstride + g * rec + d];
+            for (int i = 0; i < MC; i++) ov[k][i] = ld_dev(p_all + (int64_t)(s0 + min(i, nc - 1)) * sstride + g * rec + d);
         }
         if (s0 == 0) {
             for (int g = wave; g < G; g += NT / 64) {
                 const int sl = min(lane, n_split - 1);
-                const float m0 = p_all[(int64_t)sl * sstride + g * rec + HD];
-                const float l0 = p_all[(int64_t)sl * sstride + g * rec + HD + 1];
+                const float m0 = ld_dev(p_all + (int64_t)sl * sstride + g * rec + HD);
+                const float l0 = ld_dev(p_all + (int64_t)sl * sstride + g * rec + HD + 1);
                 const float m = lane < n_split ? m0 : -INFINITY;
                 const float M = wave_max_dpp(m);
                 const float w = m == -INFINITY ? 0.f : expf(m - M);

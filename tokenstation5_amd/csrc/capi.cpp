@@ -320,7 +320,7 @@ int ts5hip_attn_decode(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n
     if (B * n_head_kv > 4096) return fail(ctx, TS5HIP_ERR_ARG, "batch of %d x %d KV heads", B, n_head_kv);
     if (n_split <= 0) n_split = attn_splits(B, n_head_kv, ctx->n_cu);
     if (n_split > 64) return fail(ctx, TS5HIP_ERR_ARG, "n_split %d (at most 64)", n_split);
-    if (int rc = ensure_scratch(ctx, attn_partial_bytes(B, n_split, n_head, head_dim))) return rc;
+    if (int rc = ensure_scratch(ctx, attn_partial_bytes(B, n_split, n_head, n_head_kv, head_dim))) return rc;
     AttnIO io{};
     io.q = q, io.q_stride = (int64_t)n_head * head_dim, io.rope = 0, io.append = 0;
     io.kv = KvLayer{(int8_t *)k8, (uint16_t *)ks, (int8_t *)v8, (uint16_t *)vs};

@@ -126,6 +126,14 @@ __host__ __device__ inline CAct cact_view(const void *base, int64_t n) {
     return CAct{a.hi, a.lo, a.scale, a.sum, a.isum};
 }
 
+// Split-K decode attention partials: per (query, key split, KV head) a group
+// of G records [HD values, m, l], padded to whole 128-byte lines so that no
+// line holds records of two groups (each group is handed to its merging
+// workgroup on its own).
+__host__ __device__ constexpr inline size_t attn_group_floats(int G, int HD) {
+    return align_up((size_t)G * (HD + 2), 32);
+}
+
 #if defined(__HIPCC__)
 // ---------------------------------------------------------------------------
 // Device helpers.
@@ -149,11 +157,19 @@ __device__ inline int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(
 // device-coherent (global_store ... sc1, written through past this XCD's L2);
 // the writer waits for its stores (s_waitcnt vmcnt(0): __syncthreads does not
 // on gfx950) before signalling, with a relaxed atomic, that they are done.
-// Readers use ordinary cached loads of addresses that were not read earlier in
-// the same kernel, so no stale copy can sit in their L1/L2. None of this needs
-// buffer_wbl2 / buffer_inv, which __threadfence() would emit.
+// The reader loads them device-coherent too (ld_dev). Each XCD has its own L2,
+// and the L2s are not coherent with one another: an ordinary load that reads
+// part of a 128-byte line could leave a copy of the whole line in this XCD's
+// L2, and a later ordinary load of another part of it, written since by a
+// workgroup on another XCD, would hit that stale copy. Buffers handed over
+// this way are also laid out so that no 128-byte line holds data of two
+// different hand-offs. None of this needs buffer_wbl2 / buffer_inv, which
+// __threadfence() would emit.
 __device__ inline void st_dev(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ inline void st_dev(int *p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ inline float ld_dev(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ inline void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
 template <typename T>

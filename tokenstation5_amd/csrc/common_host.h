@@ -57,8 +57,8 @@ inline int attn_splits(int B, int n_head_kv, int slots) {
     const int s = slots / (B * n_head_kv);
     return s < 1 ? 1 : (s > 64 ? 64 : s);  // at most 64 (the merge's table)
 }
-inline size_t attn_partial_bytes(int B, int n_split, int H, int HD) {
-    return (size_t)B * n_split * H * (HD + 2) * sizeof(float);
+inline size_t attn_partial_bytes(int B, int n_split, int H, int HKV, int HD) {
+    return (size_t)B * n_split * HKV * attn_group_floats(H / HKV, HD) * sizeof(float);
 }
 
 // The draw of Engine::sample (engine/src/engine.cpp:34-45) from k candidates

@@ -577,14 +577,20 @@ static hipError_t launch_gemm_reduce(const float *part, int ks, int M, int nrows
 }
 
 // ---------------------------------------------------------------------------
+// Past 16 tokens Q4_K rows take the fp16 prompt matmul (launch_gemm_wide), so
+// k_gemm is built for Q6_K and Q8_0 only.
 template <int FMT, int MODE>
 static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
-    if (a.M <= 16) hipLaunchKernelGGL((k_gemm_small<FMT, MODE>), dim3((a.nrows + 15) / 16), dim3(256), 0, s, a);
-    else if constexpr (FMT != F_Q6K) {
+    if (a.M <= 16) {
+        hipLaunchKernelGGL((k_gemm_small<FMT, MODE>), dim3((a.nrows + 15) / 16), dim3(256), 0, s, a);
+    } else if constexpr (FMT == F_Q80) {
         if (tn == 4) hipLaunchKernelGGL((k_gemm<FMT, MODE, 4>), grid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((k_gemm<FMT, MODE, 1>), grid, dim3(256), 0, s, a);
+    } else if constexpr (FMT == F_Q6K) {
+        hipLaunchKernelGGL((k_gemm<FMT, MODE, 1>), grid, dim3(256), 0, s, a);
+    } else {
+        return hipErrorInvalidValue;
     }
-    else hipLaunchKernelGGL((k_gemm<FMT, MODE, 1>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -598,9 +604,9 @@ static hipError_t gemm_fmt(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) 
     return hipErrorInvalidValue;
 }
 
-// Token groups of 16 per wave: 4 for batches past 16 tokens (Q6_K rows keep
-// 1: its 4-group kernel does not fit the register file).
-static int gemm_tn(uint32_t t, int M) { return M > 16 && t != T_Q6_K ? 4 : 1; }
+// Token groups of 16 per wave: 4 for Q8_0 batches past 16 tokens (Q6_K rows
+// keep 1: its 4-group kernel does not fit the register file).
+static int gemm_tn(uint32_t t, int M) { return M > 16 && t == T_Q8_0 ? 4 : 1; }
 
 static int g_gemm_cu = 256;
 void set_gemm_cu_count(int n) { g_gemm_cu = n > 0 ? n : 256; }

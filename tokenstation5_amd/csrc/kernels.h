@@ -97,7 +97,7 @@ struct AttnIO {
     const int32_t *n_keys;
     int B, H, HKV, HD, n_split;
     float scale;
-    float *part;    // B * n_split * H * (HD + 2) floats
+    float *part;    // attn_partial_bytes(B, n_split, H, HKV, HD), 128-byte aligned
     int *counters;  // B * HKV * CTR_STRIDE ints, zero before the first launch (kept zero after)
     float *out;     // [B][H * HD]
 };
@@ -109,48 +109,6 @@ bool attn_prefill_supported(int H, int HKV, int HD);
 size_t attn_prefill_partial_bytes(int nq, int H, int HD, int64_t max_keys);
 hipError_t launch_attn_prefill(const float *q, int64_t q_stride, KvLayer kv, int n_ctx, int H, int HKV, int HD, int p0,
                                int nq, float scale, float *part, float *out, hipStream_t s);
-// decode.hip: one token as one persistent kernel (cooperative launch) that
-// streams the weights through LDS and hands values between workgroups as
-// tagged 64-bit words (value bits, launch tag).
-enum { DPH_MV = 0, DPH_ADD = 1, DPH_GLU = 2, DPH_LOGITS = 3, DPH_ARGMAX = 4, DPH_ATTN = 5 };
-struct DecodePhaseIn {
-    int kind;
-    uint32_t t;  // weight type (matrix phases)
-    int ne0, nrows;
-    const void *w, *w2;        // GLU: gate, up
-    const void *x;             // tagged input words
-    const float *norm_w;       // fused rmsnorm, or null
-    void *y;                   // tagged output words
-    const void *y_in;          // ADD: tagged residual words
-    float *logits;             // LOGITS: plain fp32
-    KvLayer kv;                // ATTN: the layer's cache
-    const float *bias, *q_norm, *k_norm;
-    void *part;                // ATTN: n_split * H * (HD + 2) tagged words
-};
-struct DecodeIn {
-    int E, H, HKV, HD, V, n_ctx, n_rot, neox, n_split, max_in;
-    float eps, scale;
-    const void *phases;  // device array of fill_decode_phase records
-    int n_phases;
-    uint32_t t_embd;
-    const void *embd;
-    const float *rope;
-    void *x0;              // tagged embedding output (the first phase's input)
-    int32_t *seq, *state;  // state[0] position, state[1] greedy id
-    int head_mode;         // 0: no head phase, 1: logits, 2: logits + greedy argmax into seq[p + 1]
-    void *best;            // 2 * grid tagged words
-    void *sync;            // decode_sync_bytes(), zeroed with the arena
-    int grid;
-    size_t lds_bytes;
-    uint64_t *trace;  // optional: grid * (n_phases + 2) * 4 timestamps
-};
-size_t decode_phase_bytes();
-size_t decode_sync_bytes();
-size_t decode_lds_bytes(int HD, int G, int max_in);
-int decode_grid(int HD, int G, int n_cu, size_t lds_bytes);
-int fill_decode_phase(void *dst_host, const DecodePhaseIn &in, int grid);  // 0, or -1: not streamable
-hipError_t launch_decode(const DecodeIn &in, hipStream_t s);
-
 hipError_t launch_kv_read(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, float *out, hipStream_t s);
 
 // sample.hip

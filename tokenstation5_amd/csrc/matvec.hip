@@ -90,15 +90,6 @@ __global__ __launch_bounds__(WAVES *WAVE) void k_mv(const void *w, const void *w
     }
 }
 
-// Q4_K plain / accumulate / gate-up matvecs through the per-wave LDS ring
-// (mv_run_dma): one workgroup of 4 waves per CU.
-template <class F, int R, int MODE, int NS, int WAVES>
-__global__ __launch_bounds__(WAVES *WAVE) void k_mv_ring(MvArgs a) {
-    extern __shared__ __align__(1024) uint8_t lds[];
-    __shared__ float red[WAVES];
-    mv_run_dma<F, R, MODE, NS, WAVES>(a, lds, red);
-}
-
 // ---------------------------------------------------------------------------
 // Launch shapes. Rows per group = R * WAVES; the grid is capped at two
 // workgroups per CU, so large matrices loop over their groups with the next
@@ -150,39 +141,8 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Off by default: on the 8B decode shapes the ring kernel measured 5% slower
-// than k_mv (fused gate/up 20.4 us against 19.4 us), with twice k_mv's DRAM
-// credit stalls at the same bytes. Build with -DTS5_MV_RING=1 to use it.
-#ifndef TS5_MV_RING
-#define TS5_MV_RING 0
-#endif
-#ifndef TS5_RING_GLU_R
-#define TS5_RING_GLU_R 2
-#endif
-#ifndef TS5_RING_GLU_WAVES
-#define TS5_RING_GLU_WAVES 4
-#endif
-// The ring kernel when its LDS fits (160 KB per workgroup), else false.
-template <class F, int R, int MODE, int NS, int WAVES = 4>
-static bool mv_ring_go(const MvArgs &a, hipStream_t s, hipError_t &e) {
-    const size_t lds = MvRing<F, R, MODE, NS, WAVES>::lds_bytes(a.n_in);
-    if (!TS5_MV_RING || lds > 160 * 1024) return false;
-    const int64_t ngroups = (a.nrows + WAVES * R - 1) / (WAVES * R);
-    const unsigned grid = (unsigned)std::min<int64_t>(ngroups, g_n_cu);
-    hipLaunchKernelGGL((k_mv_ring<F, R, MODE, NS, WAVES>), dim3(grid), dim3(WAVES * WAVE), lds, s, a);
-    e = hipGetLastError();
-    return true;
-}
-
 template <int MODE>
 static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
-    if constexpr (MODE != MV_ARGMAX) {
-        hipError_t e = hipSuccess;
-        if (a.t == T_Q4_K &&
-            (MODE == MV_GLU ? mv_ring_go<Q4K, TS5_RING_GLU_R, MODE, 3, TS5_RING_GLU_WAVES>(a, s, e)
-                            : mv_ring_go<Q4K, 2, MODE, 4>(a, s, e)))
-            return e;
-    }
     switch (a.t) {
     case T_Q4_K:
         return MODE == MV_GLU ? mv_go<Q4K, TS5_MV_GLU_R, TS5_MV_GLU_WAVES, MODE>(a, s)

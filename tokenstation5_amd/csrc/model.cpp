@@ -74,27 +74,6 @@ struct ts5hip_model {
     hipGraphExec_t graph[N_GRAPHS] = {nullptr, nullptr, nullptr};
     bool graphs_stale = true;
     bool use_graphs = true;  // TS5HIP_GRAPHS=0: launch each token's kernels directly (profilers)
-    // The whole-token persistent kernel (decode.hip), used for single-token
-    // steps with TS5HIP_DECODE=1 when every tensor fits it (the graph replay
-    // is faster on the 8B for now).
-    bool want_decode = true, use_decode = false;
-    int dec_grid = 0, dec_split = 32, dec_nph = 0, dec_max_in = 0;
-    size_t dec_lds = 0;
-    void *dec_phases = nullptr;  // the token program: 5 phases per layer, then the head
-    void *dec_sync = nullptr;    // error flag and launch count
-    uint64_t *arena = nullptr;   // the persistent kernel's per-phase buffers (tagged words)
-    uint64_t *dec_best = nullptr;
-    int64_t a_sx = 0, a_sqkv = 0, a_satt = 0, a_sffn = 0, a_spart = 0;
-    uint64_t *trace = nullptr;  // per-workgroup phase timestamps (profile mode)
-    std::vector<uint64_t> trace_host;
-    // Per phase kind (embed qkv attn wo glu down head), summed over tokens:
-    // span (last done - previous last done), hand-off (first input ready -
-    // previous last done), ready spread, tail (last done - last ready), and
-    // mean work per workgroup (done - ready).
-    double ph_span[7] = {0}, ph_hand[7] = {0}, ph_spread[7] = {0}, ph_tail[7] = {0}, ph_work[7] = {0};
-    double ph_wait[7] = {0};  // ... of which waiting for weight slots
-    int ph_count[7] = {0};
-    int phase_tokens = 0;
     // Several tokens per call (prompt chunks, speculative verification): the
     // chunk's activations [CHUNK][...], its quantized activations, the
     // matmul's split-K partials, attention partials and merge counters.
@@ -386,150 +365,9 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
     return TS5HIP_OK;
 }
 
-// Sets up the persistent whole-token kernel when every tensor fits it: the
-// token program (one record per phase), the arena of tagged words every
-// phase writes, and the kernel's LDS and grid.
-int prepare_decode(ts5hip_model *m) {
-    m->use_decode = false;
-    if (!m->want_decode) return TS5HIP_OK;
-    const ts5hip_hparams &hp = m->hp;
-    const DevT &out = m->output.set ? m->output : m->tok_embd;
-    const int E = hp.n_embd, F = hp.n_ff, AH = hp.n_head * hp.head_dim, L = hp.n_layer;
-    const int max_in = std::max({E, F, AH});
-    const size_t lds = decode_lds_bytes(hp.head_dim, hp.n_head / hp.n_head_kv, max_in);
-    if (!lds) return TS5HIP_OK;
-    const int grid = decode_grid(hp.head_dim, hp.n_head / hp.n_head_kv, m->ctx->n_cu, lds);
-    if (grid < 1) return TS5HIP_OK;
-    for (int l = 0; l < L; l++) {
-        const LayerDev &Ld = m->layers[l];
-        if (!(Ld.in_qkv[0] && Ld.in_qkv[1] && Ld.in_qkv[2]) || Ld.gate.type != Ld.up.type) return TS5HIP_OK;
-    }
-    const int split = std::min(64, std::max(1, grid / hp.n_head_kv));  // one item per workgroup, at most 64 splits
-    auto row = [](int64_t n) { return (int64_t)align_up((size_t)n, 32); };  // 256-byte rows of 8-byte words
-    const int64_t sx = row(E), sqkv = row(m->qkv_rows()), satt = row(AH), sffn = row(F);
-    const int64_t spart = row((int64_t)split * hp.n_head * (hp.head_dim + 2));
-    if (m->arena && (sx != m->a_sx || sqkv != m->a_sqkv || satt != m->a_satt || sffn != m->a_sffn ||
-                     spart != m->a_spart))
-        return fail(m->ctx, TS5HIP_ERR_STATE, "decode arena shape changed");
-    if (!m->arena) {
-        m->a_sx = sx, m->a_sqkv = sqkv, m->a_satt = satt, m->a_sffn = sffn, m->a_spart = spart;
-        const size_t n = (size_t)((2 * L + 1) * sx + L * (sqkv + satt + sffn + spart));
-        if (int rc = alloc_t(m, n, &m->arena)) return rc;
-        if (int rc = alloc(m, decode_sync_bytes(), &m->dec_sync)) return rc;
-        if (int rc = alloc_t(m, 2 * (size_t)grid, &m->dec_best)) return rc;
-        TS5_HIP(m->ctx, hipMemsetAsync(m->arena, 0, n * 8, m->ctx->stream));
-        TS5_HIP(m->ctx, hipMemsetAsync(m->dec_sync, 0, decode_sync_bytes(), m->ctx->stream));
-        TS5_HIP(m->ctx, hipMemsetAsync(m->dec_best, 0, 2 * (size_t)grid * 8, m->ctx->stream));
-    }
-    uint64_t *X = m->arena, *QKV = X + (2 * L + 1) * sx, *ATT = QKV + L * sqkv, *FFN = ATT + L * satt;
-    uint64_t *PART = FFN + L * sffn;
-    const int nph = 5 * L + 1;
-    const size_t rec = decode_phase_bytes();
-    std::vector<uint8_t> host((size_t)nph * rec);
-    int k = 0;
-    auto add = [&](const DecodePhaseIn &in) { return fill_decode_phase(host.data() + (size_t)k++ * rec, in, grid); };
-    for (int l = 0; l < L; l++) {
-        const LayerDev &Ld = m->layers[l];
-        uint64_t *x0 = X + 2 * l * sx, *x1 = x0 + sx, *x2 = x1 + sx;
-        DecodePhaseIn q{};
-        q.kind = DPH_MV, q.t = Ld.qkv.type, q.ne0 = E, q.nrows = m->qkv_rows(), q.w = Ld.qkv.d, q.x = x0;
-        q.norm_w = (const float *)Ld.attn_norm.d, q.y = QKV + l * sqkv;
-        DecodePhaseIn at{};
-        at.kind = DPH_ATTN, at.x = QKV + l * sqkv, at.y = ATT + l * satt, at.kv = m->kv_layer(l);
-        at.bias = m->has_bias[l] ? m->bias + (int64_t)l * m->qkv_rows() : nullptr;
-        at.q_norm = Ld.q_norm.set ? (const float *)Ld.q_norm.d : nullptr;
-        at.k_norm = Ld.k_norm.set ? (const float *)Ld.k_norm.d : nullptr;
-        at.part = PART + l * spart;
-        DecodePhaseIn o{};
-        o.kind = DPH_ADD, o.t = Ld.wo.type, o.ne0 = AH, o.nrows = E, o.w = Ld.wo.d, o.x = ATT + l * satt;
-        o.y = x1, o.y_in = x0;
-        DecodePhaseIn gu{};
-        gu.kind = DPH_GLU, gu.t = Ld.gate.type, gu.ne0 = E, gu.nrows = F, gu.w = Ld.gate.d, gu.w2 = Ld.up.d;
-        gu.x = x1, gu.norm_w = (const float *)Ld.ffn_norm.d, gu.y = FFN + l * sffn;
-        DecodePhaseIn dn{};
-        dn.kind = DPH_ADD, dn.t = Ld.down.type, dn.ne0 = F, dn.nrows = E, dn.w = Ld.down.d, dn.x = FFN + l * sffn;
-        dn.y = x2, dn.y_in = x1;
-        if (add(q) || add(at) || add(o) || add(gu) || add(dn)) return TS5HIP_OK;
-    }
-    DecodePhaseIn h{};
-    h.kind = DPH_LOGITS, h.t = out.type, h.ne0 = E, h.nrows = hp.n_vocab, h.w = out.d, h.x = X + 2 * L * sx;
-    h.norm_w = (const float *)m->out_norm.d, h.logits = m->logits;
-    if (add(h)) return TS5HIP_OK;
-    if (!m->dec_phases && alloc(m, host.size(), &m->dec_phases)) return TS5HIP_ERR_HIP;
-    if (int rc = ts5hip_upload(m->ctx, m->dec_phases, host.data(), host.size())) return rc;
-    if (m->profile && !m->trace) {
-        const size_t n = (size_t)grid * (nph + 2) * 4;
-        if (int rc = alloc_t(m, n, &m->trace)) return rc;
-        m->trace_host.assign(n, 0);
-    }
-    m->dec_grid = grid, m->dec_lds = lds, m->dec_split = split, m->dec_nph = nph, m->dec_max_in = max_in;
-    m->use_decode = true;
-    return TS5HIP_OK;
-}
-
-int launch_decode_token(ts5hip_model *m, int head_mode) {
-    const ts5hip_hparams &hp = m->hp;
-    DecodeIn in{};
-    in.E = hp.n_embd, in.H = hp.n_head, in.HKV = hp.n_head_kv, in.HD = hp.head_dim, in.V = hp.n_vocab;
-    in.n_ctx = m->n_ctx, in.n_rot = hp.rope_dims, in.neox = hp.rope_neox, in.n_split = m->dec_split;
-    in.max_in = m->dec_max_in, in.eps = hp.rms_eps, in.scale = hp.attn_scale;
-    in.phases = m->dec_phases, in.n_phases = head_mode ? m->dec_nph : m->dec_nph - 1;
-    in.t_embd = m->tok_embd.type, in.embd = m->tok_embd.d, in.rope = m->rope_cs, in.x0 = m->arena;
-    in.seq = m->seq, in.state = m->state, in.head_mode = head_mode, in.best = m->dec_best, in.sync = m->dec_sync;
-    in.grid = m->dec_grid, in.lds_bytes = m->dec_lds, in.trace = m->profile ? m->trace : nullptr;
-    if (m->profile) TS5_HIP(m->ctx, hipMemsetAsync(m->trace, 0, m->trace_host.size() * 8, m->ctx->stream));
-    TS5_HIP(m->ctx, launch_decode(in, m->ctx->stream));
-    if (m->profile) {
-        TS5_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
-        TS5_HIP(m->ctx, hipMemcpy(m->trace_host.data(), m->trace, m->trace_host.size() * 8, hipMemcpyDeviceToHost));
-        const int K = m->dec_nph + 2, grid = m->dec_grid;
-        auto at = [&](int wg, int k, int e) { return m->trace_host[((size_t)wg * K + k) * 4 + e]; };
-        uint64_t prev_done = 0;
-        for (int wg = 0; wg < grid; wg++) prev_done = std::max(prev_done, at(wg, 0, 2));
-        for (int k = 1; k <= in.n_phases; k++) {
-            uint64_t rmin = UINT64_MAX, rmax = 0, dmax = 0;
-            double work = 0, wait = 0;
-            int n = 0;
-            for (int wg = 0; wg < grid; wg++) {
-                const uint64_t r = at(wg, k, 1), d = at(wg, k, 2);
-                if (!r || !d) continue;
-                rmin = std::min(rmin, r), rmax = std::max(rmax, r), dmax = std::max(dmax, d);
-                work += (double)(d - r), wait += (double)at(wg, k, 3), n++;
-            }
-            if (!n) continue;
-            const int kind = k - 1 < 5 * hp.n_layer ? 1 + (k - 1) % 5 : 6;
-            auto us = [](double t) { return t / 100.0; };
-            m->ph_span[kind] += us((double)dmax - (double)prev_done);
-            m->ph_hand[kind] += us((double)rmin - (double)prev_done);
-            m->ph_spread[kind] += us((double)(rmax - rmin));
-            m->ph_tail[kind] += us((double)dmax - (double)rmax);
-            m->ph_work[kind] += us(work / n);
-            m->ph_wait[kind] += us(wait / n);
-            m->ph_count[kind]++;
-            prev_done = dmax;
-        }
-        uint64_t t0 = UINT64_MAX, e0 = 0;
-        for (int wg = 0; wg < grid; wg++) t0 = std::min(t0, at(wg, 0, 0)), e0 = std::max(e0, at(wg, 0, 2));
-        m->ph_span[0] += (double)(e0 - t0) / 100.0;
-        m->ph_count[0]++;
-        m->phase_tokens++;
-    }
-    return TS5HIP_OK;
-}
-
-// After a synchronisation: a persistent-kernel poll that gave up waiting.
-int check_decode(ts5hip_model *m) {
-    if (!m->use_decode) return TS5HIP_OK;
-    int err = 0;
-    TS5_HIP(m->ctx, hipMemcpy(&err, m->dec_sync, sizeof err, hipMemcpyDeviceToHost));
-    if (err) return fail(m->ctx, TS5HIP_ERR_HIP, "decode kernel: a phase input never arrived");
-    return TS5HIP_OK;
-}
-
 int build_graphs(ts5hip_model *m) {
     if (!m->graphs_stale) return TS5HIP_OK;
     if (int rc = check_complete(m)) return rc;
-    if (int rc = prepare_decode(m)) return rc;
     if (!m->use_graphs) {
         m->graphs_stale = false;
         return TS5HIP_OK;
@@ -558,10 +396,8 @@ int build_graphs(ts5hip_model *m) {
     return TS5HIP_OK;
 }
 
-// One token's kernels: the persistent kernel, a replay of the captured
-// graph, or direct launches.
+// One token's kernels: a replay of the captured graph, or direct launches.
 int launch_token(ts5hip_model *m, int g) {
-    if (m->use_decode) return launch_decode_token(m, g == G_KV ? 0 : g == G_LOGITS ? 1 : 2);
     if (!m->use_graphs) return enqueue_token(m, g != G_KV, g == G_GREEDY ? 1 : 0);
     TS5_HIP(m->ctx, hipGraphLaunch(m->graph[g], m->ctx->stream));
     return TS5HIP_OK;
@@ -606,7 +442,7 @@ int ensure_batch(ts5hip_model *m) {
                 if (L.part[p].set) g(QR, E, L.part[p].type);
         }
         g(hp.n_vocab, E, out.type);
-        part = std::max(part, attn_partial_bytes(M, attn_splits(M, hp.n_head_kv, m->ctx->n_cu), hp.n_head, hp.head_dim));
+        part = std::max(part, attn_partial_bytes(M, attn_splits(M, hp.n_head_kv, m->ctx->n_cu), hp.n_head, hp.n_head_kv, hp.head_dim));
     }
     part = std::max(part, attn_prefill_partial_bytes(CHUNK, hp.n_head, hp.head_dim, m->n_ctx));
     int rc = 0;
@@ -732,7 +568,6 @@ int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool wan
     }
     if (m->profile) TS5_HIP(ctx, hipEventRecord(ctx->ev1, s));
     TS5_HIP(ctx, hipStreamSynchronize(s));
-    if (int rc = check_decode(m)) return rc;
     if (m->profile) {
         float ms = 0;
         TS5_HIP(ctx, hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
@@ -774,8 +609,6 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
     m->profile = prof && *prof && std::strcmp(prof, "0") != 0;
     const char *graphs = std::getenv("TS5HIP_GRAPHS");
     m->use_graphs = !(graphs && std::strcmp(graphs, "0") == 0);
-    const char *dec = std::getenv("TS5HIP_DECODE");
-    m->want_decode = dec && std::strcmp(dec, "1") == 0;
     const int64_t E = hp->n_embd, F = hp->n_ff, HD = hp->head_dim, H = hp->n_head, HKV = hp->n_head_kv;
     const int64_t kv_elems = (int64_t)hp->n_layer * HKV * n_ctx * HD;
     int rc = 0;
@@ -785,7 +618,7 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
         (rc = alloc_t(m, (size_t)hp->n_layer * m->qkv_rows(), &m->bias)) || (rc = alloc_t(m, E, &m->x)) ||
         (rc = alloc_t(m, m->qkv_rows(), &m->qkv)) || (rc = alloc_t(m, H * HD, &m->att)) ||
         (rc = alloc_t(m, F, &m->ffn)) || (rc = alloc_t(m, hp->n_vocab, &m->logits)) ||
-        (rc = alloc_t(m, attn_partial_bytes(1, 64, H, HD) / 4, &m->part)) ||
+        (rc = alloc_t(m, attn_partial_bytes(1, 64, H, HKV, HD) / 4, &m->part)) ||
         (rc = alloc_t(m, HKV * CTR_STRIDE + ARGMAX_CTR_INTS, &m->counters)) ||
         (rc = alloc(m, matvec_argmax_scratch_bytes(), &m->amax)) || (rc = alloc(m, topk_scratch_bytes(), &m->topk)) ||
         (rc = alloc_t(m, 64, &m->topk_v)) || (rc = alloc_t(m, 64, &m->topk_i)) ||
@@ -857,7 +690,7 @@ int ts5hip_kv_type(const ts5hip_model *m) { return m ? m->kv_type : -1; }
 int ts5hip_token_path(ts5hip_model *m) {
     if (!m) return fail(nullptr, TS5HIP_ERR_ARG, "null model");
     if (int rc = build_graphs(m)) return rc;
-    return m->use_decode ? 2 : m->use_graphs ? 1 : 0;
+    return m->use_graphs ? 1 : 0;
 }
 
 int32_t ts5hip_model_sample(ts5hip_model *m, ts5hip_sampler *s, int row, float temperature, float top_p, int top_k) {
@@ -899,7 +732,6 @@ int ts5hip_generate_greedy(ts5hip_model *m, int32_t token, int pos, int n_steps,
         if (int rc = launch_token(m, G_GREEDY)) return rc;
     TS5_HIP(ctx, hipMemcpyAsync(m->pinned_ids, m->seq + pos + 1, (size_t)n_steps * 4, hipMemcpyDeviceToHost, s));
     TS5_HIP(ctx, hipStreamSynchronize(s));
-    if (int rc = check_decode(m)) return rc;
     if (ids_out) std::memcpy(ids_out, m->pinned_ids, (size_t)n_steps * 4);
     m->rows_valid = 0;
     return TS5HIP_OK;
@@ -929,29 +761,7 @@ int ts5hip_take_profile(ts5hip_model *m, char *buf, int len) {
                       m->prof_calls, m->prof_tokens, m->prof_ms, m->prof_ms / std::max(1, m->prof_tokens));
         s = line;
     }
-    if (m->profile && m->phase_tokens) {
-        static const char *names[7] = {"embed", "qkv", "attn", "wo", "ffn_glu", "ffn_down", "head"};
-        char line[256];
-        std::snprintf(line, sizeof line,
-                      "persistent kernel, %d tokens; us per phase: span (hand-off + ready spread + tail), "
-                      "mean work per workgroup\n",
-                      m->phase_tokens);
-        s += line;
-        for (int k = 0; k < 7; k++) {
-            if (!m->ph_count[k]) continue;
-            const double n = m->ph_count[k];
-            std::snprintf(line, sizeof line,
-                          "  %-9s %8.2f (%6.2f + %6.2f + %6.2f)  work %6.2f (slot waits %6.2f)  x%d/token\n", names[k],
-                          m->ph_span[k] / n, m->ph_hand[k] / n, m->ph_spread[k] / n, m->ph_tail[k] / n,
-                          m->ph_work[k] / n, m->ph_wait[k] / n, (int)(n / m->phase_tokens));
-            s += line;
-        }
-    }
     m->prof_ms = 0, m->prof_calls = 0, m->prof_tokens = 0;
-    for (int k = 0; k < 7; k++)
-        m->ph_span[k] = m->ph_hand[k] = m->ph_spread[k] = m->ph_tail[k] = m->ph_work[k] = m->ph_wait[k] = 0,
-        m->ph_count[k] = 0;
-    m->phase_tokens = 0;
     std::strncpy(buf, s.c_str(), (size_t)len - 1);
     buf[len - 1] = 0;
     return TS5HIP_OK;

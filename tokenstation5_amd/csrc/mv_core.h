@@ -95,31 +95,6 @@ struct Q4K {
         r.qb = ld16(blk + 32 + 32 * sub);
         return r;
     }
-    // The same from a row of blocks staged in LDS (scales unused: Q4_K keeps
-    // its own in the block).
-    __device__ static W load_w_lds(const uint8_t *row, const uint8_t *, int b, int sub) {
-        const uint8_t *blk = row + b * Q4K_BYTES;
-        W r;
-        r.hdr = ld16(blk);
-        r.qa = ld16(blk + 16 + 32 * sub);
-        r.qb = ld16(blk + 32 + 32 * sub);
-        return r;
-    }
-    // The same three 16-byte pieces as LDS DMA sources (piece k of the lane's
-    // share of block b), and read back from a slot where piece k of all 64
-    // lanes sits at 1024 k + 16 lane.
-    static constexpr int NPIECE = 3;
-    __device__ static const uint8_t *piece(const WPtr &w, int64_t row, int nb, int b, int sub, int k) {
-        const uint8_t *blk = w.body + ((size_t)row * nb + b) * Q4K_BYTES;
-        return k == 0 ? blk : blk + 16 * k + 32 * sub;
-    }
-    __device__ static W from_slot(const uint8_t *slot, int lane) {
-        W r;
-        r.hdr = ld16(slot + 16 * lane);
-        r.qa = ld16(slot + 1024 + 16 * lane);
-        r.qb = ld16(slot + 2048 + 16 * lane);
-        return r;
-    }
     __device__ static float dot(const W &w, const X &x, int sub) {
         const uint32_t q[8] = {w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w};
         int ah0 = 0, al0 = 0, ah1 = 0, al1 = 0;
@@ -176,18 +151,6 @@ struct Q6K {
         r.qh = ld16(body + 128 + 32 * h + i0);
         r.sc = ld16(body + 192);
         r.d = h2f(w.dscale[blk]);
-        return r;
-    }
-    // The same from a row of bodies staged in LDS, its f16 scales at sc.
-    __device__ static W load_w_lds(const uint8_t *row, const uint8_t *sc, int b, int sub) {
-        const uint8_t *body = row + b * Q6K_BODY;
-        const int h = sub >> 1, i0 = (sub & 1) * 16;
-        W r;
-        r.qla = ld16(body + 64 * h + i0);
-        r.qlb = ld16(body + 64 * h + 32 + i0);
-        r.qh = ld16(body + 128 + 32 * h + i0);
-        r.sc = ld16(body + 192);
-        r.d = h2f(*(const uint16_t *)(sc + 2 * b));
         return r;
     }
     __device__ static float dot(const W &w, const X &x, int sub) {
@@ -249,12 +212,6 @@ struct Q80 {
         W r;
         r.q = ld16(w.body + blk * Q8_BODY + 16 * sub);
         r.d = h2f(w.dscale[blk]);
-        return r;
-    }
-    __device__ static W load_w_lds(const uint8_t *row, const uint8_t *sc, int b, int sub) {
-        W r;
-        r.q = ld16(row + b * Q8_BODY + 16 * sub);
-        r.d = h2f(*(const uint16_t *)(sc + 2 * b));
         return r;
     }
     __device__ static float dot(const W &w, const X &x, int) {
@@ -694,146 +651,5 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
         __syncthreads();
     }
 }
-
-// ---------------------------------------------------------------------------
-// The matvec with its weights streamed through a per-wave LDS ring. A wave
-// requests each step's blocks by LDS DMA (global_load_lds_dwordx4: lane l's
-// 16 bytes of piece k land at slot + 1024 k + 16 l, which is where lane l
-// reads them back), so NS - 1 steps are in flight while it computes one,
-// with no registers held for them. The DMA completes in order and is counted
-// explicitly (vmcnt); the compiler issues no global loads inside the loop.
-// MV_ADD also brings the group's residual rows into the slot (one dword DMA,
-// lanes < R), so the epilogue does not wait on a load of its own.
-// One workgroup per CU (the ring is most of the LDS); 4 waves.
-// ---------------------------------------------------------------------------
-// (dma16, dma4, wait_vm_n, lds_addr: common.h)
-
-template <class F, int R, int MODE, int NS, int WAVES = 4>
-struct MvRing {
-    static constexpr int NW = MODE == MV_GLU ? 2 : 1;
-    static constexpr int PIECES = NW * R * F::NPIECE;           // 1 KB DMAs per step
-    static constexpr int PER_STEP = PIECES + (MODE == MV_ADD);  // DMA instructions per step
-    static constexpr int SLOT = PIECES * 1024 + (MODE == MV_ADD ? 256 : 0);
-    static constexpr size_t lds_bytes(int n_in) { return align_up(act_bytes(n_in), 1024) + (size_t)WAVES * NS * SLOT; }
-};
-
-// vmcnt(PER_STEP * newer) for newer = 0 .. NS-1 (wave-uniform).
-template <int PER_STEP, int NS>
-__device__ inline void wait_steps(int newer) {
-    switch (newer) {
-    case 0: wait_vm_n<0>(); break;
-    case 1: wait_vm_n<PER_STEP>(); break;
-    case 2: wait_vm_n<(NS > 2 ? 2 : 1) * PER_STEP>(); break;
-    case 3: wait_vm_n<(NS > 3 ? 3 : 1) * PER_STEP>(); break;
-    default: wait_vm_n<(NS > 4 ? 4 : 1) * PER_STEP>(); break;
-    }
-}
-
-template <class F, int R, int MODE, int NS, int WAVES = 4>
-__device__ inline void mv_run_dma(const MvArgs &a, uint8_t *lds, float *red) {
-    static_assert(MODE != MV_ARGMAX && NS >= 2 && NS <= 5, "ring matvec shape");
-    using RG = MvRing<F, R, MODE, NS, WAVES>;
-    constexpr int NT = WAVES * WAVE, BPI = WAVE / F::LPB, NW = RG::NW;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int bsub = lane / F::LPB, sub = lane % F::LPB;
-    const int64_t rpg = (int64_t)R * WAVES;
-    const int64_t ngroups = (a.nrows + rpg - 1) / rpg;
-    const int spg = (a.nb + BPI - 1) / BPI;
-    const int64_t nblocks = (int64_t)a.nb * a.nrows;
-    const WPtr w1 = wptr(a.t, a.w, nblocks), w2 = wptr(a.t, MODE == MV_GLU ? a.w2 : a.w, nblocks);
-    const int64_t nwg = gridDim.x, wg = blockIdx.x;
-#ifndef TS5_MV_BLOCKED
-#define TS5_MV_BLOCKED 0
-#endif
-#if TS5_MV_BLOCKED
-    const int64_t gpw = (ngroups + nwg - 1) / nwg, gfirst = wg * gpw, gstride = 1;
-    const int64_t nsteps = max((int64_t)0, min(ngroups, gfirst + gpw) - gfirst) * spg;
-#else
-    const int64_t gfirst = wg, gstride = nwg;
-    const int64_t nsteps = (ngroups > wg ? (ngroups - 1 - wg) / nwg + 1 : 0) * spg;
-#endif
-    uint8_t *ring = lds + align_up(act_bytes(a.n_in), 1024) + (size_t)wave * NS * RG::SLOT;
-    const uint32_t ring_lds = lds_addr(ring);
-
-    auto issue = [&](int64_t s) {
-        const int64_t row0 = (gfirst + gstride * (s / spg)) * rpg + (int64_t)wave * R;
-        const int it = (int)(s % spg);
-        const int b = min(it * BPI + bsub, a.nb - 1);  // lanes past the row's end re-read its last block
-        const uint32_t slot = ring_lds + (uint32_t)((s % NS) * RG::SLOT);
-#pragma unroll
-        for (int m = 0; m < NW; m++)
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const int64_t row = min(row0 + r, a.nrows - 1);
-#pragma unroll
-                for (int k = 0; k < F::NPIECE; k++)
-                    dma16(F::piece(m ? w2 : w1, row, a.nb, b, sub, k),
-                          slot + (uint32_t)(((m * R + r) * F::NPIECE + k) * 1024));
-            }
-        if constexpr (MODE == MV_ADD) {
-            if (lane < R) dma4(a.y_in + min(row0 + lane, a.nrows - 1), slot + RG::PIECES * 1024);
-        }
-    };
-
-    int64_t issued = 0;
-    for (; issued < NS - 1 && issued < nsteps; issued++) issue(issued);
-    const Act xa = act_view(lds, a.n_in);
-    build_act<NT>(a.x, a.norm_w, a.eps, a.n_in, xa, red);
-    const CAct x{xa.hi, xa.lo, xa.scale, xa.sum, xa.isum};
-
-    float acc[NW][R];
-#pragma unroll
-    for (int m = 0; m < NW; m++)
-#pragma unroll
-        for (int r = 0; r < R; r++) acc[m][r] = 0.f;
-    for (int64_t s = 0; s < nsteps; s++) {
-        if (issued < nsteps) {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot being refilled has been read
-            issue(issued);
-            issued++;
-        }
-        wait_steps<RG::PER_STEP, NS>((int)(issued - s - 1));
-        const uint8_t *slot = ring + (s % NS) * RG::SLOT;
-        const int it = (int)(s % spg);
-        const int b = it * BPI + bsub;
-        if (b < a.nb) {
-            const typename F::X xf = F::load_x(x, b, sub);
-#pragma unroll
-            for (int m = 0; m < NW; m++)
-#pragma unroll
-                for (int r = 0; r < R; r++)
-                    acc[m][r] += F::dot(F::from_slot(slot + (m * R + r) * F::NPIECE * 1024, lane), xf, sub);
-        }
-        if (it == spg - 1) {
-            const int64_t row0 = (gfirst + gstride * (s / spg)) * rpg + (int64_t)wave * R;
-#pragma unroll
-            for (int m = 0; m < NW; m++)
-#pragma unroll
-                for (int r = 0; r < R; r++) acc[m][r] = wave_sum_dpp(acc[m][r]);
-            if (lane < R && row0 + lane < a.nrows) {
-                float v = acc[0][0], u = acc[NW - 1][0];
-#pragma unroll
-                for (int r = 1; r < R; r++)
-                    if (lane == r) v = acc[0][r], u = acc[NW - 1][r];
-                const int64_t row = row0 + lane;
-                if (MODE == MV_ADD) {
-                    st_dev(a.y + row, ((const float *)(slot + RG::PIECES * 1024))[lane] + v);
-                } else if (MODE == MV_GLU) {
-                    st_dev(a.y + row, v / (1.0f + expf(-v)) * u);  // engine/src/cpu_backend.cpp:260-261
-                } else {
-                    st_dev(a.y + row, v);
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < NW; m++)
-#pragma unroll
-                for (int r = 0; r < R; r++) acc[m][r] = 0.f;
-        }
-    }
-}
-
-struct NoHook {
-    __device__ void operator()() const {}
-};
 
 }  // namespace ts5hip

@@ -387,10 +387,10 @@ class Model:
         return out
 
     def token_path(self) -> str:
-        """How single-token steps run: "persistent", "graphs" or "direct"."""
+        """How single-token steps run: "graphs" or "direct"."""
         rc = lib().ts5hip_token_path(self.h)
         self.ctx.check(min(rc, 0))
-        return ("direct", "graphs", "persistent")[rc]
+        return ("direct", "graphs")[rc]
 
     def take_profile(self) -> str:
         buf = C.create_string_buffer(4096)

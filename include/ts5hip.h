@@ -172,8 +172,9 @@ int ts5hip_model_synth_tensor(ts5hip_model *m, const char *name, uint32_t type, 
  * the last token, or of all n when all_logits, into logits ([n or 1][n_vocab]); logits null:
  * fill the KV cache only. */
 int ts5hip_forward(ts5hip_model *m, const int32_t *tokens, int n, int pos0, float *logits, int all_logits);
-/* Backend::forward_in_place / logits_view (engine/src/backend.h:25-33): logits stay in pinned
- * host memory at ts5hip_logits_view (room for 256 rows). */
+/* Backend::forward_in_place / logits_view (engine/src/backend.h:25-33): the logits rows stay
+ * in HBM; ts5hip_logits_view copies them to pinned host memory on its first call after a
+ * forward (room for 256 rows) and returns that copy. */
 int ts5hip_forward_in_place(ts5hip_model *m, const int32_t *tokens, int n, int pos0, int all_logits);
 const float *ts5hip_logits_view(const ts5hip_model *m);
 /* Backend::n_ctx / kv_type (engine/src/backend.h:34-39). */
@@ -183,7 +184,17 @@ int ts5hip_kv_type(const ts5hip_model *m);
  * launches (TS5HIP_GRAPHS=0 at model creation); < 0 an error. No counterpart in the
  * reference (its Vulkan backend has one path): for tests and profiles. */
 int ts5hip_token_path(ts5hip_model *m);
-/* Top-k of the last forward's logits row `row` on the GPU and the host draw (Engine::sample). */
+/* The k (1..64) largest logits of rows [row0, row0 + nrows) of the last forward, found on the
+ * GPU where the rows stay, descending with ties by ascending id, into host arrays
+ * vals/ids [nrows][k]. k = 1 is the greedy pick of engine/src/engine.cpp:17. This is the
+ * additive Backend::topk_view hook that lets Engine::sample (engine/src/engine.cpp:16-46) and
+ * the draft model's greedy step (engine/src/engine.cpp:124) read k candidates per row
+ * instead of n_vocab floats; the logits rows reach the host only if ts5hip_logits_view is
+ * called. */
+int ts5hip_logits_topk(ts5hip_model *m, int row0, int nrows, int k, float *vals, int32_t *ids);
+/* Engine::sample (engine/src/engine.cpp:16-46) of row `row` of the last forward: the GPU
+ * argmax (temperature <= 0) or top-k candidates and the host draw; the whole row is read on
+ * the host only when ties or a top_k past 63 leave the candidates short of deciding it. */
 int32_t ts5hip_model_sample(ts5hip_model *m, ts5hip_sampler *s, int row, float temperature, float top_p,
                             int top_k);
 /* Greedy decode kept on the device (run_bench's generation loop, engine/src/checks.cpp:195-199,

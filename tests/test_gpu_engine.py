@@ -99,3 +99,41 @@ def test_end_of_generation_stops(ctx):
     first = int(np.argmax(ids == stop))
     ids2, st2 = ts5hip.Engine(m).generate(SPEC["prompt"], max_tokens=20, draft=4, eog=[stop])
     assert list(ids2) == list(ids[:first]) and st2[5] == 1
+
+
+def test_logits_topk_rows(ctx):
+    """The GPU pick over the rows of a verify-shaped forward: each row's top 40
+    (and top 1) equal a stable descending sort of the row read on the host."""
+    m = load(ctx, "tiny_llama_c")
+    toks = SPEC["prompt"][:6]
+    m.forward_in_place(toks[:-5], 0)
+    m.ctx.check(ts5hip.lib().ts5hip_forward_in_place(m.h, toks[-5:].ctypes.data, 5, toks.size - 5, 1))
+    v, i = m.logits_topk(0, 5, 40)
+    v1, i1 = m.logits_topk(2, 3, 1)
+    rows = m.forward_in_place(toks[-5:], toks.size - 5, all_logits=True)  # the same rows, read on the host
+    for r in range(5):
+        want = np.argsort(-rows[r], kind="stable")[:40]
+        assert list(i[r]) == list(want) and np.array_equal(v[r], rows[r][want]), r
+    assert list(i1[:, 0]) == [int(np.argmax(rows[r])) for r in range(2, 5)]
+    with pytest.raises(ts5hip.Ts5HipError):
+        m.logits_topk(3, 3, 5)
+
+
+def test_sample_with_ties_equals_reference_heap(ctx):
+    """Logits full of ties (a zero output head: every logit 0) leave the
+    candidates to the order of Engine::sample's heap: the draw must then come
+    from the whole row on the host and equal the oracle's restatement of
+    engine/src/engine.cpp:16-46 (pinned to the reference by sampler.npz)."""
+    import oracle
+    hp = dict(MODELS["tiny_llama_c"]["hparams"])
+    tensors = synth.model_tensors(hp, make_golden.MODEL_SEED)
+    t, ne0, ne1, data = tensors["output.weight"]
+    tensors["output.weight"] = (t, ne0, ne1, np.zeros_like(data))
+    m = ts5hip.Model(ctx, hp, 64)
+    m.set_tensors(tensors)
+    lg = m.forward(SPEC["prompt"][:4], 0)[0]
+    assert np.all(lg == 0)
+    smp, ref = ts5hip.Sampler(9), oracle.Sampler(9)
+    for k, p in ((40, 0.9), (5, 1.0), (0, 0.5)):
+        for _ in range(6):
+            assert m.sample(smp, 0, 0.7, p, k) == ref.sample(lg, 0.7, p, k), (k, p)

@@ -357,8 +357,8 @@ int ts5hip_topk(ts5hip_ctx *ctx, const float *x, int n, int k, float *vals_dev, 
     if (!ctx || !x || !vals_dev || !ids_dev) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
     if (k <= 0 || k > topk_max() || n < k || n > topk_max_n())
         return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "top-%d of %d (k <= %d, n <= %d)", k, n, topk_max(), topk_max_n());
-    if (int rc = ensure_scratch(ctx, topk_scratch_bytes())) return rc;
-    TS5_HIP(ctx, launch_topk(x, n, k, ctx->scratch, vals_dev, ids_dev, ctx->stream));
+    if (int rc = ensure_scratch(ctx, topk_scratch_bytes(1))) return rc;
+    TS5_HIP(ctx, launch_topk(x, n, k, 1, ctx->scratch, vals_dev, ids_dev, ctx->stream));
     return TS5HIP_OK;
 }
 

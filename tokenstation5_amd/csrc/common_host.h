@@ -84,6 +84,22 @@ inline int32_t sampler_draw(std::mt19937_64 &rng, std::vector<double> &w, const 
     return ids[pick(rng)];
 }
 
+// Engine::sample (engine/src/engine.cpp:16-46) over rows of the last
+// forward's logits, which stay in HBM: the candidates of rows
+// [row0, row0 + nrows) are picked on the GPU in one pass (greedy: the first
+// maximum; top-k: the best k + 1, sorted), then model_draw makes row i's draw
+// on the host, with the row itself brought over only when the candidates do
+// not fix the result (ties, NaN, top-k past the GPU pick) (model.cpp).
+enum { PICK_GREEDY = 0, PICK_TOPK = 1, PICK_HOST = 2 };
+struct RowPicks {
+    int mode = PICK_HOST, row0 = 0, nrows = 0, k = 0, kk = 0;
+    std::vector<float> v;
+    std::vector<int32_t> id;
+};
+int model_pick_rows(ts5hip_model *m, int row0, int nrows, float temperature, int top_k, RowPicks &pk);
+int32_t model_draw(ts5hip_model *m, ts5hip_sampler *s, const RowPicks &pk, int i, float temperature, float top_p,
+                   int top_k);
+
 // Engine::sample over a host row of logits (capi.cpp).
 int32_t sample_host_row(ts5hip_sampler *s, const float *lg, int n, float temperature, float top_p, int top_k);
 // Engine::generate's rng_.seed(seed) (capi.cpp).

@@ -1,19 +1,28 @@
-// The decode driver: ts5's Engine::generate (engine/src/engine.cpp:149-292)
-// over this backend, with its speculation: prompt-lookup drafts
-// (engine/src/engine.cpp:134-147) and, where lookup finds nothing, a draft
-// model's greedy continuation (engine/src/engine.cpp:75-129), verified in one
-// batched forward and kept while the target's own sample equals the draft.
+// The decode driver over the C ABI: generation with speculative decoding, the
+// behaviour of ts5's Engine::generate (engine/src/engine.cpp:149-292).
 //
-// Host code over the library's C ABI: every forward is ts5hip_forward /
-// ts5hip_forward_in_place (the batch runs on the matrix cores), every sample
-// is Engine::sample on the pinned logits rows (capi.cpp sample_host_row, the
-// same mt19937_64 stream). The output ids, and the counts of drafted and
-// accepted tokens, are the reference's for the same model, prompt and seed.
+// A generation keeps a history (the token ids whose K/V the target's cache
+// holds, position = index) and runs in steps. Each step forwards the pending
+// token plus up to `room` drafted continuations as one batch and keeps the
+// drafts the target's own sampler reproduces, so the output is the one a
+// token-at-a-time loop would give with the same sampler stream. Drafts come
+// from two sources, cheapest first:
+//   * the history itself: what followed the most recent earlier occurrence
+//     of the last three tokens (else two), found by a hash-chain match
+//     finder over the history's 2-grams (the prompt-lookup drafting of
+//     engine.cpp:134-147);
+//   * a draft model (engine.cpp:75-129): its greedy continuation, after
+//     catching its own cache up with the history.
+// How many tokens to draft follows the recent acceptance rate (engine.cpp:
+// 218-228): a running average of accepted / proposed picks full, short or no
+// drafts, with a periodic short probe while drafting is off.
+//
+// Sampling reads no logits row on the host unless it must: every row of a
+// step's batch is reduced on the GPU in one pass (greedy argmax, or the top
+// k + 1 candidates), and the host draws from those (model_draw).
 #include <algorithm>
 #include <cstring>
 #include <random>
-#include <string>
-#include <unordered_map>
 #include <vector>
 
 #include "common_host.h"
@@ -21,99 +30,178 @@
 
 using namespace ts5hip;
 
-struct ts5hip_engine {
-    ts5hip_model *m = nullptr, *dm = nullptr;
-    ts5hip_sampler *rng = nullptr;  // Engine::rng_: std::mt19937_64, default-seeded
-    std::vector<int32_t> cached;    // ids whose K/V the target holds, position = index
-    size_t dcached = 0;             // ... and how many of them the draft model holds
-    int written = 0;
-    bool drafter_ok = false;
-    std::unordered_map<uint64_t, int32_t> gram2, gram3;  // n-gram -> position after its last occurrence
-    std::vector<int32_t> cu;
-};
-
 namespace {
 
-uint64_t gram_key(int32_t a, int32_t b) { return ((uint64_t)(uint32_t)a << 21) | (uint32_t)b; }
+// Batches of prompt (and draft catch-up) tokens per forward: the reference's
+// chunk (engine.cpp:172, :97), which is also the backend's logits capacity.
+constexpr int kChunk = 256;
 
-// The n-grams ending at positions from.. of cached, later ones replacing
-// earlier ones (a lookup finds the most recent occurrence).
-void index_grams(ts5hip_engine *e, size_t from) {
-    const std::vector<int32_t> &c = e->cached;
-    for (size_t j = std::max<size_t>(from, 1); j < c.size(); j++) {
-        e->gram2[gram_key(c[j - 1], c[j])] = (int32_t)j + 1;
-        if (j >= 2) e->gram3[(gram_key(c[j - 2], c[j - 1]) << 21) | (uint32_t)c[j]] = (int32_t)j + 1;
+// ---------------------------------------------------------------------------
+// Prompt lookup: a match finder over the history. Every 2-gram (h[j-1], h[j])
+// is linked into a chain of the positions j that end a 2-gram of the same
+// hash, newest first (the hash chains of LZ77 match finders). A lookup for the
+// pending token t walks the chain of (h[n-1], t): the first real match whose
+// predecessor is also h[n-2] is the newest 3-gram occurrence; failing that the
+// first real match is the newest 2-gram one. The drafts are what followed it
+// in the history extended by t.
+// ---------------------------------------------------------------------------
+class MatchFinder {
+public:
+    void rebuild(const std::vector<int32_t> &h) {
+        size_t want = 1024;
+        while (want < 2 * h.size() + 2) want <<= 1;
+        head_.assign(want, -1);
+        mask_ = (uint32_t)(want - 1);
+        link_.clear();
+        indexed_ = 0;
+        extend(h);
     }
-}
-
-// Up to k drafts after `tok`: what followed the most recent earlier
-// occurrence of the text's last 3-gram (then 2-gram).
-void draft_lookup(ts5hip_engine *e, int32_t tok, int k, std::vector<int32_t> &out) {
-    const std::vector<int32_t> &c = e->cached;
-    const size_t sz = c.size();
-    int32_t p = -1;
-    if (sz >= 2) {
-        auto it = e->gram3.find((gram_key(c[sz - 2], c[sz - 1]) << 21) | (uint32_t)tok);
-        if (it != e->gram3.end()) p = it->second;
+    // Links the 2-grams ending at the positions added since the last call.
+    void extend(const std::vector<int32_t> &h) {
+        if (2 * h.size() + 2 > head_.size()) {
+            rebuild(h);
+            return;
+        }
+        link_.resize(h.size(), -1);
+        for (size_t j = std::max<size_t>(indexed_, 1); j < h.size(); j++) {
+            int32_t &slot = head_[bucket(h[j - 1], h[j])];
+            link_[j] = slot;
+            slot = (int32_t)j;
+        }
+        indexed_ = h.size();
     }
-    if (p < 0 && sz >= 1) {
-        auto it = e->gram2.find(gram_key(c[sz - 1], tok));
-        if (it != e->gram2.end()) p = it->second;
+    // The position just past the newest match for pending token t, or -1.
+    int64_t find(const std::vector<int32_t> &h, int32_t t) const {
+        const size_t n = h.size();
+        if (n == 0 || head_.empty()) return -1;
+        const int32_t a = h[n - 1];
+        int64_t newest2 = -1;
+        for (int32_t j = head_[bucket(a, t)]; j >= 0; j = link_[(size_t)j]) {
+            if (h[(size_t)j - 1] != a || h[(size_t)j] != t) continue;  // another 2-gram of the same hash
+            if (newest2 < 0) newest2 = j + 1;
+            if (n >= 2 && j >= 2 && h[(size_t)j - 2] == h[n - 2]) return j + 1;
+        }
+        return newest2;
     }
-    if (p < 0) return;
-    for (size_t i = (size_t)p; i <= sz && (int)out.size() < k + 1; i++) out.push_back(i < sz ? c[i] : tok);
-}
 
-bool is_eog(const int32_t *eog, int n_eog, int32_t t) { return std::find(eog, eog + n_eog, t) != eog + n_eog; }
+private:
+    uint32_t bucket(int32_t a, int32_t b) const {
+        uint64_t x = (uint64_t)(uint32_t)a * 0x9E3779B97F4A7C15ull ^ (uint64_t)(uint32_t)b * 0xC2B2AE3D27D4EB4Full;
+        x ^= x >> 29;
+        return (uint32_t)(x ^ (x >> 32)) & mask_;
+    }
+    std::vector<int32_t> head_, link_;
+    uint32_t mask_ = 0;
+    size_t indexed_ = 0;
+};
 
-// Up to k drafts: the draft model's greedy continuation after catching its
-// cache up to the confirmed history plus `tok` (a backlog of 256 or more is
-// caught up one chunk per step, without drafting). A failure stops drafting
-// by model, not the request.
-void draft_model(ts5hip_engine *e, int32_t tok, int k, const int32_t *eog, int n_eog, std::vector<int32_t> &out) {
-    ts5hip_model *dm = e->dm;
-    const int nv = model_vocab(dm);
-    const int pos = (int)e->cached.size();
-    if (pos + k + 2 > ts5hip_n_ctx(dm)) return;
-    auto fits = [&](const int32_t *p, size_t n) {
+// ---------------------------------------------------------------------------
+// The draft model: its cache holds the first `synced` history positions.
+// ---------------------------------------------------------------------------
+struct Drafter {
+    ts5hip_model *m = nullptr;
+    size_t synced = 0;
+    bool live = false;  // false once a forward failed or a token fell outside its vocabulary
+    RowPicks pick;
+    std::vector<int32_t> feed;
+
+    bool all_known(const int32_t *ids, size_t n) {
+        const int nv = model_vocab(m);
         for (size_t i = 0; i < n; i++)
-            if (p[i] >= nv) {
-                e->drafter_ok = false;
-                return false;
-            }
+            if (ids[i] >= nv) return live = false;
         return true;
-    };
-    const size_t CHUNK = 256;
-    if (e->cached.size() - e->dcached >= CHUNK) {
-        if (!fits(e->cached.data() + e->dcached, CHUNK)) return;
-        if (ts5hip_forward(dm, e->cached.data() + e->dcached, (int)CHUNK, (int)e->dcached, nullptr, 0) != TS5HIP_OK) {
-            e->drafter_ok = false;
+    }
+
+    // Up to `room` drafts after pending token t at position h.size(), appended
+    // to out. A backlog of a whole chunk or more is caught up by one chunk
+    // instead (no drafts this step), so no step stalls on a long prompt.
+    void propose(const std::vector<int32_t> &h, int32_t t, int room, int target_vocab, const int32_t *eog,
+                 int n_eog, std::vector<int32_t> &out) {
+        const size_t pos = h.size();
+        if ((int64_t)pos + room + 2 > ts5hip_n_ctx(m)) return;
+        if (pos - synced >= (size_t)kChunk) {
+            if (!all_known(h.data() + synced, kChunk)) return;
+            if (ts5hip_forward(m, h.data() + synced, kChunk, (int)synced, nullptr, 0) != TS5HIP_OK) live = false;
+            else synced += kChunk;
             return;
         }
-        e->dcached += CHUNK;
-        return;
-    }
-    e->cu.assign(e->cached.begin() + (ptrdiff_t)e->dcached, e->cached.end());
-    e->cu.push_back(tok);
-    if (!fits(e->cu.data(), e->cu.size())) return;
-    int32_t t = -1;
-    for (int i = 0; i < k; i++) {
-        const int32_t *in = i == 0 ? e->cu.data() : &t;
-        const int n = i == 0 ? (int)e->cu.size() : 1;
-        const int p0 = i == 0 ? (int)e->dcached : pos + i;
-        if (ts5hip_forward_in_place(dm, in, n, p0, 0) != TS5HIP_OK) {
-            e->drafter_ok = false;
+        feed.assign(h.begin() + (ptrdiff_t)synced, h.end());
+        feed.push_back(t);
+        if (!all_known(feed.data(), feed.size())) return;
+        // The first draft is the greedy pick after the catch-up batch; the
+        // rest come from the device-side greedy loop in one call (it writes
+        // K/V past a stop as well; those positions are re-fed before use).
+        if (ts5hip_forward_in_place(m, feed.data(), (int)feed.size(), (int)synced, 0) != TS5HIP_OK ||
+            model_pick_rows(m, 0, 1, 0.f, 0, pick) != TS5HIP_OK) {
+            live = false;
             return;
         }
-        const float *lg = ts5hip_logits_view(dm);
-        t = (int32_t)(std::max_element(lg, lg + nv) - lg);
-        if (t >= model_vocab(e->m)) break;  // a padded drafter row is no target token
-        out.push_back(t);
-        if (is_eog(eog, n_eog, t)) break;
+        int32_t next[256];
+        next[0] = pick.id[0];
+        if (room > 1 && next[0] < target_vocab && std::find(eog, eog + n_eog, next[0]) == eog + n_eog &&
+            ts5hip_generate_greedy(m, next[0], (int)pos + 1, room - 1, next + 1) != TS5HIP_OK) {
+            live = false;
+            room = 1;
+        }
+        for (int i = 0; i < room; i++) {
+            if (next[i] >= target_vocab) break;  // a padded drafter row is no target token
+            out.push_back(next[i]);
+            if (std::find(eog, eog + n_eog, next[i]) != eog + n_eog) break;  // nothing follows an end
+        }
     }
-}
+};
+
+// ---------------------------------------------------------------------------
+// Draft length from the running acceptance rate (engine.cpp:218-228, :270-273):
+// below 15 % no drafts (but a short probe every 16th step), below 50 % at most
+// 3, else the full length. The average moves a fifth of the way to each
+// judged batch's rate.
+// ---------------------------------------------------------------------------
+class DraftGovernor {
+public:
+    explicit DraftGovernor(bool adaptive) : adaptive_(adaptive) {}
+    int length(int full) {
+        int n = full;
+        if (adaptive_ && rate_ >= 0) {
+            const int shortlen = std::min(full, kShort);
+            n = rate_ < kOff ? 0 : rate_ < kHalf ? shortlen : full;
+            if (n == 0 && step_ % kProbeEvery == 0) n = shortlen;
+        }
+        step_++;
+        return n;
+    }
+    void judged(int accepted, int proposed) {
+        if (proposed <= 0) return;
+        const float r = (float)accepted / (float)proposed;
+        rate_ = rate_ < 0 ? r : kKeep * rate_ + kTake * r;
+    }
+
+private:
+    static constexpr float kOff = 0.15f, kHalf = 0.5f, kKeep = 0.8f, kTake = 0.2f;
+    static constexpr int kShort = 3, kProbeEvery = 16;
+    bool adaptive_;
+    float rate_ = -1;  // < 0 until a batch with drafts has been judged
+    int step_ = 0;
+};
+
+bool ends(const int32_t *eog, int n_eog, int32_t t) { return std::find(eog, eog + n_eog, t) != eog + n_eog; }
 
 }  // namespace
+
+struct ts5hip_engine {
+    ts5hip_model *m = nullptr;
+    ts5hip_sampler *rng = nullptr;  // the sampler stream (std::mt19937_64, default-seeded at creation)
+    std::vector<int32_t> history;
+    MatchFinder finder;
+    Drafter drafter;
+    RowPicks picks;
+    std::vector<int32_t> batch;
+
+    void forget() {
+        history.clear();
+        drafter.synced = 0;
+    }
+};
 
 extern "C" {
 
@@ -134,9 +222,9 @@ void ts5hip_engine_free(ts5hip_engine *e) {
 
 int ts5hip_engine_set_drafter(ts5hip_engine *e, ts5hip_model *dm) {
     if (!e) return fail(nullptr, TS5HIP_ERR_ARG, "null engine");
-    e->dm = dm;
-    e->dcached = 0;
-    e->drafter_ok = dm != nullptr;
+    e->drafter = Drafter{};
+    e->drafter.m = dm;
+    e->drafter.live = dm != nullptr;
     return TS5HIP_OK;
 }
 
@@ -145,97 +233,98 @@ int ts5hip_engine_generate(ts5hip_engine *e, const int32_t *prompt, int n_prompt
     if (!e || !prompt || !p || !out || (n_eog > 0 && !eog)) return fail(nullptr, TS5HIP_ERR_ARG, "null argument");
     ts5hip_model *m = e->m;
     ts5hip_ctx *ctx = model_ctx(m);
-    if (p->seed) sampler_reseed(e->rng, p->seed);
-    const int nv = model_vocab(m);
-    int32_t st[6] = {n_prompt, 0, 0, 0, 0, 0};  // prompt, evaluated, generated, drafted, accepted, stopped
     if (n_prompt <= 0) return fail(ctx, TS5HIP_ERR_ARG, "empty prompt");
     if (n_prompt + 1 > ts5hip_n_ctx(m)) return fail(ctx, TS5HIP_ERR_CONTEXT_FULL, "prompt longer than the context");
-    // The cached prefix is reused; the last prompt token is always evaluated.
-    size_t keep = 0;
-    while (keep < e->cached.size() && keep < (size_t)n_prompt && e->cached[keep] == prompt[keep]) keep++;
-    if (keep == (size_t)n_prompt) keep--;
-    if (keep == 0) e->written = 0;
-    e->cached.resize(keep);
-    if (e->dcached > keep) e->dcached = keep;
-    const int chunk = 256;
-    for (size_t i = keep; i < (size_t)n_prompt; i += chunk) {
-        const int n = (int)std::min<size_t>(chunk, (size_t)n_prompt - i);
-        const bool last = i + (size_t)n >= (size_t)n_prompt;
-        const int rc = last ? ts5hip_forward_in_place(m, prompt + i, n, (int)i, 0)
-                            : ts5hip_forward(m, prompt + i, n, (int)i, nullptr, 0);
+    if (p->seed) sampler_reseed(e->rng, p->seed);
+    const int n_ctx = ts5hip_n_ctx(m);
+    std::vector<int32_t> &h = e->history;
+    enum { S_PROMPT, S_EVAL, S_GEN, S_DRAFTED, S_ACCEPTED, S_EOG };
+    int32_t st[6] = {n_prompt, 0, 0, 0, 0, 0};
+
+    // The prompt: the cached history's common prefix is kept, except that the
+    // last prompt token is always run (its logits start the generation).
+    const size_t common = std::mismatch(h.begin(), h.begin() + std::min(h.size(), (size_t)n_prompt), prompt).first -
+                          h.begin();
+    const size_t keep = std::min(common, (size_t)n_prompt - 1);
+    h.resize(keep);
+    e->drafter.synced = std::min(e->drafter.synced, keep);
+    for (size_t at = keep; at < (size_t)n_prompt; at += kChunk) {
+        const int n = (int)std::min<size_t>(kChunk, (size_t)n_prompt - at);
+        const bool last = at + (size_t)n == (size_t)n_prompt;
+        const int rc = last ? ts5hip_forward_in_place(m, prompt + at, n, (int)at, 0)
+                            : ts5hip_forward(m, prompt + at, n, (int)at, nullptr, 0);
         if (rc != TS5HIP_OK) {
-            e->cached.clear();
-            e->dcached = 0;
+            e->forget();
             return rc;
         }
-        e->written = std::max(e->written, (int)(i + n));
-        e->cached.insert(e->cached.end(), prompt + i, prompt + i + n);
+        h.insert(h.end(), prompt + at, prompt + at + n);
     }
-    st[1] = (int32_t)(n_prompt - keep);
-    int dmax = p->draft < 0 ? 7 : std::min(p->draft, 255);
-    e->gram3.clear();
-    e->gram2.clear();
-    if (dmax > 0) index_grams(e, 0);
+    st[S_EVAL] = (int32_t)(n_prompt - keep);
+
+    const int full = p->draft < 0 ? 7 : std::min(p->draft, 255);  // a batch must fit one 256-row chunk
+    if (full > 0) e->finder.rebuild(h);
+    DraftGovernor governor(p->adapt != 0);
     int n_out = 0;
     auto emit = [&](int32_t t) {
-        st[2]++;
+        st[S_GEN]++;
         if (n_out < p->max_tokens) out[n_out++] = t;
     };
-    float acc = -1;  // accepted / proposed, an EWMA; < 0 until a batch has been judged
-    int step = 0;
-    std::vector<int32_t> batch;
-    int32_t tok = sample_host_row(e->rng, ts5hip_logits_view(m), nv, p->temperature, p->top_p, p->top_k);
-    while (true) {
-        if (is_eog(eog, n_eog, tok)) {
-            st[5] = 1;
+    auto sample_rows = [&](int nrows) { return model_pick_rows(m, 0, nrows, p->temperature, p->top_k, e->picks); };
+    auto draw = [&](int row) { return model_draw(m, e->rng, e->picks, row, p->temperature, p->top_p, p->top_k); };
+
+    if (int rc = sample_rows(1)) return rc;
+    int32_t tok = draw(0);
+    if (tok < 0) return tok;
+    for (;;) {
+        if (ends(eog, n_eog, tok)) {
+            st[S_EOG] = 1;
             break;
         }
         emit(tok);
-        if (st[2] >= p->max_tokens) break;
-        if ((int)e->cached.size() + 1 >= ts5hip_n_ctx(m)) break;
-        batch.assign(1, tok);
-        int want = dmax;
-        if (p->adapt && acc >= 0) {
-            want = acc < 0.15f ? 0 : acc < 0.5f ? std::min(dmax, 3) : dmax;
-            if (want == 0 && step % 16 == 0) want = std::min(dmax, 3);
+        if (st[S_GEN] >= p->max_tokens || (int)h.size() + 1 >= n_ctx) break;
+
+        // Drafts: lookup first, the draft model where lookup finds nothing.
+        std::vector<int32_t> &b = e->batch;
+        b.assign(1, tok);
+        const int room = std::min({governor.length(full), p->max_tokens - st[S_GEN], n_ctx - (int)h.size() - 2});
+        if (room > 0) {
+            const int64_t from = e->finder.find(h, tok);
+            for (int64_t i = from; from >= 0 && i <= (int64_t)h.size() && (int)b.size() <= room; i++)
+                b.push_back(i < (int64_t)h.size() ? h[(size_t)i] : tok);
         }
-        step++;
-        int room = std::min(want, p->max_tokens - st[2]);
-        room = std::min(room, ts5hip_n_ctx(m) - (int)e->cached.size() - 2);
-        if (room > 0) draft_lookup(e, tok, room, batch);
-        const bool by_model = batch.size() == 1 && room > 0 && e->dm && e->drafter_ok;
-        if (by_model) draft_model(e, tok, room, eog, n_eog, batch);
-        const int nb = (int)batch.size();
-        if (int rc = ts5hip_forward_in_place(m, batch.data(), nb, (int)e->cached.size(), nb > 1 ? 1 : 0)) {
-            e->cached.clear();
-            e->dcached = 0;
+        const bool by_model = b.size() == 1 && room > 0 && e->drafter.live;
+        if (by_model) e->drafter.propose(h, tok, room, model_vocab(m), eog, n_eog, b);
+
+        // Verify: one forward of the batch, then walk its rows while the
+        // target's own sample equals the next draft.
+        const int nb = (int)b.size();
+        const size_t pos = h.size();
+        int rc = ts5hip_forward_in_place(m, b.data(), nb, (int)pos, nb > 1 ? 1 : 0);
+        if (rc == TS5HIP_OK) rc = sample_rows(nb);
+        if (rc != TS5HIP_OK) {
+            e->forget();
             return rc;
         }
-        e->written = std::max(e->written, (int)e->cached.size() + nb);
-        const float *lg = ts5hip_logits_view(m);
-        st[3] += nb - 1;
-        int accepted = 0;
+        st[S_DRAFTED] += nb - 1;
+        int kept = 0;
         int32_t next = -1;
         for (int i = 0; i < nb; i++) {
-            next = sample_host_row(e->rng, lg + (size_t)i * nv, nv, p->temperature, p->top_p, p->top_k);
-            if (i + 1 < nb && next == batch[i + 1] && !is_eog(eog, n_eog, next)) {
-                accepted++;
-                continue;
+            next = draw(i);
+            if (next < 0) {
+                e->forget();
+                return next;
             }
-            break;
+            if (i + 1 == nb || next != b[(size_t)i + 1] || ends(eog, n_eog, next)) break;
+            kept++;
         }
-        st[4] += accepted;
-        if (nb > 1) {
-            const float r = (float)accepted / (float)(nb - 1);
-            acc = acc < 0 ? r : 0.8f * acc + 0.2f * r;
-        }
-        e->cached.insert(e->cached.end(), batch.begin(), batch.begin() + accepted + 1);
-        if (dmax > 0) index_grams(e, e->cached.size() - (size_t)(accepted + 1));
-        // The drafter holds batch[0..nb-2]; with everything accepted its last
-        // draft was never forwarded.
-        if (by_model && batch.size() > 1) e->dcached = e->cached.size() - (accepted == nb - 1 ? 1 : 0);
-        for (int i = 1; i <= accepted; i++) emit(batch[i]);
-        if (st[2] >= p->max_tokens) break;
+        st[S_ACCEPTED] += kept;
+        governor.judged(kept, nb - 1);
+        h.insert(h.end(), b.begin(), b.begin() + kept + 1);
+        if (full > 0) e->finder.extend(h);
+        // The drafter forwarded the batch's tokens but its last draft.
+        if (by_model && nb > 1) e->drafter.synced = std::min(h.size(), pos + (size_t)nb - 1);
+        for (int i = 1; i <= kept; i++) emit(b[(size_t)i]);
+        if (st[S_GEN] >= p->max_tokens) break;
         tok = next;
     }
     if (stats) std::memcpy(stats, st, sizeof st);

@@ -118,9 +118,12 @@ hipError_t launch_argmax(const float *x, int n, int rows, void *scratch, int32_t
                          hipStream_t s);
 hipError_t launch_advance(int32_t *pos, hipStream_t s);
 hipError_t launch_set_pos(int32_t *pos, int32_t v, hipStream_t s);
-size_t topk_scratch_bytes();
+// The k (<= topk_max()) largest of each of `rows` rows of n (<= topk_max_n())
+// logits, descending, ties by ascending id: vals / ids [rows][k].
+size_t topk_scratch_bytes(int rows);
 int topk_max();
 int topk_max_n();
-hipError_t launch_topk(const float *x, int n, int k, void *scratch, float *vals, int32_t *ids, hipStream_t s);
+hipError_t launch_topk(const float *x, int n, int k, int rows, void *scratch, float *vals, int32_t *ids,
+                       hipStream_t s);
 
 }  // namespace ts5hip

@@ -13,6 +13,7 @@
 // step, and greedy decoding never returns to the host between tokens.
 #include <algorithm>
 #include <chrono>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -62,14 +63,19 @@ struct ts5hip_model {
     // Activations and scratch.
     float *x = nullptr, *qkv = nullptr, *att = nullptr, *ffn = nullptr, *logits = nullptr, *part = nullptr;
     int *counters = nullptr;  // HKV attention merges (CTR_STRIDE apart), then the head argmax's; zero between launches
-    void *amax = nullptr, *topk = nullptr;
-    float *topk_v = nullptr;
-    int32_t *topk_i = nullptr;
+    void *amax = nullptr;
     int32_t *seq = nullptr;    // [n_ctx + 1] token id at each position
     int32_t *state = nullptr;  // [0] position, [1] last argmax
-    // Logits rows of the last forward: on the device, and in pinned host memory.
+    // Logits rows of the last forward: on the device, and in pinned host memory
+    // (copied there only when a caller reads them on the host).
     float *dev_rows = nullptr, *host_rows = nullptr;
     int rows_cap = 0, rows_valid = 0;
+    bool host_fresh = false;
+    // GPU picks over those rows: top-k / argmax scratch and results, for up to
+    // rows_cap rows of PICK_K candidates (allocated with the rows).
+    void *pick_scratch = nullptr;
+    float *pick_v = nullptr;
+    int32_t *pick_i = nullptr;
     int32_t *pinned_ids = nullptr;  // [n_ctx + 1]
     hipGraphExec_t graph[N_GRAPHS] = {nullptr, nullptr, nullptr};
     bool graphs_stale = true;
@@ -403,18 +409,45 @@ int launch_token(ts5hip_model *m, int g) {
     return TS5HIP_OK;
 }
 
+// Candidates per row of a GPU pick: top-k with k <= PICK_K - 1, plus one more
+// to see whether the k-th value is tied with the next.
+constexpr int PICK_K = 64;
+
+void free_rows(ts5hip_model *m) {
+    if (m->dev_rows) (void)hipFree(m->dev_rows);
+    if (m->host_rows) (void)hipHostFree(m->host_rows);
+    if (m->pick_scratch) (void)hipFree(m->pick_scratch);
+    if (m->pick_v) (void)hipFree(m->pick_v);
+    if (m->pick_i) (void)hipFree(m->pick_i);
+    m->dev_rows = nullptr, m->host_rows = nullptr, m->pick_scratch = nullptr, m->pick_v = nullptr;
+    m->pick_i = nullptr, m->rows_cap = 0, m->rows_valid = 0, m->host_fresh = false;
+}
+
 int ensure_rows(ts5hip_model *m, int rows) {
     if (rows <= m->rows_cap) return TS5HIP_OK;
     ts5hip_ctx *ctx = m->ctx;
     TS5_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    if (m->dev_rows) TS5_HIP(ctx, hipFree(m->dev_rows));
-    if (m->host_rows) TS5_HIP(ctx, hipHostFree(m->host_rows));
-    m->dev_rows = nullptr, m->host_rows = nullptr, m->rows_cap = 0, m->rows_valid = 0;
+    free_rows(m);
     const int cap = std::max(rows, 8);
     const size_t bytes = (size_t)cap * m->hp.n_vocab * 4;
+    const size_t pick = std::max(topk_scratch_bytes(cap), argmax_scratch_bytes(cap));
     TS5_HIP(ctx, hipMalloc((void **)&m->dev_rows, bytes));
     TS5_HIP(ctx, hipHostMalloc((void **)&m->host_rows, bytes, hipHostMallocDefault));
+    TS5_HIP(ctx, hipMalloc(&m->pick_scratch, pick));
+    TS5_HIP(ctx, hipMalloc((void **)&m->pick_v, (size_t)cap * PICK_K * 4));
+    TS5_HIP(ctx, hipMalloc((void **)&m->pick_i, (size_t)cap * PICK_K * 4));
     m->rows_cap = cap;
+    return TS5HIP_OK;
+}
+
+// The last forward's logits rows in pinned host memory (copied on first use).
+int host_rows_ready(ts5hip_model *m) {
+    if (m->host_fresh || !m->rows_valid) return TS5HIP_OK;
+    ts5hip_ctx *ctx = m->ctx;
+    TS5_HIP(ctx, hipMemcpyAsync(m->host_rows, m->dev_rows, (size_t)m->rows_valid * m->hp.n_vocab * 4,
+                                hipMemcpyDeviceToHost, ctx->stream));
+    TS5_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    m->host_fresh = true;
     return TS5HIP_OK;
 }
 
@@ -563,9 +596,6 @@ int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool wan
         }
         TS5_HIP(ctx, launch_set_pos(m->state, pos0 + n, s));
     }
-    if (rows) {
-        TS5_HIP(ctx, hipMemcpyAsync(m->host_rows, m->dev_rows, rows * row_bytes, hipMemcpyDeviceToHost, s));
-    }
     if (m->profile) TS5_HIP(ctx, hipEventRecord(ctx->ev1, s));
     TS5_HIP(ctx, hipStreamSynchronize(s));
     if (m->profile) {
@@ -574,6 +604,7 @@ int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool wan
         m->prof_ms += ms, m->prof_calls++, m->prof_tokens += n;
     }
     m->rows_valid = rows;
+    m->host_fresh = false;
     return TS5HIP_OK;
 }
 
@@ -582,6 +613,54 @@ int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool wan
 namespace ts5hip {
 int model_vocab(const ts5hip_model *m) { return m->hp.n_vocab; }
 ts5hip_ctx *model_ctx(const ts5hip_model *m) { return m->ctx; }
+
+int model_pick_rows(ts5hip_model *m, int row0, int nrows, float temperature, int top_k, RowPicks &pk) {
+    ts5hip_ctx *ctx = m->ctx;
+    const int nv = m->hp.n_vocab;
+    if (row0 < 0 || nrows < 1 || row0 + nrows > m->rows_valid)
+        return fail(ctx, TS5HIP_ERR_STATE, "rows %d..%d of %d logits rows", row0, row0 + nrows, m->rows_valid);
+    const float *rows = m->dev_rows + (size_t)row0 * nv;
+    pk.row0 = row0, pk.nrows = nrows, pk.k = 0, pk.kk = 0;
+    if (temperature <= 0) {
+        pk.mode = PICK_GREEDY;
+        pk.id.resize((size_t)nrows);
+        TS5_HIP(ctx, launch_argmax(rows, nv, nrows, m->pick_scratch, m->pick_i, nullptr, nullptr, ctx->stream));
+        TS5_HIP(ctx, hipMemcpyAsync(pk.id.data(), m->pick_i, (size_t)nrows * 4, hipMemcpyDeviceToHost, ctx->stream));
+        TS5_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        return TS5HIP_OK;
+    }
+    const int k = top_k > 0 ? std::min(top_k, nv) : nv;
+    if (k + 1 <= PICK_K && k < nv && nv <= topk_max_n()) {
+        pk.mode = PICK_TOPK, pk.k = k, pk.kk = k + 1;
+        pk.v.resize((size_t)nrows * pk.kk);
+        pk.id.resize((size_t)nrows * pk.kk);
+        TS5_HIP(ctx, launch_topk(rows, nv, pk.kk, nrows, m->pick_scratch, m->pick_v, m->pick_i, ctx->stream));
+        TS5_HIP(ctx, hipMemcpyAsync(pk.v.data(), m->pick_v, pk.v.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
+        TS5_HIP(ctx, hipMemcpyAsync(pk.id.data(), m->pick_i, pk.id.size() * 4, hipMemcpyDeviceToHost, ctx->stream));
+        TS5_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        return TS5HIP_OK;
+    }
+    pk.mode = PICK_HOST;
+    return host_rows_ready(m);
+}
+
+int32_t model_draw(ts5hip_model *m, ts5hip_sampler *s, const RowPicks &pk, int i, float temperature, float top_p,
+                   int top_k) {
+    const int nv = m->hp.n_vocab;
+    if (i < 0 || i >= pk.nrows) return fail(m->ctx, TS5HIP_ERR_ARG, "pick %d of %d", i, pk.nrows);
+    if (pk.mode == PICK_GREEDY) return pk.id[(size_t)i];
+    if (pk.mode == PICK_TOPK) {
+        // Distinct values through the (k+1)-th: the candidate set and its order
+        // are the only ones Engine::sample's heap can produce. A tie or a NaN
+        // leaves them to the heap's own order: the whole row, on the host.
+        const float *v = pk.v.data() + (size_t)i * pk.kk;
+        bool distinct = !std::isnan(v[0]);
+        for (int j = 1; j < pk.kk && distinct; j++) distinct = !std::isnan(v[j]) && v[j] != v[j - 1];
+        if (distinct) return ts5hip_sampler_draw(s, pk.id.data() + (size_t)i * pk.kk, v, pk.k, temperature, top_p);
+    }
+    if (int rc = host_rows_ready(m)) return rc;
+    return sample_host_row(s, m->host_rows + (size_t)(pk.row0 + i) * nv, nv, temperature, top_p, top_k);
+}
 }  // namespace ts5hip
 
 extern "C" {
@@ -620,8 +699,7 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
         (rc = alloc_t(m, F, &m->ffn)) || (rc = alloc_t(m, hp->n_vocab, &m->logits)) ||
         (rc = alloc_t(m, attn_partial_bytes(1, 64, H, HKV, HD) / 4, &m->part)) ||
         (rc = alloc_t(m, HKV * CTR_STRIDE + ARGMAX_CTR_INTS, &m->counters)) ||
-        (rc = alloc(m, matvec_argmax_scratch_bytes(), &m->amax)) || (rc = alloc(m, topk_scratch_bytes(), &m->topk)) ||
-        (rc = alloc_t(m, 64, &m->topk_v)) || (rc = alloc_t(m, 64, &m->topk_i)) ||
+        (rc = alloc(m, matvec_argmax_scratch_bytes(), &m->amax)) ||
         (rc = alloc_t(m, (size_t)n_ctx + 1, &m->seq)) || (rc = alloc_t(m, 4, &m->state))) {
         ts5hip_model_destroy(m);
         return rc;
@@ -650,8 +728,7 @@ void ts5hip_model_destroy(ts5hip_model *m) {
     for (auto &g : m->graph)
         if (g) (void)hipGraphExecDestroy(g);
     for (void *p : m->allocs) (void)hipFree(p);
-    if (m->dev_rows) (void)hipFree(m->dev_rows);
-    if (m->host_rows) (void)hipHostFree(m->host_rows);
+    free_rows(m);
     if (m->pinned_ids) (void)hipHostFree(m->pinned_ids);
     delete m;
 }
@@ -674,7 +751,10 @@ int ts5hip_model_synth_tensor(ts5hip_model *m, const char *name, uint32_t type, 
 int ts5hip_forward(ts5hip_model *m, const int32_t *tokens, int n, int pos0, float *logits, int all_logits) {
     if (!m) return fail(nullptr, TS5HIP_ERR_ARG, "null model");
     if (int rc = run_tokens(m, tokens, n, pos0, logits != nullptr, all_logits != 0)) return rc;
-    if (logits) std::memcpy(logits, m->host_rows, (size_t)m->rows_valid * m->hp.n_vocab * 4);
+    if (logits) {
+        if (int rc = host_rows_ready(m)) return rc;
+        std::memcpy(logits, m->host_rows, (size_t)m->rows_valid * m->hp.n_vocab * 4);
+    }
     return TS5HIP_OK;
 }
 
@@ -683,7 +763,13 @@ int ts5hip_forward_in_place(ts5hip_model *m, const int32_t *tokens, int n, int p
     return run_tokens(m, tokens, n, pos0, true, all_logits != 0);
 }
 
-const float *ts5hip_logits_view(const ts5hip_model *m) { return m && m->rows_valid ? m->host_rows : nullptr; }
+const float *ts5hip_logits_view(const ts5hip_model *m) {
+    if (!m || !m->rows_valid) return nullptr;
+    // The rows are copied to the host here, on first use after a forward: a
+    // caller that samples on the GPU (ts5hip_logits_topk) never pays for it.
+    if (host_rows_ready(const_cast<ts5hip_model *>(m)) != TS5HIP_OK) return nullptr;
+    return m->host_rows;
+}
 int ts5hip_n_ctx(const ts5hip_model *m) { return m ? m->n_ctx : 0; }
 int ts5hip_kv_type(const ts5hip_model *m) { return m ? m->kv_type : -1; }
 
@@ -695,26 +781,25 @@ int ts5hip_token_path(ts5hip_model *m) {
 
 int32_t ts5hip_model_sample(ts5hip_model *m, ts5hip_sampler *s, int row, float temperature, float top_p, int top_k) {
     if (!m || !s) return fail(m ? m->ctx : nullptr, TS5HIP_ERR_ARG, "null argument");
+    if (row < 0 || row >= m->rows_valid) return fail(m->ctx, TS5HIP_ERR_ARG, "row %d of %d", row, m->rows_valid);
+    RowPicks pk;
+    if (int rc = model_pick_rows(m, row, 1, temperature, top_k, pk)) return rc;
+    return model_draw(m, s, pk, 0, temperature, top_p, top_k);
+}
+
+int ts5hip_logits_topk(ts5hip_model *m, int row0, int nrows, int k, float *vals, int32_t *ids) {
+    if (!m || !vals || !ids) return fail(m ? m->ctx : nullptr, TS5HIP_ERR_ARG, "null argument");
+    if (row0 < 0 || nrows < 1 || row0 + nrows > m->rows_valid)
+        return fail(m->ctx, TS5HIP_ERR_ARG, "rows %d..%d of %d", row0, row0 + nrows, m->rows_valid);
+    if (k < 1 || k > PICK_K || k > m->hp.n_vocab || m->hp.n_vocab > topk_max_n())
+        return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "top-%d of %d logits", k, m->hp.n_vocab);
     ts5hip_ctx *ctx = m->ctx;
-    if (row < 0 || row >= m->rows_valid) return fail(ctx, TS5HIP_ERR_ARG, "row %d of %d", row, m->rows_valid);
-    const int nv = m->hp.n_vocab;
-    const float *dl = m->dev_rows + (size_t)row * nv;
-    if (temperature <= 0) {
-        TS5_HIP(ctx, launch_argmax(dl, nv, 1, m->amax, m->state + 1, nullptr, nullptr, ctx->stream));
-        int32_t id = 0;
-        if (int rc = ts5hip_download(ctx, &id, m->state + 1, 4)) return rc;
-        return id;
-    }
-    if (top_k > 0 && top_k <= topk_max() && nv <= topk_max_n()) {
-        TS5_HIP(ctx, launch_topk(dl, nv, top_k, m->topk, m->topk_v, m->topk_i, ctx->stream));
-        float v[64];
-        int32_t id[64];
-        if (int rc = ts5hip_download(ctx, v, m->topk_v, (size_t)top_k * 4)) return rc;
-        if (int rc = ts5hip_download(ctx, id, m->topk_i, (size_t)top_k * 4)) return rc;
-        return ts5hip_sampler_draw(s, id, v, top_k, temperature, top_p);
-    }
-    // No top-k, or a k beyond the GPU reduction: the whole row, on the host.
-    return sample_host_row(s, m->host_rows + (size_t)row * nv, nv, temperature, top_p, top_k);
+    TS5_HIP(ctx, launch_topk(m->dev_rows + (size_t)row0 * m->hp.n_vocab, m->hp.n_vocab, k, nrows, m->pick_scratch,
+                             m->pick_v, m->pick_i, ctx->stream));
+    TS5_HIP(ctx, hipMemcpyAsync(vals, m->pick_v, (size_t)nrows * k * 4, hipMemcpyDeviceToHost, ctx->stream));
+    TS5_HIP(ctx, hipMemcpyAsync(ids, m->pick_i, (size_t)nrows * k * 4, hipMemcpyDeviceToHost, ctx->stream));
+    TS5_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return TS5HIP_OK;
 }
 
 int ts5hip_generate_greedy(ts5hip_model *m, int32_t token, int pos, int n_steps, int32_t *ids_out) {

@@ -110,38 +110,43 @@ __device__ inline void bitonic(float *v, int *ix) {
     __syncthreads();
 }
 
+// grid (TOPK_WG, rows): workgroup x of row y sorts its slice of that row.
 __global__ __launch_bounds__(256) void k_topk_part(const float *__restrict__ x, int n, int k, float *__restrict__ cv,
                                                    int *__restrict__ ci) {
     __shared__ float v[TOPK_SLICE];
     __shared__ int ix[TOPK_SLICE];
+    const float *xr = x + (int64_t)blockIdx.y * n;
     const int per = (n + gridDim.x - 1) / gridDim.x;
     const int lo = blockIdx.x * per;
     for (int t = threadIdx.x; t < TOPK_SLICE; t += 256) {
         const int g = lo + t;
         const bool ok = t < per && g < n;
-        v[t] = ok ? x[g] : -INFINITY;
+        v[t] = ok ? xr[g] : -INFINITY;
         ix[t] = ok ? g : INT_MAX;
     }
     bitonic<TOPK_SLICE>(v, ix);
+    const int64_t o = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * k;
     for (int t = threadIdx.x; t < k; t += 256) {
-        cv[blockIdx.x * k + t] = v[t];
-        ci[blockIdx.x * k + t] = ix[t];
+        cv[o + t] = v[t];
+        ci[o + t] = ix[t];
     }
 }
 
+// One workgroup per row: the row's TOPK_WG * k candidates sorted, the best k out.
 __global__ __launch_bounds__(256) void k_topk_final(const float *__restrict__ cv, const int *__restrict__ ci, int nc,
                                                     int k, float *__restrict__ out_v, int32_t *__restrict__ out_i) {
     constexpr int N = TOPK_WG * TOPK_MAX;
     __shared__ float v[N];
     __shared__ int ix[N];
+    const int64_t o = (int64_t)blockIdx.x * nc;
     for (int t = threadIdx.x; t < N; t += 256) {
-        v[t] = t < nc ? cv[t] : -INFINITY;
-        ix[t] = t < nc ? ci[t] : INT_MAX;
+        v[t] = t < nc ? cv[o + t] : -INFINITY;
+        ix[t] = t < nc ? ci[o + t] : INT_MAX;
     }
     bitonic<N>(v, ix);
     for (int t = threadIdx.x; t < k; t += 256) {
-        out_v[t] = v[t];
-        out_i[t] = ix[t];
+        out_v[(int64_t)blockIdx.x * k + t] = v[t];
+        out_i[(int64_t)blockIdx.x * k + t] = ix[t];
     }
 }
 
@@ -170,15 +175,17 @@ hipError_t launch_set_pos(int32_t *pos, int32_t v, hipStream_t s) {
     return hipGetLastError();
 }
 
-size_t topk_scratch_bytes() { return (size_t)TOPK_WG * TOPK_MAX * 8; }
+size_t topk_scratch_bytes(int rows) { return (size_t)rows * TOPK_WG * TOPK_MAX * 8; }
 int topk_max() { return TOPK_MAX; }
 int topk_max_n() { return TOPK_WG * TOPK_SLICE; }
 
-hipError_t launch_topk(const float *x, int n, int k, void *scratch, float *vals, int32_t *ids, hipStream_t s) {
+hipError_t launch_topk(const float *x, int n, int k, int rows, void *scratch, float *vals, int32_t *ids,
+                       hipStream_t s) {
+    if (rows < 1 || k < 1 || k > TOPK_MAX || n > TOPK_WG * TOPK_SLICE) return hipErrorInvalidValue;
     float *cv = (float *)scratch;
-    int *ci = (int *)((char *)scratch + (size_t)TOPK_WG * TOPK_MAX * 4);
-    hipLaunchKernelGGL(k_topk_part, dim3(TOPK_WG), dim3(256), 0, s, x, n, k, cv, ci);
-    hipLaunchKernelGGL(k_topk_final, dim3(1), dim3(256), 0, s, cv, ci, TOPK_WG * k, k, vals, ids);
+    int *ci = (int *)((char *)scratch + (size_t)rows * TOPK_WG * TOPK_MAX * 4);
+    hipLaunchKernelGGL(k_topk_part, dim3(TOPK_WG, rows), dim3(256), 0, s, x, n, k, cv, ci);
+    hipLaunchKernelGGL(k_topk_final, dim3(rows), dim3(256), 0, s, cv, ci, TOPK_WG * k, k, vals, ids);
     return hipGetLastError();
 }
 

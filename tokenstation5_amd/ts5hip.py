@@ -83,6 +83,7 @@ _SIGS = {
     "ts5hip_kv_type": (_i32, [_vp]),
     "ts5hip_token_path": (_i32, [_vp]),
     "ts5hip_model_sample": (C.c_int32, [_vp, _vp, _i32, _f32, _f32, _i32]),
+    "ts5hip_logits_topk": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp]),
     "ts5hip_generate_greedy": (_i32, [_vp, C.c_int32, _i32, _i32, _vp]),
     "ts5hip_kv_read": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
     "ts5hip_take_profile": (_i32, [_vp, C.c_char_p, _i32]),
@@ -374,6 +375,13 @@ class Model:
         if r < 0:
             self.ctx.check(r)
         return int(r)
+
+    def logits_topk(self, row0: int, nrows: int, k: int):
+        """The k largest logits of rows row0.. of the last forward, found on the GPU: (vals, ids) [nrows][k]."""
+        v = np.empty((nrows, k), np.float32)
+        i = np.empty((nrows, k), np.int32)
+        self.ctx.check(lib().ts5hip_logits_topk(self.h, row0, nrows, k, v.ctypes.data, i.ctypes.data))
+        return v, i
 
     def generate_greedy(self, token: int, pos: int, n_steps: int) -> np.ndarray:
         out = np.empty(n_steps, np.int32)

@@ -49,34 +49,13 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def model_tensor_specs(hp: dict):
-    """(name, type, ne0, ne1) of every tensor (engine/src/model.cpp:89-119 names)."""
-    E, F, H, HKV, HD, V = (hp[k] for k in ("n_embd", "n_ff", "n_head", "n_head_kv", "head_dim", "n_vocab"))
-    wt = hp["wtype"]
-    yield "token_embd.weight", hp["embd_type"], E, V
-    yield "output_norm.weight", synth.F32, E, 1
-    if hp.get("head_type") is not None:
-        yield "output.weight", hp["head_type"], E, V
-    for i in range(hp["n_layer"]):
-        p = f"blk.{i}."
-        yield p + "attn_norm.weight", synth.F32, E, 1
-        yield p + "ffn_norm.weight", synth.F32, E, 1
-        yield p + "attn_q.weight", wt, E, H * HD
-        yield p + "attn_k.weight", wt, E, HKV * HD
-        yield p + "attn_v.weight", wt, E, HKV * HD
-        yield p + "attn_output.weight", wt, H * HD, E
-        yield p + "ffn_gate.weight", wt, E, F
-        yield p + "ffn_up.weight", wt, E, F
-        yield p + "ffn_down.weight", hp.get("down_type", wt), F, E
-
-
 def decode_bench(ctx, hp, steps: int, warmup: int, prompt_len: int = PROMPT):
     """The timed decode; also the prompt's prefill rate and the cost of a
     5-token verify batch (one token + 4 drafts, all logits) against one step."""
     n_ctx = prompt_len + max(steps, warmup) + 16
     m = ts5hip.Model(ctx, hp, n_ctx)
     t0 = time.time()
-    for name, t, ne0, ne1 in model_tensor_specs(hp):
+    for name, t, ne0, ne1 in synth.tensor_specs(hp):
         m.synth_tensor(name, t, ne0, ne1, SEED)
     ctx.sync()
     log(f"weights generated in HBM ({time.time() - t0:.1f} s)")
@@ -181,7 +160,7 @@ def prefill_only(hp, prompt_len: int = PROMPT):
     timed with HIP events on the library's stream."""
     ctx = ts5hip.Context(0)
     m = ts5hip.Model(ctx, hp, prompt_len + 16)
-    for name, t, ne0, ne1 in model_tensor_specs(hp):
+    for name, t, ne0, ne1 in synth.tensor_specs(hp):
         m.synth_tensor(name, t, ne0, ne1, SEED)
     prompt = np.random.default_rng(SEED).integers(0, hp["n_vocab"], prompt_len).astype(np.int32)
     m.forward(prompt[:256], 0, logits=False)

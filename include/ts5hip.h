@@ -30,7 +30,7 @@ extern "C" {
 
 /* GGML type ids (engine/src/gguf.h:12-16) with kernels here. */
 enum { TS5HIP_F32 = 0, TS5HIP_F16 = 1, TS5HIP_Q8_0 = 8, TS5HIP_Q4_K = 12, TS5HIP_Q6_K = 14 };
-/* KvType (engine/src/backend.h:13). Only Q8 is implemented on the GPU. */
+/* KvType (engine/src/backend.h:13). Q8 and F16 caches are implemented on the GPU. */
 enum { TS5HIP_KV_F32 = 0, TS5HIP_KV_F16 = 1, TS5HIP_KV_Q8 = 2 };
 
 typedef struct ts5hip_ctx ts5hip_ctx;
@@ -128,6 +128,13 @@ int ts5hip_rope_kv_append(ts5hip_ctx *ctx, const float *qkv, int ntok, const int
 int ts5hip_attn_decode(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n_head_kv, int head_dim,
                        const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx,
                        const int32_t *n_keys_dev, int kv_per_batch, float scale, int n_split, float *out);
+/* ts5hip_attn_decode over an f16 cache (KvType::F16, engine/src/backend.h:13; the reference's
+ * long-context attn_dec, engine/shaders/attn_dec.glsl, policy engine/src/vk_backend.cpp:958-960):
+ * k16 / v16 hold f16 values [n_head_kv][n_ctx][head_dim] (or B such caches with kv_per_batch),
+ * no scales; otherwise as ts5hip_attn_decode. */
+int ts5hip_attn_decode_f16(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n_head_kv, int head_dim,
+                           const void *k16, const void *v16, int n_ctx, const int32_t *n_keys_dev, int kv_per_batch,
+                           float scale, int n_split, float *out);
 /* Causal prompt attention on the matrix cores (attn_pf, engine/shaders/attn_pf.glsl with its
  * policy at engine/src/vk_backend.cpp:954-961; CPU engine/src/cpu_backend.cpp:222-248): nq
  * queries at positions pos0 .. pos0 + nq - 1 over one q8 cache (the layout above), query t
@@ -165,6 +172,11 @@ void ts5hip_model_destroy(ts5hip_model *m);
 /* A tensor from its GGUF bytes on the host. */
 int ts5hip_model_set_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, int64_t ne1,
                             const void *gguf);
+/* Rows [row0, row0 + nrows) of a tensor of ne1 rows from their GGUF bytes (a loader streaming
+ * a file through a bounded buffer; vectors are set whole). The tensor counts as set once its
+ * last rows are. */
+int ts5hip_model_set_tensor_rows(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, int64_t ne1,
+                                 int64_t row0, int64_t nrows, const void *gguf);
 /* A tensor generated in HBM (ts5hip_weight_synth). */
 int ts5hip_model_synth_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, int64_t ne1,
                               uint64_t seed, int centered);
@@ -204,8 +216,68 @@ int ts5hip_generate_greedy(ts5hip_model *m, int32_t token, int pos, int n_steps,
 /* K (which 0) or V (1) of `layer` at positions [pos0, pos0+n), dequantized to fp32
  * [n][n_head_kv * head_dim] (the CPU cache's layout, engine/src/cpu_backend.cpp:95-97). */
 int ts5hip_kv_read(ts5hip_model *m, int layer, int which, int pos0, int n, float *out);
+/* The reverse of ts5hip_kv_read, for tests: fp32 K (which 0) or V (1) values [n][n_head_kv *
+ * head_dim] stored at positions [pos0, pos0 + n) of `layer`, rounded as the cache keeps them (q8 as
+ * round_kv, engine/src/cpu_backend.cpp:78-90, or f16): values already so rounded are stored
+ * exactly. No counterpart in the reference (its Backend exposes no cache). */
+int ts5hip_kv_write(ts5hip_model *m, int layer, int which, int pos0, int n, const float *in);
 /* Backend::take_profile (engine/src/backend.h:40-43): text since the last call. */
 int ts5hip_take_profile(ts5hip_model *m, char *buf, int len);
+
+/* ---- GGUF files, KV sizing (engine/src/backend.h:53-81, engine/src/model.cpp:13-138,
+ * engine/src/vk_backend.cpp:531-600, :620-648, :1364-1402) ---- */
+
+/* kv_bytes_per_token (engine/src/backend.h:56): bytes of K and V per token of context over all
+ * layers in a cache of kv_type (q8: a byte per value and an f16 scale per 32). */
+uint64_t ts5hip_kv_bytes_per_token(const ts5hip_hparams *hp, int kv_type);
+/* fit_context (engine/src/backend.h:72): the context that fits in `memory` beside `used` bytes and
+ * 1 GiB kept for everything else, a multiple of 1024 up to cap; 0 if not even 1024 tokens fit. */
+int ts5hip_fit_context(uint64_t memory, uint64_t used, uint64_t per_token, int cap);
+/* f16_reaches (engine/src/backend.h:76): whether an f16 context of f16_ctx tokens is the whole
+ * training context (then a q8 request gets an f16 cache). */
+int ts5hip_f16_reaches(int f16_ctx, int train);
+/* The hyperparameters of a GGUF file as Model::open derives them (engine/src/model.cpp:13-68; llama,
+ * mistral, qwen2, qwen3), its training context, and the HBM bytes the model takes beside its KV
+ * cache (weights in their HBM layouts, activations, scratch). */
+int ts5hip_gguf_hparams(const char *path, ts5hip_hparams *hp, int *n_ctx_train, int64_t *fixed_bytes);
+/* make_vk_backend(Model&, path, n_ctx, device, err) for HIP with the file included
+ * (engine/src/backend.h:82; Model::open + load, engine/src/model.cpp:13-138; the weight upload,
+ * engine/src/vk_backend.cpp:531-600): the model of a GGUF file with a cache of n_ctx positions,
+ * its tensors read by `threads` workers (<= 0: 4) with pread into pinned buffers while earlier
+ * slices go to HBM. n_ctx 0: the context that fits the device's free memory, at most the training
+ * context (engine/src/vk_backend.cpp:620-648), and a q8 request gets an f16 cache when f16
+ * reaches the training context. kv_type_out (may be null): the cache type chosen. */
+int ts5hip_model_load(ts5hip_ctx *ctx, const char *path, int n_ctx, int kv_type, int threads, ts5hip_model **out,
+                      int *kv_type_out);
+
+/* ---- ts5 check (engine/src/checks.h, engine/src/checks.cpp:22-160) ---- */
+
+/* CheckResult (engine/src/checks.h:17-24). */
+typedef struct {
+    int32_t n, same_top, worst; /* worst: the position of max_diff */
+    double max_diff, rel, gpu_ms;
+    int32_t pass, saved; /* saved: the reference logits came from a .ts5ref file */
+} ts5hip_check_result;
+/* The check's n test tokens (engine/src/checks.cpp:22-26): 1000 + (i * 7919) % (n_vocab - 1000). */
+int ts5hip_check_tokens(int n, int n_vocab, int32_t *out);
+/* A model file's id in .ts5ref files (engine/src/checks.cpp:40-50): its size and the FNV-1a hash of
+ * its first MiB. */
+int ts5hip_model_file_id(const char *path, uint64_t *size, uint64_t *hash);
+/* Where a model's saved reference logits live (engine/src/checks.cpp:56-58): MODEL.ts5ref for an
+ * f16 cache, MODEL.q8.ts5ref, MODEL.f32.ts5ref. */
+int ts5hip_ref_path(const char *model_path, int kv_type, char *out, int len);
+/* load_ref / save_ref (engine/src/checks.cpp:78-110) in the reference's file format: the first n
+ * positions' logits [n][n_vocab] of a file of this model (size and hash), cache type and at least
+ * n positions; saving keeps a file that already holds more positions. */
+int ts5hip_ref_load(const char *model_path, int n, int n_vocab, int kv_type, float *logits);
+int ts5hip_ref_save(const char *model_path, int n, int n_vocab, int kv_type, const float *logits);
+/* run_check (engine/src/checks.cpp:112-160) on model m: the n test tokens as n - min(4, n/2)
+ * positions in one call with every position's logits, then the rest one token per call; against
+ * ref_logits ([n][n_vocab], ts5's CPU backend with the same cache rounding) or, when null, the
+ * saved file of model_path. Passes when max |diff| is under 0.5 % of the largest reference logit
+ * (2 % with a q8 cache). */
+int ts5hip_check_run(ts5hip_model *m, const char *model_path, int n, const float *ref_logits,
+                     ts5hip_check_result *r);
 
 /* ---- the decode driver: Engine (engine/src/engine.h:33-66) over this backend ---- */
 

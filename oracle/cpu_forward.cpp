@@ -46,7 +46,26 @@ int ts5o_matmul(uint32_t type, const void *W, int64_t rb, int64_t n_in, int64_t 
         std::vector<float> w((size_t)n_in);
         for (int64_t r = t; r < n_out; r += nt) {
             ts5o_dequantize_row(type, base + r * rb, w.data(), n_in);
-            for (int j = 0; j < n; j++) {
+            // Four tokens' sums side by side: each is still one chain of fp64
+            // adds in index order (the products are exact), so every result is
+            // the reference's bit for bit; the chains only overlap in time.
+            int j = 0;
+            for (; j + 4 <= n; j += 4) {
+                const float *x0 = X + (size_t)j * n_in, *x1 = x0 + n_in, *x2 = x1 + n_in, *x3 = x2 + n_in;
+                double a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+                for (int64_t i = 0; i < n_in; i++) {
+                    const double wi = w[i];
+                    a0 += wi * x0[i];
+                    a1 += wi * x1[i];
+                    a2 += wi * x2[i];
+                    a3 += wi * x3[i];
+                }
+                Y[(size_t)j * ystride + r] = (float)a0;
+                Y[(size_t)(j + 1) * ystride + r] = (float)a1;
+                Y[(size_t)(j + 2) * ystride + r] = (float)a2;
+                Y[(size_t)(j + 3) * ystride + r] = (float)a3;
+            }
+            for (; j < n; j++) {
                 const float *x = X + (size_t)j * n_in;
                 double acc = 0;
                 for (int64_t i = 0; i < n_in; i++) acc += (double)w[i] * x[i];

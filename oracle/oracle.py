@@ -243,6 +243,7 @@ def ref():
         L.ts5r_cpu_close.argtypes = [C.c_void_p]
         L.ts5r_sample_table.argtypes = [_f32p, C.c_int, C.c_int, C.c_float, C.c_float, C.c_int, C.c_uint64,
                                         C.c_int, _i32p]
+        L.ts5r_check.argtypes = [C.c_char_p, C.c_int, C.c_int, C.POINTER(C.c_double)]
         L.ts5r_generate.argtypes = [C.c_char_p, C.c_char_p, C.c_int, C.c_int, _i32p, C.c_int, C.c_float, C.c_float,
                                     C.c_int, C.c_uint64, C.c_int, C.c_int, _i32p, _i32p]
         _ref = L

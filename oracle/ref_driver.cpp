@@ -2,7 +2,7 @@
 //
 // A small C-ABI over ts5's own CPU code, compiled by oracle/Makefile from the
 // reference sources where they lie (engine/src/{gguf,quants,model,
-// cpu_backend,engine,tokenizer,log}.cpp) into oracle/_ref/libts5ref.so. It is
+// cpu_backend,engine,tokenizer,log,checks}.cpp) into oracle/_ref/libts5ref.so. It is
 // used only to write and check golden vectors; nothing of the reference is
 // copied into this repository.
 #include <cstdint>
@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "backend.h"
+#include "checks.h"
 #include "engine.h"
 #include "model.h"
 #include "quants.h"
@@ -51,6 +52,24 @@ public:
 private:
     const float *rows_;
     int n_rows_, nv_, n_ctx_, next_ = 0;
+};
+
+// The CPU backend with the KV rounding of `kv`, reporting that cache type
+// (CpuBackend itself reports F32), so run_check treats it as a GPU backend
+// with such a cache.
+class KvTagged : public Backend {
+public:
+    KvTagged(Backend *inner, KvType kv) : inner_(inner), kv_(kv) {}
+    const char *name() const override { return "cpu"; }
+    int n_ctx() const override { return inner_->n_ctx(); }
+    KvType kv_type() const override { return kv_; }
+    bool forward(const int32_t *t, int n, int pos0, float *logits, bool all, std::string &err) override {
+        return inner_->forward(t, n, pos0, logits, all, err);
+    }
+
+private:
+    std::unique_ptr<Backend> inner_;
+    KvType kv_;
 };
 
 // A token list whose pieces decode back to "<id>".
@@ -165,6 +184,20 @@ int ts5r_generate(const char *path, const char *draft_path, int n_ctx, int kv, c
         stats[2] = st.draft_accepted;
     }
     return parse_ids(text, out, max_tokens);
+}
+
+// ts5 check (run_check, engine/src/checks.cpp) of a GGUF model with the CPU
+// backend in the GPU's place: it writes the reference's logits for the n test
+// tokens next to the model (MODEL.gguf[.q8].ts5ref) as the reference saves
+// them. res: max_diff, rel, worst, same_top, pass.
+int ts5r_check(const char *path, int kv, int n, double *res) {
+    Model m;
+    if (!m.open(path, g_err) || !m.load(nullptr, g_err)) return -1;
+    KvTagged b(make_cpu_backend(m, n, kv_of(kv)), kv_of(kv));
+    CheckResult r;
+    if (!run_check(m, b, n, r, g_err, nullptr, true)) return -1;
+    res[0] = r.max_diff, res[1] = r.rel, res[2] = r.worst, res[3] = r.same_top, res[4] = r.pass;
+    return 0;
 }
 
 }  // extern "C"

@@ -12,6 +12,7 @@ The reference runs here only; its files never travel with the fixtures.
 """
 from __future__ import annotations
 
+import ctypes as C
 import hashlib
 import json
 import os
@@ -135,7 +136,7 @@ def golden_models():
             digests = {k: sha(v[3]) for k, v in tensors.items()}
             nv = hp["n_vocab"]
             res = {}
-            for kv in (0, 2):
+            for kv in (0, 1, 2):
                 toks, lg = check_schedule(R, path, 12, kv, nv)
                 res[f"kv{kv}_tokens"] = toks
                 res[f"kv{kv}_logits"] = lg
@@ -148,10 +149,39 @@ def golden_models():
             assert n == 64, (n, R.ts5r_last_error())
             res["greedy_prompt"] = prompt
             res["greedy_q8_ids"] = ids
+            # The same with an f16 cache (KvType::F16, the Vulkan backend's default).
+            ids16 = np.zeros(64, np.int32)
+            n = R.ts5r_generate(path.encode(), b"", 128, 1, prompt, prompt.size, 0.0, 0.95, 40, 1, 0, 64, ids16,
+                                stats)
+            assert n == 64, (n, R.ts5r_last_error())
+            res["greedy_f16_ids"] = ids16
             np.savez_compressed(os.path.join(OUT, f"model_{name}.npz"), **res)
             manifest[name] = dict(seed=MODEL_SEED, hparams={k: v for k, v in hp.items()}, tensor_sha256=digests)
     with open(os.path.join(OUT, "models.json"), "w") as f:
         json.dump(manifest, f, indent=1, sort_keys=True)
+
+
+# ts5 check's test tokens need a vocabulary past 1000 (engine/src/checks.cpp:22-26).
+TINY_CHECK = dict(synth.TINY_LLAMA_C, n_vocab=2048)
+CHECK_N = 16
+
+
+def golden_check():
+    """`ts5 check` run by the reference itself (run_check with its CPU backend
+    in the GPU's place) on a small GGUF: the .ts5ref files it saves next to
+    the model (f16 and q8 caches), byte for byte, and its result."""
+    R = oracle.ref()
+    res = {}
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "check.gguf")
+        write_model(TINY_CHECK, path)
+        res["gguf_sha"] = np.frombuffer(hashlib.sha256(open(path, "rb").read()).digest(), np.uint8)
+        for kv, suffix in ((1, ".ts5ref"), (2, ".q8.ts5ref")):
+            out = (C.c_double * 5)()
+            assert R.ts5r_check(path.encode(), kv, CHECK_N, out) == 0, R.ts5r_last_error()
+            res[f"kv{kv}_result"] = np.array(list(out), np.float64)
+            res[f"kv{kv}_file"] = np.frombuffer(open(path + suffix, "rb").read(), np.uint8)
+    np.savez_compressed(os.path.join(OUT, "check.npz"), **res)
 
 
 def sampler_table(seed: int, rows: int, nv: int) -> np.ndarray:
@@ -219,6 +249,7 @@ def main():
     golden_models()
     golden_sampler()
     golden_speculation()
+    golden_check()
     print("golden vectors written to", OUT)
 
 

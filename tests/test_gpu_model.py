@@ -36,10 +36,10 @@ def token_path(request, monkeypatch):
     return request.param
 
 
-def load(ctx, name, n_ctx):
+def load(ctx, name, n_ctx, kv=ts5hip.KV_Q8):
     hp = dict(MODELS[name]["hparams"])
     tensors = synth.model_tensors(hp, make_golden.MODEL_SEED)
-    m = ts5hip.Model(ctx, hp, n_ctx)
+    m = ts5hip.Model(ctx, hp, n_ctx, kv)
     m.set_tensors(tensors)
     want = "graphs" if os.environ.get("TS5HIP_GRAPHS") != "0" else "direct"
     assert m.token_path() == want
@@ -71,14 +71,35 @@ def test_check_schedule_logits(ctx, name):
     print(f"{name}: top-1 agreement {top:.3f}")
 
 
-@pytest.mark.parametrize("name", ["tiny_llama_c", "tiny_draft_c"])
-def test_greedy_64_tokens_match_reference(ctx, name):
+@pytest.mark.parametrize("name", ["tiny_llama", "tiny_draft", "tiny_llama_c", "tiny_draft_c"])
+def test_check_schedule_logits_f16_cache(ctx, name):
+    """The same schedule with an f16 cache against the reference's f16 logits,
+    at the reference's bar for that cache (engine/src/checks.cpp:159: 5e-3 of
+    the largest logit)."""
+    hp, _, m = load(ctx, name, 64, ts5hip.KV_F16)
+    assert m.kv_type() == ts5hip.KV_F16
+    g = np.load(os.path.join(G, f"model_{name}.npz"))
+    toks, want = g["kv1_tokens"], g["kv1_logits"]
+    n = toks.size
+    got = np.empty_like(want)
+    got[:n - 4] = m.forward(toks[:n - 4], 0, all_logits=True)
+    for i in range(n - 4, n):
+        got[i] = m.forward(toks[i:i + 1], i)[0]
+    check_rows(got, want, tol=5e-3)
+
+
+@pytest.mark.parametrize("name,kv,key", [("tiny_llama_c", ts5hip.KV_Q8, "greedy_q8_ids"),
+                                         ("tiny_draft_c", ts5hip.KV_Q8, "greedy_q8_ids"),
+                                         ("tiny_llama_c", ts5hip.KV_F16, "greedy_f16_ids"),
+                                         ("tiny_draft_c", ts5hip.KV_F16, "greedy_f16_ids")])
+def test_greedy_64_tokens_match_reference(ctx, name, kv, key):
     """100 % argmax agreement over the first 64 generated tokens, with the
-    device-resident greedy loop (argmax feeding the next step)."""
-    hp, _, m = load(ctx, name, 128)
+    device-resident greedy loop (argmax feeding the next step), for q8 and
+    f16 caches."""
+    hp, _, m = load(ctx, name, 128, kv)
     g = np.load(os.path.join(G, f"model_{name}.npz"))
     prompt = g["greedy_prompt"]
-    want = list(g["greedy_q8_ids"])
+    want = list(g[key])
     m.forward(prompt[:-1], 0, logits=False)
     got = list(m.generate_greedy(int(prompt[-1]), prompt.size - 1, 64))
     div = next((i for i in range(64) if got[i] != want[i]), None)

@@ -74,20 +74,25 @@ def test_dequantize_bit_exact_random(ctx, t, ne0, rows):
 
 # ---- activations ----------------------------------------------------------------------
 
+XQ_MAX = 2 ** 22 - 1
+
+
 def act_unpack(buf, n, ntok=1):
-    """(x16 values, scale, sum, isum) of ntok activations from the device."""
+    """(X values, scale, sum, isum) of ntok activations from the device:
+    X = 65536 hi + 256 mid + lo from the three int8 planes."""
     ab = ts5hip.Context.act_bytes(n)
     raw = buf.download(np.uint8)[:ab * ntok].reshape(ntok, ab)
     al = lambda v: -(-v // 256) * 256  # noqa: E731
-    hi = raw[:, :n].view(np.int8).astype(np.int32)
-    lo = raw[:, al(n):al(n) + n].view(np.int8).astype(np.int32)
-    o = 2 * al(n)
+    planes = [raw[:, k * al(n):k * al(n) + n].view(np.int8).astype(np.int64) for k in range(3)]
+    X = 65536 * planes[0] + 256 * planes[1] + planes[2]
+    assert np.abs(planes[0]).max() <= 64
+    o = 3 * al(n)
     sc = raw[:, o:o + n // 32 * 4].copy().view(np.float32)
     o += al(n // 32 * 4)
     sm = raw[:, o:o + n // 32 * 4].copy().view(np.float32)
     o += al(n // 32 * 4)
     isum = raw[:, o:o + n // 16 * 4].copy().view(np.int32)
-    return 256 * hi + lo, sc, sm, isum
+    return X, sc, sm, isum
 
 
 @pytest.mark.parametrize("n,norm", [(4096, True), (14336, False), (896, True)])
@@ -98,17 +103,17 @@ def test_act_quantize(ctx, n, norm):
     dx, dw = ctx.to_device(x), ctx.to_device(w)
     act = ctx.alloc(ctx.act_bytes(n))
     ctx.act_quantize(dx, dw if norm else None, 1e-5, n, 1, act)
-    x16, sc, sm, isum = act_unpack(act, n)
+    X, sc, sm, isum = act_unpack(act, n)
     ref = oracle.rmsnorm(x, w, 1e-5) if norm else x
     rb = ref.reshape(-1, 32)
-    assert np.abs(x16).max() <= 16383
-    # Per sub-block the scale is max|x| / 16383 and every value within half a step.
-    assert np.allclose(sc[0], np.abs(rb).max(1) / 16383, rtol=1e-5)
-    # Nearest step, up to the fp32 roundings of v * (16383 / amax) (a few ulp of |v|).
-    err = np.abs(x16[0].reshape(-1, 32) * sc[0][:, None].astype(np.float64) - rb)
+    assert np.abs(X).max() <= XQ_MAX
+    # Per sub-block the scale is max|x| / XQ_MAX and every value within half a step.
+    assert np.allclose(sc[0], np.abs(rb).max(1) / XQ_MAX, rtol=1e-5)
+    # Nearest step, up to the fp32 roundings of v * (XQ_MAX / amax) (a few ulp of |v|).
+    err = np.abs(X[0].reshape(-1, 32) * sc[0][:, None].astype(np.float64) - rb)
     assert np.all(err <= 0.5 * sc[0][:, None] + 4 * 2.0 ** -24 * np.abs(rb) + 1e-30)
     assert np.allclose(sm[0], rb.astype(np.float64).sum(1), rtol=1e-4, atol=1e-6 * np.abs(rb).max())
-    assert np.array_equal(isum[0], x16[0].reshape(-1, 16).sum(1))
+    assert np.array_equal(isum[0], X[0].reshape(-1, 16).sum(1))
 
 
 @pytest.mark.parametrize("n", [4096, 1000, 8192])  # one pass in registers up to 4096, else two passes
@@ -160,6 +165,30 @@ def test_matvec_centered_weights(ctx):
     got = run_matvec(ctx, synth.Q4_K, W, 4096, 512, x)
     want = oracle.matmul(synth.Q4_K, W, 4096, x)[0]
     assert rel_l2(got, want) <= REL_L2
+
+
+@pytest.mark.parametrize("t,ne0,rows,centered", [(synth.Q4_K, 4096, 2048, True), (synth.Q4_K, 14336, 512, True),
+                                                  (synth.Q4_K, 4096, 2048, False), (synth.Q6_K, 4096, 1024, False),
+                                                  (synth.Q8_0, 896, 1024, False)])
+def test_matvec_precision(ctx, t, ne0, rows, centered):
+    """The activation keeps 23 significant bits per 32 values (65536 hi +
+    256 mid + lo), the precision of the fp32 input the reference multiplies
+    (engine/src/cpu_backend.cpp:30): against the fp64-accumulated oracle the
+    one-token matvec and the several-token matmul (5 tokens, the verify
+    batch) stay within 2e-6 relative L2, far inside the 1e-3 bar, also on
+    zero-mean rows whose outputs cancel."""
+    W = synth.tensor(t, ne0, rows, 8, f"prec{t}_{ne0}", centered=centered)
+    rng = np.random.default_rng(ne0 + rows)
+    x = rng.standard_normal((5, ne0)).astype(np.float32)
+    got = run_matvec(ctx, t, W, ne0, rows, x[0])
+    want = oracle.matmul(t, W, ne0, x)
+    assert rel_l2(got, want[0]) <= 2e-6, rel_l2(got, want[0])
+    w = ctx.weight(t, ne0, rows, W)
+    y = ctx.alloc(5 * rows * 4)
+    ctx.matmul(t, w, ne0, rows, ctx.to_device(x), 5, y)
+    got5 = y.download(np.float32, (5, rows))
+    for k in range(5):
+        assert rel_l2(got5[k], want[k]) <= 2e-6, (k, rel_l2(got5[k], want[k]))
 
 
 def test_matvec_accumulate_and_scales(ctx):
@@ -300,6 +329,29 @@ def test_attention_vs_oracle(ctx, B, ctxlen, H, HKV, HD):
     for b in range(B):
         kc = deq[b].transpose(1, 0, 2).reshape(ctxlen, HKV * HD)
         vc = vdeq[b].transpose(1, 0, 2).reshape(ctxlen, HKV * HD)
+        want = oracle.attention(q[b], kc, vc, H, HKV, HD, ctxlen - 1, scale)
+        assert rel_l2(got[b], want) <= REL_L2, (b, rel_l2(got[b], want))
+
+
+@pytest.mark.parametrize("B,ctxlen,H,HKV,HD,n_split", [(1, 8192, 32, 8, 128, 0), (4, 8192, 32, 8, 128, 0),
+                                                       (16, 8192, 32, 8, 128, 0), (1, 32768, 32, 8, 128, 0),
+                                                       (4, 32768, 32, 8, 128, 0), (16, 32768, 32, 8, 128, 0),
+                                                       (2, 70, 14, 2, 64, 0), (1, 5000, 32, 8, 128, 64)])
+def test_attention_f16_vs_oracle(ctx, B, ctxlen, H, HKV, HD, n_split):
+    """cfg3's attention over an f16 cache (KvType::F16, the reference's
+    default; each value the nearest half of N(0,1)), long contexts included."""
+    rng = np.random.default_rng(B * 11 + ctxlen)
+    k = rng.standard_normal((B, HKV, ctxlen, HD), dtype=np.float32).astype(np.float16)
+    v = rng.standard_normal((B, HKV, ctxlen, HD), dtype=np.float32).astype(np.float16)
+    q = rng.standard_normal((B, H * HD)).astype(np.float32)
+    scale = float(np.float32(1) / np.sqrt(np.float32(HD)))
+    out = ctx.alloc(q.nbytes)
+    ctx.attn_decode_f16(ctx.to_device(q), B, H, HKV, HD, ctx.to_device(k), ctx.to_device(v), ctxlen,
+                        ctx.to_device(np.full(B, ctxlen, np.int32)), 1, scale, out, n_split=n_split)
+    got = out.download(np.float32, (B, H * HD))
+    for b in range(B):
+        kc = k[b].astype(np.float32).transpose(1, 0, 2).reshape(ctxlen, HKV * HD)
+        vc = v[b].astype(np.float32).transpose(1, 0, 2).reshape(ctxlen, HKV * HD)
         want = oracle.attention(q[b], kc, vc, H, HKV, HD, ctxlen - 1, scale)
         assert rel_l2(got[b], want) <= REL_L2, (b, rel_l2(got[b], want))
 

@@ -160,7 +160,7 @@ def _check_model(name):
     tensors = synth.model_tensors(hp, make_golden.MODEL_SEED)
     assert {k: sha(v[3]) for k, v in tensors.items()} == digests
     g = np.load(os.path.join(G, f"model_{name}.npz"))
-    for kv in (0, 2):
+    for kv in (0, 1, 2):  # f32, f16 and q8 caches
         toks, want = g[f"kv{kv}_tokens"], g[f"kv{kv}_logits"]
         m = oracle.Model(hp, tensors, 64, kv)
         n = toks.size
@@ -179,17 +179,18 @@ def test_model_logits_match_reference(name):
 
 
 @pytest.mark.parametrize("name", ["tiny_llama_c", "tiny_draft_c"])
-def test_greedy_decode_matches_reference(name):
+@pytest.mark.parametrize("kv,key", [(2, "greedy_q8_ids"), (1, "greedy_f16_ids")])
+def test_greedy_decode_matches_reference(name, kv, key):
     hp = dict(json.load(open(os.path.join(G, "models.json")))[name]["hparams"])
     g = np.load(os.path.join(G, f"model_{name}.npz"))
-    m = oracle.Model(hp, synth.model_tensors(hp, make_golden.MODEL_SEED), 128, 2)
+    m = oracle.Model(hp, synth.model_tensors(hp, make_golden.MODEL_SEED), 128, kv)
     prompt = g["greedy_prompt"]
     lg = m.forward(prompt, 0)[0]
     ids = []
     for i in range(64):
         ids.append(int(np.argmax(lg)))
         lg = m.forward(np.array([ids[-1]]), prompt.size + i)[0]
-    assert ids == list(g["greedy_q8_ids"])
+    assert ids == list(g[key])
 
 
 def test_sampler_matches_reference():

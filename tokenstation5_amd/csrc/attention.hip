@@ -29,7 +29,7 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float *__restrict__ qkv, i
                                                 const float *__restrict__ k_norm, float eps,
                                                 const float2 *__restrict__ rope_cs, int n_rot, int neox,
                                                 const int32_t *__restrict__ pos0p, int H, int HKV, int HD,
-                                                int n_ctx, float *__restrict__ q_out, KvLayer kv) {
+                                                int n_ctx, float *__restrict__ q_out, KvLayer kv, int kv_f16) {
     __shared__ float v[256];
     const int hh = blockIdx.x, t = blockIdx.y, i = threadIdx.x;
     const int pos = pos0p[0] + t;
@@ -63,8 +63,15 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float *__restrict__ qkv, i
         for (int j = i; j < HD; j += 64) dst[j] = v[j];
         return;
     }
-    // q8: per 32 values sc = f16(amax / 127), q = clamp(rint(v / sc), +-127).
     const int kvh = is_k ? hh - H : hh - H - HKV;
+    if (kv_f16) {  // f16: each value to the nearest half (engine/src/cpu_backend.cpp:80)
+        uint16_t *c16 = (uint16_t *)(is_k ? kv.k : kv.v);
+        const int64_t slot = (int64_t)kvh * n_ctx + pos;
+        if (2 * i < HD)
+            *(uint32_t *)(c16 + slot * HD + 2 * i) = (uint32_t)f2h(v[2 * i]) | (uint32_t)f2h(v[2 * i + 1]) << 16;
+        return;
+    }
+    // q8: per 32 values sc = f16(amax / 127), q = clamp(rint(v / sc), +-127).
     int8_t *q8 = is_k ? kv.k : kv.v;
     uint16_t *sc8 = is_k ? kv.ks : kv.vs;
     const int64_t slot = (int64_t)kvh * n_ctx + pos;
@@ -96,7 +103,7 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float *__restrict__ qkv, i
 #endif
 constexpr int ATTN_NT = TS5_ATTN_NT;  // threads per work item: 8 waves, two per SIMD
 
-template <int HD, int G>
+template <int HD, int G, bool F16>
 __global__ __launch_bounds__(ATTN_NT) void k_attn(const int8_t *k8, const uint16_t *ks, const int8_t *v8,
                                                   const uint16_t *vs, const int32_t *n_keys, int n_ctx, int HKV,
                                                   int flags, int n_split, AttnArgs tail) {
@@ -106,42 +113,84 @@ __global__ __launch_bounds__(ATTN_NT) void k_attn(const int8_t *k8, const uint16
                    const_cast<uint16_t *>(vs)};
     a.n_keys = n_keys, a.n_ctx = n_ctx, a.HKV = HKV;
     a.kv_per_batch = flags & 1, a.append = (flags >> 1) & 1, a.rope = (flags >> 2) & 1;
-    attn_slice<HD, G, ATTN_NT>(a, blockIdx.x, blockIdx.y, blockIdx.z, n_split, S);
+    attn_slice<HD, G, ATTN_NT, F16>(a, blockIdx.x, blockIdx.y, blockIdx.z, n_split, S);
 }
 
 // K (which 0) or V (1) at positions [pos0, pos0 + n) dequantized to fp32
 // [n][HKV * HD] (engine/src/cpu_backend.cpp:95-97's row layout).
-__global__ void k_kv_read(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, float *__restrict__ out) {
+__global__ void k_kv_read(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, int kv_f16,
+                          float *__restrict__ out) {
     const int64_t total = (int64_t)n * HKV * HD;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
         const int p = (int)(e / (HKV * HD)), h = (int)(e / HD % HKV), d = (int)(e % HD);
         const int64_t slot = (int64_t)h * n_ctx + pos0 + p;
-        const int8_t q = (which ? kv.v : kv.k)[slot * HD + d];
-        out[e] = (float)q * h2f((which ? kv.vs : kv.ks)[slot * (HD / 32) + d / 32]);
+        if (kv_f16) {
+            out[e] = h2f(((const uint16_t *)(which ? kv.v : kv.k))[slot * HD + d]);
+        } else {
+            const int8_t q = (which ? kv.v : kv.k)[slot * HD + d];
+            out[e] = (float)q * h2f((which ? kv.vs : kv.ks)[slot * (HD / 32) + d / 32]);
+        }
     }
 }
 
+// K (which 0) or V (1) values [n][HKV * HD] (fp32) into positions
+// [pos0, pos0 + n) of the cache, rounded as the cache keeps them (q8 per 32
+// values as round_kv, engine/src/cpu_backend.cpp:78-90, or f16). One wave per
+// (position, KV head), two values a lane.
+__global__ __launch_bounds__(64) void k_kv_write(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0,
+                                                 int kv_f16, const float *__restrict__ in) {
+    const int p = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
+    if (2 * i >= HD) return;
+    const float *src = in + ((int64_t)p * HKV + h) * HD;
+    const int64_t slot = (int64_t)h * n_ctx + pos0 + p;
+    const float a0 = src[2 * i], a1 = src[2 * i + 1];
+    if (kv_f16) {
+        *(uint32_t *)((uint16_t *)(which ? kv.v : kv.k) + slot * HD + 2 * i) =
+            (uint32_t)f2h(a0) | (uint32_t)f2h(a1) << 16;
+        return;
+    }
+    float amax = fmaxf(fabsf(a0), fabsf(a1));
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+    const uint16_t sh = f2h(amax / 127.0f);
+    const float sc = h2f(sh);
+    int q0 = 0, q1 = 0;
+    if (sc > 0.f) {
+        q0 = (int)fminf(127.f, fmaxf(-127.f, rintf(a0 / sc)));
+        q1 = (int)fminf(127.f, fmaxf(-127.f, rintf(a1 / sc)));
+    }
+    *(uint16_t *)((which ? kv.v : kv.k) + slot * HD + 2 * i) = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
+    if ((i & 15) == 0) (which ? kv.vs : kv.ks)[slot * (HD / 32) + i / 16] = sh;
+}
+
+hipError_t launch_kv_write(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, int kv_f16,
+                           const float *in, hipStream_t s) {
+    hipLaunchKernelGGL(k_kv_write, dim3(n, HKV), dim3(64), 0, s, kv, which, HKV, HD, n_ctx, pos0, kv_f16, in);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
-hipError_t launch_kv_read(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, float *out, hipStream_t s) {
-    hipLaunchKernelGGL(k_kv_read, dim3(256), dim3(256), 0, s, kv, which, HKV, HD, n_ctx, pos0, n, out);
+hipError_t launch_kv_read(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, int kv_f16, float *out,
+                          hipStream_t s) {
+    hipLaunchKernelGGL(k_kv_read, dim3(256), dim3(256), 0, s, kv, which, HKV, HD, n_ctx, pos0, n, kv_f16, out);
     return hipGetLastError();
 }
 
 hipError_t launch_rope_kv(const float *qkv, int64_t qkv_stride, const float *bias, const float *q_norm,
                           const float *k_norm, float eps, const float *rope_cs, int n_rot, int neox,
                           const int32_t *pos0, int H, int HKV, int HD, int n_ctx, int ntok, float *q_out, KvLayer kv,
-                          hipStream_t s) {
+                          int kv_f16, hipStream_t s) {
     hipLaunchKernelGGL(k_rope_kv, dim3(H + 2 * HKV, ntok), dim3(64), 0, s, qkv, qkv_stride, bias, q_norm, k_norm,
-                       eps, (const float2 *)rope_cs, n_rot, neox, pos0, H, HKV, HD, n_ctx, q_out, kv);
+                       eps, (const float2 *)rope_cs, n_rot, neox, pos0, H, HKV, HD, n_ctx, q_out, kv, kv_f16);
     return hipGetLastError();
 }
 
-template <int HD>
+template <int HD, bool F16>
 static hipError_t attn_launch(int G, dim3 grid, const AttnArgs &a, hipStream_t s) {
     const int flags = (a.kv_per_batch ? 1 : 0) | (a.append ? 2 : 0) | (a.rope ? 4 : 0);
 #define TS5_ATTN(GG)                                                                                          \
     case GG:                                                                                                  \
-        hipLaunchKernelGGL((k_attn<HD, GG>), grid, dim3(ATTN_NT), 0, s, (const int8_t *)a.kv.k,               \
+        hipLaunchKernelGGL((k_attn<HD, GG, F16>), grid, dim3(ATTN_NT), 0, s, (const int8_t *)a.kv.k,          \
                            (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs, a.n_keys, \
                            a.n_ctx, a.HKV, flags, (int)grid.x, a);                                           \
         break;
@@ -172,7 +221,9 @@ hipError_t launch_attn(const AttnIO &io, hipStream_t s) {
     a.H = io.H, a.HKV = io.HKV, a.n_keys = io.n_keys, a.scale = io.scale, a.part = io.part;
     a.counters = io.counters, a.out = io.out;
     const dim3 grid(io.n_split, io.HKV, io.B);
-    return io.HD == 128 ? attn_launch<128>(io.H / io.HKV, grid, a, s) : attn_launch<64>(io.H / io.HKV, grid, a, s);
+    const int G = io.H / io.HKV;
+    if (io.kv_f16) return io.HD == 128 ? attn_launch<128, true>(G, grid, a, s) : attn_launch<64, true>(G, grid, a, s);
+    return io.HD == 128 ? attn_launch<128, false>(G, grid, a, s) : attn_launch<64, false>(G, grid, a, s);
 }
 
 }  // namespace ts5hip

@@ -1,7 +1,8 @@
-// Device core of split-K flash decode over the q8 KV cache, shared by the
-// standalone kernel (attention.hip) and the whole-token persistent kernel
-// (decode.hip).
+// Device core of split-K flash decode over the KV cache (q8, or f16), used
+// by the kernels of attention.hip.
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -111,8 +112,9 @@ __device__ inline AttnSpan attn_span(const AttnArgs &a, int split, int kvh, int 
 // 1. The G query heads of KV head kvh (and, when the slice holds the new key,
 //    that token's K and V) into LDS, from q(e) = element e of the token's
 //    q|k|v row; bias, per-head norm and RoPE when a.rope; the new K and V
-//    rounded to q8 and stored at their cache slot.
-template <int HD, int G, int NT, class QLoad, class Lds>
+//    rounded as the cache keeps them (q8, or f16 with F16) and stored at
+//    their cache slot.
+template <int HD, int G, int NT, bool F16, class QLoad, class Lds>
 __device__ inline void attn_prepare(const AttnArgs &a, int kvh, const AttnSpan &sp, Lds &S, QLoad qload) {
     constexpr int NWV = NT / 64;
     auto &q_s = S.q_s;
@@ -161,7 +163,18 @@ __device__ inline void attn_prepare(const AttnArgs &a, int kvh, const AttnSpan &
         }
         __syncthreads();
     }
-    if (has_new && tid < 128) {
+    if (F16 && has_new && tid < 128) {
+        // f16 (engine/src/cpu_backend.cpp:80): each value rounded to the
+        // nearest f16. Wave 0 rounds K, wave 1 V, a pair per lane.
+        const int which = tid >> 6, i = tid & 63;
+        if (2 * i < HD) {
+            const uint32_t pair = (uint32_t)f2h(kv_s[which][2 * i]) | (uint32_t)f2h(kv_s[which][2 * i + 1]) << 16;
+            const int64_t slot = sp.head_base + pq;
+            *(uint32_t *)(S.new16[which] + 2 * i) = pair;
+            *(uint32_t *)((uint16_t *)(which ? a.kv.v : a.kv.k) + slot * HD + 2 * i) = pair;
+        }
+    }
+    if (!F16 && has_new && tid < 128) {
         // q8 (engine/src/cpu_backend.cpp:78-90): per 32 values sc = f16(amax / 127),
         // q = clamp(rint(v / sc), +-127). Wave 0 rounds K, wave 1 V, a pair per lane.
         const int which = tid >> 6, i = tid & 63;
@@ -213,6 +226,7 @@ struct SliceLds {
     float kv_s[2][HD];                    // the new token's K and V before rounding
     __align__(16) int8_t new8[2][HD];     // ... and after, as int8
     uint16_t new_sc[2][HD / 32];          // ... with their f16 scales
+    __align__(16) uint16_t new16[2][HD];  // ... or as f16 (an f16 cache)
     __align__(16) float o_s[NT / 64][G * HD];  // each wave's p * v sums
     __align__(16) float wts[G][ATTN_MAX_SPLIT];  // the merge's weight per (head, split), 0 past n_split
     int last;
@@ -228,18 +242,31 @@ struct SliceShape {
                   "attention slice shape");
 };
 
-template <int HD, int G, int NT>
+// The cache's values: q8 (int8 with an f16 scale per 32) or, with F16, f16
+// (2 bytes a value, no scales; ks / vs unused). A lane's 8 V dims are one
+// uint2 of int8 or one uint4 of f16.
+template <bool F16>
+using VRow = typename std::conditional<F16, uint4, uint2>::type;
+template <bool F16>
+__device__ inline float kv_value(const uint32_t *w, int e) {
+    if constexpr (F16) return h2f((w[e >> 1] >> (16 * (e & 1))) & 0xffff);
+    else return (float)(int8_t)((w[e >> 2] >> (8 * (e & 3))) & 0xff);
+}
+
+template <int HD, int G, int NT, bool F16 = false>
 __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, int n_split,
                                   SliceLds<HD, G, NT> &S) {
     using SH = SliceShape<HD, G, NT>;
     constexpr int NW = SH::NW, NQ = SH::NQ, KS = SH::KS, NPASS = SH::NPASS, LPV = SH::LPV, KPW = SH::KPW,
                   KPS = SH::KPS, NVS = SH::NVS, SMX = ATTN_KT / 64;
+    constexpr int VB = F16 ? 2 : 1;  // bytes per cached value
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kk = tid >> 2, qq = tid & 3;              // scores: key kk of a sweep, quarter qq of the dims
     const int vk = lane / LPV, vc = lane % LPV;         // p * v: key vk of a wave's step, dims 8 vc ..
     const AttnSpan sp = attn_span<16>(a, split, kvh, b, n_split);
-    const int8_t *kb = a.kv.k + sp.head_base * HD, *vb = a.kv.v + sp.head_base * HD;
-    const uint16_t *ksb = a.kv.ks + sp.head_base * (HD / 32), *vsb = a.kv.vs + sp.head_base * (HD / 32);
+    const int8_t *kb = a.kv.k + sp.head_base * HD * VB, *vb = a.kv.v + sp.head_base * HD * VB;
+    const uint16_t *ksb = F16 ? nullptr : a.kv.ks + sp.head_base * (HD / 32);
+    const uint16_t *vsb = F16 ? nullptr : a.kv.vs + sp.head_base * (HD / 32);
     float o[G][8];
 #pragma unroll
     for (int g = 0; g < G; g++)
@@ -249,25 +276,25 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
     for (int t0 = sp.p0; t0 < sp.p1 || !prepared; t0 += ATTN_KT) {
         const int nt = max(0, min(ATTN_KT, sp.p1 - t0));
         const int kmax = max(sp.p1 - 1, 0);  // loads past the slice read its last key (zero weight)
-        KRow<NQ> kr[NPASS];
+        KRow<NQ * VB> kr[NPASS];
         uint16_t ksr[NPASS];
 #pragma unroll
         for (int j = 0; j < NPASS; j++) {
             const int key = min(t0 + KS * j + kk, kmax);
-            kr[j] = load_krow<NQ>(kb + (int64_t)key * HD + qq * NQ);
-            ksr[j] = ksb[(int64_t)key * (HD / 32) + (qq * NQ) / 32];
+            kr[j] = load_krow<NQ * VB>(kb + ((int64_t)key * HD + qq * NQ) * VB);
+            if constexpr (!F16) ksr[j] = ksb[(int64_t)key * (HD / 32) + (qq * NQ) / 32];
         }
-        uint2 vr[NVS];
+        VRow<F16> vr[NVS];
         uint16_t vsr[NVS];
 #pragma unroll
         for (int s2 = 0; s2 < NVS; s2++) {
             const int key = min(t0 + s2 * KPS + wave * KPW + vk, kmax);
-            vr[s2] = *(const uint2 *)(vb + (int64_t)key * HD + 8 * vc);
-            vsr[s2] = vsb[(int64_t)key * (HD / 32) + (8 * vc) / 32];
+            vr[s2] = *(const VRow<F16> *)(vb + ((int64_t)key * HD + 8 * vc) * VB);
+            if constexpr (!F16) vsr[s2] = vsb[(int64_t)key * (HD / 32) + (8 * vc) / 32];
         }
         if (!prepared) {
             const float *row = a.q + (int64_t)b * a.q_stride;
-            attn_prepare<HD, G, NT>(a, kvh, sp, S, [&](int64_t e) { return row[e]; });
+            attn_prepare<HD, G, NT, F16>(a, kvh, sp, S, [&](int64_t e) { return row[e]; });
             prepared = true;
             if (nt == 0) break;
         }
@@ -276,21 +303,25 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
         for (int j = 0; j < NPASS; j++) {
             if (KS * j >= nt) break;
             const int idx = KS * j + kk, key = t0 + idx;
-            float ks = h2f(ksr[j]);
+            float ks = F16 ? 1.f : h2f(ksr[j]);
             if (sp.has_new && key == sp.pq) {
+                if constexpr (F16) {
 #pragma unroll
-                for (int c = 0; c < NQ / 4; c++) kr[j].w[c] = *(const uint32_t *)(S.new8[0] + qq * NQ + 4 * c);
-                ks = h2f(S.new_sc[0][(qq * NQ) / 32]);
+                    for (int c = 0; c < NQ / 2; c++) kr[j].w[c] = *(const uint32_t *)(S.new16[0] + qq * NQ + 2 * c);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < NQ / 4; c++) kr[j].w[c] = *(const uint32_t *)(S.new8[0] + qq * NQ + 4 * c);
+                    ks = h2f(S.new_sc[0][(qq * NQ) / 32]);
+                }
             }
             float acc[G];
 #pragma unroll
             for (int g = 0; g < G; g++) acc[g] = 0.f;
 #pragma unroll
             for (int e4 = 0; e4 < NQ / 4; e4++) {
-                const uint32_t w = kr[j].w[e4];
                 float kf[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) kf[i] = (float)(int8_t)((w >> (8 * i)) & 0xff) * ks;
+                for (int i = 0; i < 4; i++) kf[i] = kv_value<F16>(kr[j].w, 4 * e4 + i) * ks;
 #pragma unroll
                 for (int g = 0; g < G; g++) {
                     const float4 qv = *(const float4 *)&S.q_s[g][qq * NQ + 4 * e4];
@@ -346,18 +377,23 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
         for (int s2 = 0; s2 < NVS; s2++) {
             if (s2 * KPS >= nt) break;
             const int idx = s2 * KPS + wave * KPW + vk, key = t0 + idx;
-            uint2 v8 = vr[s2];
-            float vs = h2f(vsr[s2]);
+            VRow<F16> v8 = vr[s2];
+            float vs = F16 ? 1.f : h2f(vsr[s2]);
             if (sp.has_new && key == sp.pq) {
-                v8 = *(const uint2 *)(S.new8[1] + 8 * vc);
-                vs = h2f(S.new_sc[1][(8 * vc) / 32]);
+                if constexpr (F16) {
+                    v8 = *(const VRow<F16> *)(S.new16[1] + 8 * vc);
+                } else {
+                    v8 = *(const VRow<F16> *)(S.new8[1] + 8 * vc);
+                    vs = h2f(S.new_sc[1][(8 * vc) / 32]);
+                }
             }
             float w[G];
 #pragma unroll
             for (int g = 0; g < G; g++) w[g] = S.p_s[idx][g] * vs;  // idx < 64 * ceil(nt / 64): a written row
+            const uint32_t *vw = (const uint32_t *)&v8;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                const float vf = (float)(int8_t)((((e < 4) ? v8.x : v8.y) >> (8 * (e & 3))) & 0xff);
+                const float vf = kv_value<F16>(vw, e);
 #pragma unroll
                 for (int g = 0; g < G; g++) o[g][e] += w[g] * vf;
             }

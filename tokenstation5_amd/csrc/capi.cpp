@@ -306,29 +306,52 @@ int ts5hip_rope_kv_append(ts5hip_ctx *ctx, const float *qkv, int ntok, const int
                     head_dim, n_rot);
     const KvLayer kv{(int8_t *)k8, (uint16_t *)ks, (int8_t *)v8, (uint16_t *)vs};
     TS5_HIP(ctx, launch_rope_kv(qkv, (int64_t)(n_head + 2 * n_head_kv) * head_dim, bias, q_norm, k_norm, eps, rope_cs,
-                                n_rot, neox, pos0_dev, n_head, n_head_kv, head_dim, n_ctx, ntok, q_out, kv,
+                                n_rot, neox, pos0_dev, n_head, n_head_kv, head_dim, n_ctx, ntok, q_out, kv, 0,
                                 ctx->stream));
+    return TS5HIP_OK;
+}
+
+// The split-K decode attention with its partials and merge counters at
+// `part` / `counters`, or (null) in the context's growable scratch.
+static int attn_decode_into(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n_head_kv, int head_dim,
+                            const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx,
+                            const int32_t *n_keys_dev, int kv_per_batch, float scale, int n_split, float *out,
+                            float *part, int *counters, int kv_f16 = 0) {
+    if (!ctx || !q || !k8 || !v8 || (!kv_f16 && (!ks || !vs)) || !n_keys_dev || !out)
+        return fail(ctx, TS5HIP_ERR_ARG, "null argument");
+    if (B <= 0 || n_ctx <= 0 || !attn_supported(n_head, n_head_kv, head_dim))
+        return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "attention for %d/%d heads of %d", n_head, n_head_kv, head_dim);
+    if (B * n_head_kv > 4096) return fail(ctx, TS5HIP_ERR_ARG, "batch of %d x %d KV heads", B, n_head_kv);
+    if (n_split <= 0) n_split = attn_splits(B, n_head_kv, ctx->n_cu);
+    if (n_split > 64) return fail(ctx, TS5HIP_ERR_ARG, "n_split %d (at most 64)", n_split);
+    const size_t need = attn_partial_bytes(B, n_split, n_head, n_head_kv, head_dim);
+    if (!part) {
+        if (int rc = ensure_scratch(ctx, need)) return rc;
+        part = (float *)ctx->scratch, counters = ctx->counters;
+    }
+    AttnIO io{};
+    io.q = q, io.q_stride = (int64_t)n_head * head_dim, io.rope = 0, io.append = 0;
+    io.kv = KvLayer{(int8_t *)k8, (uint16_t *)ks, (int8_t *)v8, (uint16_t *)vs};
+    io.kv_f16 = kv_f16;
+    io.kv_per_batch = kv_per_batch, io.n_ctx = n_ctx, io.n_keys = n_keys_dev;
+    io.B = B, io.H = n_head, io.HKV = n_head_kv, io.HD = head_dim, io.n_split = n_split, io.scale = scale;
+    io.part = part, io.counters = counters, io.out = out;
+    TS5_HIP(ctx, launch_attn(io, ctx->stream));
     return TS5HIP_OK;
 }
 
 int ts5hip_attn_decode(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n_head_kv, int head_dim,
                        const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx,
                        const int32_t *n_keys_dev, int kv_per_batch, float scale, int n_split, float *out) {
-    if (!ctx || !q || !k8 || !ks || !v8 || !vs || !n_keys_dev || !out) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
-    if (B <= 0 || n_ctx <= 0 || !attn_supported(n_head, n_head_kv, head_dim))
-        return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "attention for %d/%d heads of %d", n_head, n_head_kv, head_dim);
-    if (B * n_head_kv > 4096) return fail(ctx, TS5HIP_ERR_ARG, "batch of %d x %d KV heads", B, n_head_kv);
-    if (n_split <= 0) n_split = attn_splits(B, n_head_kv, ctx->n_cu);
-    if (n_split > 64) return fail(ctx, TS5HIP_ERR_ARG, "n_split %d (at most 64)", n_split);
-    if (int rc = ensure_scratch(ctx, attn_partial_bytes(B, n_split, n_head, n_head_kv, head_dim))) return rc;
-    AttnIO io{};
-    io.q = q, io.q_stride = (int64_t)n_head * head_dim, io.rope = 0, io.append = 0;
-    io.kv = KvLayer{(int8_t *)k8, (uint16_t *)ks, (int8_t *)v8, (uint16_t *)vs};
-    io.kv_per_batch = kv_per_batch, io.n_ctx = n_ctx, io.n_keys = n_keys_dev;
-    io.B = B, io.H = n_head, io.HKV = n_head_kv, io.HD = head_dim, io.n_split = n_split, io.scale = scale;
-    io.part = (float *)ctx->scratch, io.counters = ctx->counters, io.out = out;
-    TS5_HIP(ctx, launch_attn(io, ctx->stream));
-    return TS5HIP_OK;
+    return attn_decode_into(ctx, q, B, n_head, n_head_kv, head_dim, k8, ks, v8, vs, n_ctx, n_keys_dev, kv_per_batch,
+                            scale, n_split, out, nullptr, nullptr);
+}
+
+int ts5hip_attn_decode_f16(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n_head_kv, int head_dim,
+                           const void *k16, const void *v16, int n_ctx, const int32_t *n_keys_dev, int kv_per_batch,
+                           float scale, int n_split, float *out) {
+    return attn_decode_into(ctx, q, B, n_head, n_head_kv, head_dim, k16, nullptr, v16, nullptr, n_ctx, n_keys_dev,
+                            kv_per_batch, scale, n_split, out, nullptr, nullptr, 1);
 }
 
 int ts5hip_attn_prompt(ts5hip_ctx *ctx, const float *q, int nq, int n_head, int n_head_kv, int head_dim,

@@ -61,39 +61,45 @@ __host__ __device__ inline size_t device_bytes(uint32_t t, int64_t ne0, int64_t 
 // ---------------------------------------------------------------------------
 // Quantized activations ("act"): the form in which every matvec reads its
 // input vector x of n values (n a multiple of 32). Per 32-value sub-block s:
-//   scale[s] = max|x| / 16383, x16 = rint(x / scale[s]) in [-16383, 16383],
-//   x16 = 256 * hi + lo with lo in [-128, 127] and hi in [-64, 64],
-//   sum[s]  = sum of x over the sub-block (fp32, the unquantized values),
-// and per 16-value run r: isum[r] = sum of x16 over the run (exact).
-// The two int8 planes feed v_dot4_i32_i8 directly against int8/uint4
-// weights: sum(q * x16) = 256 * dot4(q, hi) + dot4(q, lo), exact in int32.
-// The relative rounding error per value is at most 1/32766 of the
-// sub-block's largest magnitude.
+//   scale[s] = max|x| / XQ_MAX, X = rint(x / scale[s]) in [-XQ_MAX, XQ_MAX]
+//   (XQ_MAX = 2^22 - 1: 23 significant bits, the precision of the fp32
+//   input itself), X = 65536 * hi + 256 * mid + lo with lo, mid in
+//   [-128, 127] and hi in [-64, 64] (xq_split),
+//   sum[s] = sum of x over the sub-block (fp32, the unquantized values),
+// and per 16-value run r: isum[r] = sum of X over the run (exact, int32).
+// The three int8 planes feed v_dot4_i32_i8 directly against int8/uint4
+// weights: sum(q * X) = 65536 dot4(q, hi) + 256 dot4(q, mid) + dot4(q, lo),
+// each dot exact in int32. The rounding error per value is at most 1/2^23
+// of the sub-block's largest magnitude, so a dot product over n values keeps
+// a relative error of a few 1e-7 whatever the signs of its terms.
 // ---------------------------------------------------------------------------
+constexpr int XQ_MAX = (1 << 22) - 1;
+
 struct Act {
-    int8_t *hi, *lo;
+    int8_t *hi, *mid, *lo;
     float *scale, *sum;
     int32_t *isum;
 };
 struct CAct {
-    const int8_t *hi, *lo;
+    const int8_t *hi, *mid, *lo;
     const float *scale, *sum;
     const int32_t *isum;
 };
 
 __host__ __device__ inline size_t act_bytes(int64_t n) {
-    return 2 * align_up((size_t)n, 256) + 2 * align_up((size_t)n / 32 * 4, 256) + align_up((size_t)n / 16 * 4, 256);
+    return 3 * align_up((size_t)n, 256) + 2 * align_up((size_t)n / 32 * 4, 256) + align_up((size_t)n / 16 * 4, 256);
 }
 // The matrix-core matmuls' activation for Q4_K / Q6_K rows (n a multiple of
-// 256): the same x16 = 256 hi + lo values, scales and sums as Act, ordered per
-// 256-value block so that a lane feeding k-group kq of the MFMA finds its 8
-// bytes of all 8 chunks side by side:
+// 256): the same X = 65536 hi + 256 mid + lo values, scales and sums as Act,
+// ordered per 256-value block so that a lane feeding k-group kq of the MFMA
+// finds its 8 bytes of all 8 chunks side by side:
 //   hi[4][8][8]   k-group kq, chunk c, the chunk's bytes 8 kq .. 8 kq + 7
+//   mid[4][8][8]
 //   lo[4][8][8]
 //   scale[8], sum[8] (f32 per chunk), isum[16] (i32 per 16 values)
-// 640 bytes a block.
-constexpr int MACT_BLOCK = 640;
-constexpr int MACT_LO = 256, MACT_SCALE = 512, MACT_SUM = 544, MACT_ISUM = 576;
+// 896 bytes a block.
+constexpr int MACT_BLOCK = 896;
+constexpr int MACT_MID = 256, MACT_LO = 512, MACT_SCALE = 768, MACT_SUM = 800, MACT_ISUM = 832;
 __host__ __device__ inline size_t mact_bytes(int64_t n) { return align_up((size_t)(n / 256) * MACT_BLOCK, 256); }
 // The prompt matmuls' activation (Q4_K rows, batches past 16 tokens; n a
 // multiple of 256): each token's values scaled by a power of two, 2^-e, that
@@ -112,6 +118,8 @@ __host__ __device__ inline Act act_view(void *base, int64_t n) {
     Act a;
     a.hi = (int8_t *)p;
     p += align_up((size_t)n, 256);
+    a.mid = (int8_t *)p;
+    p += align_up((size_t)n, 256);
     a.lo = (int8_t *)p;
     p += align_up((size_t)n, 256);
     a.scale = (float *)p;
@@ -123,7 +131,7 @@ __host__ __device__ inline Act act_view(void *base, int64_t n) {
 }
 __host__ __device__ inline CAct cact_view(const void *base, int64_t n) {
     Act a = act_view(const_cast<void *>(base), n);
-    return CAct{a.hi, a.lo, a.scale, a.sum, a.isum};
+    return CAct{a.hi, a.mid, a.lo, a.scale, a.sum, a.isum};
 }
 
 // Split-K decode attention partials: per (query, key split, KV head) a group
@@ -226,31 +234,14 @@ __device__ inline float wave_max(float v) {
     return v;
 }
 
-// Quantizes 32 values held one per lane of a 32-lane segment (lane32 =
-// 0..31, all 32 lanes active) into sub-block `group` of an Act.
-__device__ inline void quant32(float v, int lane32, const Act &a, int64_t group) {
-    float amax = fabsf(v), s = v;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, o, 32));
-        s += __shfl_xor(s, o, 32);
-    }
-    int x16 = 0;
-    if (amax > 0.f) x16 = max(-16383, min(16383, (int)rintf(v * (16383.0f / amax))));
-    const int lo = (int)(int8_t)(x16 & 255);
-    const int hi = (x16 - lo) >> 8;
-    a.hi[group * 32 + lane32] = (int8_t)hi;
-    a.lo[group * 32 + lane32] = (int8_t)lo;
-    int is = x16;
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) is += __shfl_xor(is, o, 16);
-    if (lane32 == 0) {
-        a.scale[group] = amax / 16383.0f;
-        a.sum[group] = s;
-        a.isum[2 * group] = is;
-    } else if (lane32 == 16) {
-        a.isum[2 * group + 1] = is;
-    }
+// X (|X| <= XQ_MAX) as its three planes: X = 65536 hi + 256 mid + lo,
+// lo and mid in [-128, 127], hi in [-64, 64]; each plane is a byte of the
+// returned words' lanes when packed by the caller.
+__device__ inline void xq_split(int X, int &hi, int &mid, int &lo) {
+    lo = (int)(int8_t)(X & 255);
+    const int r = (X - lo) >> 8;  // exact: X - lo is a multiple of 256
+    mid = (int)(int8_t)(r & 255);
+    hi = (r - mid) >> 8;
 }
 
 // The 6-bit scale and min of sub-block j (0..7) of a K-quant block, from its

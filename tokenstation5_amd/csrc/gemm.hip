@@ -4,16 +4,17 @@
 // matmul_big for prompts, engine/src/vk_backend.cpp:835-918).
 //
 // Matrix cores. The activations are the same quantized form the one-token
-// matvec reads (common.h Act: x16 = 256*hi + lo, a scale per 32 values), so
-// every product is exact in int32 and only the per-sub-block scaling runs in
-// fp32. One v_mfma_i32_16x16x32_i8 multiplies 16 rows x 32 weights (A: the raw
-// quants, 0..15 or 0..63 or int8) by 32 values of 16 tokens' hi plane (B), a
-// second by their lo plane; 256*C_hi + C_lo is then sum q * x16 for each
+// matvec reads (common.h Act: X = 65536*hi + 256*mid + lo, a scale per 32
+// values), so every product is exact in integers and only the per-sub-block
+// scaling runs in fp32. One v_mfma_i32_16x16x32_i8 multiplies 16 rows x 32
+// weights (A: the raw quants, 0..15 or 0..63 or int8) by 32 values of 16
+// tokens' hi plane (B), a second by their mid plane, a third by their lo
+// plane; 65536*C_hi + 256*C_mid + C_lo is then sum q * X for each
 // (row, token) of the sub-block, and
-//   Q4_K: y += d*sc * xs * (sum q x16) - dmin*m * (sum x)       per 32 values
-//   Q6_K: y += d*sc * xs * (sum q x16 - 32 * sum x16)          per 16 values
-//   Q8_0: y += d * xs * (sum q x16)                             per 32 values
-// (engine/src/quants.cpp:133-202). Q6_K's 16-value groups each get an MFMA of
+//   Q4_K: y += d*sc * xs * (sum q X) - dmin*m * (sum x)         per 32 values
+//   Q6_K: y += d*sc * xs * (sum q X - 32 * sum X)              per 16 values
+//   Q8_0: y += d * xs * (sum q X)                               per 32 values
+// (engine/src/quants.cpp:133-202). Q6_K's 16-value groups each get MFMAs of
 // their own, the other half of the 32-value A operand zeroed.
 //
 // Lane layout of the 16x16x32 int8 MFMA (checked on the device): A lane l =
@@ -54,6 +55,19 @@ __device__ inline uint4 ld16(const void *p) { return *(const uint4 *)p; }
 __device__ inline v4i mfma(uint64_t a, uint64_t b) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)a, (long)b, v4i{0, 0, 0, 0}, 0, 0, 0);
 }
+// The three planes' products of A with one B fragment, combined per entry:
+// sum q X = 65536 C_hi + 256 C_mid + C_lo, in 64 bits (int8 or 6-bit quants
+// can take the hi term past 2^31).
+struct Prod3 {
+    v4i c[3];
+    __device__ long long at(int i) const { return (long long)c[0][i] * 65536 + c[1][i] * 256 + c[2][i]; }
+};
+__device__ inline Prod3 mfma3(uint64_t a, const uint64_t (&b)[3]) {
+    Prod3 r;
+#pragma unroll
+    for (int P = 0; P < 3; P++) r.c[P] = mfma(a, b[P]);
+    return r;
+}
 
 // Per-wave LDS for the scale exchange: [sub-block or group][row] (scale, min).
 struct GemmLds {
@@ -66,7 +80,7 @@ constexpr int F_Q4K = 0, F_Q6K = 1, F_Q80 = 2;
 // kq, and the chunk's scale and sum: Q4_K / Q6_K rows read the matmul layout
 // (MACT_*), Q8_0 rows Act (its block is one chunk, s = 0).
 struct AFrag {
-    uint64_t hi, lo;
+    uint64_t p[3];  // planes hi, mid, lo
     float xs, xsum;
 };
 template <int FMT>
@@ -75,18 +89,20 @@ __device__ inline const uint8_t *mact_blk(const GemmArgs &a, int tok, int b) {
 }
 template <int FMT>
 __device__ inline AFrag act_frag(const GemmArgs &a, int tok, int b, int s, int kq) {
-    AFrag f{0, 0, 0.f, 0.f};
+    AFrag f{{0, 0, 0}, 0.f, 0.f};
     if (tok < a.M) {
         if constexpr (FMT == F_Q80) {
             const CAct x = cact_view(a.act + (int64_t)tok * a.act_stride, a.n_in);
-            f.hi = ld8(x.hi + 32 * b + 8 * kq);
-            f.lo = ld8(x.lo + 32 * b + 8 * kq);
+            f.p[0] = ld8(x.hi + 32 * b + 8 * kq);
+            f.p[1] = ld8(x.mid + 32 * b + 8 * kq);
+            f.p[2] = ld8(x.lo + 32 * b + 8 * kq);
             f.xs = x.scale[b];
             f.xsum = x.sum[b];
         } else {
             const uint8_t *blk = mact_blk<FMT>(a, tok, b);
-            f.hi = ld8(blk + 64 * kq + 8 * s);
-            f.lo = ld8(blk + MACT_LO + 64 * kq + 8 * s);
+            f.p[0] = ld8(blk + 64 * kq + 8 * s);
+            f.p[1] = ld8(blk + MACT_MID + 64 * kq + 8 * s);
+            f.p[2] = ld8(blk + MACT_LO + 64 * kq + 8 * s);
             f.xs = ((const float *)(blk + MACT_SCALE))[s];
             f.xsum = ((const float *)(blk + MACT_SUM))[s];
         }
@@ -116,45 +132,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 
     for (int b = b0; b < b1; b++) {
         __builtin_amdgcn_wave_barrier();  // this wave's reads of the last block's scales are issued
-        if constexpr (FMT == F_Q4K) {
-            uint64_t q[NW][4];
-#pragma unroll
-            for (int m = 0; m < NW; m++) {
-                const uint8_t *blk = (m ? a.w2 : a.w) + ((int64_t)(rin ? row : 0) * a.nb + b) * Q4K_BYTES;
-                uint4 hdr = ld16(blk);
-                if (!rin) hdr = make_uint4(0, 0, 0, 0);
-#pragma unroll
-                for (int g = 0; g < 4; g++) q[m][g] = rin ? ld8(blk + 16 + 32 * g + 8 * kq) : 0;
-                int sc0, m0, sc1, m1;
-                kq_scale_min_pair(kq, hdr.y, hdr.z, hdr.w, sc0, m0, sc1, m1);
-                const float d = h2f(hdr.x & 0xffff), dmin = h2f(hdr.x >> 16);
-                S.scl[m][2 * kq][rl] = make_float2(d * (float)sc0, dmin * (float)m0);
-                S.scl[m][2 * kq + 1][rl] = make_float2(d * (float)sc1, dmin * (float)m1);
-            }
-            __builtin_amdgcn_wave_barrier();
-#pragma unroll
-            for (int s = 0; s < 8; s++) {
-                AFrag x[TN];
-#pragma unroll
-                for (int g = 0; g < TN; g++) x[g] = act_frag<FMT>(a, t0 + 16 * g + rl, b, s, kq);
-#pragma unroll
-                for (int m = 0; m < NW; m++) {
-                    const uint64_t qa = (s & 1) ? (q[m][s >> 1] >> 4) & 0x0F0F0F0F0F0F0F0Full
-                                                : q[m][s >> 1] & 0x0F0F0F0F0F0F0F0Full;
-                    const float4 sA = *(const float4 *)&S.scl[m][s][4 * kq];
-                    const float4 sB = *(const float4 *)&S.scl[m][s][4 * kq + 2];
-                    const float dsc[4] = {sA.x, sA.z, sB.x, sB.z}, dm[4] = {sA.y, sA.w, sB.y, sB.w};
-#pragma unroll
-                    for (int g = 0; g < TN; g++) {
-                        const v4i ch = mfma(qa, x[g].hi), cl = mfma(qa, x[g].lo);
-#pragma unroll
-                        for (int i = 0; i < 4; i++)
-                            acc[m][g][i] += dsc[i] * x[g].xs * (float)(ch[i] * 256 + cl[i]) - dm[i] * x[g].xsum;
-                    }
-                }
-                if constexpr (TN > 1) __builtin_amdgcn_sched_barrier(0);  // one chunk's loads at a time
-            }
-        } else if constexpr (FMT == F_Q80) {
+        if constexpr (FMT == F_Q80) {
             uint64_t q[NW];
 #pragma unroll
             for (int m = 0; m < NW; m++) {
@@ -173,9 +151,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
                 const float d[4] = {sA.x, sA.z, sB.x, sB.z};
 #pragma unroll
                 for (int g = 0; g < TN; g++) {
-                    const v4i ch = mfma(q[m], x[g].hi), cl = mfma(q[m], x[g].lo);
+                    const Prod3 c = mfma3(q[m], x[g].p);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) acc[m][g][i] += d[i] * x[g].xs * (float)(ch[i] * 256 + cl[i]);
+                    for (int i = 0; i < 4; i++) acc[m][g][i] += d[i] * x[g].xs * (float)c.at(i);
                 }
             }
         } else {  // Q6_K
@@ -227,12 +205,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
                     const float e0[4] = {s0A.x, s0A.z, s0B.x, s0B.z}, e1[4] = {s1A.x, s1A.z, s1B.x, s1B.z};
 #pragma unroll
                     for (int g = 0; g < TN; g++) {
-                        const v4i h0 = mfma(qa0, x[g].hi), l0 = mfma(qa0, x[g].lo);
-                        const v4i h1 = mfma(qa1, x[g].hi), l1 = mfma(qa1, x[g].lo);
+                        const Prod3 c0 = mfma3(qa0, x[g].p), c1 = mfma3(qa1, x[g].p);
 #pragma unroll
                         for (int i = 0; i < 4; i++)
-                            acc[m][g][i] += x[g].xs * (e0[i] * (float)(h0[i] * 256 + l0[i] - 32 * is0[g]) +
-                                                       e1[i] * (float)(h1[i] * 256 + l1[i] - 32 * is1[g]));
+                            acc[m][g][i] += x[g].xs * (e0[i] * (float)(c0.at(i) - 32ll * is0[g]) +
+                                                       e1[i] * (float)(c1.at(i) - 32ll * is1[g]));
                     }
                 }
                 if constexpr (TN > 1) __builtin_amdgcn_sched_barrier(0);  // one chunk's loads at a time
@@ -326,7 +303,7 @@ __device__ inline void mask_wblk(WBlk<FMT, NW> &w, bool rin) {
 template <int FMT>
 struct ABlk {
     static constexpr int C = FMT == F_Q80 ? 1 : 8;  // 32-value chunks per block
-    uint64_t hi[C], lo[C];
+    uint64_t p[C][3];  // [chunk][plane hi, mid, lo]
     float xs[C], xsum[C];
     int is[FMT == F_Q6K ? 16 : 1];
 };
@@ -337,17 +314,21 @@ __device__ inline ABlk<FMT> load_ablk(const GemmArgs &a, int tok, int kq, int b)
     tok = min(tok, a.M - 1);
     if constexpr (FMT == F_Q80) {
         const CAct xa = cact_view(a.act + (int64_t)tok * a.act_stride, a.n_in);
-        x.hi[0] = ld8(xa.hi + 32 * b + 8 * kq);
-        x.lo[0] = ld8(xa.lo + 32 * b + 8 * kq);
+        x.p[0][0] = ld8(xa.hi + 32 * b + 8 * kq);
+        x.p[0][1] = ld8(xa.mid + 32 * b + 8 * kq);
+        x.p[0][2] = ld8(xa.lo + 32 * b + 8 * kq);
         x.xs[0] = xa.scale[b];
         x.xsum[0] = xa.sum[b];
     } else {  // the lane's 8 bytes of every chunk, side by side: 16-byte loads
         const uint8_t *blk = mact_blk<FMT>(a, tok, b);
 #pragma unroll
         for (int c = 0; c < 8; c += 2) {
-            const uint4 h = ld16(blk + 64 * kq + 8 * c), l = ld16(blk + MACT_LO + 64 * kq + 8 * c);
-            x.hi[c] = ((uint64_t)h.y << 32) | h.x, x.hi[c + 1] = ((uint64_t)h.w << 32) | h.z;
-            x.lo[c] = ((uint64_t)l.y << 32) | l.x, x.lo[c + 1] = ((uint64_t)l.w << 32) | l.z;
+            const int plane[3] = {0, MACT_MID, MACT_LO};
+#pragma unroll
+            for (int P = 0; P < 3; P++) {
+                const uint4 v = ld16(blk + plane[P] + 64 * kq + 8 * c);
+                x.p[c][P] = ((uint64_t)v.y << 32) | v.x, x.p[c + 1][P] = ((uint64_t)v.w << 32) | v.z;
+            }
         }
 #pragma unroll
         for (int c = 0; c < 8; c += 4) {
@@ -408,18 +389,22 @@ __device__ inline void compute_blk(GemmLds &S, const WBlk<FMT, NW> &w, const ABl
                 const float4 sA = *(const float4 *)&S.scl[m][s][4 * kq];
                 const float4 sB = *(const float4 *)&S.scl[m][s][4 * kq + 2];
                 const float dsc[4] = {sA.x, sA.z, sB.x, sB.z}, dm[4] = {sA.y, sA.w, sB.y, sB.w};
-                const v4i ch = mfma(qa, x.hi[s]), cl = mfma(qa, x.lo[s]);
+                v4i c[3];
+#pragma unroll
+                for (int P = 0; P < 3; P++) c[P] = mfma(qa, x.p[s][P]);
+                // Exact in int32 for 4-bit quants: |.| <= 32 * 15 * (64 * 65536 + 128 * 257) < 2^31.
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    acc[m][i] += dsc[i] * x.xs[s] * (float)(ch[i] * 256 + cl[i]) - dm[i] * x.xsum[s];
+                    acc[m][i] += dsc[i] * x.xs[s] * (float)(c[0][i] * 65536 + c[1][i] * 256 + c[2][i]) -
+                                 dm[i] * x.xsum[s];
             }
         } else if constexpr (FMT == F_Q80) {
             const float4 sA = *(const float4 *)&S.scl[m][0][4 * kq];
             const float4 sB = *(const float4 *)&S.scl[m][0][4 * kq + 2];
             const float d[4] = {sA.x, sA.z, sB.x, sB.z};
-            const v4i ch = mfma(w.q[m][0], x.hi[0]), cl = mfma(w.q[m][0], x.lo[0]);
+            const Prod3 c = mfma3(w.q[m][0], x.p[0]);
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[m][i] += d[i] * x.xs[0] * (float)(ch[i] * 256 + cl[i]);
+            for (int i = 0; i < 4; i++) acc[m][i] += d[i] * x.xs[0] * (float)c.at(i);
         } else {
 #pragma unroll
             for (int c32 = 0; c32 < 8; c32++) {
@@ -433,12 +418,11 @@ __device__ inline void compute_blk(GemmLds &S, const WBlk<FMT, NW> &w, const ABl
                 const float4 s1A = *(const float4 *)&S.scl[m][2 * c32 + 1][4 * kq];
                 const float4 s1B = *(const float4 *)&S.scl[m][2 * c32 + 1][4 * kq + 2];
                 const float e0[4] = {s0A.x, s0A.z, s0B.x, s0B.z}, e1[4] = {s1A.x, s1A.z, s1B.x, s1B.z};
-                const v4i h0 = mfma(qa0, x.hi[c32]), l0 = mfma(qa0, x.lo[c32]);
-                const v4i h1 = mfma(qa1, x.hi[c32]), l1 = mfma(qa1, x.lo[c32]);
+                const Prod3 c0 = mfma3(qa0, x.p[c32]), c1 = mfma3(qa1, x.p[c32]);
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    acc[m][i] += x.xs[c32] * (e0[i] * (float)(h0[i] * 256 + l0[i] - 32 * x.is[2 * c32]) +
-                                                e1[i] * (float)(h1[i] * 256 + l1[i] - 32 * x.is[2 * c32 + 1]));
+                    acc[m][i] += x.xs[c32] * (e0[i] * (float)(c0.at(i) - 32ll * x.is[2 * c32]) +
+                                                e1[i] * (float)(c1.at(i) - 32ll * x.is[2 * c32 + 1]));
             }
         }
     }

@@ -5,7 +5,8 @@
 
 namespace ts5hip {
 
-// One layer's q8 KV cache (layout in attention.hip).
+// One layer's KV cache (layout in attention.hip): q8 (k, v int8 with f16
+// scales ks, vs), or f16 (k, v hold uint16 halves; ks, vs null).
 struct KvLayer {
     int8_t *k;
     uint16_t *ks;
@@ -76,10 +77,12 @@ hipError_t launch_matvec_argmax(uint32_t t, const void *w, int64_t ne0, int64_t 
                                 int32_t *seq, int32_t *pos, hipStream_t s);
 
 // attention.hip
+// kv_f16: the cache holds f16 values (k / v as uint16 [HKV][n_ctx][HD], no
+// scales) instead of q8.
 hipError_t launch_rope_kv(const float *qkv, int64_t qkv_stride, const float *bias, const float *q_norm,
                           const float *k_norm, float eps, const float *rope_cs, int n_rot, int neox,
                           const int32_t *pos0, int H, int HKV, int HD, int n_ctx, int ntok, float *q_out, KvLayer kv,
-                          hipStream_t s);
+                          int kv_f16, hipStream_t s);
 bool attn_supported(int H, int HKV, int HD);
 // Flash decode (attention.hip: k_attn). q rows of B queries; with rope each
 // row holds the token's raw q, k, v ((H + 2 HKV) HD values), and q (with
@@ -93,6 +96,7 @@ struct AttnIO {
     const float *rope_cs;
     int n_rot, neox;
     KvLayer kv;
+    int kv_f16;  // the cache holds f16 values (no scales) instead of q8
     int kv_per_batch, n_ctx;
     const int32_t *n_keys;
     int B, H, HKV, HD, n_split;
@@ -109,7 +113,10 @@ bool attn_prefill_supported(int H, int HKV, int HD);
 size_t attn_prefill_partial_bytes(int nq, int H, int HD, int64_t max_keys);
 hipError_t launch_attn_prefill(const float *q, int64_t q_stride, KvLayer kv, int n_ctx, int H, int HKV, int HD, int p0,
                                int nq, float scale, float *part, float *out, hipStream_t s);
-hipError_t launch_kv_read(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, float *out, hipStream_t s);
+hipError_t launch_kv_read(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, int kv_f16, float *out,
+                          hipStream_t s);
+hipError_t launch_kv_write(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, int kv_f16,
+                           const float *in, hipStream_t s);
 
 // sample.hip
 size_t argmax_scratch_bytes(int rows);

@@ -143,12 +143,18 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
 
 template <int MODE>
 static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
-    switch (a.t) {
-    case T_Q4_K:
-        return MODE == MV_GLU ? mv_go<Q4K, TS5_MV_GLU_R, TS5_MV_GLU_WAVES, MODE>(a, s)
-                              : mv_go<Q4K, TS5_MV_R, 4, MODE>(a, s);
-    case T_Q6_K: return MODE == MV_GLU ? mv_go<Q6K, 2, 4, MODE>(a, s) : mv_go<Q6K, 4, 4, MODE>(a, s);
-    case T_Q8_0: return MODE == MV_GLU ? mv_go<Q80, 2, 4, MODE>(a, s) : mv_go<Q80, 4, 4, MODE>(a, s);
+    if constexpr (MODE == MV_GLU) {
+        switch (a.t) {
+        case T_Q4_K: return mv_go<Q4K, TS5_MV_GLU_R, TS5_MV_GLU_WAVES, MODE>(a, s);
+        case T_Q6_K: return mv_go<Q6K, 2, 4, MODE>(a, s);
+        case T_Q8_0: return mv_go<Q80, 2, 4, MODE>(a, s);
+        }
+    } else {
+        switch (a.t) {
+        case T_Q4_K: return mv_go<Q4K, TS5_MV_R, 4, MODE>(a, s);
+        case T_Q6_K: return mv_go<Q6K, 4, 4, MODE>(a, s);
+        case T_Q8_0: return mv_go<Q80, 4, 4, MODE>(a, s);
+        }
     }
     return hipErrorInvalidValue;
 }

@@ -55,7 +55,8 @@ struct ts5hip_model {
     std::vector<LayerDev> layers;
     float *bias = nullptr;  // [n_layer][(H + 2 HKV) HD], zero where absent
     std::vector<bool> has_bias;
-    // KV cache (all layers) and RoPE table.
+    // KV cache (all layers) and RoPE table. q8: k8 / v8 int8 values with f16
+    // scales ks / vs; f16: k8 / v8 hold the halves (2 bytes a value), no scales.
     int8_t *k8 = nullptr, *v8 = nullptr;
     uint16_t *ks = nullptr, *vs = nullptr;
     float *rope_cs = nullptr;
@@ -94,8 +95,10 @@ struct ts5hip_model {
 
     int qkv_rows() const { return (hp.n_head + 2 * hp.n_head_kv) * hp.head_dim; }
     int64_t kv_head_elems() const { return (int64_t)n_ctx * hp.head_dim; }
+    bool kv_f16() const { return kv_type == KV_F16; }
     KvLayer kv_layer(int l) const {
         const int64_t per = (int64_t)hp.n_head_kv * n_ctx * hp.head_dim;
+        if (kv_f16()) return KvLayer{k8 + 2 * l * per, nullptr, v8 + 2 * l * per, nullptr};
         const int64_t per_s = per / 32;
         return KvLayer{k8 + l * per, ks + l * per_s, v8 + l * per, vs + l * per_s};
     }
@@ -156,11 +159,17 @@ int matrix_slot(ts5hip_model *m, DevT &t, uint32_t type, int64_t ne0, int64_t ne
     return TS5HIP_OK;
 }
 
-// Source of a tensor's bytes: GGUF on the host, or a synthesis seed.
+// Source of a tensor's bytes: GGUF on the host, or a synthesis seed; rows
+// [row0, row0 + nrows) of the tensor (nrows < 0: all of them), the GGUF bytes
+// being those rows' only.
 struct Source {
     const void *gguf;
     uint64_t seed;
     int centered;
+    int64_t row0 = 0, nrows = -1;
+    int64_t rows(int64_t ne1) const { return nrows < 0 ? ne1 : nrows; }
+    bool whole(int64_t ne1) const { return row0 == 0 && rows(ne1) == ne1; }
+    bool last(int64_t ne1) const { return row0 + rows(ne1) == ne1; }
 };
 
 int fill_rows(ts5hip_model *m, const DevT &t, int64_t row0, int64_t nrows, const Source &src) {
@@ -175,9 +184,11 @@ int set_matrix(ts5hip_model *m, DevT &t, uint32_t type, int64_t ne0, int64_t ne1
     if (ne0 != want0 || ne1 != want1)
         return fail(m->ctx, TS5HIP_ERR_ARG, "%s is %lld x %lld, expected %lld x %lld", name, (long long)ne0,
                     (long long)ne1, (long long)want0, (long long)want1);
+    if (src.row0 < 0 || src.row0 + src.rows(ne1) > ne1)
+        return fail(m->ctx, TS5HIP_ERR_ARG, "%s: rows %lld.. past %lld", name, (long long)src.row0, (long long)ne1);
     if (int rc = matrix_slot(m, t, type, ne0, ne1)) return rc;
-    if (int rc = fill_rows(m, t, 0, ne1, src)) return rc;
-    t.set = true;
+    if (int rc = fill_rows(m, t, src.row0, src.rows(ne1), src)) return rc;
+    if (src.last(ne1)) t.set = true;
     return TS5HIP_OK;
 }
 
@@ -186,6 +197,7 @@ int set_vector(ts5hip_model *m, DevT &t, uint32_t type, int64_t n, int64_t want,
                const char *name) {
     if (n != want) return fail(m->ctx, TS5HIP_ERR_ARG, "%s has %lld values, expected %lld", name, (long long)n,
                                (long long)want);
+    if (!src.whole(1)) return fail(m->ctx, TS5HIP_ERR_ARG, "%s: a vector is set whole", name);
     if (!t.d) {
         if (int rc = alloc(m, (size_t)n * 4, &t.d)) return rc;
         t.type = T_F32, t.ne0 = n, t.ne1 = 1;
@@ -210,6 +222,7 @@ int set_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, in
         if (type != T_F32 && type != T_F16 && !ts5hip_supports_type(type))
             return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "token_embd of type %u", type);
         if (ne0 != E || ne1 != hp.n_vocab) return fail(m->ctx, TS5HIP_ERR_ARG, "token_embd shape");
+        if (src.row0 < 0 || src.row0 + src.rows(ne1) > ne1) return fail(m->ctx, TS5HIP_ERR_ARG, "token_embd rows");
         if (!m->tok_embd.d) {
             const size_t bytes = (type == T_F32 || type == T_F16) ? (size_t)ne0 * ne1 * (type == T_F32 ? 4 : 2)
                                                                   : device_bytes(type, ne0, ne1);
@@ -218,18 +231,21 @@ int set_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, in
         }
         if (type == T_F32 || type == T_F16) {
             if (!src.gguf) return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "synthetic float embeddings");
-            if (int rc = ts5hip_upload(m->ctx, m->tok_embd.d, src.gguf, (size_t)ne0 * ne1 * (type == T_F32 ? 4 : 2)))
+            const size_t vb = type == T_F32 ? 4 : 2;
+            if (int rc = ts5hip_upload(m->ctx, (uint8_t *)m->tok_embd.d + (size_t)src.row0 * ne0 * vb, src.gguf,
+                                       (size_t)ne0 * src.rows(ne1) * vb))
                 return rc;
-        } else if (int rc = fill_rows(m, m->tok_embd, 0, ne1, src)) {
+        } else if (int rc = fill_rows(m, m->tok_embd, src.row0, src.rows(ne1), src)) {
             return rc;
         }
-        m->tok_embd.set = true;
+        if (src.last(ne1)) m->tok_embd.set = true;
         return TS5HIP_OK;
     }
     if (n == "output_norm.weight") return set_vector(m, m->out_norm, type, ne0 * ne1, E, src, name);
     if (n == "output.weight") return set_matrix(m, m->output, type, ne0, ne1, E, hp.n_vocab, src, name);
     if (n == "rope_freqs.weight") {
         if (!src.gguf) return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "synthetic rope_freqs");
+        if (!src.whole(1)) return fail(m->ctx, TS5HIP_ERR_ARG, "%s: a vector is set whole", name);
         if (ne0 * ne1 != hp.rope_dims / 2) return fail(m->ctx, TS5HIP_ERR_ARG, "rope_freqs has %lld values", (long long)(ne0 * ne1));
         m->rope_ready = false;
         return host_floats(m->ctx, type, ne0 * ne1, src.gguf, m->freqs);
@@ -253,9 +269,10 @@ int set_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, in
     for (int p = 0; p < 3; p++) {
         if (r == std::string(parts[p]) + ".weight") {
             if (ne0 != E || ne1 != rows[p]) return fail(m->ctx, TS5HIP_ERR_ARG, "%s shape", name);
+            if (src.row0 < 0 || src.row0 + src.rows(ne1) > ne1) return fail(m->ctx, TS5HIP_ERR_ARG, "%s rows", name);
             if (!L.qkv.d || L.qkv.type == type) {
                 if (int rc = matrix_slot(m, L.qkv, type, E, m->qkv_rows())) return rc;
-                if (int rc = fill_rows(m, L.qkv, row0[p], rows[p], src)) return rc;
+                if (int rc = fill_rows(m, L.qkv, row0[p] + src.row0, src.rows(ne1), src)) return rc;
                 L.in_qkv[p] = true;
                 L.part[p].set = false;
             } else {
@@ -266,6 +283,7 @@ int set_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, in
         }
         if (r == std::string(parts[p]) + ".bias") {
             if (!src.gguf) return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "synthetic bias");
+            if (!src.whole(1)) return fail(m->ctx, TS5HIP_ERR_ARG, "%s: a vector is set whole", name);
             if (ne0 * ne1 != rows[p]) return fail(m->ctx, TS5HIP_ERR_ARG, "%s shape", name);
             std::vector<float> f;
             if (int rc = host_floats(m->ctx, type, rows[p], src.gguf, f)) return rc;
@@ -348,8 +366,8 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
         io.q_norm = L.q_norm.set ? (const float *)L.q_norm.d : nullptr;
         io.k_norm = L.k_norm.set ? (const float *)L.k_norm.d : nullptr;
         io.eps = hp.rms_eps, io.rope_cs = m->rope_cs, io.n_rot = hp.rope_dims, io.neox = hp.rope_neox;
-        io.kv = m->kv_layer(l), io.kv_per_batch = 0, io.n_ctx = m->n_ctx, io.n_keys = m->state;
-        io.B = 1, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = m->n_split, io.scale = hp.attn_scale;
+        io.kv = m->kv_layer(l), io.kv_f16 = m->kv_f16(), io.kv_per_batch = 0, io.n_ctx = m->n_ctx;
+        io.n_keys = m->state, io.B = 1, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = m->n_split, io.scale = hp.attn_scale;
         io.part = m->part, io.counters = m->counters, io.out = m->att;
         TS5_HIP(ctx, launch_attn(io, s));
         TS5_HIP(ctx, launch_matvec(L.wo.type, L.wo.d, (int64_t)H * HD, E, m->att, nullptr, 0.f, m->x, 1, s));
@@ -536,15 +554,15 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
         const float *qn = L.q_norm.set ? (const float *)L.q_norm.d : nullptr;
         const float *kn = L.k_norm.set ? (const float *)L.k_norm.d : nullptr;
         TS5_HIP(ctx, launch_rope_kv(m->bqkv, QR, bias, qn, kn, eps, m->rope_cs, hp.rope_dims, hp.rope_neox, m->state,
-                                    H, HKV, HD, m->n_ctx, nc, m->bq, m->kv_layer(l), s));
-        if (nc > 16 && attn_prefill_supported(H, HKV, HD)) {  // prompt chunks: flash attention on the matrix cores
+                                    H, HKV, HD, m->n_ctx, nc, m->bq, m->kv_layer(l), m->kv_f16(), s));
+        if (nc > 16 && !m->kv_f16() && attn_prefill_supported(H, HKV, HD)) {  // prompt chunks on the matrix cores
             TS5_HIP(ctx, launch_attn_prefill(m->bq, AH, m->kv_layer(l), m->n_ctx, H, HKV, HD, p0, nc, hp.attn_scale,
                                              m->bpart, m->batt, s));
         } else {
             AttnIO io{};
             io.q = m->bq, io.q_stride = AH, io.rope = 0, io.append = 0;
-            io.kv = m->kv_layer(l), io.kv_per_batch = 0, io.n_ctx = m->n_ctx, io.n_keys = m->state;
-            io.B = nc, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = attn_splits(nc, HKV, ctx->n_cu);
+            io.kv = m->kv_layer(l), io.kv_f16 = m->kv_f16(), io.kv_per_batch = 0, io.n_ctx = m->n_ctx;
+            io.n_keys = m->state, io.B = nc, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = attn_splits(nc, HKV, ctx->n_cu);
             io.scale = hp.attn_scale, io.part = m->bpart, io.counters = m->bcounters, io.out = m->batt;
             TS5_HIP(ctx, launch_attn(io, s));
         }
@@ -668,7 +686,8 @@ extern "C" {
 int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, int kv_type, ts5hip_model **out) {
     if (!ctx || !hp || !out) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
     *out = nullptr;
-    if (kv_type != KV_Q8) return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "KV type %d (the GPU cache is q8)", kv_type);
+    if (kv_type != KV_Q8 && kv_type != KV_F16)
+        return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "KV type %d (the GPU cache is q8 or f16)", kv_type);
     // Rows are whole 32-value blocks (Q8_0; Q4_K/Q6_K tensors also check ne0 % 256).
     if (hp->n_embd <= 0 || hp->n_embd % 32 || hp->n_ff <= 0 || hp->n_ff % 32 || hp->n_layer <= 0 ||
         hp->n_vocab <= 0 || n_ctx <= 0 || hp->rope_dims <= 0 || hp->rope_dims > hp->head_dim || hp->rope_dims % 2)
@@ -691,8 +710,9 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
     const int64_t E = hp->n_embd, F = hp->n_ff, HD = hp->head_dim, H = hp->n_head, HKV = hp->n_head_kv;
     const int64_t kv_elems = (int64_t)hp->n_layer * HKV * n_ctx * HD;
     int rc = 0;
-    if ((rc = alloc_t(m, kv_elems, &m->k8)) || (rc = alloc_t(m, kv_elems, &m->v8)) ||
-        (rc = alloc_t(m, kv_elems / 32, &m->ks)) || (rc = alloc_t(m, kv_elems / 32, &m->vs)) ||
+    const int64_t kv_value_bytes = kv_type == KV_F16 ? 2 : 1, kv_scales = kv_type == KV_F16 ? 0 : kv_elems / 32;
+    if ((rc = alloc_t(m, kv_elems * kv_value_bytes, &m->k8)) || (rc = alloc_t(m, kv_elems * kv_value_bytes, &m->v8)) ||
+        (kv_scales && ((rc = alloc_t(m, kv_scales, &m->ks)) || (rc = alloc_t(m, kv_scales, &m->vs)))) ||
         (rc = alloc_t(m, (size_t)n_ctx * hp->rope_dims, &m->rope_cs)) ||
         (rc = alloc_t(m, (size_t)hp->n_layer * m->qkv_rows(), &m->bias)) || (rc = alloc_t(m, E, &m->x)) ||
         (rc = alloc_t(m, m->qkv_rows(), &m->qkv)) || (rc = alloc_t(m, H * HD, &m->att)) ||
@@ -708,10 +728,10 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
     if ((e = hipMemsetAsync(m->bias, 0, (size_t)hp->n_layer * m->qkv_rows() * 4, ctx->stream)) != hipSuccess ||
         (e = hipMemsetAsync(m->seq, 0, ((size_t)n_ctx + 1) * 4, ctx->stream)) != hipSuccess ||
         (e = hipMemsetAsync(m->counters, 0, ((size_t)HKV * CTR_STRIDE + ARGMAX_CTR_INTS) * 4, ctx->stream)) != hipSuccess ||
-        (e = hipMemsetAsync(m->k8, 0, kv_elems, ctx->stream)) != hipSuccess ||
-        (e = hipMemsetAsync(m->v8, 0, kv_elems, ctx->stream)) != hipSuccess ||
-        (e = hipMemsetAsync(m->ks, 0, kv_elems / 32 * 2, ctx->stream)) != hipSuccess ||
-        (e = hipMemsetAsync(m->vs, 0, kv_elems / 32 * 2, ctx->stream)) != hipSuccess ||
+        (e = hipMemsetAsync(m->k8, 0, kv_elems * kv_value_bytes, ctx->stream)) != hipSuccess ||
+        (e = hipMemsetAsync(m->v8, 0, kv_elems * kv_value_bytes, ctx->stream)) != hipSuccess ||
+        (kv_scales && (e = hipMemsetAsync(m->ks, 0, kv_scales * 2, ctx->stream)) != hipSuccess) ||
+        (kv_scales && (e = hipMemsetAsync(m->vs, 0, kv_scales * 2, ctx->stream)) != hipSuccess) ||
         (e = hipHostMalloc((void **)&m->pinned_ids, ((size_t)n_ctx + 2) * 4, hipHostMallocDefault)) != hipSuccess ||
         (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) {
         hip_fail(ctx, e, "model buffers");
@@ -731,6 +751,14 @@ void ts5hip_model_destroy(ts5hip_model *m) {
     free_rows(m);
     if (m->pinned_ids) (void)hipHostFree(m->pinned_ids);
     delete m;
+}
+
+int ts5hip_model_set_tensor_rows(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, int64_t ne1,
+                                 int64_t row0, int64_t nrows, const void *gguf) {
+    if (!m || !name || !gguf || nrows <= 0) return fail(m ? m->ctx : nullptr, TS5HIP_ERR_ARG, "bad argument");
+    Source src{gguf, 0, 0};
+    src.row0 = row0, src.nrows = nrows;
+    return set_tensor(m, name, type, ne0, ne1, src);
 }
 
 int ts5hip_model_set_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, int64_t ne1,
@@ -830,11 +858,31 @@ int ts5hip_kv_read(ts5hip_model *m, int layer, int which, int pos0, int n, float
     const int64_t w = (int64_t)m->hp.n_head_kv * m->hp.head_dim;
     float *d = nullptr;
     TS5_HIP(ctx, hipMalloc((void **)&d, (size_t)n * w * 4));
-    hipError_t e = launch_kv_read(m->kv_layer(layer), which, m->hp.n_head_kv, m->hp.head_dim, m->n_ctx, pos0, n, d,
+    hipError_t e = launch_kv_read(m->kv_layer(layer), which, m->hp.n_head_kv, m->hp.head_dim, m->n_ctx, pos0, n,
+                                  m->kv_f16(), d,
                                   ctx->stream);
     int rc = e == hipSuccess ? ts5hip_download(ctx, out, d, (size_t)n * w * 4) : hip_fail(ctx, e, "kv_read");
     (void)hipFree(d);
     return rc;
+}
+
+int ts5hip_kv_write(ts5hip_model *m, int layer, int which, int pos0, int n, const float *in) {
+    if (!m || !in) return fail(m ? m->ctx : nullptr, TS5HIP_ERR_ARG, "null argument");
+    ts5hip_ctx *ctx = m->ctx;
+    if (layer < 0 || layer >= m->hp.n_layer || (which != 0 && which != 1) || pos0 < 0 || n <= 0 || pos0 + n > m->n_ctx)
+        return fail(ctx, TS5HIP_ERR_ARG, "bad layer/range");
+    if (m->hp.head_dim > 128 || m->hp.head_dim % 32) return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "head_dim %d", m->hp.head_dim);
+    const size_t bytes = (size_t)n * m->hp.n_head_kv * m->hp.head_dim * 4;
+    float *d = nullptr;
+    TS5_HIP(ctx, hipMalloc((void **)&d, bytes));
+    hipError_t e = hipMemcpyAsync(d, in, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess)
+        e = launch_kv_write(m->kv_layer(layer), which, m->hp.n_head_kv, m->hp.head_dim, m->n_ctx, pos0, n, m->kv_f16(),
+                            d, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(d);
+    if (e != hipSuccess) return hip_fail(ctx, e, "kv_write");
+    return TS5HIP_OK;
 }
 
 int ts5hip_take_profile(ts5hip_model *m, char *buf, int len) {

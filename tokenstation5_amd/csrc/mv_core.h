@@ -1,5 +1,4 @@
-// Device core of the one-token k-quant matvec, shared by the standalone
-// kernels (matvec.hip) and the whole-token persistent kernel (decode.hip).
+// Device core of the one-token k-quant matvec kernels (matvec.hip).
 //
 // The reference computes y[r] = sum_i deq(W[r,i]) * x[i] with fp64
 // accumulation (engine/src/cpu_backend.cpp:18-37); its GPU path reads 8
@@ -7,21 +6,21 @@
 // Here:
 //  * A workgroup first turns the fp32 input (rms-normalised when a norm
 //    weight is given, engine/src/cpu_backend.cpp:48-53) into the quantized
-//    activation of common.h in LDS: x16 = 256*hi + lo per value, a scale per
-//    32. The weights are the only HBM stream; the input is read from L2.
+//    activation of common.h in LDS: X = 65536*hi + 256*mid + lo per value
+//    (23 significant bits), a scale per 32. The weights are the only HBM
+//    stream; the input is read from L2.
 //  * Weights stay packed in registers. A lane takes whole 32-value
-//    sub-blocks, multiplies raw quants with the activation's two int8 planes
-//    on v_dot4_i32_i8 (exact int32) and applies the block scales once per
-//    sub-block in fp32:
-//      Q4_K: y += d*sc*(xs*sum q*x16) - dmin*m*(sum x)   (quants.cpp:140-157)
-//      Q6_K: y += d*sc*xs*(sum q*x16 - 32*sum x16)       (quants.cpp:179-202)
-//      Q8_0: y += d*xs*(sum q*x16)                       (quants.cpp:133-139)
+//    sub-blocks, multiplies raw quants with the activation's three int8
+//    planes on v_dot4_i32_i8 (exact int32) and applies the block scales once
+//    per sub-block in fp32:
+//      Q4_K: y += d*sc*(xs*sum q*X) - dmin*m*(sum x)     (quants.cpp:140-157)
+//      Q6_K: y += d*sc*xs*(sum q*X - 32*sum X)           (quants.cpp:179-202)
+//      Q8_0: y += d*xs*(sum q*X)                         (quants.cpp:133-139)
 //  * Persistent row groups: a workgroup walks its groups (R rows per wave)
 //    as a flat sequence of steps (one 64-lane sweep of 64/LPB blocks each)
 //    and always has the next step's weight loads in flight while it computes
 //    the current one. The first step's loads are issued before the
-//    activation is built (and, in the persistent kernel, before the grid
-//    barrier that precedes it). Every weight byte is read once.
+//    activation is built. Every weight byte is read once.
 // Bandwidth-bound: no MFMA.
 #pragma once
 #include <climits>
@@ -54,8 +53,8 @@ __device__ inline uint4 ld16(const void *p) { return *(const uint4 *)p; }
 struct Q4K {
     static constexpr int LPB = 4, VALUES = 256;  // lanes per block, values per block
     struct X {
-        uint32_t h0[8], h1[8], l0[8], l1[8];
-        float s0, s1, m0, m1;
+        uint32_t p[3][2][8];  // [plane hi, mid, lo][sub-block 2 sub, 2 sub + 1][dword]
+        float s0, s1, u0, u1;  // the two sub-blocks' scales and sums
     };
     struct W {
         uint4 hdr, qa, qb;
@@ -63,28 +62,21 @@ struct Q4K {
     __device__ static X load_x(const CAct &x, int b, int sub) {
         X r;
         const int base = b * 256 + 64 * sub;
-        uint4 v[4];
+        const int8_t *plane[3] = {x.hi, x.mid, x.lo};
 #pragma unroll
-        for (int k = 0; k < 4; k++) v[k] = ld16(x.hi + base + 16 * k);
+        for (int P = 0; P < 3; P++) {
 #pragma unroll
-        for (int k = 0; k < 2; k++) {
-            r.h0[4 * k] = v[k].x, r.h0[4 * k + 1] = v[k].y, r.h0[4 * k + 2] = v[k].z, r.h0[4 * k + 3] = v[k].w;
-            r.h1[4 * k] = v[k + 2].x, r.h1[4 * k + 1] = v[k + 2].y, r.h1[4 * k + 2] = v[k + 2].z,
-                     r.h1[4 * k + 3] = v[k + 2].w;
-        }
-#pragma unroll
-        for (int k = 0; k < 4; k++) v[k] = ld16(x.lo + base + 16 * k);
-#pragma unroll
-        for (int k = 0; k < 2; k++) {
-            r.l0[4 * k] = v[k].x, r.l0[4 * k + 1] = v[k].y, r.l0[4 * k + 2] = v[k].z, r.l0[4 * k + 3] = v[k].w;
-            r.l1[4 * k] = v[k + 2].x, r.l1[4 * k + 1] = v[k + 2].y, r.l1[4 * k + 2] = v[k + 2].z,
-                     r.l1[4 * k + 3] = v[k + 2].w;
+            for (int k = 0; k < 4; k++) {
+                const uint4 v = ld16(plane[P] + base + 16 * k);
+                uint32_t *d = &r.p[P][k >> 1][4 * (k & 1)];
+                d[0] = v.x, d[1] = v.y, d[2] = v.z, d[3] = v.w;
+            }
         }
         const int s = b * 8 + 2 * sub;
         r.s0 = x.scale[s];
         r.s1 = x.scale[s + 1];
-        r.m0 = x.sum[s];
-        r.m1 = x.sum[s + 1];
+        r.u0 = x.sum[s];
+        r.u1 = x.sum[s + 1];
         return r;
     }
     __device__ static W load_w(const WPtr &w, int64_t row, int nb, int b, int sub) {
@@ -97,20 +89,25 @@ struct Q4K {
     }
     __device__ static float dot(const W &w, const X &x, int sub) {
         const uint32_t q[8] = {w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w};
-        int ah0 = 0, al0 = 0, ah1 = 0, al1 = 0;
+        int a[3][2] = {{0, 0}, {0, 0}, {0, 0}};
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const int lo = (int)(q[k] & 0x0F0F0F0Fu), hi = (int)((q[k] >> 4) & 0x0F0F0F0Fu);
-            ah0 = dot4(lo, (int)x.h0[k], ah0);
-            al0 = dot4(lo, (int)x.l0[k], al0);
-            ah1 = dot4(hi, (int)x.h1[k], ah1);
-            al1 = dot4(hi, (int)x.l1[k], al1);
+#pragma unroll
+            for (int P = 0; P < 3; P++) {
+                a[P][0] = dot4(lo, (int)x.p[P][0][k], a[P][0]);
+                a[P][1] = dot4(hi, (int)x.p[P][1][k], a[P][1]);
+            }
         }
+        // sum q X per sub-block, exact in int32: |.| <= 32 * 15 * (64 * 65536 +
+        // 128 * 256 + 128) = 2,029,056,000 < 2^31.
+        const int v0 = a[0][0] * 65536 + a[1][0] * 256 + a[2][0];
+        const int v1 = a[0][1] * 65536 + a[1][1] * 256 + a[2][1];
         int sc0, m0, sc1, m1;
         kq_scale_min_pair(sub, w.hdr.y, w.hdr.z, w.hdr.w, sc0, m0, sc1, m1);
         const float d = h2f(w.hdr.x & 0xffff), dmin = h2f(w.hdr.x >> 16);
-        const float p = (float)sc0 * x.s0 * (float)(ah0 * 256 + al0) + (float)sc1 * x.s1 * (float)(ah1 * 256 + al1);
-        return d * p - dmin * ((float)m0 * x.m0 + (float)m1 * x.m1);
+        const float p = (float)sc0 * x.s0 * (float)v0 + (float)sc1 * x.s1 * (float)v1;
+        return d * p - dmin * ((float)m0 * x.u0 + (float)m1 * x.u1);
     }
 };
 
@@ -119,7 +116,7 @@ struct Q4K {
 struct Q6K {
     static constexpr int LPB = 4, VALUES = 256;
     struct X {
-        uint32_t h[4][4], l[4][4];  // [run c][dword]
+        uint32_t p[3][4][4];  // [plane][run c][dword]
         float s[4];
         int is[4];
     };
@@ -130,12 +127,15 @@ struct Q6K {
     __device__ static X load_x(const CAct &x, int b, int sub) {
         X r;
         const int h = sub >> 1, i0 = (sub & 1) * 16;
+        const int8_t *plane[3] = {x.hi, x.mid, x.lo};
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const int base = b * 256 + 128 * h + 32 * c + i0;
-            const uint4 vh = ld16(x.hi + base), vl = ld16(x.lo + base);
-            r.h[c][0] = vh.x, r.h[c][1] = vh.y, r.h[c][2] = vh.z, r.h[c][3] = vh.w;
-            r.l[c][0] = vl.x, r.l[c][1] = vl.y, r.l[c][2] = vl.z, r.l[c][3] = vl.w;
+#pragma unroll
+            for (int P = 0; P < 3; P++) {
+                const uint4 v = ld16(plane[P] + base);
+                r.p[P][c][0] = v.x, r.p[P][c][1] = v.y, r.p[P][c][2] = v.z, r.p[P][c][3] = v.w;
+            }
             r.s[c] = x.scale[base / 32];
             r.is[c] = x.isum[base / 16];
         }
@@ -157,21 +157,17 @@ struct Q6K {
         const uint32_t qa[4] = {w.qla.x, w.qla.y, w.qla.z, w.qla.w};
         const uint32_t qb[4] = {w.qlb.x, w.qlb.y, w.qlb.z, w.qlb.w};
         const uint32_t qh[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
-        int ah[4] = {0, 0, 0, 0}, al[4] = {0, 0, 0, 0};
+        int a[3][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const uint32_t q0 = (qa[k] & 0x0F0F0F0Fu) | ((qh[k] << 4) & 0x30303030u);
-            const uint32_t q1 = (qb[k] & 0x0F0F0F0Fu) | ((qh[k] << 2) & 0x30303030u);
-            const uint32_t q2 = ((qa[k] >> 4) & 0x0F0F0F0Fu) | (qh[k] & 0x30303030u);
-            const uint32_t q3 = ((qb[k] >> 4) & 0x0F0F0F0Fu) | ((qh[k] >> 2) & 0x30303030u);
-            ah[0] = dot4((int)q0, (int)x.h[0][k], ah[0]);
-            al[0] = dot4((int)q0, (int)x.l[0][k], al[0]);
-            ah[1] = dot4((int)q1, (int)x.h[1][k], ah[1]);
-            al[1] = dot4((int)q1, (int)x.l[1][k], al[1]);
-            ah[2] = dot4((int)q2, (int)x.h[2][k], ah[2]);
-            al[2] = dot4((int)q2, (int)x.l[2][k], al[2]);
-            ah[3] = dot4((int)q3, (int)x.h[3][k], ah[3]);
-            al[3] = dot4((int)q3, (int)x.l[3][k], al[3]);
+            const uint32_t q[4] = {(qa[k] & 0x0F0F0F0Fu) | ((qh[k] << 4) & 0x30303030u),
+                                   (qb[k] & 0x0F0F0F0Fu) | ((qh[k] << 2) & 0x30303030u),
+                                   ((qa[k] >> 4) & 0x0F0F0F0Fu) | (qh[k] & 0x30303030u),
+                                   ((qb[k] >> 4) & 0x0F0F0F0Fu) | ((qh[k] >> 2) & 0x30303030u)};
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+                for (int P = 0; P < 3; P++) a[P][c] = dot4((int)q[c], (int)x.p[P][c][k], a[P][c]);
         }
         // Run c's scale is byte 8h + sub%2 + 2c of the 16: dword 2h (c < 2)
         // or 2h + 1 (c >= 2), byte sub%2 + 2(c%2).
@@ -182,7 +178,9 @@ struct Q6K {
         for (int c = 0; c < 4; c++) {
             const uint32_t word = c < 2 ? s01 : s23;
             const int sc = (int)(int8_t)((word >> (sh + 16 * (c & 1))) & 0xff);
-            const int v = ah[c] * 256 + al[c] - 32 * x.is[c];
+            // sum (q - 32) X over the run, exact in 64 bits (q up to 63: the hi
+            // plane's term alone can pass 2^31).
+            const long long v = (long long)a[0][c] * 65536 + a[1][c] * 256 + a[2][c] - 32ll * x.is[c];
             p += (float)sc * x.s[c] * (float)v;
         }
         return w.d * p;
@@ -193,7 +191,7 @@ struct Q6K {
 struct Q80 {
     static constexpr int LPB = 2, VALUES = 32;
     struct X {
-        uint4 h, l;
+        uint4 p[3];  // the planes' 16 bytes
         float s;
     };
     struct W {
@@ -202,8 +200,9 @@ struct Q80 {
     };
     __device__ static X load_x(const CAct &x, int b, int sub) {
         X r;
-        r.h = ld16(x.hi + b * 32 + 16 * sub);
-        r.l = ld16(x.lo + b * 32 + 16 * sub);
+        r.p[0] = ld16(x.hi + b * 32 + 16 * sub);
+        r.p[1] = ld16(x.mid + b * 32 + 16 * sub);
+        r.p[2] = ld16(x.lo + b * 32 + 16 * sub);
         r.s = x.scale[b];
         return r;
     }
@@ -215,16 +214,16 @@ struct Q80 {
         return r;
     }
     __device__ static float dot(const W &w, const X &x, int) {
-        int ah = 0, al = 0;
-        ah = dot4((int)w.q.x, (int)x.h.x, ah);
-        ah = dot4((int)w.q.y, (int)x.h.y, ah);
-        ah = dot4((int)w.q.z, (int)x.h.z, ah);
-        ah = dot4((int)w.q.w, (int)x.h.w, ah);
-        al = dot4((int)w.q.x, (int)x.l.x, al);
-        al = dot4((int)w.q.y, (int)x.l.y, al);
-        al = dot4((int)w.q.z, (int)x.l.z, al);
-        al = dot4((int)w.q.w, (int)x.l.w, al);
-        return w.d * x.s * (float)(ah * 256 + al);
+        int a[3] = {0, 0, 0};
+#pragma unroll
+        for (int P = 0; P < 3; P++) {
+            a[P] = dot4((int)w.q.x, (int)x.p[P].x, a[P]);
+            a[P] = dot4((int)w.q.y, (int)x.p[P].y, a[P]);
+            a[P] = dot4((int)w.q.z, (int)x.p[P].z, a[P]);
+            a[P] = dot4((int)w.q.w, (int)x.p[P].w, a[P]);
+        }
+        const long long v = (long long)a[0] * 65536 + a[1] * 256 + a[2];  // int8 quants: past 2^31 in 64 bits
+        return w.d * x.s * (float)v;
     }
 };
 
@@ -251,13 +250,14 @@ __device__ inline float act_rms(const float *__restrict__ x, const float *__rest
     return 1.0f / sqrtf(ss / (float)n + eps);
 }
 
-// 16-run r of Act a (half r & 1 of sub-block r / 2) from its 16 values. Two
-// threads per 32-value sub-block, in adjacent lanes, exchange their max and
-// sum once (both call this together).
+// 16-run r of an activation (half r & 1 of sub-block r / 2) from its 16
+// values: the three planes' bytes, the run's sum of X, and the 32-value
+// chunk's scale and sum. Two threads per 32-value sub-block, in adjacent
+// lanes, exchange their max and sum once (both call this together).
 struct Run16 {
-    uint32_t hw[4], lw[4];  // hi and lo bytes of the 16 values
+    uint32_t pw[3][4];  // [plane hi, mid, lo][dword] of the 16 values
     int isum;
-    float scale, sum;       // of the 32-value chunk (both threads of the pair)
+    float scale, sum;   // of the 32-value chunk (both threads of the pair)
 };
 __device__ inline Run16 quant16(const float (&v)[16]) {
     Run16 q;
@@ -269,36 +269,39 @@ __device__ inline Run16 quant16(const float (&v)[16]) {
     }
     amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
     sum += __shfl_xor(sum, 1, WAVE);
-    const float inv = amax > 0.f ? 16383.0f / amax : 0.f;
+    const float inv = amax > 0.f ? (float)XQ_MAX / amax : 0.f;
     int is = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        uint32_t h = 0, l = 0;
+        uint32_t w[3] = {0, 0, 0};
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int x16 = max(-16383, min(16383, (int)rintf(v[4 * k + e] * inv)));
-            const int lo = (int)(int8_t)(x16 & 255);
-            const int hi = (x16 - lo) >> 8;
-            h |= (uint32_t)(hi & 255) << (8 * e);
-            l |= (uint32_t)(lo & 255) << (8 * e);
-            is += x16;
+            const int X = max(-XQ_MAX, min(XQ_MAX, (int)rintf(v[4 * k + e] * inv)));
+            int p[3];
+            xq_split(X, p[0], p[1], p[2]);
+#pragma unroll
+            for (int P = 0; P < 3; P++) w[P] |= (uint32_t)(p[P] & 255) << (8 * e);
+            is += X;
         }
-        q.hw[k] = h, q.lw[k] = l;
+#pragma unroll
+        for (int P = 0; P < 3; P++) q.pw[P][k] = w[P];
     }
-    q.isum = is, q.scale = amax / 16383.0f, q.sum = sum;
+    q.isum = is, q.scale = amax / (float)XQ_MAX, q.sum = sum;
     return q;
 }
 // Run r into the matmul layout at `m` (the token's MAct): block r / 16, chunk
 // (r % 16) / 2, bytes 16 (r & 1) .. +15 of the chunk, i.e. k-groups
-// 2 (r & 1) and 2 (r & 1) + 1.
+// 2 (r & 1) and 2 (r & 1) + 1, in each plane.
 __device__ inline void quant_run_m(const float (&v)[16], int r, uint8_t *m) {
     const Run16 q = quant16(v);
     uint8_t *blk = m + (size_t)(r / 16) * MACT_BLOCK;
     const int c = (r % 16) / 2, kq = 2 * (r & 1);
-    *(uint2 *)(blk + kq * 64 + 8 * c) = make_uint2(q.hw[0], q.hw[1]);
-    *(uint2 *)(blk + (kq + 1) * 64 + 8 * c) = make_uint2(q.hw[2], q.hw[3]);
-    *(uint2 *)(blk + MACT_LO + kq * 64 + 8 * c) = make_uint2(q.lw[0], q.lw[1]);
-    *(uint2 *)(blk + MACT_LO + (kq + 1) * 64 + 8 * c) = make_uint2(q.lw[2], q.lw[3]);
+    const int plane[3] = {0, MACT_MID, MACT_LO};
+#pragma unroll
+    for (int P = 0; P < 3; P++) {
+        *(uint2 *)(blk + plane[P] + kq * 64 + 8 * c) = make_uint2(q.pw[P][0], q.pw[P][1]);
+        *(uint2 *)(blk + plane[P] + (kq + 1) * 64 + 8 * c) = make_uint2(q.pw[P][2], q.pw[P][3]);
+    }
     ((int *)(blk + MACT_ISUM))[r % 16] = q.isum;
     if ((r & 1) == 0) {
         ((float *)(blk + MACT_SCALE))[c] = q.scale;
@@ -307,37 +310,14 @@ __device__ inline void quant_run_m(const float (&v)[16], int r, uint8_t *m) {
 }
 
 __device__ inline void quant_run(const float (&v)[16], int r, const Act &a) {
-    float amax = 0.f, sum = 0.f;
+    const Run16 q = quant16(v);
+    int8_t *plane[3] = {a.hi, a.mid, a.lo};
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        amax = fmaxf(amax, fabsf(v[i]));
-        sum += v[i];
-    }
-    amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
-    sum += __shfl_xor(sum, 1, WAVE);
-    const float inv = amax > 0.f ? 16383.0f / amax : 0.f;
-    uint32_t hw[4], lw[4];
-    int is = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        uint32_t h = 0, l = 0;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int x16 = max(-16383, min(16383, (int)rintf(v[4 * k + e] * inv)));
-            const int lo = (int)(int8_t)(x16 & 255);
-            const int hi = (x16 - lo) >> 8;
-            h |= (uint32_t)(hi & 255) << (8 * e);
-            l |= (uint32_t)(lo & 255) << (8 * e);
-            is += x16;
-        }
-        hw[k] = h, lw[k] = l;
-    }
-    *(uint4 *)(a.hi + 16 * r) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    *(uint4 *)(a.lo + 16 * r) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-    a.isum[r] = is;
+    for (int P = 0; P < 3; P++) *(uint4 *)(plane[P] + 16 * r) = make_uint4(q.pw[P][0], q.pw[P][1], q.pw[P][2], q.pw[P][3]);
+    a.isum[r] = q.isum;
     if ((r & 1) == 0) {
-        a.scale[r / 2] = amax / 16383.0f;
-        a.sum[r / 2] = sum;
+        a.scale[r / 2] = q.scale;
+        a.sum[r / 2] = q.sum;
     }
 }
 
@@ -519,7 +499,7 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
     const Act xa = act_view(lds, a.n_in);
     if constexpr (RUNS > 0) act_in_build<NT, RUNS, NORM>(ain, a.eps, a.n_in, xa, red);
     else if (g < ngroups) build_act<NT>(a.x, a.norm_w, a.eps, a.n_in, xa, red);
-    const CAct x{xa.hi, xa.lo, xa.scale, xa.sum, xa.isum};
+    const CAct x{xa.hi, xa.mid, xa.lo, xa.scale, xa.sum, xa.isum};
 
     float acc[NW][R];
 #pragma unroll

@@ -61,18 +61,19 @@ def pack_scale_min(sc: np.ndarray, m: np.ndarray) -> np.ndarray:
     return out
 
 
-def blocks(t: int, n_blocks: int, rng: np.random.Generator, centered: bool = False) -> np.ndarray:
+def blocks(t: int, n_blocks: int, rng: np.random.Generator, centered: bool = False, dscale: float = 0.01) -> np.ndarray:
     """n_blocks blocks of type t as a (n_blocks, block_bytes) uint8 array.
 
     centered (Q4_K only): dmin = 8 d and each min = round(7.5 scale / 8), so a
     sub-block's values centre near zero instead of near 7.5 d scale. The
     benchmark's distribution has every weight's mean far above zero, which
     makes a random model's output almost independent of its input; the
-    centred variant is for parity tests whose argmax should vary with it."""
+    centred variant is for parity tests whose argmax should vary with it.
+    dscale (centred only): d = f16(|N(0,1)| * dscale)."""
     bb = BLOCK[t][1]
     out = np.frombuffer(rng.bytes(n_blocks * bb), dtype=np.uint8).reshape(n_blocks, bb).copy()
     if t == Q4_K and centered:
-        d = (np.abs(rng.standard_normal(n_blocks)) * 0.01).astype(np.float16)
+        d = (np.abs(rng.standard_normal(n_blocks)) * dscale).astype(np.float16)
         out[:, 0:2] = np.ascontiguousarray(d).view(np.uint8).reshape(-1, 2)
         out[:, 2:4] = _half_bytes(d.astype(np.float32) * 8)
         sc = rng.integers(0, 64, size=(n_blocks, 8))
@@ -94,11 +95,12 @@ def blocks(t: int, n_blocks: int, rng: np.random.Generator, centered: bool = Fal
     return out
 
 
-def tensor(t: int, ne0: int, ne1: int, seed: int, name: str, centered: bool = False) -> np.ndarray:
+def tensor(t: int, ne0: int, ne1: int, seed: int, name: str, centered: bool = False,
+           dscale: float = 0.01) -> np.ndarray:
     """A (ne1, row_bytes) uint8 matrix of type t: rows are output rows."""
     rb = row_bytes(t, ne0)
     bv, bb = BLOCK[t]
-    b = blocks(t, ne0 // bv * ne1, rng_for(seed, name), centered)
+    b = blocks(t, ne0 // bv * ne1, rng_for(seed, name), centered, dscale)
     return b.reshape(ne1, rb)
 
 
@@ -142,7 +144,7 @@ def model_tensors(hp: dict, seed: int):
     out = {}
 
     def mat(name, t, ne0, ne1):
-        out[name] = (t, ne0, ne1, tensor(t, ne0, ne1, seed, name, hp.get("centered", False)))
+        out[name] = (t, ne0, ne1, tensor(t, ne0, ne1, seed, name, hp.get("centered", False), hp.get("dscale", 0.01)))
 
     mat("token_embd.weight", hp["embd_type"], E, V)
     out["output_norm.weight"] = (F32, E, 1, norm_weight(E, seed, "output_norm.weight"))
@@ -160,6 +162,28 @@ def model_tensors(hp: dict, seed: int):
         mat(p + "ffn_up.weight", wt, E, F)
         mat(p + "ffn_down.weight", hp.get("down_type", wt), F, E)
     return out
+
+
+def tensor_specs(hp: dict):
+    """(name, type, ne0, ne1) of every tensor of a model (engine/src/model.cpp:89-119 names),
+    for weights generated in HBM (ts5hip Model.synth_tensor)."""
+    E, F, H, HKV, HD, V = (hp[k] for k in ("n_embd", "n_ff", "n_head", "n_head_kv", "head_dim", "n_vocab"))
+    wt = hp["wtype"]
+    yield "token_embd.weight", hp["embd_type"], E, V
+    yield "output_norm.weight", F32, E, 1
+    if hp.get("head_type") is not None:
+        yield "output.weight", hp["head_type"], E, V
+    for i in range(hp["n_layer"]):
+        p = f"blk.{i}."
+        yield p + "attn_norm.weight", F32, E, 1
+        yield p + "ffn_norm.weight", F32, E, 1
+        yield p + "attn_q.weight", wt, E, H * HD
+        yield p + "attn_k.weight", wt, E, HKV * HD
+        yield p + "attn_v.weight", wt, E, HKV * HD
+        yield p + "attn_output.weight", wt, H * HD, E
+        yield p + "ffn_gate.weight", wt, E, F
+        yield p + "ffn_up.weight", wt, E, F
+        yield p + "ffn_down.weight", hp.get("down_type", wt), F, E
 
 
 def weight_bytes(hp: dict) -> dict:

@@ -18,7 +18,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "ts5hip.h")
 
 OK, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED, ERR_CONTEXT_FULL, ERR_STATE = 0, -1, -2, -3, -4, -5
 F32, F16, Q8_0, Q4_K, Q6_K = 0, 1, 8, 12, 14
-KV_Q8 = 2
+KV_F32, KV_F16, KV_Q8 = 0, 1, 2
 
 _vp, _i64, _i32, _u32, _u64, _f32 = C.c_void_p, C.c_int64, C.c_int, C.c_uint32, C.c_uint64, C.c_float
 
@@ -27,6 +27,12 @@ class HParams(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("n_vocab", "n_embd", "n_layer", "n_ff", "n_head", "n_head_kv",
                                           "head_dim", "rope_dims", "rope_neox")] + \
                [(n, C.c_float) for n in ("rms_eps", "rope_base", "attn_scale", "rope_scale")]
+
+
+class CheckResult(C.Structure):
+    """ts5hip_check_result: CheckResult (engine/src/checks.h:17-24)."""
+    _fields_ = [("n", C.c_int32), ("same_top", C.c_int32), ("worst", C.c_int32), ("max_diff", C.c_double),
+                ("rel", C.c_double), ("gpu_ms", C.c_double), ("pass_", C.c_int32), ("saved", C.c_int32)]
 
 
 class SampleParams(C.Structure):
@@ -66,6 +72,7 @@ _SIGS = {
                                      _f32, _vp, _vp, _vp, _vp, _vp]),
     "ts5hip_attn_decode": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _f32, _i32,
                                   _vp]),
+    "ts5hip_attn_decode_f16": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _i32, _f32, _i32, _vp]),
     "ts5hip_attn_prompt": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "ts5hip_argmax": (_i32, [_vp, _vp, _i32, _i32, _vp]),
     "ts5hip_topk": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp]),
@@ -86,7 +93,20 @@ _SIGS = {
     "ts5hip_logits_topk": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp]),
     "ts5hip_generate_greedy": (_i32, [_vp, C.c_int32, _i32, _i32, _vp]),
     "ts5hip_kv_read": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
+    "ts5hip_kv_write": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
     "ts5hip_take_profile": (_i32, [_vp, C.c_char_p, _i32]),
+    "ts5hip_model_set_tensor_rows": (_i32, [_vp, C.c_char_p, _u32, _i64, _i64, _i64, _i64, _vp]),
+    "ts5hip_kv_bytes_per_token": (_u64, [C.POINTER(HParams), _i32]),
+    "ts5hip_fit_context": (_i32, [_u64, _u64, _u64, _i32]),
+    "ts5hip_f16_reaches": (_i32, [_i32, _i32]),
+    "ts5hip_gguf_hparams": (_i32, [C.c_char_p, C.POINTER(HParams), C.POINTER(_i32), C.POINTER(_i64)]),
+    "ts5hip_model_load": (_i32, [_vp, C.c_char_p, _i32, _i32, _i32, C.POINTER(_vp), C.POINTER(_i32)]),
+    "ts5hip_check_tokens": (_i32, [_i32, _i32, _vp]),
+    "ts5hip_model_file_id": (_i32, [C.c_char_p, C.POINTER(_u64), C.POINTER(_u64)]),
+    "ts5hip_ref_path": (_i32, [C.c_char_p, _i32, C.c_char_p, _i32]),
+    "ts5hip_ref_load": (_i32, [C.c_char_p, _i32, _i32, _i32, _vp]),
+    "ts5hip_ref_save": (_i32, [C.c_char_p, _i32, _i32, _i32, _vp]),
+    "ts5hip_check_run": (_i32, [_vp, C.c_char_p, _i32, _vp, _vp]),
     "ts5hip_engine_new": (_i32, [_vp, C.POINTER(_vp)]),
     "ts5hip_engine_free": (None, [_vp]),
     "ts5hip_engine_set_drafter": (_i32, [_vp, _vp]),
@@ -286,6 +306,10 @@ class Context:
         self.check(lib().ts5hip_attn_decode(self.h, _ptr(q), B, H, HKV, HD, _ptr(k8), _ptr(ks), _ptr(v8), _ptr(vs),
                                             n_ctx, _ptr(n_keys_dev), int(kv_per_batch), scale, n_split, _ptr(out)))
 
+    def attn_decode_f16(self, q, B, H, HKV, HD, k16, v16, n_ctx, n_keys_dev, kv_per_batch, scale, out, n_split=0):
+        self.check(lib().ts5hip_attn_decode_f16(self.h, _ptr(q), B, H, HKV, HD, _ptr(k16), _ptr(v16), n_ctx,
+                                                _ptr(n_keys_dev), int(kv_per_batch), scale, n_split, _ptr(out)))
+
     def attn_prompt(self, q, nq, H, HKV, HD, k8, ks, v8, vs, n_ctx, pos0, scale, out):
         self.check(lib().ts5hip_attn_prompt(self.h, _ptr(q), nq, H, HKV, HD, _ptr(k8), _ptr(ks), _ptr(v8), _ptr(vs),
                                             n_ctx, pos0, scale, _ptr(out)))
@@ -388,6 +412,25 @@ class Model:
         self.ctx.check(lib().ts5hip_generate_greedy(self.h, token, pos, n_steps, out.ctypes.data))
         return out
 
+    def n_ctx(self) -> int:
+        return lib().ts5hip_n_ctx(self.h)
+
+    def check_run(self, model_path: "str | None", n: int, ref_logits: "np.ndarray | None" = None) -> CheckResult:
+        """ts5 check (run_check) of this model against ref_logits or the saved .ts5ref of model_path."""
+        r = CheckResult()
+        ref = None if ref_logits is None else np.ascontiguousarray(ref_logits, np.float32)
+        self.ctx.check(lib().ts5hip_check_run(self.h, model_path.encode() if model_path else None, n,
+                                              _ptr(ref), C.byref(r)))
+        return r
+
+    def kv_write(self, layer: int, which: int, pos0: int, values: np.ndarray):
+        """fp32 [n][n_head_kv * head_dim] into the cache at pos0.., rounded as the cache keeps them."""
+        v = np.ascontiguousarray(values, np.float32)
+        self.ctx.check(lib().ts5hip_kv_write(self.h, layer, which, pos0, v.shape[0], v.ctypes.data))
+
+    def kv_type(self) -> int:
+        return lib().ts5hip_kv_type(self.h)
+
     def kv(self, layer: int, which: int, pos0: int, n: int) -> np.ndarray:
         w = self.hp["n_head_kv"] * self.hp["head_dim"]
         out = np.empty((n, w), np.float32)
@@ -404,6 +447,19 @@ class Model:
         buf = C.create_string_buffer(4096)
         self.ctx.check(lib().ts5hip_take_profile(self.h, buf, 4096))
         return buf.value.decode()
+
+
+def load_model(ctx: "Context", path: str, n_ctx: int = 0, kv: int = KV_Q8, threads: int = 0) -> "Model":
+    """ts5hip_model_load: a Model of a GGUF file (n_ctx 0: the context that fits)."""
+    h, kv_out = _vp(), _i32()
+    ctx.check(lib().ts5hip_model_load(ctx.h, path.encode(), n_ctx, kv, threads, C.byref(h), C.byref(kv_out)))
+    hp_raw, _, _ = gguf_hparams(path)
+    m = Model.__new__(Model)
+    m.ctx, m.hp, m.h = ctx, hp_raw, h.value
+    ctx._models.add(m)
+    m.n_vocab = hp_raw["n_vocab"]
+    m.chosen_kv = kv_out.value
+    return m
 
 
 class Engine:
@@ -444,3 +500,66 @@ class Engine:
             self.close()
         except Exception:
             pass
+
+
+# ---- GGUF files, KV sizing, ts5 check --------------------------------------------------------
+
+def kv_bytes_per_token(hp: dict, kv: int) -> int:
+    h = hparams(hp)
+    return int(lib().ts5hip_kv_bytes_per_token(C.byref(h), kv))
+
+
+def fit_context(memory: int, used: int, per_token: int, cap: int) -> int:
+    return int(lib().ts5hip_fit_context(memory, used, per_token, cap))
+
+
+def f16_reaches(f16_ctx: int, train: int) -> bool:
+    return bool(lib().ts5hip_f16_reaches(f16_ctx, train))
+
+
+def gguf_hparams(path: str):
+    """(hparams fields as a dict, training context, HBM bytes beside the KV cache) of a GGUF file."""
+    h, train, fixed = HParams(), _i32(), _i64()
+    rc = lib().ts5hip_gguf_hparams(path.encode(), C.byref(h), C.byref(train), C.byref(fixed))
+    if rc != OK:
+        raise Ts5HipError(rc, lib().ts5hip_last_error(None).decode())
+    return {f: getattr(h, f) for f, _ in HParams._fields_}, train.value, fixed.value
+
+
+def check_tokens(n: int, n_vocab: int) -> np.ndarray:
+    out = np.empty(n, np.int32)
+    rc = lib().ts5hip_check_tokens(n, n_vocab, out.ctypes.data)
+    if rc != OK:
+        raise Ts5HipError(rc, lib().ts5hip_last_error(None).decode())
+    return out
+
+
+def model_file_id(path: str):
+    size, h = _u64(), _u64()
+    rc = lib().ts5hip_model_file_id(path.encode(), C.byref(size), C.byref(h))
+    if rc != OK:
+        raise Ts5HipError(rc, lib().ts5hip_last_error(None).decode())
+    return size.value, h.value
+
+
+def ref_path(model_path: str, kv: int) -> str:
+    buf = C.create_string_buffer(4096)
+    rc = lib().ts5hip_ref_path(model_path.encode(), kv, buf, 4096)
+    if rc != OK:
+        raise Ts5HipError(rc, lib().ts5hip_last_error(None).decode())
+    return buf.value.decode()
+
+
+def ref_load(model_path: str, n: int, n_vocab: int, kv: int) -> np.ndarray:
+    out = np.empty((n, n_vocab), np.float32)
+    rc = lib().ts5hip_ref_load(model_path.encode(), n, n_vocab, kv, out.ctypes.data)
+    if rc != OK:
+        raise Ts5HipError(rc, lib().ts5hip_last_error(None).decode())
+    return out
+
+
+def ref_save(model_path: str, kv: int, logits: np.ndarray) -> None:
+    lg = np.ascontiguousarray(logits, np.float32)
+    rc = lib().ts5hip_ref_save(model_path.encode(), lg.shape[0], lg.shape[1], kv, lg.ctypes.data)
+    if rc != OK:
+        raise Ts5HipError(rc, lib().ts5hip_last_error(None).decode())

@@ -135,6 +135,17 @@ int ts5hip_attn_decode(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n
 int ts5hip_attn_decode_f16(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n_head_kv, int head_dim,
                            const void *k16, const void *v16, int n_ctx, const int32_t *n_keys_dev, int kv_per_batch,
                            float scale, int n_split, float *out);
+/* ts5hip_attn_decode without any allocation: no counterpart in the reference. For callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The same arguments, kernels and results as
+ * ts5hip_attn_decode, but the split partials and merge counters live in a static device array
+ * of 4 MiB per GPU (held until the process ends; its address is looked up at ts5hip_init):
+ * calls needing more than 3.5 MiB of partials (B x n_split x n_head_kv x ~2 KB at head_dim
+ * 128) fail with TS5HIP_ERR_ARG. Every call on one GPU shares that array, whichever context
+ * makes it: calls that overlap on one GPU (other streams, other contexts, other threads) race. */
+int ts5hip_attn_decode_noalloc(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n_head_kv, int head_dim,
+                               const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx,
+                               const int32_t *n_keys_dev, int kv_per_batch, float scale, int n_split, float *out);
 /* Causal prompt attention on the matrix cores (attn_pf, engine/shaders/attn_pf.glsl with its
  * policy at engine/src/vk_backend.cpp:954-961; CPU engine/src/cpu_backend.cpp:222-248): nq
  * queries at positions pos0 .. pos0 + nq - 1 over one q8 cache (the layout above), query t

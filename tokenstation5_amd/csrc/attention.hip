@@ -16,6 +16,8 @@
 // Cache layout per layer: K8/V8 int8 [seq][kv_head][slot][head_dim] and
 // Ks/Vs f16 [seq][kv_head][slot][head_dim/32]: one KV head's keys are
 // contiguous, 128 + 8 bytes per key at head_dim 128.
+#include <mutex>
+
 #include "attn_core.h"
 
 namespace ts5hip {
@@ -167,6 +169,36 @@ hipError_t launch_kv_write(KvLayer kv, int which, int HKV, int HD, int n_ctx, in
                            const float *in, hipStream_t s) {
     hipLaunchKernelGGL(k_kv_write, dim3(n, HKV), dim3(64), 0, s, kv, which, HKV, HD, n_ctx, pos0, kv_f16, in);
     return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// The scratch of the no-allocation entry point (ts5hip_attn_decode_noalloc):
+// the merge counters (NOALLOC_COUNTER_BYTES, kept at zero between launches by
+// the kernels themselves), then the split partials. Each GPU holds its own
+// copy for the life of the process. Host code never passes `scratch` itself
+// to a kernel (its host name is a stand-in, not a device address); it uses
+// the address hipGetSymbolAddress gives for the current device.
+static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
+
+namespace {
+std::mutex g_noalloc_mu;
+void *g_noalloc[NOALLOC_DEVICES];  // the array's address on each device, once looked up
+}  // namespace
+
+hipError_t attn_noalloc_setup(int device, void **ptr, hipStream_t s) {
+    if (device < 0 || device >= NOALLOC_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc[device]) {
+        void *p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));  // device `device` is current
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        if ((e = hipMemsetAsync(p, 0, NOALLOC_COUNTER_BYTES, s)) != hipSuccess) return e;
+        if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
+        g_noalloc[device] = p;
+    }
+    *ptr = g_noalloc[device];
+    return hipSuccess;
 }
 
 // ---------------------------------------------------------------------------

@@ -101,6 +101,11 @@ int ts5hip_init(int device, ts5hip_ctx **out) {
         ts5hip_destroy(c);
         return TS5HIP_ERR_HIP;
     }
+    if ((e = attn_noalloc_setup(device, &c->noalloc, c->stream)) != hipSuccess) {
+        hip_fail(nullptr, e, "no-allocation scratch (hipGetSymbolAddress)");
+        ts5hip_destroy(c);
+        return TS5HIP_ERR_HIP;
+    }
     *out = c;
     return TS5HIP_OK;
 }
@@ -325,7 +330,13 @@ static int attn_decode_into(ts5hip_ctx *ctx, const float *q, int B, int n_head, 
     if (n_split <= 0) n_split = attn_splits(B, n_head_kv, ctx->n_cu);
     if (n_split > 64) return fail(ctx, TS5HIP_ERR_ARG, "n_split %d (at most 64)", n_split);
     const size_t need = attn_partial_bytes(B, n_split, n_head, n_head_kv, head_dim);
-    if (!part) {
+    if (part) {
+        if (need > NOALLOC_BYTES - NOALLOC_COUNTER_BYTES)
+            return fail(ctx, TS5HIP_ERR_ARG,
+                        "%d queries x %d splits x %d KV heads need %zu bytes of partials; the no-allocation "
+                        "scratch holds %zu",
+                        B, n_split, n_head_kv, need, NOALLOC_BYTES - NOALLOC_COUNTER_BYTES);
+    } else {
         if (int rc = ensure_scratch(ctx, need)) return rc;
         part = (float *)ctx->scratch, counters = ctx->counters;
     }
@@ -352,6 +363,15 @@ int ts5hip_attn_decode_f16(ts5hip_ctx *ctx, const float *q, int B, int n_head, i
                            float scale, int n_split, float *out) {
     return attn_decode_into(ctx, q, B, n_head, n_head_kv, head_dim, k16, nullptr, v16, nullptr, n_ctx, n_keys_dev,
                             kv_per_batch, scale, n_split, out, nullptr, nullptr, 1);
+}
+
+int ts5hip_attn_decode_noalloc(ts5hip_ctx *ctx, const float *q, int B, int n_head, int n_head_kv, int head_dim,
+                               const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx,
+                               const int32_t *n_keys_dev, int kv_per_batch, float scale, int n_split, float *out) {
+    if (!ctx || !ctx->noalloc) return fail(ctx, TS5HIP_ERR_STATE, "no context or no-allocation scratch");
+    uint8_t *base = (uint8_t *)ctx->noalloc;
+    return attn_decode_into(ctx, q, B, n_head, n_head_kv, head_dim, k8, ks, v8, vs, n_ctx, n_keys_dev, kv_per_batch,
+                            scale, n_split, out, (float *)(base + NOALLOC_COUNTER_BYTES), (int *)base);
 }
 
 int ts5hip_attn_prompt(ts5hip_ctx *ctx, const float *q, int nq, int n_head, int n_head_kv, int head_dim,

@@ -106,6 +106,16 @@ struct AttnIO {
     float *out;     // [B][H * HD]
 };
 hipError_t launch_attn(const AttnIO &io, hipStream_t s);
+// The no-allocation entry point's scratch: a static device array of
+// NOALLOC_BYTES per GPU, merge counters first (up to 4096 (query, KV head)
+// pairs, CTR_STRIDE ints apart), then up to NOALLOC_BYTES -
+// NOALLOC_COUNTER_BYTES of split partials. attn_noalloc_setup (once per
+// device, that device current; the library's init calls it) looks up its
+// address there and zeroes the counters.
+constexpr size_t NOALLOC_BYTES = 4u << 20;
+constexpr size_t NOALLOC_COUNTER_BYTES = (size_t)4096 * CTR_STRIDE * 4;
+constexpr int NOALLOC_DEVICES = 64;
+hipError_t attn_noalloc_setup(int device, void **ptr, hipStream_t s);
 // attn_prefill.hip: causal attention of nq consecutive queries (positions p0..,
 // rows q [nq][q_stride]) over one q8 cache on the matrix cores; out [nq][H * HD];
 // part: attn_prefill_partial_bytes(nq, H, HD, p0 + nq) bytes.

@@ -22,6 +22,8 @@ struct ts5hip_ctx {
     size_t scratch_bytes = 0;
     // Zeroed once; kernels that count finished workgroups leave them zero.
     int *counters = nullptr;  // 4096 attention counters (CTR_STRIDE apart), then the head argmax's
+    // The device's no-allocation scratch (attention.hip `scratch`), looked up at init.
+    void *noalloc = nullptr;
 };
 
 namespace ts5hip {

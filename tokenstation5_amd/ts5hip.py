@@ -73,6 +73,8 @@ _SIGS = {
     "ts5hip_attn_decode": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _f32, _i32,
                                   _vp]),
     "ts5hip_attn_decode_f16": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _vp, _i32, _f32, _i32, _vp]),
+    "ts5hip_attn_decode_noalloc": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32,
+                                          _f32, _i32, _vp]),
     "ts5hip_attn_prompt": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "ts5hip_argmax": (_i32, [_vp, _vp, _i32, _i32, _vp]),
     "ts5hip_topk": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp]),
@@ -309,6 +311,12 @@ class Context:
     def attn_decode_f16(self, q, B, H, HKV, HD, k16, v16, n_ctx, n_keys_dev, kv_per_batch, scale, out, n_split=0):
         self.check(lib().ts5hip_attn_decode_f16(self.h, _ptr(q), B, H, HKV, HD, _ptr(k16), _ptr(v16), n_ctx,
                                                 _ptr(n_keys_dev), int(kv_per_batch), scale, n_split, _ptr(out)))
+
+    def attn_decode_noalloc(self, q, B, H, HKV, HD, k8, ks, v8, vs, n_ctx, n_keys_dev, kv_per_batch, scale, out,
+                            n_split=0):
+        self.check(lib().ts5hip_attn_decode_noalloc(self.h, _ptr(q), B, H, HKV, HD, _ptr(k8), _ptr(ks), _ptr(v8),
+                                                    _ptr(vs), n_ctx, _ptr(n_keys_dev), int(kv_per_batch), scale,
+                                                    n_split, _ptr(out)))
 
     def attn_prompt(self, q, nq, H, HKV, HD, k8, ks, v8, vs, n_ctx, pos0, scale, out):
         self.check(lib().ts5hip_attn_prompt(self.h, _ptr(q), nq, H, HKV, HD, _ptr(k8), _ptr(ks), _ptr(v8), _ptr(vs),

@@ -134,6 +134,173 @@ def glu_roofline(ctx, hp, launches: int = 200):
                 algorithmic_bytes=int(algo))
 
 
+_busy = {}
+
+
+def timed(ctx, fn, n: int, warm: int = 3, busy: bool = True) -> float:
+    """Mean microseconds of fn(i) over n calls on the library's stream, HIP
+    events around them (after `warm` untimed ones). With `busy`, the stream is
+    first given RMSNorm work over 1 GiB (~0.4 ms a launch, enough for the host
+    to queue every timed launch meanwhile), so that the events time kernels
+    back to back rather than the host's launch rate."""
+    for i in range(warm):
+        fn(i)
+    if busy:
+        if ctx not in _busy:
+            bx, by = ctx.alloc(4096 * 65536 * 4), ctx.alloc(4096 * 65536 * 4)
+            bx.zero()
+            _busy[ctx] = (bx, by, ctx.to_device(np.ones(4096, np.float32)))
+        bx, by, ones = _busy[ctx]
+        ctx.sync()
+        for _ in range(2 + n // 10):
+            ctx.rmsnorm(bx, ones, 1e-5, 4096, 65536, by)
+    else:
+        ctx.sync()
+    ctx.timer_begin()
+    for i in range(n):
+        fn(i)
+    return ctx.timer_end() * 1e3 / n
+
+
+def free_busy(ctx):
+    for b in _busy.pop(ctx, ())[:2]:
+        b.free()
+
+
+def cfg1_matvec(ctx):
+    """cfg1: the 4096x4096 Q4_K matvec alone, 40 rotated copies (378 MB, past
+    the 256 MB Infinity Cache), 200 launches."""
+    E = 4096
+    copies = 40
+    ws = [ctx.weight_synth(synth.Q4_K, E, E, 300 + i) for i in range(copies)]
+    x = ctx.to_device(np.random.default_rng(1).standard_normal(E).astype(np.float32))
+    y = ctx.alloc(E * 4)
+    us = timed(ctx, lambda i: ctx.matvec(synth.Q4_K, ws[i % copies], E, E, x, y), 200)
+    algo = E * E // 256 * 144 + 4 * E + 4 * E  # 9,469,952 B
+    for w in ws:
+        w.free()
+    return dict(us=round(us, 2), gbs=round(algo / us / 1e3, 1), bytes=algo)
+
+
+def cfg3_attention(ctx):
+    """cfg3: flash decode over q8 (and f16) caches, one query per sequence,
+    32/8 heads of 128, every key. Buffers are rotated so each launch reads
+    past the Infinity Cache (> 300 MB of caches in rotation)."""
+    H, HKV, HD = 32, 8, 128
+    scale = float(np.float32(1) / np.sqrt(np.float32(HD)))
+    out = {}
+    for B in (1, 4, 16):
+        for n in (8192, 32768):
+            for kvn, f16 in (("q8", False), ("f16", True)):
+                vb = 2 if f16 else 1
+                cache = B * HKV * n * HD * vb
+                copies = max(1, -(-(300 << 20) // (2 * cache)))
+                bufs = []
+                for c in range(copies):
+                    k, v = ctx.alloc(cache), ctx.alloc(cache)
+                    k.upload(np.full(cache, 0x1d + c, np.uint8))
+                    v.upload(np.full(cache, 0x2e + c, np.uint8))
+                    sk = sv = None
+                    if not f16:
+                        sk, sv = ctx.alloc(cache // 16), ctx.alloc(cache // 16)
+                        sk.upload(np.full(cache // 16, 0x21, np.uint8))
+                        sv.upload(np.full(cache // 16, 0x21, np.uint8))
+                    bufs.append((k, sk, v, sv))
+                q = ctx.to_device(np.random.default_rng(B).standard_normal((B, H * HD)).astype(np.float32))
+                o = ctx.alloc(B * H * HD * 4)
+                nk = ctx.to_device(np.full(B, n, np.int32))
+
+                def run(i):
+                    k, sk, v, sv = bufs[i % copies]
+                    if f16:
+                        ctx.attn_decode_f16(q, B, H, HKV, HD, k, v, n, nk, 1, scale, o)
+                    else:
+                        ctx.attn_decode(q, B, H, HKV, HD, k, sk, v, sv, n, nk, 1, scale, o)
+
+                us = timed(ctx, run, 40 if B * n <= 65536 else 10)
+                algo = B * n * HKV * 2 * HD * (vb + (0 if f16 else 2 / 32)) + 2 * B * H * HD * 4
+                out[f"{kvn}_B{B}_{n // 1024}k"] = dict(us=round(us, 1), gbs=round(algo / us / 1e3, 1))
+                for t in bufs:
+                    for b in t:
+                        if b is not None:
+                            b.free()
+    return out
+
+
+def cfg4_head_sampling(ctx):
+    """cfg4: the Q6_K head 128256x4096 (431 MB, two copies in rotation), then
+    the GPU top-40 and the host draw at T 0.7, p 0.9; and the head with the
+    greedy pick fused in."""
+    E, V = 4096, 128256
+    ws = [ctx.weight_synth(synth.Q6_K, E, V, 400 + i) for i in range(2)]
+    rng = np.random.default_rng(4)
+    h = ctx.to_device(rng.standard_normal(E).astype(np.float32))
+    nw = ctx.to_device((1 + 0.02 * rng.standard_normal(E)).astype(np.float32))
+    y, out = ctx.alloc(V * 4), ctx.alloc(4)
+    head = timed(ctx, lambda i: ctx.matvec(synth.Q6_K, ws[i % 2], E, V, h, y, norm_w=nw, eps=1e-5), 50)
+    fused = timed(ctx, lambda i: ctx.matvec_argmax(synth.Q6_K, ws[i % 2], E, V, h, y, out, norm_w=nw, eps=1e-5), 50)
+    vals, ids = ctx.alloc(40 * 4), ctx.alloc(40 * 4)
+    topk = timed(ctx, lambda i: ctx.topk(y, V, 40, vals, ids), 50)
+    smp = ts5hip.Sampler(7)
+    t0 = time.perf_counter()
+    for _ in range(100):
+        smp.draw(ids.download(np.int32), vals.download(np.float32), 0.7, 0.9)
+    draw_us = (time.perf_counter() - t0) / 100 * 1e6
+    for w in ws:
+        w.free()
+    algo = V * E // 256 * 210 + 4 * E * 2 + 4 * V
+    return dict(head_us=round(head, 1), head_gbs=round(algo / head / 1e3, 1), head_argmax_us=round(fused, 1),
+                topk40_us=round(topk, 1), host_draw_us=round(draw_us, 1),
+                step_us=round(head + topk + draw_us, 1))
+
+
+def cfg5_speculation(ctx, gen: int = 512, prompt_len: int = 2048):
+    """cfg5: the 24-layer 896-wide draft model proposing k = 4 per step for
+    the 48-layer 5120-wide target and for the 8B, after a 2048-token prompt
+    of uniform ids, 512 tokens, greedy (random-init weights of the configs'
+    own distribution). Per target: tok/s without and with drafting, output
+    equality, drafted / accepted, a 5-token verify forward against one step,
+    and the draft model's time per drafted token."""
+    n_ctx = prompt_len + gen + 16
+    draft = ts5hip.Model(ctx, synth.DRAFT_0P5B, n_ctx)
+    for name, t, ne0, ne1 in synth.tensor_specs(synth.DRAFT_0P5B):
+        draft.synth_tensor(name, t, ne0, ne1, SEED + 5)
+    res = {}
+    for tag, hp in (("target_48x5120", synth.TARGET_14B), ("llama_8b", synth.LLAMA_8B)):
+        m = ts5hip.Model(ctx, hp, n_ctx)
+        for name, t, ne0, ne1 in synth.tensor_specs(hp):
+            m.synth_tensor(name, t, ne0, ne1, SEED + 5)
+        prompt = np.random.default_rng(5).integers(0, hp["n_vocab"], prompt_len).astype(np.int32)
+        runs = {}
+        for k in (0, 4):
+            e = ts5hip.Engine(m)
+            e.set_drafter(draft if k else None)
+            e.generate(prompt, temperature=0.0, max_tokens=8, draft=k)  # the prompt cached on both models
+            t0 = time.time()
+            ids, st = e.generate(prompt, temperature=0.0, max_tokens=gen, draft=k)
+            dt = time.time() - t0
+            runs[k] = (ids, st, dt)
+            e.close()
+        pos = prompt_len + 8
+        batch = np.array(runs[0][0][:5], np.int32)
+
+        def fwd(model, n):  # the engine's call: every row's logits kept in HBM
+            ctx.check(ts5hip.lib().ts5hip_forward_in_place(model.h, batch.ctypes.data, n, pos, int(n > 1)))
+
+        step = timed(ctx, lambda i: fwd(m, 1), 10, 2, busy=False)
+        verify = timed(ctx, lambda i: fwd(m, 5), 10, 2, busy=False)
+        dstep = timed(ctx, lambda i: fwd(draft, 1), 10, 2, busy=False)
+        (ids0, st0, dt0), (ids4, st4, dt4) = runs[0], runs[4]
+        res[tag] = dict(tok_s_draft0=round(gen / dt0, 1), tok_s_draft4=round(gen / dt4, 1),
+                        same_output=bool(np.array_equal(ids0, ids4)), drafted=int(st4[3]), accepted=int(st4[4]),
+                        step_ms=round(step / 1e3, 3), verify5_ms=round(verify / 1e3, 3),
+                        verify5_over_step=round(verify / step, 3), draft_ms_per_token=round(dstep / 1e3, 3))
+        log(f"cfg5 {tag}: {res[tag]}")
+        m.close()
+    draft.close()
+    return res
+
+
 def roofline_only(hp):
     """The roofline kernel's launches alone, then one RMSNorm over 256 MiB
     (k_rmsnorm_reg: 16384 rows of 4096 values, each row held in registers
@@ -174,18 +341,38 @@ def prefill_only(hp, prompt_len: int = PROMPT):
                       "prefill_tok_s": round(prompt_len / ms * 1e3, 1)}), flush=True)
 
 
-def cpu_baseline(hp, steps: int = 3, keys: int = PROMPT):
-    """The CPU oracle decoding `steps` tokens of the same model shape at
-    `keys` cached positions (KV seeded with random q8-rounded values)."""
+def cpu_baseline(hp, steps: int = 4, keys: int = PROMPT):
+    """The CPU oracle (the restatement of ts5's CPU backend: per-row dequant,
+    fp64 dots, rows striped over threads) on the host cores: the cfg2 8B
+    decoding `steps` tokens at `keys` cached positions (KV seeded with random
+    q8-rounded values), and cfg1's matvec and cfg4's head with all threads
+    and with one."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle  # test infrastructure: the checker, timed only as the CPU baseline
 
-    threads = min(os.cpu_count() or 1, 16)
+    nproc = os.cpu_count() or 1
+    threads = min(nproc, 16)  # the GPU box's share of host cores
+    rng = np.random.default_rng(3)
+    W1 = synth.tensor(synth.Q4_K, 4096, 4096, SEED, "cfg1")
+    x1 = rng.standard_normal(4096).astype(np.float32)
+
+    def best_ms(fn, reps):
+        t = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            t.append((time.perf_counter() - t0) * 1e3)
+        return float(np.median(t))
+
+    cfg1_ms = best_ms(lambda: oracle.matmul(synth.Q4_K, W1, 4096, x1, threads=threads), 9)
+    cfg1_ms_1t = best_ms(lambda: oracle.matmul(synth.Q4_K, W1, 4096, x1, threads=1), 3)
     t0 = time.time()
     tensors = synth.model_tensors(hp, SEED)
     log(f"cpu baseline: host weights generated ({time.time() - t0:.1f} s)")
+    head = tensors["output.weight"][3]
+    cfg4_ms = best_ms(lambda: oracle.matmul(synth.Q6_K, head, 4096, x1, threads=threads), 3)
+    cfg4_ms_1t = best_ms(lambda: oracle.matmul(synth.Q6_K, head, 4096, x1, threads=1), 1)
     m = oracle.Model(hp, tensors, keys + steps + 1, 2, threads=threads)
-    rng = np.random.default_rng(3)
     for layer in range(hp["n_layer"]):
         for which in (0, 1):
             kv = m.kv(which, layer)
@@ -197,9 +384,12 @@ def cpu_baseline(hp, steps: int = 3, keys: int = PROMPT):
         lg = m.forward(tok, keys + 1 + i)
         tok = np.array([int(np.argmax(lg[0]))], np.int32)
     dt = time.time() - t0
-    return dict(value=round(steps / dt, 4), unit="tok/s", cores=threads, kind="port",
+    return dict(value=round(steps / dt, 4), unit="tok/s", cores=threads, kind="port", nproc=nproc,
                 sample=f"{steps} greedy decode steps of the cfg2 8B shape at {keys} seeded q8 keys, "
-                       f"oracle/cpu_forward.cpp (fp64 dots, rows over {threads} threads)")
+                       f"oracle/cpu_forward.cpp (per-row dequant, fp64 dots, rows over {threads} of {nproc} "
+                       f"host threads); cfg1 / cfg4 matvecs median of 9 / 3 runs",
+                cfg1_matvec_ms=round(cfg1_ms, 2), cfg1_matvec_ms_1thread=round(cfg1_ms_1t, 2),
+                cfg4_head_ms=round(cfg4_ms, 1), cfg4_head_ms_1thread=round(cfg4_ms_1t, 1))
 
 
 def main():
@@ -213,6 +403,10 @@ def main():
                     help="only the roofline kernel's launches and a 256 MiB device copy (for rocprofv3 --pmc)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prompt's prefill, timed on the device (for rocprofv3 runs)")
+    ap.add_argument("--no-configs", action="store_true", help="skip the cfg1/cfg3/cfg4/cfg5 measurements")
+    ap.add_argument("--no-spec", action="store_true", help="skip cfg5 (draft model + two targets, ~1 min)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the cfg2 decode and its JSON line (for rocprofv3 runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this backend runs ts5's token loop on one GPU (batch 1); "
@@ -228,8 +422,23 @@ def main():
     ctx = ts5hip.Context(0)
     log(f"device {ctx.arch}, {ctx.n_cu} CUs, {ctx.hbm / 2**30:.0f} GiB")
     ms, ids, extra = decode_bench(ctx, hp, args.steps, args.warmup, args.prompt)
-    roof = glu_roofline(ctx, hp)
-    log(f"roofline: {roof}")
+    configs = {}
+    if args.decode_only:
+        roof = None
+        args.no_cpu = True
+    else:
+        roof = glu_roofline(ctx, hp)
+        log(f"roofline: {roof}")
+        if not args.no_configs:
+            configs["cfg1_q4k_matvec_4096"] = cfg1_matvec(ctx)
+            log(f"cfg1: {configs['cfg1_q4k_matvec_4096']}")
+            configs["cfg3_attention"] = cfg3_attention(ctx)
+            log(f"cfg3: {configs['cfg3_attention']}")
+            configs["cfg4_head_sampling"] = cfg4_head_sampling(ctx)
+            log(f"cfg4: {configs['cfg4_head_sampling']}")
+            free_busy(ctx)
+            if not args.no_spec:
+                configs["cfg5_speculation"] = cfg5_speculation(ctx)
     ctx.close()
     cpu = None if args.no_cpu else cpu_baseline(hp)
     if cpu:
@@ -242,12 +451,13 @@ def main():
         "metric": "decode tok/s (8B Q4_K, bs1, 4k ctx, 1 GPU)",
         "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms / args.steps, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "q4_k/q6_k weights, int8 x int16 dot, fp32 accum",
+        "vs_baseline": None, "dtype": "q4_k/q6_k weights, int8 x 23-bit activation dot (exact int32), fp32 accum",
         "data": "synthetic (random-init weights generated in HBM, uniform prompt ids)",
         "config": {"workload": "cfg2: Llama-style 8B decode, 4096-token prompt, greedy, q8 KV",
                    "global_batch": 1, "seq_len": args.prompt, "parallelism": "none (1 GPU)",
                    "decode_hbm_gbs": round(token_bytes * value / 1e9, 1),
-                   "decode_roofline_frac": round(token_bytes * value / 1e9 / HBM_PEAK_GBS, 4), **extra},
+                   "decode_roofline_frac": round(token_bytes * value / 1e9 / HBM_PEAK_GBS, 4), **extra,
+                   **configs},
         "roofline": roof, "cpu_baseline": cpu,
     }), flush=True)
 

@@ -100,10 +100,7 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float *__restrict__ qkv, i
 // file builds with -amdgpu-kernarg-preload-count=16); the rest of AttnArgs
 // (query, RoPE, norms, partials, output) follows in `tail`. flags: 1
 // kv_per_batch, 2 append, 4 rope.
-#ifndef TS5_ATTN_NT
-#define TS5_ATTN_NT 512
-#endif
-constexpr int ATTN_NT = TS5_ATTN_NT;  // threads per work item: 8 waves, two per SIMD
+constexpr int ATTN_NT = 512;  // threads per work item: 8 waves, two per SIMD
 
 template <int HD, int G, bool F16>
 __global__ __launch_bounds__(ATTN_NT) void k_attn(const int8_t *k8, const uint16_t *ks, const int8_t *v8,

@@ -63,30 +63,6 @@ __device__ inline void rope_inplace(float *v, int n_rot, int neox, const float2 
 constexpr int ATTN_MAX_SPLIT = 64;
 constexpr int ATTN_TILE = 64;
 
-// K bytes per lane of a key's score: NQ = HD / (NT / 64) lanes' worth.
-template <int NQ>
-struct KRow {
-    uint32_t w[NQ / 4];
-};
-template <int NQ>
-__device__ inline KRow<NQ> load_krow(const int8_t *p) {
-    KRow<NQ> r;
-    if constexpr (NQ % 16 == 0) {
-#pragma unroll
-        for (int c = 0; c < NQ / 16; c++) {
-            const uint4 v = *(const uint4 *)(p + 16 * c);
-            r.w[4 * c] = v.x, r.w[4 * c + 1] = v.y, r.w[4 * c + 2] = v.z, r.w[4 * c + 3] = v.w;
-        }
-    } else {
-#pragma unroll
-        for (int c = 0; c < NQ / 8; c++) {
-            const uint2 v = *(const uint2 *)(p + 8 * c);
-            r.w[2 * c] = v.x, r.w[2 * c + 1] = v.y;
-        }
-    }
-    return r;
-}
-
 // Where work item (split, kvh, b) of n_split reads keys: [p0, p1) of the nk
 // keys [0, nk) of query b (at position pq = nk - 1), in 64-key tiles.
 struct AttnSpan {
@@ -204,290 +180,401 @@ __device__ inline void attn_prepare(const AttnArgs &a, int kvh, const AttnSpan &
 }
 
 // ---------------------------------------------------------------------------
-// One work item (split, KV head kvh, query b) of n_split over its whole key
-// slice, in passes of up to ATTN_KT keys: every K and V byte of a pass is
-// requested before the query's preparation and held in registers, so the
-// slice costs one memory round trip rather than one per 64-key tile.
-//   scores   4 lanes per key (HD/4 dims each), 64 keys per sweep of the
-//            workgroup, q from LDS, the 4 partial sums added by DPP;
-//   softmax  a wave per head over the pass, online across passes;
-//   p * v    8 dims per lane straight from the V rows in registers, G heads
-//            per V value; the lanes and waves that took other keys of the
-//            same dims are added at the end (shuffles, then LDS).
-// Then the partial record and the merge of attn_item.
+// One work item (split, KV head kvh, query b) of n_split over its key slice
+// [p0, p1). Each wave walks its own keys with its own online softmax, with
+// no workgroup barrier until the end:
+//   lanes    LPK lanes a key, DPL dims a lane (16 with HD 128 and G <= 4,
+//            else 8); KPS = 64 / LPK keys side by side a sweep, S sweeps a
+//            chunk of 16 keys; the G query heads' DPL dims stay in registers;
+//   chunks   a wave's chunk is 32 consecutive keys of the workgroup's chunk
+//            of 32 * (NT / 64); the next chunk's K and V are requested before
+//            the current one is used (buffer loads bounded by the slice: past
+//            p1 they return zeros and touch no memory);
+//   scores   DPL-dim partial dots added over the key's LPK lanes by DPP;
+//   softmax  per head, the chunk's maximum over the wave, then
+//            p = e^(s - m) and the running (m, l);
+//   p * v    each lane adds p * v over its keys for its DPL dims; the keys of
+//            other lanes are added once at the end.
+// The waves' (m, l, o) then combine in LDS into the work item's partial, and
+// the last of the n_split work items of a (query, KV head) to finish merges
+// the partials (attn_merge.comp:18-47), reading them device-coherent.
 // ---------------------------------------------------------------------------
-constexpr int ATTN_KT = 256;
+template <int HD, int G>
+struct SliceShape {
+    static constexpr int DPL = (HD == 128 && G <= 4) ? 16 : 8;  // dims a lane
+    static constexpr int LPK = HD / DPL;                         // lanes a key: 8 or 16
+    static constexpr int KPS = 64 / LPK;                         // keys a sweep: 8 or 4
+    static constexpr int S = 16 / KPS;                           // sweeps a chunk (16 keys)
+    static_assert(LPK == 8 || LPK == 16, "attention lane shape");
+};
 
 template <int HD, int G, int NT = 256>
 struct SliceLds {
     float q_s[G][HD];
-    __align__(16) float p_s[ATTN_KT][G];  // scores, then probabilities
-    float alpha_s[G], m_s[G], l_s[G], red[G];
+    float m_s[G], l_s[G], red[G];
     float kv_s[2][HD];                    // the new token's K and V before rounding
     __align__(16) int8_t new8[2][HD];     // ... and after, as int8
     uint16_t new_sc[2][HD / 32];          // ... with their f16 scales
     __align__(16) uint16_t new16[2][HD];  // ... or as f16 (an f16 cache)
-    __align__(16) float o_s[NT / 64][G * HD];  // each wave's p * v sums
+    __align__(16) float o_w[NT / 64][G][HD];  // each wave's o
+    float m_w[NT / 64][G], l_w[NT / 64][G];   // ... and (m, l)
     __align__(16) float wts[G][ATTN_MAX_SPLIT];  // the merge's weight per (head, split), 0 past n_split
     int last;
 };
 
-template <int HD, int G, int NT>
-struct SliceShape {
-    // Scores: LPK lanes a key, KS keys a sweep of the workgroup, NPASS sweeps a
-    // pass. p * v: DPL dims a lane, KPW keys a wave, KPS keys a step, NVS steps.
-    static constexpr int NW = NT / 64, LPK = 4, NQ = HD / LPK, KS = NT / LPK, NPASS = ATTN_KT / KS;
-    static constexpr int DPL = 8, LPV = HD / DPL, KPW = 64 / LPV, KPS = NW * KPW, NVS = ATTN_KT / KPS;
-    static_assert(NQ % 8 == 0 && LPV <= 64 && 64 % LPV == 0 && 64 % KPS == 0 && ATTN_KT % KS == 0,
-                  "attention slice shape");
-};
-
 // The cache's values: q8 (int8 with an f16 scale per 32) or, with F16, f16
-// (2 bytes a value, no scales; ks / vs unused). A lane's 8 V dims are one
-// uint2 of int8 or one uint4 of f16.
-template <bool F16>
-using VRow = typename std::conditional<F16, uint4, uint2>::type;
+// (2 bytes a value, no scales; ks / vs unused).
 template <bool F16>
 __device__ inline float kv_value(const uint32_t *w, int e) {
     if constexpr (F16) return h2f((w[e >> 1] >> (16 * (e & 1))) & 0xffff);
     else return (float)(int8_t)((w[e >> 2] >> (8 * (e & 3))) & 0xff);
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// A buffer resource over [base, base + bytes): loads past the end return 0
+// without a memory access (gfx9 raw buffers).
+__device__ inline __amdgpu_buffer_rsrc_t slice_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+template <int BYTES>
+struct Raw {
+    uint32_t w[BYTES / 4];
+};
+template <int BYTES>
+__device__ inline Raw<BYTES> buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    Raw<BYTES> v;
+    if constexpr (BYTES == 32) {
+        const auto a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+        const auto b = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) v.w[i] = a[i], v.w[4 + i] = b[i];
+    } else if constexpr (BYTES == 16) {
+        const auto a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) v.w[i] = a[i];
+    } else {
+        static_assert(BYTES == 8, "buffer load size");
+        const auto a = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+        v.w[0] = a[0], v.w[1] = a[1];
+    }
+    return v;
+}
+
 template <int HD, int G, int NT, bool F16 = false>
 __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, int n_split,
                                   SliceLds<HD, G, NT> &S) {
-    using SH = SliceShape<HD, G, NT>;
-    constexpr int NW = SH::NW, NQ = SH::NQ, KS = SH::KS, NPASS = SH::NPASS, LPV = SH::LPV, KPW = SH::KPW,
-                  KPS = SH::KPS, NVS = SH::NVS, SMX = ATTN_KT / 64;
-    constexpr int VB = F16 ? 2 : 1;  // bytes per cached value
+    using SH = SliceShape<HD, G>;
+    constexpr int NW = NT / 64, DPL = SH::DPL, LPK = SH::LPK, KPS = SH::KPS, NS = SH::S;
+    constexpr int VB = F16 ? 2 : 1;         // bytes per cached value
+    constexpr int RB = DPL * VB;            // bytes of a key a lane reads
+    constexpr int WCH = NS * KPS, GCH = NW * WCH;  // keys a wave chunk, a workgroup chunk
+    constexpr float LOG2E = 1.4426950408889634f;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int kk = tid >> 2, qq = tid & 3;              // scores: key kk of a sweep, quarter qq of the dims
-    const int vk = lane / LPV, vc = lane % LPV;         // p * v: key vk of a wave's step, dims 8 vc ..
+    const int ks_ = lane / LPK, dq = lane % LPK;  // key slot of a sweep, dim quarter
+    const int d0 = DPL * dq;
     const AttnSpan sp = attn_span<16>(a, split, kvh, b, n_split);
-    const int8_t *kb = a.kv.k + sp.head_base * HD * VB, *vb = a.kv.v + sp.head_base * HD * VB;
-    const uint16_t *ksb = F16 ? nullptr : a.kv.ks + sp.head_base * (HD / 32);
-    const uint16_t *vsb = F16 ? nullptr : a.kv.vs + sp.head_base * (HD / 32);
-    float o[G][8];
+    const int nkeys = max(sp.p1 - sp.p0, 0);
+    // The slice's K and V (and scales) as bounded buffers from key p0.
+    const int8_t *kb = a.kv.k + (sp.head_base + sp.p0) * HD * VB, *vb = a.kv.v + (sp.head_base + sp.p0) * HD * VB;
+    const __amdgpu_buffer_rsrc_t rk = slice_rsrc(kb, (uint32_t)nkeys * HD * VB);
+    const __amdgpu_buffer_rsrc_t rv = slice_rsrc(vb, (uint32_t)nkeys * HD * VB);
+    __amdgpu_buffer_rsrc_t rks = rk, rvs = rv;
+    if constexpr (!F16) {
+        rks = slice_rsrc(a.kv.ks + (sp.head_base + sp.p0) * (HD / 32), (uint32_t)nkeys * (HD / 32) * 2);
+        rvs = slice_rsrc(a.kv.vs + (sp.head_base + sp.p0) * (HD / 32), (uint32_t)nkeys * (HD / 32) * 2);
+    }
+    struct Chunk {
+        Raw<RB> k[NS], v[NS];
+        uint32_t ks[NS], vs[NS];
+    };
+    // Chunk c of the slice, this wave's 16 keys: key (relative to p0)
+    // c * GCH + wave * WCH + s * KPS + ks_.
+    auto request = [&](Chunk &ch, int c) {
 #pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) o[g][e] = 0.f;
-    bool prepared = false;
-    for (int t0 = sp.p0; t0 < sp.p1 || !prepared; t0 += ATTN_KT) {
-        const int nt = max(0, min(ATTN_KT, sp.p1 - t0));
-        const int kmax = max(sp.p1 - 1, 0);  // loads past the slice read its last key (zero weight)
-        KRow<NQ * VB> kr[NPASS];
-        uint16_t ksr[NPASS];
-#pragma unroll
-        for (int j = 0; j < NPASS; j++) {
-            const int key = min(t0 + KS * j + kk, kmax);
-            kr[j] = load_krow<NQ * VB>(kb + ((int64_t)key * HD + qq * NQ) * VB);
-            if constexpr (!F16) ksr[j] = ksb[(int64_t)key * (HD / 32) + (qq * NQ) / 32];
+        for (int s2 = 0; s2 < NS; s2++) {
+            const uint32_t key = (uint32_t)(c * GCH + wave * WCH + s2 * KPS + ks_);
+            const uint32_t off = (key * HD + d0) * VB;
+            ch.k[s2] = buf_load<RB>(rk, off);
+            ch.v[s2] = buf_load<RB>(rv, off);
+            if constexpr (!F16) {
+                const uint32_t so = (key * (HD / 32) + d0 / 32) * 2;
+                ch.ks[s2] = __builtin_amdgcn_raw_buffer_load_b16(rks, so, 0, 0);
+                ch.vs[s2] = __builtin_amdgcn_raw_buffer_load_b16(rvs, so, 0, 0);
+            }
         }
-        VRow<F16> vr[NVS];
-        uint16_t vsr[NVS];
+    };
+    Chunk A, B;
+    request(A, 0);
+    request(B, 1);
+    {
+        const float *row = a.q + (int64_t)b * a.q_stride;
+        attn_prepare<HD, G, NT, F16>(a, kvh, sp, S, [&](int64_t e) { return row[e]; });
+    }
+    float q[G][DPL], o[G][DPL], m[G], l[G];
 #pragma unroll
-        for (int s2 = 0; s2 < NVS; s2++) {
-            const int key = min(t0 + s2 * KPS + wave * KPW + vk, kmax);
-            vr[s2] = *(const VRow<F16> *)(vb + ((int64_t)key * HD + 8 * vc) * VB);
-            if constexpr (!F16) vsr[s2] = vsb[(int64_t)key * (HD / 32) + (8 * vc) / 32];
+    for (int g = 0; g < G; g++) {
+#pragma unroll
+        for (int e = 0; e < DPL; e += 4) {
+            const float4 v = *(const float4 *)&S.q_s[g][d0 + e];
+            q[g][e] = v.x, q[g][e + 1] = v.y, q[g][e + 2] = v.z, q[g][e + 3] = v.w;
         }
-        if (!prepared) {
-            const float *row = a.q + (int64_t)b * a.q_stride;
-            attn_prepare<HD, G, NT, F16>(a, kvh, sp, S, [&](int64_t e) { return row[e]; });
-            prepared = true;
-            if (nt == 0) break;
-        }
-        // Scores of the pass.
 #pragma unroll
-        for (int j = 0; j < NPASS; j++) {
-            if (KS * j >= nt) break;
-            const int idx = KS * j + kk, key = t0 + idx;
-            float ks = F16 ? 1.f : h2f(ksr[j]);
-            if (sp.has_new && key == sp.pq) {
-                if constexpr (F16) {
+        for (int e = 0; e < DPL; e++) o[g][e] = 0.f;
+        m[g] = -INFINITY, l[g] = 0.f;
+    }
+    const int pq_rel = sp.pq - sp.p0;  // the new key (when sp.has_new), relative to p0
+    // One chunk: scores, softmax update, p * v.
+    auto consume = [&](Chunk &ch, int c) {
+        // Whether the token's own key is among this wave's 16 (the same for
+        // the whole wave).
+        const bool new_here = sp.has_new && (unsigned)(pq_rel - (c * GCH + wave * WCH)) < (unsigned)WCH;
+        float sc[NS][G];
 #pragma unroll
-                    for (int c = 0; c < NQ / 2; c++) kr[j].w[c] = *(const uint32_t *)(S.new16[0] + qq * NQ + 2 * c);
-                } else {
+        for (int s2 = 0; s2 < NS; s2++) {
+            const int key = c * GCH + wave * WCH + s2 * KPS + ks_;
+            uint32_t kw[RB / 4];
 #pragma unroll
-                    for (int c = 0; c < NQ / 4; c++) kr[j].w[c] = *(const uint32_t *)(S.new8[0] + qq * NQ + 4 * c);
-                    ks = h2f(S.new_sc[0][(qq * NQ) / 32]);
-                }
+            for (int i = 0; i < RB / 4; i++) kw[i] = ch.k[s2].w[i];
+            float kscale = F16 ? 1.f : h2f(ch.ks[s2]);
+            if (new_here && key == pq_rel) {  // the token's own key, from LDS
+#pragma unroll
+                for (int i = 0; i < RB / 4; i++)
+                    kw[i] = F16 ? *(const uint32_t *)(S.new16[0] + d0 + 2 * i) : *(const uint32_t *)(S.new8[0] + d0 + 4 * i);
+                if constexpr (!F16) kscale = h2f(S.new_sc[0][d0 / 32]);
             }
             float acc[G];
 #pragma unroll
             for (int g = 0; g < G; g++) acc[g] = 0.f;
 #pragma unroll
-            for (int e4 = 0; e4 < NQ / 4; e4++) {
-                float kf[4];
+            for (int e = 0; e < DPL; e++) {
+                const float kf = kv_value<F16>(kw, e);
 #pragma unroll
-                for (int i = 0; i < 4; i++) kf[i] = kv_value<F16>(kr[j].w, 4 * e4 + i) * ks;
-#pragma unroll
-                for (int g = 0; g < G; g++) {
-                    const float4 qv = *(const float4 *)&S.q_s[g][qq * NQ + 4 * e4];
-                    acc[g] += qv.x * kf[0] + qv.y * kf[1] + qv.z * kf[2] + qv.w * kf[3];
-                }
+                for (int g = 0; g < G; g++) acc[g] += q[g][e] * kf;
             }
 #pragma unroll
             for (int g = 0; g < G; g++) {
-                acc[g] = dpp_add<0xB1, 0xF, true>(acc[g]);  // quad_perm [1,0,3,2]
-                acc[g] = dpp_add<0x4E, 0xF, true>(acc[g]);  // quad_perm [2,3,0,1]
-            }
-            if (qq == 0) {
-#pragma unroll
-                for (int g = 0; g < G; g++) S.p_s[idx][g] = idx < nt ? acc[g] * a.scale : -INFINITY;
-            }
-        }
-        __syncthreads();
-        // Online softmax per head over the pass.
-        for (int g = wave; g < G; g += NT / 64) {
-            float v[SMX];
-            float mt = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < SMX; i++) {
-                v[i] = 64 * i + lane < nt ? S.p_s[64 * i + lane][g] : -INFINITY;
-                mt = fmaxf(mt, v[i]);
-            }
-            mt = wave_max_dpp(mt);
-            const float mo = S.m_s[g], mn = fmaxf(mo, mt);
-            float ls = 0.f;
-#pragma unroll
-            for (int i = 0; i < SMX; i++) {
-                const float pe = v[i] == -INFINITY ? 0.f : expf(v[i] - mn);
-                if (64 * i < nt) S.p_s[64 * i + lane][g] = pe;
-                ls += pe;
-            }
-            ls = wave_sum_dpp(ls);
-            if (lane == 0) {
-                const float al = mo == -INFINITY ? 0.f : expf(mo - mn);
-                S.alpha_s[g] = al;
-                S.m_s[g] = mn;
-                S.l_s[g] = S.l_s[g] * al + ls;
+                // Each lane's dims lie in one 32-value block of the key: its
+                // own scale before the key's lanes are added.
+                float v = acc[g] * kscale;
+                v = dpp_add<0xB1, 0xF, true>(v);   // quad_perm [1,0,3,2]
+                v = dpp_add<0x4E, 0xF, true>(v);   // quad_perm [2,3,0,1]
+                v = dpp_add<0x141, 0xF, true>(v);  // row_half_mirror: the 8 lanes
+                if constexpr (LPK == 16) v = dpp_add<0x140, 0xF, true>(v);  // row_mirror: 16
+                sc[s2][g] = key < nkeys ? v * a.scale : -INFINITY;
             }
         }
-        __syncthreads();
-        // o = o * alpha + sum over the pass's keys of p * v.
+        // The chunk's largest score per head over the wave's key slots.
+        float alpha[G], p[NS][G];
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            const float al = S.alpha_s[g];
+            float cm = sc[0][g];
 #pragma unroll
-            for (int e = 0; e < 8; e++) o[g][e] *= al;
+            for (int s2 = 1; s2 < NS; s2++) cm = fmaxf(cm, sc[s2][g]);
+            if constexpr (LPK == 8) cm = dpp_max<0x128, 0xF, true>(cm);  // row_ror:8
+            {
+                const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(cm), __float_as_uint(cm), false, false);
+                cm = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+                const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(cm), __float_as_uint(cm), false, false);
+                cm = fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+            }
+            const float mn = fmaxf(m[g], cm);
+            alpha[g] = m[g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m[g] - mn) * LOG2E);
+            float ls = 0.f;
+#pragma unroll
+            for (int s2 = 0; s2 < NS; s2++) {
+                p[s2][g] = sc[s2][g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((sc[s2][g] - mn) * LOG2E);
+                ls += p[s2][g];
+            }
+            if constexpr (LPK == 8) ls = dpp_add<0x128, 0xF, true>(ls);
+            ls = add_xor32(add_xor16(ls));
+            m[g] = mn;
+            l[g] = l[g] * alpha[g] + ls;
+        }
+        bool same = true;  // no head's maximum moved: o stays as it is
+#pragma unroll
+        for (int g = 0; g < G; g++) same = same && alpha[g] == 1.f;
+        if (!same) {
+#pragma unroll
+            for (int g = 0; g < G; g++)
+#pragma unroll
+                for (int e = 0; e < DPL; e++) o[g][e] *= alpha[g];
         }
 #pragma unroll
-        for (int s2 = 0; s2 < NVS; s2++) {
-            if (s2 * KPS >= nt) break;
-            const int idx = s2 * KPS + wave * KPW + vk, key = t0 + idx;
-            VRow<F16> v8 = vr[s2];
-            float vs = F16 ? 1.f : h2f(vsr[s2]);
-            if (sp.has_new && key == sp.pq) {
-                if constexpr (F16) {
-                    v8 = *(const VRow<F16> *)(S.new16[1] + 8 * vc);
-                } else {
-                    v8 = *(const VRow<F16> *)(S.new8[1] + 8 * vc);
-                    vs = h2f(S.new_sc[1][(8 * vc) / 32]);
-                }
+        for (int s2 = 0; s2 < NS; s2++) {
+            const int key = c * GCH + wave * WCH + s2 * KPS + ks_;
+            uint32_t vw[RB / 4];
+#pragma unroll
+            for (int i = 0; i < RB / 4; i++) vw[i] = ch.v[s2].w[i];
+            float vscale = F16 ? 1.f : h2f(ch.vs[s2]);
+            if (new_here && key == pq_rel) {
+#pragma unroll
+                for (int i = 0; i < RB / 4; i++)
+                    vw[i] = F16 ? *(const uint32_t *)(S.new16[1] + d0 + 2 * i) : *(const uint32_t *)(S.new8[1] + d0 + 4 * i);
+                if constexpr (!F16) vscale = h2f(S.new_sc[1][d0 / 32]);
             }
             float w[G];
 #pragma unroll
-            for (int g = 0; g < G; g++) w[g] = S.p_s[idx][g] * vs;  // idx < 64 * ceil(nt / 64): a written row
-            const uint32_t *vw = (const uint32_t *)&v8;
+            for (int g = 0; g < G; g++) w[g] = p[s2][g] * vscale;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
+            for (int e = 0; e < DPL; e++) {
                 const float vf = kv_value<F16>(vw, e);
 #pragma unroll
                 for (int g = 0; g < G; g++) o[g][e] += w[g] * vf;
             }
         }
-        __syncthreads();  // p_s is rewritten by the next pass
+    };
+    // Two register buffers in turn, both requested before the query is
+    // prepared; each is refilled with the chunk two on as soon as it is
+    // consumed (past the slice: no memory access).
+    const int nch = (nkeys + GCH - 1) / GCH;
+    for (int c = 0; c < nch; c += 2) {
+        consume(A, c);
+        if (c + 1 >= nch) break;
+        request(A, c + 2);
+        consume(B, c + 1);
+        request(B, c + 3);
     }
-    // The wave's KPW key groups of the same dims (lanes i ^ 8, ^ 16, ^ 32),
-    // then the 4 waves.
+    // The key slots of a wave hold the same dims: add them over lanes i ^ 32,
+    // i ^ 16 (and i ^ 8 within a 16-lane row when LPK is 8) by a butterfly
+    // that pairs different values in each swap: v_permlane32_swap of (a, b)
+    // leaves a's pair sums in lanes 0-31 and b's in lanes 32-63, and
+    // v_permlane16_swap does the same for rows 0 / 1 and 2 / 3. The NV values
+    // end as NV / 4 registers, row r of register i holding value
+    // i + (NV / 4) r summed over every slot.
+    constexpr int NV = G * DPL, N2 = NV / 2, N4 = NV / 4;
+    static_assert(NV % 4 == 0, "o butterfly");
+    float r2[N4];
+    {
+        float r1[N2];
 #pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            float v = o[g][e];
-            if constexpr (LPV <= 8) v = dpp_add<0x128, 0xF, true>(v);  // row_ror:8 within 16-lane rows
-            if constexpr (LPV <= 16) v = add_xor16(v);
-            o[g][e] = add_xor32(v);
+        for (int i = 0; i < N2; i++) {
+            const float x = o[i / DPL][i % DPL], y = o[(i + N2) / DPL][(i + N2) % DPL];
+            const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+            r1[i] = __uint_as_float(t[0]) + __uint_as_float(t[1]);
         }
-    if (vk == 0) {
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            *(float4 *)&S.o_s[wave][g * HD + 8 * vc] = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
-            *(float4 *)&S.o_s[wave][g * HD + 8 * vc + 4] = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
+        for (int i = 0; i < N4; i++) {
+            const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(r1[i]), __float_as_uint(r1[i + N4]), false, false);
+            float v = __uint_as_float(t[0]) + __uint_as_float(t[1]);
+            if constexpr (LPK == 8) v = dpp_add<0x128, 0xF, true>(v);  // row_ror:8
+            r2[i] = v;
         }
+    }
+    if ((lane & 15) < LPK) {  // row r, dims of lane % LPK
+        const int row = lane >> 4;
+#pragma unroll
+        for (int i = 0; i < N4; i++) {
+            const int j = i + N4 * row, g = j / DPL, e = j % DPL;
+            S.o_w[wave][g][d0 + e] = r2[i];
+        }
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++) S.m_w[wave][g] = m[g], S.l_w[wave][g] = l[g];
     }
     __syncthreads();
 
-    constexpr int64_t rec = HD + 2, grp = attn_group_floats(G, HD);
-    float *pb = a.part + (((int64_t)b * n_split + split) * a.HKV + kvh) * grp;
-    for (int j = tid; j < G * HD; j += NT) {
+    // The work item's (m, l, o) from its waves'.
+    constexpr int NOUT = G * HD;
+    constexpr int64_t grp = attn_group_floats(G, HD);
+    auto item_value = [&](int j, float &mo, float &lo_) -> float {
         const int g = j / HD, d = j % HD;
-        float v = 0.f;
+        float M = S.m_w[0][g];
 #pragma unroll
-        for (int w = 0; w < NW; w++) v += S.o_s[w][j];
-        st_dev(pb + g * rec + d, v);
+        for (int w = 1; w < NW; w++) M = fmaxf(M, S.m_w[w][g]);
+        float O = 0.f, L = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float wt = S.m_w[w][g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((S.m_w[w][g] - M) * LOG2E);
+            O += wt * S.o_w[w][g][d];
+            L += wt * S.l_w[w][g];
+        }
+        mo = M, lo_ = L;
+        return O;
+    };
+    if (n_split == 1) {  // the only work item: the output directly
+        for (int j = tid; j < NOUT; j += NT) {
+            float M, L;
+            const float O = item_value(j, M, L);
+            a.out[(int64_t)b * a.H * HD + (int64_t)kvh * G * HD + j] = L > 0.f ? O / L : 0.f;
+        }
+        return;
     }
-    if (tid < G) {
-        st_dev(pb + tid * rec + HD, S.m_s[tid]);
-        st_dev(pb + tid * rec + HD + 1, S.l_s[tid]);
+    // Partial layout per (query, split, KV head): [G][HD] values, then (m, l)
+    // per head, grp floats in all (whole 128-byte lines).
+    float *pb = a.part + (((int64_t)b * n_split + split) * a.HKV + kvh) * grp;
+    for (int j = tid; j < NOUT; j += NT) {
+        float M, L;
+        st_dev(pb + j, item_value(j, M, L));
+        if (j % HD == 0) {
+            st_dev(pb + NOUT + 2 * (j / HD), M);
+            st_dev(pb + NOUT + 2 * (j / HD) + 1, L);
+        }
     }
     wait_stores();
     __syncthreads();
     if (tid == 0) S.last = atomicAdd(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 1) == n_split - 1;
     __syncthreads();
     if (!S.last) return;
-    // The merge: this thread's outputs of every split (up to 32 at a time)
-    // and every split's (m, l) are requested together; a wave per head turns
-    // the (m, l) into weights, a lane per split.
+    // The merge: the n_split partials, read device-coherent (buffer loads with
+    // sc1), two values a thread, up to 32 splits' worth requested together
+    // with the (m, l) that weigh them; a wave per head turns the (m, l) into
+    // weights, a lane per split.
     const float *p_all = a.part + ((int64_t)b * n_split * a.HKV + kvh) * grp;
-    const int64_t sstride = (int64_t)a.HKV * grp;
-    constexpr int OPT = (G * HD + NT - 1) / NT, MC = 32;
-    float acc[OPT];
+    const int64_t sstride = (int64_t)a.HKV * grp;  // floats between splits
+    const __amdgpu_buffer_rsrc_t rp = slice_rsrc(p_all, (uint32_t)((n_split - 1) * sstride + grp) * 4);
+    constexpr int MB = 32;  // splits a batch
+    constexpr int NQ2 = NOUT / 2, PER = (NQ2 + NT - 1) / NT;
+    u32x2 v[PER][MB];
+    auto fetch = [&](int s0) {
 #pragma unroll
-    for (int k = 0; k < OPT; k++) acc[k] = 0.f;
-    for (int s0 = 0; s0 < n_split; s0 += MC) {
-        const int nc = min(MC, n_split - s0);
-        float ov[OPT][MC];
+        for (int k = 0; k < PER; k++) {
+            const int j2 = min(tid + NT * k, NQ2 - 1);
 #pragma unroll
-        for (int k = 0; k < OPT; k++) {
-            const int j = min(tid + NT * k, G * HD - 1), g = j / HD, d = j % HD;
-#pragma unroll
-            for (int i = 0; i < MC; i++) ov[k][i] = ld_dev(p_all + (int64_t)(s0 + min(i, nc - 1)) * sstride + g * rec + d);
-        }
-        if (s0 == 0) {
-            for (int g = wave; g < G; g += NT / 64) {
-                const int sl = min(lane, n_split - 1);
-                const float m0 = ld_dev(p_all + (int64_t)sl * sstride + g * rec + HD);
-                const float l0 = ld_dev(p_all + (int64_t)sl * sstride + g * rec + HD + 1);
-                const float m = lane < n_split ? m0 : -INFINITY;
-                const float M = wave_max_dpp(m);
-                const float w = m == -INFINITY ? 0.f : expf(m - M);
-                const float L = wave_sum_dpp(w * (lane < n_split ? l0 : 0.f));
-                S.wts[g][lane] = w;  // lanes past n_split: 0
-                if (lane == 0) S.red[g] = L;
+            for (int i = 0; i < MB; i++) {
+                const int sl = min(s0 + i, n_split - 1);
+                v[k][i] = __builtin_amdgcn_raw_buffer_load_b64(rp, (uint32_t)((sl * sstride + 2 * j2) * 4), 0, 16);
             }
-            __syncthreads();
         }
+    };
+    fetch(0);
+    for (int g = wave; g < G; g += NW) {
+        const int sl = min(lane, n_split - 1);
+        const auto ml = __builtin_amdgcn_raw_buffer_load_b64(rp, (uint32_t)((sl * sstride + NOUT + 2 * g) * 4), 0, 16);
+        const float m0 = __uint_as_float(ml[0]), l0 = __uint_as_float(ml[1]);
+        const float mm = lane < n_split ? m0 : -INFINITY;
+        const float M = wave_max_dpp(mm);
+        const float w = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((mm - M) * LOG2E);
+        const float L = wave_sum_dpp(w * (lane < n_split ? l0 : 0.f));
+        S.wts[g][lane] = w;  // lanes past n_split: 0
+        if (lane == 0) S.red[g] = L;
+    }
+    __syncthreads();
+    float2 acc[PER];
 #pragma unroll
-        for (int k = 0; k < OPT; k++) {
-            const int j = min(tid + NT * k, G * HD - 1), g = j / HD;
-            float v = acc[k];
+    for (int k = 0; k < PER; k++) acc[k] = make_float2(0.f, 0.f);
+    for (int s0 = 0; s0 < n_split; s0 += MB) {
+        if (s0) fetch(s0);
 #pragma unroll
-            for (int i4 = 0; i4 < MC / 4; i4++) {  // weights past n_split are 0 (their o: a valid split's)
-                const float4 w = *(const float4 *)&S.wts[g][s0 + 4 * i4];
-                v += w.x * ov[k][4 * i4] + w.y * ov[k][4 * i4 + 1] + w.z * ov[k][4 * i4 + 2] + w.w * ov[k][4 * i4 + 3];
+        for (int k = 0; k < PER; k++) {
+            const int g = (2 * min(tid + NT * k, NQ2 - 1)) / HD;
+#pragma unroll
+            for (int i = 0; i < MB; i++) {
+                const float w = s0 + i < n_split ? S.wts[g][s0 + i] : 0.f;
+                acc[k].x += w * __uint_as_float(v[k][i][0]);
+                acc[k].y += w * __uint_as_float(v[k][i][1]);
             }
-            acc[k] = v;
         }
     }
 #pragma unroll
-    for (int k = 0; k < OPT; k++) {
-        const int j = tid + NT * k;
-        if (j < G * HD) {
-            const int g = j / HD, d = j % HD;
-            st_dev(a.out + (int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d, acc[k] / S.red[g]);
+    for (int k = 0; k < PER; k++) {
+        const int j2 = tid + NT * k;
+        if (j2 < NQ2) {
+            const float L = S.red[(2 * j2) / HD];
+            const float2 r = L > 0.f ? make_float2(acc[k].x / L, acc[k].y / L) : make_float2(0.f, 0.f);
+            *(float2 *)(a.out + (int64_t)b * a.H * HD + (int64_t)kvh * G * HD + 2 * j2) = r;
         }
     }
     if (tid == 0) st_dev(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 0);  // ready for the next use

@@ -517,6 +517,47 @@ def test_topk(ctx, n, k):
     assert np.array_equal(vals.download(np.float32), x[want])
 
 
+@pytest.mark.parametrize("case", ["all_equal", "int_ties", "signed_zeros", "minus_inf", "two_slices", "n_is_k",
+                                  "one"])
+def test_topk_edge_cases(ctx, case):
+    """The top k in rank order (larger value, then smaller id, as a stable
+    descending sort) where the selection is exact only by its tie handling:
+    a row of one value (more tied entries than the gather holds: the sorted
+    lists are merged), small integers (ties at the k-th), -0 and +0 across
+    the cut (equal values, ranked by id), -inf entries, a last slice of one
+    logit, n == k."""
+    rng = np.random.default_rng(sum(map(ord, case)))
+    n, k = 128256, 40
+    if case == "all_equal":
+        x = np.ones(n, np.float32)
+    elif case == "int_ties":
+        x = np.rint(rng.standard_normal(n) * 2).astype(np.float32)
+    elif case == "signed_zeros":
+        n, k = 5000, 64
+        x = -np.abs(rng.standard_normal(n)).astype(np.float32) - 1
+        x[rng.choice(n, 30, replace=False)] = 0.0
+        x[rng.choice(n, 30, replace=False)] = -0.0
+        x[rng.choice(n, 20, replace=False)] = 1.0
+    elif case == "minus_inf":
+        x = rng.standard_normal(n).astype(np.float32)
+        x[rng.choice(n, n - 50, replace=False)] = -np.inf
+    elif case == "two_slices":
+        n, k = 1025, 64
+        x = rng.standard_normal(n).astype(np.float32)
+        x[1024] = 9.0
+    elif case == "n_is_k":
+        n, k = 64, 64
+        x = rng.standard_normal(n).astype(np.float32)
+    else:
+        n, k = 1, 1
+        x = np.array([-3.0], np.float32)
+    vals, ids = ctx.alloc(k * 4), ctx.alloc(k * 4)
+    ctx.topk(ctx.to_device(x), n, k, vals, ids)
+    want = np.argsort(-x, kind="stable")[:k]
+    assert list(ids.download(np.int32)) == list(want)
+    assert np.array_equal(vals.download(np.float32), x[want])
+
+
 def test_sampling_cfg4_matches_reference_draws(ctx):
     """cfg4's sampling step: GPU top-40 then the host draw (T 0.7, p 0.9) gives
     the reference engine's ids on the golden logit table."""

@@ -242,6 +242,36 @@ def test_head_argmax(ctx, t, ne0, rows):
     assert rel_l2(lg, want) <= REL_L2
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 6, 8, 9, 16])
+@pytest.mark.parametrize("ne0,rows,mode", [(4096, 1000, "store"), (14336, 528, "add"), (512, 37, "glu")])
+def test_q4k_small_batch_matmul(ctx, M, ne0, rows, mode):
+    """The Q4_K matmul of 1-16 tokens (k_gemm_m up to 8, k_gemm_small past
+    it): every token's rows within 2e-6 relative L2 of the oracle, in each
+    mode (plain, accumulating into a residual, fused gate/up + SiLU), with
+    row counts that leave partial 16-row tiles."""
+    rng = np.random.default_rng(M * 100 + rows)
+    W = synth.tensor(synth.Q4_K, ne0, rows, 21, f"sb{ne0}", centered=True)
+    x = rng.standard_normal((M, ne0)).astype(np.float32)
+    w = ctx.weight(synth.Q4_K, ne0, rows, W)
+    if mode == "glu":
+        U = synth.tensor(synth.Q4_K, ne0, rows, 22, f"sbu{ne0}", centered=True)
+        y = ctx.alloc(M * rows * 4)
+        ctx.matmul_glu(synth.Q4_K, w, ctx.weight(synth.Q4_K, ne0, rows, U), ne0, rows, ctx.to_device(x), M, y)
+        want = oracle.swiglu(oracle.matmul(synth.Q4_K, W, ne0, x), oracle.matmul(synth.Q4_K, U, ne0, x))
+    elif mode == "add":
+        y0 = rng.standard_normal((M, rows)).astype(np.float32)
+        y = ctx.to_device(y0)
+        ctx.matmul(synth.Q4_K, w, ne0, rows, ctx.to_device(x), M, y, accumulate=True)
+        want = y0.astype(np.float64) + oracle.matmul(synth.Q4_K, W, ne0, x)
+    else:
+        y = ctx.alloc(M * rows * 4)
+        ctx.matmul(synth.Q4_K, w, ne0, rows, ctx.to_device(x), M, y)
+        want = oracle.matmul(synth.Q4_K, W, ne0, x)
+    got = y.download(np.float32, (M, rows))
+    for k in range(M):
+        assert rel_l2(got[k], want[k]) <= 2e-6, (k, rel_l2(got[k], want[k]))
+
+
 @pytest.mark.parametrize("t,ne0,rows", [(synth.Q4_K, 4096, 14336), (synth.Q8_0, 896, 4864), (synth.Q4_K, 512, 64)])
 def test_glu_vs_oracle(ctx, t, ne0, rows):
     Wg = synth.tensor(t, ne0, rows, 6, "gate")

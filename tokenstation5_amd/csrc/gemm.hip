@@ -28,6 +28,7 @@
 // (16 TN), KS). With KS > 1 the blocks of a row are split over KS workgroups
 // whose partial sums a second kernel adds in a fixed order.
 #include <algorithm>
+#include <cstdlib>
 
 #include "common.h"
 #include "kernels.h"
@@ -35,6 +36,7 @@
 namespace ts5hip {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+static int g_gemm_m_cu = 256;  // CUs, for k_gemm_m's row tiles a workgroup
 
 struct GemmArgs {
     uint32_t t;
@@ -489,6 +491,198 @@ __global__ __launch_bounds__(256) void k_gemm_small(GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K rows, up to 8 tokens (k_gemm_m): the roles of the MFMA operands
+// swapped so that each lane's result is one (token, row) pair. A = 16
+// activation rows, 4 tokens x 4 planes (hi, mid, lo, and a zero plane), of a
+// 32-value sub-block; B = the sub-block's quants of 16 weight rows. D lane l
+// then holds the 4 planes of token l/16 for weight row l%16, so
+// 65536 C_hi + 256 C_mid + C_lo and the block scaling
+//   y += d*sc * xs * (sum q X) - dmin*m * (sum x)       (quants.cpp:140-157)
+// happen in the lane, every lane holding a pair of the output. NT (1 or 2)
+// tiles of 4 tokens, RT tiles of 16 rows a workgroup; the 4 waves split each row's
+// blocks in quarters, and a wave keeps a block's activation fragments while it
+// walks the RT row tiles (weights one item ahead), so the activation is read
+// once per block and row group. The quarters meet in LDS in a fixed order.
+// ---------------------------------------------------------------------------
+template <int NT>
+struct MAFrag {
+    uint64_t p[NT][8];          // A: [token tile][sub-block] 8 bytes of plane (l%16)%4 of token (l%16)/4
+    float xs[NT][8], xsum[NT][8];  // epilogue token l/16 of each tile: scale, sum per sub-block
+};
+template <int NW>
+struct MWFrag {
+    uint4 hdr[NW];
+    uint64_t q[NW][4];  // B: the lane's k-group bytes of the 4 nibble groups of row l%16
+};
+
+template <int NT>
+__device__ inline void load_mafrag(const GemmArgs &a, int b, int l, MAFrag<NT> &f) {
+    const int kq = l >> 4, ar = l & 15, at = ar >> 2, ap = ar & 3, et = kq;
+    const int plane = ap == 0 ? 0 : ap == 1 ? MACT_MID : MACT_LO;
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) {
+        const int tok = min(4 * tt + at, a.M - 1);
+        const uint8_t *blk = a.act + (int64_t)tok * a.act_stride + (int64_t)b * MACT_BLOCK + plane + 64 * kq;
+#pragma unroll
+        for (int s2 = 0; s2 < 8; s2 += 2) {
+            const uint4 v = ld16(blk + 8 * s2);
+            f.p[tt][s2] = ap == 3 ? 0ull : ((uint64_t)v.y << 32) | v.x;
+            f.p[tt][s2 + 1] = ap == 3 ? 0ull : ((uint64_t)v.w << 32) | v.z;
+        }
+        const int etok = min(4 * tt + et, a.M - 1);
+        const uint8_t *eb = a.act + (int64_t)etok * a.act_stride + (int64_t)b * MACT_BLOCK;
+#pragma unroll
+        for (int c = 0; c < 8; c += 4) {
+            const float4 sc = *(const float4 *)(eb + MACT_SCALE + 4 * c);
+            const float4 su = *(const float4 *)(eb + MACT_SUM + 4 * c);
+            f.xs[tt][c] = sc.x, f.xs[tt][c + 1] = sc.y, f.xs[tt][c + 2] = sc.z, f.xs[tt][c + 3] = sc.w;
+            f.xsum[tt][c] = su.x, f.xsum[tt][c + 1] = su.y, f.xsum[tt][c + 2] = su.z, f.xsum[tt][c + 3] = su.w;
+        }
+    }
+}
+
+template <int NW>
+__device__ inline void load_mwfrag(const GemmArgs &a, int row, int kq, int b, MWFrag<NW> &w) {
+    const int64_t blk = (int64_t)min(row, a.nrows - 1) * a.nb + b;
+#pragma unroll
+    for (int m = 0; m < NW; m++) {
+        const uint8_t *p = (m ? a.w2 : a.w) + blk * Q4K_BYTES;
+        w.hdr[m] = ld16(p);
+#pragma unroll
+        for (int g = 0; g < 4; g++) w.q[m][g] = ld8(p + 16 + 32 * g + 8 * kq);
+    }
+}
+
+template <int MODE, int NT, int RT>
+__global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
+    constexpr int NW = MODE == G_GLU ? 2 : 1;
+    __shared__ float red[3][RT][NW][NT][64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, kq = l >> 4, rl = l & 15;
+    const int r0 = blockIdx.x * 16 * RT;
+    const int bpq = (a.nb + 3) / 4, b0 = wave * bpq, b1 = min(a.nb, b0 + bpq);
+    float acc[RT][NW][NT];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int m = 0; m < NW; m++)
+#pragma unroll
+            for (int tt = 0; tt < NT; tt++) acc[r][m][tt] = 0.f;
+    auto compute = [&](const MWFrag<NW> &w, const MAFrag<NT> &x, int r) {
+#pragma unroll
+        for (int m = 0; m < NW; m++) {
+            const bool rin = r0 + 16 * r + rl < a.nrows;
+            const float d = rin ? h2f(w.hdr[m].x & 0xffff) : 0.f, dmin = rin ? h2f(w.hdr[m].x >> 16) : 0.f;
+            float dsc[8], dm[8];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                int sc0, m0, sc1, m1;
+                kq_scale_min_pair(g, w.hdr[m].y, w.hdr[m].z, w.hdr[m].w, sc0, m0, sc1, m1);
+                dsc[2 * g] = d * (float)sc0, dm[2 * g] = dmin * (float)m0;
+                dsc[2 * g + 1] = d * (float)sc1, dm[2 * g + 1] = dmin * (float)m1;
+            }
+            // Every MFMA of the item first, the scaling after: the results are
+            // not waited for one at a time.
+            v4i c[8][NT];
+#pragma unroll
+            for (int s8 = 0; s8 < 8; s8++) {
+                const uint64_t qb = (s8 & 1) ? (w.q[m][s8 >> 1] >> 4) & 0x0F0F0F0F0F0F0F0Full
+                                             : w.q[m][s8 >> 1] & 0x0F0F0F0F0F0F0F0Full;
+#pragma unroll
+                for (int tt = 0; tt < NT; tt++)
+                    c[s8][tt] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x.p[tt][s8], (long)qb, v4i{0, 0, 0, 0}, 0, 0, 0);
+            }
+#pragma unroll
+            for (int s8 = 0; s8 < 8; s8++)
+#pragma unroll
+                for (int tt = 0; tt < NT; tt++) {
+                    // Exact in int32 for 4-bit quants: |.| <= 32 * 15 * (64 * 65536 + 128 * 257) < 2^31.
+                    const int v = c[s8][tt][0] * 65536 + c[s8][tt][1] * 256 + c[s8][tt][2];
+                    acc[r][m][tt] += dsc[s8] * x.xs[tt][s8] * (float)v - dm[s8] * x.xsum[tt][s8];
+                }
+        }
+    };
+    if (b0 < b1) {
+        MAFrag<NT> x;
+        MWFrag<NW> wA, wB;
+        load_mwfrag<NW>(a, r0 + rl, kq, b0, wA);
+        // Items (block b, row tile r) in order; the next one's weights are
+        // requested before the current one is computed (two buffers in turn).
+        int b = b0, r = 0;
+        auto next = [&](int &nb2, int &nr) {
+            nr = r + 1, nb2 = b;
+            if (nr == RT) nr = 0, nb2 = b + 1;
+            nb2 = min(nb2, b1 - 1);  // past the last item: a repeat, not used
+        };
+        for (;;) {
+            if (r == 0) load_mafrag<NT>(a, b, l, x);
+            int nb2, nr;
+            next(nb2, nr);
+            load_mwfrag<NW>(a, r0 + 16 * nr + rl, kq, nb2, wB);
+            compute(wA, x, r);
+            if (++r == RT) r = 0, ++b;
+            if (b >= b1) break;
+            if (r == 0) load_mafrag<NT>(a, b, l, x);
+            next(nb2, nr);
+            load_mwfrag<NW>(a, r0 + 16 * nr + rl, kq, nb2, wA);
+            compute(wB, x, r);
+            if (++r == RT) r = 0, ++b;
+            if (b >= b1) break;
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int m = 0; m < NW; m++)
+#pragma unroll
+                for (int tt = 0; tt < NT; tt++) red[wave - 1][r][m][tt][l] = acc[r][m][tt];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int q = 0; q < 3; q++)
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int m = 0; m < NW; m++)
+#pragma unroll
+                for (int tt = 0; tt < NT; tt++) acc[r][m][tt] += red[q][r][m][tt][l];
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        const int row = r0 + 16 * r + rl;
+#pragma unroll
+        for (int tt = 0; tt < NT; tt++) {
+            const int tok = 4 * tt + kq;
+            if (row >= a.nrows || tok >= a.M) continue;
+            const int64_t o = (int64_t)tok * a.ldy + row;
+            const float v = acc[r][0][tt];
+            if (MODE == G_ADD) a.out[o] = a.y_in[o] + v;
+            else if (MODE == G_GLU) a.out[o] = v / (1.0f + expf(-v)) * acc[r][NW - 1][tt];  // cpu_backend.cpp:260-261
+            else a.out[o] = v;
+        }
+    }
+}
+
+template <int MODE, int NT>
+static void launch_gemm_m_nt(const GemmArgs &a, int rt, hipStream_t s) {
+    const unsigned grid = (unsigned)((a.nrows + 16 * rt - 1) / (16 * rt));
+    if (rt == 4) hipLaunchKernelGGL((k_gemm_m<MODE, NT, 4>), dim3(grid), dim3(256), 0, s, a);
+    else if (rt == 2) hipLaunchKernelGGL((k_gemm_m<MODE, NT, 2>), dim3(grid), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_gemm_m<MODE, NT, 1>), dim3(grid), dim3(256), 0, s, a);
+}
+
+template <int MODE>
+static hipError_t launch_gemm_m(const GemmArgs &a, hipStream_t s) {
+    // Row tiles a workgroup: as many as keep about one workgroup a CU.
+    const int tiles = (a.nrows + 15) / 16;
+    const int rt = tiles >= 4 * g_gemm_m_cu ? 4 : tiles >= 2 * g_gemm_m_cu ? 2 : 1;
+    if (a.M <= 4) launch_gemm_m_nt<MODE, 1>(a, rt, s);
+    else launch_gemm_m_nt<MODE, 2>(a, rt, s);
+    return hipGetLastError();
+}
+
 // Split-K: y[t][r] = (y_in +) sum over splits in order (GLU: silu(g) * u).
 // Four consecutive values a thread (rows of one token when nrows % 4 == 0,
 // else one value at a time), every split's partial requested before the
@@ -565,6 +759,16 @@ static hipError_t launch_gemm_reduce(const float *part, int ks, int M, int nrows
 // k_gemm is built for Q6_K and Q8_0 only.
 template <int FMT, int MODE>
 static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
+    if constexpr (FMT == F_Q4K) {
+        // Up to 8 tokens on k_gemm_m (5 tokens: as fast as k_gemm_small; 1-4
+        // tokens ~20 % faster); 9-16 on k_gemm_small. TS5HIP_GEMM_M=0 keeps
+        // every batch on k_gemm_small, for comparison.
+        static const bool use_m = [] {
+            const char *e = getenv("TS5HIP_GEMM_M");
+            return !(e && e[0] == '0');
+        }();
+        if (a.M <= 8 && use_m) return launch_gemm_m<MODE>(a, s);
+    }
     if (a.M <= 16) {
         hipLaunchKernelGGL((k_gemm_small<FMT, MODE>), dim3((a.nrows + 15) / 16), dim3(256), 0, s, a);
     } else if constexpr (FMT == F_Q80) {
@@ -593,7 +797,7 @@ static hipError_t gemm_fmt(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) 
 static int gemm_tn(uint32_t t, int M) { return M > 16 && t == T_Q8_0 ? 4 : 1; }
 
 static int g_gemm_cu = 256;
-void set_gemm_cu_count(int n) { g_gemm_cu = n > 0 ? n : 256; }
+void set_gemm_cu_count(int n) { g_gemm_cu = g_gemm_m_cu = n > 0 ? n : 256; }
 
 // Splits of K that give the launch about four workgroups per CU when the
 // tokens alone do not (small M: the matmul is a weight stream).

@@ -18,7 +18,7 @@
 // contiguous, 128 + 8 bytes per key at head_dim 128.
 #include <mutex>
 
-#include "attn_core.h"
+#include "attn_lds.h"
 
 namespace ts5hip {
 
@@ -101,6 +101,21 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float *__restrict__ qkv, i
 // (query, RoPE, norms, partials, output) follows in `tail`. flags: 1
 // kv_per_batch, 2 append, 4 rope.
 constexpr int ATTN_NT = 512;  // threads per work item: 8 waves, two per SIMD
+
+// The same work item for short slices (one query, a cache of up to
+// LDS_MAX_CTX positions): attn_slice_lds shares the slice through LDS.
+template <int HD, int G, bool F16>
+__global__ __launch_bounds__(ATTN_NT) void k_attn_lds(const int8_t *k8, const uint16_t *ks, const int8_t *v8,
+                                                      const uint16_t *vs, const int32_t *n_keys, int n_ctx, int HKV,
+                                                      int flags, int n_split, AttnArgs tail) {
+    __shared__ LdsSliceLds<HD, G, ATTN_NT> S;
+    AttnArgs a = tail;
+    a.kv = KvLayer{const_cast<int8_t *>(k8), const_cast<uint16_t *>(ks), const_cast<int8_t *>(v8),
+                   const_cast<uint16_t *>(vs)};
+    a.n_keys = n_keys, a.n_ctx = n_ctx, a.HKV = HKV;
+    a.kv_per_batch = flags & 1, a.append = (flags >> 1) & 1, a.rope = (flags >> 2) & 1;
+    attn_slice_lds<HD, G, ATTN_NT, F16>(a, blockIdx.x, blockIdx.y, blockIdx.z, n_split, S);
+}
 
 template <int HD, int G, bool F16>
 __global__ __launch_bounds__(ATTN_NT) void k_attn(const int8_t *k8, const uint16_t *ks, const int8_t *v8,
@@ -214,14 +229,26 @@ hipError_t launch_rope_kv(const float *qkv, int64_t qkv_stride, const float *bia
     return hipGetLastError();
 }
 
+// One query over a cache of up to this many positions takes k_attn_lds
+// (4096 keys: 12.4 against 14.1 us a layer inside a decode token; the two
+// meet near 8192; past it, and for several queries, k_attn is faster: B 16 x
+// 32768 keys 331 against 413 us).
+constexpr int LDS_MAX_CTX = 8192;
+
 template <int HD, bool F16>
 static hipError_t attn_launch(int G, dim3 grid, const AttnArgs &a, hipStream_t s) {
     const int flags = (a.kv_per_batch ? 1 : 0) | (a.append ? 2 : 0) | (a.rope ? 4 : 0);
+    const bool lds = grid.z == 1 && a.n_ctx <= LDS_MAX_CTX;
 #define TS5_ATTN(GG)                                                                                          \
     case GG:                                                                                                  \
-        hipLaunchKernelGGL((k_attn<HD, GG, F16>), grid, dim3(ATTN_NT), 0, s, (const int8_t *)a.kv.k,          \
-                           (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs, a.n_keys, \
-                           a.n_ctx, a.HKV, flags, (int)grid.x, a);                                           \
+        if (lds)                                                                                              \
+            hipLaunchKernelGGL((k_attn_lds<HD, GG, F16>), grid, dim3(ATTN_NT), 0, s, (const int8_t *)a.kv.k,  \
+                               (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs,  \
+                               a.n_keys, a.n_ctx, a.HKV, flags, (int)grid.x, a);                             \
+        else                                                                                                  \
+            hipLaunchKernelGGL((k_attn<HD, GG, F16>), grid, dim3(ATTN_NT), 0, s, (const int8_t *)a.kv.k,      \
+                               (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs,  \
+                               a.n_keys, a.n_ctx, a.HKV, flags, (int)grid.x, a);                             \
         break;
     switch (G) {
         TS5_ATTN(1)

@@ -36,11 +36,11 @@ from tokenstation5_amd import synth, ts5hip  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the roofline kernel, from rocprofv3 --pmc runs of
 # `bench.py --roofline-only` (profiles/glu_roofline_counters.md): FETCH_SIZE
-# 32,442.0 KiB and WRITE_SIZE 448 KiB per dispatch, scaled by what the same
+# 32,447.5 KiB and WRITE_SIZE 448 KiB per dispatch, scaled by what the same
 # counters read for the one-pass RMSNorm stream of 256 MiB in and 256 MiB out
-# (131,226.9 and 262,144 KiB: factors 1.9976 and 1.0). 1.010 x the algorithmic
+# (131,215.4 and 262,144 KiB: factors 1.9978 and 1.0). 1.010 x the algorithmic
 # bytes.
-GLU_TRAFFIC_BYTES = 66821554
+GLU_TRAFFIC_BYTES = 66838609
 PROMPT = 4096
 SEED = 20241201
 
@@ -341,6 +341,31 @@ def prefill_only(hp, prompt_len: int = PROMPT):
                       "prefill_tok_s": round(prompt_len / ms * 1e3, 1)}), flush=True)
 
 
+def verify_only(hp, prompt_len: int = PROMPT, reps: int = 20):
+    """The verify batch alone (for rocprofv3 runs of the several-token
+    kernels): after the prompt, `reps` forwards of 5 tokens (one token + 4
+    drafts, every row's logits kept in HBM, as the engine's speculative step
+    calls it) and `reps` single-token forwards at the same position, each
+    set timed with HIP events on the library's stream."""
+    ctx = ts5hip.Context(0)
+    m = ts5hip.Model(ctx, hp, prompt_len + 16)
+    for name, t, ne0, ne1 in synth.tensor_specs(hp):
+        m.synth_tensor(name, t, ne0, ne1, SEED)
+    prompt = np.random.default_rng(SEED).integers(0, hp["n_vocab"], prompt_len).astype(np.int32)
+    m.forward(prompt, 0, logits=False)
+    batch = np.ascontiguousarray(prompt[-5:])
+
+    def fwd(n):
+        ctx.check(ts5hip.lib().ts5hip_forward_in_place(m.h, batch.ctypes.data, n, prompt_len, int(n > 1)))
+
+    step = timed(ctx, lambda i: fwd(1), reps, 2, busy=False)
+    verify = timed(ctx, lambda i: fwd(5), reps, 2, busy=False)
+    m.close()
+    ctx.close()
+    print(json.dumps({"step_us": round(step, 1), "verify5_us": round(verify, 1),
+                      "verify5_over_step": round(verify / step, 3)}), flush=True)
+
+
 def cpu_baseline(hp, steps: int = 4, keys: int = PROMPT):
     """The CPU oracle (the restatement of ts5's CPU backend: per-row dequant,
     fp64 dots, rows striped over threads) on the host cores: the cfg2 8B
@@ -403,6 +428,8 @@ def main():
                     help="only the roofline kernel's launches and a 256 MiB device copy (for rocprofv3 --pmc)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prompt's prefill, timed on the device (for rocprofv3 runs)")
+    ap.add_argument("--verify-only", action="store_true",
+                    help="only 5-token verify forwards and single steps, device-timed (for rocprofv3 runs)")
     ap.add_argument("--no-configs", action="store_true", help="skip the cfg1/cfg3/cfg4/cfg5 measurements")
     ap.add_argument("--no-spec", action="store_true", help="skip cfg5 (draft model + two targets, ~1 min)")
     ap.add_argument("--decode-only", action="store_true",
@@ -418,6 +445,9 @@ def main():
         return
     if args.prefill_only:
         prefill_only(hp, args.prompt)
+        return
+    if args.verify_only:
+        verify_only(hp, args.prompt)
         return
     ctx = ts5hip.Context(0)
     log(f"device {ctx.arch}, {ctx.n_cu} CUs, {ctx.hbm / 2**30:.0f} GiB")

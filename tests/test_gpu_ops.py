@@ -143,6 +143,7 @@ def run_matvec(ctx, t, W, ne0, rows, x, accumulate=None, norm=None, eps=1e-5):
     (synth.Q4_K, 4096, 1024),     # wk/wv
     (synth.Q4_K, 14336, 4096),    # ffn_down
     (synth.Q4_K, 4864, 896),      # the draft's ffn_down (19 blocks per row)
+    (synth.Q4_K, 4352, 37),       # 17 blocks: split 9 + 8 across waves, ragged rows
     (synth.Q4_K, 256, 37),        # one block, ragged rows
     (synth.Q6_K, 4096, 4096),
     (synth.Q6_K, 512, 1000),
@@ -191,17 +192,19 @@ def test_matvec_precision(ctx, t, ne0, rows, centered):
         assert rel_l2(got5[k], want[k]) <= 2e-6, (k, rel_l2(got5[k], want[k]))
 
 
-def test_matvec_accumulate_and_scales(ctx):
+@pytest.mark.parametrize("ne0,rows", [(1024, 256), (14336, 200)])
+def test_matvec_accumulate_and_scales(ctx, ne0, rows):
     """Input magnitudes from 1e-6 to 1e7 (the activation scale is per 32
-    values), and accumulation into an existing fp32 vector (y += W x)."""
-    W = synth.tensor(synth.Q4_K, 1024, 256, 3, "acc")
+    values), and accumulation into an existing fp32 vector (y += W x), for
+    rows of one step and rows whose blocks the workgroup's waves split."""
+    W = synth.tensor(synth.Q4_K, ne0, rows, 3, f"acc{ne0}")
     rng = np.random.default_rng(4)
     for scale in (1e-6, 1.0, 1e7):
-        x = (rng.standard_normal(1024) * scale).astype(np.float32)
-        want = oracle.matmul(synth.Q4_K, W, 1024, x)[0]
-        assert rel_l2(run_matvec(ctx, synth.Q4_K, W, 1024, 256, x), want) <= REL_L2, scale
-        y0 = (rng.standard_normal(256) * np.abs(want).mean()).astype(np.float32)
-        got = run_matvec(ctx, synth.Q4_K, W, 1024, 256, x, accumulate=y0.copy())
+        x = (rng.standard_normal(ne0) * scale).astype(np.float32)
+        want = oracle.matmul(synth.Q4_K, W, ne0, x)[0]
+        assert rel_l2(run_matvec(ctx, synth.Q4_K, W, ne0, rows, x), want) <= REL_L2, scale
+        y0 = (rng.standard_normal(rows) * np.abs(want).mean()).astype(np.float32)
+        got = run_matvec(ctx, synth.Q4_K, W, ne0, rows, x, accumulate=y0.copy())
         assert rel_l2(got, y0.astype(np.float64) + want) <= REL_L2, scale
 
 

@@ -24,7 +24,7 @@ struct MvTail {
 // with -amdgpu-kernarg-preload-count=16; two of the 16 user SGPRs hold the
 // argument pointer), so a launch does not start with a round trip to its
 // argument buffer. nwg is the grid size.
-template <class F, int R, int WAVES, int MODE, int RUNS, bool NORM>
+template <class F, int R, int WAVES, int KS, int MODE, int RUNS, bool NORM>
 __global__ __launch_bounds__(WAVES *WAVE) void k_mv(const void *w, const void *w2, const float *x,
                                                     const float *norm_w, float *y, int nrows, int n_in, int nwg,
                                                     float eps, MvTail tail) {
@@ -44,7 +44,7 @@ __global__ __launch_bounds__(WAVES *WAVE) void k_mv(const void *w, const void *w
     auto fetch_tail = [&]() {
         if constexpr (MODE == MV_ADD) asm volatile("" ::"s"(a.y_in));
     };
-    mv_run<F, R, WAVES, MODE, RUNS, NORM>(a, blockIdx.x, nwg, lds, red, fetch_tail, best_v, best_i);
+    mv_run<F, R, WAVES, KS, MODE, RUNS, NORM>(a, blockIdx.x, nwg, lds, red, fetch_tail, best_v, best_i);
     if (MODE != MV_ARGMAX) return;
     // Each workgroup's best, then the last workgroup to finish picks the
     // winner. Workgroup w counts into sub-counter w % ARGMAX_FAN, the last
@@ -113,10 +113,10 @@ void set_cu_count(int n) { g_n_cu = n > 0 ? n : 256; }
 // head's argmax.
 static size_t mv_max_grid() { return (size_t)TS5_MV_WG_PER_CU * g_n_cu; }
 
-template <class F, int R, int WAVES, int MODE>
+template <class F, int R, int WAVES, int KS, int MODE>
 static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
     if (a.nrows > INT32_MAX) return hipErrorInvalidValue;  // the kernel takes a 32-bit row count
-    const int64_t rpg = (int64_t)R * WAVES;
+    const int64_t rpg = (int64_t)R * (WAVES / KS);
     const int64_t ngroups = (a.nrows + rpg - 1) / rpg;
     const int64_t cap = (int64_t)mv_max_grid();
     const int64_t per = (ngroups + cap - 1) / cap;  // groups per workgroup
@@ -129,7 +129,7 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
     const size_t lds = act_bytes(a.n_in);
     const MvTail tail{a.t, a.nb, a.y_in, a.best_v, a.best_i, a.counter, a.out, a.seq, a.pos};
 #define TS5_MV_LAUNCH(RUNS, NORM)                                                                                 \
-    hipLaunchKernelGGL((k_mv<F, R, WAVES, MODE, RUNS, NORM>), g, b, lds, s, a.w, a.w2, a.x, a.norm_w, a.y,        \
+    hipLaunchKernelGGL((k_mv<F, R, WAVES, KS, MODE, RUNS, NORM>), g, b, lds, s, a.w, a.w2, a.x, a.norm_w, a.y,        \
                        (int)a.nrows, a.n_in, (int)grid, a.eps, tail)
     if (nr <= nt && norm) TS5_MV_LAUNCH(1, true);
     else if (nr <= nt) TS5_MV_LAUNCH(1, false);
@@ -141,19 +141,38 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Q4_K rows of more than one step (nb > 16 blocks, the down projection):
+// the workgroup's waves split each row's blocks, so that a CU has more weight
+// bytes in flight than its few row groups give it.
+#ifndef TS5_MV_KS
+#define TS5_MV_KS 2
+#endif
+#ifndef TS5_MV_KS_R
+#define TS5_MV_KS_R 4
+#endif
+#ifndef TS5_MV_KS_WAVES
+#define TS5_MV_KS_WAVES 8
+#endif
+#ifndef TS5_MV_KS_MINNB
+#define TS5_MV_KS_MINNB 17
+#endif
+
 template <int MODE>
 static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
     if constexpr (MODE == MV_GLU) {
         switch (a.t) {
-        case T_Q4_K: return mv_go<Q4K, TS5_MV_GLU_R, TS5_MV_GLU_WAVES, MODE>(a, s);
-        case T_Q6_K: return mv_go<Q6K, 2, 4, MODE>(a, s);
-        case T_Q8_0: return mv_go<Q80, 2, 4, MODE>(a, s);
+        case T_Q4_K: return mv_go<Q4K, TS5_MV_GLU_R, TS5_MV_GLU_WAVES, 1, MODE>(a, s);
+        case T_Q6_K: return mv_go<Q6K, 2, 4, 1, MODE>(a, s);
+        case T_Q8_0: return mv_go<Q80, 2, 4, 1, MODE>(a, s);
         }
     } else {
         switch (a.t) {
-        case T_Q4_K: return mv_go<Q4K, TS5_MV_R, 4, MODE>(a, s);
-        case T_Q6_K: return mv_go<Q6K, 4, 4, MODE>(a, s);
-        case T_Q8_0: return mv_go<Q80, 4, 4, MODE>(a, s);
+        case T_Q4_K:
+            if (MODE != MV_ARGMAX && TS5_MV_KS > 1 && a.nb >= TS5_MV_KS_MINNB)
+                return mv_go<Q4K, TS5_MV_KS_R, TS5_MV_KS_WAVES, TS5_MV_KS, MODE>(a, s);
+            return mv_go<Q4K, TS5_MV_R, 4, 1, MODE>(a, s);
+        case T_Q6_K: return mv_go<Q6K, 4, 4, 1, MODE>(a, s);
+        case T_Q8_0: return mv_go<Q80, 4, 4, 1, MODE>(a, s);
         }
     }
     return hipErrorInvalidValue;

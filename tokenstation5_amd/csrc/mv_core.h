@@ -20,7 +20,9 @@
 //    as a flat sequence of steps (one 64-lane sweep of 64/LPB blocks each)
 //    and always has the next step's weight loads in flight while it computes
 //    the current one. The first step's loads are issued before the
-//    activation is built. Every weight byte is read once.
+//    activation is built. Rows of many blocks (the down projection) are
+//    split between the workgroup's waves, whose sums meet in LDS. Every
+//    weight byte is read once.
 // Bandwidth-bound: no MFMA.
 #pragma once
 #include <climits>
@@ -52,6 +54,7 @@ __device__ inline uint4 ld16(const void *p) { return *(const uint4 *)p; }
 // nibbles) and 2g+1 (high nibbles), 64 values.
 struct Q4K {
     static constexpr int LPB = 4, VALUES = 256;  // lanes per block, values per block
+    static constexpr int LOADS = 3;              // vector memory loads per load_w
     struct X {
         uint32_t p[3][2][8];  // [plane hi, mid, lo][sub-block 2 sub, 2 sub + 1][dword]
         float s0, s1, u0, u1;  // the two sub-blocks' scales and sums
@@ -115,6 +118,7 @@ struct Q4K {
 // the four 16-value runs at 128h + 32c + i0 (c = 0..3), 64 values.
 struct Q6K {
     static constexpr int LPB = 4, VALUES = 256;
+    static constexpr int LOADS = 5;  // vector memory loads per load_w
     struct X {
         uint32_t p[3][4][4];  // [plane][run c][dword]
         float s[4];
@@ -190,6 +194,7 @@ struct Q6K {
 // Q8_0: 2 lanes per 32-value block, 16 values each.
 struct Q80 {
     static constexpr int LPB = 2, VALUES = 32;
+    static constexpr int LOADS = 2;  // vector memory loads per load_w
     struct X {
         uint4 p[3];  // the planes' 16 bytes
         float s;
@@ -444,9 +449,9 @@ struct MvArgs {
 };
 
 template <class F, int R>
-__device__ inline void load_rows(const WPtr &w, int64_t row0, int64_t nrows, int nb, int b, int sub,
+__device__ inline void load_rows(const WPtr &w, int64_t row0, int64_t nrows, int nb, int b, int bmax, int sub,
                                  typename F::W (&wf)[R]) {
-    const int bb = min(b, nb - 1);  // lanes past the row's end re-read its last block (in bounds), not used
+    const int bb = min(b, bmax);  // lanes past the split's end re-read its last block (in bounds), not used
 #pragma unroll
     for (int r = 0; r < R; r++) wf[r] = F::load_w(w, min(row0 + r, nrows - 1), nb, bb, sub);
 }
@@ -462,23 +467,34 @@ __device__ inline void best_pick_wave(float &v, int &i) {
     }
 }
 
-// The workgroup `wg` of `nwg` computes its row groups of a.  before_act()
+// The workgroup `wg` of `nwg` computes its row groups of a. Its WAVES waves
+// are KS splits of WAVES / KS row waves: row wave rw takes rows rw*R ..
+// rw*R + R-1 of each group, split ks the blocks ks*nbk .. ks*nbk + nbk-1 of
+// those rows (nbk = ceil(nb / KS)); the splits' sums meet in LDS and the
+// first split finishes the rows, adding them in split order. before_act()
 // runs after the first weight loads are issued and before the activation is
-// built (the persistent kernel's grid barrier). lds: act_bytes(a.n_in)
-// bytes; red: NT/64 floats. MV_ARGMAX returns this workgroup's best
-// (value, row) in best_v / best_i (every thread).
-template <class F, int R, int WAVES, int MODE, int RUNS, bool NORM, class Hook>
+// built. lds: act_bytes(a.n_in) bytes; red: NT/64 floats. MV_ARGMAX returns
+// this workgroup's best (value, row) in best_v / best_i (every thread).
+template <class F, int R, int WAVES, int KS, int MODE, int RUNS, bool NORM, class Hook>
 __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, float *red, Hook before_act,
                               float &best_v, int &best_i) {
-    constexpr int NT = WAVES * WAVE, BPI = WAVE / F::LPB, NW = MODE == MV_GLU ? 2 : 1;
+    static_assert(WAVES % KS == 0, "splits of whole row waves");
+    constexpr int NT = WAVES * WAVE, BPI = WAVE / F::LPB, NW = MODE == MV_GLU ? 2 : 1, RW = WAVES / KS;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, bsub = lane / F::LPB, sub = lane % F::LPB;
-    const int64_t rpg = (int64_t)R * WAVES;
+    const int rw = wave % RW, ks = wave / RW;
+    const int64_t rpg = (int64_t)R * RW;
     const int64_t ngroups = (a.nrows + rpg - 1) / rpg;
-    const int spg = (a.nb + BPI - 1) / BPI;  // steps per row group
+    const int nbk = KS == 1 ? a.nb : (a.nb + KS - 1) / KS;
+    const int spg = (nbk + BPI - 1) / BPI;  // steps per row group
+    const int kb0 = ks * nbk, kb1 = min(a.nb, kb0 + nbk);
     const int64_t nblocks = (int64_t)a.nb * a.nrows;
     const WPtr w1 = wptr(a.t, a.w, nblocks), w2 = wptr(a.t, MODE == MV_GLU ? a.w2 : a.w, nblocks);
     best_v = -INFINITY;
     best_i = INT_MAX;
+    // The splits' row sums, double-buffered by group parity: the first split
+    // reads buffer p after the barrier of its group, and a split writes p
+    // again only after the next group's barrier, which that read precedes.
+    __shared__ float kpart[KS > 1 ? 2 : 1][KS][RW][NW][R];
 
     // Every argument the prologue and the first loads need, fetched together
     // (the compiler would fetch each where first used: a round trip apiece).
@@ -489,133 +505,128 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
     ActIn<NT, RUNS ? RUNS : 1, NORM> ain;
     if constexpr (RUNS > 0) act_in_load<NT, RUNS, NORM>(ain, a.x, a.norm_w, a.n_in);
     typename F::W cur[NW][R], nxt[NW][R];
-    {  // unconditional (rows are clamped; every launch has wg < ngroups), so no
-       // branch makes the compiler's waits for the activation cover these
-        const int64_t row0 = g * rpg + (int64_t)wave * R;
-        load_rows<F, R>(w1, row0, a.nrows, a.nb, bsub, sub, cur[0]);
-        if (MODE == MV_GLU) load_rows<F, R>(w2, row0, a.nrows, a.nb, bsub, sub, cur[NW - 1]);
-    }
+    // The weights of step `i` of group `gi` into `buf`.
+    auto issue = [&](int64_t gi, int i, typename F::W (&buf)[NW][R]) {
+        const int64_t row0 = gi * rpg + (int64_t)rw * R;
+        load_rows<F, R>(w1, row0, a.nrows, a.nb, kb0 + i * BPI + bsub, kb1 - 1, sub, buf[0]);
+        if (MODE == MV_GLU) load_rows<F, R>(w2, row0, a.nrows, a.nb, kb0 + i * BPI + bsub, kb1 - 1, sub, buf[NW - 1]);
+    };
+    // Unconditional (rows are clamped; every launch has wg < ngroups), so no
+    // branch makes the compiler's waits for the activation cover these.
+    // (Issuing the second step here as well, before the activation is built,
+    // measured slower: the input's loads then return later.)
+    issue(g, 0, cur);
     before_act();
     const Act xa = act_view(lds, a.n_in);
     if constexpr (RUNS > 0) act_in_build<NT, RUNS, NORM>(ain, a.eps, a.n_in, xa, red);
     else if (g < ngroups) build_act<NT>(a.x, a.norm_w, a.eps, a.n_in, xa, red);
     const CAct x{xa.hi, xa.mid, xa.lo, xa.scale, xa.sum, xa.isum};
+    // The input runs (older than the first step's weights) are all in; said
+    // explicitly, so that the compiler's count does not carry those of
+    // threads that had no run into the loop as still open (it then waited
+    // for most of a step's loads before issuing the next step's).
+    wait_vmcnt<F::LOADS * R * NW>();
 
     float acc[NW][R];
 #pragma unroll
     for (int k = 0; k < NW; k++)
 #pragma unroll
         for (int r = 0; r < R; r++) acc[k][r] = 0.f;
-    // The fused gate/up uses its two register buffers in turn (the loop body
-    // runs twice per trip with their roles swapped): copying the next step's
-    // buffer into the current one makes the compiler wait for the next step's
-    // loads in the middle of this step's arithmetic (16.7 against 18.3 us on
-    // the 8B gate/up). The other modes keep the copy loop below: the swap
-    // made them slower (1.84 against 1.80 ms a token when every mode swapped;
-    // the Q6_K head alone 105 against 87 us).
-    auto step = [&](typename F::W (&cb)[NW][R], typename F::W (&nbuf)[NW][R]) -> bool {
+    int par = 0;
+    // Step `it` of group g on the weights in cb; at the group's last step, the
+    // rows' results.
+    auto compute = [&](const typename F::W (&cb)[NW][R]) {
+        // Branch-free: lanes past the split's end compute on its last block
+        // (loaded clamped) and add nothing, so no path skips the arithmetic
+        // whose waits the compiler must then assume still open.
+        const int b = kb0 + it * BPI + bsub;
+        const bool valid = b < kb1;
+        const typename F::X xf = F::load_x(x, min(b, kb1 - 1), sub);
+#pragma unroll
+        for (int k = 0; k < NW; k++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const float d = F::dot(cb[k][r], xf, sub);
+                acc[k][r] += valid ? d : 0.f;
+            }
+        if (it != spg - 1) return;
+#pragma unroll
+        for (int k = 0; k < NW; k++)
+#pragma unroll
+            for (int r = 0; r < R; r++) acc[k][r] = wave_sum_dpp(acc[k][r]);
+        if constexpr (KS > 1) {
+            if (lane == 0)
+#pragma unroll
+                for (int k = 0; k < NW; k++)
+#pragma unroll
+                    for (int r = 0; r < R; r++) kpart[par][ks][rw][k][r] = acc[k][r];
+            __syncthreads();
+            if (ks == 0)
+#pragma unroll
+                for (int k = 0; k < NW; k++)
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        float v = kpart[par][0][rw][k][r];
+#pragma unroll
+                        for (int j = 1; j < KS; j++) v += kpart[par][j][rw][k][r];
+                        acc[k][r] = v;
+                    }
+            par ^= 1;
+        }
+        const int64_t row0 = g * rpg + (int64_t)rw * R;
+        if (ks == 0 && lane < R && row0 + lane < a.nrows) {
+            float v = acc[0][0], u = acc[NW - 1][0];
+#pragma unroll
+            for (int r = 1; r < R; r++)
+                if (lane == r) v = acc[0][r], u = acc[NW - 1][r];
+            const int64_t row = row0 + lane;
+            if (MODE == MV_ADD) {
+                st_dev(a.y + row, a.y_in[row] + v);
+            } else if (MODE == MV_GLU) {
+                st_dev(a.y + row, v / (1.0f + expf(-v)) * u);  // engine/src/cpu_backend.cpp:260-261
+            } else {
+                st_dev(a.y + row, v);
+                if (MODE == MV_ARGMAX && (v > best_v || (v == best_v && row < best_i))) best_v = v, best_i = (int)row;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NW; k++)
+#pragma unroll
+            for (int r = 0; r < R; r++) acc[k][r] = 0.f;
+    };
+    // The steps of this workgroup (its groups wg, wg + nwg, ... times spg) run
+    // through the two register buffers in turn: the next step's loads are
+    // issued, unconditionally, right before this step's arithmetic in the
+    // same block, so the compiler's wait for this step's weights leaves the
+    // next step's in flight. (Loads issued under a branch that joins before
+    // the arithmetic made it wait for all of them, vmcnt(0), and a copy from
+    // one buffer to the other waits for the copied loads.) Only the last step
+    // is computed with nothing behind it.
+    const int64_t nsteps = (ngroups - wg + nwg - 1) / nwg * spg;
+    auto issue_next = [&](typename F::W (&buf)[NW][R]) {  // the step after (g, it)
         int64_t gn = g;
         int itn = it + 1;
         if (itn == spg) itn = 0, gn = g + nwg;
-        const bool more = gn < ngroups;
-        if (more) {
-            const int64_t row0n = gn * rpg + (int64_t)wave * R;
-            load_rows<F, R>(w1, row0n, a.nrows, a.nb, itn * BPI + bsub, sub, nbuf[0]);
-            if (MODE == MV_GLU) load_rows<F, R>(w2, row0n, a.nrows, a.nb, itn * BPI + bsub, sub, nbuf[NW - 1]);
-        }
-        const int b = it * BPI + bsub;
-        if (b < a.nb) {
-            const typename F::X xf = F::load_x(x, b, sub);
-#pragma unroll
-            for (int k = 0; k < NW; k++)
-#pragma unroll
-                for (int r = 0; r < R; r++) acc[k][r] += F::dot(cb[k][r], xf, sub);
-        }
-        if (it == spg - 1) {
-            const int64_t row0 = g * rpg + (int64_t)wave * R;
-#pragma unroll
-            for (int k = 0; k < NW; k++)
-#pragma unroll
-                for (int r = 0; r < R; r++) acc[k][r] = wave_sum_dpp(acc[k][r]);
-            if (lane < R && row0 + lane < a.nrows) {
-                float v = acc[0][0], u = acc[NW - 1][0];
-#pragma unroll
-                for (int r = 1; r < R; r++)
-                    if (lane == r) v = acc[0][r], u = acc[NW - 1][r];
-                const int64_t row = row0 + lane;
-                if (MODE == MV_ADD) {
-                    st_dev(a.y + row, a.y_in[row] + v);
-                } else if (MODE == MV_GLU) {
-                    st_dev(a.y + row, v / (1.0f + expf(-v)) * u);  // engine/src/cpu_backend.cpp:260-261
-                } else {
-                    st_dev(a.y + row, v);
-                    if (MODE == MV_ARGMAX && (v > best_v || (v == best_v && row < best_i))) best_v = v, best_i = (int)row;
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < NW; k++)
-#pragma unroll
-                for (int r = 0; r < R; r++) acc[k][r] = 0.f;
-        }
-        g = gn, it = itn;
-        return more;
+        issue(gn, itn, buf);
     };
-    if constexpr (MODE == MV_GLU) {
-        if (g < ngroups)
-            while (step(cur, nxt) && step(nxt, cur)) {
-            }
-    } else {
-        while (g < ngroups) {
-            int64_t gn = g;
-            int itn = it + 1;
-            if (itn == spg) itn = 0, gn = g + nwg;
-            const bool more = gn < ngroups;
-            if (more) {
-                const int64_t row0n = gn * rpg + (int64_t)wave * R;
-                load_rows<F, R>(w1, row0n, a.nrows, a.nb, itn * BPI + bsub, sub, nxt[0]);
-                if (MODE == MV_GLU) load_rows<F, R>(w2, row0n, a.nrows, a.nb, itn * BPI + bsub, sub, nxt[NW - 1]);
-            }
-            const int b = it * BPI + bsub;
-            if (b < a.nb) {
-                const typename F::X xf = F::load_x(x, b, sub);
-#pragma unroll
-                for (int k = 0; k < NW; k++)
-#pragma unroll
-                    for (int r = 0; r < R; r++) acc[k][r] += F::dot(cur[k][r], xf, sub);
-            }
-            if (it == spg - 1) {
-                const int64_t row0 = g * rpg + (int64_t)wave * R;
-#pragma unroll
-                for (int k = 0; k < NW; k++)
-#pragma unroll
-                    for (int r = 0; r < R; r++) acc[k][r] = wave_sum_dpp(acc[k][r]);
-                if (lane < R && row0 + lane < a.nrows) {
-                    float v = acc[0][0], u = acc[NW - 1][0];
-#pragma unroll
-                    for (int r = 1; r < R; r++)
-                        if (lane == r) v = acc[0][r], u = acc[NW - 1][r];
-                    const int64_t row = row0 + lane;
-                    if (MODE == MV_ADD) {
-                        st_dev(a.y + row, a.y_in[row] + v);
-                    } else if (MODE == MV_GLU) {
-                        st_dev(a.y + row, v / (1.0f + expf(-v)) * u);  // engine/src/cpu_backend.cpp:260-261
-                    } else {
-                        st_dev(a.y + row, v);
-                        if (MODE == MV_ARGMAX && (v > best_v || (v == best_v && row < best_i))) best_v = v, best_i = (int)row;
-                    }
-                }
-#pragma unroll
-                for (int k = 0; k < NW; k++)
-#pragma unroll
-                    for (int r = 0; r < R; r++) acc[k][r] = 0.f;
-            }
-            if (!more) break;
-#pragma unroll
-            for (int k = 0; k < NW; k++)
-#pragma unroll
-                for (int r = 0; r < R; r++) cur[k][r] = nxt[k][r];
-            g = gn, it = itn;
+    auto advance = [&]() {
+        if (++it == spg) it = 0, g += nwg;
+    };
+    for (int64_t s = 0;; s += 2) {
+        if (s + 1 >= nsteps) {
+            compute(cur);
+            break;
         }
+        issue_next(nxt);
+        compute(cur);
+        advance();
+        if (s + 2 >= nsteps) {
+            compute(nxt);
+            break;
+        }
+        issue_next(cur);
+        compute(nxt);
+        advance();
     }
     if (MODE == MV_ARGMAX) {
         // The first maximum wins (std::max_element): larger value, then lower row.

@@ -29,9 +29,19 @@
 // whose partial sums a second kernel adds in a fixed order.
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "common.h"
 #include "kernels.h"
+
+#ifndef TS5_GM_SCHED
+#define TS5_GM_SCHED 1
+#endif
+#if TS5_GM_SCHED
+#define TS5_GM_SB() __builtin_amdgcn_sched_barrier(0)
+#else
+#define TS5_GM_SB() (void)0
+#endif
 
 namespace ts5hip {
 
@@ -494,7 +504,7 @@ __global__ __launch_bounds__(256) void k_gemm_small(GemmArgs a) {
 // ---------------------------------------------------------------------------
 // Q4_K rows, up to 8 tokens (k_gemm_m): the roles of the MFMA operands
 // swapped so that each lane's result is one (token, row) pair. A = 16
-// activation rows, 4 tokens x 4 planes (hi, mid, lo, and a zero plane), of a
+// activation rows, 4 tokens x 4 planes (hi, mid, lo, and an unused fourth), of a
 // 32-value sub-block; B = the sub-block's quants of 16 weight rows. D lane l
 // then holds the 4 planes of token l/16 for weight row l%16, so
 // 65536 C_hi + 256 C_mid + C_lo and the block scaling
@@ -519,6 +529,9 @@ struct MWFrag {
 template <int NT>
 __device__ inline void load_mafrag(const GemmArgs &a, int b, int l, MAFrag<NT> &f) {
     const int kq = l >> 4, ar = l & 15, at = ar >> 2, ap = ar & 3, et = kq;
+    // Row plane 3 of the A tile repeats the lo plane: its D row is computed
+    // and never read (the combine takes planes 0-2), so the loaded values go
+    // to the MFMA untouched and nothing here waits for them.
     const int plane = ap == 0 ? 0 : ap == 1 ? MACT_MID : MACT_LO;
 #pragma unroll
     for (int tt = 0; tt < NT; tt++) {
@@ -527,8 +540,8 @@ __device__ inline void load_mafrag(const GemmArgs &a, int b, int l, MAFrag<NT> &
 #pragma unroll
         for (int s2 = 0; s2 < 8; s2 += 2) {
             const uint4 v = ld16(blk + 8 * s2);
-            f.p[tt][s2] = ap == 3 ? 0ull : ((uint64_t)v.y << 32) | v.x;
-            f.p[tt][s2 + 1] = ap == 3 ? 0ull : ((uint64_t)v.w << 32) | v.z;
+            f.p[tt][s2] = ((uint64_t)v.y << 32) | v.x;
+            f.p[tt][s2 + 1] = ((uint64_t)v.w << 32) | v.z;
         }
         const int etok = min(4 * tt + et, a.M - 1);
         const uint8_t *eb = a.act + (int64_t)etok * a.act_stride + (int64_t)b * MACT_BLOCK;
@@ -604,31 +617,46 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
         }
     };
     if (b0 < b1) {
-        MAFrag<NT> x;
+        MAFrag<NT> xA, xB;
         MWFrag<NW> wA, wB;
+        // In the order the loop requests them (weights, then activation), so
+        // that the loop starts in the state its back edge brings.
         load_mwfrag<NW>(a, r0 + rl, kq, b0, wA);
-        // Items (block b, row tile r) in order; the next one's weights are
-        // requested before the current one is computed (two buffers in turn).
-        int b = b0, r = 0;
-        auto next = [&](int &nb2, int &nr) {
-            nr = r + 1, nb2 = b;
-            if (nr == RT) nr = 0, nb2 = b + 1;
-            nb2 = min(nb2, b1 - 1);  // past the last item: a repeat, not used
+        load_mafrag<NT>(a, b0, l, xA);
+        // Items (block b, row tile r) in order through two weight buffers in
+        // turn, the blocks' activation fragments through two more: an item
+        // first requests the next item's weights (at a block's last tile also
+        // the next block's activation), unconditionally (past the last item a
+        // repeat, in bounds and not used), then computes. No branch sits
+        // between a request and the arithmetic after it, so the compiler's
+        // waits for this item leave the next one's loads in flight (a request
+        // under a branch made it wait for everything, vmcnt(0)).
+        auto run_block = [&](auto par, int b, MAFrag<NT> &xc, MAFrag<NT> &xn) {
+            constexpr int P = decltype(par)::value;
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const bool last = r == RT - 1;
+                const int nb2 = last ? min(b + 1, b1 - 1) : b, nr = last ? 0 : r + 1;
+                // sched_barrier: the scheduler would otherwise sink the requests
+                // below the arithmetic (register pressure) and lose the overlap.
+                if ((P + r) & 1) {
+                    load_mwfrag<NW>(a, r0 + 16 * nr + rl, kq, nb2, wA);
+                    if (last) load_mafrag<NT>(a, nb2, l, xn);
+                    TS5_GM_SB();
+                    compute(wB, xc, r);
+                } else {
+                    load_mwfrag<NW>(a, r0 + 16 * nr + rl, kq, nb2, wB);
+                    if (last) load_mafrag<NT>(a, nb2, l, xn);
+                    TS5_GM_SB();
+                    compute(wA, xc, r);
+                }
+            }
         };
-        for (;;) {
-            if (r == 0) load_mafrag<NT>(a, b, l, x);
-            int nb2, nr;
-            next(nb2, nr);
-            load_mwfrag<NW>(a, r0 + 16 * nr + rl, kq, nb2, wB);
-            compute(wA, x, r);
-            if (++r == RT) r = 0, ++b;
-            if (b >= b1) break;
-            if (r == 0) load_mafrag<NT>(a, b, l, x);
-            next(nb2, nr);
-            load_mwfrag<NW>(a, r0 + 16 * nr + rl, kq, nb2, wA);
-            compute(wB, x, r);
-            if (++r == RT) r = 0, ++b;
-            if (b >= b1) break;
+        for (int b = b0;; b += 2) {
+            run_block(std::integral_constant<int, 0>{}, b, xA, xB);
+            if (b + 1 >= b1) break;
+            run_block(std::integral_constant<int, RT & 1>{}, b + 1, xB, xA);
+            if (b + 2 >= b1) break;
         }
     }
     if (wave > 0) {

@@ -140,7 +140,8 @@ def run_matvec(ctx, t, W, ne0, rows, x, accumulate=None, norm=None, eps=1e-5):
 
 @pytest.mark.parametrize("t,ne0,rows", [
     (synth.Q4_K, 4096, 4096),     # cfg1
-    (synth.Q4_K, 4096, 1024),     # wk/wv
+    (synth.Q4_K, 4096, 1024),     # wk/wv (2 rows a wave)
+    (synth.Q4_K, 4096, 6144),     # fused QKV (3 rows a wave)
     (synth.Q4_K, 14336, 4096),    # ffn_down
     (synth.Q4_K, 4864, 896),      # the draft's ffn_down (19 blocks per row)
     (synth.Q4_K, 4352, 37),       # 17 blocks: split 9 + 8 across waves, ragged rows

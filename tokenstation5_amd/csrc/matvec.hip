@@ -104,6 +104,9 @@ __global__ __launch_bounds__(WAVES *WAVE) void k_mv(const void *w, const void *w
 #ifndef TS5_MV_GLU_R
 #define TS5_MV_GLU_R 1  // with its alternating buffers, 16.3 us on the 8B gate/up against 16.8 at 2 rows
 #endif
+#ifndef TS5_MV_Q6_R
+#define TS5_MV_Q6_R 2  // the 8B head: 97 against 107 us at 4 rows a wave
+#endif
 #ifndef TS5_MV_R
 #define TS5_MV_R 4
 #endif
@@ -157,6 +160,23 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
 #define TS5_MV_KS_MINNB 17
 #endif
 
+// Rows per wave of a Q4_K matvec whose row groups all fit the grid at once
+// (one step each): the count that leaves the busiest CU the fewest rows per
+// wave, ties to more rows per wave (more bytes in flight). QKV of the 8B
+// (6144 rows): 3 rows, 512 workgroups, two a CU (7.6 -> 6.8 us); at 4 rows
+// its 384 workgroups leave half the CUs with two and half with one.
+static int mv_rows_per_wave(int64_t nrows) {
+    if ((nrows + 15) / 16 > (int64_t)mv_max_grid()) return TS5_MV_R;  // a persistent grid
+    int best = 4;
+    int64_t best_cost = INT64_MAX;
+    for (int r = 4; r >= 2; r--) {
+        const int64_t groups = (nrows + 4 * r - 1) / (4 * r);
+        const int64_t cost = (groups + g_n_cu - 1) / g_n_cu * r;
+        if (cost < best_cost) best = r, best_cost = cost;
+    }
+    return best;
+}
+
 template <int MODE>
 static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
     if constexpr (MODE == MV_GLU) {
@@ -170,8 +190,12 @@ static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
         case T_Q4_K:
             if (MODE != MV_ARGMAX && TS5_MV_KS > 1 && a.nb >= TS5_MV_KS_MINNB)
                 return mv_go<Q4K, TS5_MV_KS_R, TS5_MV_KS_WAVES, TS5_MV_KS, MODE>(a, s);
-            return mv_go<Q4K, TS5_MV_R, 4, 1, MODE>(a, s);
-        case T_Q6_K: return mv_go<Q6K, 4, 4, 1, MODE>(a, s);
+            switch (mv_rows_per_wave(a.nrows)) {
+            case 3: return mv_go<Q4K, 3, 4, 1, MODE>(a, s);
+            case 2: return mv_go<Q4K, 2, 4, 1, MODE>(a, s);
+            default: return mv_go<Q4K, 4, 4, 1, MODE>(a, s);
+            }
+        case T_Q6_K: return mv_go<Q6K, TS5_MV_Q6_R, 4, 1, MODE>(a, s);
         case T_Q8_0: return mv_go<Q80, 4, 4, 1, MODE>(a, s);
         }
     }

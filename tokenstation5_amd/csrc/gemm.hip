@@ -34,6 +34,9 @@
 #include "common.h"
 #include "kernels.h"
 
+#ifndef TS5_GM_P5
+#define TS5_GM_P5 1
+#endif
 #ifndef TS5_GM_SCHED
 #define TS5_GM_SCHED 1
 #endif
@@ -515,10 +518,11 @@ __global__ __launch_bounds__(256) void k_gemm_small(GemmArgs a) {
 // walks the RT row tiles (weights one item ahead), so the activation is read
 // once per block and row group. The quarters meet in LDS in a fixed order.
 // ---------------------------------------------------------------------------
-template <int NT>
+template <int NT, bool P5>
 struct MAFrag {
     uint64_t p[NT][8];          // A: [token tile][sub-block] 8 bytes of plane (l%16)%4 of token (l%16)/4
     float xs[NT][8], xsum[NT][8];  // epilogue token l/16 of each tile: scale, sum per sub-block
+    float xs4[P5 ? 8 : 1], xsum4[P5 ? 8 : 1];  // P5: the fifth token's scales and sums
 };
 template <int NW>
 struct MWFrag {
@@ -526,16 +530,19 @@ struct MWFrag {
     uint64_t q[NW][4];  // B: the lane's k-group bytes of the 4 nibble groups of row l%16
 };
 
-template <int NT>
-__device__ inline void load_mafrag(const GemmArgs &a, int b, int l, MAFrag<NT> &f) {
+template <int NT, bool P5>
+__device__ inline void load_mafrag(const GemmArgs &a, int b, int l, MAFrag<NT, P5> &f) {
     const int kq = l >> 4, ar = l & 15, at = ar >> 2, ap = ar & 3, et = kq;
     // Row plane 3 of the A tile repeats the lo plane: its D row is computed
     // and never read (the combine takes planes 0-2), so the loaded values go
-    // to the MFMA untouched and nothing here waits for them.
-    const int plane = ap == 0 ? 0 : ap == 1 ? MACT_MID : MACT_LO;
+    // to the MFMA untouched and nothing here waits for them. With P5 (five
+    // tokens in one tile) row 4t + 3 carries plane t of the fifth token
+    // instead (t < 3; row 15 repeats its lo plane, unused).
+    const int plane_of = P5 && ap == 3 ? min(at, 2) : ap;
+    const int plane = plane_of == 0 ? 0 : plane_of == 1 ? MACT_MID : MACT_LO;
 #pragma unroll
     for (int tt = 0; tt < NT; tt++) {
-        const int tok = min(4 * tt + at, a.M - 1);
+        const int tok = P5 && ap == 3 ? 4 : min(4 * tt + at, a.M - 1);
         const uint8_t *blk = a.act + (int64_t)tok * a.act_stride + (int64_t)b * MACT_BLOCK + plane + 64 * kq;
 #pragma unroll
         for (int s2 = 0; s2 < 8; s2 += 2) {
@@ -553,6 +560,16 @@ __device__ inline void load_mafrag(const GemmArgs &a, int b, int l, MAFrag<NT> &
             f.xsum[tt][c] = su.x, f.xsum[tt][c + 1] = su.y, f.xsum[tt][c + 2] = su.z, f.xsum[tt][c + 3] = su.w;
         }
     }
+    if constexpr (P5) {
+        const uint8_t *eb = a.act + 4 * a.act_stride + (int64_t)b * MACT_BLOCK;
+#pragma unroll
+        for (int c = 0; c < 8; c += 4) {
+            const float4 sc = *(const float4 *)(eb + MACT_SCALE + 4 * c);
+            const float4 su = *(const float4 *)(eb + MACT_SUM + 4 * c);
+            f.xs4[c] = sc.x, f.xs4[c + 1] = sc.y, f.xs4[c + 2] = sc.z, f.xs4[c + 3] = sc.w;
+            f.xsum4[c] = su.x, f.xsum4[c + 1] = su.y, f.xsum4[c + 2] = su.z, f.xsum4[c + 3] = su.w;
+        }
+    }
 }
 
 template <int NW>
@@ -567,22 +584,33 @@ __device__ inline void load_mwfrag(const GemmArgs &a, int row, int kq, int b, MW
     }
 }
 
-template <int MODE, int NT, int RT>
+// TM: 1 (up to 4 tokens, one A tile), 2 (5-8 tokens, two tiles) or 5
+// (exactly 5 tokens in one tile: rows 4t + 3 carry the fifth token's planes,
+// one per lane group, so D lane group t holds the fifth token's plane t for
+// its row; each lane accumulates its plane's share of the fifth token,
+// weighted by 65536 / 256 / 1, and the four groups' shares are added once at
+// the end). A verify batch is the pending token and 4 drafts: 5 tokens.
+template <int MODE, int TM, int RT>
 __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
-    constexpr int NW = MODE == G_GLU ? 2 : 1;
-    __shared__ float red[3][RT][NW][NT][64];
+    constexpr int NW = MODE == G_GLU ? 2 : 1, NT = TM == 2 ? 2 : 1;
+    constexpr bool P5 = TM == 5;
+    constexpr int NA = NT + (P5 ? 1 : 0);  // accumulators per (row tile, matrix): tiles, then the fifth token
+    __shared__ float red[3][RT][NW][NA][64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l = threadIdx.x & 63, kq = l >> 4, rl = l & 15;
     const int r0 = blockIdx.x * 16 * RT;
     const int bpq = (a.nb + 3) / 4, b0 = wave * bpq, b1 = min(a.nb, b0 + bpq);
-    float acc[RT][NW][NT];
+    // P5: lane group kq's plane of the fifth token and its weight in X.
+    const float pw = kq == 0 ? 65536.f : kq == 1 ? 256.f : kq == 2 ? 1.f : 0.f;
+    const float mw = kq == 0 ? 1.f : 0.f;  // the min term once, in group 0
+    float acc[RT][NW][NA];
 #pragma unroll
     for (int r = 0; r < RT; r++)
 #pragma unroll
         for (int m = 0; m < NW; m++)
 #pragma unroll
-            for (int tt = 0; tt < NT; tt++) acc[r][m][tt] = 0.f;
-    auto compute = [&](const MWFrag<NW> &w, const MAFrag<NT> &x, int r) {
+            for (int tt = 0; tt < NA; tt++) acc[r][m][tt] = 0.f;
+    auto compute = [&](const MWFrag<NW> &w, const MAFrag<NT, P5> &x, int r) {
 #pragma unroll
         for (int m = 0; m < NW; m++) {
             const bool rin = r0 + 16 * r + rl < a.nrows;
@@ -614,15 +642,20 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
                     const int v = c[s8][tt][0] * 65536 + c[s8][tt][1] * 256 + c[s8][tt][2];
                     acc[r][m][tt] += dsc[s8] * x.xs[tt][s8] * (float)v - dm[s8] * x.xsum[tt][s8];
                 }
+            if constexpr (P5) {
+#pragma unroll
+                for (int s8 = 0; s8 < 8; s8++)
+                    acc[r][m][NT] += dsc[s8] * x.xs4[s8] * pw * (float)c[s8][0][3] - mw * dm[s8] * x.xsum4[s8];
+            }
         }
     };
     if (b0 < b1) {
-        MAFrag<NT> xA, xB;
+        MAFrag<NT, P5> xA, xB;
         MWFrag<NW> wA, wB;
         // In the order the loop requests them (weights, then activation), so
         // that the loop starts in the state its back edge brings.
         load_mwfrag<NW>(a, r0 + rl, kq, b0, wA);
-        load_mafrag<NT>(a, b0, l, xA);
+        load_mafrag<NT, P5>(a, b0, l, xA);
         // Items (block b, row tile r) in order through two weight buffers in
         // turn, the blocks' activation fragments through two more: an item
         // first requests the next item's weights (at a block's last tile also
@@ -631,7 +664,7 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
         // between a request and the arithmetic after it, so the compiler's
         // waits for this item leave the next one's loads in flight (a request
         // under a branch made it wait for everything, vmcnt(0)).
-        auto run_block = [&](auto par, int b, MAFrag<NT> &xc, MAFrag<NT> &xn) {
+        auto run_block = [&](auto par, int b, MAFrag<NT, P5> &xc, MAFrag<NT, P5> &xn) {
             constexpr int P = decltype(par)::value;
 #pragma unroll
             for (int r = 0; r < RT; r++) {
@@ -641,12 +674,12 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
                 // below the arithmetic (register pressure) and lose the overlap.
                 if ((P + r) & 1) {
                     load_mwfrag<NW>(a, r0 + 16 * nr + rl, kq, nb2, wA);
-                    if (last) load_mafrag<NT>(a, nb2, l, xn);
+                    if (last) load_mafrag<NT, P5>(a, nb2, l, xn);
                     TS5_GM_SB();
                     compute(wB, xc, r);
                 } else {
                     load_mwfrag<NW>(a, r0 + 16 * nr + rl, kq, nb2, wB);
-                    if (last) load_mafrag<NT>(a, nb2, l, xn);
+                    if (last) load_mafrag<NT, P5>(a, nb2, l, xn);
                     TS5_GM_SB();
                     compute(wA, xc, r);
                 }
@@ -665,7 +698,7 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
 #pragma unroll
             for (int m = 0; m < NW; m++)
 #pragma unroll
-                for (int tt = 0; tt < NT; tt++) red[wave - 1][r][m][tt][l] = acc[r][m][tt];
+                for (int tt = 0; tt < NA; tt++) red[wave - 1][r][m][tt][l] = acc[r][m][tt];
     }
     __syncthreads();
     if (wave != 0) return;
@@ -676,14 +709,19 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
 #pragma unroll
             for (int m = 0; m < NW; m++)
 #pragma unroll
-                for (int tt = 0; tt < NT; tt++) acc[r][m][tt] += red[q][r][m][tt][l];
+                for (int tt = 0; tt < NA; tt++) acc[r][m][tt] += red[q][r][m][tt][l];
+    if constexpr (P5)  // the four lane groups' shares of the fifth token, in every lane
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int m = 0; m < NW; m++) acc[r][m][NT] = add_xor32(add_xor16(acc[r][m][NT]));
 #pragma unroll
     for (int r = 0; r < RT; r++) {
         const int row = r0 + 16 * r + rl;
 #pragma unroll
-        for (int tt = 0; tt < NT; tt++) {
-            const int tok = 4 * tt + kq;
-            if (row >= a.nrows || tok >= a.M) continue;
+        for (int tt = 0; tt < NA; tt++) {
+            const int tok = tt == NT ? 4 : 4 * tt + kq;  // the fifth token: written by lane group 0
+            if (row >= a.nrows || tok >= a.M || (tt == NT && kq != 0)) continue;
             const int64_t o = (int64_t)tok * a.ldy + row;
             const float v = acc[r][0][tt];
             if (MODE == G_ADD) a.out[o] = a.y_in[o] + v;
@@ -693,12 +731,12 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
     }
 }
 
-template <int MODE, int NT>
+template <int MODE, int TM>
 static void launch_gemm_m_nt(const GemmArgs &a, int rt, hipStream_t s) {
     const unsigned grid = (unsigned)((a.nrows + 16 * rt - 1) / (16 * rt));
-    if (rt == 4) hipLaunchKernelGGL((k_gemm_m<MODE, NT, 4>), dim3(grid), dim3(256), 0, s, a);
-    else if (rt == 2) hipLaunchKernelGGL((k_gemm_m<MODE, NT, 2>), dim3(grid), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((k_gemm_m<MODE, NT, 1>), dim3(grid), dim3(256), 0, s, a);
+    if (rt == 4) hipLaunchKernelGGL((k_gemm_m<MODE, TM, 4>), dim3(grid), dim3(256), 0, s, a);
+    else if (rt == 2) hipLaunchKernelGGL((k_gemm_m<MODE, TM, 2>), dim3(grid), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_gemm_m<MODE, TM, 1>), dim3(grid), dim3(256), 0, s, a);
 }
 
 template <int MODE>
@@ -707,6 +745,7 @@ static hipError_t launch_gemm_m(const GemmArgs &a, hipStream_t s) {
     const int tiles = (a.nrows + 15) / 16;
     const int rt = tiles >= 4 * g_gemm_m_cu ? 4 : tiles >= 2 * g_gemm_m_cu ? 2 : 1;
     if (a.M <= 4) launch_gemm_m_nt<MODE, 1>(a, rt, s);
+    else if (a.M == 5 && TS5_GM_P5) launch_gemm_m_nt<MODE, 5>(a, rt, s);
     else launch_gemm_m_nt<MODE, 2>(a, rt, s);
     return hipGetLastError();
 }

@@ -276,6 +276,31 @@ def test_q4k_small_batch_matmul(ctx, M, ne0, rows, mode):
         assert rel_l2(got[k], want[k]) <= 2e-6, (k, rel_l2(got[k], want[k]))
 
 
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 6])
+@pytest.mark.parametrize("ne0,rows,mode", [(4096, 1000, "store"), (512, 515, "add"), (4096, 20000, "store")])
+def test_q6k_small_batch_matmul(ctx, M, ne0, rows, mode):
+    """The Q6_K matmul of 1-6 tokens (k_gemm_m up to 5 tokens with centred
+    quants and two MFMAs per 32 values, k_gemm_small past it): every token's
+    rows within 2e-6 relative L2 of the oracle; 20000 rows take the 4-tile
+    workgroups of the verify batch's head (a ragged last workgroup)."""
+    rng = np.random.default_rng(M * 1000 + rows)
+    W = synth.tensor(synth.Q6_K, ne0, rows, 23, f"q6sb{ne0}_{rows}")
+    x = rng.standard_normal((M, ne0)).astype(np.float32)
+    w = ctx.weight(synth.Q6_K, ne0, rows, W)
+    if mode == "add":
+        y0 = rng.standard_normal((M, rows)).astype(np.float32)
+        y = ctx.to_device(y0)
+        ctx.matmul(synth.Q6_K, w, ne0, rows, ctx.to_device(x), M, y, accumulate=True)
+        want = y0.astype(np.float64) + oracle.matmul(synth.Q6_K, W, ne0, x)
+    else:
+        y = ctx.alloc(M * rows * 4)
+        ctx.matmul(synth.Q6_K, w, ne0, rows, ctx.to_device(x), M, y)
+        want = oracle.matmul(synth.Q6_K, W, ne0, x)
+    got = y.download(np.float32, (M, rows))
+    for k in range(M):
+        assert rel_l2(got[k], want[k]) <= 2e-6, (k, rel_l2(got[k], want[k]))
+
+
 @pytest.mark.parametrize("t,ne0,rows", [(synth.Q4_K, 4096, 14336), (synth.Q8_0, 896, 4864), (synth.Q4_K, 512, 64)])
 def test_glu_vs_oracle(ctx, t, ne0, rows):
     Wg = synth.tensor(t, ne0, rows, 6, "gate")

@@ -518,20 +518,30 @@ __global__ __launch_bounds__(256) void k_gemm_small(GemmArgs a) {
 // walks the RT row tiles (weights one item ahead), so the activation is read
 // once per block and row group. The quarters meet in LDS in a fixed order.
 // ---------------------------------------------------------------------------
-template <int NT, bool P5>
+template <int FMT, int NT, bool P5>
 struct MAFrag {
+    static constexpr int NQ = FMT == F_Q6K ? NT : 1, NQ4 = FMT == F_Q6K && P5 ? 16 : 1;
     uint64_t p[NT][8];          // A: [token tile][sub-block] 8 bytes of plane (l%16)%4 of token (l%16)/4
     float xs[NT][8], xsum[NT][8];  // epilogue token l/16 of each tile: scale, sum per sub-block
     float xs4[P5 ? 8 : 1], xsum4[P5 ? 8 : 1];  // P5: the fifth token's scales and sums
+    int is[NQ][16], is4[NQ4];  // Q6_K: sum of X per 16 values (the -32 offset of its quants)
 };
+template <int FMT, int NW>
+struct MWFrag;
 template <int NW>
-struct MWFrag {
+struct MWFrag<F_Q4K, NW> {
     uint4 hdr[NW];
     uint64_t q[NW][4];  // B: the lane's k-group bytes of the 4 nibble groups of row l%16
 };
+template <int NW>
+struct MWFrag<F_Q6K, NW> {
+    uint64_t ql[NW][2][2], qh[NW][2];  // per half: ql bytes 8kq.. and 32 + 8kq.., qh bytes 8kq..
+    uint4 sc[NW];                      // the row's 16 int8 scales
+    float d[NW];
+};
 
-template <int NT, bool P5>
-__device__ inline void load_mafrag(const GemmArgs &a, int b, int l, MAFrag<NT, P5> &f) {
+template <int FMT, int NT, bool P5>
+__device__ inline void load_mafrag(const GemmArgs &a, int b, int l, MAFrag<FMT, NT, P5> &f) {
     const int kq = l >> 4, ar = l & 15, at = ar >> 2, ap = ar & 3, et = kq;
     // Row plane 3 of the A tile repeats the lo plane: its D row is computed
     // and never read (the combine takes planes 0-2), so the loaded values go
@@ -555,32 +565,60 @@ __device__ inline void load_mafrag(const GemmArgs &a, int b, int l, MAFrag<NT, P
 #pragma unroll
         for (int c = 0; c < 8; c += 4) {
             const float4 sc = *(const float4 *)(eb + MACT_SCALE + 4 * c);
-            const float4 su = *(const float4 *)(eb + MACT_SUM + 4 * c);
             f.xs[tt][c] = sc.x, f.xs[tt][c + 1] = sc.y, f.xs[tt][c + 2] = sc.z, f.xs[tt][c + 3] = sc.w;
-            f.xsum[tt][c] = su.x, f.xsum[tt][c + 1] = su.y, f.xsum[tt][c + 2] = su.z, f.xsum[tt][c + 3] = su.w;
+            if constexpr (FMT == F_Q4K) {
+                const float4 su = *(const float4 *)(eb + MACT_SUM + 4 * c);
+                f.xsum[tt][c] = su.x, f.xsum[tt][c + 1] = su.y, f.xsum[tt][c + 2] = su.z, f.xsum[tt][c + 3] = su.w;
+            }
         }
+        if constexpr (FMT == F_Q6K)
+#pragma unroll
+            for (int c = 0; c < 16; c += 4) {
+                const int4 v = *(const int4 *)(eb + MACT_ISUM + 4 * c);
+                f.is[tt][c] = v.x, f.is[tt][c + 1] = v.y, f.is[tt][c + 2] = v.z, f.is[tt][c + 3] = v.w;
+            }
     }
     if constexpr (P5) {
         const uint8_t *eb = a.act + 4 * a.act_stride + (int64_t)b * MACT_BLOCK;
 #pragma unroll
         for (int c = 0; c < 8; c += 4) {
             const float4 sc = *(const float4 *)(eb + MACT_SCALE + 4 * c);
-            const float4 su = *(const float4 *)(eb + MACT_SUM + 4 * c);
             f.xs4[c] = sc.x, f.xs4[c + 1] = sc.y, f.xs4[c + 2] = sc.z, f.xs4[c + 3] = sc.w;
-            f.xsum4[c] = su.x, f.xsum4[c + 1] = su.y, f.xsum4[c + 2] = su.z, f.xsum4[c + 3] = su.w;
+            if constexpr (FMT == F_Q4K) {
+                const float4 su = *(const float4 *)(eb + MACT_SUM + 4 * c);
+                f.xsum4[c] = su.x, f.xsum4[c + 1] = su.y, f.xsum4[c + 2] = su.z, f.xsum4[c + 3] = su.w;
+            }
         }
+        if constexpr (FMT == F_Q6K)
+#pragma unroll
+            for (int c = 0; c < 16; c += 4) {
+                const int4 v = *(const int4 *)(eb + MACT_ISUM + 4 * c);
+                f.is4[c] = v.x, f.is4[c + 1] = v.y, f.is4[c + 2] = v.z, f.is4[c + 3] = v.w;
+            }
     }
 }
 
-template <int NW>
-__device__ inline void load_mwfrag(const GemmArgs &a, int row, int kq, int b, MWFrag<NW> &w) {
+template <int FMT, int NW>
+__device__ inline void load_mwfrag(const GemmArgs &a, int row, int kq, int b, MWFrag<FMT, NW> &w) {
     const int64_t blk = (int64_t)min(row, a.nrows - 1) * a.nb + b;
 #pragma unroll
     for (int m = 0; m < NW; m++) {
-        const uint8_t *p = (m ? a.w2 : a.w) + blk * Q4K_BYTES;
-        w.hdr[m] = ld16(p);
+        if constexpr (FMT == F_Q4K) {
+            const uint8_t *p = (m ? a.w2 : a.w) + blk * Q4K_BYTES;
+            w.hdr[m] = ld16(p);
 #pragma unroll
-        for (int g = 0; g < 4; g++) w.q[m][g] = ld8(p + 16 + 32 * g + 8 * kq);
+            for (int g = 0; g < 4; g++) w.q[m][g] = ld8(p + 16 + 32 * g + 8 * kq);
+        } else {
+            const uint8_t *body = (m ? a.w2 : a.w) + blk * Q6K_BODY;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                w.ql[m][h][0] = ld8(body + 64 * h + 8 * kq);
+                w.ql[m][h][1] = ld8(body + 64 * h + 32 + 8 * kq);
+                w.qh[m][h] = ld8(body + 128 + 32 * h + 8 * kq);
+            }
+            w.sc[m] = ld16(body + 192);
+            w.d[m] = h2f((m ? a.s2 : a.s)[blk]);
+        }
     }
 }
 
@@ -590,10 +628,16 @@ __device__ inline void load_mwfrag(const GemmArgs &a, int row, int kq, int b, MW
 // its row; each lane accumulates its plane's share of the fifth token,
 // weighted by 65536 / 256 / 1, and the four groups' shares are added once at
 // the end). A verify batch is the pending token and 4 drafts: 5 tokens.
-template <int MODE, int TM, int RT>
+// Q6_K rows (FMT F_Q6K; one A tile: TM 1 or 5): the quants enter B centred,
+// q - 32 as int8 ((q | 0x80) - 0x20, then bit 7 flipped, per byte with no
+// borrow between bytes), and each 32-value chunk takes two MFMAs, B's values
+// 0-15 (lane groups 0-1) and 16-31 (groups 2-3) apart, for the two int8
+// scales of 16 values: y += d * sc * xs * sum (q - 32) X (quants.cpp:179-202).
+template <int FMT, int MODE, int TM, int RT>
 __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
     constexpr int NW = MODE == G_GLU ? 2 : 1, NT = TM == 2 ? 2 : 1;
     constexpr bool P5 = TM == 5;
+    static_assert(FMT == F_Q4K || NT == 1, "Q6_K rows: up to 5 tokens");
     constexpr int NA = NT + (P5 ? 1 : 0);  // accumulators per (row tile, matrix): tiles, then the fifth token
     __shared__ float red[3][RT][NW][NA][64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -610,7 +654,44 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
         for (int m = 0; m < NW; m++)
 #pragma unroll
             for (int tt = 0; tt < NA; tt++) acc[r][m][tt] = 0.f;
-    auto compute = [&](const MWFrag<NW> &w, const MAFrag<NT, P5> &x, int r) {
+    auto compute = [&](const MWFrag<FMT, NW> &w, const MAFrag<FMT, NT, P5> &x, int r) {
+      if constexpr (FMT == F_Q6K) {
+        constexpr uint64_t M0F = 0x0F0F0F0F0F0F0F0Full, M30 = 0x3030303030303030ull, M80 = 0x8080808080808080ull,
+                           M20 = 0x2020202020202020ull;
+        const uint64_t mlo = kq < 2 ? ~0ull : 0ull;  // lane groups 0-1 hold values 0-15 of a chunk
+#pragma unroll
+        for (int m = 0; m < NW; m++) {
+            const bool rin = r0 + 16 * r + rl < a.nrows;
+            const float d = rin ? w.d[m] : 0.f;
+            const uint32_t scw[4] = {w.sc[m].x, w.sc[m].y, w.sc[m].z, w.sc[m].w};
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint64_t qa = w.ql[m][h][0], qb = w.ql[m][h][1], qh = w.qh[m][h];
+                const uint64_t q[4] = {(qa & M0F) | ((qh << 4) & M30), (qb & M0F) | ((qh << 2) & M30),
+                                       ((qa >> 4) & M0F) | (qh & M30), ((qb >> 4) & M0F) | ((qh >> 2) & M30)};
+                v4i c[4][2];
+#pragma unroll
+                for (int cq = 0; cq < 4; cq++) {
+                    const uint64_t qc = ((q[cq] | M80) - M20) ^ M80;  // q - 32 per byte
+                    c[cq][0] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x.p[0][4 * h + cq], (long)(qc & mlo),
+                                                                     v4i{0, 0, 0, 0}, 0, 0, 0);
+                    c[cq][1] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x.p[0][4 * h + cq], (long)(qc & ~mlo),
+                                                                     v4i{0, 0, 0, 0}, 0, 0, 0);
+                }
+#pragma unroll
+                for (int cq = 0; cq < 4; cq++)
+#pragma unroll
+                    for (int g = 0; g < 2; g++) {
+                        const int si = 8 * h + 2 * cq + g;
+                        const float ds = d * (float)(int8_t)(scw[si >> 2] >> (8 * (si & 3)));
+                        // |65536 C_hi| <= 2^31 (exact in fp32), |256 C_mid + C_lo| <= 2^24 + 2^16.
+                        const float v = (float)c[cq][g][0] * 65536.f + (float)(c[cq][g][1] * 256 + c[cq][g][2]);
+                        acc[r][m][0] += ds * x.xs[0][4 * h + cq] * v;
+                        if constexpr (P5) acc[r][m][1] += ds * x.xs4[4 * h + cq] * pw * (float)c[cq][g][3];
+                    }
+            }
+        }
+      } else {
 #pragma unroll
         for (int m = 0; m < NW; m++) {
             const bool rin = r0 + 16 * r + rl < a.nrows;
@@ -648,14 +729,15 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
                     acc[r][m][NT] += dsc[s8] * x.xs4[s8] * pw * (float)c[s8][0][3] - mw * dm[s8] * x.xsum4[s8];
             }
         }
+      }
     };
     if (b0 < b1) {
-        MAFrag<NT, P5> xA, xB;
-        MWFrag<NW> wA, wB;
+        MAFrag<FMT, NT, P5> xA, xB;
+        MWFrag<FMT, NW> wA, wB;
         // In the order the loop requests them (weights, then activation), so
         // that the loop starts in the state its back edge brings.
-        load_mwfrag<NW>(a, r0 + rl, kq, b0, wA);
-        load_mafrag<NT, P5>(a, b0, l, xA);
+        load_mwfrag<FMT, NW>(a, r0 + rl, kq, b0, wA);
+        load_mafrag<FMT, NT, P5>(a, b0, l, xA);
         // Items (block b, row tile r) in order through two weight buffers in
         // turn, the blocks' activation fragments through two more: an item
         // first requests the next item's weights (at a block's last tile also
@@ -664,7 +746,7 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
         // between a request and the arithmetic after it, so the compiler's
         // waits for this item leave the next one's loads in flight (a request
         // under a branch made it wait for everything, vmcnt(0)).
-        auto run_block = [&](auto par, int b, MAFrag<NT, P5> &xc, MAFrag<NT, P5> &xn) {
+        auto run_block = [&](auto par, int b, MAFrag<FMT, NT, P5> &xc, MAFrag<FMT, NT, P5> &xn) {
             constexpr int P = decltype(par)::value;
 #pragma unroll
             for (int r = 0; r < RT; r++) {
@@ -673,13 +755,13 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
                 // sched_barrier: the scheduler would otherwise sink the requests
                 // below the arithmetic (register pressure) and lose the overlap.
                 if ((P + r) & 1) {
-                    load_mwfrag<NW>(a, r0 + 16 * nr + rl, kq, nb2, wA);
-                    if (last) load_mafrag<NT, P5>(a, nb2, l, xn);
+                    load_mwfrag<FMT, NW>(a, r0 + 16 * nr + rl, kq, nb2, wA);
+                    if (last) load_mafrag<FMT, NT, P5>(a, nb2, l, xn);
                     TS5_GM_SB();
                     compute(wB, xc, r);
                 } else {
-                    load_mwfrag<NW>(a, r0 + 16 * nr + rl, kq, nb2, wB);
-                    if (last) load_mafrag<NT, P5>(a, nb2, l, xn);
+                    load_mwfrag<FMT, NW>(a, r0 + 16 * nr + rl, kq, nb2, wB);
+                    if (last) load_mafrag<FMT, NT, P5>(a, nb2, l, xn);
                     TS5_GM_SB();
                     compute(wA, xc, r);
                 }
@@ -731,22 +813,30 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
     }
 }
 
-template <int MODE, int TM>
+template <int FMT, int MODE, int TM>
 static void launch_gemm_m_nt(const GemmArgs &a, int rt, hipStream_t s) {
     const unsigned grid = (unsigned)((a.nrows + 16 * rt - 1) / (16 * rt));
-    if (rt == 4) hipLaunchKernelGGL((k_gemm_m<MODE, TM, 4>), dim3(grid), dim3(256), 0, s, a);
-    else if (rt == 2) hipLaunchKernelGGL((k_gemm_m<MODE, TM, 2>), dim3(grid), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((k_gemm_m<MODE, TM, 1>), dim3(grid), dim3(256), 0, s, a);
+    if (rt == 4) hipLaunchKernelGGL((k_gemm_m<FMT, MODE, TM, 4>), dim3(grid), dim3(256), 0, s, a);
+    else if (rt == 2) hipLaunchKernelGGL((k_gemm_m<FMT, MODE, TM, 2>), dim3(grid), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_gemm_m<FMT, MODE, TM, 1>), dim3(grid), dim3(256), 0, s, a);
 }
 
-template <int MODE>
+// Q4_K: 1-8 tokens; Q6_K (not the fused gate/up): 1-5 tokens.
+template <int FMT, int MODE>
+static bool gemm_m_fits(int M) {
+    if constexpr (FMT == F_Q4K) return M <= 8;
+    else if constexpr (FMT == F_Q6K && MODE != G_GLU) return M <= 4 || (M == 5 && TS5_GM_P5);
+    else return false;
+}
+
+template <int FMT, int MODE>
 static hipError_t launch_gemm_m(const GemmArgs &a, hipStream_t s) {
     // Row tiles a workgroup: as many as keep about one workgroup a CU.
     const int tiles = (a.nrows + 15) / 16;
     const int rt = tiles >= 4 * g_gemm_m_cu ? 4 : tiles >= 2 * g_gemm_m_cu ? 2 : 1;
-    if (a.M <= 4) launch_gemm_m_nt<MODE, 1>(a, rt, s);
-    else if (a.M == 5 && TS5_GM_P5) launch_gemm_m_nt<MODE, 5>(a, rt, s);
-    else launch_gemm_m_nt<MODE, 2>(a, rt, s);
+    if (a.M <= 4) launch_gemm_m_nt<FMT, MODE, 1>(a, rt, s);
+    else if (a.M == 5 && TS5_GM_P5) launch_gemm_m_nt<FMT, MODE, 5>(a, rt, s);
+    else if constexpr (FMT == F_Q4K) launch_gemm_m_nt<FMT, MODE, 2>(a, rt, s);
     return hipGetLastError();
 }
 
@@ -826,15 +916,15 @@ static hipError_t launch_gemm_reduce(const float *part, int ks, int M, int nrows
 // k_gemm is built for Q6_K and Q8_0 only.
 template <int FMT, int MODE>
 static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
-    if constexpr (FMT == F_Q4K) {
-        // Up to 8 tokens on k_gemm_m (5 tokens: as fast as k_gemm_small; 1-4
-        // tokens ~20 % faster); 9-16 on k_gemm_small. TS5HIP_GEMM_M=0 keeps
-        // every batch on k_gemm_small, for comparison.
+    if constexpr (FMT == F_Q4K || (FMT == F_Q6K && MODE != G_GLU)) {
+        // Q4_K up to 8 tokens and Q6_K up to 5 (the verify batch's head) on
+        // k_gemm_m; the rest on k_gemm_small. TS5HIP_GEMM_M=0 keeps every
+        // batch on k_gemm_small, for comparison.
         static const bool use_m = [] {
             const char *e = getenv("TS5HIP_GEMM_M");
             return !(e && e[0] == '0');
         }();
-        if (a.M <= 8 && use_m) return launch_gemm_m<MODE>(a, s);
+        if (use_m && gemm_m_fits<FMT, MODE>(a.M)) return launch_gemm_m<FMT, MODE>(a, s);
     }
     if (a.M <= 16) {
         hipLaunchKernelGGL((k_gemm_small<FMT, MODE>), dim3((a.nrows + 15) / 16), dim3(256), 0, s, a);

@@ -262,6 +262,10 @@ static int matmul_any(ts5hip_ctx *ctx, uint32_t type, const void *w, const void 
     if (!ctx || !w || !x || !y || (mode == 2 && !w2)) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
     if (ntok < 1 || ntok > 4096) return fail(ctx, TS5HIP_ERR_ARG, "ntok %d outside 1..4096", ntok);
     if (int rc = check_matrix(ctx, type, ne0, ne1)) return rc;
+    if (gemm_fused_fits(type, ne0, ntok)) {
+        TS5_HIP(ctx, launch_gemm_fused(w, w2, ne0, ne1, x, ne0, norm_w, eps, ntok, mode, y, y, ne1, ctx->stream));
+        return TS5HIP_OK;
+    }
     const size_t act = align_up((size_t)ntok * gemm_act_bytes(type, ne0, ntok), 256);
     const size_t part = gemm_scratch_bytes(ne1, ntok, (int)(ne0 / block_values(type)));
     if (int rc = ensure_scratch(ctx, act + part)) return rc;

@@ -34,6 +34,15 @@
 #include "common.h"
 #include "kernels.h"
 
+#ifndef TS5_GM_WAVES
+#define TS5_GM_WAVES 4
+#endif
+#ifndef TS5_GM_RTMAX
+#define TS5_GM_RTMAX 4
+#endif
+#ifndef TS5_GM_FUSED
+#define TS5_GM_FUSED 1
+#endif
 #ifndef TS5_GM_P5
 #define TS5_GM_P5 1
 #endif
@@ -47,6 +56,7 @@
 #endif
 
 namespace ts5hip {
+constexpr int GM_WAVES = TS5_GM_WAVES;  // k_gemm_m's waves a workgroup, each a share of the row's blocks
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 static int g_gemm_m_cu = 256;  // CUs, for k_gemm_m's row tiles a workgroup
@@ -61,6 +71,11 @@ struct GemmArgs {
     float *out;               // ks == 1: y [M][ldy]; ks > 1: partials [ks][2][M][nrows]
     const float *y_in;        // MODE_ADD: residual [M][ldy] (may be out)
     int64_t ldy;
+    // k_gemm_m with its activation built in LDS (launch_gemm_fused): the fp32
+    // input [M][xin_stride], rms-normalised by norm_w (may be null) first.
+    const float *xin, *norm_w;
+    int64_t xin_stride;
+    float eps;
 };
 
 enum { G_STORE = 0, G_ADD = 1, G_GLU = 2 };
@@ -541,7 +556,16 @@ struct MWFrag<F_Q6K, NW> {
 };
 
 template <int FMT, int NT, bool P5>
+__device__ inline void load_mafrag_at(const uint8_t *act, int64_t act_stride, int M, int b, int l,
+                                      MAFrag<FMT, NT, P5> &f);
+template <int FMT, int NT, bool P5>
 __device__ inline void load_mafrag(const GemmArgs &a, int b, int l, MAFrag<FMT, NT, P5> &f) {
+    load_mafrag_at<FMT, NT, P5>(a.act, a.act_stride, a.M, b, l, f);
+}
+// The records of M tokens at act (global memory, or a workgroup's LDS copy).
+template <int FMT, int NT, bool P5>
+__device__ inline void load_mafrag_at(const uint8_t *act, int64_t act_stride, int M, int b, int l,
+                                      MAFrag<FMT, NT, P5> &f) {
     const int kq = l >> 4, ar = l & 15, at = ar >> 2, ap = ar & 3, et = kq;
     // Row plane 3 of the A tile repeats the lo plane: its D row is computed
     // and never read (the combine takes planes 0-2), so the loaded values go
@@ -552,16 +576,16 @@ __device__ inline void load_mafrag(const GemmArgs &a, int b, int l, MAFrag<FMT, 
     const int plane = plane_of == 0 ? 0 : plane_of == 1 ? MACT_MID : MACT_LO;
 #pragma unroll
     for (int tt = 0; tt < NT; tt++) {
-        const int tok = P5 && ap == 3 ? 4 : min(4 * tt + at, a.M - 1);
-        const uint8_t *blk = a.act + (int64_t)tok * a.act_stride + (int64_t)b * MACT_BLOCK + plane + 64 * kq;
+        const int tok = P5 && ap == 3 ? 4 : min(4 * tt + at, M - 1);
+        const uint8_t *blk = act + (int64_t)tok * act_stride + (int64_t)b * MACT_BLOCK + plane + 64 * kq;
 #pragma unroll
         for (int s2 = 0; s2 < 8; s2 += 2) {
             const uint4 v = ld16(blk + 8 * s2);
             f.p[tt][s2] = ((uint64_t)v.y << 32) | v.x;
             f.p[tt][s2 + 1] = ((uint64_t)v.w << 32) | v.z;
         }
-        const int etok = min(4 * tt + et, a.M - 1);
-        const uint8_t *eb = a.act + (int64_t)etok * a.act_stride + (int64_t)b * MACT_BLOCK;
+        const int etok = min(4 * tt + et, M - 1);
+        const uint8_t *eb = act + (int64_t)etok * act_stride + (int64_t)b * MACT_BLOCK;
 #pragma unroll
         for (int c = 0; c < 8; c += 4) {
             const float4 sc = *(const float4 *)(eb + MACT_SCALE + 4 * c);
@@ -579,7 +603,7 @@ __device__ inline void load_mafrag(const GemmArgs &a, int b, int l, MAFrag<FMT, 
             }
     }
     if constexpr (P5) {
-        const uint8_t *eb = a.act + 4 * a.act_stride + (int64_t)b * MACT_BLOCK;
+        const uint8_t *eb = act + 4 * act_stride + (int64_t)b * MACT_BLOCK;
 #pragma unroll
         for (int c = 0; c < 8; c += 4) {
             const float4 sc = *(const float4 *)(eb + MACT_SCALE + 4 * c);
@@ -633,17 +657,23 @@ __device__ inline void load_mwfrag(const GemmArgs &a, int row, int kq, int b, MW
 // borrow between bytes), and each 32-value chunk takes two MFMAs, B's values
 // 0-15 (lane groups 0-1) and 16-31 (groups 2-3) apart, for the two int8
 // scales of 16 values: y += d * sc * xs * sum (q - 32) X (quants.cpp:179-202).
-template <int FMT, int MODE, int TM, int RT>
-__global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
+//
+// XL (Q4_K, up to 5 tokens, n_in <= 4096): the workgroup builds the tokens'
+// activation records itself, in LDS, from the fp32 input (one 16-value run a
+// thread per token, rms-normalised first when norm_w is given), while its
+// first weights are in flight, instead of a separate quantization launch
+// writing them to HBM; the items then read their fragments from LDS.
+template <int FMT, int MODE, int TM, int RT, bool XL = false>
+__global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_m(GemmArgs a) {
     constexpr int NW = MODE == G_GLU ? 2 : 1, NT = TM == 2 ? 2 : 1;
     constexpr bool P5 = TM == 5;
     static_assert(FMT == F_Q4K || NT == 1, "Q6_K rows: up to 5 tokens");
     constexpr int NA = NT + (P5 ? 1 : 0);  // accumulators per (row tile, matrix): tiles, then the fifth token
-    __shared__ float red[3][RT][NW][NA][64];
+    __shared__ float red[GM_WAVES - 1][RT][NW][NA][64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l = threadIdx.x & 63, kq = l >> 4, rl = l & 15;
     const int r0 = blockIdx.x * 16 * RT;
-    const int bpq = (a.nb + 3) / 4, b0 = wave * bpq, b1 = min(a.nb, b0 + bpq);
+    const int bpq = (a.nb + GM_WAVES - 1) / GM_WAVES, b0 = wave * bpq, b1 = min(a.nb, b0 + bpq);
     // P5: lane group kq's plane of the fifth token and its weight in X.
     const float pw = kq == 0 ? 65536.f : kq == 1 ? 256.f : kq == 2 ? 1.f : 0.f;
     const float mw = kq == 0 ? 1.f : 0.f;  // the min term once, in group 0
@@ -731,7 +761,97 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
         }
       }
     };
-    if (b0 < b1) {
+    if constexpr (XL) {
+        static_assert(FMT == F_Q4K && NT == 1 && GM_WAVES == 4, "fused activation: Q4_K, up to 5 tokens");
+        extern __shared__ __align__(16) uint8_t lx[];  // [M][nb] activation records
+        __shared__ float ssr[5][GM_WAVES];
+        constexpr int MT = P5 ? 5 : 4;  // token slots read (past a.M: repeats, not used)
+        const int nr = a.n_in / 16, run = min((int)threadIdx.x, nr - 1);
+        const int64_t tstride = (int64_t)a.nb * MACT_BLOCK;
+        // The input runs first (loads return in order), then the first item's
+        // weights, all unconditional: rows, blocks and runs are clamped.
+        float4 xv[MT][4], nw[4];
+        const float *nwp = a.norm_w ? a.norm_w : a.xin;
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                xv[t][j] = *(const float4 *)(a.xin + (int64_t)min(t, a.M - 1) * a.xin_stride + 16 * run + 4 * j);
+#pragma unroll
+        for (int j = 0; j < 4; j++) nw[j] = *(const float4 *)(nwp + 16 * run + 4 * j);
+        MWFrag<FMT, NW> wA, wB;
+        load_mwfrag<FMT, NW>(a, r0 + rl, kq, min(b0, a.nb - 1), wA);
+        const bool mine = (int)threadIdx.x < nr;
+        float sc[MT];
+#pragma unroll
+        for (int t = 0; t < MT; t++) sc[t] = 1.f;
+        if (a.norm_w) {  // engine/src/cpu_backend.cpp:48-53, per token
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                float ss = 0.f;
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    ss += xv[t][j].x * xv[t][j].x + xv[t][j].y * xv[t][j].y + xv[t][j].z * xv[t][j].z +
+                          xv[t][j].w * xv[t][j].w;
+                ss = wave_sum_dpp(mine ? ss : 0.f);
+                if (l == 0) ssr[t][wave] = ss;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                float ss = 0.f;
+#pragma unroll
+                for (int w = 0; w < GM_WAVES; w++) ss += ssr[t][w];
+                sc[t] = 1.0f / sqrtf(ss / (float)a.n_in + a.eps);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            float v[16];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float4 f = xv[t][j], g = nw[j];
+                v[4 * j] = f.x, v[4 * j + 1] = f.y, v[4 * j + 2] = f.z, v[4 * j + 3] = f.w;
+                if (a.norm_w) {
+                    v[4 * j] = v[4 * j] * sc[t] * g.x, v[4 * j + 1] = v[4 * j + 1] * sc[t] * g.y;
+                    v[4 * j + 2] = v[4 * j + 2] * sc[t] * g.z, v[4 * j + 3] = v[4 * j + 3] * sc[t] * g.w;
+                }
+            }
+            // quant_run_m pairs adjacent lanes (runs 2g, 2g + 1): nr is a
+            // multiple of 16, so both or neither are `mine`.
+            if (t < a.M && mine) quant_run_m(v, run, lx + t * tstride);
+        }
+        __syncthreads();
+        wait_vmcnt<5 * NW>();  // the input loads are in: only the first item's weights may be open
+        // Items (block b, row tile r) through the two weight buffers in turn,
+        // each block's activation fragments read from LDS once.
+        auto run_block = [&](auto par, int b) {
+            constexpr int P = decltype(par)::value;
+            MAFrag<FMT, NT, P5> xc;
+            load_mafrag_at<FMT, NT, P5>(lx, tstride, a.M, b, l, xc);
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const bool last = r == RT - 1;
+                const int nb2 = last ? min(b + 1, b1 - 1) : b, nr2 = last ? 0 : r + 1;
+                if ((P + r) & 1) {
+                    load_mwfrag<FMT, NW>(a, r0 + 16 * nr2 + rl, kq, nb2, wA);
+                    TS5_GM_SB();
+                    compute(wB, xc, r);
+                } else {
+                    load_mwfrag<FMT, NW>(a, r0 + 16 * nr2 + rl, kq, nb2, wB);
+                    TS5_GM_SB();
+                    compute(wA, xc, r);
+                }
+            }
+        };
+        if (b0 < b1)
+            for (int b = b0;; b += 2) {
+                run_block(std::integral_constant<int, 0>{}, b);
+                if (b + 1 >= b1) break;
+                run_block(std::integral_constant<int, RT & 1>{}, b + 1);
+                if (b + 2 >= b1) break;
+            }
+    } else if (b0 < b1) {
         MAFrag<FMT, NT, P5> xA, xB;
         MWFrag<FMT, NW> wA, wB;
         // In the order the loop requests them (weights, then activation), so
@@ -785,7 +905,7 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
-    for (int q = 0; q < 3; q++)
+    for (int q = 0; q < GM_WAVES - 1; q++)
 #pragma unroll
         for (int r = 0; r < RT; r++)
 #pragma unroll
@@ -816,9 +936,44 @@ __global__ __launch_bounds__(256) void k_gemm_m(GemmArgs a) {
 template <int FMT, int MODE, int TM>
 static void launch_gemm_m_nt(const GemmArgs &a, int rt, hipStream_t s) {
     const unsigned grid = (unsigned)((a.nrows + 16 * rt - 1) / (16 * rt));
-    if (rt == 4) hipLaunchKernelGGL((k_gemm_m<FMT, MODE, TM, 4>), dim3(grid), dim3(256), 0, s, a);
-    else if (rt == 2) hipLaunchKernelGGL((k_gemm_m<FMT, MODE, TM, 2>), dim3(grid), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((k_gemm_m<FMT, MODE, TM, 1>), dim3(grid), dim3(256), 0, s, a);
+    if (rt == 4) hipLaunchKernelGGL((k_gemm_m<FMT, MODE, TM, 4>), dim3(grid), dim3(64 * GM_WAVES), 0, s, a);
+    else if (rt == 2) hipLaunchKernelGGL((k_gemm_m<FMT, MODE, TM, 2>), dim3(grid), dim3(64 * GM_WAVES), 0, s, a);
+    else hipLaunchKernelGGL((k_gemm_m<FMT, MODE, TM, 1>), dim3(grid), dim3(64 * GM_WAVES), 0, s, a);
+}
+
+template <int MODE, int TM>
+static void launch_gemm_fused_tm(const GemmArgs &a, int rt, size_t lds, hipStream_t s) {
+    const unsigned grid = (unsigned)((a.nrows + 16 * rt - 1) / (16 * rt));
+    if (rt == 4) hipLaunchKernelGGL((k_gemm_m<F_Q4K, MODE, TM, 4, true>), dim3(grid), dim3(256), lds, s, a);
+    else if (rt == 2) hipLaunchKernelGGL((k_gemm_m<F_Q4K, MODE, TM, 2, true>), dim3(grid), dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((k_gemm_m<F_Q4K, MODE, TM, 1, true>), dim3(grid), dim3(256), lds, s, a);
+}
+
+bool gemm_fused_fits(uint32_t t, int64_t ne0, int M) {
+    return TS5_GM_FUSED && t == T_Q4_K && ne0 % 256 == 0 && ne0 <= 4096 && M >= 1 && M <= 5;
+}
+
+hipError_t launch_gemm_fused(const void *w, const void *w2, int64_t ne0, int64_t ne1, const float *x,
+                             int64_t xstride, const float *norm_w, float eps, int M, int mode, float *y,
+                             const float *y_in, int64_t ldy, hipStream_t s) {
+    if (!gemm_fused_fits(T_Q4_K, ne0, M)) return hipErrorInvalidValue;
+    GemmArgs a{};
+    a.t = T_Q4_K, a.w = (const uint8_t *)w, a.w2 = (const uint8_t *)w2, a.nrows = (int)ne1;
+    a.nb = (int)(ne0 / 256), a.n_in = (int)ne0, a.M = M, a.ks = 1, a.out = y, a.y_in = y_in, a.ldy = ldy;
+    a.xin = x, a.xin_stride = xstride, a.norm_w = norm_w, a.eps = eps;
+    const size_t lds = (size_t)M * a.nb * MACT_BLOCK;
+    const int tiles = (a.nrows + 15) / 16;
+    int rt = tiles >= 4 * g_gemm_m_cu ? 4 : tiles >= 2 * g_gemm_m_cu ? 2 : 1;
+    if (TS5_GM_RTMAX < rt) rt = TS5_GM_RTMAX;
+    auto go = [&](auto mode_c) {
+        constexpr int MD = decltype(mode_c)::value;
+        if (M == 5) launch_gemm_fused_tm<MD, 5>(a, rt, lds, s);
+        else launch_gemm_fused_tm<MD, 1>(a, rt, lds, s);
+    };
+    if (mode == G_ADD) go(std::integral_constant<int, G_ADD>{});
+    else if (mode == G_GLU) go(std::integral_constant<int, G_GLU>{});
+    else go(std::integral_constant<int, G_STORE>{});
+    return hipGetLastError();
 }
 
 // Q4_K: 1-8 tokens; Q6_K (not the fused gate/up): 1-5 tokens.
@@ -833,7 +988,8 @@ template <int FMT, int MODE>
 static hipError_t launch_gemm_m(const GemmArgs &a, hipStream_t s) {
     // Row tiles a workgroup: as many as keep about one workgroup a CU.
     const int tiles = (a.nrows + 15) / 16;
-    const int rt = tiles >= 4 * g_gemm_m_cu ? 4 : tiles >= 2 * g_gemm_m_cu ? 2 : 1;
+    int rt = tiles >= 4 * g_gemm_m_cu ? 4 : tiles >= 2 * g_gemm_m_cu ? 2 : 1;
+    if (TS5_GM_RTMAX < rt) rt = TS5_GM_RTMAX;
     if (a.M <= 4) launch_gemm_m_nt<FMT, MODE, 1>(a, rt, s);
     else if (a.M == 5 && TS5_GM_P5) launch_gemm_m_nt<FMT, MODE, 5>(a, rt, s);
     else if constexpr (FMT == F_Q4K) launch_gemm_m_nt<FMT, MODE, 2>(a, rt, s);

@@ -37,6 +37,13 @@ hipError_t launch_gemm_wide(const void *w, const void *w2, int64_t ne0, int64_t 
 size_t gemm_scratch_bytes(int64_t rows, int M, int nb);
 hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, int64_t ne1, const void *act, int M,
                        int mode, float *y, const float *y_in, int64_t ldy, void *scratch, hipStream_t s);
+// Q4_K, 1-5 tokens, ne0 a multiple of 256 up to 4096: the matmul with the
+// activation built by each workgroup in LDS from the fp32 x [M][xstride]
+// (rms-normalised by norm_w first when given): no launch_gemm_act record.
+bool gemm_fused_fits(uint32_t t, int64_t ne0, int M);
+hipError_t launch_gemm_fused(const void *w, const void *w2, int64_t ne0, int64_t ne1, const float *x,
+                             int64_t xstride, const float *norm_w, float eps, int M, int mode, float *y,
+                             const float *y_in, int64_t ldy, hipStream_t s);
 
 // act.hip
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int ntok, float *y, hipStream_t s);

@@ -521,6 +521,10 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
     const float eps = hp.rms_eps;
     auto proj = [&](uint32_t t, const void *w, const void *w2, int64_t ne0, int64_t ne1, const float *x,
                     int64_t xstride, const float *norm, int ntok, int mode, float *y, int64_t ldy) -> int {
+        if (gemm_fused_fits(t, ne0, ntok)) {
+            TS5_HIP(ctx, launch_gemm_fused(w, w2, ne0, ne1, x, xstride, norm, eps, ntok, mode, y, y, ldy, s));
+            return TS5HIP_OK;
+        }
         TS5_HIP(ctx, launch_gemm_act(t, x, xstride, norm, eps, (int)ne0, ntok, m->bact, s));
         TS5_HIP(ctx, launch_gemm(t, w, w2, ne0, ne1, m->bact, ntok, mode, y, y, ldy, m->bgemm, s));
         return TS5HIP_OK;

@@ -255,65 +255,6 @@ __device__ inline float act_rms(const float *__restrict__ x, const float *__rest
     return 1.0f / sqrtf(ss / (float)n + eps);
 }
 
-// 16-run r of an activation (half r & 1 of sub-block r / 2) from its 16
-// values: the three planes' bytes, the run's sum of X, and the 32-value
-// chunk's scale and sum. Two threads per 32-value sub-block, in adjacent
-// lanes, exchange their max and sum once (both call this together).
-struct Run16 {
-    uint32_t pw[3][4];  // [plane hi, mid, lo][dword] of the 16 values
-    int isum;
-    float scale, sum;   // of the 32-value chunk (both threads of the pair)
-};
-__device__ inline Run16 quant16(const float (&v)[16]) {
-    Run16 q;
-    float amax = 0.f, sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        amax = fmaxf(amax, fabsf(v[i]));
-        sum += v[i];
-    }
-    amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
-    sum += __shfl_xor(sum, 1, WAVE);
-    const float inv = amax > 0.f ? (float)XQ_MAX / amax : 0.f;
-    int is = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        uint32_t w[3] = {0, 0, 0};
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int X = max(-XQ_MAX, min(XQ_MAX, (int)rintf(v[4 * k + e] * inv)));
-            int p[3];
-            xq_split(X, p[0], p[1], p[2]);
-#pragma unroll
-            for (int P = 0; P < 3; P++) w[P] |= (uint32_t)(p[P] & 255) << (8 * e);
-            is += X;
-        }
-#pragma unroll
-        for (int P = 0; P < 3; P++) q.pw[P][k] = w[P];
-    }
-    q.isum = is, q.scale = amax / (float)XQ_MAX, q.sum = sum;
-    return q;
-}
-// Run r into the matmul layout at `m` (the token's MAct): block r / 16, chunk
-// (r % 16) / 2, bytes 16 (r & 1) .. +15 of the chunk, i.e. k-groups
-// 2 (r & 1) and 2 (r & 1) + 1, in each plane.
-__device__ inline void quant_run_m(const float (&v)[16], int r, uint8_t *m) {
-    const Run16 q = quant16(v);
-    uint8_t *blk = m + (size_t)(r / 16) * MACT_BLOCK;
-    const int c = (r % 16) / 2, kq = 2 * (r & 1);
-    const int plane[3] = {0, MACT_MID, MACT_LO};
-#pragma unroll
-    for (int P = 0; P < 3; P++) {
-        *(uint2 *)(blk + plane[P] + kq * 64 + 8 * c) = make_uint2(q.pw[P][0], q.pw[P][1]);
-        *(uint2 *)(blk + plane[P] + (kq + 1) * 64 + 8 * c) = make_uint2(q.pw[P][2], q.pw[P][3]);
-    }
-    ((int *)(blk + MACT_ISUM))[r % 16] = q.isum;
-    if ((r & 1) == 0) {
-        ((float *)(blk + MACT_SCALE))[c] = q.scale;
-        ((float *)(blk + MACT_SUM))[c] = q.sum;
-    }
-}
-
 __device__ inline void quant_run(const float (&v)[16], int r, const Act &a) {
     const Run16 q = quant16(v);
     int8_t *plane[3] = {a.hi, a.mid, a.lo};

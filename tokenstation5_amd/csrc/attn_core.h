@@ -6,7 +6,12 @@
 #include "common.h"
 #include "kernels.h"
 
+#ifndef TS5_ATTN_KMIN
+#define TS5_ATTN_KMIN 128
+#endif
+
 namespace ts5hip {
+constexpr int ATTN_MIN_KEYS = TS5_ATTN_KMIN;
 
 // x0*c - x1*s and x0*s + x1*c with separate roundings, as the reference's
 // scalar float code computes them (engine/src/cpu_backend.cpp:63-64).
@@ -67,6 +72,7 @@ constexpr int ATTN_TILE = 64;
 // keys [0, nk) of query b (at position pq = nk - 1), in 64-key tiles.
 struct AttnSpan {
     int pq, p0, p1;
+    int used;           // splits that hold keys: the others (later ones) are empty
     int64_t head_base;  // cache slot of key 0 for this KV head
     bool has_new;       // the new key (pq) falls in this slice
 };
@@ -75,8 +81,13 @@ __device__ inline AttnSpan attn_span(const AttnArgs &a, int split, int kvh, int 
     AttnSpan sp;
     const int nk = a.kv_per_batch ? a.n_keys[b] : a.n_keys[0] + b + 1;
     sp.pq = nk - 1;
-    int chunk = (nk + n_split - 1) / n_split;
+    // At least ATTN_MIN_KEYS keys a split: a short cache (or a small model's
+    // few KV heads) leaves the later splits empty rather than merging many
+    // slivers; an empty split's work item returns at once, and the merge
+    // counts and reads the `used` ones only.
+    int chunk = max((nk + n_split - 1) / n_split, ATTN_MIN_KEYS);
     chunk = (chunk + TILE - 1) / TILE * TILE;
+    sp.used = (nk + chunk - 1) / chunk;
     sp.p0 = split * chunk;
     sp.p1 = min(nk, sp.p0 + chunk);
     const int seq = a.kv_per_batch ? b : 0;
@@ -275,6 +286,7 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
     const int ks_ = lane / LPK, dq = lane % LPK;  // key slot of a sweep, dim quarter
     const int d0 = DPL * dq;
     const AttnSpan sp = attn_span<16>(a, split, kvh, b, n_split);
+    if (split >= sp.used) return;  // an empty split: not counted, not merged
     const int nkeys = max(sp.p1 - sp.p0, 0);
     // The slice's K and V (and scales) as bounded buffers from key p0.
     const int8_t *kb = a.kv.k + (sp.head_base + sp.p0) * HD * VB, *vb = a.kv.v + (sp.head_base + sp.p0) * HD * VB;
@@ -515,16 +527,16 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
     }
     wait_stores();
     __syncthreads();
-    if (tid == 0) S.last = atomicAdd(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 1) == n_split - 1;
+    if (tid == 0) S.last = atomicAdd(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 1) == sp.used - 1;
     __syncthreads();
     if (!S.last) return;
-    // The merge: the n_split partials, read device-coherent (buffer loads with
+    // The merge: the used splits' partials, read device-coherent (buffer loads with
     // sc1), two values a thread, up to 32 splits' worth requested together
     // with the (m, l) that weigh them; a wave per head turns the (m, l) into
     // weights, a lane per split.
     const float *p_all = a.part + ((int64_t)b * n_split * a.HKV + kvh) * grp;
     const int64_t sstride = (int64_t)a.HKV * grp;  // floats between splits
-    const __amdgpu_buffer_rsrc_t rp = slice_rsrc(p_all, (uint32_t)((n_split - 1) * sstride + grp) * 4);
+    const __amdgpu_buffer_rsrc_t rp = slice_rsrc(p_all, (uint32_t)((sp.used - 1) * sstride + grp) * 4);
     constexpr int MB = 32;  // splits a batch
     constexpr int NQ2 = NOUT / 2, PER = (NQ2 + NT - 1) / NT;
     u32x2 v[PER][MB];
@@ -534,35 +546,35 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
             const int j2 = min(tid + NT * k, NQ2 - 1);
 #pragma unroll
             for (int i = 0; i < MB; i++) {
-                const int sl = min(s0 + i, n_split - 1);
+                const int sl = min(s0 + i, sp.used - 1);
                 v[k][i] = __builtin_amdgcn_raw_buffer_load_b64(rp, (uint32_t)((sl * sstride + 2 * j2) * 4), 0, 16);
             }
         }
     };
     fetch(0);
     for (int g = wave; g < G; g += NW) {
-        const int sl = min(lane, n_split - 1);
+        const int sl = min(lane, sp.used - 1);
         const auto ml = __builtin_amdgcn_raw_buffer_load_b64(rp, (uint32_t)((sl * sstride + NOUT + 2 * g) * 4), 0, 16);
         const float m0 = __uint_as_float(ml[0]), l0 = __uint_as_float(ml[1]);
-        const float mm = lane < n_split ? m0 : -INFINITY;
+        const float mm = lane < sp.used ? m0 : -INFINITY;
         const float M = wave_max_dpp(mm);
         const float w = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((mm - M) * LOG2E);
-        const float L = wave_sum_dpp(w * (lane < n_split ? l0 : 0.f));
-        S.wts[g][lane] = w;  // lanes past n_split: 0
+        const float L = wave_sum_dpp(w * (lane < sp.used ? l0 : 0.f));
+        S.wts[g][lane] = w;  // lanes past the used splits: 0
         if (lane == 0) S.red[g] = L;
     }
     __syncthreads();
     float2 acc[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) acc[k] = make_float2(0.f, 0.f);
-    for (int s0 = 0; s0 < n_split; s0 += MB) {
+    for (int s0 = 0; s0 < sp.used; s0 += MB) {
         if (s0) fetch(s0);
 #pragma unroll
         for (int k = 0; k < PER; k++) {
             const int g = (2 * min(tid + NT * k, NQ2 - 1)) / HD;
 #pragma unroll
             for (int i = 0; i < MB; i++) {
-                const float w = s0 + i < n_split ? S.wts[g][s0 + i] : 0.f;
+                const float w = s0 + i < sp.used ? S.wts[g][s0 + i] : 0.f;
                 acc[k].x += w * __uint_as_float(v[k][i][0]);
                 acc[k].y += w * __uint_as_float(v[k][i][1]);
             }

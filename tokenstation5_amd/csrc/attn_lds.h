@@ -87,6 +87,7 @@ __device__ inline void attn_slice_lds(const AttnArgs &a, int split, int kvh, int
     const int kk = tid >> 2, qq = tid & 3;              // scores: key kk of a sweep, quarter qq of the dims
     const int vk = lane / LPV, vc = lane % LPV;         // p * v: key vk of a wave's step, dims 8 vc ..
     const AttnSpan sp = attn_span<16>(a, split, kvh, b, n_split);
+    if (split >= sp.used) return;  // an empty split: not counted, not merged
     const int8_t *kb = a.kv.k + sp.head_base * HD * VB, *vb = a.kv.v + sp.head_base * HD * VB;
     const uint16_t *ksb = F16 ? nullptr : a.kv.ks + sp.head_base * (HD / 32);
     const uint16_t *vsb = F16 ? nullptr : a.kv.vs + sp.head_base * (HD / 32);
@@ -258,7 +259,7 @@ __device__ inline void attn_slice_lds(const AttnArgs &a, int split, int kvh, int
     }
     wait_stores();
     __syncthreads();
-    if (tid == 0) S.last = atomicAdd(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 1) == n_split - 1;
+    if (tid == 0) S.last = atomicAdd(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 1) == sp.used - 1;
     __syncthreads();
     if (!S.last) return;
     // The merge: this thread's outputs of every split (up to 32 at a time)
@@ -270,8 +271,8 @@ __device__ inline void attn_slice_lds(const AttnArgs &a, int split, int kvh, int
     float acc[OPT];
 #pragma unroll
     for (int k = 0; k < OPT; k++) acc[k] = 0.f;
-    for (int s0 = 0; s0 < n_split; s0 += MC) {
-        const int nc = min(MC, n_split - s0);
+    for (int s0 = 0; s0 < sp.used; s0 += MC) {
+        const int nc = min(MC, sp.used - s0);
         float ov[OPT][MC];
 #pragma unroll
         for (int k = 0; k < OPT; k++) {
@@ -281,14 +282,14 @@ __device__ inline void attn_slice_lds(const AttnArgs &a, int split, int kvh, int
         }
         if (s0 == 0) {
             for (int g = wave; g < G; g += NT / 64) {
-                const int sl = min(lane, n_split - 1);
+                const int sl = min(lane, sp.used - 1);
                 const float m0 = ld_dev(p_all + (int64_t)sl * sstride + g * rec + HD);
                 const float l0 = ld_dev(p_all + (int64_t)sl * sstride + g * rec + HD + 1);
-                const float m = lane < n_split ? m0 : -INFINITY;
+                const float m = lane < sp.used ? m0 : -INFINITY;
                 const float M = wave_max_dpp(m);
                 const float w = m == -INFINITY ? 0.f : expf(m - M);
-                const float L = wave_sum_dpp(w * (lane < n_split ? l0 : 0.f));
-                S.wts[g][lane] = w;  // lanes past n_split: 0
+                const float L = wave_sum_dpp(w * (lane < sp.used ? l0 : 0.f));
+                S.wts[g][lane] = w;  // lanes past the used splits: 0
                 if (lane == 0) S.red[g] = L;
             }
             __syncthreads();
@@ -298,7 +299,7 @@ __device__ inline void attn_slice_lds(const AttnArgs &a, int split, int kvh, int
             const int j = min(tid + NT * k, G * HD - 1), g = j / HD;
             float v = acc[k];
 #pragma unroll
-            for (int i4 = 0; i4 < MC / 4; i4++) {  // weights past n_split are 0 (their o: a valid split's)
+            for (int i4 = 0; i4 < MC / 4; i4++) {  // weights past the used splits are 0 (their o: a used split's)
                 const float4 w = *(const float4 *)&S.wts[g][s0 + 4 * i4];
                 v += w.x * ov[k][4 * i4] + w.y * ov[k][4 * i4 + 1] + w.z * ov[k][4 * i4 + 2] + w.w * ov[k][4 * i4 + 3];
             }

@@ -12,7 +12,7 @@ namespace ts5hip {
 // The arguments only some modes need, passed after the others.
 struct MvTail {
     uint32_t t;
-    int nb;
+    int nb, nfirst, n1;
     const float *y_in;
     float *best_v;
     int *best_i, *counter;
@@ -33,6 +33,7 @@ __global__ __launch_bounds__(WAVES *WAVE) void k_mv(const void *w, const void *w
     a.eps = eps, a.y = y, a.y_in = tail.y_in;
     a.best_v = tail.best_v, a.best_i = tail.best_i, a.counter = tail.counter, a.out = tail.out, a.seq = tail.seq;
     a.pos = tail.pos;
+    a.nfirst = tail.nfirst, a.n1 = tail.n1;
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[2 * WAVES];
     __shared__ int last;
@@ -95,6 +96,9 @@ __global__ __launch_bounds__(WAVES *WAVE) void k_mv(const void *w, const void *w
 // workgroups per CU, so large matrices loop over their groups with the next
 // step's weights in flight.
 // ---------------------------------------------------------------------------
+#ifndef TS5_MV_FIRST_SHARE
+#define TS5_MV_FIRST_SHARE 0.62
+#endif
 #ifndef TS5_MV_WG_PER_CU
 #define TS5_MV_WG_PER_CU 2
 #endif
@@ -130,7 +134,19 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
     const bool norm = a.norm_w != nullptr;
     const dim3 g(grid), b(WAVES * WAVE);
     const size_t lds = act_bytes(a.n_in);
-    const MvTail tail{a.t, a.nb, a.y_in, a.best_v, a.best_i, a.counter, a.out, a.seq, a.pos};
+    // A persistent grid of two workgroups a CU: the ones dispatched first
+    // (one a CU) run ahead of the second on the same CU (their waves are
+    // older), so they take a larger share of the groups and both halves end
+    // together (with equal shares the gate/up's second half ended 4 us after
+    // the first; at 62 % the halves end within 0.4 us: 17.0 -> 16.1 us, the
+    // Q6_K head 100.8 -> 97 us).
+    int nfirst = 0, n1 = 0;
+    if (per > 1 && grid > (unsigned)g_n_cu && TS5_MV_FIRST_SHARE > 0) {
+        nfirst = g_n_cu;
+        const int64_t want = (int64_t)(TS5_MV_FIRST_SHARE * (double)ngroups / nfirst + 0.5) * nfirst;
+        n1 = (int)std::min<int64_t>(std::max<int64_t>(want, nfirst), ngroups - ((int64_t)grid - nfirst));
+    }
+    const MvTail tail{a.t, a.nb, nfirst, n1, a.y_in, a.best_v, a.best_i, a.counter, a.out, a.seq, a.pos};
 #define TS5_MV_LAUNCH(RUNS, NORM)                                                                                 \
     hipLaunchKernelGGL((k_mv<F, R, WAVES, KS, MODE, RUNS, NORM>), g, b, lds, s, a.w, a.w2, a.x, a.norm_w, a.y,        \
                        (int)a.nrows, a.n_in, (int)grid, a.eps, tail)

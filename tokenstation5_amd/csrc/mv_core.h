@@ -387,6 +387,10 @@ struct MvArgs {
     float *best_v;
     int *best_i, *counter;
     int32_t *out, *seq, *pos;
+    // A persistent grid's groups: with n1 > 0, the first nfirst workgroups
+    // (dispatched first, one a CU) take groups [0, n1) in turn and the others
+    // [n1, ngroups); else workgroup wg takes wg, wg + nwg, ...
+    int nfirst, n1;
 };
 
 template <class F, int R>
@@ -441,7 +445,13 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
     // (the compiler would fetch each where first used: a round trip apiece).
     asm volatile("" ::"s"(a.w), "s"(a.w2), "s"(a.x), "s"(a.norm_w), "s"(a.y), "s"(a.nrows), "s"(a.nb), "s"(a.n_in),
                  "s"(a.eps), "s"(nwg));
-    int64_t g = wg;
+    // This workgroup's groups: gbeg, gbeg + gstr, ... below gend.
+    int64_t gbeg = wg, gstr = nwg, gend = ngroups;
+    if (a.n1 > 0) {
+        if (wg < a.nfirst) gstr = a.nfirst, gend = a.n1;
+        else gbeg = a.n1 + (wg - a.nfirst), gstr = nwg - a.nfirst;
+    }
+    int64_t g = gbeg;
     int it = 0;
     ActIn<NT, RUNS ? RUNS : 1, NORM> ain;
     if constexpr (RUNS > 0) act_in_load<NT, RUNS, NORM>(ain, a.x, a.norm_w, a.n_in);
@@ -452,7 +462,7 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
         load_rows<F, R>(w1, row0, a.nrows, a.nb, kb0 + i * BPI + bsub, kb1 - 1, sub, buf[0]);
         if (MODE == MV_GLU) load_rows<F, R>(w2, row0, a.nrows, a.nb, kb0 + i * BPI + bsub, kb1 - 1, sub, buf[NW - 1]);
     };
-    // Unconditional (rows are clamped; every launch has wg < ngroups), so no
+    // Unconditional (rows are clamped; every workgroup has gbeg < gend), so no
     // branch makes the compiler's waits for the activation cover these.
     // (Issuing the second step here as well, before the activation is built,
     // measured slower: the input's loads then return later.)
@@ -460,7 +470,7 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
     before_act();
     const Act xa = act_view(lds, a.n_in);
     if constexpr (RUNS > 0) act_in_build<NT, RUNS, NORM>(ain, a.eps, a.n_in, xa, red);
-    else if (g < ngroups) build_act<NT>(a.x, a.norm_w, a.eps, a.n_in, xa, red);
+    else if (g < gend) build_act<NT>(a.x, a.norm_w, a.eps, a.n_in, xa, red);
     const CAct x{xa.hi, xa.mid, xa.lo, xa.scale, xa.sum, xa.isum};
     // The input runs (older than the first step's weights) are all in; said
     // explicitly, so that the compiler's count does not carry those of
@@ -543,15 +553,15 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
     // the arithmetic made it wait for all of them, vmcnt(0), and a copy from
     // one buffer to the other waits for the copied loads.) Only the last step
     // is computed with nothing behind it.
-    const int64_t nsteps = (ngroups - wg + nwg - 1) / nwg * spg;
+    const int64_t nsteps = (gend - gbeg + gstr - 1) / gstr * spg;
     auto issue_next = [&](typename F::W (&buf)[NW][R]) {  // the step after (g, it)
         int64_t gn = g;
         int itn = it + 1;
-        if (itn == spg) itn = 0, gn = g + nwg;
+        if (itn == spg) itn = 0, gn = g + gstr;
         issue(gn, itn, buf);
     };
     auto advance = [&]() {
-        if (++it == spg) it = 0, g += nwg;
+        if (++it == spg) it = 0, g += gstr;
     };
     for (int64_t s = 0;; s += 2) {
         if (s + 1 >= nsteps) {

@@ -64,7 +64,8 @@ __host__ __device__ inline size_t device_bytes(uint32_t t, int64_t ne0, int64_t 
 //   scale[s] = max|x| / XQ_MAX, X = rint(x / scale[s]) in [-XQ_MAX, XQ_MAX]
 //   (XQ_MAX = 2^22 - 1: 23 significant bits, the precision of the fp32
 //   input itself), X = 65536 * hi + 256 * mid + lo with lo, mid in
-//   [-128, 127] and hi in [-64, 64] (xq_split),
+//   [-128, 127] and hi in [-64, 64] (the one base-256 expansion with such
+//   digits),
 //   sum[s] = sum of x over the sub-block (fp32, the unquantized values),
 // and per 16-value run r: isum[r] = sum of X over the run (exact, int32).
 // The three int8 planes feed v_dot4_i32_i8 directly against int8/uint4
@@ -241,16 +242,6 @@ __device__ inline float wave_max(float v) {
     return v;
 }
 
-// X (|X| <= XQ_MAX) as its three planes: X = 65536 hi + 256 mid + lo,
-// lo and mid in [-128, 127], hi in [-64, 64]; each plane is a byte of the
-// returned words' lanes when packed by the caller.
-__device__ inline void xq_split(int X, int &hi, int &mid, int &lo) {
-    lo = (int)(int8_t)(X & 255);
-    const int r = (X - lo) >> 8;  // exact: X - lo is a multiple of 256
-    mid = (int)(int8_t)(r & 255);
-    hi = (r - mid) >> 8;
-}
-
 // The 6-bit scale and min of sub-block j (0..7) of a K-quant block, from its
 // 12 packed bytes held as three little-endian dwords a (bytes 0-3),
 // b (4-7), c (8-11): sub-blocks 0-3 keep theirs in the low 6 bits of bytes j
@@ -358,21 +349,30 @@ __device__ inline Run16 quant16(const float (&v)[16]) {
     amax = fmaxf(amax, __shfl_xor(amax, 1, WAVE));
     sum += __shfl_xor(sum, 1, WAVE);
     const float inv = amax > 0.f ? (float)XQ_MAX / amax : 0.f;
+    // The planes as bytes: with Y = X + 128 (65536 + 256 + 1), bytes 0, 1, 2
+    // of Y are lo + 128, mid + 128 and hi + 128 (X = 65536 hi + 256 mid + lo
+    // is the one base-256 expansion with digits in [-128, 127]; 0 < Y < 2^24
+    // for |X| <= XQ_MAX), so byte permutes gather each plane of 4 values and
+    // one xor with 0x80 per byte turns the offsets back into signed digits.
+    constexpr int YOFF = 128 * (65536 + 256 + 1);
     int is = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        uint32_t w[3] = {0, 0, 0};
+        uint32_t y[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int X = max(-XQ_MAX, min(XQ_MAX, (int)rintf(v[4 * k + e] * inv)));
-            int p[3];
-            xq_split(X, p[0], p[1], p[2]);
-#pragma unroll
-            for (int P = 0; P < 3; P++) w[P] |= (uint32_t)(p[P] & 255) << (8 * e);
+            y[e] = (uint32_t)(X + YOFF);
             is += X;
         }
-#pragma unroll
-        for (int P = 0; P < 3; P++) q.pw[P][k] = w[P];
+        // t_lo: bytes 0, 1 of values 0 and 1 (or 2 and 3) interleaved, t_hi: byte 2 of each.
+        const uint32_t t01 = __builtin_amdgcn_perm(y[1], y[0], 0x05010400u);
+        const uint32_t t23 = __builtin_amdgcn_perm(y[3], y[2], 0x05010400u);
+        const uint32_t h01 = __builtin_amdgcn_perm(y[1], y[0], 0x0C0C0602u);
+        const uint32_t h23 = __builtin_amdgcn_perm(y[3], y[2], 0x0C0C0602u);
+        q.pw[2][k] = __builtin_amdgcn_perm(t23, t01, 0x05040100u) ^ 0x80808080u;  // lo
+        q.pw[1][k] = __builtin_amdgcn_perm(t23, t01, 0x07060302u) ^ 0x80808080u;  // mid
+        q.pw[0][k] = __builtin_amdgcn_perm(h23, h01, 0x05040100u) ^ 0x80808080u;  // hi
     }
     q.isum = is, q.scale = amax / (float)XQ_MAX, q.sum = sum;
     return q;

@@ -117,7 +117,7 @@ def test_matmul_prompt_chunk_vs_oracle(ctx, t, ne0, rows, ntok):
         assert rel_l2(got[i], want[i]) <= REL_L2, (i, rel_l2(got[i], want[i]))
 
 
-@pytest.mark.parametrize("t,ne0,rows", [(synth.Q4_K, 4096, 1536), (synth.Q8_0, 896, 4864)])
+@pytest.mark.parametrize("t,ne0,rows", [(synth.Q4_K, 4096, 1536), (synth.Q4_K, 4096, 14336), (synth.Q8_0, 896, 4864)])
 @pytest.mark.parametrize("ntok", [1, 5, 40, 256])
 def test_matmul_glu_vs_oracle(ctx, t, ne0, rows, ntok):
     """silu(Wg x') * (Wu x') per token (engine/src/cpu_backend.cpp:253-261)."""

@@ -43,6 +43,9 @@
 #ifndef TS5_GM_FUSED
 #define TS5_GM_FUSED 1
 #endif
+#ifndef TS5_GM_MX
+#define TS5_GM_MX 1
+#endif
 #ifndef TS5_GM_P5
 #define TS5_GM_P5 1
 #endif
@@ -646,6 +649,105 @@ __device__ inline void load_mwfrag(const GemmArgs &a, int row, int kq, int b, MW
     }
 }
 
+// P5: lane group kq holds plane kq of the fifth token; its scales are taken
+// times that plane's weight in X (65536, 256, 1; 0 for the unused fourth),
+// and its sums times 1 in group 0 only (the min term once), once per block
+// rather than per item: the weights are powers of two or 0 and 1, so the
+// products are exact and the results those of applying them per item.
+template <int FMT, int NT, bool P5>
+__device__ inline void gm_prescale(MAFrag<FMT, NT, P5> &x, int kq) {
+    if constexpr (P5) {
+        const float pw = kq == 0 ? 65536.f : kq == 1 ? 256.f : kq == 2 ? 1.f : 0.f;
+        const float mw = kq == 0 ? 1.f : 0.f;
+#pragma unroll
+        for (int s8 = 0; s8 < 8; s8++) {
+            x.xs4[s8] *= pw;
+            if constexpr (FMT == F_Q4K) x.xsum4[s8] *= mw;
+        }
+    }
+}
+
+// One item of k_gemm_m / k_gemm_mx: block b of a row tile of 16 rows, the
+// lane's row (rin: the row exists) and token planes; every MFMA of the
+// item, then the scaling into acc (per matrix, per token tile).
+template <int FMT, int NW, int NT, bool P5, int NA>
+__device__ inline void gm_item(const MWFrag<FMT, NW> &w, const MAFrag<FMT, NT, P5> &x, float (&acc)[NW][NA], bool rin,
+                               int kq) {
+    if constexpr (FMT == F_Q6K) {
+        constexpr uint64_t M0F = 0x0F0F0F0F0F0F0F0Full, M30 = 0x3030303030303030ull, M80 = 0x8080808080808080ull,
+                           M20 = 0x2020202020202020ull;
+        const uint64_t mlo = kq < 2 ? ~0ull : 0ull;  // lane groups 0-1 hold values 0-15 of a chunk
+#pragma unroll
+        for (int m = 0; m < NW; m++) {
+            const float d = rin ? w.d[m] : 0.f;
+            const uint32_t scw[4] = {w.sc[m].x, w.sc[m].y, w.sc[m].z, w.sc[m].w};
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint64_t qa = w.ql[m][h][0], qb = w.ql[m][h][1], qh = w.qh[m][h];
+                const uint64_t q[4] = {(qa & M0F) | ((qh << 4) & M30), (qb & M0F) | ((qh << 2) & M30),
+                                       ((qa >> 4) & M0F) | (qh & M30), ((qb >> 4) & M0F) | ((qh >> 2) & M30)};
+                v4i c[4][2];
+#pragma unroll
+                for (int cq = 0; cq < 4; cq++) {
+                    const uint64_t qc = ((q[cq] | M80) - M20) ^ M80;  // q - 32 per byte
+                    c[cq][0] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x.p[0][4 * h + cq], (long)(qc & mlo),
+                                                                     v4i{0, 0, 0, 0}, 0, 0, 0);
+                    c[cq][1] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x.p[0][4 * h + cq], (long)(qc & ~mlo),
+                                                                     v4i{0, 0, 0, 0}, 0, 0, 0);
+                }
+#pragma unroll
+                for (int cq = 0; cq < 4; cq++)
+#pragma unroll
+                    for (int g = 0; g < 2; g++) {
+                        const int si = 8 * h + 2 * cq + g;
+                        const float ds = d * (float)(int8_t)(scw[si >> 2] >> (8 * (si & 3)));
+                        // |65536 C_hi| <= 2^31 (exact in fp32), |256 C_mid + C_lo| <= 2^24 + 2^16.
+                        const float v = (float)c[cq][g][0] * 65536.f + (float)(c[cq][g][1] * 256 + c[cq][g][2]);
+                        acc[m][0] += ds * x.xs[0][4 * h + cq] * v;
+                        if constexpr (P5) acc[m][1] += ds * x.xs4[4 * h + cq] * (float)c[cq][g][3];
+                    }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < NW; m++) {
+            const float d = rin ? h2f(w.hdr[m].x & 0xffff) : 0.f, dmin = rin ? h2f(w.hdr[m].x >> 16) : 0.f;
+            float dsc[8], dm[8];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                int sc0, m0, sc1, m1;
+                kq_scale_min_pair(g, w.hdr[m].y, w.hdr[m].z, w.hdr[m].w, sc0, m0, sc1, m1);
+                dsc[2 * g] = d * (float)sc0, dm[2 * g] = dmin * (float)m0;
+                dsc[2 * g + 1] = d * (float)sc1, dm[2 * g + 1] = dmin * (float)m1;
+            }
+            // Every MFMA of the item first, the scaling after: the results are
+            // not waited for one at a time.
+            v4i c[8][NT];
+#pragma unroll
+            for (int s8 = 0; s8 < 8; s8++) {
+                const uint64_t qb = (s8 & 1) ? (w.q[m][s8 >> 1] >> 4) & 0x0F0F0F0F0F0F0F0Full
+                                             : w.q[m][s8 >> 1] & 0x0F0F0F0F0F0F0F0Full;
+#pragma unroll
+                for (int tt = 0; tt < NT; tt++)
+                    c[s8][tt] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x.p[tt][s8], (long)qb, v4i{0, 0, 0, 0}, 0, 0, 0);
+            }
+#pragma unroll
+            for (int s8 = 0; s8 < 8; s8++)
+#pragma unroll
+                for (int tt = 0; tt < NT; tt++) {
+                    // Exact in int32 for 4-bit quants: |.| <= 32 * 15 * (64 * 65536 + 128 * 257) < 2^31.
+                    const int v = c[s8][tt][0] * 65536 + c[s8][tt][1] * 256 + c[s8][tt][2];
+                    acc[m][tt] += dsc[s8] * x.xs[tt][s8] * (float)v - dm[s8] * x.xsum[tt][s8];
+                }
+            if constexpr (P5) {
+#pragma unroll
+                for (int s8 = 0; s8 < 8; s8++)
+                    acc[m][NT] += dsc[s8] * x.xs4[s8] * (float)c[s8][0][3] - dm[s8] * x.xsum4[s8];
+            }
+        }
+    }
+}
+
 // TM: 1 (up to 4 tokens, one A tile), 2 (5-8 tokens, two tiles) or 5
 // (exactly 5 tokens in one tile: rows 4t + 3 carry the fifth token's planes,
 // one per lane group, so D lane group t holds the fifth token's plane t for
@@ -674,9 +776,6 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_m(GemmArgs a) {
     const int l = threadIdx.x & 63, kq = l >> 4, rl = l & 15;
     const int r0 = blockIdx.x * 16 * RT;
     const int bpq = (a.nb + GM_WAVES - 1) / GM_WAVES, b0 = wave * bpq, b1 = min(a.nb, b0 + bpq);
-    // P5: lane group kq's plane of the fifth token and its weight in X.
-    const float pw = kq == 0 ? 65536.f : kq == 1 ? 256.f : kq == 2 ? 1.f : 0.f;
-    const float mw = kq == 0 ? 1.f : 0.f;  // the min term once, in group 0
     float acc[RT][NW][NA];
 #pragma unroll
     for (int r = 0; r < RT; r++)
@@ -685,82 +784,9 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_m(GemmArgs a) {
 #pragma unroll
             for (int tt = 0; tt < NA; tt++) acc[r][m][tt] = 0.f;
     auto compute = [&](const MWFrag<FMT, NW> &w, const MAFrag<FMT, NT, P5> &x, int r) {
-      if constexpr (FMT == F_Q6K) {
-        constexpr uint64_t M0F = 0x0F0F0F0F0F0F0F0Full, M30 = 0x3030303030303030ull, M80 = 0x8080808080808080ull,
-                           M20 = 0x2020202020202020ull;
-        const uint64_t mlo = kq < 2 ? ~0ull : 0ull;  // lane groups 0-1 hold values 0-15 of a chunk
-#pragma unroll
-        for (int m = 0; m < NW; m++) {
-            const bool rin = r0 + 16 * r + rl < a.nrows;
-            const float d = rin ? w.d[m] : 0.f;
-            const uint32_t scw[4] = {w.sc[m].x, w.sc[m].y, w.sc[m].z, w.sc[m].w};
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const uint64_t qa = w.ql[m][h][0], qb = w.ql[m][h][1], qh = w.qh[m][h];
-                const uint64_t q[4] = {(qa & M0F) | ((qh << 4) & M30), (qb & M0F) | ((qh << 2) & M30),
-                                       ((qa >> 4) & M0F) | (qh & M30), ((qb >> 4) & M0F) | ((qh >> 2) & M30)};
-                v4i c[4][2];
-#pragma unroll
-                for (int cq = 0; cq < 4; cq++) {
-                    const uint64_t qc = ((q[cq] | M80) - M20) ^ M80;  // q - 32 per byte
-                    c[cq][0] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x.p[0][4 * h + cq], (long)(qc & mlo),
-                                                                     v4i{0, 0, 0, 0}, 0, 0, 0);
-                    c[cq][1] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x.p[0][4 * h + cq], (long)(qc & ~mlo),
-                                                                     v4i{0, 0, 0, 0}, 0, 0, 0);
-                }
-#pragma unroll
-                for (int cq = 0; cq < 4; cq++)
-#pragma unroll
-                    for (int g = 0; g < 2; g++) {
-                        const int si = 8 * h + 2 * cq + g;
-                        const float ds = d * (float)(int8_t)(scw[si >> 2] >> (8 * (si & 3)));
-                        // |65536 C_hi| <= 2^31 (exact in fp32), |256 C_mid + C_lo| <= 2^24 + 2^16.
-                        const float v = (float)c[cq][g][0] * 65536.f + (float)(c[cq][g][1] * 256 + c[cq][g][2]);
-                        acc[r][m][0] += ds * x.xs[0][4 * h + cq] * v;
-                        if constexpr (P5) acc[r][m][1] += ds * x.xs4[4 * h + cq] * pw * (float)c[cq][g][3];
-                    }
-            }
-        }
-      } else {
-#pragma unroll
-        for (int m = 0; m < NW; m++) {
-            const bool rin = r0 + 16 * r + rl < a.nrows;
-            const float d = rin ? h2f(w.hdr[m].x & 0xffff) : 0.f, dmin = rin ? h2f(w.hdr[m].x >> 16) : 0.f;
-            float dsc[8], dm[8];
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                int sc0, m0, sc1, m1;
-                kq_scale_min_pair(g, w.hdr[m].y, w.hdr[m].z, w.hdr[m].w, sc0, m0, sc1, m1);
-                dsc[2 * g] = d * (float)sc0, dm[2 * g] = dmin * (float)m0;
-                dsc[2 * g + 1] = d * (float)sc1, dm[2 * g + 1] = dmin * (float)m1;
-            }
-            // Every MFMA of the item first, the scaling after: the results are
-            // not waited for one at a time.
-            v4i c[8][NT];
-#pragma unroll
-            for (int s8 = 0; s8 < 8; s8++) {
-                const uint64_t qb = (s8 & 1) ? (w.q[m][s8 >> 1] >> 4) & 0x0F0F0F0F0F0F0F0Full
-                                             : w.q[m][s8 >> 1] & 0x0F0F0F0F0F0F0F0Full;
-#pragma unroll
-                for (int tt = 0; tt < NT; tt++)
-                    c[s8][tt] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x.p[tt][s8], (long)qb, v4i{0, 0, 0, 0}, 0, 0, 0);
-            }
-#pragma unroll
-            for (int s8 = 0; s8 < 8; s8++)
-#pragma unroll
-                for (int tt = 0; tt < NT; tt++) {
-                    // Exact in int32 for 4-bit quants: |.| <= 32 * 15 * (64 * 65536 + 128 * 257) < 2^31.
-                    const int v = c[s8][tt][0] * 65536 + c[s8][tt][1] * 256 + c[s8][tt][2];
-                    acc[r][m][tt] += dsc[s8] * x.xs[tt][s8] * (float)v - dm[s8] * x.xsum[tt][s8];
-                }
-            if constexpr (P5) {
-#pragma unroll
-                for (int s8 = 0; s8 < 8; s8++)
-                    acc[r][m][NT] += dsc[s8] * x.xs4[s8] * pw * (float)c[s8][0][3] - mw * dm[s8] * x.xsum4[s8];
-            }
-        }
-      }
+        gm_item<FMT, NW, NT, P5, NA>(w, x, acc[r], r0 + 16 * r + rl < a.nrows, kq);
     };
+    auto prescale = [&](MAFrag<FMT, NT, P5> &x) { gm_prescale<FMT, NT, P5>(x, kq); };
     if constexpr (XL) {
         static_assert(FMT == F_Q4K && NT == 1 && GM_WAVES == 4, "fused activation: Q4_K, up to 5 tokens");
         extern __shared__ __align__(16) uint8_t lx[];  // [M][nb] activation records
@@ -829,6 +855,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_m(GemmArgs a) {
             constexpr int P = decltype(par)::value;
             MAFrag<FMT, NT, P5> xc;
             load_mafrag_at<FMT, NT, P5>(lx, tstride, a.M, b, l, xc);
+            prescale(xc);
 #pragma unroll
             for (int r = 0; r < RT; r++) {
                 const bool last = r == RT - 1;
@@ -878,11 +905,13 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_m(GemmArgs a) {
                     load_mwfrag<FMT, NW>(a, r0 + 16 * nr + rl, kq, nb2, wA);
                     if (last) load_mafrag<FMT, NT, P5>(a, nb2, l, xn);
                     TS5_GM_SB();
+                    if (r == 0) prescale(xc);
                     compute(wB, xc, r);
                 } else {
                     load_mwfrag<FMT, NW>(a, r0 + 16 * nr + rl, kq, nb2, wB);
                     if (last) load_mafrag<FMT, NT, P5>(a, nb2, l, xn);
                     TS5_GM_SB();
+                    if (r == 0) prescale(xc);
                     compute(wA, xc, r);
                 }
             }
@@ -941,6 +970,178 @@ static void launch_gemm_m_nt(const GemmArgs &a, int rt, hipStream_t s) {
     else hipLaunchKernelGGL((k_gemm_m<FMT, MODE, TM, 1>), dim3(grid), dim3(64 * GM_WAVES), 0, s, a);
 }
 
+// ---------------------------------------------------------------------------
+// The fused small-batch matmul (Q4_K, 1-5 tokens, inputs up to 4096 wide:
+// launch_gemm_fused) as one workgroup of 8 waves a CU. The workgroup builds
+// the tokens' activation records in LDS once, from the fp32 input (norm
+// fused), its threads in two halves of 256 with a token's 16-value runs to
+// one half, and then takes RT row tiles of 16 rows, gridDim.x tiles apart
+// (tile blockIdx.x + r * gridDim.x; past the last tile its loads repeat the
+// last row and add nothing), each wave an eighth of every tile's blocks, the
+// weights one item ahead. The waves' sums then meet in LDS and each thread
+// finishes one (row tile, token tile, lane) entry, adding the waves in
+// order. Against one workgroup of 4 waves per row tile (k_gemm_m's XL path)
+// the activation is built once a CU, not once a tile, and never by two
+// workgroups sharing a CU's SIMDs: that build is the VALU work the kernel
+// repeats most.
+// ---------------------------------------------------------------------------
+constexpr int GX_WAVES = 8;
+
+template <int MODE, int TM, int RT>
+__global__ __launch_bounds__(64 * GX_WAVES) void k_gemm_mx(GemmArgs a) {
+    constexpr int FMT = F_Q4K, NW = MODE == G_GLU ? 2 : 1, NT = 1;
+    constexpr bool P5 = TM == 5;
+    static_assert(TM == 1 || TM == 5, "fused small-batch matmul: up to 5 tokens");
+    constexpr int NA = NT + (P5 ? 1 : 0);
+    constexpr int MT = P5 ? 5 : 4;      // token slots read (past a.M: repeats, not used)
+    constexpr int TH = (MT + 1) / 2;    // token slots of a half of the threads (the second half: MT - TH)
+    extern __shared__ __align__(16) uint8_t lx[];  // [M][nb] activation records, then the waves' sums
+    __shared__ float ssr[MT][4];
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l = tid & 63, kq = l >> 4, rl = l & 15;
+    const int bpq = (a.nb + GX_WAVES - 1) / GX_WAVES, b0 = wave * bpq, b1 = min(a.nb, b0 + bpq);
+    const int64_t tstride = (int64_t)a.nb * MACT_BLOCK;
+    auto rowbase = [&](int r) { return (int)(blockIdx.x + (unsigned)r * gridDim.x) * 16; };
+    // The input runs first (loads return in order), then the first item's
+    // weights, all unconditional: tokens, rows, blocks and runs are clamped.
+    const int half = wave >> 2, tb = half ? TH : 0, tn = half ? MT - TH : TH;
+    const int nr = a.n_in / 16, run0 = tid & 255, run = min(run0, nr - 1);
+    const bool mine = run0 < nr;
+    float4 xv[TH][4], nw[4];
+    const float *nwp = a.norm_w ? a.norm_w : a.xin;
+#pragma unroll
+    for (int j = 0; j < TH; j++)
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            xv[j][q] = *(const float4 *)(a.xin + (int64_t)min(tb + j, a.M - 1) * a.xin_stride + 16 * run + 4 * q);
+#pragma unroll
+    for (int q = 0; q < 4; q++) nw[q] = *(const float4 *)(nwp + 16 * run + 4 * q);
+    TS5_GM_SB();  // the weights after the input: the scheduler would otherwise put them between
+    MWFrag<FMT, NW> wA, wB;
+    load_mwfrag<FMT, NW>(a, rowbase(0) + rl, kq, min(b0, a.nb - 1), wA);
+    float sc[TH];
+#pragma unroll
+    for (int j = 0; j < TH; j++) sc[j] = 1.f;
+    if (a.norm_w) {  // engine/src/cpu_backend.cpp:48-53, per token; the 4 waves of a half in order
+#pragma unroll
+        for (int j = 0; j < TH; j++) {
+            float ss = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                ss += xv[j][q].x * xv[j][q].x + xv[j][q].y * xv[j][q].y + xv[j][q].z * xv[j][q].z +
+                      xv[j][q].w * xv[j][q].w;
+            ss = wave_sum_dpp(mine ? ss : 0.f);
+            if (l == 0 && j < tn) ssr[tb + j][wave & 3] = ss;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < TH; j++) {
+            const int t = min(tb + j, MT - 1);
+            float ss = 0.f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) ss += ssr[t][w];
+            sc[j] = 1.0f / sqrtf(ss / (float)a.n_in + a.eps);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < TH; j++) {
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 f = xv[j][q], g = nw[q];
+            v[4 * q] = f.x, v[4 * q + 1] = f.y, v[4 * q + 2] = f.z, v[4 * q + 3] = f.w;
+            if (a.norm_w) {
+                v[4 * q] = v[4 * q] * sc[j] * g.x, v[4 * q + 1] = v[4 * q + 1] * sc[j] * g.y;
+                v[4 * q + 2] = v[4 * q + 2] * sc[j] * g.z, v[4 * q + 3] = v[4 * q + 3] * sc[j] * g.w;
+            }
+        }
+        // quant_run_m pairs adjacent lanes (runs 2g, 2g + 1): nr is a
+        // multiple of 16, so both or neither are `mine`.
+        if (j < tn && tb + j < a.M && mine) quant_run_m(v, run, lx + (tb + j) * tstride);
+    }
+    __syncthreads();
+    wait_vmcnt<5 * NW>();  // the input loads are in: only the first item's weights may be open
+    float acc[RT][NW][NA];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int m = 0; m < NW; m++)
+#pragma unroll
+            for (int tt = 0; tt < NA; tt++) acc[r][m][tt] = 0.f;
+    // Items (block b, row tile r) through the two weight buffers in turn,
+    // each block's activation fragments read from LDS once.
+    auto run_block = [&](auto par, int b) {
+        constexpr int P = decltype(par)::value;
+        MAFrag<FMT, NT, P5> xc;
+        load_mafrag_at<FMT, NT, P5>(lx, tstride, a.M, b, l, xc);
+        gm_prescale<FMT, NT, P5>(xc, kq);
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const bool last = r == RT - 1;
+            const int nb2 = last ? min(b + 1, b1 - 1) : b, nrow = rowbase(last ? 0 : r + 1) + rl;
+            const bool rin = rowbase(r) + rl < a.nrows;
+            if ((P + r) & 1) {
+                load_mwfrag<FMT, NW>(a, nrow, kq, nb2, wA);
+                TS5_GM_SB();
+                gm_item<FMT, NW, NT, P5, NA>(wB, xc, acc[r], rin, kq);
+            } else {
+                load_mwfrag<FMT, NW>(a, nrow, kq, nb2, wB);
+                TS5_GM_SB();
+                gm_item<FMT, NW, NT, P5, NA>(wA, xc, acc[r], rin, kq);
+            }
+        }
+    };
+    if (b0 < b1)
+        for (int b = b0;; b += 2) {
+            run_block(std::integral_constant<int, 0>{}, b);
+            if (b + 1 >= b1) break;
+            run_block(std::integral_constant<int, RT & 1>{}, b + 1);
+            if (b + 2 >= b1) break;
+        }
+    // The waves' sums: [wave][r][m][tt][lane] after the records.
+    float *red = (float *)(lx + (size_t)a.M * tstride);
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int m = 0; m < NW; m++)
+#pragma unroll
+            for (int tt = 0; tt < NA; tt++) red[(((wave * RT + r) * NW + m) * NA + tt) * 64 + l] = acc[r][m][tt];
+    __syncthreads();
+    constexpr int E = RT * NA * 64;  // entries (row tile, token tile, lane)
+    static_assert(E <= 64 * GX_WAVES, "one entry a thread");
+    if (tid >= E) return;
+    const int r = tid / (NA * 64), tt = (tid / 64) % NA, ln = tid & 63;
+    auto wsum = [&](int m, int lane) {
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < GX_WAVES; w++) v += red[(((w * RT + r) * NW + m) * NA + tt) * 64 + lane];
+        return v;
+    };
+    float v[NW];
+#pragma unroll
+    for (int m = 0; m < NW; m++) {
+        if (P5 && tt == NT) {  // the fifth token: the four lane groups' shares of the row, (g0 + g1) + (g2 + g3)
+            const int lr = ln & 15;
+            v[m] = (wsum(m, lr) + wsum(m, lr + 16)) + (wsum(m, lr + 32) + wsum(m, lr + 48));
+        } else {
+            v[m] = wsum(m, ln);
+        }
+    }
+    const int row = rowbase(r) + (ln & 15), tok = tt == NT ? 4 : 4 * tt + (ln >> 4);
+    if (row >= a.nrows || tok >= a.M || (tt == NT && (ln >> 4) != 0)) return;
+    const int64_t o = (int64_t)tok * a.ldy + row;
+    if (MODE == G_ADD) a.out[o] = a.y_in[o] + v[0];
+    else if (MODE == G_GLU) a.out[o] = v[0] / (1.0f + expf(-v[0])) * v[NW - 1];  // cpu_backend.cpp:260-261
+    else a.out[o] = v[0];
+}
+
+template <int MODE, int TM>
+static void launch_gemm_mx_tm(const GemmArgs &a, int rt, unsigned grid, size_t lds, hipStream_t s) {
+    if (rt == 4) hipLaunchKernelGGL((k_gemm_mx<MODE, TM, 4>), dim3(grid), dim3(64 * GX_WAVES), lds, s, a);
+    else if (rt == 2) hipLaunchKernelGGL((k_gemm_mx<MODE, TM, 2>), dim3(grid), dim3(64 * GX_WAVES), lds, s, a);
+    else hipLaunchKernelGGL((k_gemm_mx<MODE, TM, 1>), dim3(grid), dim3(64 * GX_WAVES), lds, s, a);
+}
+
 template <int MODE, int TM>
 static void launch_gemm_fused_tm(const GemmArgs &a, int rt, size_t lds, hipStream_t s) {
     const unsigned grid = (unsigned)((a.nrows + 16 * rt - 1) / (16 * rt));
@@ -963,6 +1164,25 @@ hipError_t launch_gemm_fused(const void *w, const void *w2, int64_t ne0, int64_t
     a.xin = x, a.xin_stride = xstride, a.norm_w = norm_w, a.eps = eps;
     const size_t lds = (size_t)M * a.nb * MACT_BLOCK;
     const int tiles = (a.nrows + 15) / 16;
+    const unsigned grid = (unsigned)std::min(tiles, g_gemm_m_cu);
+    const int rt_mx = (tiles + (int)grid - 1) / (int)grid;
+    if (TS5_GM_MX && rt_mx <= 4) {
+        // One workgroup a CU (at most), each RT tiles gridDim.x apart; its
+        // LDS: the records, then the 8 waves' sums (RT x 2 x 2 x 64 floats
+        // each at most: 64 KiB, with the records' 5 x 16 x 896 B under 160 KiB).
+        const int rtp = rt_mx > 2 ? 4 : rt_mx;
+        const int na = M == 5 ? 2 : 1, nw = mode == G_GLU ? 2 : 1;
+        const size_t lds_mx = lds + (size_t)GX_WAVES * rtp * nw * na * 64 * sizeof(float);
+        auto go = [&](auto mode_c) {
+            constexpr int MD = decltype(mode_c)::value;
+            if (M == 5) launch_gemm_mx_tm<MD, 5>(a, rtp, grid, lds_mx, s);
+            else launch_gemm_mx_tm<MD, 1>(a, rtp, grid, lds_mx, s);
+        };
+        if (mode == G_ADD) go(std::integral_constant<int, G_ADD>{});
+        else if (mode == G_GLU) go(std::integral_constant<int, G_GLU>{});
+        else go(std::integral_constant<int, G_STORE>{});
+        return hipGetLastError();
+    }
     int rt = tiles >= 4 * g_gemm_m_cu ? 4 : tiles >= 2 * g_gemm_m_cu ? 2 : 1;
     if (TS5_GM_RTMAX < rt) rt = TS5_GM_RTMAX;
     auto go = [&](auto mode_c) {

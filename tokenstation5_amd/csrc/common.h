@@ -329,6 +329,14 @@ __device__ inline void dma16(const void *g, uint32_t lds_base) {
 __device__ inline void dma4(const void *g, uint32_t lds_base) {
     asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_base) : "memory");
 }
+// The same from a buffer resource at byte offset voff: offsets at or past
+// the resource's size read zeros and touch no memory.
+__device__ inline __amdgpu_buffer_rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ inline void dma16b(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds_base) {
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds_base) : "memory");
+}
 // 16-run r of an activation (half r & 1 of sub-block r / 2) from its 16
 // values: the three planes' bytes, the run's sum of X, and the 32-value
 // chunk's scale and sum. Two threads per 32-value sub-block, in adjacent

@@ -1001,6 +1001,41 @@ __global__ __launch_bounds__(64 * GX_WAVES) void k_gemm_mx(GemmArgs a) {
     const int l = tid & 63, kq = l >> 4, rl = l & 15;
     const int bpq = (a.nb + GX_WAVES - 1) / GX_WAVES, b0 = wave * bpq, b1 = min(a.nb, b0 + bpq);
     const int64_t tstride = (int64_t)a.nb * MACT_BLOCK;
+    // An item's weights (16 rows x 144 bytes of one block, per matrix) come
+    // into the wave's own LDS slot by DMA as row-contiguous 16-byte pieces
+    // (piece c = 64 i + lane of request i: row c / 9, bytes 16 (c % 9); the
+    // third request's first 16 lanes end the 144 pieces), two slots in turn,
+    // one item ahead; the MFMA lanes then read their fragments from LDS.
+    // Requested so, the bytes stream at about 1.7 times the rate of each
+    // lane fetching its own 8-byte pieces of 16 rows from memory.
+    constexpr int WSLOT = 16 * Q4K_BYTES;
+    uint8_t *stg = lx + (size_t)a.M * tstride + (size_t)wave * 2 * NW * WSLOT;
+    const uint32_t wbytes = (uint32_t)a.nrows * a.nb * Q4K_BYTES;  // rows past the last read zeros
+    const __amdgpu_buffer_rsrc_t rw[2] = {buf_rsrc(a.w, wbytes), buf_rsrc(NW == 2 ? a.w2 : a.w, wbytes)};
+    uint32_t coff[3];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const int c = min(64 * i + l, 143);
+        coff[i] = (uint32_t)((c / 9) * a.nb * Q4K_BYTES + 16 * (c % 9));
+    }
+    auto issue = [&](int row0, int b, int slot) {
+        uint32_t base = ((uint32_t)row0 * a.nb + b) * Q4K_BYTES;
+        asm volatile("" : "+s"(base));  // opaque: the per-lane sums are formed here, not hoisted out of the loop
+#pragma unroll
+        for (int m = 0; m < NW; m++)
+#pragma unroll
+            for (int i = 0; i < 3; i++)
+                if (i < 2 || l < 16) dma16b(rw[m], base + coff[i], lds_addr(stg + (slot * NW + m) * WSLOT + 1024 * i));
+    };
+    auto fetch = [&](int slot, MWFrag<FMT, NW> &w) {
+#pragma unroll
+        for (int m = 0; m < NW; m++) {
+            const uint8_t *p = stg + (slot * NW + m) * WSLOT + Q4K_BYTES * rl;
+            w.hdr[m] = *(const uint4 *)p;
+#pragma unroll
+            for (int g = 0; g < 4; g++) w.q[m][g] = *(const uint64_t *)(p + 16 + 32 * g + 8 * kq);
+        }
+    };
     auto rowbase = [&](int r) { return (int)(blockIdx.x + (unsigned)r * gridDim.x) * 16; };
     // The input runs first (loads return in order), then the first item's
     // weights, all unconditional: tokens, rows, blocks and runs are clamped.
@@ -1016,9 +1051,12 @@ __global__ __launch_bounds__(64 * GX_WAVES) void k_gemm_mx(GemmArgs a) {
             xv[j][q] = *(const float4 *)(a.xin + (int64_t)min(tb + j, a.M - 1) * a.xin_stride + 16 * run + 4 * q);
 #pragma unroll
     for (int q = 0; q < 4; q++) nw[q] = *(const float4 *)(nwp + 16 * run + 4 * q);
-    TS5_GM_SB();  // the weights after the input: the scheduler would otherwise put them between
-    MWFrag<FMT, NW> wA, wB;
-    load_mwfrag<FMT, NW>(a, rowbase(0) + rl, kq, min(b0, a.nb - 1), wA);
+    // The input in (a wait the compiler sees: it then has no load of its own
+    // left to wait for, and never waits for the weight requests, which it
+    // does not see), then the first item's weights, in flight through the
+    // norm and the quantization.
+    wait_vmcnt<0>();
+    issue(rowbase(0), min(b0, a.nb - 1), 0);
     float sc[TH];
 #pragma unroll
     for (int j = 0; j < TH; j++) sc[j] = 1.f;
@@ -1060,7 +1098,6 @@ __global__ __launch_bounds__(64 * GX_WAVES) void k_gemm_mx(GemmArgs a) {
         if (j < tn && tb + j < a.M && mine) quant_run_m(v, run, lx + (tb + j) * tstride);
     }
     __syncthreads();
-    wait_vmcnt<5 * NW>();  // the input loads are in: only the first item's weights may be open
     float acc[RT][NW][NA];
 #pragma unroll
     for (int r = 0; r < RT; r++)
@@ -1068,44 +1105,44 @@ __global__ __launch_bounds__(64 * GX_WAVES) void k_gemm_mx(GemmArgs a) {
         for (int m = 0; m < NW; m++)
 #pragma unroll
             for (int tt = 0; tt < NA; tt++) acc[r][m][tt] = 0.f;
-    // Items (block b, row tile r) through the two weight buffers in turn,
-    // each block's activation fragments read from LDS once.
-    auto run_block = [&](auto par, int b) {
-        constexpr int P = decltype(par)::value;
-        MAFrag<FMT, NT, P5> xc;
-        load_mafrag_at<FMT, NT, P5>(lx, tstride, a.M, b, l, xc);
-        gm_prescale<FMT, NT, P5>(xc, kq);
+    // Items (row tile r, block b), the tiles outermost, through the two
+    // weight slots in turn (tiles innermost, sharing a block's activation
+    // fragments, held too many registers); an item reads its block's
+    // activation fragments from LDS. Before an item's request for the next
+    // one: the LDS reads of the slot it overwrites are in (lgkmcnt 0); before
+    // its fragment reads: its own requests are in. Past the last item the
+    // request repeats one, in bounds and unused.
+    int sl = 0;
 #pragma unroll
-        for (int r = 0; r < RT; r++) {
-            const bool last = r == RT - 1;
-            const int nb2 = last ? min(b + 1, b1 - 1) : b, nrow = rowbase(last ? 0 : r + 1) + rl;
-            const bool rin = rowbase(r) + rl < a.nrows;
-            if ((P + r) & 1) {
-                load_mwfrag<FMT, NW>(a, nrow, kq, nb2, wA);
-                TS5_GM_SB();
-                gm_item<FMT, NW, NT, P5, NA>(wB, xc, acc[r], rin, kq);
-            } else {
-                load_mwfrag<FMT, NW>(a, nrow, kq, nb2, wB);
-                TS5_GM_SB();
-                gm_item<FMT, NW, NT, P5, NA>(wA, xc, acc[r], rin, kq);
-            }
+    for (int r = 0; r < RT; r++) {
+        const bool rin = rowbase(r) + rl < a.nrows;
+        for (int b = b0; b < b1; b++) {
+            const bool lastb = b + 1 >= b1;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(rowbase(lastb ? min(r + 1, RT - 1) : r), lastb ? b0 : b + 1, sl ^ 1);
+            wait_vm_n<3 * NW>();
+            MAFrag<FMT, NT, P5> xc;
+            load_mafrag_at<FMT, NT, P5>(lx, tstride, a.M, b, l, xc);
+            gm_prescale<FMT, NT, P5>(xc, kq);
+            MWFrag<FMT, NW> w;
+            fetch(sl, w);
+            gm_item<FMT, NW, NT, P5, NA>(w, xc, acc[r], rin, kq);
+            TS5_GM_SB();  // one item at a time
+            sl ^= 1;
         }
-    };
-    if (b0 < b1)
-        for (int b = b0;; b += 2) {
-            run_block(std::integral_constant<int, 0>{}, b);
-            if (b + 1 >= b1) break;
-            run_block(std::integral_constant<int, RT & 1>{}, b + 1);
-            if (b + 2 >= b1) break;
-        }
-    // The waves' sums: [wave][r][m][tt][lane] after the records.
-    float *red = (float *)(lx + (size_t)a.M * tstride);
+    }
+    // The waves' sums, [r][m][tt][lane] in each wave's own weight slots once
+    // its last (repeated) request is in.
+    wait_vm_n<0>();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    static_assert(RT * NA * 64 * sizeof(float) <= 2 * WSLOT, "the waves' sums fit their weight slots");
+    auto red = [&](int w) { return (float *)(lx + (size_t)a.M * tstride + (size_t)w * 2 * NW * WSLOT); };
 #pragma unroll
     for (int r = 0; r < RT; r++)
 #pragma unroll
         for (int m = 0; m < NW; m++)
 #pragma unroll
-            for (int tt = 0; tt < NA; tt++) red[(((wave * RT + r) * NW + m) * NA + tt) * 64 + l] = acc[r][m][tt];
+            for (int tt = 0; tt < NA; tt++) red(wave)[((r * NW + m) * NA + tt) * 64 + l] = acc[r][m][tt];
     __syncthreads();
     constexpr int E = RT * NA * 64;  // entries (row tile, token tile, lane)
     static_assert(E <= 64 * GX_WAVES, "one entry a thread");
@@ -1114,7 +1151,7 @@ __global__ __launch_bounds__(64 * GX_WAVES) void k_gemm_mx(GemmArgs a) {
     auto wsum = [&](int m, int lane) {
         float v = 0.f;
 #pragma unroll
-        for (int w = 0; w < GX_WAVES; w++) v += red[(((w * RT + r) * NW + m) * NA + tt) * 64 + lane];
+        for (int w = 0; w < GX_WAVES; w++) v += red(w)[((r * NW + m) * NA + tt) * 64 + lane];
         return v;
     };
     float v[NW];
@@ -1168,11 +1205,12 @@ hipError_t launch_gemm_fused(const void *w, const void *w2, int64_t ne0, int64_t
     const int rt_mx = (tiles + (int)grid - 1) / (int)grid;
     if (TS5_GM_MX && rt_mx <= 4) {
         // One workgroup a CU (at most), each RT tiles gridDim.x apart; its
-        // LDS: the records, then the 8 waves' sums (RT x 2 x 2 x 64 floats
-        // each at most: 64 KiB, with the records' 5 x 16 x 896 B under 160 KiB).
+        // LDS: the records, then each wave's two weight slots of 16 rows x
+        // 144 B per matrix (GLU: 72 KiB; with the records' 5 x 16 x 896 B
+        // under 160 KiB).
         const int rtp = rt_mx > 2 ? 4 : rt_mx;
-        const int na = M == 5 ? 2 : 1, nw = mode == G_GLU ? 2 : 1;
-        const size_t lds_mx = lds + (size_t)GX_WAVES * rtp * nw * na * 64 * sizeof(float);
+        const int nw = mode == G_GLU ? 2 : 1;
+        const size_t lds_mx = lds + (size_t)GX_WAVES * 2 * nw * 16 * Q4K_BYTES;
         auto go = [&](auto mode_c) {
             constexpr int MD = decltype(mode_c)::value;
             if (M == 5) launch_gemm_mx_tm<MD, 5>(a, rtp, grid, lds_mx, s);

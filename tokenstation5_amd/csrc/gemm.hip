@@ -46,6 +46,9 @@
 #ifndef TS5_GM_MX
 #define TS5_GM_MX 1
 #endif
+#ifndef TS5_GM_MW
+#define TS5_GM_MW 1
+#endif
 #ifndef TS5_GM_P5
 #define TS5_GM_P5 1
 #endif
@@ -1172,6 +1175,113 @@ __global__ __launch_bounds__(64 * GX_WAVES) void k_gemm_mx(GemmArgs a) {
     else a.out[o] = v[0];
 }
 
+// ---------------------------------------------------------------------------
+// The same small-batch matmul (Q4_K, 1-5 tokens, no gate/up) over activation
+// records already in memory (k_act_quant_m's, for inputs wider than the
+// fused kernel's LDS holds: the down projection), one workgroup of 8 waves a
+// CU walking row tiles gridDim.x apart. Per item (row tile, block of the
+// wave's eighth) both the weights (16 rows x 144 bytes) and the block's
+// records of the M tokens (M x 896 bytes) come into the wave's LDS slots by
+// DMA, one item ahead; the waves' sums of a tile meet in LDS and a thread
+// per (token tile, lane) finishes the tile's outputs.
+// ---------------------------------------------------------------------------
+template <int MODE, int TM>
+__global__ __launch_bounds__(64 * GX_WAVES) void k_gemm_mw(GemmArgs a) {
+    constexpr int FMT = F_Q4K, NW = 1, NT = 1;
+    constexpr bool P5 = TM == 5;
+    static_assert(MODE != G_GLU && (TM == 1 || TM == 5), "wide small-batch matmul: up to 5 tokens, one matrix");
+    constexpr int NA = NT + (P5 ? 1 : 0);
+    constexpr int WSLOT = 16 * Q4K_BYTES, RSLOT = 5 * 1024;  // weights; records (5 requests of 64 x 16 B)
+    extern __shared__ __align__(16) uint8_t lw[];  // per wave: 2 weight slots, 2 record slots; then the sums
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l = tid & 63, kq = l >> 4, rl = l & 15;
+    const int ntile = (a.nrows + 15) / 16;
+    const int bpq = (a.nb + GX_WAVES - 1) / GX_WAVES, b0 = wave * bpq, b1 = min(a.nb, b0 + bpq);
+    uint8_t *wst = lw + (size_t)wave * 2 * (WSLOT + RSLOT), *rst = wst + 2 * WSLOT;
+    float *red = (float *)(lw + (size_t)GX_WAVES * 2 * (WSLOT + RSLOT));  // [wave][tt][64]
+    const uint32_t wbytes = (uint32_t)a.nrows * a.nb * Q4K_BYTES;  // rows past the last read zeros
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(a.w, wbytes);
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a.act, (uint32_t)(a.M * a.act_stride));
+    // Weight pieces: c = 64 i + lane, row c / 9, bytes 16 (c % 9). Record
+    // pieces: c = 64 i + lane, token c / 56 (past the M tokens: the last
+    // one's, into LDS past the records, unused), bytes 16 (c % 56).
+    uint32_t coff[3], roff[5];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const int c = min(64 * i + l, 143);
+        coff[i] = (uint32_t)((c / 9) * a.nb * Q4K_BYTES + 16 * (c % 9));
+    }
+#pragma unroll
+    for (int i = 0; i < 5; i++) {
+        const int c = 64 * i + l, t = min(c / 56, a.M - 1);
+        roff[i] = (uint32_t)(t * a.act_stride + 16 * (c % 56));
+    }
+    auto issue = [&](int tile, int b, int slot) {
+        uint32_t wb = ((uint32_t)tile * 16 * a.nb + b) * Q4K_BYTES, rb = (uint32_t)b * MACT_BLOCK;
+        asm volatile("" : "+s"(wb), "+s"(rb));  // opaque: the per-lane sums are formed here
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+            if (i < 2 || l < 16) dma16b(rw, wb + coff[i], lds_addr(wst + slot * WSLOT + 1024 * i));
+#pragma unroll
+        for (int i = 0; i < 5; i++) dma16b(ra, rb + roff[i], lds_addr(rst + slot * RSLOT + 1024 * i));
+    };
+    int sl = 0;
+    issue(blockIdx.x, min(b0, a.nb - 1), 0);
+    for (int tile = blockIdx.x; tile < ntile; tile += gridDim.x) {
+        const bool rin = tile * 16 + rl < a.nrows;
+        float acc[NW][NA];
+#pragma unroll
+        for (int tt = 0; tt < NA; tt++) acc[0][tt] = 0.f;
+        for (int b = b0; b < b1; b++) {
+            // The next item: the next block, or the next tile's first (past
+            // the last tile a repeat, in bounds and unused).
+            const bool lastb = b + 1 >= b1;
+            const int ntl = lastb ? min(tile + (int)gridDim.x, ntile - 1) : tile;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(ntl, lastb ? b0 : b + 1, sl ^ 1);
+            wait_vm_n<8>();  // this item's 8 requests are in
+            MAFrag<FMT, NT, P5> xc;
+            load_mafrag_at<FMT, NT, P5>(rst + sl * RSLOT, MACT_BLOCK, a.M, 0, l, xc);
+            gm_prescale<FMT, NT, P5>(xc, kq);
+            MWFrag<FMT, NW> w;
+            const uint8_t *p = wst + sl * WSLOT + Q4K_BYTES * rl;
+            w.hdr[0] = *(const uint4 *)p;
+#pragma unroll
+            for (int g = 0; g < 4; g++) w.q[0][g] = *(const uint64_t *)(p + 16 + 32 * g + 8 * kq);
+            gm_item<FMT, NW, NT, P5, NA>(w, xc, acc, rin, kq);
+            TS5_GM_SB();  // one item at a time
+            sl ^= 1;
+        }
+#pragma unroll
+        for (int tt = 0; tt < NA; tt++) red[(wave * NA + tt) * 64 + l] = acc[0][tt];
+        __syncthreads();
+        if (tid < NA * 64) {
+            const int tt = tid / 64, ln = tid & 63;
+            auto wsum = [&](int lane) {
+                float v = 0.f;
+#pragma unroll
+                for (int w2 = 0; w2 < GX_WAVES; w2++) v += red[(w2 * NA + tt) * 64 + lane];
+                return v;
+            };
+            float v;
+            if (P5 && tt == NT) {  // the fifth token: (g0 + g1) + (g2 + g3)
+                const int lr = ln & 15;
+                v = (wsum(lr) + wsum(lr + 16)) + (wsum(lr + 32) + wsum(lr + 48));
+            } else {
+                v = wsum(ln);
+            }
+            const int row = tile * 16 + (ln & 15), tok = tt == NT ? 4 : 4 * tt + (ln >> 4);
+            if (row < a.nrows && tok < a.M && (tt < NT || (ln >> 4) == 0)) {
+                const int64_t o = (int64_t)tok * a.ldy + row;
+                if (MODE == G_ADD) a.out[o] = a.y_in[o] + v;
+                else a.out[o] = v;
+            }
+        }
+        __syncthreads();  // the sums are read before the next tile writes them
+    }
+    wait_vm_n<0>();  // the last (repeated) requests are in before the waves end
+}
+
 template <int MODE, int TM>
 static void launch_gemm_mx_tm(const GemmArgs &a, int rt, unsigned grid, size_t lds, hipStream_t s) {
     if (rt == 4) hipLaunchKernelGGL((k_gemm_mx<MODE, TM, 4>), dim3(grid), dim3(64 * GX_WAVES), lds, s, a);
@@ -1338,6 +1448,15 @@ static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
             const char *e = getenv("TS5HIP_GEMM_M");
             return !(e && e[0] == '0');
         }();
+        if constexpr (FMT == F_Q4K && MODE != G_GLU)
+            if (use_m && TS5_GM_MW && a.M <= 5 && a.ks == 1) {
+                const int tiles = (a.nrows + 15) / 16;
+                const size_t lds = (size_t)GX_WAVES * 2 * (16 * Q4K_BYTES + 5 * 1024) + GX_WAVES * 2 * 64 * 4;
+                const dim3 g((unsigned)std::min(tiles, g_gemm_m_cu)), blk(64 * GX_WAVES);
+                if (a.M == 5) hipLaunchKernelGGL((k_gemm_mw<MODE, 5>), g, blk, lds, s, a);
+                else hipLaunchKernelGGL((k_gemm_mw<MODE, 1>), g, blk, lds, s, a);
+                return hipGetLastError();
+            }
         if (use_m && gemm_m_fits<FMT, MODE>(a.M)) return launch_gemm_m<FMT, MODE>(a, s);
     }
     if (a.M <= 16) {

@@ -270,6 +270,8 @@ bool attn_supported(int H, int HKV, int HD) {
 }
 
 hipError_t launch_attn(const AttnIO &io, hipStream_t s) {
+    // A batch on one cache that appends reads its new keys from LDS: at most ATTN_MAX_NEW.
+    if (io.append && !io.kv_per_batch && io.B > ATTN_MAX_NEW) return hipErrorInvalidValue;
     AttnArgs a{};
     a.q = io.q, a.q_stride = io.q_stride, a.bias = io.bias, a.q_norm = io.q_norm, a.k_norm = io.k_norm;
     a.eps = io.eps, a.rope_cs = (const float2 *)io.rope_cs, a.n_rot = io.n_rot, a.neox = io.neox;

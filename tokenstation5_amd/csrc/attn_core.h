@@ -31,9 +31,12 @@ __device__ inline void rope_pair(float &x0, float &x1, float c, float s) {
 //   nk = n_keys[0] + b + 1 (one cache, a batch of consecutive positions).
 // 1. The G query heads of this KV head: q (+ bias, per-head norm, RoPE
 //    when `rope`) -> LDS.
-// 2. `append` (B == 1): the workgroup whose key slice holds the new key
-//    rounds that token's K (RoPE'd) and V to q8, stores them at their slot,
-//    and keeps a copy in LDS that it reads instead of the cache.
+// 2. `append`: the batch's new keys (one cache: positions n_keys[0] ..
+//    n_keys[0] + B - 1; kv_per_batch: each query's own) are not in the cache
+//    yet: a workgroup whose key slice holds some of query b's new keys rounds
+//    those tokens' K (RoPE'd) and V to q8 itself, keeps them in LDS and reads
+//    them there instead of the cache; query b's workgroup stores its own
+//    token's K and V at their slot (one writer per key).
 // 3. 64-key tiles: scores (NT/64 lanes per key), online softmax per head,
 //    p*v with the tile's V staged in LDS.
 // 4. The unnormalised partial (sum p*v, m, l) per head goes to `part`; the
@@ -74,7 +77,8 @@ struct AttnSpan {
     int pq, p0, p1;
     int used;           // splits that hold keys: the others (later ones) are empty
     int64_t head_base;  // cache slot of key 0 for this KV head
-    bool has_new;       // the new key (pq) falls in this slice
+    int n_lo, n_hi;     // the new keys (append) in this slice: [n_lo, n_hi)
+    bool has_new;       // n_lo < n_hi
 };
 template <int TILE = ATTN_TILE>
 __device__ inline AttnSpan attn_span(const AttnArgs &a, int split, int kvh, int b, int n_split) {
@@ -92,34 +96,35 @@ __device__ inline AttnSpan attn_span(const AttnArgs &a, int split, int kvh, int 
     sp.p1 = min(nk, sp.p0 + chunk);
     const int seq = a.kv_per_batch ? b : 0;
     sp.head_base = ((int64_t)seq * a.HKV + kvh) * a.n_ctx;
-    sp.has_new = a.append && sp.pq >= sp.p0 && sp.pq < sp.p1;
+    const int first = a.kv_per_batch ? sp.pq : a.n_keys[0];  // the batch's first new key
+    sp.n_lo = max(first, sp.p0), sp.n_hi = a.append ? min(sp.pq + 1, sp.p1) : sp.n_lo;
+    sp.has_new = sp.n_lo < sp.n_hi;
     return sp;
 }
 
-// 1. The G query heads of KV head kvh (and, when the slice holds the new key,
-//    that token's K and V) into LDS, from q(e) = element e of the token's
-//    q|k|v row; bias, per-head norm and RoPE when a.rope; the new K and V
-//    rounded as the cache keeps them (q8, or f16 with F16) and stored at
-//    their cache slot.
-template <int HD, int G, int NT, bool F16, class QLoad, class Lds>
-__device__ inline void attn_prepare(const AttnArgs &a, int kvh, const AttnSpan &sp, Lds &S, QLoad qload) {
+// 1. The G query heads of KV head kvh into LDS from query b's row; bias,
+//    per-head norm and RoPE when a.rope. Then each new key of the slice
+//    (n_lo .. n_hi - 1; the rows of those tokens, query b's row for key pq),
+//    rounded as the cache keeps it (q8, or f16 with F16) into LDS slot
+//    j - n_lo, and query b's own (pq) stored at its cache slot.
+template <int HD, int G, int NT, bool F16, class Lds>
+__device__ inline void attn_prepare(const AttnArgs &a, int kvh, int b, const AttnSpan &sp, Lds &S) {
     constexpr int NWV = NT / 64;
     auto &q_s = S.q_s;
     auto &kv_s = S.kv_s;
-    auto &new8 = S.new8;
-    auto &new_sc = S.new_sc;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pq = sp.pq;
-    const bool has_new = sp.has_new;
+    const int nn = sp.n_hi - sp.n_lo;  // new keys in the slice, prepared together with the query
+    const float *qrow = a.q + (int64_t)b * a.q_stride;
     for (int j = tid; j < G * HD; j += NT) {
         const int64_t e = (int64_t)(kvh * G + j / HD) * HD + j % HD;
-        q_s[j / HD][j % HD] = qload(e) + (a.rope && a.bias ? a.bias[e] : 0.f);
+        q_s[j / HD][j % HD] = qrow[e] + (a.rope && a.bias ? a.bias[e] : 0.f);
     }
-    if (has_new) {
-        for (int j = tid; j < 2 * HD; j += NT) {
-            const int64_t e = (int64_t)((j < HD ? a.H : a.H + a.HKV) + kvh) * HD + j % HD;
-            kv_s[j / HD][j % HD] = qload(e) + (a.bias ? a.bias[e] : 0.f);
-        }
+    for (int j = tid; j < nn * 2 * HD; j += NT) {
+        const int kk = j / (2 * HD), which = (j / HD) & 1, d = j % HD;
+        const float *row = a.q + (int64_t)(b - (pq - (sp.n_lo + kk))) * a.q_stride;  // the token at that position
+        const int64_t e = (int64_t)((which ? a.H + a.HKV : a.H) + kvh) * HD + d;
+        kv_s[kk][which][d] = row[e] + (a.bias ? a.bias[e] : 0.f);
     }
     if (tid < G) {
         S.m_s[tid] = -INFINITY;
@@ -127,12 +132,13 @@ __device__ inline void attn_prepare(const AttnArgs &a, int kvh, const AttnSpan &
     }
     __syncthreads();
     if (a.rope) {
-        // Per-head RMSNorm (qwen3's q_norm / k_norm), then RoPE.
-        if (a.q_norm || (has_new && a.k_norm)) {
-            for (int g = wave; g < G + 1; g += NWV) {
-                const float *nw = g < G ? a.q_norm : (has_new ? a.k_norm : nullptr);
+        // Per-head RMSNorm (qwen3's q_norm, k_norm), then RoPE: the query
+        // heads at the query's position, each key at its own.
+        if (a.q_norm || (nn && a.k_norm)) {
+            for (int g = wave; g < G + nn; g += NWV) {
+                const float *nw = g < G ? a.q_norm : a.k_norm;
                 if (!nw) continue;
-                float *v = g < G ? q_s[g] : kv_s[0];
+                float *v = g < G ? q_s[g] : kv_s[g - G][0];
                 float ss = 0.f;
                 for (int j = lane; j < HD; j += 64) ss += v[j] * v[j];
                 ss = wave_sum(ss);
@@ -141,32 +147,34 @@ __device__ inline void attn_prepare(const AttnArgs &a, int kvh, const AttnSpan &
             }
             __syncthreads();
         }
-        const float2 *cs = a.rope_cs + (int64_t)pq * (a.n_rot / 2);
-        for (int j = tid; j < (G + 1) * (HD / 2); j += NT) {
+        const int nr2 = a.n_rot / 2;
+        for (int j = tid; j < G * (HD / 2); j += NT) {
             const int g = j / (HD / 2), i = j % (HD / 2);
-            if (i >= a.n_rot / 2) continue;
-            if (g < G) rope_inplace(q_s[g], a.n_rot, a.neox, cs, i);
-            else if (has_new) rope_inplace(kv_s[0], a.n_rot, a.neox, cs, i);
+            if (i < nr2) rope_inplace(q_s[g], a.n_rot, a.neox, a.rope_cs + (int64_t)pq * nr2, i);
+        }
+        __syncthreads();
+        for (int j = tid; j < nn * nr2; j += NT) {
+            const int kk = j / nr2, i = j % nr2;
+            rope_inplace(kv_s[kk][0], a.n_rot, a.neox, a.rope_cs + (int64_t)(sp.n_lo + kk) * nr2, i);
         }
         __syncthreads();
     }
-    if (F16 && has_new && tid < 128) {
-        // f16 (engine/src/cpu_backend.cpp:80): each value rounded to the
-        // nearest f16. Wave 0 rounds K, wave 1 V, a pair per lane.
-        const int which = tid >> 6, i = tid & 63;
-        if (2 * i < HD) {
-            const uint32_t pair = (uint32_t)f2h(kv_s[which][2 * i]) | (uint32_t)f2h(kv_s[which][2 * i + 1]) << 16;
-            const int64_t slot = sp.head_base + pq;
-            *(uint32_t *)(S.new16[which] + 2 * i) = pair;
-            *(uint32_t *)((uint16_t *)(which ? a.kv.v : a.kv.k) + slot * HD + 2 * i) = pair;
-        }
-    }
-    if (!F16 && has_new && tid < 128) {
-        // q8 (engine/src/cpu_backend.cpp:78-90): per 32 values sc = f16(amax / 127),
-        // q = clamp(rint(v / sc), +-127). Wave 0 rounds K, wave 1 V, a pair per lane.
-        const int which = tid >> 6, i = tid & 63;
-        if (2 * i < HD) {
-            const float a0 = kv_s[which][2 * i], a1 = kv_s[which][2 * i + 1];
+    if (nn == 0) return;
+    // Rounded as the cache keeps them, a wave per (key, K or V), a pair of
+    // values a lane; query b's own token (pq) also stored at its slot.
+    for (int pr = wave; pr < 2 * nn; pr += NWV) {
+        const int kk = pr >> 1, which = pr & 1, i = lane, key = sp.n_lo + kk;
+        const bool own = key == pq;
+        const int64_t slot = sp.head_base + key;
+        if (2 * i >= HD) continue;
+        if constexpr (F16) {  // engine/src/cpu_backend.cpp:80: each value to the nearest f16
+            const uint32_t pair = (uint32_t)f2h(kv_s[kk][which][2 * i]) | (uint32_t)f2h(kv_s[kk][which][2 * i + 1]) << 16;
+            *(uint32_t *)(S.new16[kk][which] + 2 * i) = pair;
+            if (own) *(uint32_t *)((uint16_t *)(which ? a.kv.v : a.kv.k) + slot * HD + 2 * i) = pair;
+        } else {
+            // q8 (engine/src/cpu_backend.cpp:78-90): per 32 values sc = f16(amax / 127),
+            // q = clamp(rint(v / sc), +-127).
+            const float a0 = kv_s[kk][which][2 * i], a1 = kv_s[kk][which][2 * i + 1];
             float amax = fmaxf(fabsf(a0), fabsf(a1));
 #pragma unroll
             for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
@@ -178,12 +186,11 @@ __device__ inline void attn_prepare(const AttnArgs &a, int kvh, const AttnSpan &
                 q1 = (int)fminf(127.f, fmaxf(-127.f, rintf(a1 / sc)));
             }
             const uint16_t packed = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
-            const int64_t slot = sp.head_base + pq;
-            *(uint16_t *)(new8[which] + 2 * i) = packed;
-            *(uint16_t *)((which ? a.kv.v : a.kv.k) + slot * HD + 2 * i) = packed;
+            *(uint16_t *)(S.new8[kk][which] + 2 * i) = packed;
+            if (own) *(uint16_t *)((which ? a.kv.v : a.kv.k) + slot * HD + 2 * i) = packed;
             if ((i & 15) == 0) {
-                new_sc[which][i / 16] = sh;
-                (which ? a.kv.vs : a.kv.ks)[slot * (HD / 32) + i / 16] = sh;
+                S.new_sc[kk][which][i / 16] = sh;
+                if (own) (which ? a.kv.vs : a.kv.ks)[slot * (HD / 32) + i / 16] = sh;
             }
         }
     }
@@ -223,10 +230,10 @@ template <int HD, int G, int NT = 256>
 struct SliceLds {
     float q_s[G][HD];
     float m_s[G], l_s[G], red[G];
-    float kv_s[2][HD];                    // the new token's K and V before rounding
-    __align__(16) int8_t new8[2][HD];     // ... and after, as int8
-    uint16_t new_sc[2][HD / 32];          // ... with their f16 scales
-    __align__(16) uint16_t new16[2][HD];  // ... or as f16 (an f16 cache)
+    float kv_s[ATTN_MAX_NEW][2][HD];                     // the new keys' K and V before rounding
+    __align__(16) int8_t new8[ATTN_MAX_NEW][2][HD];     // ... and after, as int8
+    uint16_t new_sc[ATTN_MAX_NEW][2][HD / 32];          // ... with their f16 scales
+    __align__(16) uint16_t new16[ATTN_MAX_NEW][2][HD];  // ... or as f16 (an f16 cache)
     __align__(16) float o_w[NT / 64][G][HD];  // each wave's o
     float m_w[NT / 64][G], l_w[NT / 64][G];   // ... and (m, l)
     __align__(16) float wts[G][ATTN_MAX_SPLIT];  // the merge's weight per (head, split), 0 past n_split
@@ -320,10 +327,7 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
     Chunk A, B;
     request(A, 0);
     request(B, 1);
-    {
-        const float *row = a.q + (int64_t)b * a.q_stride;
-        attn_prepare<HD, G, NT, F16>(a, kvh, sp, S, [&](int64_t e) { return row[e]; });
-    }
+    attn_prepare<HD, G, NT, F16>(a, kvh, b, sp, S);
     float q[G][DPL], o[G][DPL], m[G], l[G];
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -336,12 +340,13 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
         for (int e = 0; e < DPL; e++) o[g][e] = 0.f;
         m[g] = -INFINITY, l[g] = 0.f;
     }
-    const int pq_rel = sp.pq - sp.p0;  // the new key (when sp.has_new), relative to p0
+    const int nlo_rel = sp.n_lo - sp.p0, nnew = sp.n_hi - sp.n_lo;  // the new keys, relative to p0
     // One chunk: scores, softmax update, p * v.
     auto consume = [&](Chunk &ch, int c) {
-        // Whether the token's own key is among this wave's 16 (the same for
-        // the whole wave).
-        const bool new_here = sp.has_new && (unsigned)(pq_rel - (c * GCH + wave * WCH)) < (unsigned)WCH;
+        // Whether a new key is among this wave's 16 (the same for the whole
+        // wave).
+        const int cb = c * GCH + wave * WCH;
+        const bool new_here = sp.has_new && cb < nlo_rel + nnew && nlo_rel < cb + WCH;
         float sc[NS][G];
 #pragma unroll
         for (int s2 = 0; s2 < NS; s2++) {
@@ -350,11 +355,13 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
 #pragma unroll
             for (int i = 0; i < RB / 4; i++) kw[i] = ch.k[s2].w[i];
             float kscale = F16 ? 1.f : h2f(ch.ks[s2]);
-            if (new_here && key == pq_rel) {  // the token's own key, from LDS
+            if (new_here && (unsigned)(key - nlo_rel) < (unsigned)nnew) {  // a new key, from LDS
+                const int jj = key - nlo_rel;
 #pragma unroll
                 for (int i = 0; i < RB / 4; i++)
-                    kw[i] = F16 ? *(const uint32_t *)(S.new16[0] + d0 + 2 * i) : *(const uint32_t *)(S.new8[0] + d0 + 4 * i);
-                if constexpr (!F16) kscale = h2f(S.new_sc[0][d0 / 32]);
+                    kw[i] = F16 ? *(const uint32_t *)(S.new16[jj][0] + d0 + 2 * i)
+                                : *(const uint32_t *)(S.new8[jj][0] + d0 + 4 * i);
+                if constexpr (!F16) kscale = h2f(S.new_sc[jj][0][d0 / 32]);
             }
             float acc[G];
 #pragma unroll
@@ -420,11 +427,13 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
 #pragma unroll
             for (int i = 0; i < RB / 4; i++) vw[i] = ch.v[s2].w[i];
             float vscale = F16 ? 1.f : h2f(ch.vs[s2]);
-            if (new_here && key == pq_rel) {
+            if (new_here && (unsigned)(key - nlo_rel) < (unsigned)nnew) {
+                const int jj = key - nlo_rel;
 #pragma unroll
                 for (int i = 0; i < RB / 4; i++)
-                    vw[i] = F16 ? *(const uint32_t *)(S.new16[1] + d0 + 2 * i) : *(const uint32_t *)(S.new8[1] + d0 + 4 * i);
-                if constexpr (!F16) vscale = h2f(S.new_sc[1][d0 / 32]);
+                    vw[i] = F16 ? *(const uint32_t *)(S.new16[jj][1] + d0 + 2 * i)
+                                : *(const uint32_t *)(S.new8[jj][1] + d0 + 4 * i);
+                if constexpr (!F16) vscale = h2f(S.new_sc[jj][1][d0 / 32]);
             }
             float w[G];
 #pragma unroll

@@ -52,10 +52,10 @@ struct LdsSliceLds {
     float q_s[G][HD];
     __align__(16) float p_s[LDS_KT][G];  // scores, then probabilities
     float alpha_s[G], m_s[G], l_s[G], red[G];
-    float kv_s[2][HD];                    // the new token's K and V before rounding
-    __align__(16) int8_t new8[2][HD];     // ... and after, as int8
-    uint16_t new_sc[2][HD / 32];          // ... with their f16 scales
-    __align__(16) uint16_t new16[2][HD];  // ... or as f16 (an f16 cache)
+    float kv_s[1][2][HD];                    // the new token's K and V before rounding (one query: one new key)
+    __align__(16) int8_t new8[1][2][HD];     // ... and after, as int8
+    uint16_t new_sc[1][2][HD / 32];          // ... with their f16 scales
+    __align__(16) uint16_t new16[1][2][HD];  // ... or as f16 (an f16 cache)
     __align__(16) float o_s[NT / 64][G * HD];  // each wave's p * v sums
     __align__(16) float wts[G][ATTN_MAX_SPLIT];  // the merge's weight per (head, split), 0 past n_split
     int last;
@@ -117,8 +117,7 @@ __device__ inline void attn_slice_lds(const AttnArgs &a, int split, int kvh, int
             if constexpr (!F16) vsr[s2] = vsb[(int64_t)key * (HD / 32) + (8 * vc) / 32];
         }
         if (!prepared) {
-            const float *row = a.q + (int64_t)b * a.q_stride;
-            attn_prepare<HD, G, NT, F16>(a, kvh, sp, S, [&](int64_t e) { return row[e]; });
+            attn_prepare<HD, G, NT, F16>(a, kvh, b, sp, S);
             prepared = true;
             if (nt == 0) break;
         }
@@ -131,11 +130,11 @@ __device__ inline void attn_slice_lds(const AttnArgs &a, int split, int kvh, int
             if (sp.has_new && key == sp.pq) {
                 if constexpr (F16) {
 #pragma unroll
-                    for (int c = 0; c < NQ / 2; c++) kr[j].w[c] = *(const uint32_t *)(S.new16[0] + qq * NQ + 2 * c);
+                    for (int c = 0; c < NQ / 2; c++) kr[j].w[c] = *(const uint32_t *)(S.new16[0][0] + qq * NQ + 2 * c);
                 } else {
 #pragma unroll
-                    for (int c = 0; c < NQ / 4; c++) kr[j].w[c] = *(const uint32_t *)(S.new8[0] + qq * NQ + 4 * c);
-                    ks = h2f(S.new_sc[0][(qq * NQ) / 32]);
+                    for (int c = 0; c < NQ / 4; c++) kr[j].w[c] = *(const uint32_t *)(S.new8[0][0] + qq * NQ + 4 * c);
+                    ks = h2f(S.new_sc[0][0][(qq * NQ) / 32]);
                 }
             }
             float acc[G];
@@ -205,10 +204,10 @@ __device__ inline void attn_slice_lds(const AttnArgs &a, int split, int kvh, int
             float vs = F16 ? 1.f : h2f(vsr[s2]);
             if (sp.has_new && key == sp.pq) {
                 if constexpr (F16) {
-                    v8 = *(const LdsVRow<F16> *)(S.new16[1] + 8 * vc);
+                    v8 = *(const LdsVRow<F16> *)(S.new16[0][1] + 8 * vc);
                 } else {
-                    v8 = *(const LdsVRow<F16> *)(S.new8[1] + 8 * vc);
-                    vs = h2f(S.new_sc[1][(8 * vc) / 32]);
+                    v8 = *(const LdsVRow<F16> *)(S.new8[0][1] + 8 * vc);
+                    vs = h2f(S.new_sc[0][1][(8 * vc) / 32]);
                 }
             }
             float w[G];

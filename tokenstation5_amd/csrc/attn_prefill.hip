@@ -308,18 +308,35 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(PfArgs a) {
 
 // out[t][hh] = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s over the splits
 // that hold keys of row t (s * split_keys <= p0 + t), in split order.
+constexpr int PF_MAX_SPLIT = 64;  // partials a row can merge (k_attn_pf makes at most 16)
+
 template <int HD>
 __global__ __launch_bounds__(HD) void k_attn_pf_merge(PfArgs a) {
+    // The splits' weights 2^(m_s - M) and w_s l_s: wave 0, a lane per split;
+    // their sum in split order; then each thread's d over every split, its
+    // partials requested 16 at a time before they are added in split order.
+    __shared__ float wts[PF_MAX_SPLIT], wl[PF_MAX_SPLIT];
     const int row = blockIdx.x, t = row / a.H, d = threadIdx.x;
     const int ns = min(a.n_split, (a.p0 + t) / a.split_keys + 1);
     const float *p = a.part + (int64_t)row * a.n_split * (HD + 4);
-    float mx = -INFINITY;
-    for (int s = 0; s < ns; s++) mx = fmaxf(mx, p[s * (HD + 4)]);
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < ns; s++) {
-        const float w = exp2f(p[s * (HD + 4)] - mx);
-        num += w * p[s * (HD + 4) + 4 + d];
-        den += w * p[s * (HD + 4) + 1];
+    if (d < 64) {
+        const int sl = min(d, ns - 1);
+        const float ms = d < ns ? p[(int64_t)sl * (HD + 4)] : -INFINITY;
+        const float ls = p[(int64_t)sl * (HD + 4) + 1];
+        const float mx = wave_max(ms);
+        const float w = ms == -INFINITY ? 0.f : exp2f(ms - mx);
+        wts[d] = w, wl[d] = w * ls;
+    }
+    __syncthreads();
+    float den = 0.f, num = 0.f;
+    for (int s2 = 0; s2 < ns; s2++) den += wl[s2];
+    for (int s0 = 0; s0 < ns; s0 += 16) {
+        float o[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) o[j] = p[(int64_t)min(s0 + j, ns - 1) * (HD + 4) + 4 + d];
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+            if (s0 + j < ns) num += wts[s0 + j] * o[j];
     }
     a.out[(int64_t)row * HD + d] = num / den;
 }

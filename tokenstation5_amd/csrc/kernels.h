@@ -94,6 +94,9 @@ bool attn_supported(int H, int HKV, int HD);
 // Flash decode (attention.hip: k_attn). q rows of B queries; with rope each
 // row holds the token's raw q, k, v ((H + 2 HKV) HD values), and q (with
 // append, B == 1, also the token's K/V) gets bias / norm / RoPE here.
+// New keys a query of a batch on one cache reads from its workgroup's LDS
+// (append: batches of up to this many tokens round and append their own K/V).
+constexpr int ATTN_MAX_NEW = 16;
 struct AttnIO {
     const float *q;
     int64_t q_stride;

@@ -557,14 +557,25 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
         const float *bias = m->has_bias[l] ? m->bias + (int64_t)l * QR : nullptr;
         const float *qn = L.q_norm.set ? (const float *)L.q_norm.d : nullptr;
         const float *kn = L.k_norm.set ? (const float *)L.k_norm.d : nullptr;
-        TS5_HIP(ctx, launch_rope_kv(m->bqkv, QR, bias, qn, kn, eps, m->rope_cs, hp.rope_dims, hp.rope_neox, m->state,
-                                    H, HKV, HD, m->n_ctx, nc, m->bq, m->kv_layer(l), m->kv_f16(), s));
+        // Batches of up to ATTN_MAX_NEW tokens (verify steps) leave RoPE and the
+        // K/V append to the attention's work items; longer chunks round and
+        // append first (k_rope_kv) and read the cache.
+        const bool fused = nc <= ATTN_MAX_NEW;
+        if (!fused)
+            TS5_HIP(ctx, launch_rope_kv(m->bqkv, QR, bias, qn, kn, eps, m->rope_cs, hp.rope_dims, hp.rope_neox,
+                                        m->state, H, HKV, HD, m->n_ctx, nc, m->bq, m->kv_layer(l), m->kv_f16(), s));
         if (nc > 16 && !m->kv_f16() && attn_prefill_supported(H, HKV, HD)) {  // prompt chunks on the matrix cores
             TS5_HIP(ctx, launch_attn_prefill(m->bq, AH, m->kv_layer(l), m->n_ctx, H, HKV, HD, p0, nc, hp.attn_scale,
                                              m->bpart, m->batt, s));
         } else {
             AttnIO io{};
-            io.q = m->bq, io.q_stride = AH, io.rope = 0, io.append = 0;
+            if (fused) {
+                io.q = m->bqkv, io.q_stride = QR, io.rope = 1, io.append = 1;
+                io.bias = bias, io.q_norm = qn, io.k_norm = kn, io.eps = eps, io.rope_cs = m->rope_cs;
+                io.n_rot = hp.rope_dims, io.neox = hp.rope_neox;
+            } else {
+                io.q = m->bq, io.q_stride = AH, io.rope = 0, io.append = 0;
+            }
             io.kv = m->kv_layer(l), io.kv_f16 = m->kv_f16(), io.kv_per_batch = 0, io.n_ctx = m->n_ctx;
             io.n_keys = m->state, io.B = nc, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = attn_splits(nc, HKV, ctx->n_cu);
             io.scale = hp.attn_scale, io.part = m->bpart, io.counters = m->bcounters, io.out = m->batt;

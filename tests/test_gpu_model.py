@@ -201,6 +201,30 @@ def test_long_prompt_logits_and_greedy_match_oracle(ctx, name):
             break
 
 
+def test_small_batches_wide_ffn_match_oracle(ctx):
+    """Batches of 5, 3 and 1 tokens (the verify step's shapes) on a model whose
+    ffn is wider than the fused matmul's LDS input (4608 > 4096): the gate/up
+    writes the down projection's activation records itself and the down
+    projection reads them (no separate quantization launch); the attention
+    ropes and appends each batch's keys in its own work items. Every row's
+    logits against the oracle's, at the int8 paths' bar of the long-prompt
+    test (2e-3)."""
+    hp = dict(MODELS["tiny_llama_c"]["hparams"], n_ff=4608)
+    tensors = synth.model_tensors(hp, make_golden.MODEL_SEED)
+    m = ts5hip.Model(ctx, hp, 128, ts5hip.KV_Q8)
+    m.set_tensors(tensors)
+    ref = oracle.Model(hp, tensors, 128, 2)
+    toks = np.array([(11 + 7 * i + (i * i) % 13) % hp["n_vocab"] for i in range(49)], np.int32)
+    pos = 0
+    for n in (40, 5, 3, 1):
+        got = m.forward(toks[pos:pos + n], pos, all_logits=True)
+        want = ref.forward(toks[pos:pos + n], pos, all_logits=True)
+        err, cos = row_errors(got, want)
+        print(f"{n} tokens at {pos}: worst row {err.max():.2e}")
+        assert err.max() <= 2e-3 and cos.min() > 0.999, (n, pos, err.argmax(), err.max(), cos.min())
+        pos += n
+
+
 def test_forward_in_place_and_sampling(ctx):
     hp, _, m = load(ctx, "tiny_llama_c", 64)
     toks = np.array([3, 1, 4, 1, 5, 9, 2, 6], np.int32)

@@ -82,6 +82,10 @@ struct GemmArgs {
     const float *xin, *norm_w;
     int64_t xin_stride;
     float eps;
+    // k_gemm_mx only: the outputs also as the next matmul's activation
+    // records (mact_bytes(nrows) per token), row tiles then taken in pairs
+    // (a 32-row chunk a workgroup; nrows a multiple of 256). Null: none.
+    uint8_t *qout;
 };
 
 enum { G_STORE = 0, G_ADD = 1, G_GLU = 2 };
@@ -1039,7 +1043,12 @@ __global__ __launch_bounds__(64 * GX_WAVES) void k_gemm_mx(GemmArgs a) {
             for (int g = 0; g < 4; g++) w.q[m][g] = *(const uint64_t *)(p + 16 + 32 * g + 8 * kq);
         }
     };
-    auto rowbase = [&](int r) { return (int)(blockIdx.x + (unsigned)r * gridDim.x) * 16; };
+    // Row tile r of the workgroup: tile blockIdx.x + r gridDim.x, or with
+    // qout, tile 2 p + (r & 1) of pair p = blockIdx.x + (r / 2) gridDim.x.
+    auto rowbase = [&](int r) {
+        return a.qout ? (int)(2 * (blockIdx.x + (unsigned)(r >> 1) * gridDim.x) + (r & 1)) * 16
+                      : (int)(blockIdx.x + (unsigned)r * gridDim.x) * 16;
+    };
     // The input runs first (loads return in order), then the first item's
     // weights, all unconditional: tokens, rows, blocks and runs are clamped.
     const int half = wave >> 2, tb = half ? TH : 0, tn = half ? MT - TH : TH;
@@ -1149,30 +1158,53 @@ __global__ __launch_bounds__(64 * GX_WAVES) void k_gemm_mx(GemmArgs a) {
     __syncthreads();
     constexpr int E = RT * NA * 64;  // entries (row tile, token tile, lane)
     static_assert(E <= 64 * GX_WAVES, "one entry a thread");
-    if (tid >= E) return;
-    const int r = tid / (NA * 64), tt = (tid / 64) % NA, ln = tid & 63;
-    auto wsum = [&](int m, int lane) {
-        float v = 0.f;
+    float *ys = (float *)(lx + (size_t)a.M * tstride + (size_t)GX_WAVES * 2 * NW * WSLOT);  // qout: [MT][RT * 16]
+    if (tid < E) {
+        const int r = tid / (NA * 64), tt = (tid / 64) % NA, ln = tid & 63;
+        auto wsum = [&](int m, int lane) {
+            float v = 0.f;
 #pragma unroll
-        for (int w = 0; w < GX_WAVES; w++) v += red(w)[((r * NW + m) * NA + tt) * 64 + lane];
-        return v;
-    };
-    float v[NW];
+            for (int w = 0; w < GX_WAVES; w++) v += red(w)[((r * NW + m) * NA + tt) * 64 + lane];
+            return v;
+        };
+        float v[NW];
 #pragma unroll
-    for (int m = 0; m < NW; m++) {
-        if (P5 && tt == NT) {  // the fifth token: the four lane groups' shares of the row, (g0 + g1) + (g2 + g3)
-            const int lr = ln & 15;
-            v[m] = (wsum(m, lr) + wsum(m, lr + 16)) + (wsum(m, lr + 32) + wsum(m, lr + 48));
-        } else {
-            v[m] = wsum(m, ln);
+        for (int m = 0; m < NW; m++) {
+            if (P5 && tt == NT) {  // the fifth token: the four lane groups' shares of the row, (g0 + g1) + (g2 + g3)
+                const int lr = ln & 15;
+                v[m] = (wsum(m, lr) + wsum(m, lr + 16)) + (wsum(m, lr + 32) + wsum(m, lr + 48));
+            } else {
+                v[m] = wsum(m, ln);
+            }
+        }
+        const int row = rowbase(r) + (ln & 15), tok = tt == NT ? 4 : 4 * tt + (ln >> 4);
+        if (row < a.nrows && tok < a.M && (tt < NT || (ln >> 4) == 0)) {
+            const int64_t o = (int64_t)tok * a.ldy + row;
+            float y;
+            if (MODE == G_ADD) y = a.y_in[o] + v[0];
+            else if (MODE == G_GLU) y = v[0] / (1.0f + expf(-v[0])) * v[NW - 1];  // cpu_backend.cpp:260-261
+            else y = v[0];
+            a.out[o] = y;
+            if (a.qout) ys[(tok * RT + r) * 16 + (ln & 15)] = y;
         }
     }
-    const int row = rowbase(r) + (ln & 15), tok = tt == NT ? 4 : 4 * tt + (ln >> 4);
-    if (row >= a.nrows || tok >= a.M || (tt == NT && (ln >> 4) != 0)) return;
-    const int64_t o = (int64_t)tok * a.ldy + row;
-    if (MODE == G_ADD) a.out[o] = a.y_in[o] + v[0];
-    else if (MODE == G_GLU) a.out[o] = v[0] / (1.0f + expf(-v[0])) * v[NW - 1];  // cpu_backend.cpp:260-261
-    else a.out[o] = v[0];
+    if (a.qout) {
+        // Each (token, row tile) as a 16-value run of the next matmul's
+        // records: quant_run_m (the pairs of one 32-row chunk in adjacent
+        // lanes, RT even), as k_act_quant_m would write them from y.
+        static_assert(RT % 2 == 0 || RT == 1, "row tiles in pairs");
+        __syncthreads();
+        constexpr int MT = P5 ? 5 : 4;
+        if (tid < MT * RT) {
+            const int tok = tid / RT, run = tid % RT, row0 = rowbase(run);
+            if (tok < a.M && row0 < a.nrows) {
+                float v[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++) v[i] = ys[(tok * RT + run) * 16 + i];
+                quant_run_m(v, row0 / 16, a.qout + (int64_t)tok * mact_bytes(a.nrows));
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1301,26 +1333,34 @@ bool gemm_fused_fits(uint32_t t, int64_t ne0, int M) {
     return TS5_GM_FUSED && t == T_Q4_K && ne0 % 256 == 0 && ne0 <= 4096 && M >= 1 && M <= 5;
 }
 
+bool gemm_fused_qout_fits(int64_t ne0, int64_t ne1, int M) {
+    const int64_t pairs = (ne1 + 31) / 32, grid = std::min<int64_t>(pairs, g_gemm_m_cu);
+    return gemm_fused_fits(T_Q4_K, ne0, M) && TS5_GM_MX && ne1 % 256 == 0 && (pairs + grid - 1) / grid <= 2;
+}
+
 hipError_t launch_gemm_fused(const void *w, const void *w2, int64_t ne0, int64_t ne1, const float *x,
                              int64_t xstride, const float *norm_w, float eps, int M, int mode, float *y,
-                             const float *y_in, int64_t ldy, hipStream_t s) {
+                             const float *y_in, int64_t ldy, hipStream_t s, void *qout) {
     if (!gemm_fused_fits(T_Q4_K, ne0, M)) return hipErrorInvalidValue;
+    if (qout && !gemm_fused_qout_fits(ne0, ne1, M)) return hipErrorInvalidValue;
     GemmArgs a{};
     a.t = T_Q4_K, a.w = (const uint8_t *)w, a.w2 = (const uint8_t *)w2, a.nrows = (int)ne1;
     a.nb = (int)(ne0 / 256), a.n_in = (int)ne0, a.M = M, a.ks = 1, a.out = y, a.y_in = y_in, a.ldy = ldy;
-    a.xin = x, a.xin_stride = xstride, a.norm_w = norm_w, a.eps = eps;
+    a.xin = x, a.xin_stride = xstride, a.norm_w = norm_w, a.eps = eps, a.qout = (uint8_t *)qout;
     const size_t lds = (size_t)M * a.nb * MACT_BLOCK;
     const int tiles = (a.nrows + 15) / 16;
-    const unsigned grid = (unsigned)std::min(tiles, g_gemm_m_cu);
-    const int rt_mx = (tiles + (int)grid - 1) / (int)grid;
+    // qout: tiles in pairs, pairs gridDim.x apart (2 or 4 tiles a workgroup).
+    const int units = qout ? (tiles + 1) / 2 : tiles;
+    const unsigned grid = (unsigned)std::min(units, g_gemm_m_cu);
+    const int rt_mx = (qout ? 2 : 1) * ((units + (int)grid - 1) / (int)grid);
     if (TS5_GM_MX && rt_mx <= 4) {
         // One workgroup a CU (at most), each RT tiles gridDim.x apart; its
         // LDS: the records, then each wave's two weight slots of 16 rows x
         // 144 B per matrix (GLU: 72 KiB; with the records' 5 x 16 x 896 B
-        // under 160 KiB).
+        // under 160 KiB), then (qout) the outputs of its tiles.
         const int rtp = rt_mx > 2 ? 4 : rt_mx;
         const int nw = mode == G_GLU ? 2 : 1;
-        const size_t lds_mx = lds + (size_t)GX_WAVES * 2 * nw * 16 * Q4K_BYTES;
+        const size_t lds_mx = lds + (size_t)GX_WAVES * 2 * nw * 16 * Q4K_BYTES + (qout ? 5 * 4 * 16 * sizeof(float) : 0);
         auto go = [&](auto mode_c) {
             constexpr int MD = decltype(mode_c)::value;
             if (M == 5) launch_gemm_mx_tm<MD, 5>(a, rtp, grid, lds_mx, s);

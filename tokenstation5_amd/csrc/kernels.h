@@ -41,9 +41,13 @@ hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, i
 // activation built by each workgroup in LDS from the fp32 x [M][xstride]
 // (rms-normalised by norm_w first when given): no launch_gemm_act record.
 bool gemm_fused_fits(uint32_t t, int64_t ne0, int M);
+// qout (optional): the outputs also as launch_gemm_act's Q4_K records for
+// the next matmul (mact records of ne1 values per token, so that it needs
+// no launch_gemm_act); where gemm_fused_qout_fits.
+bool gemm_fused_qout_fits(int64_t ne0, int64_t ne1, int M);
 hipError_t launch_gemm_fused(const void *w, const void *w2, int64_t ne0, int64_t ne1, const float *x,
                              int64_t xstride, const float *norm_w, float eps, int M, int mode, float *y,
-                             const float *y_in, int64_t ldy, hipStream_t s);
+                             const float *y_in, int64_t ldy, hipStream_t s, void *qout = nullptr);
 
 // act.hip
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int ntok, float *y, hipStream_t s);

@@ -582,9 +582,20 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
             TS5_HIP(ctx, launch_attn(io, s));
         }
         if (int rc = proj(L.wo.type, L.wo.d, nullptr, AH, E, m->batt, AH, nullptr, nc, 1, m->bx, E)) return rc;
-        if (int rc = proj(L.gate.type, L.gate.d, L.up.d, E, F, m->bx, E, (const float *)L.ffn_norm.d, nc, 2, m->bffn, F))
-            return rc;
-        if (int rc = proj(L.down.type, L.down.d, nullptr, F, E, m->bffn, F, nullptr, nc, 1, m->bx, E)) return rc;
+        // A verify batch's gate/up also writes the down projection's
+        // activation records (no separate quantization launch between them).
+        const bool down_rec = L.gate.type == T_Q4_K && L.down.type == T_Q4_K && nc <= 5 &&
+                              gemm_fused_qout_fits(E, F, nc) && !gemm_fused_fits(L.down.type, F, nc);
+        if (down_rec) {
+            TS5_HIP(ctx, launch_gemm_fused(L.gate.d, L.up.d, E, F, m->bx, E, (const float *)L.ffn_norm.d, eps, nc, 2,
+                                           m->bffn, m->bffn, F, s, m->bact));
+            TS5_HIP(ctx, launch_gemm(L.down.type, L.down.d, nullptr, F, E, m->bact, nc, 1, m->bx, m->bx, E, m->bgemm, s));
+        } else {
+            if (int rc = proj(L.gate.type, L.gate.d, L.up.d, E, F, m->bx, E, (const float *)L.ffn_norm.d, nc, 2,
+                              m->bffn, F))
+                return rc;
+            if (int rc = proj(L.down.type, L.down.d, nullptr, F, E, m->bffn, F, nullptr, nc, 1, m->bx, E)) return rc;
+        }
     }
     if (rows) {
         const DevT &out = m->output.set ? m->output : m->tok_embd;

@@ -36,11 +36,11 @@ from tokenstation5_amd import synth, ts5hip  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the roofline kernel, from rocprofv3 --pmc runs of
 # `bench.py --roofline-only` (profiles/glu_roofline_counters.md): FETCH_SIZE
-# 32,481.4 KiB and WRITE_SIZE 448 KiB per dispatch, scaled by what the same
+# 32,477.4 KiB and WRITE_SIZE 448 KiB per dispatch, scaled by what the same
 # counters read for the one-pass RMSNorm stream of 256 MiB in and 256 MiB out
-# (131,217.1 and 262,144 KiB: factors 1.9978 and 1.0). 1.011 x the algorithmic
+# (131,237.4 and 262,144 KiB: factors 1.9975 and 1.0). 1.011 x the algorithmic
 # bytes.
-GLU_TRAFFIC_BYTES = 66907183
+GLU_TRAFFIC_BYTES = 66888639
 PROMPT = 4096
 SEED = 20241201
 

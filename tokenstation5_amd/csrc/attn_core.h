@@ -10,8 +10,13 @@
 #define TS5_ATTN_KMIN 128
 #endif
 
+#ifndef TS5_ATTN_DEPTH
+#define TS5_ATTN_DEPTH 2
+#endif
+
 namespace ts5hip {
 constexpr int ATTN_MIN_KEYS = TS5_ATTN_KMIN;
+constexpr int ATTN_DEPTH = TS5_ATTN_DEPTH;  // chunks of K and V in flight per wave (attn_slice)
 
 // x0*c - x1*s and x0*s + x1*c with separate roundings, as the reference's
 // scalar float code computes them (engine/src/cpu_backend.cpp:63-64).
@@ -230,12 +235,23 @@ template <int HD, int G, int NT = 256>
 struct SliceLds {
     float q_s[G][HD];
     float m_s[G], l_s[G], red[G];
-    float kv_s[ATTN_MAX_NEW][2][HD];                     // the new keys' K and V before rounding
-    __align__(16) int8_t new8[ATTN_MAX_NEW][2][HD];     // ... and after, as int8
-    uint16_t new_sc[ATTN_MAX_NEW][2][HD / 32];          // ... with their f16 scales
-    __align__(16) uint16_t new16[ATTN_MAX_NEW][2][HD];  // ... or as f16 (an f16 cache)
-    __align__(16) float o_w[NT / 64][G][HD];  // each wave's o
-    float m_w[NT / 64][G], l_w[NT / 64][G];   // ... and (m, l)
+    // The new keys' K and V before rounding live until the preparation's
+    // last barrier; the waves' results are written after it: one space.
+    union {
+        float kv_s[ATTN_MAX_NEW][2][HD];
+        struct {
+            __align__(16) float o_w[NT / 64][G][HD];  // each wave's o
+            float m_w[NT / 64][G], l_w[NT / 64][G];   // ... and (m, l)
+        };
+    };
+    // The rounded new keys: int8 with f16 scales (a q8 cache) or f16.
+    union {
+        struct {
+            __align__(16) int8_t new8[ATTN_MAX_NEW][2][HD];
+            uint16_t new_sc[ATTN_MAX_NEW][2][HD / 32];
+        };
+        __align__(16) uint16_t new16[ATTN_MAX_NEW][2][HD];
+    };
     __align__(16) float wts[G][ATTN_MAX_SPLIT];  // the merge's weight per (head, split), 0 past n_split
     int last;
 };
@@ -324,9 +340,9 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
             }
         }
     };
-    Chunk A, B;
-    request(A, 0);
-    request(B, 1);
+    Chunk buf[ATTN_DEPTH];
+#pragma unroll
+    for (int i = 0; i < ATTN_DEPTH; i++) request(buf[i], i);
     attn_prepare<HD, G, NT, F16>(a, kvh, b, sp, S);
     float q[G][DPL], o[G][DPL], m[G], l[G];
 #pragma unroll
@@ -446,16 +462,17 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
             }
         }
     };
-    // Two register buffers in turn, both requested before the query is
-    // prepared; each is refilled with the chunk two on as soon as it is
-    // consumed (past the slice: no memory access).
+    // ATTN_DEPTH register buffers in turn, all requested before the query
+    // is prepared; each is refilled with the chunk ATTN_DEPTH on as soon as
+    // it is consumed (past the slice: no memory access).
     const int nch = (nkeys + GCH - 1) / GCH;
-    for (int c = 0; c < nch; c += 2) {
-        consume(A, c);
-        if (c + 1 >= nch) break;
-        request(A, c + 2);
-        consume(B, c + 1);
-        request(B, c + 3);
+    for (int c = 0; c < nch; c += ATTN_DEPTH) {
+#pragma unroll
+        for (int i = 0; i < ATTN_DEPTH; i++) {
+            if (c + i >= nch) break;
+            consume(buf[i], c + i);
+            request(buf[i], c + i + ATTN_DEPTH);
+        }
     }
     // The key slots of a wave hold the same dims: add them over lanes i ^ 32,
     // i ^ 16 (and i ^ 8 within a 16-lane row when LPK is 8) by a butterfly

@@ -486,6 +486,36 @@ def test_attention_verify_batch(ctx, n_split):
         assert rel_l2(got[b], want) <= REL_L2, (b, rel_l2(got[b], want))
 
 
+@pytest.mark.parametrize("B,H,HKV,n_ctx,p0,n_split", [(2, 32, 8, 4400, 4300, 32), (8, 32, 8, 3000, 2990, 32),
+                                                     (16, 8, 8, 1200, 1100, 16), (16, 16, 8, 700, 600, 0),
+                                                     (6, 40, 8, 2100, 2000, 40), (4, 64, 8, 900, 800, 7),
+                                                     (5, 32, 8, 64, 10, 32), (5, 32, 8, 300, 0, 1),
+                                                     (3, 4, 1, 5000, 4096, 64), (5, 32, 8, 4200, 4094, 61)])
+def test_attention_batch_matrix_cores(ctx, B, H, HKV, n_ctx, p0, n_split):
+    """One cache, 2-16 consecutive queries, B x G <= 32 rows of head
+    dimension 128: the batch's queries together in each work item, on the
+    matrix cores (fp16 hi + lo query and p planes, exact int8 keys and
+    values), against the oracle to 2e-5: G 1-8, splits from 1 (one work
+    item writes the output) to 64, short slices, keys from position 0,
+    split boundaries between the batch's queries."""
+    rng = np.random.default_rng(B * 31 + H + n_ctx + n_split)
+    HD = 128
+    q8, sc, deq = q8_cache(rng, 1, HKV, n_ctx, HD)
+    v8, vsc, vdeq = q8_cache(rng, 1, HKV, n_ctx, HD)
+    q = (rng.standard_normal((B, H * HD)) * 2).astype(np.float32)
+    scale = float(np.float32(1) / np.sqrt(np.float32(HD)))
+    out = ctx.alloc(q.nbytes)
+    ctx.attn_decode(ctx.to_device(q), B, H, HKV, HD, ctx.to_device(q8), ctx.to_device(sc), ctx.to_device(v8),
+                    ctx.to_device(vsc), n_ctx, ctx.to_device(np.array([p0], np.int32)), 0, scale, out,
+                    n_split=n_split)
+    got = out.download(np.float32, (B, H * HD))
+    kc = deq[0].transpose(1, 0, 2).reshape(n_ctx, HKV * HD)
+    vc = vdeq[0].transpose(1, 0, 2).reshape(n_ctx, HKV * HD)
+    for b in range(B):
+        want = oracle.attention(q[b], kc, vc, H, HKV, HD, p0 + b, scale)
+        assert rel_l2(got[b], want) <= 2e-5, (b, rel_l2(got[b], want))
+
+
 def test_attention_causal_batch(ctx):
     """kv_per_batch = 0: query b at position p0 + b sees keys 0..p0+b."""
     rng = np.random.default_rng(6)

@@ -19,6 +19,11 @@
 #include <mutex>
 
 #include "attn_lds.h"
+#include "attn_mq.h"
+
+#ifndef TS5_ATTN_MQ
+#define TS5_ATTN_MQ 1
+#endif
 
 namespace ts5hip {
 
@@ -128,6 +133,27 @@ __global__ __launch_bounds__(ATTN_NT) void k_attn(const int8_t *k8, const uint16
     a.n_keys = n_keys, a.n_ctx = n_ctx, a.HKV = HKV;
     a.kv_per_batch = flags & 1, a.append = (flags >> 1) & 1, a.rope = (flags >> 2) & 1;
     attn_slice<HD, G, ATTN_NT, F16>(a, blockIdx.x, blockIdx.y, blockIdx.z, n_split, S);
+}
+
+// A batch of B consecutive queries on one q8 cache, B x G <= 32 rows of
+// head dimension 128: every query of the batch in one work item per (split,
+// KV head), on the matrix cores (attn_mq.h).
+__global__ __launch_bounds__(MQ_NT) void k_attn_mq(const int8_t *k8, const uint16_t *ks, const int8_t *v8,
+                                                   const uint16_t *vs, const int32_t *n_keys, int n_ctx, int HKV,
+                                                   int flags, int n_split, int G, int B, AttnArgs tail) {
+    __shared__ MqLds S;
+    AttnArgs a = tail;
+    a.kv = KvLayer{const_cast<int8_t *>(k8), const_cast<uint16_t *>(ks), const_cast<int8_t *>(v8),
+                   const_cast<uint16_t *>(vs)};
+    a.n_keys = n_keys, a.n_ctx = n_ctx, a.HKV = HKV;
+    a.kv_per_batch = 0, a.append = (flags >> 1) & 1, a.rope = (flags >> 2) & 1;
+    attn_mq(a, G, B, blockIdx.x, blockIdx.y, n_split, S);
+}
+// Its splits' merge: grid (B x G rows, HKV), a thread per dimension.
+__global__ __launch_bounds__(MQ_HD) void k_attn_mq_merge(const int32_t *n_keys, int n_split, int G, int B,
+                                                         AttnArgs a) {
+    a.n_keys = n_keys;
+    attn_mq_merge(a, G, B, n_split, blockIdx.x, blockIdx.y);
 }
 
 // K (which 0) or V (1) at positions [pos0, pos0 + n) dequantized to fp32
@@ -263,6 +289,11 @@ static hipError_t attn_launch(int G, dim3 grid, const AttnArgs &a, hipStream_t s
     return hipGetLastError();
 }
 
+bool attn_mq_fits(int B, int H, int HKV, int HD, int kv_f16, int kv_per_batch) {
+    return TS5_ATTN_MQ && !kv_f16 && !kv_per_batch && HD == MQ_HD && HKV > 0 && H % HKV == 0 && B >= 2 &&
+           B <= ATTN_MAX_NEW && B * (H / HKV) <= MQ_ROWS;
+}
+
 bool attn_supported(int H, int HKV, int HD) {
     if (HKV <= 0 || H % HKV) return false;
     const int G = H / HKV;
@@ -278,8 +309,18 @@ hipError_t launch_attn(const AttnIO &io, hipStream_t s) {
     a.rope = io.rope, a.append = io.append, a.kv = io.kv, a.kv_per_batch = io.kv_per_batch, a.n_ctx = io.n_ctx;
     a.H = io.H, a.HKV = io.HKV, a.n_keys = io.n_keys, a.scale = io.scale, a.part = io.part;
     a.counters = io.counters, a.out = io.out;
-    const dim3 grid(io.n_split, io.HKV, io.B);
     const int G = io.H / io.HKV;
+    if (attn_mq_fits(io.B, io.H, io.HKV, io.HD, io.kv_f16, io.kv_per_batch)) {
+        const int flags = (a.append ? 2 : 0) | (a.rope ? 4 : 0);
+        hipLaunchKernelGGL(k_attn_mq, dim3(io.n_split, io.HKV), dim3(MQ_NT), 0, s, (const int8_t *)a.kv.k,
+                           (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs, a.n_keys,
+                           a.n_ctx, a.HKV, flags, io.n_split, G, io.B, a);
+        if (io.n_split > 1)
+            hipLaunchKernelGGL(k_attn_mq_merge, dim3(io.B * G, io.HKV), dim3(MQ_HD), 0, s, a.n_keys, io.n_split, G,
+                               io.B, a);
+        return hipGetLastError();
+    }
+    const dim3 grid(io.n_split, io.HKV, io.B);
     if (io.kv_f16) return io.HD == 128 ? attn_launch<128, true>(G, grid, a, s) : attn_launch<64, true>(G, grid, a, s);
     return io.HD == 128 ? attn_launch<128, false>(G, grid, a, s) : attn_launch<64, false>(G, grid, a, s);
 }

@@ -61,15 +61,6 @@ struct PfLds {
     uint2 vl[HD][PF_KB / 4];       // V^T lo
 };
 
-__device__ inline float max_xor16(float v) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ inline float max_xor32(float v) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
 // Raw block at key kb (keys past n_ctx read the last slot; they are masked).
 template <int HD>
 __device__ inline void pf_issue(const PfArgs &a, PfLds<HD> &L, int64_t slot0, int kb, int wave, int lane) {

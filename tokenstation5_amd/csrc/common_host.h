@@ -57,6 +57,12 @@ inline int attn_splits(int B, int n_head_kv, int slots) {
     const int s = slots / (B * n_head_kv);
     return s < 1 ? 1 : (s > 64 ? 64 : s);  // at most 64 (the merge's table)
 }
+// Key splits of the multi-query batch attention: one work item a CU over the
+// KV heads (all the batch's queries in each).
+inline int attn_mq_splits(int n_head_kv, int slots) {
+    const int s = slots / n_head_kv;
+    return s < 1 ? 1 : (s > 64 ? 64 : s);
+}
 inline size_t attn_partial_bytes(int B, int n_split, int H, int HKV, int HD) {
     return (size_t)B * n_split * HKV * attn_group_floats(H / HKV, HD) * sizeof(float);
 }

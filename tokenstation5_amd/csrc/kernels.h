@@ -120,6 +120,11 @@ struct AttnIO {
     float *out;     // [B][H * HD]
 };
 hipError_t launch_attn(const AttnIO &io, hipStream_t s);
+// Whether launch_attn takes the batch's queries together on the matrix cores
+// (one q8 cache, 2..ATTN_MAX_NEW queries, B x G <= 32, head dimension 128);
+// its partials fit attn_partial_bytes(B, n_split, ...) as the per-query
+// kernel's do, with the split count from attn_mq_splits.
+bool attn_mq_fits(int B, int H, int HKV, int HD, int kv_f16, int kv_per_batch);
 // The no-allocation entry point's scratch: a static device array of
 // NOALLOC_BYTES per GPU, merge counters first (up to 4096 (query, KV head)
 // pairs, CTR_STRIDE ints apart), then up to NOALLOC_BYTES -

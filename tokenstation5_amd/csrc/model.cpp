@@ -494,6 +494,9 @@ int ensure_batch(ts5hip_model *m) {
         }
         g(hp.n_vocab, E, out.type);
         part = std::max(part, attn_partial_bytes(M, attn_splits(M, hp.n_head_kv, m->ctx->n_cu), hp.n_head, hp.n_head_kv, hp.head_dim));
+        if (attn_mq_fits(M, hp.n_head, hp.n_head_kv, hp.head_dim, m->kv_f16(), 0))
+            part = std::max(part, attn_partial_bytes(M, attn_mq_splits(hp.n_head_kv, m->ctx->n_cu), hp.n_head,
+                                                     hp.n_head_kv, hp.head_dim));
     }
     part = std::max(part, attn_prefill_partial_bytes(CHUNK, hp.n_head, hp.head_dim, m->n_ctx));
     int rc = 0;
@@ -577,7 +580,7 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
                 io.q = m->bq, io.q_stride = AH, io.rope = 0, io.append = 0;
             }
             io.kv = m->kv_layer(l), io.kv_f16 = m->kv_f16(), io.kv_per_batch = 0, io.n_ctx = m->n_ctx;
-            io.n_keys = m->state, io.B = nc, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = attn_splits(nc, HKV, ctx->n_cu);
+            io.n_keys = m->state, io.B = nc, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = attn_mq_fits(nc, H, HKV, HD, io.kv_f16, 0) ? attn_mq_splits(HKV, ctx->n_cu) : attn_splits(nc, HKV, ctx->n_cu);
             io.scale = hp.attn_scale, io.part = m->bpart, io.counters = m->bcounters, io.out = m->batt;
             TS5_HIP(ctx, launch_attn(io, s));
         }

@@ -407,19 +407,28 @@ __device__ inline void attn_mq(const AttnArgs &a, int G, int B, int split, int k
         if (kq == 0) S.m_w[wave][r] = m[qt], S.l_w[wave][r] = l[qt];
     }
     __syncthreads();
-    // The work item's (m, l, O) per row from its waves'.
-    auto item = [&](int r, int d, float &M, float &L) {
-        M = S.m_w[0][r];
+    // The work item's (m, l) per row from its waves' (a thread per row; the
+    // waves' weights 2^(m_w - M) overwrite their m), then its O.
+    if (tid < MQ_ROWS) {
+        const int r = tid;
+        float M = S.m_w[0][r];
 #pragma unroll
         for (int w = 1; w < MQ_NW; w++) M = fmaxf(M, S.m_w[w][r]);
-        float Ov = 0.f;
-        L = 0.f;
+        float L = 0.f;
 #pragma unroll
         for (int w = 0; w < MQ_NW; w++) {
             const float wt = S.m_w[w][r] == -INFINITY ? 0.f : exp2f(S.m_w[w][r] - M);
-            Ov += wt * S.o_w[w][r][4 + d];
             L += wt * S.l_w[w][r];
+            S.m_w[w][r] = wt;
         }
+        S.l_w[0][r] = M, S.l_w[1][r] = L;
+    }
+    __syncthreads();
+    auto item = [&](int r, int d, float &M, float &L) {
+        float Ov = 0.f;
+#pragma unroll
+        for (int w = 0; w < MQ_NW; w++) Ov += S.m_w[w][r] * S.o_w[w][r][4 + d];
+        M = S.l_w[0][r], L = S.l_w[1][r];
         return Ov;
     };
     auto out_at = [&](int r, int d) -> float * {
@@ -458,7 +467,7 @@ __device__ inline void attn_mq_merge(const AttnArgs &a, int G, int B, int n_spli
     if (used == 1) return;
     const int64_t sstride = (int64_t)a.HKV * R * MQ_REC;
     const float *p = a.part + ((int64_t)kvh * R + r) * MQ_REC;
-    constexpr int SB = 16;  // splits whose values are requested with the weights
+    constexpr int SB = 32;  // splits whose values are requested with the weights
     float o[SB];
 #pragma unroll
     for (int j = 0; j < SB; j++) o[j] = p[min(j, used - 1) * sstride + 4 + d];

@@ -309,15 +309,15 @@ hipError_t launch_attn(const AttnIO &io, hipStream_t s) {
     a.rope = io.rope, a.append = io.append, a.kv = io.kv, a.kv_per_batch = io.kv_per_batch, a.n_ctx = io.n_ctx;
     a.H = io.H, a.HKV = io.HKV, a.n_keys = io.n_keys, a.scale = io.scale, a.part = io.part;
     a.counters = io.counters, a.out = io.out;
+    a.act_out = (uint8_t *)io.act_out, a.act_stride = io.act_stride;
     const int G = io.H / io.HKV;
     if (attn_mq_fits(io.B, io.H, io.HKV, io.HD, io.kv_f16, io.kv_per_batch)) {
         const int flags = (a.append ? 2 : 0) | (a.rope ? 4 : 0);
         hipLaunchKernelGGL(k_attn_mq, dim3(io.n_split, io.HKV), dim3(MQ_NT), 0, s, (const int8_t *)a.kv.k,
                            (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs, a.n_keys,
                            a.n_ctx, a.HKV, flags, io.n_split, G, io.B, a);
-        if (io.n_split > 1)
-            hipLaunchKernelGGL(k_attn_mq_merge, dim3(io.B * G, io.HKV), dim3(MQ_HD), 0, s, a.n_keys, io.n_split, G,
-                               io.B, a);
+        hipLaunchKernelGGL(k_attn_mq_merge, dim3(io.B * G, io.HKV), dim3(MQ_HD), 0, s, a.n_keys, io.n_split, G, io.B,
+                           a);
         return hipGetLastError();
     }
     const dim3 grid(io.n_split, io.HKV, io.B);

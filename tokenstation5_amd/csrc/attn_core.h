@@ -63,6 +63,8 @@ struct AttnArgs {
     float *part;    // [B][n_split][HKV] groups of G records [HD + 2], attn_group_floats(G, HD) floats apart
     int *counters;  // [B * HKV] at CTR_STRIDE ints apart, zero between launches
     float *out;     // [B][H * HD]
+    uint8_t *act_out;    // or null: the output also as matmul activation records (multi-query kernel)
+    int64_t act_stride;  // bytes between tokens' records
 };
 
 __device__ inline void rope_inplace(float *v, int n_rot, int neox, const float2 *cs, int i) {

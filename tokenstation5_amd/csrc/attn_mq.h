@@ -23,7 +23,8 @@
 //     registers).
 //  3. The waves' (m, l, O) combine in LDS into the work item's partial;
 //     a second launch (a workgroup per row and KV head) merges the splits'
-//     partials in split order: O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+//     partials in split order: O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s,
+//     and can write the output as the next matmul's activation records too.
 #pragma once
 #include "attn_core.h"
 
@@ -431,18 +432,8 @@ __device__ inline void attn_mq(const AttnArgs &a, int G, int B, int split, int k
         M = S.l_w[0][r], L = S.l_w[1][r];
         return Ov;
     };
-    auto out_at = [&](int r, int d) -> float * {
-        return a.out + (int64_t)(r / G) * a.H * MQ_HD + (int64_t)(kvh * G + r % G) * MQ_HD + d;
-    };
-    if (used == 1) {  // the only work item: the output directly
-        for (int j = tid; j < R * MQ_HD; j += MQ_NT) {
-            float M, L;
-            const float Ov = item(j / MQ_HD, j % MQ_HD, M, L);
-            *out_at(j / MQ_HD, j % MQ_HD) = L > 0.f ? Ov / L : 0.f;
-        }
-        return;
-    }
-    // The partial, merged by k_attn_mq_merge (the next launch on the stream).
+    // The partial, merged by k_attn_mq_merge (the next launch on the stream;
+    // also with one used split).
     float *rec = a.part + ((int64_t)split * a.HKV + kvh) * R * MQ_REC;
     for (int j = tid; j < R * MQ_HD; j += MQ_NT) {
         const int r = j / MQ_HD, d = j % MQ_HD;
@@ -455,16 +446,16 @@ __device__ inline void attn_mq(const AttnArgs &a, int G, int B, int split, int k
 // 3. The merge of the used splits' partials for row r of KV head kvh (one
 // workgroup, a thread per dimension): out = sum_s 2^(m_s - M) O_s /
 // sum_s 2^(m_s - M) l_s in split order (attn_merge.comp:18-47), every
-// split's value requested before any is added. One used split: its work
-// item wrote the output itself.
+// split's value requested before any is added; with act_out, the head's 128
+// values also as 8 runs of the token's activation records (quant_run_m, as
+// k_act_quant_m writes them).
 __device__ inline void attn_mq_merge(const AttnArgs &a, int G, int B, int n_split, int r, int kvh) {
-    __shared__ float wts[ATTN_MAX_SPLIT], wl[ATTN_MAX_SPLIT];
+    __shared__ float wts[ATTN_MAX_SPLIT], wl[ATTN_MAX_SPLIT], ov[MQ_HD];
     const int d = threadIdx.x, R = B * G;
     const int nk = a.n_keys[0] + B;
     int chunk = (nk + n_split - 1) / n_split;
     chunk = (chunk + MQ_STEP - 1) / MQ_STEP * MQ_STEP;
     const int used = (nk + chunk - 1) / chunk;
-    if (used == 1) return;
     const int64_t sstride = (int64_t)a.HKV * R * MQ_REC;
     const float *p = a.part + ((int64_t)kvh * R + r) * MQ_REC;
     constexpr int SB = 32;  // splits whose values are requested with the weights
@@ -490,7 +481,18 @@ __device__ inline void attn_mq_merge(const AttnArgs &a, int G, int B, int n_spli
         for (int j = 0; j < SB; j++)
             if (s0 + j < used) num += wts[s0 + j] * o[j];
     }
-    a.out[(int64_t)(r / G) * a.H * MQ_HD + (int64_t)(kvh * G + r % G) * MQ_HD + d] = den > 0.f ? num / den : 0.f;
+    const float res = den > 0.f ? num / den : 0.f;
+    const int b = r / G, h = kvh * G + r % G;
+    a.out[(int64_t)b * a.H * MQ_HD + (int64_t)h * MQ_HD + d] = res;
+    if (!a.act_out) return;
+    ov[d] = res;
+    __syncthreads();
+    if (d < MQ_HD / 16) {  // runs 8 h .. 8 h + 7, pairs in adjacent lanes
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = ov[16 * d + i];
+        quant_run_m(v, (MQ_HD / 16) * h + d, a.act_out + (int64_t)b * a.act_stride);
+    }
 }
 
 }  // namespace ts5hip

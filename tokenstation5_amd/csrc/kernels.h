@@ -118,6 +118,11 @@ struct AttnIO {
     float *part;    // attn_partial_bytes(B, n_split, H, HKV, HD), 128-byte aligned
     int *counters;  // B * HKV * CTR_STRIDE ints, zero before the first launch (kept zero after)
     float *out;     // [B][H * HD]
+    // Or null: with attn_mq_fits, the output also as the Q4_K small-batch
+    // matmul's activation records of the H * HD values, act_stride bytes a
+    // token (the next projection then reads them instead of quantizing).
+    void *act_out;
+    int64_t act_stride;
 };
 hipError_t launch_attn(const AttnIO &io, hipStream_t s);
 // Whether launch_attn takes the batch's queries together on the matrix cores

@@ -23,6 +23,10 @@
 #include "kernels.h"
 #include "runtime.h"
 
+#ifndef TS5_WO_REC
+#define TS5_WO_REC 1
+#endif
+
 using namespace ts5hip;
 
 namespace {
@@ -564,6 +568,10 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
         // K/V append to the attention's work items; longer chunks round and
         // append first (k_rope_kv) and read the cache.
         const bool fused = nc <= ATTN_MAX_NEW;
+        // Up to 5 tokens with the multi-query attention: it also writes wo's
+        // activation records, and wo runs on them (k_gemm_mw).
+        const bool wo_rec = TS5_WO_REC && fused && nc <= 5 && L.wo.type == T_Q4_K && AH % 256 == 0 &&
+                            attn_mq_fits(nc, H, HKV, HD, m->kv_f16(), 0);
         if (!fused)
             TS5_HIP(ctx, launch_rope_kv(m->bqkv, QR, bias, qn, kn, eps, m->rope_cs, hp.rope_dims, hp.rope_neox,
                                         m->state, H, HKV, HD, m->n_ctx, nc, m->bq, m->kv_layer(l), m->kv_f16(), s));
@@ -582,9 +590,15 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
             io.kv = m->kv_layer(l), io.kv_f16 = m->kv_f16(), io.kv_per_batch = 0, io.n_ctx = m->n_ctx;
             io.n_keys = m->state, io.B = nc, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = attn_mq_fits(nc, H, HKV, HD, io.kv_f16, 0) ? attn_mq_splits(HKV, ctx->n_cu) : attn_splits(nc, HKV, ctx->n_cu);
             io.scale = hp.attn_scale, io.part = m->bpart, io.counters = m->bcounters, io.out = m->batt;
+            // A verify batch's attention also writes wo's activation records.
+            if (wo_rec) io.act_out = m->bact, io.act_stride = (int64_t)gemm_act_bytes(L.wo.type, AH, nc);
             TS5_HIP(ctx, launch_attn(io, s));
         }
-        if (int rc = proj(L.wo.type, L.wo.d, nullptr, AH, E, m->batt, AH, nullptr, nc, 1, m->bx, E)) return rc;
+        if (wo_rec) {
+            TS5_HIP(ctx, launch_gemm(L.wo.type, L.wo.d, nullptr, AH, E, m->bact, nc, 1, m->bx, m->bx, E, m->bgemm, s));
+        } else if (int rc = proj(L.wo.type, L.wo.d, nullptr, AH, E, m->batt, AH, nullptr, nc, 1, m->bx, E)) {
+            return rc;
+        }
         // A verify batch's gate/up also writes the down projection's
         // activation records (no separate quantization launch between them).
         const bool down_rec = L.gate.type == T_Q4_K && L.down.type == T_Q4_K && nc <= 5 &&

@@ -5,13 +5,14 @@
 // query; merge attn_merge.comp:18-47), with every query of the batch in one
 // work item, so that each key is read and converted once for all of them.
 //
-// Grid (n_split, HKV), four waves. Row r = G b + g is head g of KV head kvh
+// Grid (n_split, HKV), 8 waves (two sets of 4, 16 rows each; with
+// TS5_MQ_QT 2 one set of 4 with all 32). Row r = G b + g is head g of KV head kvh
 // for token b (position n0 + b, keys [0, n0 + b]); rows B G .. 31 are empty.
 //  1. Preparation: the rows' queries (bias, per-head norm, RoPE when `rope`)
 //     into LDS; with `append`, the batch's new keys in this key slice (K with
 //     RoPE at its own position, V) rounded to q8 and stored at their cache
 //     slots, then read back with the slice like every other key.
-//  2. Each wave takes 16 keys of every 64-key step of the slice:
+//  2. Each wave of a set takes 16 keys of every 64-key step of the slice:
 //     S^T (16 keys x 32 rows) = K . Q^T on v_mfma_f32_16x16x32_f16 per
 //     32-value scale group: K as exact fp16 integers, the rows as fp16 hi +
 //     lo planes of q * scale * log2(e) * 2^-e (e per row), then S += ks * R;
@@ -37,8 +38,14 @@ typedef float mq_f4 __attribute__((ext_vector_type(4)));
 
 constexpr int MQ_HD = 128;
 constexpr int MQ_ROWS = 32;           // two 16-row MFMA tiles
-constexpr int MQ_NW = 4, MQ_NT = 64 * MQ_NW;
-constexpr int MQ_STEP = 16 * MQ_NW;   // keys of a workgroup step
+#ifndef TS5_MQ_QT
+#define TS5_MQ_QT 1
+#endif
+constexpr int MQ_QT = TS5_MQ_QT;      // 16-row tiles a wave (the rows of a wave set)
+constexpr int MQ_KG = 4;              // waves of a set, each 16 keys of a step
+constexpr int MQ_NW = MQ_KG * (MQ_ROWS / 16 / MQ_QT), MQ_NT = 64 * MQ_NW;
+constexpr int MQ_WR = 16 * MQ_QT;     // rows a wave
+constexpr int MQ_STEP = 16 * MQ_KG;   // keys of a workgroup step
 constexpr int MQ_REC = MQ_HD + 4;     // partial record: m, l, -, -, O[128]
 constexpr int MQ_VT = 10;             // dwords per dim of a wave's V^T (4 key quads + padding)
 
@@ -48,10 +55,10 @@ struct MqLds {
             float q_s[MQ_ROWS][MQ_HD];             // the rows' queries, prepared
             float kv_s[ATTN_MAX_NEW][2][MQ_HD];    // the slice's new keys before rounding
         };
-        __align__(16) float o_w[MQ_NW][MQ_ROWS][MQ_REC];  // each wave's O rows, after the keys
+        __align__(16) float o_w[MQ_NW][MQ_WR][MQ_REC];  // each wave's O rows, after the keys
     };
     __align__(16) uint32_t vt[MQ_NW][MQ_HD * MQ_VT];  // each wave's 16 keys' V^T, [d][key quad] as f16
-    float m_w[MQ_NW][MQ_ROWS], l_w[MQ_NW][MQ_ROWS];
+    float m_w[MQ_NW][MQ_WR], l_w[MQ_NW][MQ_WR];
 };
 
 // 8 int8 -> 8 exact fp16: 0x64xx is 1024 + xx, so (b + 128) in the low byte
@@ -78,10 +85,11 @@ __device__ inline void mq_prepare(const AttnArgs &a, int kvh, int G, int B, int 
     const int R = B * G;
     const int nlo = max(n0, p0), nhi = a.append ? min(n0 + B, p1) : nlo, nn = max(nhi - nlo, 0);
     constexpr int F4 = MQ_HD / 4;                       // float4s a row
-    constexpr int QK = MQ_ROWS * F4 / MQ_NT;            // query float4s a thread (4)
-    constexpr int KK = ATTN_MAX_NEW * 2 * F4 / MQ_NT;   // new-key float4s a thread (4)
-    constexpr int QP = MQ_ROWS * (MQ_HD / 2) / MQ_NT;   // query RoPE pairs a thread (8)
-    constexpr int KP = ATTN_MAX_NEW * (MQ_HD / 2) / MQ_NT;  // key RoPE pairs a thread (4)
+    constexpr int QK = MQ_ROWS * F4 / MQ_NT;            // query float4s a thread
+    constexpr int KK = ATTN_MAX_NEW * 2 * F4 / MQ_NT;   // new-key float4s a thread
+    constexpr int QP = MQ_ROWS * (MQ_HD / 2) / MQ_NT;   // query RoPE pairs a thread
+    constexpr int KP = ATTN_MAX_NEW * (MQ_HD / 2) / MQ_NT;  // key RoPE pairs a thread
+    static_assert(QK * MQ_NT == MQ_ROWS * F4 && KK * MQ_NT == ATTN_MAX_NEW * 2 * F4, "whole rows a pass");
     const int nr2 = a.n_rot / 2;
     float4 qv[QK], kv[KK];
     float2 qcs[QP], kcs[KP];
@@ -203,6 +211,7 @@ __device__ inline void attn_mq(const AttnArgs &a, int G, int B, int split, int k
     constexpr float LOG2E = 1.4426950408889634f;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rl = lane & 15, kq = lane >> 4;
+    const int kg = wave % MQ_KG, rbase = (wave / MQ_KG) * MQ_WR;  // the wave's keys of a step, its first row
     const int R = B * G;
     const int n0 = a.n_keys[0], nk = n0 + B;  // the last query reads keys [0, nk)
     int chunk = (nk + n_split - 1) / n_split;
@@ -227,7 +236,7 @@ __device__ inline void attn_mq(const AttnArgs &a, int G, int B, int split, int k
         u32x4 ks[2], vs[2];
     };
     auto load = [&](Step &w, int st) {
-        const uint32_t kl = (uint32_t)(st * MQ_STEP + wave * 16);
+        const uint32_t kl = (uint32_t)(st * MQ_STEP + kg * 16);
 #pragma unroll
         for (int c = 0; c < 4; c++) w.k[c] = __builtin_amdgcn_raw_buffer_load_b64(rk, (kl + rl) * MQ_HD + 32 * c + 8 * kq, 0, 0);
 #pragma unroll
@@ -246,14 +255,14 @@ __device__ inline void attn_mq(const AttnArgs &a, int G, int B, int split, int k
     mq_prepare(a, kvh, G, B, n0, p0, p1, S);
 
     if (fresh) load(A, 0), load(Bs, 1);
-    // The lane's rows (its MFMA columns) 16 qt + rl as B operands: dims
-    // 32 c + 8 kq .. + 7 of q * scale * log2(e) * 2^-e, hi and lo.
-    mq_h8 qh[2][4], ql[2][4];
-    float p2e[2];
-    int pos[2];
+    // The lane's rows (its MFMA columns) rbase + 16 qt + rl as B operands:
+    // dims 32 c + 8 kq .. + 7 of q * scale * log2(e) * 2^-e, hi and lo.
+    mq_h8 qh[MQ_QT][4], ql[MQ_QT][4];
+    float p2e[MQ_QT];
+    int pos[MQ_QT];
 #pragma unroll
-    for (int qt = 0; qt < 2; qt++) {
-        const int r = 16 * qt + rl;
+    for (int qt = 0; qt < MQ_QT; qt++) {
+        const int r = rbase + 16 * qt + rl;
         pos[qt] = r < R ? n0 + r / G : -1;  // empty rows take no key
         float v[4][8], amax = 0.f;
 #pragma unroll
@@ -278,17 +287,17 @@ __device__ inline void attn_mq(const AttnArgs &a, int G, int B, int split, int k
             }
     }
 
-    mq_f4 O[2][8];
-    float m[2], l[2];
+    mq_f4 O[MQ_QT][8];
+    float m[MQ_QT], l[MQ_QT];
 #pragma unroll
-    for (int qt = 0; qt < 2; qt++) {
+    for (int qt = 0; qt < MQ_QT; qt++) {
         m[qt] = -INFINITY, l[qt] = 0.f;
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) O[qt][dt] = mq_f4{0.f, 0.f, 0.f, 0.f};
     }
     uint32_t *vt = S.vt[wave];
     auto step = [&](const Step &w, int st) {
-        const int kl = st * MQ_STEP + wave * 16;
+        const int kl = st * MQ_STEP + kg * 16;
         // Scales: halfword 4 i + c of the pair of u32x4 is key kl + 4 kq + i, group c.
         float ksf[4][4], vsf[4][4];
 #pragma unroll
@@ -299,13 +308,13 @@ __device__ inline void attn_mq(const AttnArgs &a, int G, int B, int split, int k
                 ksf[i][c] = h2f((w.ks[hw >> 3][(hw >> 1) & 3] >> (16 * (hw & 1))) & 0xffff);
                 vsf[i][c] = 128.f * h2f((w.vs[hw >> 3][(hw >> 1) & 3] >> (16 * (hw & 1))) & 0xffff);
             }
-        // S^T: D[key 4 kq + i][row 16 qt + rl].
-        float s[2][4];
+        // S^T: D[key 4 kq + i][row rbase + 16 qt + rl].
+        float s[MQ_QT][4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const mq_h8 ka = mq_i8x8(w.k[c][0], w.k[c][1]);
 #pragma unroll
-            for (int qt = 0; qt < 2; qt++) {
+            for (int qt = 0; qt < MQ_QT; qt++) {
                 mq_f4 Rr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[qt][c], mq_f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                 Rr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[qt][c], Rr, 0, 0, 0);
 #pragma unroll
@@ -331,9 +340,9 @@ __device__ inline void attn_mq(const AttnArgs &a, int G, int B, int split, int k
         }
         // Online softmax per row (log2 domain), then the B operands
         // (P o vs of group g) as hi + lo.
-        mq_h4 ph[2][4], pl[2][4];
+        mq_h4 ph[MQ_QT][4], pl[MQ_QT][4];
 #pragma unroll
-        for (int qt = 0; qt < 2; qt++) {
+        for (int qt = 0; qt < MQ_QT; qt++) {
             float mx = -INFINITY;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -379,7 +388,7 @@ __device__ inline void attn_mq(const AttnArgs &a, int G, int B, int split, int k
         for (int dt = 0; dt < 8; dt++) {
             const mq_h4 va = *(const mq_h4 *)&vt[(16 * dt + rl) * MQ_VT + 2 * kq];
 #pragma unroll
-            for (int qt = 0; qt < 2; qt++) {
+            for (int qt = 0; qt < MQ_QT; qt++) {
                 O[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph[qt][dt >> 1], O[qt][dt], 0, 0, 0);
                 O[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl[qt][dt >> 1], O[qt][dt], 0, 0, 0);
             }
@@ -398,9 +407,10 @@ __device__ inline void attn_mq(const AttnArgs &a, int G, int B, int split, int k
     }
     __syncthreads();  // every wave is past its reads of q_s: o_w overlays it
 
-    // The waves' rows: O^T[d = 16 dt + 4 kq + i][row 16 qt + rl].
+    // The waves' rows: O^T[d = 16 dt + 4 kq + i][row rbase + 16 qt + rl], at
+    // the wave's local row 16 qt + rl.
 #pragma unroll
-    for (int qt = 0; qt < 2; qt++) {
+    for (int qt = 0; qt < MQ_QT; qt++) {
         const int r = 16 * qt + rl;
 #pragma unroll
         for (int dt = 0; dt < 8; dt++)
@@ -410,26 +420,28 @@ __device__ inline void attn_mq(const AttnArgs &a, int G, int B, int split, int k
     __syncthreads();
     // The work item's (m, l) per row from its waves' (a thread per row; the
     // waves' weights 2^(m_w - M) overwrite their m), then its O.
+    // Row r is local row r % MQ_WR of the MQ_KG waves of set r / MQ_WR.
     if (tid < MQ_ROWS) {
-        const int r = tid;
-        float M = S.m_w[0][r];
+        const int w0 = (tid / MQ_WR) * MQ_KG, lr = tid % MQ_WR;
+        float M = S.m_w[w0][lr];
 #pragma unroll
-        for (int w = 1; w < MQ_NW; w++) M = fmaxf(M, S.m_w[w][r]);
+        for (int w = 1; w < MQ_KG; w++) M = fmaxf(M, S.m_w[w0 + w][lr]);
         float L = 0.f;
 #pragma unroll
-        for (int w = 0; w < MQ_NW; w++) {
-            const float wt = S.m_w[w][r] == -INFINITY ? 0.f : exp2f(S.m_w[w][r] - M);
-            L += wt * S.l_w[w][r];
-            S.m_w[w][r] = wt;
+        for (int w = 0; w < MQ_KG; w++) {
+            const float wt = S.m_w[w0 + w][lr] == -INFINITY ? 0.f : exp2f(S.m_w[w0 + w][lr] - M);
+            L += wt * S.l_w[w0 + w][lr];
+            S.m_w[w0 + w][lr] = wt;
         }
-        S.l_w[0][r] = M, S.l_w[1][r] = L;
+        S.l_w[w0][lr] = M, S.l_w[w0 + 1][lr] = L;
     }
     __syncthreads();
     auto item = [&](int r, int d, float &M, float &L) {
+        const int w0 = (r / MQ_WR) * MQ_KG, lr = r % MQ_WR;
         float Ov = 0.f;
 #pragma unroll
-        for (int w = 0; w < MQ_NW; w++) Ov += S.m_w[w][r] * S.o_w[w][r][4 + d];
-        M = S.l_w[0][r], L = S.l_w[1][r];
+        for (int w = 0; w < MQ_KG; w++) Ov += S.m_w[w0 + w][lr] * S.o_w[w0 + w][lr][4 + d];
+        M = S.l_w[w0][lr], L = S.l_w[w0 + 1][lr];
         return Ov;
     };
     // The partial, merged by k_attn_mq_merge (the next launch on the stream;

@@ -4,14 +4,18 @@
 //                 (engine/src/cpu_backend.cpp:57-68, :198-221), then for K and
 //                 V heads the q8 rounding of round_kv (:78-90) written as int8
 //                 quants + f16 scales (the split layout of qkv_post.glsl:29-41).
-//                 (kept for batches of tokens: their K/V must all be in the
+//                 (kept for prompt chunks: their K/V must all be in the
 //                 cache before any of them attends).
-//  k_attn         split-K flash decode: per (key slice, KV head) one
-//                 workgroup scores its G = H/HKV query heads against 64-key
-//                 tiles with an online softmax (attn.glsl:54-162); for one
-//                 decode token it also does that token's RoPE and q8 append,
-//                 and the last workgroup per KV head merges the splits
-//                 (attn_merge.comp:18-47).
+//  k_attn_lds,    split-K flash decode: per (key slice, KV head, query) one
+//  k_attn         workgroup scores its G = H/HKV query heads against 64-key
+//                 tiles with an online softmax (attn.glsl:54-162); it also
+//                 does the RoPE and q8 append of the new keys in its slice,
+//                 and the last workgroup per (query, KV head) merges the
+//                 splits (attn_merge.comp:18-47).
+//  k_attn_mq,     the same for a batch of 2-16 consecutive queries on one q8
+//  k_attn_mq_merge cache (B x G <= 32 rows, head dimension 128): all the
+//                 batch's queries in each (key slice, KV head) work item, on
+//                 the matrix cores, and the splits merged by a second launch.
 //
 // Cache layout per layer: K8/V8 int8 [seq][kv_head][slot][head_dim] and
 // Ks/Vs f16 [seq][kv_head][slot][head_dim/32]: one KV head's keys are

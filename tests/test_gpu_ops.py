@@ -280,13 +280,15 @@ def test_q4k_small_batch_matmul(ctx, M, ne0, rows, mode):
         assert rel_l2(got[k], want[k]) <= 2e-6, (k, rel_l2(got[k], want[k]))
 
 
-@pytest.mark.parametrize("M", [1, 2, 4, 5, 6])
-@pytest.mark.parametrize("ne0,rows,mode", [(4096, 1000, "store"), (512, 515, "add"), (4096, 20000, "store")])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 6])
+@pytest.mark.parametrize("ne0,rows,mode", [(4096, 1000, "store"), (512, 515, "add"), (4096, 20000, "store"),
+                                           (4096, 40008, "store")])
 def test_q6k_small_batch_matmul(ctx, M, ne0, rows, mode):
-    """The Q6_K matmul of 1-6 tokens (k_gemm_m up to 5 tokens with centred
-    quants and two MFMAs per 32 values, k_gemm_small past it): every token's
-    rows within 2e-6 relative L2 of the oracle; 20000 rows take the 4-tile
-    workgroups of the verify batch's head (a ragged last workgroup)."""
+    """The Q6_K matmul of 1-6 tokens (up to 5: centred quants and two MFMAs
+    per 32 values, on k_gemm_mh without a residual, k_gemm_m with one;
+    k_gemm_small past it): every token's rows within 2e-6 relative L2 of the
+    oracle; a ragged last row tile, and (40008 rows, 2501 tiles) more tiles
+    than the launch has waves, as the verify batch's head has."""
     rng = np.random.default_rng(M * 1000 + rows)
     W = synth.tensor(synth.Q6_K, ne0, rows, 23, f"q6sb{ne0}_{rows}")
     x = rng.standard_normal((M, ne0)).astype(np.float32)

@@ -46,6 +46,9 @@
 #ifndef TS5_GM_MX
 #define TS5_GM_MX 1
 #endif
+#ifndef TS5_GM_MH
+#define TS5_GM_MH 1  // the verify batch's Q6_K head on k_gemm_mh
+#endif
 #ifndef TS5_GM_MW
 #define TS5_GM_MW 1
 #endif
@@ -1314,6 +1317,114 @@ __global__ __launch_bounds__(64 * GX_WAVES) void k_gemm_mw(GemmArgs a) {
     wait_vm_n<0>();  // the last (repeated) requests are in before the waves end
 }
 
+// ---------------------------------------------------------------------------
+// Q6_K rows for 1-5 tokens over activation records (the verify batch's head,
+// 128256 x 4096): one workgroup of 8 waves a CU holds the M tokens' records
+// of all nb blocks in LDS; each wave takes whole 16-row tiles (tile
+// blockIdx.x * 8 + wave, then every 8 gridDim.x-th), item by item over the
+// blocks, each item's 16 rows x 208 bytes and their 16 f16 scales brought
+// into the wave's LDS slot by DMA one item ahead; no cross-wave sums.
+// ---------------------------------------------------------------------------
+__device__ inline void dma4b(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds_base) {
+    asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds_base) : "memory");
+}
+constexpr int MH_SLOT = 16 * Q6K_BODY + 64;  // 16 rows' bodies, then their scales (a dword each)
+static size_t gemm_mh_lds(int M, int nb) { return (size_t)M * nb * MACT_BLOCK + (size_t)GX_WAVES * 2 * MH_SLOT; }
+
+template <int TM>
+__global__ __launch_bounds__(64 * GX_WAVES) void k_gemm_mh(GemmArgs a) {
+    constexpr int FMT = F_Q6K, NW = 1, NT = 1;
+    constexpr bool P5 = TM == 5;
+    static_assert(TM == 1 || TM == 5, "small-batch head: up to 5 tokens");
+    constexpr int NA = NT + (P5 ? 1 : 0);
+    extern __shared__ __align__(16) uint8_t lh[];  // the records [M][nb][896], then each wave's 2 slots
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l = tid & 63, kq = l >> 4, rl = l & 15;
+    const int nb = a.nb, ntile = (a.nrows + 15) / 16;
+    const int rstride = nb * MACT_BLOCK;  // a token's records in LDS
+    uint8_t *rec = lh, *wst = lh + (size_t)a.M * rstride + (size_t)wave * 2 * MH_SLOT;
+    const int64_t nblocks = (int64_t)a.nrows * nb;
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(a.w, (uint32_t)(nblocks * Q6K_BODY));  // past the last row: zeros
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.s, (uint32_t)(nblocks * 2));
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a.act, (uint32_t)(a.M * a.act_stride));
+    // Weight pieces: c = 64 i + lane (the fourth request: lanes 0-15), row
+    // c / 13, bytes 16 (c % 13); lanes 0-15 also bring row lane's scale (the
+    // aligned dword that holds it).
+    uint32_t coff[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = min(64 * i + l, 207);
+        coff[i] = (uint32_t)((c / 13) * nb * Q6K_BODY + 16 * (c % 13));
+    }
+    auto issue = [&](int tile, int b, int slot) {
+        uint32_t wb = ((uint32_t)tile * 16 * nb + b) * Q6K_BODY, sb = (uint32_t)tile * 16 * nb + b;
+        asm volatile("" : "+s"(wb), "+s"(sb));  // opaque: the per-lane sums are formed here
+        uint8_t *dst = wst + slot * MH_SLOT;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (i < 3 || l < 16) dma16b(rw, wb + coff[i], lds_addr(dst + 1024 * i));
+        if (l < 16) dma4b(rs, ((sb + (uint32_t)l * nb) * 2) & ~3u, lds_addr(dst + 16 * Q6K_BODY));
+    };
+    // The records (pieces p of M * nb * 56, 16 bytes each, in order), then
+    // the first item; all in before any wave reads the records.
+    const int npieces = a.M * nb * (MACT_BLOCK / 16), tpc = nb * (MACT_BLOCK / 16);
+    for (int k = 0; 64 * GX_WAVES * k < npieces; k++) {
+        const int p = 64 * GX_WAVES * k + tid;
+        if (p < npieces)
+            dma16b(ra, (uint32_t)((p / tpc) * a.act_stride + 16 * (p % tpc)),
+                   lds_addr(rec + 16 * (64 * GX_WAVES * k + 64 * wave)));
+    }
+    const int gw = blockIdx.x * GX_WAVES + wave, nwv = gridDim.x * GX_WAVES;
+    issue(min(gw, ntile - 1), 0, 0);
+    wait_vm_n<0>();
+    __syncthreads();
+    int sl = 0;
+    for (int tile = gw; tile < ntile; tile += nwv) {
+        const bool rin = tile * 16 + rl < a.nrows;
+        float acc[NW][NA];
+#pragma unroll
+        for (int tt = 0; tt < NA; tt++) acc[0][tt] = 0.f;
+        for (int b = 0; b < nb; b++) {
+            // The next item: the next block, or the next tile's first (past
+            // the wave's last tile a repeat, in bounds and unused).
+            const bool lastb = b + 1 >= nb;
+            const int ntl = lastb ? min(tile + nwv, ntile - 1) : tile;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(ntl, lastb ? 0 : b + 1, sl ^ 1);
+            wait_vm_n<5>();  // this item's 5 requests are in
+            MAFrag<FMT, NT, P5> xc;
+            load_mafrag_at<FMT, NT, P5>(rec, rstride, a.M, b, l, xc);
+            gm_prescale<FMT, NT, P5>(xc, kq);
+            MWFrag<FMT, NW> w;
+            const uint8_t *src = wst + sl * MH_SLOT;
+            const uint8_t *body = src + Q6K_BODY * rl;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                w.ql[0][h][0] = *(const uint64_t *)(body + 64 * h + 8 * kq);
+                w.ql[0][h][1] = *(const uint64_t *)(body + 64 * h + 32 + 8 * kq);
+                w.qh[0][h] = *(const uint64_t *)(body + 128 + 32 * h + 8 * kq);
+            }
+            w.sc[0] = *(const uint4 *)(body + 192);
+            const uint32_t dw = *(const uint32_t *)(src + 16 * Q6K_BODY + 4 * rl);
+            const uint32_t idx = (uint32_t)(tile * 16 + rl) * nb + b;
+            w.d[0] = h2f((dw >> (16 * (idx & 1))) & 0xffff);
+            gm_item<FMT, NW, NT, P5, NA>(w, xc, acc, rin, kq);
+            TS5_GM_SB();  // one item at a time
+            sl ^= 1;
+        }
+        // Row tile * 16 + lane % 16; token 4 tt + lane / 16, and with P5 the
+        // fifth token's four lane groups added ((g0 + g1) + (g2 + g3)).
+#pragma unroll
+        for (int tt = 0; tt < NA; tt++) {
+            float v = acc[0][tt];
+            if (P5 && tt == NT) v = add_xor32(add_xor16(v));
+            const int row = tile * 16 + rl, tok = tt == NT ? 4 : 4 * tt + kq;
+            if (row < a.nrows && tok < a.M && (tt < NT || kq == 0)) a.out[(int64_t)tok * a.ldy + row] = v;
+        }
+    }
+    wait_vm_n<0>();  // the last (repeated) requests are in before the waves end
+}
+
 template <int MODE, int TM>
 static void launch_gemm_mx_tm(const GemmArgs &a, int rt, unsigned grid, size_t lds, hipStream_t s) {
     if (rt == 4) hipLaunchKernelGGL((k_gemm_mx<MODE, TM, 4>), dim3(grid), dim3(64 * GX_WAVES), lds, s, a);
@@ -1495,6 +1606,15 @@ static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
                 const dim3 g((unsigned)std::min(tiles, g_gemm_m_cu)), blk(64 * GX_WAVES);
                 if (a.M == 5) hipLaunchKernelGGL((k_gemm_mw<MODE, 5>), g, blk, lds, s, a);
                 else hipLaunchKernelGGL((k_gemm_mw<MODE, 1>), g, blk, lds, s, a);
+                return hipGetLastError();
+            }
+        if constexpr (FMT == F_Q6K && MODE == G_STORE)
+            if (use_m && TS5_GM_MH && a.M <= 5 && a.ks == 1 && gemm_mh_lds(a.M, a.nb) <= 160 * 1024) {
+                const int tiles = (a.nrows + 15) / 16;
+                const dim3 g((unsigned)std::min((tiles + GX_WAVES - 1) / GX_WAVES, g_gemm_m_cu)), blk(64 * GX_WAVES);
+                const size_t lds = gemm_mh_lds(a.M, a.nb);
+                if (a.M == 5) hipLaunchKernelGGL((k_gemm_mh<5>), g, blk, lds, s, a);
+                else hipLaunchKernelGGL((k_gemm_mh<1>), g, blk, lds, s, a);
                 return hipGetLastError();
             }
         if (use_m && gemm_m_fits<FMT, MODE>(a.M)) return launch_gemm_m<FMT, MODE>(a, s);

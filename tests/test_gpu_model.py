@@ -225,6 +225,27 @@ def test_small_batches_wide_ffn_match_oracle(ctx):
         pos += n
 
 
+def test_small_batches_qwen2_head_dim_128_match_oracle(ctx):
+    """The verify batches' matrix-core attention on a qwen2-style model (q/k/v
+    biases, NeoX RoPE at base 1e6) with head dimension 128 and 4 query heads
+    per KV head: a prompt, then batches of 5, 3 and 2 tokens and one token,
+    every row's logits against the oracle's at the long-prompt test's bar."""
+    hp = dict(MODELS["tiny_draft_c"]["hparams"], head_dim=128, n_head=4, n_head_kv=1)
+    tensors = synth.model_tensors(hp, make_golden.MODEL_SEED)
+    m = ts5hip.Model(ctx, hp, 128, ts5hip.KV_Q8)
+    m.set_tensors(tensors)
+    ref = oracle.Model(hp, tensors, 128, 2)
+    toks = np.array([(5 + 11 * i + (i * i) % 17) % hp["n_vocab"] for i in range(41)], np.int32)
+    pos = 0
+    for n in (30, 5, 3, 2, 1):
+        got = m.forward(toks[pos:pos + n], pos, all_logits=True)
+        want = ref.forward(toks[pos:pos + n], pos, all_logits=True)
+        err, cos = row_errors(got, want)
+        print(f"{n} tokens at {pos}: worst row {err.max():.2e}")
+        assert err.max() <= 2e-3 and cos.min() > 0.999, (n, pos, err.argmax(), err.max(), cos.min())
+        pos += n
+
+
 def test_forward_in_place_and_sampling(ctx):
     hp, _, m = load(ctx, "tiny_llama_c", 64)
     toks = np.array([3, 1, 4, 1, 5, 9, 2, 6], np.int32)

@@ -67,14 +67,6 @@ struct AttnArgs {
     int64_t act_stride;  // bytes between tokens' records
 };
 
-__device__ inline void rope_inplace(float *v, int n_rot, int neox, const float2 *cs, int i) {
-    const int a = neox ? i : 2 * i, b = neox ? i + n_rot / 2 : 2 * i + 1;
-    float x0 = v[a], x1 = v[b];
-    rope_pair(x0, x1, cs[i].x, cs[i].y);
-    v[a] = x0;
-    v[b] = x1;
-}
-
 constexpr int ATTN_MAX_SPLIT = 64;
 constexpr int ATTN_TILE = 64;
 
@@ -109,29 +101,92 @@ __device__ inline AttnSpan attn_span(const AttnArgs &a, int split, int kvh, int 
     return sp;
 }
 
+// Inputs of the preparation of one query with at most one new key, loaded
+// ahead (attn_preload) so that they return before loads issued after them:
+// thread t's query values t, t + NT, ..., its values of the new key's K and V,
+// and the RoPE table entries of its query and key pairs.
+template <int HD, int G, int NT>
+struct AttnPre {
+    static constexpr int QK = (G * HD + NT - 1) / NT, KK = (2 * HD + NT - 1) / NT;
+    static constexpr int QP = (G * (HD / 2) + NT - 1) / NT, KP = (HD / 2 + NT - 1) / NT;
+    float q[QK], kv[KK];
+    float2 qcs[QP], kcs[KP];
+};
+template <int HD, int G, int NT>
+__device__ inline void attn_preload(const AttnArgs &a, int kvh, int b, const AttnSpan &sp, AttnPre<HD, G, NT> &p) {
+    using P = AttnPre<HD, G, NT>;
+    const int tid = threadIdx.x, pq = sp.pq, nn = sp.n_hi - sp.n_lo, nr2 = a.n_rot / 2;
+    const float *qrow = a.q + (int64_t)b * a.q_stride;
+#pragma unroll
+    for (int k = 0; k < P::QK; k++) {
+        const int j = tid + NT * k;
+        const int64_t e = (int64_t)(kvh * G + min(j, G * HD - 1) / HD) * HD + j % HD;
+        p.q[k] = j < G * HD ? qrow[e] + (a.rope && a.bias ? a.bias[e] : 0.f) : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < P::KK; k++) {
+        const int j = tid + NT * k, which = (j / HD) & 1, d = j % HD;
+        const int64_t e = (int64_t)((which ? a.H + a.HKV : a.H) + kvh) * HD + d;
+        p.kv[k] = j < nn * 2 * HD ? qrow[e] + (a.bias ? a.bias[e] : 0.f) : 0.f;  // the new key is query b's own
+    }
+    if (a.rope) {
+#pragma unroll
+        for (int k = 0; k < P::QP; k++) {
+            const int i = (tid + NT * k) % (HD / 2);
+            p.qcs[k] = tid + NT * k < G * (HD / 2) && i < nr2 ? a.rope_cs[(int64_t)pq * nr2 + i] : make_float2(1.f, 0.f);
+        }
+#pragma unroll
+        for (int k = 0; k < P::KP; k++) {
+            const int i = tid + NT * k;
+            p.kcs[k] = i < nn * nr2 ? a.rope_cs[(int64_t)sp.n_lo * nr2 + i] : make_float2(1.f, 0.f);
+        }
+    }
+}
+
 // 1. The G query heads of KV head kvh into LDS from query b's row; bias,
 //    per-head norm and RoPE when a.rope. Then each new key of the slice
 //    (n_lo .. n_hi - 1; the rows of those tokens, query b's row for key pq),
 //    rounded as the cache keeps it (q8, or f16 with F16) into LDS slot
 //    j - n_lo, and query b's own (pq) stored at its cache slot.
+//    With `pre`: the query's inputs from there, and the new key's when the
+//    slice's only new key is the query's own.
 template <int HD, int G, int NT, bool F16, class Lds>
-__device__ inline void attn_prepare(const AttnArgs &a, int kvh, int b, const AttnSpan &sp, Lds &S) {
+__device__ inline void attn_prepare(const AttnArgs &a, int kvh, int b, const AttnSpan &sp, Lds &S,
+                                    const AttnPre<HD, G, NT> *pre = nullptr) {
+    using P = AttnPre<HD, G, NT>;
     constexpr int NWV = NT / 64;
     auto &q_s = S.q_s;
     auto &kv_s = S.kv_s;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pq = sp.pq;
     const int nn = sp.n_hi - sp.n_lo;  // new keys in the slice, prepared together with the query
+    const bool pre_kv = pre && (nn == 0 || (nn == 1 && sp.n_lo == pq));
     const float *qrow = a.q + (int64_t)b * a.q_stride;
-    for (int j = tid; j < G * HD; j += NT) {
-        const int64_t e = (int64_t)(kvh * G + j / HD) * HD + j % HD;
-        q_s[j / HD][j % HD] = qrow[e] + (a.rope && a.bias ? a.bias[e] : 0.f);
+    if (pre) {
+#pragma unroll
+        for (int k = 0; k < P::QK; k++) {
+            const int j = tid + NT * k;
+            if (j < G * HD) q_s[j / HD][j % HD] = pre->q[k];
+        }
+    } else {
+        for (int j = tid; j < G * HD; j += NT) {
+            const int64_t e = (int64_t)(kvh * G + j / HD) * HD + j % HD;
+            q_s[j / HD][j % HD] = qrow[e] + (a.rope && a.bias ? a.bias[e] : 0.f);
+        }
     }
-    for (int j = tid; j < nn * 2 * HD; j += NT) {
-        const int kk = j / (2 * HD), which = (j / HD) & 1, d = j % HD;
-        const float *row = a.q + (int64_t)(b - (pq - (sp.n_lo + kk))) * a.q_stride;  // the token at that position
-        const int64_t e = (int64_t)((which ? a.H + a.HKV : a.H) + kvh) * HD + d;
-        kv_s[kk][which][d] = row[e] + (a.bias ? a.bias[e] : 0.f);
+    if (pre_kv) {
+#pragma unroll
+        for (int k = 0; k < P::KK; k++) {
+            const int j = tid + NT * k;
+            if (j < nn * 2 * HD) kv_s[0][(j / HD) & 1][j % HD] = pre->kv[k];
+        }
+    } else {
+        for (int j = tid; j < nn * 2 * HD; j += NT) {
+            const int kk = j / (2 * HD), which = (j / HD) & 1, d = j % HD;
+            const float *row = a.q + (int64_t)(b - (pq - (sp.n_lo + kk))) * a.q_stride;  // the token at that position
+            const int64_t e = (int64_t)((which ? a.H + a.HKV : a.H) + kvh) * HD + d;
+            kv_s[kk][which][d] = row[e] + (a.bias ? a.bias[e] : 0.f);
+        }
     }
     if (tid < G) {
         S.m_s[tid] = -INFINITY;
@@ -155,14 +210,36 @@ __device__ inline void attn_prepare(const AttnArgs &a, int kvh, int b, const Att
             __syncthreads();
         }
         const int nr2 = a.n_rot / 2;
-        for (int j = tid; j < G * (HD / 2); j += NT) {
-            const int g = j / (HD / 2), i = j % (HD / 2);
-            if (i < nr2) rope_inplace(q_s[g], a.n_rot, a.neox, a.rope_cs + (int64_t)pq * nr2, i);
+        auto rot = [&](float *v, int i, float2 cs) {
+            const int i0 = a.neox ? i : 2 * i, i1 = a.neox ? i + nr2 : 2 * i + 1;
+            float x0 = v[i0], x1 = v[i1];
+            rope_pair(x0, x1, cs.x, cs.y);
+            v[i0] = x0, v[i1] = x1;
+        };
+        if (pre) {
+#pragma unroll
+            for (int k = 0; k < P::QP; k++) {
+                const int j = tid + NT * k, i = j % (HD / 2);
+                if (j < G * (HD / 2) && i < nr2) rot(q_s[j / (HD / 2)], i, pre->qcs[k]);
+            }
+        } else {
+            for (int j = tid; j < G * (HD / 2); j += NT) {
+                const int g = j / (HD / 2), i = j % (HD / 2);
+                if (i < nr2) rot(q_s[g], i, a.rope_cs[(int64_t)pq * nr2 + i]);
+            }
         }
         __syncthreads();
-        for (int j = tid; j < nn * nr2; j += NT) {
-            const int kk = j / nr2, i = j % nr2;
-            rope_inplace(kv_s[kk][0], a.n_rot, a.neox, a.rope_cs + (int64_t)(sp.n_lo + kk) * nr2, i);
+        if (pre_kv) {
+#pragma unroll
+            for (int k = 0; k < P::KP; k++) {
+                const int i = tid + NT * k;
+                if (i < nn * nr2) rot(kv_s[0][0], i, pre->kcs[k]);
+            }
+        } else {
+            for (int j = tid; j < nn * nr2; j += NT) {
+                const int kk = j / nr2, i = j % nr2;
+                rot(kv_s[kk][0], i, a.rope_cs[(int64_t)(sp.n_lo + kk) * nr2 + i]);
+            }
         }
         __syncthreads();
     }

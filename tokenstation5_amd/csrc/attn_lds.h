@@ -96,6 +96,11 @@ __device__ inline void attn_slice_lds(const AttnArgs &a, int split, int kvh, int
     for (int g = 0; g < G; g++)
 #pragma unroll
         for (int e = 0; e < 8; e++) o[g][e] = 0.f;
+    // The query's (and its new key's) inputs are requested first: loads
+    // complete in order, so the preparation then runs while the slice's K/V
+    // (requested next) are still arriving.
+    AttnPre<HD, G, NT> pre;
+    attn_preload<HD, G, NT>(a, kvh, b, sp, pre);
     bool prepared = false;
     for (int t0 = sp.p0; t0 < sp.p1 || !prepared; t0 += LDS_KT) {
         const int nt = max(0, min(LDS_KT, sp.p1 - t0));
@@ -117,7 +122,7 @@ __device__ inline void attn_slice_lds(const AttnArgs &a, int split, int kvh, int
             if constexpr (!F16) vsr[s2] = vsb[(int64_t)key * (HD / 32) + (8 * vc) / 32];
         }
         if (!prepared) {
-            attn_prepare<HD, G, NT, F16>(a, kvh, b, sp, S);
+            attn_prepare<HD, G, NT, F16>(a, kvh, b, sp, S, &pre);
             prepared = true;
             if (nt == 0) break;
         }

@@ -34,9 +34,10 @@ __device__ inline LdsKRow<NQ> lds_load_krow(const int8_t *p) {
 
 // ---------------------------------------------------------------------------
 // One work item (split, KV head kvh, query b) of n_split over its whole key
-// slice, in passes of up to LDS_KT keys: every K and V byte of a pass is
-// requested before the query's preparation and held in registers, so the
-// slice costs one memory round trip rather than one per 64-key tile.
+// slice, in passes of up to LDS_KT keys: the query's inputs are requested
+// first, then every K and V byte of a pass, held in registers while the
+// query is prepared, so the slice costs one memory round trip rather than
+// one per 64-key tile.
 //   scores   4 lanes per key (HD/4 dims each), 64 keys per sweep of the
 //            workgroup, q from LDS, the 4 partial sums added by DPP;
 //   softmax  a wave per head over the pass, online across passes;

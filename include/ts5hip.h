@@ -271,22 +271,22 @@ typedef struct {
 } ts5hip_check_result;
 /* The check's n test tokens (engine/src/checks.cpp:22-26): 1000 + (i * 7919) % (n_vocab - 1000). */
 int ts5hip_check_tokens(int n, int n_vocab, int32_t *out);
-/* A model file's id in .ts5ref files (engine/src/checks.cpp:40-50): its size and the FNV-1a hash of
- * its first MiB. */
+/* A model file's id in .ts5ref files (engine/src/checks.cpp:39-50): its size and a 64-bit hash of
+ * its first MiB (FNV-1a steps from ts5's start value 1469598103934665603). */
 int ts5hip_model_file_id(const char *path, uint64_t *size, uint64_t *hash);
 /* Where a model's saved reference logits live (engine/src/checks.cpp:56-58): MODEL.ts5ref for an
  * f16 cache, MODEL.q8.ts5ref, MODEL.f32.ts5ref. */
 int ts5hip_ref_path(const char *model_path, int kv_type, char *out, int len);
-/* load_ref / save_ref (engine/src/checks.cpp:78-110) in the reference's file format: the first n
+/* load_ref / save_ref (engine/src/checks.cpp:73-104) in the reference's file format: the first n
  * positions' logits [n][n_vocab] of a file of this model (size and hash), cache type and at least
- * n positions; saving keeps a file that already holds more positions. */
+ * n positions; saving keeps a file of the same model and cache type that holds more positions. */
 int ts5hip_ref_load(const char *model_path, int n, int n_vocab, int kv_type, float *logits);
 int ts5hip_ref_save(const char *model_path, int n, int n_vocab, int kv_type, const float *logits);
-/* run_check (engine/src/checks.cpp:112-160) on model m: the n test tokens as n - min(4, n/2)
+/* run_check (engine/src/checks.cpp:108-160) on model m: the n test tokens as n - min(4, n/2)
  * positions in one call with every position's logits, then the rest one token per call; against
  * ref_logits ([n][n_vocab], ts5's CPU backend with the same cache rounding) or, when null, the
- * saved file of model_path. Passes when max |diff| is under 0.5 % of the largest reference logit
- * (2 % with a q8 cache). */
+ * saved file of model_path. Passes when every logit is finite and max |diff| is under 0.5 % of the
+ * largest reference logit (2 % with a q8 cache). */
 int ts5hip_check_run(ts5hip_model *m, const char *model_path, int n, const float *ref_logits,
                      ts5hip_check_result *r);
 

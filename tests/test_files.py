@@ -128,3 +128,35 @@ def test_check_tokens():
     assert list(t) == [1000 + (i * 7919) % 127256 for i in range(6)]
     with pytest.raises(ts5hip.Ts5HipError):
         ts5hip.check_tokens(4, 1000)
+
+
+def test_ref_save_replaces_another_models_file(tmp_path):
+    """A saved file keeps its place only for the same model and cache type: a
+    longer file of another model is replaced, and a file that is not a .ts5ref
+    at all is refused on load."""
+    path, tensors, g = check_model(tmp_path)
+    hp, n = make_golden.TINY_CHECK, make_golden.CHECK_N
+    kv = ts5hip.KV_Q8
+    ref = ts5hip.ref_path(path, kv)
+    with open(ref, "wb") as f:
+        f.write(bytes(g[f"kv{kv}_file"]))
+    got = ts5hip.ref_load(path, n, hp["n_vocab"], kv)
+    other = str(tmp_path / "other.gguf")
+    with open(path, "rb") as f:
+        body = bytearray(f.read())
+    body[100] ^= 0xFF
+    with open(other, "wb") as f:
+        f.write(body)
+    # The other model's file holds more positions but is for other bytes.
+    os.rename(ref, ts5hip.ref_path(other, kv))
+    with pytest.raises(ts5hip.Ts5HipError, match="another model file"):
+        ts5hip.ref_load(other, n, hp["n_vocab"], kv)
+    ts5hip.ref_save(other, kv, got[:4])
+    assert np.array_equal(ts5hip.ref_load(other, 4, hp["n_vocab"], kv), got[:4])
+    with pytest.raises(ts5hip.Ts5HipError, match="fewer positions"):
+        ts5hip.ref_load(other, 5, hp["n_vocab"], kv)
+    with open(ts5hip.ref_path(other, kv), "wb") as f:
+        f.write(b"NOTAREF!" + bytes(64))
+    with pytest.raises(ts5hip.Ts5HipError, match="not a .ts5ref"):
+        ts5hip.ref_load(other, 1, hp["n_vocab"], kv)
+    assert not os.path.exists(ts5hip.ref_path(other, kv) + ".part")

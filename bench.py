@@ -137,6 +137,19 @@ def glu_roofline(ctx, hp, launches: int = 200):
 _busy = {}
 
 
+def queue_busy(ctx, launches: int):
+    """After a sync, `launches` RMSNorm launches over 1 GiB (~0.4 ms each) on
+    the library's stream: the host queues the timed launches behind them."""
+    if ctx not in _busy:
+        bx, by = ctx.alloc(4096 * 65536 * 4), ctx.alloc(4096 * 65536 * 4)
+        bx.zero()
+        _busy[ctx] = (bx, by, ctx.to_device(np.ones(4096, np.float32)))
+    bx, by, ones = _busy[ctx]
+    ctx.sync()
+    for _ in range(launches):
+        ctx.rmsnorm(bx, ones, 1e-5, 4096, 65536, by)
+
+
 def timed(ctx, fn, n: int, warm: int = 3, busy: bool = True) -> float:
     """Mean microseconds of fn(i) over n calls on the library's stream, HIP
     events around them (after `warm` untimed ones). With `busy`, the stream is
@@ -146,14 +159,7 @@ def timed(ctx, fn, n: int, warm: int = 3, busy: bool = True) -> float:
     for i in range(warm):
         fn(i)
     if busy:
-        if ctx not in _busy:
-            bx, by = ctx.alloc(4096 * 65536 * 4), ctx.alloc(4096 * 65536 * 4)
-            bx.zero()
-            _busy[ctx] = (bx, by, ctx.to_device(np.ones(4096, np.float32)))
-        bx, by, ones = _busy[ctx]
-        ctx.sync()
-        for _ in range(2 + n // 10):
-            ctx.rmsnorm(bx, ones, 1e-5, 4096, 65536, by)
+        queue_busy(ctx, 2 + n // 10)
     else:
         ctx.sync()
     ctx.timer_begin()
@@ -167,25 +173,45 @@ def free_busy(ctx):
         b.free()
 
 
+def timed_each(ctx, fn, n: int, warm: int = 3) -> np.ndarray:
+    """Per-launch microseconds of fn(i) over n calls: an event on the
+    library's stream between consecutive launches, which are queued behind
+    ~0.4 ms RMSNorm launches so that the host's launch rate is not timed."""
+    for i in range(warm):
+        fn(i)
+    queue_busy(ctx, 2 + n // 10)
+    for i in range(n):
+        ctx.timer_mark(i)
+        fn(i)
+    ctx.timer_mark(n)
+    return ctx.timer_marks(n + 1).astype(np.float64) * 1e3
+
+
 def cfg1_matvec(ctx):
     """cfg1: the 4096x4096 Q4_K matvec alone, 40 rotated copies (378 MB, past
-    the 256 MB Infinity Cache), 200 launches."""
+    the 256 MB Infinity Cache), 200 launches: the median launch (events
+    between launches) and the mean (events around all 200)."""
     E = 4096
     copies = 40
     ws = [ctx.weight_synth(synth.Q4_K, E, E, 300 + i) for i in range(copies)]
     x = ctx.to_device(np.random.default_rng(1).standard_normal(E).astype(np.float32))
     y = ctx.alloc(E * 4)
-    us = timed(ctx, lambda i: ctx.matvec(synth.Q4_K, ws[i % copies], E, E, x, y), 200)
+    run = lambda i: ctx.matvec(synth.Q4_K, ws[i % copies], E, E, x, y)
+    mean = timed(ctx, run, 200)
+    med = float(np.median(timed_each(ctx, run, 200)))
     algo = E * E // 256 * 144 + 4 * E + 4 * E  # 9,469,952 B
     for w in ws:
         w.free()
-    return dict(us=round(us, 2), gbs=round(algo / us / 1e3, 1), bytes=algo)
+    return dict(us_median=round(med, 2), gbs_median=round(algo / med / 1e3, 1), us_mean=round(mean, 2),
+                gbs_mean=round(algo / mean / 1e3, 1), bytes=algo)
 
 
 def cfg3_attention(ctx):
     """cfg3: flash decode over q8 (and f16) caches, one query per sequence,
-    32/8 heads of 128, every key. Buffers are rotated so each launch reads
-    past the Infinity Cache (> 300 MB of caches in rotation)."""
+    32/8 heads of 128, every key. K and V are drawn N(0,1) on the device and
+    stored as the cache keeps them (q8: round_kv per 32 values; f16), q is
+    N(0,1). Buffers are rotated so each launch reads past the Infinity Cache
+    (> 300 MB of caches in rotation)."""
     H, HKV, HD = 32, 8, 128
     scale = float(np.float32(1) / np.sqrt(np.float32(HD)))
     out = {}
@@ -196,15 +222,15 @@ def cfg3_attention(ctx):
                 cache = B * HKV * n * HD * vb
                 copies = max(1, -(-(300 << 20) // (2 * cache)))
                 bufs = []
+                nval = B * HKV * n * HD
+                kvt = ts5hip.KV_F16 if f16 else ts5hip.KV_Q8
                 for c in range(copies):
                     k, v = ctx.alloc(cache), ctx.alloc(cache)
-                    k.upload(np.full(cache, 0x1d + c, np.uint8))
-                    v.upload(np.full(cache, 0x2e + c, np.uint8))
                     sk = sv = None
                     if not f16:
                         sk, sv = ctx.alloc(cache // 16), ctx.alloc(cache // 16)
-                        sk.upload(np.full(cache // 16, 0x21, np.uint8))
-                        sv.upload(np.full(cache // 16, 0x21, np.uint8))
+                    ctx.kv_synth(1000 * B + 10 * c + 1, nval, kvt, k, sk)
+                    ctx.kv_synth(1000 * B + 10 * c + 2, nval, kvt, v, sv)
                     bufs.append((k, sk, v, sv))
                 q = ctx.to_device(np.random.default_rng(B).standard_normal((B, H * HD)).astype(np.float32))
                 o = ctx.alloc(B * H * HD * 4)
@@ -259,19 +285,23 @@ def cfg5_speculation(ctx, gen: int = 512, prompt_len: int = 2048):
     the 48-layer 5120-wide target and for the 8B, after a 2048-token prompt
     of uniform ids, 512 tokens, greedy (random-init weights of the configs'
     own distribution). Per target: tok/s without and with drafting, output
-    equality, drafted / accepted, a 5-token verify forward against one step,
-    and the draft model's time per drafted token."""
+    equality, drafted / accepted by source (prompt lookup, draft model), a
+    5-token verify forward against one step, and the draft model's time per
+    drafted token. Q4_K weights are centred (synth.blocks): with the configs'
+    own distribution every weight's mean is far above zero, a random model's
+    argmax hardly depends on its input (one token repeated), and prompt lookup
+    rather than the draft model would do all the drafting."""
     n_ctx = prompt_len + gen + 16
     draft = ts5hip.Model(ctx, synth.DRAFT_0P5B, n_ctx)
     for name, t, ne0, ne1 in synth.tensor_specs(synth.DRAFT_0P5B):
-        draft.synth_tensor(name, t, ne0, ne1, SEED + 5)
+        draft.synth_tensor(name, t, ne0, ne1, SEED + 5, centered=True)
     res = {}
     for tag, hp in (("target_48x5120", synth.TARGET_14B), ("llama_8b", synth.LLAMA_8B)):
         m = ts5hip.Model(ctx, hp, n_ctx)
         for name, t, ne0, ne1 in synth.tensor_specs(hp):
-            m.synth_tensor(name, t, ne0, ne1, SEED + 5)
+            m.synth_tensor(name, t, ne0, ne1, SEED + 5, centered=True)
         prompt = np.random.default_rng(5).integers(0, hp["n_vocab"], prompt_len).astype(np.int32)
-        runs = {}
+        runs, sources = {}, {}
         for k in (0, 4):
             e = ts5hip.Engine(m)
             e.set_drafter(draft if k else None)
@@ -280,6 +310,7 @@ def cfg5_speculation(ctx, gen: int = 512, prompt_len: int = 2048):
             ids, st = e.generate(prompt, temperature=0.0, max_tokens=gen, draft=k)
             dt = time.time() - t0
             runs[k] = (ids, st, dt)
+            sources[k] = e.draft_sources()
             e.close()
         pos = prompt_len + 8
         batch = np.array(runs[0][0][:5], np.int32)
@@ -292,7 +323,8 @@ def cfg5_speculation(ctx, gen: int = 512, prompt_len: int = 2048):
         dstep = timed(ctx, lambda i: fwd(draft, 1), 10, 2, busy=False)
         (ids0, st0, dt0), (ids4, st4, dt4) = runs[0], runs[4]
         res[tag] = dict(tok_s_draft0=round(gen / dt0, 1), tok_s_draft4=round(gen / dt4, 1),
-                        same_output=bool(np.array_equal(ids0, ids4)), drafted=int(st4[3]), accepted=int(st4[4]),
+                        same_output=bool(np.array_equal(ids0, ids4)), distinct_ids=int(np.unique(ids0).size),
+                        drafted=int(st4[3]), accepted=int(st4[4]), **sources[4],
                         step_ms=round(step / 1e3, 3), verify5_ms=round(verify / 1e3, 3),
                         verify5_over_step=round(verify / step, 3), draft_ms_per_token=round(dstep / 1e3, 3))
         log(f"cfg5 {tag}: {res[tag]}")

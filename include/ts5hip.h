@@ -58,6 +58,10 @@ int ts5hip_sync(ts5hip_ctx *ctx);
 /* HIP events on the context's stream around the work enqueued between them. */
 int ts5hip_timer_begin(ts5hip_ctx *ctx);
 int ts5hip_timer_end(ts5hip_ctx *ctx, float *ms);
+/* Event i (0..4095) recorded on the context's stream; ts5hip_timer_marks: the n - 1 intervals
+ * (ms) between marks 0..n-1, after the last one completes (per-launch kernel times). */
+int ts5hip_timer_mark(ts5hip_ctx *ctx, int i);
+int ts5hip_timer_marks(ts5hip_ctx *ctx, int n, float *ms);
 
 /* ---- weights (replaces VkBackend::upload_weights, engine/src/vk_backend.cpp:531-600) ---- */
 
@@ -67,6 +71,10 @@ int ts5hip_supports_type(uint32_t type);
 int64_t ts5hip_weight_bytes(uint32_t type, int64_t ne0, int64_t ne1);
 /* GGUF bytes on the host (engine/src/model.h:44-53 Weight::data) -> HBM layout at dst. */
 int ts5hip_weight_upload(ts5hip_ctx *ctx, uint32_t type, int64_t ne0, int64_t ne1, const void *gguf, void *dst);
+/* n (a multiple of 32) values drawn N(0,1) into a cache layout, seeded: KV_Q8 as the q8 cache
+ * rounds them (int8 values, an f16 scale per 32 consecutive values: round_kv,
+ * engine/src/cpu_backend.cpp:78-90), KV_F16 as f16 values (scales unused). Benchmark inputs. */
+int ts5hip_kv_synth(ts5hip_ctx *ctx, uint64_t seed, int64_t n, int kv_type, void *values, void *scales);
 /* Seeded random-init weights written straight into HBM layout (benchmark inputs). */
 int ts5hip_weight_synth(ts5hip_ctx *ctx, uint32_t type, int64_t ne0, int64_t ne1, uint64_t seed, int centered,
                         void *dst);
@@ -318,6 +326,16 @@ int ts5hip_engine_set_drafter(ts5hip_engine *e, ts5hip_model *dm);
  * generated, drafted, accepted drafts, 1 if an end-of-generation id stopped it. */
 int ts5hip_engine_generate(ts5hip_engine *e, const int32_t *prompt, int n_prompt, const ts5hip_sample_params *p,
                            const int32_t *eog, int n_eog, int32_t *out, int32_t *stats);
+/* The draft model's state (Engine::drafter_ok_, engine/src/engine.h:70; set false with the
+ * "draft model stopped/failed" lines of engine/src/engine.cpp:82-87, :97-101, :117-121):
+ * 0 no draft model, 1 drafting, 2 stopped for the rest of the engine's life (a history token past
+ * its embedding rows, or one of its forwards failed). Drafts the drafter picks past the target's
+ * vocabulary are dropped one at a time and do not stop it. */
+int ts5hip_engine_drafter_state(const ts5hip_engine *e);
+/* The last generate call's drafts by source (the split behind stats' drafted / accepted, which
+ * ts5 prints as one "draft a/b accepted" figure, engine/src/cli.cpp:364-366): out[4] = drafted by
+ * prompt lookup, of those accepted, drafted by the draft model, of those accepted. */
+int ts5hip_engine_draft_sources(const ts5hip_engine *e, int32_t *out);
 
 #ifdef __cplusplus
 }

@@ -14,8 +14,11 @@ Bars:
   CPU batch gives every row bit for bit what single-token steps give), free
   running with an f16 cache, and step by step on the reference's own cache
   state with a q8 cache (whose 1/127 rounding steps the two sides' last-bit
-  differences can land on either side of; the free-running q8 run reports
-  where it first parts from the reference).
+  differences can land on either side of); the free-running q8 run reports
+  where it first parts from the reference, its cache over every position
+  before that token's must differ from the reference's by single q8 rounding
+  steps and nothing larger, and the oracle stepping on the GPU's own cache
+  state must pick the GPU's token at every step through the divergent one.
 
 The greedy part uses centred Q4_K weights (synth.blocks): with the benchmark's
 distribution every weight's mean is far above zero and a random model's
@@ -88,9 +91,42 @@ def centred():
     return hp, tensors
 
 
+def q8_fields(v):
+    """A q8 cache row read back as floats -> (scale, q) per 32-value block.
+    Each stored value is q * scale with scale = f16(amax / 127) and the block's
+    largest |q| exactly 127 (amax / scale rounds to 127 for any f16 rounding of
+    amax / 127), so scale = max|value| / 127 exactly and q = value / scale."""
+    b = v.reshape(v.shape[0], -1, 32).astype(np.float64)
+    sc = np.abs(b).max(axis=2) / 127.0
+    q = np.divide(b, sc[..., None], out=np.zeros_like(b), where=sc[..., None] > 0)
+    qi = np.rint(q)
+    assert np.array_equal(q, qi) and np.abs(qi).max() <= 127, "not a q8 cache row"
+    assert np.array_equal(sc.astype(np.float16).astype(np.float64), sc), "scale is not an f16 value"
+    return sc.astype(np.float16), qi.astype(np.int32)
+
+
+def cache_flips(gpu, ref):
+    """How two q8 caches ([layer][K, V] rows of floats) differ: counts of
+    entries whose q differs by one step, by more, and of blocks whose scales
+    differ by one f16 ulp and by more."""
+    one = more = sc_one = sc_more = 0
+    for g_layer, r_layer in zip(gpu, ref):
+        for g, r in zip(g_layer, r_layer):
+            gs, gq = q8_fields(g)
+            rs, rq = q8_fields(r)
+            dq = np.abs(gq - rq)
+            one += int((dq == 1).sum())
+            more += int((dq > 1).sum())
+            ulp = np.abs(gs.view(np.int16).astype(np.int32) - rs.view(np.int16).astype(np.int32))
+            sc_one += int((ulp == 1).sum())
+            sc_more += int((ulp > 1).sum())
+    return one, more, sc_one, sc_more
+
+
 @pytest.mark.parametrize("kv", [ts5hip.KV_F16, ts5hip.KV_Q8])
 def test_8b_greedy_64_tokens(ctx, centred, kv):
     hp, tensors = centred
+    L = hp["n_layer"]
     m = ts5hip.Model(ctx, hp, 96, kv)
     m.set_tensors(tensors)
     prompt = np.random.default_rng(2).integers(0, hp["n_vocab"], 4).astype(np.int32)
@@ -99,6 +135,8 @@ def test_8b_greedy_64_tokens(ctx, centred, kv):
     ids = np.concatenate([[first], m.generate_greedy(first, prompt.size, 63)]).astype(np.int32)
     say(f"GPU greedy ids[:12] {list(ids[:12])}, {np.unique(ids).size} distinct of 64")
     seq = np.concatenate([prompt, ids[:-1]]).astype(np.int32)
+    # The free-running cache, before the batch below rewrites it.
+    run_cache = [[m.kv(layer, which, 0, seq.size) for which in (0, 1)] for layer in range(L)]
     got = m.forward(seq, 0, all_logits=True)  # the same 67 positions as one batch on the GPU
     m.close()
     ref = oracle.Model(hp, tensors, 96, kv, threads=THREADS)
@@ -120,13 +158,55 @@ def test_8b_greedy_64_tokens(ctx, centred, kv):
         # and the whole 64-token continuation must be the reference's.
         assert div is None, msg
         check_rows(got, want, "centred 67 positions", tol=5e-3)
+        return
     # A q8 cache rounds each 32-value block to 1/127 of its largest value:
     # inputs differing in their last bits (fp32 GPU sums against the
     # reference's fp64) land on different sides of a rounding boundary now
-    # and then, and this random model's near one-hot attention (scores of
-    # several thousand) can turn one such step into another token. The GPU's
-    # two paths agree with each other; per-step parity on the reference's own
-    # cache state is test_8b_q8_steps_on_reference_cache.
+    # and then. The divergent token is picked from position p's logits; up to
+    # p both sides saw the same tokens, so their caches over positions
+    # 0..p-1 must differ by single rounding steps only (|q| one apart, block
+    # scales at most one f16 ulp apart) and by nothing larger. (Position p's
+    # own K/V past layer 0 differ widely: this random model's attention is
+    # nearly one-hot, with scores in the thousands, and one q8 step in a key
+    # can move its score by more than the gap between the top keys.)
+    assert div is not None or np.array_equal(picks, ids)
+    p = prompt.size - 1 + (div if div is not None else 63)
+    ref_cache = [[ref.kv(which, layer)[:p] for which in (0, 1)] for layer in range(L)]
+    gpu_cache = [[run_cache[layer][which][:p] for which in (0, 1)] for layer in range(L)]
+    one, more, sc_one, sc_more = cache_flips(gpu_cache, ref_cache)
+    total = 2 * L * p * hp["n_head_kv"] * hp["head_dim"]
+    flips = (f"{msg} (position {p}); caches over positions 0..{p - 1}: {one} of {total} K/V entries one q8 "
+             f"step apart, {more} further; {sc_one} block scales one f16 ulp apart, {sc_more} further")
+    say(f"kv {kv}: {flips}")
+    assert more == 0 and sc_more == 0, flips
+    # That the GPU's picks are the reference's own on the GPU's cache state:
+    # the oracle steps through the same positions, each time on the GPU's
+    # free-running K/V of every earlier position (written into its cache),
+    # and must pick the GPU's token at every step through the divergent one,
+    # writing K/V within single q8 steps of the GPU's.
+    replay = oracle.Model(hp, tensors, 96, kv, threads=THREADS)
+    lg = replay.forward(prompt, 0)[0]
+
+    def adopt(q):  # the GPU's K/V of position q into the oracle's cache
+        for layer in range(L):
+            for which in (0, 1):
+                replay.kv(which, layer)[q] = run_cache[layer][which][q]
+
+    for q in range(prompt.size):
+        adopt(q)
+    replay_flips = 0
+    for i in range(min(64, (div if div is not None else 63) + 3)):
+        q = prompt.size - 1 + i
+        if i > 0:
+            lg = replay.forward(seq[q:q + 1], q)[0]
+            o, mo, so, smo = cache_flips([[run_cache[layer][which][q:q + 1] for which in (0, 1)] for layer in range(L)],
+                                         [[replay.kv(which, layer)[q:q + 1] for which in (0, 1)] for layer in range(L)])
+            assert mo == 0 and smo == 0, (i, q, mo, smo)
+            replay_flips += o
+            adopt(q)
+        assert int(np.argmax(lg)) == int(ids[i]), (i, int(np.argmax(lg)), int(ids[i]), msg)
+    say(f"kv {kv}: the oracle on the GPU's cache state picks the GPU's token at all {i + 1} steps through "
+        f"the divergence; its K/V within single q8 steps of the GPU's ({replay_flips} flips)")
 
 
 def test_8b_q8_steps_on_reference_cache(ctx, centred):

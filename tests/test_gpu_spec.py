@@ -1,10 +1,10 @@
 """cfg5's speculative decoding at its stated shapes, through the decode driver
 (ts5hip_engine_generate): the 24-layer, 896-wide Q8_0 draft model (vocab
-151936, tied head) proposing k = 4 tokens per step for a 5120-wide, 40/8-head
-Q4_K target (vocab 151936, Q6_K head; layer-reduced from 48 to 4 here, every
-matrix at full size) and for the 8B of cfg2 (layer-reduced likewise), after a
-2048-token prompt of uniform ids (engine/src/engine.cpp:75-129, :186-195;
-the reference's own run, engine/tests/run.sh:222-229).
+151936, tied head) proposing k = 4 tokens per step for the 48-layer,
+5120-wide, 40/8-head Q4_K target (vocab 151936, Q6_K head) and for the
+32-layer 8B of cfg2, after a 2048-token prompt of uniform ids, 128 generated
+tokens (engine/src/engine.cpp:75-129, :186-195; the reference's own run,
+engine/tests/run.sh:222-229).
 
 Bars: the greedy output with drafting is the output without it, token for
 token (a draft is kept only when the target's own pick equals it,
@@ -20,7 +20,7 @@ from tokenstation5_amd import synth, ts5hip
 
 pytestmark = pytest.mark.gpu
 PROMPT = 2048
-GEN = 48
+GEN = 128
 
 
 @pytest.fixture(scope="module")
@@ -44,7 +44,7 @@ def drafter(ctx):
     m.close()
 
 
-TARGETS = {"target_5120x4": dict(synth.TARGET_14B, n_layer=4), "llama8b_x4": dict(synth.LLAMA_8B, n_layer=4)}
+TARGETS = {"target_48x5120": synth.TARGET_14B, "llama_8b": synth.LLAMA_8B}
 
 
 @pytest.mark.parametrize("name", list(TARGETS))
@@ -56,7 +56,8 @@ def test_draft_model_keeps_greedy_output(ctx, drafter, name):
     e = ts5hip.Engine(target)
     e.set_drafter(drafter)
     ids, st = e.generate(prompt, temperature=0.0, max_tokens=GEN, draft=4)
-    print(f"{name}: drafted {st[3]}, accepted {st[4]}; ids[:8] {list(ids[:8])}")
+    print(f"{name}: drafted {st[3]}, accepted {st[4]}; ids[:8] {list(ids[:8])}, "
+          f"{np.unique(ids).size} distinct of {ids.size}")
     assert list(ids) == list(base_ids)
     assert st[2] == GEN and st[3] > 0 and base_st[3] == 0
     e.close()
@@ -67,7 +68,7 @@ def test_self_draft_is_accepted(ctx):
     """The target as its own draft model (a second instance of the same
     weights; the reference's self-draft run): the drafts are its single-token
     greedy picks, which the batched verify forward reproduces almost always."""
-    hp = TARGETS["llama8b_x4"]
+    hp = TARGETS["llama_8b"]
     target = synth_model(ctx, hp, PROMPT + GEN + 16, 53)
     twin = synth_model(ctx, hp, PROMPT + GEN + 16, 53)
     prompt = np.random.default_rng(6).integers(0, hp["n_vocab"], PROMPT).astype(np.int32)

@@ -25,9 +25,6 @@
 #include "attn_lds.h"
 #include "attn_mq.h"
 
-#ifndef TS5_ATTN_MQ
-#define TS5_ATTN_MQ 1
-#endif
 
 namespace ts5hip {
 
@@ -294,7 +291,7 @@ static hipError_t attn_launch(int G, dim3 grid, const AttnArgs &a, hipStream_t s
 }
 
 bool attn_mq_fits(int B, int H, int HKV, int HD, int kv_f16, int kv_per_batch) {
-    return TS5_ATTN_MQ && !kv_f16 && !kv_per_batch && HD == MQ_HD && HKV > 0 && H % HKV == 0 && B >= 2 &&
+    return !kv_f16 && !kv_per_batch && HD == MQ_HD && HKV > 0 && H % HKV == 0 && B >= 2 &&
            B <= ATTN_MAX_NEW && B * (H / HKV) <= MQ_ROWS;
 }
 

@@ -6,17 +6,9 @@
 #include "common.h"
 #include "kernels.h"
 
-#ifndef TS5_ATTN_KMIN
-#define TS5_ATTN_KMIN 128
-#endif
-
-#ifndef TS5_ATTN_DEPTH
-#define TS5_ATTN_DEPTH 2
-#endif
-
 namespace ts5hip {
-constexpr int ATTN_MIN_KEYS = TS5_ATTN_KMIN;
-constexpr int ATTN_DEPTH = TS5_ATTN_DEPTH;  // chunks of K and V in flight per wave (attn_slice)
+constexpr int ATTN_MIN_KEYS = 128;  // the fewest keys a split takes
+constexpr int ATTN_DEPTH = 2;       // chunks of K and V in flight per wave (attn_slice; 3 and 4 measured slower)
 
 // x0*c - x1*s and x0*s + x1*c with separate roundings, as the reference's
 // scalar float code computes them (engine/src/cpu_backend.cpp:63-64).

@@ -5,8 +5,7 @@
 // query; merge attn_merge.comp:18-47), with every query of the batch in one
 // work item, so that each key is read and converted once for all of them.
 //
-// Grid (n_split, HKV), 8 waves (two sets of 4, 16 rows each; with
-// TS5_MQ_QT 2 one set of 4 with all 32). Row r = G b + g is head g of KV head kvh
+// Grid (n_split, HKV), 8 waves (two sets of 4, 16 rows each). Row r = G b + g is head g of KV head kvh
 // for token b (position n0 + b, keys [0, n0 + b]); rows B G .. 31 are empty.
 //  1. Preparation: the rows' queries (bias, per-head norm, RoPE when `rope`)
 //     into LDS; with `append`, the batch's new keys in this key slice (K with
@@ -38,10 +37,7 @@ typedef float mq_f4 __attribute__((ext_vector_type(4)));
 
 constexpr int MQ_HD = 128;
 constexpr int MQ_ROWS = 32;           // two 16-row MFMA tiles
-#ifndef TS5_MQ_QT
-#define TS5_MQ_QT 1
-#endif
-constexpr int MQ_QT = TS5_MQ_QT;      // 16-row tiles a wave (the rows of a wave set)
+constexpr int MQ_QT = 1;              // 16-row tiles a wave (the rows of a wave set)
 constexpr int MQ_KG = 4;              // waves of a set, each 16 keys of a step
 constexpr int MQ_NW = MQ_KG * (MQ_ROWS / 16 / MQ_QT), MQ_NT = 64 * MQ_NW;
 constexpr int MQ_WR = 16 * MQ_QT;     // rows a wave

@@ -118,6 +118,7 @@ void ts5hip_destroy(ts5hip_ctx *ctx) {
     if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
     if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
+    for (hipEvent_t e : ctx->marks) (void)hipEventDestroy(e);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -172,6 +173,22 @@ int ts5hip_timer_begin(ts5hip_ctx *ctx) {
     TS5_HIP(ctx, hipEventRecord(ctx->ev0, ctx->stream));
     return TS5HIP_OK;
 }
+int ts5hip_timer_mark(ts5hip_ctx *ctx, int i) {
+    if (!ctx || i < 0 || i >= 4096) return fail(ctx, TS5HIP_ERR_ARG, "mark %d of at most 4096", i);
+    while ((int)ctx->marks.size() <= i) {
+        hipEvent_t e;
+        TS5_HIP(ctx, hipEventCreate(&e));
+        ctx->marks.push_back(e);
+    }
+    TS5_HIP(ctx, hipEventRecord(ctx->marks[(size_t)i], ctx->stream));
+    return TS5HIP_OK;
+}
+int ts5hip_timer_marks(ts5hip_ctx *ctx, int n, float *ms) {
+    if (!ctx || !ms || n < 2 || n > (int)ctx->marks.size()) return fail(ctx, TS5HIP_ERR_ARG, "%d marks", n);
+    TS5_HIP(ctx, hipEventSynchronize(ctx->marks[(size_t)n - 1]));
+    for (int i = 0; i + 1 < n; i++) TS5_HIP(ctx, hipEventElapsedTime(ms + i, ctx->marks[(size_t)i], ctx->marks[(size_t)i + 1]));
+    return TS5HIP_OK;
+}
 int ts5hip_timer_end(ts5hip_ctx *ctx, float *ms) {
     if (!ctx || !ms) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
     TS5_HIP(ctx, hipEventRecord(ctx->ev1, ctx->stream));
@@ -203,6 +220,14 @@ int ts5hip_weight_synth(ts5hip_ctx *ctx, uint32_t type, int64_t ne0, int64_t ne1
         return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "type %u with %lld x %lld", type, (long long)ne0, (long long)ne1);
     const SplitDst d = split_dst(type, ne0, ne1, dst, 0);
     TS5_HIP(ctx, launch_synth(type, ne0, ne1, seed, centered, d.body, d.scales, ctx->stream));
+    return TS5HIP_OK;
+}
+
+int ts5hip_kv_synth(ts5hip_ctx *ctx, uint64_t seed, int64_t n, int kv_type, void *values, void *scales) {
+    if (!ctx || !values || (kv_type == KV_Q8 && !scales)) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
+    if (n <= 0 || n % 32 || (kv_type != KV_Q8 && kv_type != KV_F16))
+        return fail(ctx, TS5HIP_ERR_ARG, "n %lld (a multiple of 32), cache type %d (q8 or f16)", (long long)n, kv_type);
+    TS5_HIP(ctx, launch_kv_synth(n, seed, kv_type == KV_F16, values, scales, ctx->stream));
     return TS5HIP_OK;
 }
 

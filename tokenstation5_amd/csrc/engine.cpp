@@ -196,6 +196,8 @@ struct ts5hip_engine {
     Drafter drafter;
     RowPicks picks;
     std::vector<int32_t> batch;
+    // The last generation's drafts by source: lookup drafted, accepted; model drafted, accepted.
+    int32_t by_source[4] = {0, 0, 0, 0};
 
     void forget() {
         history.clear();
@@ -228,6 +230,17 @@ int ts5hip_engine_set_drafter(ts5hip_engine *e, ts5hip_model *dm) {
     return TS5HIP_OK;
 }
 
+int ts5hip_engine_draft_sources(const ts5hip_engine *e, int32_t *out) {
+    if (!e || !out) return fail(nullptr, TS5HIP_ERR_ARG, "null argument");
+    std::memcpy(out, e->by_source, sizeof e->by_source);
+    return TS5HIP_OK;
+}
+
+int ts5hip_engine_drafter_state(const ts5hip_engine *e) {
+    if (!e || !e->drafter.m) return 0;
+    return e->drafter.live ? 1 : 2;
+}
+
 int ts5hip_engine_generate(ts5hip_engine *e, const int32_t *prompt, int n_prompt, const ts5hip_sample_params *p,
                            const int32_t *eog, int n_eog, int32_t *out, int32_t *stats) {
     if (!e || !prompt || !p || !out || (n_eog > 0 && !eog)) return fail(nullptr, TS5HIP_ERR_ARG, "null argument");
@@ -240,6 +253,7 @@ int ts5hip_engine_generate(ts5hip_engine *e, const int32_t *prompt, int n_prompt
     std::vector<int32_t> &h = e->history;
     enum { S_PROMPT, S_EVAL, S_GEN, S_DRAFTED, S_ACCEPTED, S_EOG };
     int32_t st[6] = {n_prompt, 0, 0, 0, 0, 0};
+    std::fill(e->by_source, e->by_source + 4, 0);
 
     // The prompt: the cached history's common prefix is kept, except that the
     // last prompt token is always run (its logits start the generation).
@@ -318,6 +332,8 @@ int ts5hip_engine_generate(ts5hip_engine *e, const int32_t *prompt, int n_prompt
             kept++;
         }
         st[S_ACCEPTED] += kept;
+        e->by_source[by_model ? 2 : 0] += nb - 1;
+        e->by_source[by_model ? 3 : 1] += kept;
         governor.judged(kept, nb - 1);
         h.insert(h.end(), b.begin(), b.begin() + kept + 1);
         if (full > 0) e->finder.extend(h);

@@ -34,38 +34,12 @@
 #include "common.h"
 #include "kernels.h"
 
-#ifndef TS5_GM_WAVES
-#define TS5_GM_WAVES 4
-#endif
-#ifndef TS5_GM_RTMAX
-#define TS5_GM_RTMAX 4
-#endif
-#ifndef TS5_GM_FUSED
-#define TS5_GM_FUSED 1
-#endif
-#ifndef TS5_GM_MX
-#define TS5_GM_MX 1
-#endif
-#ifndef TS5_GM_MH
-#define TS5_GM_MH 1  // the verify batch's Q6_K head on k_gemm_mh
-#endif
-#ifndef TS5_GM_MW
-#define TS5_GM_MW 1
-#endif
-#ifndef TS5_GM_P5
-#define TS5_GM_P5 1
-#endif
-#ifndef TS5_GM_SCHED
-#define TS5_GM_SCHED 1
-#endif
-#if TS5_GM_SCHED
-#define TS5_GM_SB() __builtin_amdgcn_sched_barrier(0)
-#else
-#define TS5_GM_SB() (void)0
-#endif
-
 namespace ts5hip {
-constexpr int GM_WAVES = TS5_GM_WAVES;  // k_gemm_m's waves a workgroup, each a share of the row's blocks
+constexpr int GM_WAVES = 4;  // k_gemm_m's waves a workgroup, each a share of the row's blocks (8: 10 % slower)
+constexpr int GM_RTMAX = 4;  // k_gemm_m's most 16-row tiles a wave
+// Keeps the scheduler from moving loads or arithmetic across this point (the
+// next item's weight requests stay ahead of the current item's arithmetic).
+#define TS5_GM_SB() __builtin_amdgcn_sched_barrier(0)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 static int g_gemm_m_cu = 256;  // CUs, for k_gemm_m's row tiles a workgroup
@@ -1441,12 +1415,12 @@ static void launch_gemm_fused_tm(const GemmArgs &a, int rt, size_t lds, hipStrea
 }
 
 bool gemm_fused_fits(uint32_t t, int64_t ne0, int M) {
-    return TS5_GM_FUSED && t == T_Q4_K && ne0 % 256 == 0 && ne0 <= 4096 && M >= 1 && M <= 5;
+    return t == T_Q4_K && ne0 % 256 == 0 && ne0 <= 4096 && M >= 1 && M <= 5;
 }
 
 bool gemm_fused_qout_fits(int64_t ne0, int64_t ne1, int M) {
     const int64_t pairs = (ne1 + 31) / 32, grid = std::min<int64_t>(pairs, g_gemm_m_cu);
-    return gemm_fused_fits(T_Q4_K, ne0, M) && TS5_GM_MX && ne1 % 256 == 0 && (pairs + grid - 1) / grid <= 2;
+    return gemm_fused_fits(T_Q4_K, ne0, M) && ne1 % 256 == 0 && (pairs + grid - 1) / grid <= 2;
 }
 
 hipError_t launch_gemm_fused(const void *w, const void *w2, int64_t ne0, int64_t ne1, const float *x,
@@ -1464,7 +1438,7 @@ hipError_t launch_gemm_fused(const void *w, const void *w2, int64_t ne0, int64_t
     const int units = qout ? (tiles + 1) / 2 : tiles;
     const unsigned grid = (unsigned)std::min(units, g_gemm_m_cu);
     const int rt_mx = (qout ? 2 : 1) * ((units + (int)grid - 1) / (int)grid);
-    if (TS5_GM_MX && rt_mx <= 4) {
+    if (rt_mx <= 4) {
         // One workgroup a CU (at most), each RT tiles gridDim.x apart; its
         // LDS: the records, then each wave's two weight slots of 16 rows x
         // 144 B per matrix (GLU: 72 KiB; with the records' 5 x 16 x 896 B
@@ -1483,7 +1457,7 @@ hipError_t launch_gemm_fused(const void *w, const void *w2, int64_t ne0, int64_t
         return hipGetLastError();
     }
     int rt = tiles >= 4 * g_gemm_m_cu ? 4 : tiles >= 2 * g_gemm_m_cu ? 2 : 1;
-    if (TS5_GM_RTMAX < rt) rt = TS5_GM_RTMAX;
+    if (GM_RTMAX < rt) rt = GM_RTMAX;
     auto go = [&](auto mode_c) {
         constexpr int MD = decltype(mode_c)::value;
         if (M == 5) launch_gemm_fused_tm<MD, 5>(a, rt, lds, s);
@@ -1499,7 +1473,7 @@ hipError_t launch_gemm_fused(const void *w, const void *w2, int64_t ne0, int64_t
 template <int FMT, int MODE>
 static bool gemm_m_fits(int M) {
     if constexpr (FMT == F_Q4K) return M <= 8;
-    else if constexpr (FMT == F_Q6K && MODE != G_GLU) return M <= 4 || (M == 5 && TS5_GM_P5);
+    else if constexpr (FMT == F_Q6K && MODE != G_GLU) return M <= 5;
     else return false;
 }
 
@@ -1508,9 +1482,9 @@ static hipError_t launch_gemm_m(const GemmArgs &a, hipStream_t s) {
     // Row tiles a workgroup: as many as keep about one workgroup a CU.
     const int tiles = (a.nrows + 15) / 16;
     int rt = tiles >= 4 * g_gemm_m_cu ? 4 : tiles >= 2 * g_gemm_m_cu ? 2 : 1;
-    if (TS5_GM_RTMAX < rt) rt = TS5_GM_RTMAX;
+    if (GM_RTMAX < rt) rt = GM_RTMAX;
     if (a.M <= 4) launch_gemm_m_nt<FMT, MODE, 1>(a, rt, s);
-    else if (a.M == 5 && TS5_GM_P5) launch_gemm_m_nt<FMT, MODE, 5>(a, rt, s);
+    else if (a.M == 5) launch_gemm_m_nt<FMT, MODE, 5>(a, rt, s);
     else if constexpr (FMT == F_Q4K) launch_gemm_m_nt<FMT, MODE, 2>(a, rt, s);
     return hipGetLastError();
 }
@@ -1600,7 +1574,7 @@ static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
             return !(e && e[0] == '0');
         }();
         if constexpr (FMT == F_Q4K && MODE != G_GLU)
-            if (use_m && TS5_GM_MW && a.M <= 5 && a.ks == 1) {
+            if (use_m && a.M <= 5 && a.ks == 1) {
                 const int tiles = (a.nrows + 15) / 16;
                 const size_t lds = (size_t)GX_WAVES * 2 * (16 * Q4K_BYTES + 5 * 1024) + GX_WAVES * 2 * 64 * 4;
                 const dim3 g((unsigned)std::min(tiles, g_gemm_m_cu)), blk(64 * GX_WAVES);
@@ -1609,7 +1583,7 @@ static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
                 return hipGetLastError();
             }
         if constexpr (FMT == F_Q6K && MODE == G_STORE)
-            if (use_m && TS5_GM_MH && a.M <= 5 && a.ks == 1 && gemm_mh_lds(a.M, a.nb) <= 160 * 1024) {
+            if (use_m && a.M <= 5 && a.ks == 1 && gemm_mh_lds(a.M, a.nb) <= 160 * 1024) {
                 const int tiles = (a.nrows + 15) / 16;
                 const dim3 g((unsigned)std::min((tiles + GX_WAVES - 1) / GX_WAVES, g_gemm_m_cu)), blk(64 * GX_WAVES);
                 const size_t lds = gemm_mh_lds(a.M, a.nb);

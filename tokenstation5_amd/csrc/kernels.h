@@ -22,6 +22,8 @@ hipError_t launch_embed(uint32_t t, const void *w, int64_t ne0, int64_t n_rows, 
 // Split layouts (Q6_K, Q8_0): nblocks GGUF blocks in HBM -> bodies and f16 scales.
 hipError_t launch_repack(uint32_t t, int64_t nblocks, const void *gguf, void *body, void *scales, hipStream_t s);
 // nrows random-init rows of ne0 values (scales: the split layout's f16 array, else unused).
+// n (a multiple of 32) N(0,1) values as a q8 (int8 values + f16 scale per 32) or f16 cache.
+hipError_t launch_kv_synth(int64_t n, uint64_t seed, int kv_f16, void *vals, void *scales, hipStream_t s);
 hipError_t launch_synth(uint32_t t, int64_t ne0, int64_t nrows, uint64_t seed, int centered, void *body, void *scales,
                         hipStream_t s);
 

@@ -96,29 +96,17 @@ __global__ __launch_bounds__(WAVES *WAVE) void k_mv(const void *w, const void *w
 // workgroups per CU, so large matrices loop over their groups with the next
 // step's weights in flight.
 // ---------------------------------------------------------------------------
-#ifndef TS5_MV_FIRST_SHARE
-#define TS5_MV_FIRST_SHARE 0.62
-#endif
-#ifndef TS5_MV_WG_PER_CU
-#define TS5_MV_WG_PER_CU 2
-#endif
-#ifndef TS5_MV_GLU_WAVES
-#define TS5_MV_GLU_WAVES 4
-#endif
-#ifndef TS5_MV_GLU_R
-#define TS5_MV_GLU_R 1  // with its alternating buffers, 16.3 us on the 8B gate/up against 16.8 at 2 rows
-#endif
-#ifndef TS5_MV_Q6_R
-#define TS5_MV_Q6_R 2  // the 8B head: 97 against 107 us at 4 rows a wave
-#endif
-#ifndef TS5_MV_R
-#define TS5_MV_R 4
-#endif
+constexpr double MV_FIRST_SHARE = 0.62;  // row groups of the workgroups dispatched first (one a CU)
+constexpr int MV_WG_PER_CU = 2;
+constexpr int MV_GLU_WAVES = 4;
+constexpr int MV_GLU_R = 1;  // with its alternating buffers, 16.3 us on the 8B gate/up against 16.8 at 2 rows
+constexpr int MV_Q6_R = 2;   // the 8B head: 97 against 107 us at 4 rows a wave
+constexpr int MV_R = 4;      // rows a wave of a persistent Q4_K grid
 static int g_n_cu = 256;
 void set_cu_count(int n) { g_n_cu = n > 0 ? n : 256; }
 // The grid cap, and so the most per-workgroup (value, row) pairs of the
 // head's argmax.
-static size_t mv_max_grid() { return (size_t)TS5_MV_WG_PER_CU * g_n_cu; }
+static size_t mv_max_grid() { return (size_t)MV_WG_PER_CU * g_n_cu; }
 
 template <class F, int R, int WAVES, int KS, int MODE>
 static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
@@ -141,9 +129,9 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
     // the first; at 62 % the halves end within 0.4 us: 17.0 -> 16.1 us, the
     // Q6_K head 100.8 -> 97 us).
     int nfirst = 0, n1 = 0;
-    if (per > 1 && grid > (unsigned)g_n_cu && TS5_MV_FIRST_SHARE > 0) {
+    if (per > 1 && grid > (unsigned)g_n_cu) {
         nfirst = g_n_cu;
-        const int64_t want = (int64_t)(TS5_MV_FIRST_SHARE * (double)ngroups / nfirst + 0.5) * nfirst;
+        const int64_t want = (int64_t)(MV_FIRST_SHARE * (double)ngroups / nfirst + 0.5) * nfirst;
         n1 = (int)std::min<int64_t>(std::max<int64_t>(want, nfirst), ngroups - ((int64_t)grid - nfirst));
     }
     const MvTail tail{a.t, a.nb, nfirst, n1, a.y_in, a.best_v, a.best_i, a.counter, a.out, a.seq, a.pos};
@@ -163,18 +151,10 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
 // Q4_K rows of more than one step (nb > 16 blocks, the down projection):
 // the workgroup's waves split each row's blocks, so that a CU has more weight
 // bytes in flight than its few row groups give it.
-#ifndef TS5_MV_KS
-#define TS5_MV_KS 2
-#endif
-#ifndef TS5_MV_KS_R
-#define TS5_MV_KS_R 4
-#endif
-#ifndef TS5_MV_KS_WAVES
-#define TS5_MV_KS_WAVES 8
-#endif
-#ifndef TS5_MV_KS_MINNB
-#define TS5_MV_KS_MINNB 17
-#endif
+constexpr int MV_KS = 2;         // block splits of a row (4 measured slower)
+constexpr int MV_KS_R = 4;
+constexpr int MV_KS_WAVES = 8;   // 16 waves spill
+constexpr int MV_KS_MINNB = 17;  // rows of more than one 16-block step
 
 // Rows per wave of a Q4_K matvec whose row groups all fit the grid at once
 // (one step each): the count that leaves the busiest CU the fewest rows per
@@ -182,7 +162,7 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
 // (6144 rows): 3 rows, 512 workgroups, two a CU (7.6 -> 6.8 us); at 4 rows
 // its 384 workgroups leave half the CUs with two and half with one.
 static int mv_rows_per_wave(int64_t nrows) {
-    if ((nrows + 15) / 16 > (int64_t)mv_max_grid()) return TS5_MV_R;  // a persistent grid
+    if ((nrows + 15) / 16 > (int64_t)mv_max_grid()) return MV_R;  // a persistent grid
     int best = 4;
     int64_t best_cost = INT64_MAX;
     for (int r = 4; r >= 2; r--) {
@@ -197,21 +177,21 @@ template <int MODE>
 static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
     if constexpr (MODE == MV_GLU) {
         switch (a.t) {
-        case T_Q4_K: return mv_go<Q4K, TS5_MV_GLU_R, TS5_MV_GLU_WAVES, 1, MODE>(a, s);
+        case T_Q4_K: return mv_go<Q4K, MV_GLU_R, MV_GLU_WAVES, 1, MODE>(a, s);
         case T_Q6_K: return mv_go<Q6K, 2, 4, 1, MODE>(a, s);
         case T_Q8_0: return mv_go<Q80, 2, 4, 1, MODE>(a, s);
         }
     } else {
         switch (a.t) {
         case T_Q4_K:
-            if (MODE != MV_ARGMAX && TS5_MV_KS > 1 && a.nb >= TS5_MV_KS_MINNB)
-                return mv_go<Q4K, TS5_MV_KS_R, TS5_MV_KS_WAVES, TS5_MV_KS, MODE>(a, s);
+            if (MODE != MV_ARGMAX && a.nb >= MV_KS_MINNB)
+                return mv_go<Q4K, MV_KS_R, MV_KS_WAVES, MV_KS, MODE>(a, s);
             switch (mv_rows_per_wave(a.nrows)) {
             case 3: return mv_go<Q4K, 3, 4, 1, MODE>(a, s);
             case 2: return mv_go<Q4K, 2, 4, 1, MODE>(a, s);
             default: return mv_go<Q4K, 4, 4, 1, MODE>(a, s);
             }
-        case T_Q6_K: return mv_go<Q6K, TS5_MV_Q6_R, 4, 1, MODE>(a, s);
+        case T_Q6_K: return mv_go<Q6K, MV_Q6_R, 4, 1, MODE>(a, s);
         case T_Q8_0: return mv_go<Q80, 4, 4, 1, MODE>(a, s);
         }
     }

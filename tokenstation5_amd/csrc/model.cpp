@@ -23,9 +23,6 @@
 #include "kernels.h"
 #include "runtime.h"
 
-#ifndef TS5_WO_REC
-#define TS5_WO_REC 1
-#endif
 
 using namespace ts5hip;
 
@@ -570,7 +567,7 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
         const bool fused = nc <= ATTN_MAX_NEW;
         // Up to 5 tokens with the multi-query attention: it also writes wo's
         // activation records, and wo runs on them (k_gemm_mw).
-        const bool wo_rec = TS5_WO_REC && fused && nc <= 5 && L.wo.type == T_Q4_K && AH % 256 == 0 &&
+        const bool wo_rec = fused && nc <= 5 && L.wo.type == T_Q4_K && AH % 256 == 0 &&
                             attn_mq_fits(nc, H, HKV, HD, m->kv_f16(), 0);
         if (!fused)
             TS5_HIP(ctx, launch_rope_kv(m->bqkv, QR, bias, qn, kn, eps, m->rope_cs, hp.rope_dims, hp.rope_neox,

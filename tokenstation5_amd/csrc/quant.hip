@@ -127,6 +127,46 @@ __global__ void k_synth(uint32_t t, int64_t nblocks, uint64_t seed, int centered
         synth_block(t, seed, centered, dst, ds, blk);
 }
 
+// A synthetic KV cache (benchmark inputs): n values drawn N(0,1), stored as
+// the cache keeps them: q8 as round_kv does (engine/src/cpu_backend.cpp:78-90:
+// per 32 values sc = f16(amax / 127), q = clamp(rint(v / sc), +-127); values
+// at q, scales at sc, one per 32 consecutive values) or f16. One thread per
+// 32-value block; value k of the stream is a hash of (seed, k).
+__global__ void k_kv_synth(int64_t nblocks, uint64_t seed, int kv_f16, uint8_t *__restrict__ vals,
+                           uint16_t *__restrict__ scales) {
+    const uint64_t base = mix64(seed ^ 0x6b76ull);
+    for (int64_t blk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; blk < nblocks;
+         blk += (int64_t)gridDim.x * blockDim.x) {
+        float v[32];
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            v[i] = normal(base + (uint64_t)(blk * 32 + i) * 0x9e3779b97f4a7c15ull);
+            amax = fmaxf(amax, fabsf(v[i]));
+        }
+        if (kv_f16) {
+            uint32_t *o = (uint32_t *)(vals + blk * 64);
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[i] = (uint32_t)f2h(v[2 * i]) | (uint32_t)f2h(v[2 * i + 1]) << 16;
+            continue;
+        }
+        const uint16_t sh = f2h(amax / 127.0f);
+        const float sc = h2f(sh);
+        uint32_t *o = (uint32_t *)(vals + blk * 32);
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int q = sc > 0.f ? (int)fminf(127.f, fmaxf(-127.f, rintf(v[4 * w + b] / sc))) : 0;
+                word |= (uint32_t)(q & 0xff) << (8 * b);
+            }
+            o[w] = word;
+        }
+        scales[blk] = sh;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Launchers.
 // ---------------------------------------------------------------------------
@@ -158,6 +198,13 @@ hipError_t launch_synth(uint32_t t, int64_t ne0, int64_t nrows, uint64_t seed, i
                         hipStream_t s) {
     const int64_t nb = ne0 / block_values(t) * nrows;
     hipLaunchKernelGGL(k_synth, dim3(grid_for(nb, 256)), dim3(256), 0, s, t, nb, seed, centered, (uint8_t *)body,
+                       (uint16_t *)scales);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_synth(int64_t n, uint64_t seed, int kv_f16, void *vals, void *scales, hipStream_t s) {
+    const int64_t nb = n / 32;
+    hipLaunchKernelGGL(k_kv_synth, dim3(grid_for(nb, 256)), dim3(256), 0, s, nb, seed, kv_f16, (uint8_t *)vals,
                        (uint16_t *)scales);
     return hipGetLastError();
 }

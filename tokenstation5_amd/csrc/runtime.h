@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "../../include/ts5hip.h"
 
@@ -12,6 +13,7 @@ struct ts5hip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    std::vector<hipEvent_t> marks;  // ts5hip_timer_mark's events, made on first use
     std::string err;
     int n_cu = 0;
     std::string arch;

@@ -54,6 +54,9 @@ _SIGS = {
     "ts5hip_sync": (_i32, [_vp]),
     "ts5hip_timer_begin": (_i32, [_vp]),
     "ts5hip_timer_end": (_i32, [_vp, C.POINTER(_f32)]),
+    "ts5hip_timer_mark": (_i32, [_vp, _i32]),
+    "ts5hip_timer_marks": (_i32, [_vp, _i32, _vp]),
+    "ts5hip_kv_synth": (_i32, [_vp, _u64, _i64, _i32, _vp, _vp]),
     "ts5hip_supports_type": (_i32, [_u32]),
     "ts5hip_weight_bytes": (_i64, [_u32, _i64, _i64]),
     "ts5hip_weight_upload": (_i32, [_vp, _u32, _i64, _i64, _vp, _vp]),
@@ -113,6 +116,8 @@ _SIGS = {
     "ts5hip_engine_free": (None, [_vp]),
     "ts5hip_engine_set_drafter": (_i32, [_vp, _vp]),
     "ts5hip_engine_generate": (_i32, [_vp, _vp, _i32, C.POINTER(SampleParams), _vp, _i32, _vp, _vp]),
+    "ts5hip_engine_drafter_state": (_i32, [_vp]),
+    "ts5hip_engine_draft_sources": (_i32, [_vp, _vp]),
 }
 
 _lib = None
@@ -251,6 +256,19 @@ class Context:
         g = np.ascontiguousarray(gguf, np.uint8)
         self.check(lib().ts5hip_weight_upload(self.h, t, ne0, ne1, g.ctypes.data, d.ptr))
         return d
+
+    def timer_mark(self, i: int):
+        self.check(lib().ts5hip_timer_mark(self.h, i))
+
+    def timer_marks(self, n: int) -> np.ndarray:
+        """The n - 1 intervals (ms) between marks 0..n-1."""
+        out = np.empty(n - 1, np.float32)
+        self.check(lib().ts5hip_timer_marks(self.h, n, out.ctypes.data))
+        return out
+
+    def kv_synth(self, seed: int, n: int, kv: int, values, scales=None):
+        """n N(0,1) values into a q8 (values + scales) or f16 cache layout."""
+        self.check(lib().ts5hip_kv_synth(self.h, seed, n, kv, _ptr(values), _ptr(scales) if scales is not None else None))
 
     def weight_synth(self, t: int, ne0: int, ne1: int, seed: int, centered: bool = False) -> DeviceBuffer:
         d = DeviceBuffer(self, self.weight_bytes(t, ne0, ne1))
@@ -497,6 +515,17 @@ class Engine:
                                          stats.ctypes.data)
         self.model.ctx.check(min(n, 0))
         return out[:n], stats
+
+    def draft_sources(self) -> dict:
+        """The last generation's drafts by source: lookup / model, drafted and accepted."""
+        out = np.zeros(4, np.int32)
+        self.model.ctx.check(lib().ts5hip_engine_draft_sources(self.h, out.ctypes.data))
+        return dict(lookup_drafted=int(out[0]), lookup_accepted=int(out[1]), model_drafted=int(out[2]),
+                    model_accepted=int(out[3]))
+
+    def drafter_state(self) -> int:
+        """0 no draft model, 1 drafting, 2 stopped (Engine::drafter_ok_ false)."""
+        return int(lib().ts5hip_engine_drafter_state(self.h))
 
     def close(self):
         if self.h:

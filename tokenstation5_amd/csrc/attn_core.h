@@ -367,6 +367,134 @@ __device__ inline Raw<BYTES> buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return v;
 }
 
+// ---------------------------------------------------------------------------
+// Split partials and their merge, shared by k_attn and k_attn_lds. Per
+// (query b, split, KV head) a group of attn_group_floats(G, HD) floats (whole
+// 128-byte lines): the G heads' unnormalised output sums [G][HD], then (m, l)
+// per head. A KV head's splits run on every XCD (workgroups go to the XCDs
+// in turn), so partials are written and read device-coherent: buffer
+// accesses with sc1 (stores through to memory, loads past this XCD's L2).
+// They are 16 bytes a lane: the merging work item then reads the 32 splits
+// of a 4-head group (66 KB) in about half the time 4-byte loads take (0.8
+// against 1.6 us); it is the one work item left on the KV head's critical
+// path, so its read is issue-bound, not bandwidth-bound.
+// ---------------------------------------------------------------------------
+constexpr int BUF_SC1 = 16;  // buffer cache policy: sc1 (device coherent)
+
+template <int G, int HD>
+__device__ inline float *attn_part_group(const AttnArgs &a, int b, int split, int kvh, int n_split) {
+    return a.part + (((int64_t)b * n_split + split) * a.HKV + kvh) * (int64_t)attn_group_floats(G, HD);
+}
+
+// Writes this work item's partial: quad q of the sums is sums(q) (values 4q ..
+// 4q + 3), head g's (m, l) is ml(g). Returns when the stores are complete.
+template <int G, int HD, int NT, class Sums, class ML>
+__device__ inline void attn_publish(float *pb, Sums sums, ML ml) {
+    constexpr int NOUT = G * HD;
+    const __amdgpu_buffer_rsrc_t r = slice_rsrc(pb, (uint32_t)attn_group_floats(G, HD) * 4);
+    for (int q = threadIdx.x; q < NOUT / 4; q += NT)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sums(q)), r, (uint32_t)q * 16, 0, BUF_SC1);
+    if (threadIdx.x < G) {
+        const float2 v = ml((int)threadIdx.x);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, (uint32_t)(NOUT + 2 * threadIdx.x) * 4,
+                                              0, BUF_SC1);
+    }
+    wait_stores();
+}
+
+// The merge, by the work item that counted a KV head's `used` splits last:
+// every split's (m, l) becomes a weight (a wave a head, a lane a split: wts,
+// red), then threads in SETS sets each add up quads of the output over their
+// share of the splits, all of a batch's loads requested together; the sets'
+// sums meet in LDS (xs: (SETS - 1) * G * HD floats, free by now) and the
+// first set writes the G heads' outputs. Leaves the KV head's counter zero.
+template <int G, int HD, int NT>
+__device__ inline void attn_merge(const AttnArgs &a, int b, int kvh, int n_split, int used,
+                                  float (&wts)[G][ATTN_MAX_SPLIT], float *red, float *xs) {
+    constexpr float LOG2E = 1.4426950408889634f;
+    constexpr int NOUT = G * HD, NQ4 = NOUT / 4, NW = NT / 64;
+    constexpr int SETS = NT / NQ4 < 1 ? 1 : (NT / NQ4 > NW ? NW : NT / NQ4);
+    constexpr int PER = (NQ4 + NT - 1) / NT;  // quads a thread (SETS 1 with more quads than threads)
+    constexpr int MB = 32 / SETS;             // loads a thread per quad and batch: 32 splits a batch in all
+    constexpr int64_t grp = attn_group_floats(G, HD);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int set = SETS > 1 ? tid / NQ4 : 0, tq = SETS > 1 ? tid % NQ4 : tid;
+    // Threads past the sets' quads only help with the weights.
+    const bool active = SETS > 1 ? set < SETS : (PER > 1 || tid < NQ4);
+    const float *p_all = a.part + ((int64_t)b * n_split * a.HKV + kvh) * grp;
+    const int64_t sstride = (int64_t)a.HKV * grp;  // floats between splits
+    const __amdgpu_buffer_rsrc_t rp = slice_rsrc(p_all, (uint32_t)((used - 1) * sstride + grp) * 4);
+    u32x4 v[PER][MB];
+    auto fetch = [&](int s0) {
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const int q = min(tq + NT * k, NQ4 - 1);
+#pragma unroll
+            for (int i = 0; i < MB; i++) {
+                const int sl = min(s0 + set + SETS * i, used - 1);
+                v[k][i] = __builtin_amdgcn_raw_buffer_load_b128(rp, (uint32_t)((sl * sstride + 4 * q) * 4), 0, BUF_SC1);
+            }
+        }
+    };
+    if (active) fetch(0);
+    for (int g = wave; g < G; g += NW) {
+        const int sl = min(lane, used - 1);
+        const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(rp, (uint32_t)((sl * sstride + NOUT + 2 * g) * 4), 0, BUF_SC1);
+        const float m0 = __uint_as_float(ml[0]), l0 = __uint_as_float(ml[1]);
+        const float mm = lane < used ? m0 : -INFINITY;
+        const float M = wave_max_dpp(mm);
+        const float w = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((mm - M) * LOG2E);
+        const float L = wave_sum_dpp(w * (lane < used ? l0 : 0.f));
+        wts[g][lane] = w;  // lanes past the used splits: 0
+        if (lane == 0) red[g] = L;
+    }
+    __syncthreads();
+    float4 acc[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (active) {
+        for (int s0 = 0; s0 < used; s0 += 32) {
+            if (s0) fetch(s0);
+#pragma unroll
+            for (int k = 0; k < PER; k++) {
+                const int g = 4 * min(tq + NT * k, NQ4 - 1) / HD;
+#pragma unroll
+                for (int i = 0; i < MB; i++) {
+                    const int sl = s0 + set + SETS * i;
+                    const float w = sl < used ? wts[g][sl] : 0.f;
+                    acc[k].x += w * __uint_as_float(v[k][i][0]);
+                    acc[k].y += w * __uint_as_float(v[k][i][1]);
+                    acc[k].z += w * __uint_as_float(v[k][i][2]);
+                    acc[k].w += w * __uint_as_float(v[k][i][3]);
+                }
+            }
+        }
+    }
+    if constexpr (SETS > 1) {
+        if (active && set > 0) *(float4 *)&xs[(set - 1) * NOUT + 4 * tq] = acc[0];
+        __syncthreads();
+        if (set == 0)
+#pragma unroll
+            for (int s2 = 1; s2 < SETS; s2++) {
+                const float4 o = *(const float4 *)&xs[(s2 - 1) * NOUT + 4 * tq];
+                acc[0].x += o.x, acc[0].y += o.y, acc[0].z += o.z, acc[0].w += o.w;
+            }
+    }
+    if (set == 0) {
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const int q = tq + NT * k;
+            if (q < NQ4) {
+                const float L = red[4 * q / HD];
+                const float4 r = L > 0.f ? make_float4(acc[k].x / L, acc[k].y / L, acc[k].z / L, acc[k].w / L)
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+                *(float4 *)(a.out + (int64_t)b * a.H * HD + (int64_t)kvh * G * HD + 4 * q) = r;
+            }
+        }
+    }
+    if (tid == 0) st_dev(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 0);  // ready for the next use
+}
+
 template <int HD, int G, int NT, bool F16 = false>
 __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, int n_split,
                                   SliceLds<HD, G, NT> &S) {
@@ -587,7 +715,6 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
 
     // The work item's (m, l, o) from its waves'.
     constexpr int NOUT = G * HD;
-    constexpr int64_t grp = attn_group_floats(G, HD);
     auto item_value = [&](int j, float &mo, float &lo_) -> float {
         const int g = j / HD, d = j % HD;
         float M = S.m_w[0][g];
@@ -611,82 +738,24 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
         }
         return;
     }
-    // Partial layout per (query, split, KV head): [G][HD] values, then (m, l)
-    // per head, grp floats in all (whole 128-byte lines).
-    float *pb = a.part + (((int64_t)b * n_split + split) * a.HKV + kvh) * grp;
-    for (int j = tid; j < NOUT; j += NT) {
-        float M, L;
-        st_dev(pb + j, item_value(j, M, L));
-        if (j % HD == 0) {
-            st_dev(pb + NOUT + 2 * (j / HD), M);
-            st_dev(pb + NOUT + 2 * (j / HD) + 1, L);
-        }
-    }
-    wait_stores();
+    attn_publish<G, HD, NT>(
+        attn_part_group<G, HD>(a, b, split, kvh, n_split),
+        [&](int q) {
+            float M, L, o[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] = item_value(4 * q + i, M, L);
+            return make_float4(o[0], o[1], o[2], o[3]);
+        },
+        [&](int g) {
+            float M, L;
+            item_value(g * HD, M, L);
+            return make_float2(M, L);
+        });
     __syncthreads();
     if (tid == 0) S.last = atomicAdd(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 1) == sp.used - 1;
     __syncthreads();
     if (!S.last) return;
-    // The merge: the used splits' partials, read device-coherent (buffer loads with
-    // sc1), two values a thread, up to 32 splits' worth requested together
-    // with the (m, l) that weigh them; a wave per head turns the (m, l) into
-    // weights, a lane per split.
-    const float *p_all = a.part + ((int64_t)b * n_split * a.HKV + kvh) * grp;
-    const int64_t sstride = (int64_t)a.HKV * grp;  // floats between splits
-    const __amdgpu_buffer_rsrc_t rp = slice_rsrc(p_all, (uint32_t)((sp.used - 1) * sstride + grp) * 4);
-    constexpr int MB = 32;  // splits a batch
-    constexpr int NQ2 = NOUT / 2, PER = (NQ2 + NT - 1) / NT;
-    u32x2 v[PER][MB];
-    auto fetch = [&](int s0) {
-#pragma unroll
-        for (int k = 0; k < PER; k++) {
-            const int j2 = min(tid + NT * k, NQ2 - 1);
-#pragma unroll
-            for (int i = 0; i < MB; i++) {
-                const int sl = min(s0 + i, sp.used - 1);
-                v[k][i] = __builtin_amdgcn_raw_buffer_load_b64(rp, (uint32_t)((sl * sstride + 2 * j2) * 4), 0, 16);
-            }
-        }
-    };
-    fetch(0);
-    for (int g = wave; g < G; g += NW) {
-        const int sl = min(lane, sp.used - 1);
-        const auto ml = __builtin_amdgcn_raw_buffer_load_b64(rp, (uint32_t)((sl * sstride + NOUT + 2 * g) * 4), 0, 16);
-        const float m0 = __uint_as_float(ml[0]), l0 = __uint_as_float(ml[1]);
-        const float mm = lane < sp.used ? m0 : -INFINITY;
-        const float M = wave_max_dpp(mm);
-        const float w = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((mm - M) * LOG2E);
-        const float L = wave_sum_dpp(w * (lane < sp.used ? l0 : 0.f));
-        S.wts[g][lane] = w;  // lanes past the used splits: 0
-        if (lane == 0) S.red[g] = L;
-    }
-    __syncthreads();
-    float2 acc[PER];
-#pragma unroll
-    for (int k = 0; k < PER; k++) acc[k] = make_float2(0.f, 0.f);
-    for (int s0 = 0; s0 < sp.used; s0 += MB) {
-        if (s0) fetch(s0);
-#pragma unroll
-        for (int k = 0; k < PER; k++) {
-            const int g = (2 * min(tid + NT * k, NQ2 - 1)) / HD;
-#pragma unroll
-            for (int i = 0; i < MB; i++) {
-                const float w = s0 + i < sp.used ? S.wts[g][s0 + i] : 0.f;
-                acc[k].x += w * __uint_as_float(v[k][i][0]);
-                acc[k].y += w * __uint_as_float(v[k][i][1]);
-            }
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const int j2 = tid + NT * k;
-        if (j2 < NQ2) {
-            const float L = S.red[(2 * j2) / HD];
-            const float2 r = L > 0.f ? make_float2(acc[k].x / L, acc[k].y / L) : make_float2(0.f, 0.f);
-            *(float2 *)(a.out + (int64_t)b * a.H * HD + (int64_t)kvh * G * HD + 2 * j2) = r;
-        }
-    }
-    if (tid == 0) st_dev(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 0);  // ready for the next use
+    attn_merge<G, HD, NT>(a, b, kvh, n_split, sp.used, S.wts, S.red, &S.o_w[0][0][0]);
 }
 
 }  // namespace ts5hip

@@ -249,77 +249,23 @@ __device__ inline void attn_slice_lds(const AttnArgs &a, int split, int kvh, int
     }
     __syncthreads();
 
-    constexpr int64_t rec = HD + 2, grp = attn_group_floats(G, HD);
-    float *pb = a.part + (((int64_t)b * n_split + split) * a.HKV + kvh) * grp;
-    for (int j = tid; j < G * HD; j += NT) {
-        const int g = j / HD, d = j % HD;
-        float v = 0.f;
+    attn_publish<G, HD, NT>(
+        attn_part_group<G, HD>(a, b, split, kvh, n_split),
+        [&](int q) {
+            float4 v = *(const float4 *)&S.o_s[0][4 * q];
 #pragma unroll
-        for (int w = 0; w < NW; w++) v += S.o_s[w][j];
-        st_dev(pb + g * rec + d, v);
-    }
-    if (tid < G) {
-        st_dev(pb + tid * rec + HD, S.m_s[tid]);
-        st_dev(pb + tid * rec + HD + 1, S.l_s[tid]);
-    }
-    wait_stores();
+            for (int w = 1; w < NW; w++) {
+                const float4 o = *(const float4 *)&S.o_s[w][4 * q];
+                v.x += o.x, v.y += o.y, v.z += o.z, v.w += o.w;
+            }
+            return v;
+        },
+        [&](int g) { return make_float2(S.m_s[g], S.l_s[g]); });
     __syncthreads();
     if (tid == 0) S.last = atomicAdd(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 1) == sp.used - 1;
     __syncthreads();
     if (!S.last) return;
-    // The merge: this thread's outputs of every split (up to 32 at a time)
-    // and every split's (m, l) are requested together; a wave per head turns
-    // the (m, l) into weights, a lane per split.
-    const float *p_all = a.part + ((int64_t)b * n_split * a.HKV + kvh) * grp;
-    const int64_t sstride = (int64_t)a.HKV * grp;
-    constexpr int OPT = (G * HD + NT - 1) / NT, MC = 32;
-    float acc[OPT];
-#pragma unroll
-    for (int k = 0; k < OPT; k++) acc[k] = 0.f;
-    for (int s0 = 0; s0 < sp.used; s0 += MC) {
-        const int nc = min(MC, sp.used - s0);
-        float ov[OPT][MC];
-#pragma unroll
-        for (int k = 0; k < OPT; k++) {
-            const int j = min(tid + NT * k, G * HD - 1), g = j / HD, d = j % HD;
-#pragma unroll
-            for (int i = 0; i < MC; i++) ov[k][i] = ld_dev(p_all + (int64_t)(s0 + min(i, nc - 1)) * sstride + g * rec + d);
-        }
-        if (s0 == 0) {
-            for (int g = wave; g < G; g += NT / 64) {
-                const int sl = min(lane, sp.used - 1);
-                const float m0 = ld_dev(p_all + (int64_t)sl * sstride + g * rec + HD);
-                const float l0 = ld_dev(p_all + (int64_t)sl * sstride + g * rec + HD + 1);
-                const float m = lane < sp.used ? m0 : -INFINITY;
-                const float M = wave_max_dpp(m);
-                const float w = m == -INFINITY ? 0.f : expf(m - M);
-                const float L = wave_sum_dpp(w * (lane < sp.used ? l0 : 0.f));
-                S.wts[g][lane] = w;  // lanes past the used splits: 0
-                if (lane == 0) S.red[g] = L;
-            }
-            __syncthreads();
-        }
-#pragma unroll
-        for (int k = 0; k < OPT; k++) {
-            const int j = min(tid + NT * k, G * HD - 1), g = j / HD;
-            float v = acc[k];
-#pragma unroll
-            for (int i4 = 0; i4 < MC / 4; i4++) {  // weights past the used splits are 0 (their o: a used split's)
-                const float4 w = *(const float4 *)&S.wts[g][s0 + 4 * i4];
-                v += w.x * ov[k][4 * i4] + w.y * ov[k][4 * i4 + 1] + w.z * ov[k][4 * i4 + 2] + w.w * ov[k][4 * i4 + 3];
-            }
-            acc[k] = v;
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < OPT; k++) {
-        const int j = tid + NT * k;
-        if (j < G * HD) {
-            const int g = j / HD, d = j % HD;
-            st_dev(a.out + (int64_t)b * a.H * HD + (int64_t)(kvh * G + g) * HD + d, acc[k] / S.red[g]);
-        }
-    }
-    if (tid == 0) st_dev(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 0);  // ready for the next use
+    attn_merge<G, HD, NT>(a, b, kvh, n_split, sp.used, S.wts, S.red, &S.o_s[0][0]);
 }
 
 }  // namespace ts5hip

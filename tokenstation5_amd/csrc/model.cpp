@@ -16,6 +16,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -88,10 +89,17 @@ struct ts5hip_model {
     float *bx = nullptr, *bqkv = nullptr, *bq = nullptr, *batt = nullptr, *bffn = nullptr, *bpart = nullptr;
     void *bact = nullptr, *bgemm = nullptr;
     int *bcounters = nullptr;
-    // Profile (TS5HIP_PROFILE set): GPU time per forward call.
-    bool profile = false;
+    // Profile (TS5_PROFILE or TS5HIP_PROFILE, engine/src/vk_backend.cpp:347-358):
+    // 1 = GPU time of every kernel launch, by kernel and weight role (an event
+    // after each launch; tokens launched directly, not replayed as graphs);
+    // another nonzero value = GPU time of whole forward calls only.
+    int profile = 0;
     double prof_ms = 0;
     int prof_calls = 0, prof_tokens = 0;
+    std::vector<hipEvent_t> prof_ev;      // event pool: [0] before the first launch, [i] after launch i
+    std::vector<std::string> prof_label;  // what launch i was
+    int prof_used = 0;                    // events recorded since the last fold
+    std::map<std::string, std::pair<double, int>> prof_kernels;  // label -> (ms, launches)
     std::vector<void *> allocs;
 
     int qkv_rows() const { return (hp.n_head + 2 * hp.n_head_kv) * hp.head_dim; }
@@ -119,6 +127,73 @@ int alloc_t(ts5hip_model *m, size_t count, T **p) {
     if (int rc = alloc(m, count * sizeof(T), &v)) return rc;
     *p = (T *)v;
     return TS5HIP_OK;
+}
+
+// ---- the per-kernel profile ----------------------------------------------------
+constexpr int PROF_EVENTS = 4096;  // launches timed between two folds
+
+std::string type_tag(uint32_t t) {
+    switch (t) {
+    case T_F32: return "f32";
+    case T_F16: return "f16";
+    case T_Q8_0: return "q8_0";
+    case T_Q4_K: return "q4_k";
+    case T_Q6_K: return "q6_k";
+    default: return "t" + std::to_string(t);
+    }
+}
+
+// Adds the recorded launches' times to prof_kernels. The last event stays as
+// the start of the launches that follow.
+int prof_fold(ts5hip_model *m) {
+    if (m->profile != 1 || m->prof_used < 2) return TS5HIP_OK;
+    ts5hip_ctx *ctx = m->ctx;
+    const size_t last = (size_t)m->prof_used - 1;
+    TS5_HIP(ctx, hipEventSynchronize(m->prof_ev[last]));
+    for (size_t i = 1; i <= last; i++) {
+        float ms = 0;
+        TS5_HIP(ctx, hipEventElapsedTime(&ms, m->prof_ev[i - 1], m->prof_ev[i]));
+        auto &e = m->prof_kernels[m->prof_label[i]];
+        e.first += ms, e.second++;
+    }
+    std::swap(m->prof_ev[0], m->prof_ev[last]);
+    m->prof_used = 1;
+    return TS5HIP_OK;
+}
+
+int prof_event(ts5hip_model *m, const std::string &label) {
+    ts5hip_ctx *ctx = m->ctx;
+    if (m->prof_ev.size() <= (size_t)m->prof_used) {
+        hipEvent_t e;
+        TS5_HIP(ctx, hipEventCreate(&e));
+        m->prof_ev.push_back(e);
+        m->prof_label.emplace_back();
+    }
+    m->prof_label[(size_t)m->prof_used] = label;
+    TS5_HIP(ctx, hipEventRecord(m->prof_ev[(size_t)m->prof_used++], ctx->stream));
+    return TS5HIP_OK;
+}
+
+// The start event of a forward call's launches (none while one is open).
+int prof_start(ts5hip_model *m) {
+    if (m->profile != 1 || m->prof_used > 0) return TS5HIP_OK;
+    return prof_event(m, std::string());
+}
+
+// Folds a forward call's launches; the next call starts its own timing.
+int prof_close(ts5hip_model *m) {
+    if (int rc = prof_fold(m)) return rc;
+    m->prof_used = 0;
+    return TS5HIP_OK;
+}
+
+// The event after the launch just enqueued, labelled "kernel role".
+int prof_stamp(ts5hip_model *m, const std::string &kernel, const char *role) {
+    if (m->profile != 1) return TS5HIP_OK;
+    if (m->prof_used == 0)
+        if (int rc = prof_start(m)) return rc;  // a launch outside a forward call: timed from here on
+    if (int rc = prof_event(m, role && *role ? kernel + " " + role : kernel)) return rc;
+    return m->prof_used >= PROF_EVENTS ? prof_fold(m) : TS5HIP_OK;
 }
 
 // A vector tensor (norm weight, bias, rope freqs) as floats on the host.
@@ -329,6 +404,8 @@ int check_complete(ts5hip_model *m) {
     return TS5HIP_OK;
 }
 
+const char *const kQkvRole[3] = {"attn_q", "attn_k", "attn_v"};
+
 // The kernels of one token at position state[0] (see the file comment).
 // tail: 0 = advance the position, 1 = argmax into seq[p+1] and advance.
 int enqueue_token(ts5hip_model *m, bool head, int tail) {
@@ -337,12 +414,16 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
     const ts5hip_hparams &hp = m->hp;
     const int E = hp.n_embd, H = hp.n_head, HKV = hp.n_head_kv, HD = hp.head_dim, F = hp.n_ff;
     const int QR = m->qkv_rows();
+#define TS5_STAMP(kernel, role) \
+    if (int rc_ = prof_stamp(m, kernel, role)) return rc_
     TS5_HIP(ctx, launch_embed(m->tok_embd.type, m->tok_embd.d, E, hp.n_vocab, m->seq, m->state, 1, m->x, s));
+    TS5_STAMP("embed_" + type_tag(m->tok_embd.type), "token_embd");
     for (int l = 0; l < hp.n_layer; l++) {
         const LayerDev &L = m->layers[l];
         const float *an = (const float *)L.attn_norm.d;
         if (L.in_qkv[0] && L.in_qkv[1] && L.in_qkv[2]) {
             TS5_HIP(ctx, launch_matvec(L.qkv.type, L.qkv.d, E, QR, m->x, an, hp.rms_eps, m->qkv, 0, s));
+            TS5_STAMP("matvec_" + type_tag(L.qkv.type), "attn_qkv");
         } else {
             // Rows kept in the fused buffer are a sub-tensor only for layouts
             // without a separate scale array (Q4_K); split layouts go per part.
@@ -354,9 +435,11 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
                         return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "mixed q/k/v types with a split layout");
                     const SplitDst d = split_dst(L.qkv.type, E, QR, L.qkv.d, r0);
                     TS5_HIP(ctx, launch_matvec(L.qkv.type, d.body, E, rows[p], m->x, an, hp.rms_eps, m->qkv + r0, 0, s));
+                    TS5_STAMP("matvec_" + type_tag(L.qkv.type), kQkvRole[p]);
                 } else {
                     TS5_HIP(ctx, launch_matvec(L.part[p].type, L.part[p].d, E, rows[p], m->x, an, hp.rms_eps,
                                                m->qkv + r0, 0, s));
+                    TS5_STAMP("matvec_" + type_tag(L.part[p].type), kQkvRole[p]);
                 }
                 r0 += rows[p];
             }
@@ -371,22 +454,30 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
         io.n_keys = m->state, io.B = 1, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = m->n_split, io.scale = hp.attn_scale;
         io.part = m->part, io.counters = m->counters, io.out = m->att;
         TS5_HIP(ctx, launch_attn(io, s));
+        TS5_STAMP(m->kv_f16() ? "attention_f16" : "attention_q8", "decode");
         TS5_HIP(ctx, launch_matvec(L.wo.type, L.wo.d, (int64_t)H * HD, E, m->att, nullptr, 0.f, m->x, 1, s));
+        TS5_STAMP("matvec_" + type_tag(L.wo.type), "attn_output");
         TS5_HIP(ctx, launch_matvec_glu(L.gate.type, L.gate.d, L.up.d, E, F, m->x, (const float *)L.ffn_norm.d,
                                        hp.rms_eps, m->ffn, s));
+        TS5_STAMP("matvec_glu_" + type_tag(L.gate.type), "ffn_gate+up");
         TS5_HIP(ctx, launch_matvec(L.down.type, L.down.d, F, E, m->ffn, nullptr, 0.f, m->x, 1, s));
+        TS5_STAMP("matvec_" + type_tag(L.down.type), "ffn_down");
     }
     if (head) {
         const DevT &out = m->output.set ? m->output : m->tok_embd;
+        const char *orole = m->output.set ? "output" : "token_embd";
         const float *on = (const float *)m->out_norm.d;
         if (tail == 1) {
             TS5_HIP(ctx, launch_matvec_argmax(out.type, out.d, E, hp.n_vocab, m->x, on, hp.rms_eps, m->logits, m->amax,
                                               m->counters + HKV * CTR_STRIDE, m->state + 1, m->seq, m->state, s));
+            TS5_STAMP("matvec_argmax_" + type_tag(out.type), orole);
             return TS5HIP_OK;
         }
         TS5_HIP(ctx, launch_matvec(out.type, out.d, E, hp.n_vocab, m->x, on, hp.rms_eps, m->logits, 0, s));
+        TS5_STAMP("matvec_" + type_tag(out.type), orole);
     }
     TS5_HIP(ctx, launch_advance(m->state, s));
+    TS5_STAMP("advance", "");
     return TS5HIP_OK;
 }
 
@@ -524,22 +615,28 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
     const int QR = m->qkv_rows();
     const float eps = hp.rms_eps;
     auto proj = [&](uint32_t t, const void *w, const void *w2, int64_t ne0, int64_t ne1, const float *x,
-                    int64_t xstride, const float *norm, int ntok, int mode, float *y, int64_t ldy) -> int {
+                    int64_t xstride, const float *norm, int ntok, int mode, float *y, int64_t ldy,
+                    const char *role) -> int {
         if (gemm_fused_fits(t, ne0, ntok)) {
             TS5_HIP(ctx, launch_gemm_fused(w, w2, ne0, ne1, x, xstride, norm, eps, ntok, mode, y, y, ldy, s));
+            TS5_STAMP("matmul_fused_" + type_tag(t), role);
             return TS5HIP_OK;
         }
         TS5_HIP(ctx, launch_gemm_act(t, x, xstride, norm, eps, (int)ne0, ntok, m->bact, s));
+        TS5_STAMP("act_quant", role);
         TS5_HIP(ctx, launch_gemm(t, w, w2, ne0, ne1, m->bact, ntok, mode, y, y, ldy, m->bgemm, s));
+        TS5_STAMP("matmul_" + type_tag(t), role);
         return TS5HIP_OK;
     };
     TS5_HIP(ctx, launch_set_pos(m->state, p0, s));
+    TS5_STAMP("set_pos", "");
     TS5_HIP(ctx, launch_embed(m->tok_embd.type, m->tok_embd.d, E, hp.n_vocab, m->seq, m->state, nc, m->bx, s));
+    TS5_STAMP("embed_" + type_tag(m->tok_embd.type), "token_embd");
     for (int l = 0; l < hp.n_layer; l++) {
         const LayerDev &L = m->layers[l];
         const float *an = (const float *)L.attn_norm.d;
         if (L.in_qkv[0] && L.in_qkv[1] && L.in_qkv[2]) {
-            if (int rc = proj(L.qkv.type, L.qkv.d, nullptr, E, QR, m->bx, E, an, nc, 0, m->bqkv, QR)) return rc;
+            if (int rc = proj(L.qkv.type, L.qkv.d, nullptr, E, QR, m->bx, E, an, nc, 0, m->bqkv, QR, "attn_qkv")) return rc;
         } else {
             const int64_t prow[3] = {(int64_t)AH, (int64_t)HKV * HD, (int64_t)HKV * HD};
             int64_t r0 = 0;
@@ -548,11 +645,12 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
                     if (L.qkv.type == T_Q6_K || L.qkv.type == T_Q8_0)
                         return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "mixed q/k/v types with a split layout");
                     const SplitDst d = split_dst(L.qkv.type, E, QR, L.qkv.d, r0);
-                    if (int rc = proj(L.qkv.type, d.body, nullptr, E, prow[p], m->bx, E, an, nc, 0, m->bqkv + r0, QR))
+                    if (int rc = proj(L.qkv.type, d.body, nullptr, E, prow[p], m->bx, E, an, nc, 0, m->bqkv + r0, QR,
+                                      kQkvRole[p]))
                         return rc;
                 } else {
                     if (int rc = proj(L.part[p].type, L.part[p].d, nullptr, E, prow[p], m->bx, E, an, nc, 0,
-                                      m->bqkv + r0, QR))
+                                      m->bqkv + r0, QR, kQkvRole[p]))
                         return rc;
                 }
                 r0 += prow[p];
@@ -569,12 +667,15 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
         // activation records, and wo runs on them (k_gemm_mw).
         const bool wo_rec = fused && nc <= 5 && L.wo.type == T_Q4_K && AH % 256 == 0 &&
                             attn_mq_fits(nc, H, HKV, HD, m->kv_f16(), 0);
-        if (!fused)
+        if (!fused) {
             TS5_HIP(ctx, launch_rope_kv(m->bqkv, QR, bias, qn, kn, eps, m->rope_cs, hp.rope_dims, hp.rope_neox,
                                         m->state, H, HKV, HD, m->n_ctx, nc, m->bq, m->kv_layer(l), m->kv_f16(), s));
+            TS5_STAMP("rope_kv_append", "");
+        }
         if (nc > 16 && !m->kv_f16() && attn_prefill_supported(H, HKV, HD)) {  // prompt chunks on the matrix cores
             TS5_HIP(ctx, launch_attn_prefill(m->bq, AH, m->kv_layer(l), m->n_ctx, H, HKV, HD, p0, nc, hp.attn_scale,
                                              m->bpart, m->batt, s));
+            TS5_STAMP("attention_prompt", "");
         } else {
             AttnIO io{};
             if (fused) {
@@ -590,10 +691,13 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
             // A verify batch's attention also writes wo's activation records.
             if (wo_rec) io.act_out = m->bact, io.act_stride = (int64_t)gemm_act_bytes(L.wo.type, AH, nc);
             TS5_HIP(ctx, launch_attn(io, s));
+            TS5_STAMP(m->kv_f16() ? "attention_f16" : "attention_q8", "batch");
         }
         if (wo_rec) {
             TS5_HIP(ctx, launch_gemm(L.wo.type, L.wo.d, nullptr, AH, E, m->bact, nc, 1, m->bx, m->bx, E, m->bgemm, s));
-        } else if (int rc = proj(L.wo.type, L.wo.d, nullptr, AH, E, m->batt, AH, nullptr, nc, 1, m->bx, E)) {
+            TS5_STAMP("matmul_" + type_tag(L.wo.type), "attn_output");
+        } else if (int rc = proj(L.wo.type, L.wo.d, nullptr, AH, E, m->batt, AH, nullptr, nc, 1, m->bx, E,
+                                 "attn_output")) {
             return rc;
         }
         // A verify batch's gate/up also writes the down projection's
@@ -603,23 +707,27 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
         if (down_rec) {
             TS5_HIP(ctx, launch_gemm_fused(L.gate.d, L.up.d, E, F, m->bx, E, (const float *)L.ffn_norm.d, eps, nc, 2,
                                            m->bffn, m->bffn, F, s, m->bact));
+            TS5_STAMP("matmul_fused_" + type_tag(L.gate.type), "ffn_gate+up");
             TS5_HIP(ctx, launch_gemm(L.down.type, L.down.d, nullptr, F, E, m->bact, nc, 1, m->bx, m->bx, E, m->bgemm, s));
+            TS5_STAMP("matmul_" + type_tag(L.down.type), "ffn_down");
         } else {
             if (int rc = proj(L.gate.type, L.gate.d, L.up.d, E, F, m->bx, E, (const float *)L.ffn_norm.d, nc, 2,
-                              m->bffn, F))
+                              m->bffn, F, "ffn_gate+up"))
                 return rc;
-            if (int rc = proj(L.down.type, L.down.d, nullptr, F, E, m->bffn, F, nullptr, nc, 1, m->bx, E)) return rc;
+            if (int rc = proj(L.down.type, L.down.d, nullptr, F, E, m->bffn, F, nullptr, nc, 1, m->bx, E, "ffn_down"))
+                return rc;
         }
     }
     if (rows) {
         const DevT &out = m->output.set ? m->output : m->tok_embd;
         const float *x = rows == nc ? m->bx : m->bx + (int64_t)(nc - 1) * E;
         if (int rc = proj(out.type, out.d, nullptr, E, hp.n_vocab, x, E, (const float *)m->out_norm.d, rows, 0, logits,
-                          hp.n_vocab))
+                          hp.n_vocab, m->output.set ? "output" : "token_embd"))
             return rc;
     }
     return TS5HIP_OK;
 }
+#undef TS5_STAMP
 
 int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool want_logits, bool all) {
     ts5hip_ctx *ctx = m->ctx;
@@ -638,6 +746,7 @@ int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool wan
     TS5_HIP(ctx, hipMemcpyAsync(m->seq + pos0, m->pinned_ids, (size_t)n * 4, hipMemcpyHostToDevice, s));
     TS5_HIP(ctx, hipMemcpyAsync(m->state, m->pinned_ids + n, 4, hipMemcpyHostToDevice, s));
     if (m->profile) TS5_HIP(ctx, hipEventRecord(ctx->ev0, s));
+    if (int rc = prof_start(m)) return rc;
     const size_t row_bytes = (size_t)m->hp.n_vocab * 4;
     if (n == 1) {
         if (int rc = launch_token(m, want_logits ? G_LOGITS : G_KV)) return rc;
@@ -653,6 +762,7 @@ int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool wan
                 return rc;
         }
         TS5_HIP(ctx, launch_set_pos(m->state, pos0 + n, s));
+        if (int rc = prof_stamp(m, "set_pos", "")) return rc;
     }
     if (m->profile) TS5_HIP(ctx, hipEventRecord(ctx->ev1, s));
     TS5_HIP(ctx, hipStreamSynchronize(s));
@@ -661,6 +771,7 @@ int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool wan
         TS5_HIP(ctx, hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
         m->prof_ms += ms, m->prof_calls++, m->prof_tokens += n;
     }
+    if (int rc = prof_close(m)) return rc;
     m->rows_valid = rows;
     m->host_fresh = false;
     return TS5HIP_OK;
@@ -743,10 +854,12 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
     m->layers.resize(hp->n_layer);
     m->has_bias.assign(hp->n_layer, false);
     m->n_split = attn_splits(1, hp->n_head_kv, ctx->n_cu);
-    const char *prof = std::getenv("TS5HIP_PROFILE");
-    m->profile = prof && *prof && std::strcmp(prof, "0") != 0;
+    const char *prof = std::getenv("TS5_PROFILE");
+    if (!prof || !*prof) prof = std::getenv("TS5HIP_PROFILE");
+    m->profile = prof && *prof ? std::atoi(prof) : 0;
     const char *graphs = std::getenv("TS5HIP_GRAPHS");
-    m->use_graphs = !(graphs && std::strcmp(graphs, "0") == 0);
+    // Every kernel timed on its own: launched directly, not replayed as a graph.
+    m->use_graphs = !(graphs && std::strcmp(graphs, "0") == 0) && m->profile != 1;
     const int64_t E = hp->n_embd, F = hp->n_ff, HD = hp->head_dim, H = hp->n_head, HKV = hp->n_head_kv;
     const int64_t kv_elems = (int64_t)hp->n_layer * HKV * n_ctx * HD;
     int rc = 0;
@@ -790,6 +903,7 @@ void ts5hip_model_destroy(ts5hip_model *m) {
     for (void *p : m->allocs) (void)hipFree(p);
     free_rows(m);
     if (m->pinned_ids) (void)hipHostFree(m->pinned_ids);
+    for (hipEvent_t e : m->prof_ev) (void)hipEventDestroy(e);
     delete m;
 }
 
@@ -881,10 +995,19 @@ int ts5hip_generate_greedy(ts5hip_model *m, int32_t token, int pos, int n_steps,
     m->pinned_ids[1] = pos;
     TS5_HIP(ctx, hipMemcpyAsync(m->seq + pos, m->pinned_ids, 4, hipMemcpyHostToDevice, s));
     TS5_HIP(ctx, hipMemcpyAsync(m->state, m->pinned_ids + 1, 4, hipMemcpyHostToDevice, s));
+    if (m->profile) TS5_HIP(ctx, hipEventRecord(ctx->ev0, s));
+    if (int rc = prof_start(m)) return rc;
     for (int i = 0; i < n_steps; i++)
         if (int rc = launch_token(m, G_GREEDY)) return rc;
+    if (m->profile) TS5_HIP(ctx, hipEventRecord(ctx->ev1, s));
     TS5_HIP(ctx, hipMemcpyAsync(m->pinned_ids, m->seq + pos + 1, (size_t)n_steps * 4, hipMemcpyDeviceToHost, s));
     TS5_HIP(ctx, hipStreamSynchronize(s));
+    if (m->profile) {
+        float ms = 0;
+        TS5_HIP(ctx, hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
+        m->prof_ms += ms, m->prof_calls++, m->prof_tokens += n_steps;
+    }
+    if (int rc = prof_close(m)) return rc;
     if (ids_out) std::memcpy(ids_out, m->pinned_ids, (size_t)n_steps * 4);
     m->rows_valid = 0;
     return TS5HIP_OK;
@@ -928,15 +1051,31 @@ int ts5hip_kv_write(ts5hip_model *m, int layer, int which, int pos0, int n, cons
 int ts5hip_take_profile(ts5hip_model *m, char *buf, int len) {
     if (!m || !buf || len <= 0) return fail(m ? m->ctx : nullptr, TS5HIP_ERR_ARG, "bad argument");
     std::string s;
+    char line[320];
     if (m->profile && m->prof_calls) {
-        char line[256];
         std::snprintf(line, sizeof line, "hip: %d forward calls, %d tokens, %.3f ms GPU (%.3f ms/token)\n",
                       m->prof_calls, m->prof_tokens, m->prof_ms, m->prof_ms / std::max(1, m->prof_tokens));
         s = line;
     }
+    // Kernels by GPU time, most first: kernel and weight role, ms, share, launches.
+    std::vector<std::pair<std::string, std::pair<double, int>>> k(m->prof_kernels.begin(), m->prof_kernels.end());
+    std::stable_sort(k.begin(), k.end(), [](const auto &a, const auto &b) { return a.second.first > b.second.first; });
+    double total = 0;
+    for (const auto &e : k) total += e.second.first;
+    if (!k.empty()) {
+        std::snprintf(line, sizeof line, "GPU time %.1f ms:\n", total);
+        s += line;
+    }
+    for (const auto &e : k) {
+        std::snprintf(line, sizeof line, "  %-32s %9.3f ms %5.1f%% %7d calls\n", e.first.c_str(), e.second.first,
+                      total > 0 ? 100.0 * e.second.first / total : 0.0, e.second.second);
+        s += line;
+    }
+    // A buffer too small keeps the profile for a call with a larger one.
+    if ((int)s.size() >= len) return fail(m->ctx, TS5HIP_ERR_ARG, "a profile of %zu bytes in a buffer of %d", s.size() + 1, len);
+    std::memcpy(buf, s.c_str(), s.size() + 1);
     m->prof_ms = 0, m->prof_calls = 0, m->prof_tokens = 0;
-    std::strncpy(buf, s.c_str(), (size_t)len - 1);
-    buf[len - 1] = 0;
+    m->prof_kernels.clear();
     return TS5HIP_OK;
 }
 

@@ -470,8 +470,9 @@ class Model:
         return ("direct", "graphs")[rc]
 
     def take_profile(self) -> str:
-        buf = C.create_string_buffer(4096)
-        self.ctx.check(lib().ts5hip_take_profile(self.h, buf, 4096))
+        """Backend::take_profile: the profile text since the last call (empty unless TS5_PROFILE was set)."""
+        buf = C.create_string_buffer(1 << 16)
+        self.ctx.check(lib().ts5hip_take_profile(self.h, buf, 1 << 16))
         return buf.value.decode()
 
 

@@ -65,7 +65,10 @@ int ts5hip_timer_marks(ts5hip_ctx *ctx, int n, float *ms);
 
 /* ---- weights (replaces VkBackend::upload_weights, engine/src/vk_backend.cpp:531-600) ---- */
 
-/* Whether a matrix of this GGML type has GPU kernels (vk_supports_type, engine/src/backend.h:89). */
+/* Whether a matrix of this GGML type has GPU kernels (vk_supports_type, engine/src/backend.h:89): the
+ * reference's GPU types (engine/src/vk_backend.cpp:156-170) F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0,
+ * Q4_K, Q5_K, Q6_K. Q4_0, Q4_1, Q5_0, Q5_1 and Q5_K are unpacked at upload, exactly, into int8
+ * quants with an fp32 (scale, min) per 32 values; F16 / F32 rows are read as they are. */
 int ts5hip_supports_type(uint32_t type);
 /* Bytes of a (ne1 rows x ne0 values) tensor in its HBM layout; -1 if unsupported. */
 int64_t ts5hip_weight_bytes(uint32_t type, int64_t ne0, int64_t ne1);

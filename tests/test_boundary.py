@@ -43,8 +43,12 @@ def test_weight_layout_sizes():
     assert L.ts5hip_weight_bytes(ts5hip.Q6_K, 4096, 128256) == -(-nb * 208 // 256) * 256 + -(-nb * 2 // 256) * 256
     assert L.ts5hip_weight_bytes(ts5hip.Q8_0, 896, 896) == -(-896 * 28 * 32 // 256) * 256 + -(-896 * 28 * 2 // 256) * 256
     assert L.ts5hip_weight_bytes(ts5hip.Q4_K, 100, 4) == -1   # not whole blocks
-    assert L.ts5hip_weight_bytes(13, 256, 4) == -1           # Q5_K: no kernels
-    assert [L.ts5hip_supports_type(t) for t in (0, 1, 8, 12, 13, 14)] == [0, 0, 1, 1, 0, 1]
+    # Q4_0, Q4_1, Q5_0, Q5_1, Q5_K: an int8 quant a value and an fp32 (scale, min) pair per 32 values.
+    assert L.ts5hip_weight_bytes(13, 256, 4) == 32 * 32 + 32 * 8
+    assert L.ts5hip_weight_bytes(2, 32, 9) == 512 + 256
+    assert L.ts5hip_weight_bytes(30, 256, 4) == -1           # BF16: not a GPU type of the reference
+    # The reference's GPU matrix types (engine/src/vk_backend.cpp:156-170), and not BF16.
+    assert [L.ts5hip_supports_type(t) for t in (0, 1, 2, 3, 6, 7, 8, 12, 13, 14, 30)] == [1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0]
     assert L.ts5hip_act_bytes(4096) > 2 * 4096 and L.ts5hip_act_bytes(100) == -1
 
 

@@ -38,10 +38,11 @@ int hip_fail(ts5hip_ctx *ctx, hipError_t e, const char *what) {
 
 int upload_weight(ts5hip_ctx *ctx, uint32_t t, int64_t ne0, int64_t nrows, const void *gguf, void *dst, int64_t row0,
                   int64_t total_rows) {
-    const SplitDst d = split_dst(t, ne0, total_rows, dst, row0);
-    const int64_t nblocks = ne0 / block_values(t) * nrows;
+    const uint32_t dt = device_type(t);
+    const SplitDst d = split_dst(dt, ne0, total_rows, dst, row0);
+    const int64_t nblocks = ne0 / block_values(t) * nrows;  // GGUF blocks
     const size_t src_bytes = (size_t)nblocks * gguf_block_bytes(t);
-    if (t != T_Q6_K && t != T_Q8_0) return ts5hip_upload(ctx, d.body, gguf, src_bytes);
+    if (!split_layout(dt)) return ts5hip_upload(ctx, d.body, gguf, src_bytes);
     // Split layouts: stage the GGUF blocks in HBM, then repack on the device.
     void *tmp = nullptr;
     TS5_HIP(ctx, hipMalloc(&tmp, src_bytes));
@@ -198,7 +199,13 @@ int ts5hip_timer_end(ts5hip_ctx *ctx, float *ms) {
 }
 
 // ---- weights ------------------------------------------------------------------
-int ts5hip_supports_type(uint32_t type) { return type == T_Q4_K || type == T_Q6_K || type == T_Q8_0; }
+int ts5hip_supports_type(uint32_t type) {
+    switch (type) {
+    case T_F32: case T_F16: case T_Q4_0: case T_Q4_1: case T_Q5_0: case T_Q5_1: case T_Q8_0: case T_Q4_K:
+    case T_Q5_K: case T_Q6_K: return 1;
+    }
+    return 0;
+}
 
 int64_t ts5hip_weight_bytes(uint32_t type, int64_t ne0, int64_t ne1) {
     if (ne0 <= 0 || ne1 <= 0) return -1;
@@ -216,8 +223,8 @@ int ts5hip_weight_upload(ts5hip_ctx *ctx, uint32_t type, int64_t ne0, int64_t ne
 int ts5hip_weight_synth(ts5hip_ctx *ctx, uint32_t type, int64_t ne0, int64_t ne1, uint64_t seed, int centered,
                         void *dst) {
     if (!ctx || !dst) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
-    if (ts5hip_weight_bytes(type, ne0, ne1) < 0)
-        return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "type %u with %lld x %lld", type, (long long)ne0, (long long)ne1);
+    if (ts5hip_weight_bytes(type, ne0, ne1) < 0 || device_type(type) != type)
+        return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "synthetic type %u with %lld x %lld", type, (long long)ne0, (long long)ne1);
     const SplitDst d = split_dst(type, ne0, ne1, dst, 0);
     TS5_HIP(ctx, launch_synth(type, ne0, ne1, seed, centered, d.body, d.scales, ctx->stream));
     return TS5HIP_OK;
@@ -236,7 +243,7 @@ int ts5hip_dequantize(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0
     if (!ctx || !w || !y) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
     if (type != T_F32 && type != T_F16 && ts5hip_weight_bytes(type, ne0, rows) < 0)
         return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "type %u with ne0 %lld", type, (long long)ne0);
-    TS5_HIP(ctx, launch_dequant(type, w, ne0, rows, y, ctx->stream));
+    TS5_HIP(ctx, launch_dequant(device_type(type), w, ne0, rows, y, ctx->stream));
     return TS5HIP_OK;
 }
 
@@ -262,6 +269,7 @@ static int check_matrix(ts5hip_ctx *ctx, uint32_t type, int64_t ne0, int64_t ne1
         return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "matvec of type %u, %lld x %lld", type, (long long)ne1,
                     (long long)ne0);
     if (ne0 > 16384) return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "input of %lld values (at most 16384)", (long long)ne0);
+    if (ne0 % 32) return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "rows of %lld values (a multiple of 32)", (long long)ne0);
     return TS5HIP_OK;
 }
 
@@ -269,7 +277,7 @@ int ts5hip_matvec(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t ne0, in
                   const float *norm_w, float eps, float *y, int accumulate) {
     if (!ctx || !w || !x || !y) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
     if (int rc = check_matrix(ctx, type, ne0, ne1)) return rc;
-    TS5_HIP(ctx, launch_matvec(type, w, ne0, ne1, x, norm_w, eps, y, accumulate, ctx->stream));
+    TS5_HIP(ctx, launch_matvec(device_type(type), w, ne0, ne1, x, norm_w, eps, y, accumulate, ctx->stream));
     return TS5HIP_OK;
 }
 
@@ -277,7 +285,7 @@ int ts5hip_matvec_glu(ts5hip_ctx *ctx, uint32_t type, const void *w_gate, const 
                       const float *x, const float *norm_w, float eps, float *y) {
     if (!ctx || !w_gate || !w_up || !x || !y) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
     if (int rc = check_matrix(ctx, type, ne0, ne1)) return rc;
-    TS5_HIP(ctx, launch_matvec_glu(type, w_gate, w_up, ne0, ne1, x, norm_w, eps, y, ctx->stream));
+    TS5_HIP(ctx, launch_matvec_glu(device_type(type), w_gate, w_up, ne0, ne1, x, norm_w, eps, y, ctx->stream));
     return TS5HIP_OK;
 }
 
@@ -287,6 +295,11 @@ static int matmul_any(ts5hip_ctx *ctx, uint32_t type, const void *w, const void 
     if (!ctx || !w || !x || !y || (mode == 2 && !w2)) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
     if (ntok < 1 || ntok > 4096) return fail(ctx, TS5HIP_ERR_ARG, "ntok %d outside 1..4096", ntok);
     if (int rc = check_matrix(ctx, type, ne0, ne1)) return rc;
+    type = device_type(type);
+    if (type == T_F16 || type == T_F32) {
+        TS5_HIP(ctx, launch_matvec_tokens(type, w, w2, ne0, ne1, x, ne0, norm_w, eps, ntok, mode, y, ne1, ctx->stream));
+        return TS5HIP_OK;
+    }
     if (gemm_fused_fits(type, ne0, ntok)) {
         TS5_HIP(ctx, launch_gemm_fused(w, w2, ne0, ne1, x, ne0, norm_w, eps, ntok, mode, y, y, ne1, ctx->stream));
         return TS5HIP_OK;
@@ -315,7 +328,7 @@ int ts5hip_matvec_argmax(ts5hip_ctx *ctx, uint32_t type, const void *w, int64_t 
     if (!ctx || !w || !x || !y || !out_dev) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
     if (int rc = check_matrix(ctx, type, ne0, ne1)) return rc;
     if (int rc = ensure_scratch(ctx, matvec_argmax_scratch_bytes())) return rc;
-    TS5_HIP(ctx, launch_matvec_argmax(type, w, ne0, ne1, x, norm_w, eps, y, ctx->scratch, ctx->counters + 4096 * CTR_STRIDE,
+    TS5_HIP(ctx, launch_matvec_argmax(device_type(type), w, ne0, ne1, x, norm_w, eps, y, ctx->scratch, ctx->counters + 4096 * CTR_STRIDE,
                                       out_dev, nullptr, nullptr, ctx->stream));
     return TS5HIP_OK;
 }

@@ -13,7 +13,17 @@
 namespace ts5hip {
 
 // GGML type ids (engine/src/gguf.h:12-16).
-enum : uint32_t { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+enum : uint32_t {
+    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13,
+    T_Q6_K = 14
+};
+// The HBM layout of Q4_0, Q4_1, Q5_0, Q5_1 and Q5_K matrices (a layout id, not
+// a GGML type): per 32 values 32 int8 quants q and an fp32 pair (s, m) with
+// value = s * q + m, exactly the reference's unpacked value (below).
+constexpr uint32_t T_Q8SM = 0x100;
+__host__ __device__ inline uint32_t device_type(uint32_t t) {
+    return t == T_Q4_0 || t == T_Q4_1 || t == T_Q5_0 || t == T_Q5_1 || t == T_Q5_K ? T_Q8SM : t;
+}
 // KvType (engine/src/backend.h:13).
 enum : int { KV_F32 = 0, KV_F16 = 1, KV_Q8 = 2 };
 
@@ -32,6 +42,15 @@ __host__ __device__ constexpr inline size_t align_up(size_t v, size_t a) { retur
 //        an f16 d array behind it, so bodies load as dwordx4.
 //  Q8_0  GGUF blocks are 34 B. Split into 32 B of int8 quants per block and
 //        an f16 d array behind them.
+//  Q4_0, Q4_1, Q5_0, Q5_1, Q5_K (T_Q8SM): 32 B of int8 quants per 32 values,
+//        then an array of fp32 (s, m) pairs, value = s * q + m. Unpacked at
+//        upload with the reference's own products (engine/src/quants.cpp:
+//        89-131, :157-177), each exact in fp32: Q4_0 / Q5_0 q = nibble - 8 /
+//        5-bit - 16, s = d, m = -0 (adding -0 keeps every value, -0
+//        included); Q4_1 / Q5_1 q = nibble / 5-bit, s = d, m = m; Q5_K per
+//        32-value sub-block j q = 5-bit, s = d * sc_j, m = -(dmin * m_j), the
+//        reference's d1 * q - m1. So the quants fit the Q8_0 kernels, and the
+//        min is one more term per block against the activation's sum.
 //  F32 / F16 unchanged.
 // ---------------------------------------------------------------------------
 constexpr int Q4K_BYTES = 144;
@@ -39,23 +58,45 @@ constexpr int Q6K_BODY = 208;
 constexpr int Q8_BODY = 32;
 
 __host__ __device__ inline int block_values(uint32_t t) {
-    return t == T_Q4_K || t == T_Q6_K ? 256 : t == T_Q8_0 ? 32 : (t == T_F32 || t == T_F16) ? 1 : 0;
+    switch (t) {
+    case T_Q4_K: case T_Q5_K: case T_Q6_K: return 256;
+    case T_Q4_0: case T_Q4_1: case T_Q5_0: case T_Q5_1: case T_Q8_0: case T_Q8SM: return 32;
+    case T_F32: case T_F16: return 1;
+    }
+    return 0;
 }
 // Bytes of one GGUF block (engine/src/gguf.cpp:34-48).
 __host__ __device__ inline int gguf_block_bytes(uint32_t t) {
-    return t == T_Q4_K ? 144 : t == T_Q6_K ? 210 : t == T_Q8_0 ? 34 : t == T_F32 ? 4 : t == T_F16 ? 2 : 0;
+    switch (t) {
+    case T_F32: return 4;
+    case T_F16: return 2;
+    case T_Q4_0: return 18;
+    case T_Q4_1: return 20;
+    case T_Q5_0: return 22;
+    case T_Q5_1: return 24;
+    case T_Q8_0: return 34;
+    case T_Q4_K: return 144;
+    case T_Q5_K: return 176;
+    case T_Q6_K: return 210;
+    }
+    return 0;
 }
-// Offset of the f16 scale array of a split layout of nblocks blocks.
+// Layouts with their quants and their scales in two arrays.
+__host__ __device__ inline bool split_layout(uint32_t t) { return t == T_Q6_K || t == T_Q8_0 || t == T_Q8SM; }
+// Bytes of a block's scales in a split layout.
+__host__ __device__ inline int split_scale_bytes(uint32_t t) { return t == T_Q8SM ? 8 : 2; }
+// Offset of the scale array of a split layout of nblocks blocks.
 __host__ __device__ inline size_t split_scale_offset(uint32_t t, int64_t nblocks) {
     return align_up((size_t)nblocks * (t == T_Q6_K ? Q6K_BODY : Q8_BODY), 256);
 }
-// Bytes of a tensor in its HBM layout; 0 if unsupported.
+// Bytes of a tensor (of GGML type or layout t) in its HBM layout; 0 if unsupported.
 __host__ __device__ inline size_t device_bytes(uint32_t t, int64_t ne0, int64_t ne1) {
     const int bv = block_values(t);
     if (bv == 0 || ne0 % bv) return 0;
-    const int64_t nb = ne0 / bv * ne1;
-    if (t == T_Q6_K || t == T_Q8_0) return split_scale_offset(t, nb) + align_up((size_t)nb * 2, 256);
-    return (size_t)nb * gguf_block_bytes(t);
+    const uint32_t dt = device_type(t);
+    const int64_t nb = ne0 / block_values(dt) * ne1;
+    if (split_layout(dt)) return split_scale_offset(dt, nb) + align_up((size_t)nb * split_scale_bytes(dt), 256);
+    return (size_t)nb * gguf_block_bytes(dt);
 }
 
 // ---------------------------------------------------------------------------
@@ -297,6 +338,11 @@ __device__ inline float unpack_value(uint32_t t, const uint8_t *base, int64_t nb
         const int64_t blk = row * nb + i / 32;
         const uint16_t *ds = (const uint16_t *)(base + split_scale_offset(T_Q8_0, nblocks));
         return (float)((const int8_t *)base)[blk * Q8_BODY + (i & 31)] * h2f(ds[blk]);
+    }
+    case T_Q8SM: {  // s * q exact: one rounding, with or without contraction
+        const int64_t blk = row * nb + i / 32;
+        const float2 sm = ((const float2 *)(base + split_scale_offset(T_Q8SM, nblocks)))[blk];
+        return (float)((const int8_t *)base)[blk * Q8_BODY + (i & 31)] * sm.x + sm.y;
     }
     case T_Q4_K: {
         const uint8_t *b = base + (row * nb + i / 256) * Q4K_BYTES;

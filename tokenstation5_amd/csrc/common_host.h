@@ -18,9 +18,10 @@ inline SplitDst split_dst(uint32_t t, int64_t ne0, int64_t total_rows, void *bas
     const int bv = block_values(t);
     const int64_t nb = ne0 / bv;
     uint8_t *b = (uint8_t *)base;
-    if (t == T_Q6_K || t == T_Q8_0) {
+    if (split_layout(t)) {
         const int body = t == T_Q6_K ? Q6K_BODY : Q8_BODY;
-        return SplitDst{b + row0 * nb * body, b + split_scale_offset(t, nb * total_rows) + row0 * nb * 2};
+        return SplitDst{b + row0 * nb * body,
+                        b + split_scale_offset(t, nb * total_rows) + row0 * nb * split_scale_bytes(t)};
     }
     return SplitDst{b + (size_t)row0 * nb * gguf_block_bytes(t), nullptr};
 }

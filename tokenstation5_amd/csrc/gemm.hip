@@ -91,7 +91,11 @@ struct GemmLds {
     __align__(16) float2 scl[2][16][16];  // [matrix][sub-block / group][row]
 };
 
-constexpr int F_Q4K = 0, F_Q6K = 1, F_Q80 = 2;
+// F_Q8M: the Q8SM layout (Q4_0, Q4_1, Q5_0, Q5_1, Q5_K), Q8_0's products plus
+// a min per 32 values against the chunk's activation sum.
+constexpr int F_Q4K = 0, F_Q6K = 1, F_Q80 = 2, F_Q8M = 3;
+template <int FMT>
+constexpr bool q8_rows = FMT == F_Q80 || FMT == F_Q8M;
 
 // Activation fragments of token tok for 32-value chunk s of block b, k-group
 // kq, and the chunk's scale and sum: Q4_K / Q6_K rows read the matmul layout
@@ -108,7 +112,7 @@ template <int FMT>
 __device__ inline AFrag act_frag(const GemmArgs &a, int tok, int b, int s, int kq) {
     AFrag f{{0, 0, 0}, 0.f, 0.f};
     if (tok < a.M) {
-        if constexpr (FMT == F_Q80) {
+        if constexpr (q8_rows<FMT>) {
             const CAct x = cact_view(a.act + (int64_t)tok * a.act_stride, a.n_in);
             f.p[0] = ld8(x.hi + 32 * b + 8 * kq);
             f.p[1] = ld8(x.mid + 32 * b + 8 * kq);
@@ -149,13 +153,18 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 
     for (int b = b0; b < b1; b++) {
         __builtin_amdgcn_wave_barrier();  // this wave's reads of the last block's scales are issued
-        if constexpr (FMT == F_Q80) {
+        if constexpr (q8_rows<FMT>) {
             uint64_t q[NW];
 #pragma unroll
             for (int m = 0; m < NW; m++) {
                 const int64_t blk = (int64_t)(rin ? row : 0) * a.nb + b;
                 q[m] = rin ? ld8((m ? a.w2 : a.w) + blk * Q8_BODY + 8 * kq) : 0;
-                if (kq == 0) S.scl[m][0][rl] = make_float2(rin ? h2f((m ? a.s2 : a.s)[blk]) : 0.f, 0.f);
+                if (kq == 0) {
+                    if constexpr (FMT == F_Q8M)
+                        S.scl[m][0][rl] = rin ? ((const float2 *)(m ? a.s2 : a.s))[blk] : make_float2(0.f, 0.f);
+                    else
+                        S.scl[m][0][rl] = make_float2(rin ? h2f((m ? a.s2 : a.s)[blk]) : 0.f, 0.f);
+                }
             }
             __builtin_amdgcn_wave_barrier();
             AFrag x[TN];
@@ -165,12 +174,15 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
             for (int m = 0; m < NW; m++) {
                 const float4 sA = *(const float4 *)&S.scl[m][0][4 * kq];
                 const float4 sB = *(const float4 *)&S.scl[m][0][4 * kq + 2];
-                const float d[4] = {sA.x, sA.z, sB.x, sB.z};
+                const float d[4] = {sA.x, sA.z, sB.x, sB.z}, mn[4] = {sA.y, sA.w, sB.y, sB.w};
 #pragma unroll
                 for (int g = 0; g < TN; g++) {
                     const Prod3 c = mfma3(q[m], x[g].p);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) acc[m][g][i] += d[i] * x[g].xs * (float)c.at(i);
+                    for (int i = 0; i < 4; i++) {
+                        acc[m][g][i] += d[i] * x[g].xs * (float)c.at(i);
+                        if constexpr (FMT == F_Q8M) acc[m][g][i] += mn[i] * x[g].xsum;
+                    }
                 }
             }
         } else {  // Q6_K
@@ -271,7 +283,8 @@ struct WBlk {  // one block of the lane's row (rl) and k-group (kq), per matrix
     uint64_t q[NW][4]; // Q4_K: the 4 nibble groups' 8 bytes; Q8_0: q[m][0]; Q6_K: ql (4)
     uint64_t qh[NW][2];
     uint32_t scw[NW];  // Q6_K: the 4 int8 scales of this k-group
-    float d[NW];       // Q6_K / Q8_0 block scale
+    float d[NW];       // Q6_K / Q8_0 / Q8SM block scale
+    float mn[NW];      // Q8SM block min
 };
 
 // Loads are unconditional (a row or token past the end reads the last one,
@@ -292,6 +305,10 @@ __device__ inline WBlk<FMT, NW> load_wblk(const GemmArgs &a, int row, bool rin, 
         } else if constexpr (FMT == F_Q80) {
             w.q[m][0] = ld8(base + blk * Q8_BODY + 8 * kq);
             w.d[m] = h2f((m ? a.s2 : a.s)[blk]);
+        } else if constexpr (FMT == F_Q8M) {
+            w.q[m][0] = ld8(base + blk * Q8_BODY + 8 * kq);
+            const float2 sm = ((const float2 *)(m ? a.s2 : a.s))[blk];
+            w.d[m] = sm.x, w.mn[m] = sm.y;
         } else {
             const uint8_t *body = base + blk * Q6K_BODY;
 #pragma unroll
@@ -313,13 +330,14 @@ __device__ inline void mask_wblk(WBlk<FMT, NW> &w, bool rin) {
     for (int m = 0; m < NW; m++) {
         if constexpr (FMT == F_Q4K) w.hdr[m].x = rin ? w.hdr[m].x : 0u;  // d = dmin = 0
         else w.d[m] = rin ? w.d[m] : 0.f;
+        if constexpr (FMT == F_Q8M) w.mn[m] = rin ? w.mn[m] : 0.f;
     }
 }
 
 // Activation fragments of one block for the lane's token and k-group.
 template <int FMT>
 struct ABlk {
-    static constexpr int C = FMT == F_Q80 ? 1 : 8;  // 32-value chunks per block
+    static constexpr int C = q8_rows<FMT> ? 1 : 8;  // 32-value chunks per block
     uint64_t p[C][3];  // [chunk][plane hi, mid, lo]
     float xs[C], xsum[C];
     int is[FMT == F_Q6K ? 16 : 1];
@@ -329,7 +347,7 @@ template <int FMT>
 __device__ inline ABlk<FMT> load_ablk(const GemmArgs &a, int tok, int kq, int b) {
     ABlk<FMT> x;
     tok = min(tok, a.M - 1);
-    if constexpr (FMT == F_Q80) {
+    if constexpr (q8_rows<FMT>) {
         const CAct xa = cact_view(a.act + (int64_t)tok * a.act_stride, a.n_in);
         x.p[0][0] = ld8(xa.hi + 32 * b + 8 * kq);
         x.p[0][1] = ld8(xa.mid + 32 * b + 8 * kq);
@@ -387,8 +405,8 @@ __device__ inline void compute_blk(GemmLds &S, const WBlk<FMT, NW> &w, const ABl
             const float d = h2f(w.hdr[m].x & 0xffff), dmin = h2f(w.hdr[m].x >> 16);
             S.scl[m][2 * kq][rl] = make_float2(d * (float)sc0, dmin * (float)m0);
             S.scl[m][2 * kq + 1][rl] = make_float2(d * (float)sc1, dmin * (float)m1);
-        } else if constexpr (FMT == F_Q80) {
-            if (kq == 0) S.scl[m][0][rl] = make_float2(w.d[m], 0.f);
+        } else if constexpr (q8_rows<FMT>) {
+            if (kq == 0) S.scl[m][0][rl] = make_float2(w.d[m], FMT == F_Q8M ? w.mn[m] : 0.f);
         } else {
 #pragma unroll
             for (int j = 0; j < 4; j++)
@@ -415,13 +433,16 @@ __device__ inline void compute_blk(GemmLds &S, const WBlk<FMT, NW> &w, const ABl
                     acc[m][i] += dsc[i] * x.xs[s] * (float)(c[0][i] * 65536 + c[1][i] * 256 + c[2][i]) -
                                  dm[i] * x.xsum[s];
             }
-        } else if constexpr (FMT == F_Q80) {
+        } else if constexpr (q8_rows<FMT>) {
             const float4 sA = *(const float4 *)&S.scl[m][0][4 * kq];
             const float4 sB = *(const float4 *)&S.scl[m][0][4 * kq + 2];
-            const float d[4] = {sA.x, sA.z, sB.x, sB.z};
+            const float d[4] = {sA.x, sA.z, sB.x, sB.z}, mn[4] = {sA.y, sA.w, sB.y, sB.w};
             const Prod3 c = mfma3(w.q[m][0], x.p[0]);
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[m][i] += d[i] * x.xs[0] * (float)c.at(i);
+            for (int i = 0; i < 4; i++) {
+                acc[m][i] += d[i] * x.xs[0] * (float)c.at(i);
+                if constexpr (FMT == F_Q8M) acc[m][i] += mn[i] * x.xsum[0];
+            }
         } else {
 #pragma unroll
             for (int c32 = 0; c32 < 8; c32++) {
@@ -1595,7 +1616,7 @@ static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
     }
     if (a.M <= 16) {
         hipLaunchKernelGGL((k_gemm_small<FMT, MODE>), dim3((a.nrows + 15) / 16), dim3(256), 0, s, a);
-    } else if constexpr (FMT == F_Q80) {
+    } else if constexpr (q8_rows<FMT>) {
         if (tn == 4) hipLaunchKernelGGL((k_gemm<FMT, MODE, 4>), grid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((k_gemm<FMT, MODE, 1>), grid, dim3(256), 0, s, a);
     } else if constexpr (FMT == F_Q6K) {
@@ -1612,13 +1633,14 @@ static hipError_t gemm_fmt(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) 
     case T_Q4_K: return gemm_go<F_Q4K, MODE>(a, grid, tn, s);
     case T_Q6_K: return gemm_go<F_Q6K, MODE>(a, grid, tn, s);
     case T_Q8_0: return gemm_go<F_Q80, MODE>(a, grid, tn, s);
+    case T_Q8SM: return gemm_go<F_Q8M, MODE>(a, grid, tn, s);
     }
     return hipErrorInvalidValue;
 }
 
 // Token groups of 16 per wave: 4 for Q8_0 batches past 16 tokens (Q6_K rows
 // keep 1: its 4-group kernel does not fit the register file).
-static int gemm_tn(uint32_t t, int M) { return M > 16 && t == T_Q8_0 ? 4 : 1; }
+static int gemm_tn(uint32_t t, int M) { return M > 16 && (t == T_Q8_0 || t == T_Q8SM) ? 4 : 1; }
 
 static int g_gemm_cu = 256;
 void set_gemm_cu_count(int n) { g_gemm_cu = g_gemm_m_cu = n > 0 ? n : 256; }
@@ -1655,7 +1677,7 @@ hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, i
         return launch_gemm_reduce((const float *)scratch, ks, M, (int)ne1, mode, y, y_in, ldy, s);
     }
     a.act_stride = (int64_t)gemm_act_bytes(t, ne0, M), a.y_in = y_in, a.ldy = ldy;
-    if (t == T_Q6_K || t == T_Q8_0) {
+    if (split_layout(t)) {  // Q8SM: (scale, min) pairs behind the quants, read as float2
         const int64_t nblocks = (int64_t)a.nb * ne1;
         a.s = (const uint16_t *)(a.w + split_scale_offset(t, nblocks));
         a.s2 = w2 ? (const uint16_t *)(a.w2 + split_scale_offset(t, nblocks)) : nullptr;

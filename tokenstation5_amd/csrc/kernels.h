@@ -71,6 +71,11 @@ hipError_t launch_matvec(uint32_t t, const void *w, int64_t ne0, int64_t ne1, co
 // y = silu(Wg x) * (Wu x).
 hipError_t launch_matvec_glu(uint32_t t, const void *wg, const void *wu, int64_t ne0, int64_t ne1, const float *x,
                              const float *norm_w, float eps, float *y, hipStream_t s);
+// ntok tokens (x rows xstride apart, y rows ldy apart) one matvec launch each:
+// mode 0 store, 1 add, 2 gate/up + SiLU (w2 the up rows). F16 / F32 matrices' batches.
+hipError_t launch_matvec_tokens(uint32_t t, const void *w, const void *w2, int64_t ne0, int64_t ne1, const float *x,
+                                int64_t xstride, const float *norm_w, float eps, int ntok, int mode, float *y,
+                                int64_t ldy, hipStream_t s);
 // y = W x and out[0] = the first argmax of y; with seq: seq[*pos + 1] = it, ++*pos.
 // Completion counters (a workgroup counts in; the last one to arrive does the
 // epilogue) sit CTR_STRIDE ints apart: atomics from different workgroups to

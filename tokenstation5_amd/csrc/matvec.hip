@@ -180,6 +180,9 @@ static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
         case T_Q4_K: return mv_go<Q4K, MV_GLU_R, MV_GLU_WAVES, 1, MODE>(a, s);
         case T_Q6_K: return mv_go<Q6K, 2, 4, 1, MODE>(a, s);
         case T_Q8_0: return mv_go<Q80, 2, 4, 1, MODE>(a, s);
+        case T_Q8SM: return mv_go<Q8M, 2, 4, 1, MODE>(a, s);
+        case T_F16: return mv_go<F16W, 2, 4, 1, MODE>(a, s);
+        case T_F32: return mv_go<F32W, 2, 4, 1, MODE>(a, s);
         }
     } else {
         switch (a.t) {
@@ -193,6 +196,9 @@ static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
             }
         case T_Q6_K: return mv_go<Q6K, MV_Q6_R, 4, 1, MODE>(a, s);
         case T_Q8_0: return mv_go<Q80, 4, 4, 1, MODE>(a, s);
+        case T_Q8SM: return mv_go<Q8M, 4, 4, 1, MODE>(a, s);
+        case T_F16: return mv_go<F16W, 4, 4, 1, MODE>(a, s);
+        case T_F32: return mv_go<F32W, 2, 4, 1, MODE>(a, s);
         }
     }
     return hipErrorInvalidValue;
@@ -201,7 +207,8 @@ static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
 static MvArgs mv_args(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const float *x, const float *norm_w,
                       float eps, float *y) {
     MvArgs a{};
-    a.t = t, a.w = w, a.w2 = nullptr, a.nrows = ne1, a.nb = (int)(ne0 / block_values(t)), a.n_in = (int)ne0;
+    const int bv = t == T_F16 || t == T_F32 ? 32 : block_values(t);  // float rows: 32-value blocks
+    a.t = t, a.w = w, a.w2 = nullptr, a.nrows = ne1, a.nb = (int)(ne0 / bv), a.n_in = (int)ne0;
     a.x = x, a.norm_w = norm_w, a.eps = eps, a.y = y, a.y_in = y;
     return a;
 }
@@ -217,6 +224,21 @@ hipError_t launch_matvec_glu(uint32_t t, const void *wg, const void *wu, int64_t
     MvArgs a = mv_args(t, wg, ne0, ne1, x, norm_w, eps, y);
     a.w2 = wu;
     return mv_dispatch<MV_GLU>(a, s);
+}
+
+// Several tokens of F16 / F32 rows (no matrix-core path): the one-token
+// matvec per token.
+hipError_t launch_matvec_tokens(uint32_t t, const void *w, const void *w2, int64_t ne0, int64_t ne1, const float *x,
+                                int64_t xstride, const float *norm_w, float eps, int ntok, int mode, float *y,
+                                int64_t ldy, hipStream_t s) {
+    for (int k = 0; k < ntok; k++) {
+        const float *xk = x + (int64_t)k * xstride;
+        float *yk = y + (int64_t)k * ldy;
+        const hipError_t e = mode == 2 ? launch_matvec_glu(t, w, w2, ne0, ne1, xk, norm_w, eps, yk, s)
+                                       : launch_matvec(t, w, ne0, ne1, xk, norm_w, eps, yk, mode == 1, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 // Per-workgroup partials of the argmax epilogue: best values then best rows.

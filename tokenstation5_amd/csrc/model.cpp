@@ -30,7 +30,8 @@ using namespace ts5hip;
 namespace {
 
 struct DevT {
-    uint32_t type = 0;
+    uint32_t type = 0;   // the HBM layout the kernels read (device_type of gtype)
+    uint32_t gtype = 0;  // the GGML type the tensor came in
     int64_t ne0 = 0, ne1 = 0;
     void *d = nullptr;
     bool set = false;
@@ -41,6 +42,8 @@ struct LayerDev {
     DevT qkv;                    // [q; k; v] rows of one type
     DevT part[3];                // a q/k/v matrix whose type differs from qkv's
     bool in_qkv[3] = {false, false, false};
+    bool qkv_done[3] = {false, false, false};  // every row of the part in qkv has been set
+    bool qkv_apart = false;  // q, k and v of different types with a split layout: each in its own buffer
     DevT wo, gate, up, down;
 };
 
@@ -137,6 +140,7 @@ std::string type_tag(uint32_t t) {
     case T_F32: return "f32";
     case T_F16: return "f16";
     case T_Q8_0: return "q8_0";
+    case T_Q8SM: return "q8sm";
     case T_Q4_K: return "q4_k";
     case T_Q6_K: return "q6_k";
     default: return "t" + std::to_string(t);
@@ -224,13 +228,13 @@ int host_floats(ts5hip_ctx *ctx, uint32_t type, int64_t n, const void *src, std:
 
 // Allocates t (once) for a matrix of this shape and type.
 int matrix_slot(ts5hip_model *m, DevT &t, uint32_t type, int64_t ne0, int64_t ne1) {
-    if (ts5hip_weight_bytes(type, ne0, ne1) < 0 || !ts5hip_supports_type(type))
+    if (ts5hip_weight_bytes(type, ne0, ne1) < 0 || !ts5hip_supports_type(type) || ne0 % 32)
         return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "matrix of type %u, %lld x %lld", type, (long long)ne1,
                     (long long)ne0);
-    if (t.d && (t.type != type || t.ne0 != ne0 || t.ne1 != ne1)) return fail(m->ctx, TS5HIP_ERR_ARG, "tensor reshaped");
+    if (t.d && (t.gtype != type || t.ne0 != ne0 || t.ne1 != ne1)) return fail(m->ctx, TS5HIP_ERR_ARG, "tensor reshaped");
     if (!t.d) {
         if (int rc = alloc(m, device_bytes(type, ne0, ne1), &t.d)) return rc;
-        t.type = type, t.ne0 = ne0, t.ne1 = ne1;
+        t.type = device_type(type), t.gtype = type, t.ne0 = ne0, t.ne1 = ne1;
     }
     return TS5HIP_OK;
 }
@@ -249,7 +253,8 @@ struct Source {
 };
 
 int fill_rows(ts5hip_model *m, const DevT &t, int64_t row0, int64_t nrows, const Source &src) {
-    if (src.gguf) return upload_weight(m->ctx, t.type, t.ne0, nrows, src.gguf, t.d, row0, t.ne1);
+    if (src.gguf) return upload_weight(m->ctx, t.gtype, t.ne0, nrows, src.gguf, t.d, row0, t.ne1);
+    if (t.type != t.gtype) return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "synthetic weights of type %u", t.gtype);
     const SplitDst d = split_dst(t.type, t.ne0, t.ne1, t.d, row0);
     TS5_HIP(m->ctx, launch_synth(t.type, t.ne0, nrows, src.seed, src.centered, d.body, d.scales, m->ctx->stream));
     return TS5HIP_OK;
@@ -289,6 +294,33 @@ int set_vector(ts5hip_model *m, DevT &t, uint32_t type, int64_t n, int64_t want,
     return TS5HIP_OK;
 }
 
+// q, k and v of different types where the shared buffer has a split layout:
+// the parts already in it move to buffers of their own (a split layout's
+// matvec finds a tensor's scales right behind its own quants), and the
+// layer's q, k and v stay apart from then on.
+int unfuse_qkv(ts5hip_model *m, LayerDev &L) {
+    const ts5hip_hparams &hp = m->hp;
+    const int64_t E = hp.n_embd, rows[3] = {(int64_t)hp.n_head * hp.head_dim, (int64_t)hp.n_head_kv * hp.head_dim,
+                                            (int64_t)hp.n_head_kv * hp.head_dim};
+    const int64_t row0[3] = {0, rows[0], rows[0] + rows[1]};
+    const uint32_t t = L.qkv.type;
+    for (int p = 0; p < 3; p++) {
+        if (!L.in_qkv[p]) continue;
+        DevT &d = L.part[p];
+        if (int rc = matrix_slot(m, d, L.qkv.gtype, E, rows[p])) return rc;
+        const SplitDst from = split_dst(t, E, m->qkv_rows(), L.qkv.d, row0[p]), to = split_dst(t, E, rows[p], d.d, 0);
+        const int64_t nb = E / block_values(t) * rows[p];
+        TS5_HIP(m->ctx, hipMemcpyAsync(to.body, from.body, (size_t)nb * (t == T_Q6_K ? Q6K_BODY : Q8_BODY),
+                                       hipMemcpyDeviceToDevice, m->ctx->stream));
+        TS5_HIP(m->ctx, hipMemcpyAsync(to.scales, from.scales, (size_t)nb * split_scale_bytes(t),
+                                       hipMemcpyDeviceToDevice, m->ctx->stream));
+        d.set = L.qkv_done[p];
+        L.in_qkv[p] = false;
+    }
+    L.qkv_apart = true;
+    return TS5HIP_OK;
+}
+
 int set_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, int64_t ne1, const Source &src) {
     const ts5hip_hparams &hp = m->hp;
     const int64_t E = hp.n_embd, F = hp.n_ff, HD = hp.head_dim, H = hp.n_head, HKV = hp.n_head_kv;
@@ -303,7 +335,9 @@ int set_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, in
             const size_t bytes = (type == T_F32 || type == T_F16) ? (size_t)ne0 * ne1 * (type == T_F32 ? 4 : 2)
                                                                   : device_bytes(type, ne0, ne1);
             if (int rc = alloc(m, bytes, &m->tok_embd.d)) return rc;
-            m->tok_embd.type = type, m->tok_embd.ne0 = ne0, m->tok_embd.ne1 = ne1;
+            m->tok_embd.type = device_type(type), m->tok_embd.gtype = type, m->tok_embd.ne0 = ne0, m->tok_embd.ne1 = ne1;
+        } else if (m->tok_embd.gtype != type) {
+            return fail(m->ctx, TS5HIP_ERR_ARG, "tensor reshaped");
         }
         if (type == T_F32 || type == T_F16) {
             if (!src.gguf) return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "synthetic float embeddings");
@@ -346,11 +380,14 @@ int set_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, in
         if (r == std::string(parts[p]) + ".weight") {
             if (ne0 != E || ne1 != rows[p]) return fail(m->ctx, TS5HIP_ERR_ARG, "%s shape", name);
             if (src.row0 < 0 || src.row0 + src.rows(ne1) > ne1) return fail(m->ctx, TS5HIP_ERR_ARG, "%s rows", name);
-            if (!L.qkv.d || L.qkv.type == type) {
+            if (L.qkv.d && L.qkv.gtype != type && split_layout(L.qkv.type) && !L.qkv_apart)
+                if (int rc = unfuse_qkv(m, L)) return rc;
+            if (!L.qkv_apart && (!L.qkv.d || L.qkv.gtype == type)) {
                 if (int rc = matrix_slot(m, L.qkv, type, E, m->qkv_rows())) return rc;
                 if (int rc = fill_rows(m, L.qkv, row0[p] + src.row0, src.rows(ne1), src)) return rc;
                 L.in_qkv[p] = true;
                 L.part[p].set = false;
+                if (src.last(ne1)) L.qkv_done[p] = true;
             } else {
                 if (int rc = set_matrix(m, L.part[p], type, ne0, ne1, E, rows[p], src, name)) return rc;
                 L.in_qkv[p] = false;
@@ -378,8 +415,8 @@ int check_complete(ts5hip_model *m) {
     };
     if (int rc = need(m->tok_embd, "token_embd.weight", -1)) return rc;
     if (int rc = need(m->out_norm, "output_norm.weight", -1)) return rc;
-    if (!m->output.set && !ts5hip_supports_type(m->tok_embd.type))
-        return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "tied output head of type %u", m->tok_embd.type);
+    if (!m->output.set && !ts5hip_supports_type(m->tok_embd.gtype))
+        return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "tied output head of type %u", m->tok_embd.gtype);
     for (int l = 0; l < m->hp.n_layer; l++) {
         const LayerDev &L = m->layers[l];
         if (int rc = need(L.attn_norm, "attn_norm.weight", l)) return rc;
@@ -431,7 +468,7 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
             int64_t r0 = 0;
             for (int p = 0; p < 3; p++) {
                 if (L.in_qkv[p]) {
-                    if (L.qkv.type == T_Q6_K || L.qkv.type == T_Q8_0)
+                    if (split_layout(L.qkv.type))  // unfuse_qkv keeps this from happening
                         return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "mixed q/k/v types with a split layout");
                     const SplitDst d = split_dst(L.qkv.type, E, QR, L.qkv.d, r0);
                     TS5_HIP(ctx, launch_matvec(L.qkv.type, d.body, E, rows[p], m->x, an, hp.rms_eps, m->qkv + r0, 0, s));
@@ -617,6 +654,11 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
     auto proj = [&](uint32_t t, const void *w, const void *w2, int64_t ne0, int64_t ne1, const float *x,
                     int64_t xstride, const float *norm, int ntok, int mode, float *y, int64_t ldy,
                     const char *role) -> int {
+        if (t == T_F16 || t == T_F32) {  // float rows: the one-token matvec per token
+            TS5_HIP(ctx, launch_matvec_tokens(t, w, w2, ne0, ne1, x, xstride, norm, eps, ntok, mode, y, ldy, s));
+            TS5_STAMP("matvec_" + type_tag(t) + "_tokens", role);
+            return TS5HIP_OK;
+        }
         if (gemm_fused_fits(t, ne0, ntok)) {
             TS5_HIP(ctx, launch_gemm_fused(w, w2, ne0, ne1, x, xstride, norm, eps, ntok, mode, y, y, ldy, s));
             TS5_STAMP("matmul_fused_" + type_tag(t), role);
@@ -642,7 +684,7 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
             int64_t r0 = 0;
             for (int p = 0; p < 3; p++) {
                 if (L.in_qkv[p]) {
-                    if (L.qkv.type == T_Q6_K || L.qkv.type == T_Q8_0)
+                    if (split_layout(L.qkv.type))  // unfuse_qkv keeps this from happening
                         return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "mixed q/k/v types with a split layout");
                     const SplitDst d = split_dst(L.qkv.type, E, QR, L.qkv.d, r0);
                     if (int rc = proj(L.qkv.type, d.body, nullptr, E, prow[p], m->bx, E, an, nc, 0, m->bqkv + r0, QR,

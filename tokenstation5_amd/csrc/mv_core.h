@@ -16,6 +16,9 @@
 //      Q4_K: y += d*sc*(xs*sum q*X) - dmin*m*(sum x)     (quants.cpp:140-157)
 //      Q6_K: y += d*sc*xs*(sum q*X - 32*sum X)           (quants.cpp:179-202)
 //      Q8_0: y += d*xs*(sum q*X)                         (quants.cpp:133-139)
+//      Q8SM: y += s*xs*(sum q*X) + m*(sum x)   (Q4_0, Q4_1, Q5_0, Q5_1, Q5_K)
+//      F16 / F32: y += xs*(sum w*X), w the fp32 value, X exact in fp32
+//      (|X| < 2^22), products and sums in fp32 (quants.cpp:78-82)
 //  * Persistent row groups: a workgroup walks its groups (R rows per wave)
 //    as a flat sequence of steps (one 64-lane sweep of 64/LPB blocks each)
 //    and always has the next step's weight loads in flight while it computes
@@ -32,14 +35,16 @@
 namespace ts5hip {
 
 struct WPtr {
-    const uint8_t *body;     // blocks (Q4_K: whole blocks; Q6_K/Q8_0: bodies)
-    const uint16_t *dscale;  // f16 block scales of split layouts
+    const uint8_t *body;     // blocks (Q4_K: whole blocks; Q6_K/Q8_0/Q8SM: bodies)
+    const uint16_t *dscale;  // f16 block scales of Q6_K / Q8_0
+    const float2 *sm;        // (scale, min) pairs of Q8SM
 };
 
 __device__ inline WPtr wptr(uint32_t t, const void *w, int64_t nblocks) {
     WPtr p;
     p.body = (const uint8_t *)w;
     p.dscale = (t == T_Q6_K || t == T_Q8_0) ? (const uint16_t *)(p.body + split_scale_offset(t, nblocks)) : nullptr;
+    p.sm = t == T_Q8SM ? (const float2 *)(p.body + split_scale_offset(t, nblocks)) : nullptr;
     return p;
 }
 
@@ -231,6 +236,103 @@ struct Q80 {
         return w.d * x.s * (float)v;
     }
 };
+
+// Q8SM: Q8_0's lanes and products, and the block's min against the sum of
+// its 32 activation values (the unquantized fp32 sum), added by lane 0 of
+// the block's pair.
+struct Q8M {
+    static constexpr int LPB = 2, VALUES = 32;
+    static constexpr int LOADS = 2;  // vector memory loads per load_w
+    struct X {
+        uint4 p[3];
+        float s, u;  // scale; the block's sum of x on sub 0, else 0
+    };
+    struct W {
+        uint4 q;
+        float2 sm;
+    };
+    __device__ static X load_x(const CAct &x, int b, int sub) {
+        X r;
+        r.p[0] = ld16(x.hi + b * 32 + 16 * sub);
+        r.p[1] = ld16(x.mid + b * 32 + 16 * sub);
+        r.p[2] = ld16(x.lo + b * 32 + 16 * sub);
+        r.s = x.scale[b];
+        r.u = sub == 0 ? x.sum[b] : 0.f;
+        return r;
+    }
+    __device__ static W load_w(const WPtr &w, int64_t row, int nb, int b, int sub) {
+        const size_t blk = (size_t)row * nb + b;
+        W r;
+        r.q = ld16(w.body + blk * Q8_BODY + 16 * sub);
+        r.sm = w.sm[blk];
+        return r;
+    }
+    __device__ static float dot(const W &w, const X &x, int) {
+        int a[3] = {0, 0, 0};
+#pragma unroll
+        for (int P = 0; P < 3; P++) {
+            a[P] = dot4((int)w.q.x, (int)x.p[P].x, a[P]);
+            a[P] = dot4((int)w.q.y, (int)x.p[P].y, a[P]);
+            a[P] = dot4((int)w.q.z, (int)x.p[P].z, a[P]);
+            a[P] = dot4((int)w.q.w, (int)x.p[P].w, a[P]);
+        }
+        const long long v = (long long)a[0] * 65536 + a[1] * 256 + a[2];
+        return w.sm.x * x.s * (float)v + w.sm.y * x.u;
+    }
+};
+
+// F16 and F32 rows, in 32-value blocks (64 / 128 bytes): 16 bytes a lane (8
+// halves or 4 floats), against the activation's X = 65536 hi + 256 mid + lo
+// rebuilt per value.
+__device__ inline float x_value(uint32_t hi, uint32_t mid, uint32_t lo, int k) {
+    const int s = 8 * k;
+    return (float)((int)(int8_t)(hi >> s) * 65536 + (int)(int8_t)(mid >> s) * 256 + (int)(int8_t)(lo >> s));
+}
+template <bool HALF>
+struct FloatRows {
+    static constexpr int VPL = HALF ? 8 : 4;  // values a lane
+    static constexpr int LPB = 32 / VPL, VALUES = 32;
+    static constexpr int LOADS = 1;
+    static constexpr int BYTES = HALF ? 64 : 128;  // a block's bytes
+    struct X {
+        uint32_t p[3][VPL / 4];  // the lane's values of the three planes
+        float s;
+    };
+    struct W {
+        uint4 v;
+    };
+    __device__ static X load_x(const CAct &x, int b, int sub) {
+        X r;
+        const int i = b * 32 + VPL * sub;
+        const int8_t *plane[3] = {x.hi, x.mid, x.lo};
+#pragma unroll
+        for (int P = 0; P < 3; P++) {
+            if constexpr (HALF) {
+                const uint2 v = *(const uint2 *)(plane[P] + i);
+                r.p[P][0] = v.x, r.p[P][1] = v.y;
+            } else {
+                r.p[P][0] = *(const uint32_t *)(plane[P] + i);
+            }
+        }
+        r.s = x.scale[b];
+        return r;
+    }
+    __device__ static W load_w(const WPtr &w, int64_t row, int nb, int b, int sub) {
+        return W{ld16(w.body + ((size_t)row * nb + b) * BYTES + 16 * sub)};
+    }
+    __device__ static float dot(const W &w, const X &x, int) {
+        const uint32_t u[4] = {w.v.x, w.v.y, w.v.z, w.v.w};
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < VPL; k++) {
+            const float wv = HALF ? h2f((uint16_t)(u[k / 2] >> (16 * (k & 1)))) : __uint_as_float(u[k]);
+            acc += wv * x_value(x.p[0][k / 4], x.p[1][k / 4], x.p[2][k / 4], k & 3);
+        }
+        return x.s * acc;
+    }
+};
+using F16W = FloatRows<true>;
+using F32W = FloatRows<false>;
 
 // ---------------------------------------------------------------------------
 // The activation prologue: x (n values, optionally rms-normalised by norm_w)

@@ -57,6 +57,53 @@ __global__ void k_repack_split(uint32_t t, const uint8_t *__restrict__ src, int6
     }
 }
 
+// GGUF Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q5_K blocks -> T_Q8SM (common.h): int8
+// quants, 32 a block, and (s, m) with value = s * q + m, the reference's
+// unpack (engine/src/quants.cpp:89-131, :157-177). One thread per GGUF block
+// (a Q5_K block is 8 layout blocks).
+__device__ inline float f16_at(const uint8_t *p) { return h2f((uint16_t)(p[0] | (p[1] << 8))); }
+
+__global__ void k_repack_sm(uint32_t t, const uint8_t *__restrict__ src, int64_t nblocks, int8_t *__restrict__ dst,
+                            float2 *__restrict__ sm) {
+    for (int64_t blk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; blk < nblocks;
+         blk += (int64_t)gridDim.x * blockDim.x) {
+        if (t == T_Q5_K) {
+            const uint8_t *b = src + blk * 176;
+            const float d = f16_at(b), dmin = f16_at(b + 2);
+            const uint8_t *sc = b + 4, *qh = b + 16, *ql = b + 48;
+            const uint32_t *scw = (const uint32_t *)sc;  // 4-byte aligned: 176 B blocks
+            for (int j = 0; j < 8; j++) {
+                int s6, m6;
+                kq_scale_min(j, scw[0], scw[1], scw[2], s6, m6);
+                int8_t *o = dst + (blk * 8 + j) * Q8_BODY;
+                const uint8_t *q4 = ql + 32 * (j / 2);
+                for (int l = 0; l < 32; l++) {
+                    const int lo = j & 1 ? q4[l] >> 4 : q4[l] & 15;
+                    o[l] = (int8_t)(lo | (((qh[l] >> j) & 1) << 4));
+                }
+                sm[blk * 8 + j] = make_float2(d * (float)s6, -(dmin * (float)m6));
+            }
+            continue;
+        }
+        const int bytes = gguf_block_bytes(t);
+        const uint8_t *b = src + blk * bytes;
+        const bool has_min = t == T_Q4_1 || t == T_Q5_1, five = t == T_Q5_0 || t == T_Q5_1;
+        const float d = f16_at(b), m = has_min ? f16_at(b + 2) : -0.0f;
+        const uint8_t *h = b + (has_min ? 4 : 2);
+        const uint32_t qh = five ? (uint32_t)h[0] | (uint32_t)h[1] << 8 | (uint32_t)h[2] << 16 | (uint32_t)h[3] << 24 : 0;
+        const uint8_t *qs = h + (five ? 4 : 0);
+        const int off = has_min ? 0 : five ? 16 : 8;  // Q4_0: nibble - 8, Q5_0: 5-bit - 16
+        int8_t *o = dst + blk * Q8_BODY;
+        for (int j = 0; j < 16; j++) {
+            const int x0 = (qs[j] & 15) | (int)(((qh >> j) & 1) << 4);
+            const int x1 = (qs[j] >> 4) | (int)(((qh >> (j + 16)) & 1) << 4);
+            o[j] = (int8_t)(x0 - off);
+            o[j + 16] = (int8_t)(x1 - off);
+        }
+        sm[blk] = make_float2(d, m);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Random-init weights in HBM (benchmark inputs; no checkpoint is reachable).
 // Field distributions of the benchmark configs: uniform quant bytes, uniform
@@ -189,8 +236,12 @@ hipError_t launch_embed(uint32_t t, const void *w, int64_t ne0, int64_t n_rows, 
 }
 
 hipError_t launch_repack(uint32_t t, int64_t nblocks, const void *gguf, void *body, void *scales, hipStream_t s) {
-    hipLaunchKernelGGL(k_repack_split, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, t, (const uint8_t *)gguf,
-                       nblocks, (uint8_t *)body, (uint16_t *)scales);
+    if (device_type(t) == T_Q8SM)
+        hipLaunchKernelGGL(k_repack_sm, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, t, (const uint8_t *)gguf,
+                           nblocks, (int8_t *)body, (float2 *)scales);
+    else
+        hipLaunchKernelGGL(k_repack_split, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, t, (const uint8_t *)gguf,
+                           nblocks, (uint8_t *)body, (uint16_t *)scales);
     return hipGetLastError();
 }
 

@@ -115,7 +115,12 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
     const int64_t ngroups = (a.nrows + rpg - 1) / rpg;
     const int64_t cap = (int64_t)mv_max_grid();
     const int64_t per = (ngroups + cap - 1) / cap;  // groups per workgroup
-    const unsigned grid = (unsigned)((ngroups + per - 1) / per);
+    // Past the cap every CU holds two workgroups, which the first-dispatched
+    // share below assumes. (A grid of ceil(groups / per) left some CUs one
+    // workgroup: 608 groups gave 304 workgroups, the first 256 one group each
+    // and the other 48 seven or eight; the draft's 896 x 4864 gate/up took
+    // 10.9 us instead of 6.)
+    const unsigned grid = (unsigned)std::min(ngroups, cap);
     // The prologue's inputs in registers (runs per thread, norm weights) when
     // they fit: up to 2 runs with the norm, 4 without; else the two-pass one.
     const int nr = a.n_in / 16, nt = WAVES * WAVE;

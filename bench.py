@@ -173,24 +173,29 @@ def free_busy(ctx):
         b.free()
 
 
-def timed_each(ctx, fn, n: int, warm: int = 3) -> np.ndarray:
-    """Per-launch microseconds of fn(i) over n calls: an event on the
-    library's stream between consecutive launches, which are queued behind
-    ~0.4 ms RMSNorm launches so that the host's launch rate is not timed."""
+def timed_groups(ctx, fn, n: int, group: int, warm: int = 3) -> np.ndarray:
+    """Microseconds per launch of fn(i) in each of n / group groups of
+    back-to-back launches: an event on the library's stream between groups
+    (group 1: between every two launches, which then also times the event's
+    own gap), the launches queued behind ~0.4 ms RMSNorm launches so that the
+    host's launch rate is not timed."""
     for i in range(warm):
         fn(i)
     queue_busy(ctx, 2 + n // 10)
     for i in range(n):
-        ctx.timer_mark(i)
+        if i % group == 0:
+            ctx.timer_mark(i // group)
         fn(i)
-    ctx.timer_mark(n)
-    return ctx.timer_marks(n + 1).astype(np.float64) * 1e3
+    ctx.timer_mark(n // group)
+    return ctx.timer_marks(n // group + 1).astype(np.float64) * 1e3 / group
 
 
 def cfg1_matvec(ctx):
     """cfg1: the 4096x4096 Q4_K matvec alone, 40 rotated copies (378 MB, past
-    the 256 MB Infinity Cache), 200 launches: the median launch (events
-    between launches) and the mean (events around all 200)."""
+    the 256 MB Infinity Cache), 200 launches: the mean (events around all
+    200), the median over 20 groups of 10 back-to-back launches, and the
+    median of launches timed one by one (an event between every two, whose
+    gap it includes)."""
     E = 4096
     copies = 40
     ws = [ctx.weight_synth(synth.Q4_K, E, E, 300 + i) for i in range(copies)]
@@ -198,12 +203,13 @@ def cfg1_matvec(ctx):
     y = ctx.alloc(E * 4)
     run = lambda i: ctx.matvec(synth.Q4_K, ws[i % copies], E, E, x, y)
     mean = timed(ctx, run, 200)
-    med = float(np.median(timed_each(ctx, run, 200)))
+    med = float(np.median(timed_groups(ctx, run, 200, 10)))
+    iso = float(np.median(timed_groups(ctx, run, 200, 1)))
     algo = E * E // 256 * 144 + 4 * E + 4 * E  # 9,469,952 B
     for w in ws:
         w.free()
     return dict(us_median=round(med, 2), gbs_median=round(algo / med / 1e3, 1), us_mean=round(mean, 2),
-                gbs_mean=round(algo / mean / 1e3, 1), bytes=algo)
+                gbs_mean=round(algo / mean / 1e3, 1), us_median_one_by_one=round(iso, 2), bytes=algo)
 
 
 def cfg3_attention(ctx):
@@ -331,6 +337,27 @@ def cfg5_speculation(ctx, gen: int = 512, prompt_len: int = 2048):
         m.close()
     draft.close()
     return res
+
+
+def draft_only(prompt_len: int = 2048, steps: int = 32):
+    """cfg5's draft model alone (centred random weights generated in HBM): the
+    prompt, then `steps` greedy tokens of the device-resident loop, timed on
+    the host around the loop."""
+    ctx = ts5hip.Context(0)
+    hp = synth.DRAFT_0P5B
+    m = ts5hip.Model(ctx, hp, prompt_len + steps + 16)
+    for name, t, ne0, ne1 in synth.tensor_specs(hp):
+        m.synth_tensor(name, t, ne0, ne1, SEED + 5, centered=True)
+    prompt = np.random.default_rng(5).integers(0, hp["n_vocab"], prompt_len).astype(np.int32)
+    first = int(np.argmax(m.forward(prompt, 0)[0]))
+    ctx.sync()
+    t0 = time.perf_counter()
+    m.generate_greedy(first, prompt_len, steps)
+    dt = time.perf_counter() - t0
+    print(json.dumps({"draft_ms_per_token": round(dt / steps * 1e3, 3), "steps": steps, "prompt": prompt_len}),
+          flush=True)
+    m.close()
+    ctx.close()
 
 
 def roofline_only(hp):
@@ -466,6 +493,8 @@ def main():
     ap.add_argument("--no-spec", action="store_true", help="skip cfg5 (draft model + two targets, ~1 min)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the cfg2 decode and its JSON line (for rocprofv3 runs)")
+    ap.add_argument("--draft-only", action="store_true",
+                    help="only cfg5's draft model: a 2048-token prompt, then 32 greedy tokens (for rocprofv3 runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this backend runs ts5's token loop on one GPU (batch 1); "
@@ -480,6 +509,9 @@ def main():
         return
     if args.verify_only:
         verify_only(hp, args.prompt)
+        return
+    if args.draft_only:
+        draft_only()
         return
     ctx = ts5hip.Context(0)
     log(f"device {ctx.arch}, {ctx.n_cu} CUs, {ctx.hbm / 2**30:.0f} GiB")

@@ -3,8 +3,9 @@
 // The fp32 CPU forward pass, restated from engine/src/cpu_backend.cpp:
 // matmul :18-37, rmsnorm :48-53, rope :57-68, round_kv :78-90,
 // CpuBackend::forward :120-146, layer :188-266 (llama / mistral / qwen2 /
-// qwen3 layers: optional q/k/v bias and per-head q/k norm; Gemma 3's sliding
-// window, GELU and post-norms are outside this oracle).
+// qwen3 / gemma3 layers: optional q/k/v bias and per-head q/k norm; Gemma 3's
+// embedding scale, sliding windows with their own RoPE base, GELU and the
+// norms after attention and the FFN), gelu :71-73.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -158,13 +159,20 @@ void ts5o_swiglu(float *g, const float *u, int64_t n) {
     for (int64_t i = 0; i < n; i++) g[i] = g[i] / (1.0f + std::exp(-g[i])) * u[i];
 }
 
+void ts5o_geglu(float *g, const float *u, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        const float x = g[i];
+        g[i] = 0.5f * x * (1.0f + std::tanh(0.7978845608f * (x + 0.044715f * x * x * x))) * u[i];
+    }
+}
+
 }  // extern "C"
 
 struct ts5o_model {
     ts5o_hparams hp;
     ts5o_tensor tok_embd, output;
     std::vector<ts5o_layer> layers;
-    struct Small { std::vector<float> attn, ffn, q, k, bq, bk, bv; };
+    struct Small { std::vector<float> attn, ffn, q, k, bq, bk, bv, post_attn, post_ffn; };
     std::vector<Small> small;
     std::vector<float> out_norm, freqs;
     int n_ctx, kv, threads;
@@ -185,6 +193,10 @@ struct ts5o_model {
         matmul(L.wv, h.data(), n, v.data());
         float *kl = &kc[(size_t)l * n_ctx * KV], *vl = &vc[(size_t)l * n_ctx * KV];
         const float *ff = freqs.empty() ? nullptr : freqs.data();
+        // A sliding layer (model.h:41): its own RoPE base, no position scaling,
+        // and only the last swa_window keys.
+        const bool swa = hp.swa_window > 0 && hp.swa_pattern > 0 && l % hp.swa_pattern < hp.swa_pattern - 1;
+        const float base = swa ? hp.rope_base_swa : hp.rope_base, rs = swa ? 1.f : hp.rope_scale;
         for (int t = 0; t < n; t++) {
             float *qt = &q[(size_t)t * H * HD], *kt = &k[(size_t)t * KV], *vt = &v[(size_t)t * KV];
             const int pos = pos0 + t;
@@ -194,11 +206,11 @@ struct ts5o_model {
             }
             for (int hh = 0; hh < H; hh++) {
                 if (!S.q.empty()) ts5o_rmsnorm(&qt[hh * HD], S.q.data(), HD, hp.rms_eps);
-                ts5o_rope(&qt[hh * HD], hp.rope_dims, pos, hp.rope_base, hp.rope_neox, ff, hp.rope_scale);
+                ts5o_rope(&qt[hh * HD], hp.rope_dims, pos, base, hp.rope_neox, ff, rs);
             }
             for (int hh = 0; hh < HKV; hh++) {
                 if (!S.k.empty()) ts5o_rmsnorm(&kt[hh * HD], S.k.data(), HD, hp.rms_eps);
-                ts5o_rope(&kt[hh * HD], hp.rope_dims, pos, hp.rope_base, hp.rope_neox, ff, hp.rope_scale);
+                ts5o_rope(&kt[hh * HD], hp.rope_dims, pos, base, hp.rope_neox, ff, rs);
             }
             ts5o_round_kv(kv, kt, KV);
             ts5o_round_kv(kv, vt, KV);
@@ -206,18 +218,27 @@ struct ts5o_model {
             std::memcpy(vl + (size_t)pos * KV, vt, (size_t)KV * 4);
         }
         std::vector<float> att((size_t)n * H * HD), o((size_t)n * E);
-        for (int t = 0; t < n; t++)
-            ts5o_attention(&q[(size_t)t * H * HD], kl, vl, H, HKV, HD, 0, pos0 + t, hp.attn_scale,
+        for (int t = 0; t < n; t++) {
+            const int pos = pos0 + t, lo = swa ? std::max(0, pos - hp.swa_window + 1) : 0;
+            ts5o_attention(&q[(size_t)t * H * HD], kl, vl, H, HKV, HD, lo, pos, hp.attn_scale,
                            &att[(size_t)t * H * HD]);
+        }
         matmul(L.wo, att.data(), n, o.data());
+        if (!S.post_attn.empty())
+            for (int t = 0; t < n; t++) ts5o_rmsnorm(&o[(size_t)t * E], S.post_attn.data(), E, hp.rms_eps);
         for (size_t i = 0; i < (size_t)n * E; i++) x[i] += o[i];
         h.assign(x, x + (size_t)n * E);
         for (int t = 0; t < n; t++) ts5o_rmsnorm(&h[(size_t)t * E], S.ffn.data(), E, hp.rms_eps);
         std::vector<float> g((size_t)n * F), u((size_t)n * F);
         matmul(L.w_gate, h.data(), n, g.data());
         matmul(L.w_up, h.data(), n, u.data());
-        ts5o_swiglu(g.data(), u.data(), (int64_t)n * F);
+        if (hp.gelu)
+            ts5o_geglu(g.data(), u.data(), (int64_t)n * F);
+        else
+            ts5o_swiglu(g.data(), u.data(), (int64_t)n * F);
         matmul(L.w_down, g.data(), n, o.data());
+        if (!S.post_ffn.empty())
+            for (int t = 0; t < n; t++) ts5o_rmsnorm(&o[(size_t)t * E], S.post_ffn.data(), E, hp.rms_eps);
         for (size_t i = 0; i < (size_t)n * E; i++) x[i] += o[i];
     }
 };
@@ -241,6 +262,8 @@ ts5o_model *ts5o_model_new(const ts5o_hparams *hp, const ts5o_tensor *tok_embd, 
         s.bq = as_floats(L.bq);
         s.bk = as_floats(L.bk);
         s.bv = as_floats(L.bv);
+        s.post_attn = as_floats(L.post_attn_norm);
+        s.post_ffn = as_floats(L.post_ffn_norm);
         m->small.push_back(std::move(s));
     }
     m->out_norm = as_floats(*out_norm);
@@ -266,9 +289,12 @@ int ts5o_forward(ts5o_model *m, const int32_t *tokens, int n, int pos0, float *l
     const int E = m->hp.n_embd;
     std::vector<float> x((size_t)n * E);
     const int64_t rb = row_bytes_of(m->tok_embd);
-    for (int t = 0; t < n; t++)
+    for (int t = 0; t < n; t++) {
         ts5o_dequantize_row(m->tok_embd.type, (const uint8_t *)m->tok_embd.data + (int64_t)tokens[t] * rb,
                             x.data() + (size_t)t * E, E);
+        if (m->hp.embd_scale > 0)
+            for (int i = 0; i < E; i++) x[(size_t)t * E + i] *= m->hp.embd_scale;
+    }
     for (int l = 0; l < m->hp.n_layer; l++) m->layer(l, x.data(), n, pos0);
     if (!logits) return 0;
     const int nout = all ? n : 1;

@@ -23,7 +23,9 @@ _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
 class HParams(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("n_vocab", "n_embd", "n_layer", "n_ff", "n_head", "n_head_kv",
                                           "head_dim", "rope_dims", "rope_neox")] + \
-               [(n, C.c_float) for n in ("rms_eps", "rope_base", "attn_scale", "rope_scale")]
+               [(n, C.c_float) for n in ("rms_eps", "rope_base", "attn_scale", "rope_scale", "embd_scale",
+                                         "rope_base_swa")] + \
+               [(n, C.c_int32) for n in ("gelu", "swa_window", "swa_pattern")]
 
 
 class Tensor(C.Structure):
@@ -32,7 +34,7 @@ class Tensor(C.Structure):
 
 class Layer(C.Structure):
     _fields_ = [(n, Tensor) for n in ("attn_norm", "wq", "wk", "wv", "wo", "bq", "bk", "bv", "q_norm", "k_norm",
-                                      "ffn_norm", "w_gate", "w_up", "w_down")]
+                                      "ffn_norm", "w_gate", "w_up", "w_down", "post_attn_norm", "post_ffn_norm")]
 
 
 def build() -> None:
@@ -62,6 +64,7 @@ def lib():
         L.ts5o_attention.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                                      _f32p]
         L.ts5o_swiglu.argtypes = [_f32p, _f32p, C.c_int64]
+        L.ts5o_geglu.argtypes = [_f32p, _f32p, C.c_int64]
         L.ts5o_sampler_new.restype = C.c_void_p
         L.ts5o_sampler_new.argtypes = [C.c_uint64]
         L.ts5o_sampler_free.argtypes = [C.c_void_p]
@@ -139,6 +142,12 @@ def swiglu(g, u):
     return g
 
 
+def geglu(g, u):
+    g = np.array(g, np.float32)
+    lib().ts5o_geglu(g, np.ascontiguousarray(u, np.float32), g.size)
+    return g
+
+
 class Sampler:
     def __init__(self, seed: int):
         self.h = lib().ts5o_sampler_new(seed)
@@ -160,13 +169,24 @@ class Sampler:
 # --- whole model ------------------------------------------------------------------
 
 def hparams(hp: dict) -> HParams:
-    return HParams(n_vocab=hp["n_vocab"], n_embd=hp["n_embd"], n_layer=hp["n_layer"], n_ff=hp["n_ff"],
-                   n_head=hp["n_head"], n_head_kv=hp["n_head_kv"], head_dim=hp["head_dim"],
-                   rope_dims=hp.get("rope_dims", hp["head_dim"]),
-                   rope_neox=int(hp["arch"] in ("qwen2", "qwen3", "gemma3")),
-                   rms_eps=hp["rms_eps"], rope_base=hp["rope_base"],
-                   attn_scale=float(np.float32(1.0) / np.sqrt(np.float32(hp["head_dim"]))),
-                   rope_scale=1.0)
+    """Model::open's derived values (engine/src/model.cpp:36-63) for a synth.py dict."""
+    f32 = np.float32
+    h = HParams(n_vocab=hp["n_vocab"], n_embd=hp["n_embd"], n_layer=hp["n_layer"], n_ff=hp["n_ff"],
+                n_head=hp["n_head"], n_head_kv=hp["n_head_kv"], head_dim=hp["head_dim"],
+                rope_dims=hp.get("rope_dims", hp["head_dim"]),
+                rope_neox=int(hp["arch"] in ("qwen2", "qwen3", "gemma3")),
+                rms_eps=hp["rms_eps"], rope_base=hp["rope_base"],
+                attn_scale=float(f32(1.0) / np.sqrt(f32(hp["head_dim"]))),
+                rope_scale=1.0)
+    if hp["arch"] == "gemma3":
+        h.embd_scale = float(np.sqrt(f32(hp["n_embd"])))
+        h.gelu = 1
+        h.swa_window = hp.get("swa_window", 0)
+        h.swa_pattern = 6
+        h.rope_base_swa = 10000.0
+        if hp["n_layer"] == 62:
+            h.attn_scale = float(f32(1.0) / np.sqrt(f32(hp["n_embd"] // hp["n_head"])))
+    return h
 
 
 class Model:
@@ -191,7 +211,8 @@ class Model:
                               T(p + "attn_v.weight"), T(p + "attn_output.weight"), T(p + "attn_q.bias"),
                               T(p + "attn_k.bias"), T(p + "attn_v.bias"), T(p + "attn_q_norm.weight"),
                               T(p + "attn_k_norm.weight"), T(p + "ffn_norm.weight"), T(p + "ffn_gate.weight"),
-                              T(p + "ffn_up.weight"), T(p + "ffn_down.weight"))
+                              T(p + "ffn_up.weight"), T(p + "ffn_down.weight"), T(p + "post_attention_norm.weight"),
+                              T(p + "post_ffw_norm.weight"))
         self._hp = hparams(hp)
         emb, onorm, out, freqs = T("token_embd.weight"), T("output_norm.weight"), T("output.weight"), \
             T("rope_freqs.weight")

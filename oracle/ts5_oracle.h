@@ -58,6 +58,8 @@ void ts5o_attention(const float *q, const float *kc, const float *vc, int n_head
                     int lo, int pos, float scale, float *out);
 /* g = silu(g) * u, engine/src/cpu_backend.cpp:260-261. */
 void ts5o_swiglu(float *g, const float *u, int64_t n);
+/* g = gelu(g) * u with the tanh form of GELU, engine/src/cpu_backend.cpp:71-73, :258-259. */
+void ts5o_geglu(float *g, const float *u, int64_t n);
 
 /* Engine::sample, engine/src/engine.cpp:16-46, with its own mt19937_64. */
 typedef struct ts5o_sampler ts5o_sampler;
@@ -73,6 +75,11 @@ int32_t ts5o_sample_topk(ts5o_sampler *s, const int32_t *ids, const float *logit
 typedef struct {
     int32_t n_vocab, n_embd, n_layer, n_ff, n_head, n_head_kv, head_dim, rope_dims, rope_neox;
     float rms_eps, rope_base, attn_scale, rope_scale;
+    /* Gemma 3 (engine/src/model.h:28-41; zero for the other families): the embedding's
+     * scale (0: none), the sliding layers' RoPE base, GELU for SiLU, and every layer but
+     * each swa_pattern-th seeing only the last swa_window keys. */
+    float embd_scale, rope_base_swa;
+    int32_t gelu, swa_window, swa_pattern;
 } ts5o_hparams;
 
 typedef struct {
@@ -84,6 +91,7 @@ typedef struct {
 typedef struct {
     ts5o_tensor attn_norm, wq, wk, wv, wo, bq, bk, bv, q_norm, k_norm;
     ts5o_tensor ffn_norm, w_gate, w_up, w_down;
+    ts5o_tensor post_attn_norm, post_ffn_norm; /* Gemma 3; absent elsewhere */
 } ts5o_layer;
 
 typedef struct ts5o_model ts5o_model;

@@ -76,6 +76,8 @@ def model_kv(hp: dict, vocab_pieces: bool = True) -> dict:
         f"{a}.rope.freq_base": float(hp["rope_base"]),
         f"{a}.rope.dimension_count": hp["head_dim"],
     }
+    if hp.get("swa_window"):
+        kv[f"{a}.attention.sliding_window"] = hp["swa_window"]
     if vocab_pieces:
         # Pieces that decode back to "<id>" (no merges, no end-of-generation).
         kv["tokenizer.ggml.model"] = "gpt2"

@@ -125,12 +125,20 @@ def check_schedule(R, path, n, kv, nv):
     return toks, out
 
 
-def golden_models():
+MODELS = {"tiny_llama": synth.TINY_LLAMA, "tiny_draft": synth.TINY_DRAFT, "tiny_llama_c": synth.TINY_LLAMA_C,
+          "tiny_draft_c": synth.TINY_DRAFT_C, "tiny_gemma3": synth.TINY_GEMMA3}
+
+
+def golden_models(names=None):
+    """Each model's check-schedule logits (f32, f16, q8 caches) and 64 greedy
+    ids; `names` regenerates only those (the manifest keeps the others)."""
     R = oracle.ref()
-    manifest = {}
+    mpath = os.path.join(OUT, "models.json")
+    manifest = json.load(open(mpath)) if names and os.path.exists(mpath) else {}
     with tempfile.TemporaryDirectory() as d:
-        for name, hp in (("tiny_llama", synth.TINY_LLAMA), ("tiny_draft", synth.TINY_DRAFT),
-                         ("tiny_llama_c", synth.TINY_LLAMA_C), ("tiny_draft_c", synth.TINY_DRAFT_C)):
+        for name, hp in MODELS.items():
+            if names and name not in names:
+                continue
             path = os.path.join(d, name + ".gguf")
             tensors = write_model(hp, path)
             digests = {k: sha(v[3]) for k, v in tensors.items()}
@@ -157,7 +165,7 @@ def golden_models():
             res["greedy_f16_ids"] = ids16
             np.savez_compressed(os.path.join(OUT, f"model_{name}.npz"), **res)
             manifest[name] = dict(seed=MODEL_SEED, hparams={k: v for k, v in hp.items()}, tensor_sha256=digests)
-    with open(os.path.join(OUT, "models.json"), "w") as f:
+    with open(mpath, "w") as f:
         json.dump(manifest, f, indent=1, sort_keys=True)
 
 
@@ -244,6 +252,11 @@ def main():
     subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "all", "ref"], check=True)
     os.environ.pop("TS5_DRAFT", None)
     os.environ.pop("TS5_ADAPT", None)
+    os.environ.pop("TS5_SWA_WINDOW", None)
+    if len(sys.argv) > 1:  # model fixtures only: make_golden.py tiny_gemma3 ...
+        golden_models(sys.argv[1:])
+        print("model fixtures written:", " ".join(sys.argv[1:]))
+        return
     golden_fp16()
     golden_quants()
     golden_models()

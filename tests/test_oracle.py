@@ -154,6 +154,37 @@ def test_attention_softmax():
         assert np.allclose(got[h * HD:(h + 1) * HD], want, rtol=1e-5, atol=1e-6)
 
 
+def test_attention_window():
+    """lo > 0 (a sliding layer's window): the softmax over keys lo..pos only."""
+    H, HKV, HD, n, lo = 4, 1, 256, 30, 22
+    rng = np.random.default_rng(12)
+    q = rng.standard_normal(H * HD).astype(np.float32)
+    kc = rng.standard_normal((n, HKV * HD)).astype(np.float32)
+    vc = rng.standard_normal((n, HKV * HD)).astype(np.float32)
+    got = oracle.attention(q, kc, vc, H, HKV, HD, n - 1, 0.0625, lo=lo)
+    want = oracle.attention(q, kc[lo:], vc[lo:], H, HKV, HD, n - 1 - lo, 0.0625)
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-7)
+    # A window of one key returns that key's values.
+    one = oracle.attention(q, kc, vc, H, HKV, HD, n - 1, 0.0625, lo=n - 1)
+    assert np.allclose(one, np.tile(vc[n - 1], H), rtol=0, atol=1e-7)
+
+
+def test_geglu_against_erf_gelu():
+    """The tanh form of GELU stays within 1e-3 of x * Phi(x) (its published
+    error is a few 1e-4), is 0 at 0, x for large x and 0 for very negative x."""
+    from scipy.special import erf
+    x = np.linspace(-8, 8, 4001).astype(np.float32)
+    u = np.ones_like(x)
+    got = oracle.geglu(x, u).astype(np.float64)
+    exact = 0.5 * x * (1 + erf(x / np.sqrt(2.0)))
+    assert np.abs(got - exact).max() < 1e-3
+    assert oracle.geglu(np.float32([0.0]), np.float32([3.0]))[0] == 0.0
+    big = oracle.geglu(np.float32([12.0, -12.0]), np.float32([2.0, 2.0]))
+    assert big[0] == 24.0 and abs(big[1]) < 1e-30
+    # The up projection multiplies.
+    assert np.allclose(oracle.geglu(x, 3 * u), 3 * got, rtol=1e-6, atol=1e-7)
+
+
 def _check_model(name):
     hp = dict(json.load(open(os.path.join(G, "models.json")))[name]["hparams"])
     digests = json.load(open(os.path.join(G, "models.json")))[name]["tensor_sha256"]
@@ -173,12 +204,12 @@ def _check_model(name):
     return hp, tensors, g
 
 
-@pytest.mark.parametrize("name", ["tiny_llama", "tiny_draft", "tiny_llama_c", "tiny_draft_c"])
+@pytest.mark.parametrize("name", ["tiny_llama", "tiny_draft", "tiny_llama_c", "tiny_draft_c", "tiny_gemma3"])
 def test_model_logits_match_reference(name):
     _check_model(name)
 
 
-@pytest.mark.parametrize("name", ["tiny_llama_c", "tiny_draft_c"])
+@pytest.mark.parametrize("name", ["tiny_llama_c", "tiny_draft_c", "tiny_gemma3"])
 @pytest.mark.parametrize("kv,key", [(2, "greedy_q8_ids"), (1, "greedy_f16_ids")])
 def test_greedy_decode_matches_reference(name, kv, key):
     hp = dict(json.load(open(os.path.join(G, "models.json")))[name]["hparams"])

@@ -69,7 +69,7 @@ def blocks(t: int, n_blocks: int, rng: np.random.Generator, centered: bool = Fal
     benchmark's distribution has every weight's mean far above zero, which
     makes a random model's output almost independent of its input; the
     centred variant is for parity tests whose argmax should vary with it.
-    dscale (centred only): d = f16(|N(0,1)| * dscale)."""
+    dscale (centred Q4_K only): d = f16(|N(0,1)| * dscale)."""
     bb = BLOCK[t][1]
     out = np.frombuffer(rng.bytes(n_blocks * bb), dtype=np.uint8).reshape(n_blocks, bb).copy()
     if t == Q4_K and centered:
@@ -132,6 +132,26 @@ TINY_DRAFT = dict(arch="qwen2", n_vocab=1000, n_embd=448, n_layer=2, n_ff=768, n
 # The same shapes with centred Q4_K weights (input-dependent argmax).
 TINY_LLAMA_C = dict(TINY_LLAMA, centered=True)
 TINY_DRAFT_C = dict(TINY_DRAFT, centered=True)
+# Gemma 3's layer (engine/src/model.cpp:44-63): head_dim 256 as in its 1B-12B
+# models, per-head q/k norms, norms after attention and the FFN, GELU, a
+# scaled embedding, tied Q6_K head (one small block scale for every row, so
+# that no row outweighs the others and the layers, not the token's own
+# embedding, decide the next token); 7 layers so that layer 5 is global and
+# the others slide, over an 8-key window that short sequences already cross.
+TINY_GEMMA3 = dict(arch="gemma3", n_vocab=1000, n_embd=512, n_layer=7, n_ff=1536, n_head=4, n_head_kv=1,
+                   head_dim=256, rope_base=1000000.0, rms_eps=1e-6, swa_window=8, wtype=Q4_K, head_type=None,
+                   embd_type=Q6_K, centered=True, embd_d=5e-6)
+
+
+def _extra_norms(hp: dict, p: str):
+    """(name, length) of a layer's per-head q/k norms (qwen3, gemma3) and
+    Gemma 3's norms after attention and the FFN (engine/src/model.cpp:108-116)."""
+    if hp["arch"] in ("qwen3", "gemma3"):
+        yield p + "attn_q_norm.weight", hp["head_dim"]
+        yield p + "attn_k_norm.weight", hp["head_dim"]
+    if hp["arch"] == "gemma3":
+        yield p + "post_attention_norm.weight", hp["n_embd"]
+        yield p + "post_ffw_norm.weight", hp["n_embd"]
 
 
 def model_tensors(hp: dict, seed: int):
@@ -146,12 +166,19 @@ def model_tensors(hp: dict, seed: int):
     def mat(name, t, ne0, ne1):
         out[name] = (t, ne0, ne1, tensor(t, ne0, ne1, seed, name, hp.get("centered", False), hp.get("dscale", 0.01)))
 
-    mat("token_embd.weight", hp["embd_type"], E, V)
+    t, ne0, ne1 = hp["embd_type"], E, V
+    emb = tensor(t, ne0, ne1, seed, "token_embd.weight", hp.get("centered", False), hp.get("dscale", 0.01))
+    if hp.get("embd_d") and t == Q6_K:  # one block scale for every row: no row outweighs the rest as a tied head
+        b = emb.reshape(-1, BLOCK[t][1])
+        b[:, 208:210] = _half_bytes(np.full(b.shape[0], hp["embd_d"]))
+    out["token_embd.weight"] = (t, ne0, ne1, emb)
     out["output_norm.weight"] = (F32, E, 1, norm_weight(E, seed, "output_norm.weight"))
     if hp.get("head_type") is not None:
         mat("output.weight", hp["head_type"], E, V)
     for i in range(hp["n_layer"]):
         p = f"blk.{i}."
+        for name, n in _extra_norms(hp, p):
+            out[name] = (F32, n, 1, norm_weight(n, seed, name))
         out[p + "attn_norm.weight"] = (F32, E, 1, norm_weight(E, seed, p + "attn_norm.weight"))
         out[p + "ffn_norm.weight"] = (F32, E, 1, norm_weight(E, seed, p + "ffn_norm.weight"))
         mat(p + "attn_q.weight", wt, E, H * HD)
@@ -175,6 +202,8 @@ def tensor_specs(hp: dict):
         yield "output.weight", hp["head_type"], E, V
     for i in range(hp["n_layer"]):
         p = f"blk.{i}."
+        for name, n in _extra_norms(hp, p):
+            yield name, F32, n, 1
         yield p + "attn_norm.weight", F32, E, 1
         yield p + "ffn_norm.weight", F32, E, 1
         yield p + "attn_q.weight", wt, E, H * HD

@@ -181,10 +181,19 @@ int32_t ts5hip_sampler_draw(ts5hip_sampler *s, const int32_t *ids, const float *
 
 /* ---- model: Backend (engine/src/backend.h:16-44) over HIP ---- */
 
-/* HParams (engine/src/model.h:14-42), the fields the token loop reads. */
+/* HParams (engine/src/model.h:14-42), the fields the token loop reads. The last five are
+ * Gemma 3's (model.h:28-41, set by engine/src/model.cpp:44-63; zero for the other families):
+ * the embedding's scale (0: none), the RoPE base of the sliding layers (which also skip
+ * rope_scale), GELU (tanh form) for SiLU, and every layer l with l % swa_pattern <
+ * swa_pattern - 1 seeing only the last swa_window keys. Layers with post_attention_norm /
+ * post_ffw_norm tensors normalize their attention / FFN output before the residual add.
+ * Every layer keeps a full cache here (the 288 GB of HBM hold the training context of every
+ * Gemma 3 size), so rewind_limit stays unlimited. */
 typedef struct {
     int32_t n_vocab, n_embd, n_layer, n_ff, n_head, n_head_kv, head_dim, rope_dims, rope_neox;
     float rms_eps, rope_base, attn_scale, rope_scale;
+    float embd_scale, rope_base_swa;
+    int32_t gelu, swa_window, swa_pattern;
 } ts5hip_hparams;
 
 /* make_vk_backend (engine/src/backend.h:82) for HIP: a model of these hyperparameters with a

@@ -43,7 +43,7 @@ def test_kv_sizing():
     assert not ts5hip.f16_reaches(7168, 8192) and not ts5hip.f16_reaches(4096, 512)
 
 
-@pytest.mark.parametrize("hp", [synth.TINY_LLAMA, synth.TINY_DRAFT])
+@pytest.mark.parametrize("hp", [synth.TINY_LLAMA, synth.TINY_DRAFT, synth.TINY_GEMMA3])
 def test_gguf_hparams(tmp_path, hp):
     path = str(tmp_path / "m.gguf")
     tensors = synth.model_tensors(hp, 3)
@@ -62,10 +62,15 @@ def test_gguf_errors(tmp_path):
     bad.write_bytes(b"NOPE" + bytes(64))
     with pytest.raises(ts5hip.Ts5HipError):
         ts5hip.gguf_hparams(str(bad))
+    # A gemma3 file without its layers' norms after attention and the FFN (model.cpp:114-116).
     hp = dict(synth.TINY_LLAMA, arch="gemma3")
     path = str(tmp_path / "g.gguf")
     gguf_writer.write(path, gguf_writer.model_kv(hp), synth.model_tensors(synth.TINY_LLAMA, 3))
-    with pytest.raises(ts5hip.Ts5HipError, match="gemma3"):
+    with pytest.raises(ts5hip.Ts5HipError, match="post_attention_norm"):
+        ts5hip.gguf_hparams(path)
+    hp = dict(synth.TINY_LLAMA, arch="mamba")
+    gguf_writer.write(path, gguf_writer.model_kv(hp), synth.model_tensors(synth.TINY_LLAMA, 3))
+    with pytest.raises(ts5hip.Ts5HipError, match="mamba"):
         ts5hip.gguf_hparams(path)
     trunc = str(tmp_path / "t.gguf")
     gguf_writer.write(trunc, gguf_writer.model_kv(synth.TINY_LLAMA), synth.model_tensors(synth.TINY_LLAMA, 3))
@@ -73,6 +78,27 @@ def test_gguf_errors(tmp_path):
         f.truncate(os.path.getsize(trunc) // 2)  # tensors past the end of the file
     with pytest.raises(ts5hip.Ts5HipError):
         ts5hip.gguf_hparams(trunc)
+
+
+def test_gemma3_hparams(tmp_path, monkeypatch):
+    """What the loader adds for gemma3 files (engine/src/model.cpp:44-63):
+    sqrt(n_embd) embedding scale, GELU, a window on five layers of six with
+    RoPE base 10000, the 27B's query scale 1/sqrt(n_embd / n_head) at 62
+    layers, and TS5_SWA_WINDOW replacing the file's window."""
+    hp = dict(synth.TINY_GEMMA3, n_layer=62, swa_window=1024)
+    tensors = {k: v for k, v in synth.model_tensors(dict(synth.TINY_GEMMA3, n_layer=62), 3).items()
+               if "norm" in k or k == "token_embd.weight"}  # hparams need no matrices
+    path = str(tmp_path / "g62.gguf")
+    gguf_writer.write(path, gguf_writer.model_kv(hp), tensors)
+    got, train, _ = ts5hip.gguf_hparams(path)
+    assert got["embd_scale"] == np.float32(np.sqrt(np.float32(512)))
+    assert (got["gelu"], got["swa_window"], got["swa_pattern"], got["rope_base_swa"]) == (1, 1024, 6, 10000.0)
+    assert got["attn_scale"] == np.float32(1) / np.sqrt(np.float32(512 // 4))  # not 1 / sqrt(head_dim 256)
+    assert got["rope_neox"] == 1 and train == 32768
+    monkeypatch.setenv("TS5_SWA_WINDOW", "16")
+    assert ts5hip.gguf_hparams(path)[0]["swa_window"] == 16
+    # Every layer keeps a full cache: K and V of all 62 layers per token.
+    assert ts5hip.kv_bytes_per_token(hp, ts5hip.KV_F16) == 2 * 62 * 1 * 256 * 2
 
 
 def check_model(tmp_path):

@@ -36,6 +36,31 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
     for (int i = threadIdx.x; i < n; i += blockDim.x) yt[i] = xt[i] * s * w[i];
 }
 
+// Gemma 3's norm after attention / the FFN, then the residual add
+// (engine/src/cpu_backend.cpp:250-252, :263-265): x_t += rmsnorm(o_t) * w for
+// token blockIdx.x; rows of at most 256 * PER values held in registers.
+template <int PER>
+__global__ __launch_bounds__(256) void k_norm_add(const float *__restrict__ o, int64_t ostride,
+                                                  const float *__restrict__ w, float eps, int n, float *x,
+                                                  int64_t xstride) {
+    __shared__ float red[4];
+    const float *ot = o + (int64_t)blockIdx.x * ostride;
+    float *xt = x + (int64_t)blockIdx.x * xstride;
+    float v[PER], ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int i = threadIdx.x + 256 * k;
+        v[k] = i < n ? ot[i] : 0.f;
+        ss += v[k] * v[k];
+    }
+    const float sc = 1.0f / sqrtf(block_sum256(ss, red) / (float)n + eps);
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < n) xt[i] += v[k] * sc * w[i];
+    }
+}
+
 // Act of x (optionally rms-normalised by w first): token blockIdx.x, 16-runs
 // 256*blockIdx.y .. +255 (one per thread; the norm's sum over the whole row
 // is taken by every slice).
@@ -278,6 +303,15 @@ hipError_t launch_gemm_act(uint32_t t, const float *x, int64_t xstride, const fl
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int ntok, float *y, hipStream_t s) {
     if (n <= 256 * 16) hipLaunchKernelGGL(k_rmsnorm_reg<16>, dim3(ntok), dim3(256), 0, s, x, w, eps, n, y);
     else hipLaunchKernelGGL(k_rmsnorm, dim3(ntok), dim3(256), 0, s, x, w, eps, n, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_norm_add(const float *o, int64_t ostride, const float *w, float eps, int n, int ntok, float *x,
+                           int64_t xstride, hipStream_t s) {
+    if (n <= 256 * 8) hipLaunchKernelGGL(k_norm_add<8>, dim3(ntok), dim3(256), 0, s, o, ostride, w, eps, n, x, xstride);
+    else if (n <= 256 * 16) hipLaunchKernelGGL(k_norm_add<16>, dim3(ntok), dim3(256), 0, s, o, ostride, w, eps, n, x, xstride);
+    else if (n <= 256 * 32) hipLaunchKernelGGL(k_norm_add<32>, dim3(ntok), dim3(256), 0, s, o, ostride, w, eps, n, x, xstride);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

@@ -31,7 +31,8 @@ namespace ts5hip {
 
 __device__ inline float block_sum64(float v) { return wave_sum(v); }
 
-// grid (H + 2*HKV, ntok), 64 threads (one wave): thread i holds values 2i, 2i+1.
+// grid (H + 2*HKV, ntok), 64 threads (one wave): thread i holds values 2i, 2i+1
+// (and 2i + 128, 2i + 129 at head dimension 256).
 __global__ __launch_bounds__(64) void k_rope_kv(const float *__restrict__ qkv, int64_t qkv_stride,
                                                 const float *__restrict__ bias, const float *__restrict__ q_norm,
                                                 const float *__restrict__ k_norm, float eps,
@@ -56,9 +57,9 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float *__restrict__ qkv, i
         __syncthreads();
     }
     if (is_q || is_k) {
-        if (i < n_rot / 2) {
-            const int a = neox ? i : 2 * i, b = neox ? i + n_rot / 2 : 2 * i + 1;
-            const float2 cs = rope_cs[(int64_t)pos * (n_rot / 2) + i];
+        for (int r = i; r < n_rot / 2; r += 64) {
+            const int a = neox ? r : 2 * r, b = neox ? r + n_rot / 2 : 2 * r + 1;
+            const float2 cs = rope_cs[(int64_t)pos * (n_rot / 2) + r];
             float x0 = v[a], x1 = v[b];
             rope_pair(x0, x1, cs.x, cs.y);
             v[a] = x0;
@@ -75,16 +76,16 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float *__restrict__ qkv, i
     if (kv_f16) {  // f16: each value to the nearest half (engine/src/cpu_backend.cpp:80)
         uint16_t *c16 = (uint16_t *)(is_k ? kv.k : kv.v);
         const int64_t slot = (int64_t)kvh * n_ctx + pos;
-        if (2 * i < HD)
-            *(uint32_t *)(c16 + slot * HD + 2 * i) = (uint32_t)f2h(v[2 * i]) | (uint32_t)f2h(v[2 * i + 1]) << 16;
+        for (int d = 2 * i; d < HD; d += 128)
+            *(uint32_t *)(c16 + slot * HD + d) = (uint32_t)f2h(v[d]) | (uint32_t)f2h(v[d + 1]) << 16;
         return;
     }
     // q8: per 32 values sc = f16(amax / 127), q = clamp(rint(v / sc), +-127).
     int8_t *q8 = is_k ? kv.k : kv.v;
     uint16_t *sc8 = is_k ? kv.ks : kv.vs;
     const int64_t slot = (int64_t)kvh * n_ctx + pos;
-    if (2 * i < HD) {
-        float a0 = v[2 * i], a1 = v[2 * i + 1];
+    for (int d = 2 * i; d < HD; d += 128) {
+        float a0 = v[d], a1 = v[d + 1];
         float amax = fmaxf(fabsf(a0), fabsf(a1));
 #pragma unroll
         for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
@@ -96,8 +97,8 @@ __global__ __launch_bounds__(64) void k_rope_kv(const float *__restrict__ qkv, i
             q1 = (int)fminf(127.f, fmaxf(-127.f, rintf(a1 / sc)));
         }
         uint16_t packed = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
-        *(uint16_t *)(q8 + slot * HD + 2 * i) = packed;
-        if ((i & 15) == 0) sc8[slot * (HD / 32) + (2 * i) / 32] = sh;
+        *(uint16_t *)(q8 + slot * HD + d) = packed;
+        if ((i & 15) == 0) sc8[slot * (HD / 32) + d / 32] = sh;
     }
 }
 
@@ -180,15 +181,16 @@ __global__ void k_kv_read(KvLayer kv, int which, int HKV, int HD, int n_ctx, int
 // (position, KV head), two values a lane.
 __global__ __launch_bounds__(64) void k_kv_write(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0,
                                                  int kv_f16, const float *__restrict__ in) {
-    const int p = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
-    if (2 * i >= HD) return;
+    const int p = blockIdx.x, h = blockIdx.y;
     const float *src = in + ((int64_t)p * HKV + h) * HD;
     const int64_t slot = (int64_t)h * n_ctx + pos0 + p;
+    for (int d = 2 * (int)threadIdx.x; d < HD; d += 128) {  // values d, d + 1 a lane
+    const int i = d / 2;
     const float a0 = src[2 * i], a1 = src[2 * i + 1];
     if (kv_f16) {
         *(uint32_t *)((uint16_t *)(which ? kv.v : kv.k) + slot * HD + 2 * i) =
             (uint32_t)f2h(a0) | (uint32_t)f2h(a1) << 16;
-        return;
+        continue;
     }
     float amax = fmaxf(fabsf(a0), fabsf(a1));
 #pragma unroll
@@ -202,6 +204,7 @@ __global__ __launch_bounds__(64) void k_kv_write(KvLayer kv, int which, int HKV,
     }
     *(uint16_t *)((which ? kv.v : kv.k) + slot * HD + 2 * i) = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
     if ((i & 15) == 0) (which ? kv.vs : kv.ks)[slot * (HD / 32) + i / 16] = sh;
+    }
 }
 
 hipError_t launch_kv_write(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, int kv_f16,
@@ -266,6 +269,21 @@ template <int HD, bool F16>
 static hipError_t attn_launch(int G, dim3 grid, const AttnArgs &a, hipStream_t s) {
     const int flags = (a.kv_per_batch ? 1 : 0) | (a.append ? 2 : 0) | (a.rope ? 4 : 0);
     const bool lds = grid.z == 1 && a.n_ctx <= LDS_MAX_CTX;
+    if constexpr (HD == 256) {  // Gemma 3's heads (G 1, 2 or 4): the per-wave kernel
+        auto go = [&](auto gc) {
+            constexpr int GG = decltype(gc)::value;
+            hipLaunchKernelGGL((k_attn<256, GG, F16>), grid, dim3(ATTN_NT), 0, s, (const int8_t *)a.kv.k,
+                               (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs, a.n_keys,
+                               a.n_ctx, a.HKV, flags, (int)grid.x, a);
+        };
+        switch (G) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        case 4: go(std::integral_constant<int, 4>{}); break;
+        default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    } else {
 #define TS5_ATTN(GG)                                                                                          \
     case GG:                                                                                                  \
         if (lds)                                                                                              \
@@ -288,6 +306,7 @@ static hipError_t attn_launch(int G, dim3 grid, const AttnArgs &a, hipStream_t s
     }
 #undef TS5_ATTN
     return hipGetLastError();
+    }
 }
 
 bool attn_mq_fits(int B, int H, int HKV, int HD, int kv_f16, int kv_per_batch) {
@@ -298,6 +317,7 @@ bool attn_mq_fits(int B, int H, int HKV, int HD, int kv_f16, int kv_per_batch) {
 bool attn_supported(int H, int HKV, int HD) {
     if (HKV <= 0 || H % HKV) return false;
     const int G = H / HKV;
+    if (HD == 256) return G == 1 || G == 2 || G == 4;
     return (HD == 64 || HD == 128) && (G == 1 || G == 2 || G == 4 || G == 5 || G == 7 || G == 8);
 }
 
@@ -310,9 +330,10 @@ hipError_t launch_attn(const AttnIO &io, hipStream_t s) {
     a.rope = io.rope, a.append = io.append, a.kv = io.kv, a.kv_per_batch = io.kv_per_batch, a.n_ctx = io.n_ctx;
     a.H = io.H, a.HKV = io.HKV, a.n_keys = io.n_keys, a.scale = io.scale, a.part = io.part;
     a.counters = io.counters, a.out = io.out;
-    a.act_out = (uint8_t *)io.act_out, a.act_stride = io.act_stride;
+    a.act_out = (uint8_t *)io.act_out, a.act_stride = io.act_stride, a.win = io.win;
+    if (!attn_supported(io.H, io.HKV, io.HD)) return hipErrorInvalidValue;
     const int G = io.H / io.HKV;
-    if (attn_mq_fits(io.B, io.H, io.HKV, io.HD, io.kv_f16, io.kv_per_batch)) {
+    if (!io.win && attn_mq_fits(io.B, io.H, io.HKV, io.HD, io.kv_f16, io.kv_per_batch)) {
         const int flags = (a.append ? 2 : 0) | (a.rope ? 4 : 0);
         hipLaunchKernelGGL(k_attn_mq, dim3(io.n_split, io.HKV), dim3(MQ_NT), 0, s, (const int8_t *)a.kv.k,
                            (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs, a.n_keys,
@@ -322,8 +343,13 @@ hipError_t launch_attn(const AttnIO &io, hipStream_t s) {
         return hipGetLastError();
     }
     const dim3 grid(io.n_split, io.HKV, io.B);
-    if (io.kv_f16) return io.HD == 128 ? attn_launch<128, true>(G, grid, a, s) : attn_launch<64, true>(G, grid, a, s);
-    return io.HD == 128 ? attn_launch<128, false>(G, grid, a, s) : attn_launch<64, false>(G, grid, a, s);
+    if (io.kv_f16)
+        return io.HD == 256   ? attn_launch<256, true>(G, grid, a, s)
+               : io.HD == 128 ? attn_launch<128, true>(G, grid, a, s)
+                              : attn_launch<64, true>(G, grid, a, s);
+    return io.HD == 256   ? attn_launch<256, false>(G, grid, a, s)
+           : io.HD == 128 ? attn_launch<128, false>(G, grid, a, s)
+                          : attn_launch<64, false>(G, grid, a, s);
 }
 
 }  // namespace ts5hip

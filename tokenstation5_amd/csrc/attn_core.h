@@ -57,13 +57,15 @@ struct AttnArgs {
     float *out;     // [B][H * HD]
     uint8_t *act_out;    // or null: the output also as matmul activation records (multi-query kernel)
     int64_t act_stride;  // bytes between tokens' records
+    int win;             // > 0: a query sees only its last win keys (a sliding layer)
 };
 
 constexpr int ATTN_MAX_SPLIT = 64;
 constexpr int ATTN_TILE = 64;
 
-// Where work item (split, kvh, b) of n_split reads keys: [p0, p1) of the nk
-// keys [0, nk) of query b (at position pq = nk - 1), in 64-key tiles.
+// Where work item (split, kvh, b) of n_split reads keys: [p0, p1) of the
+// keys [lo, nk) of query b (at position pq = nk - 1; lo = 0, or nk - win for a
+// sliding window of win keys), in 64-key tiles.
 struct AttnSpan {
     int pq, p0, p1;
     int used;           // splits that hold keys: the others (later ones) are empty
@@ -76,14 +78,15 @@ __device__ inline AttnSpan attn_span(const AttnArgs &a, int split, int kvh, int 
     AttnSpan sp;
     const int nk = a.kv_per_batch ? a.n_keys[b] : a.n_keys[0] + b + 1;
     sp.pq = nk - 1;
+    const int lo = a.win > 0 ? max(0, nk - a.win) : 0, nw = nk - lo;
     // At least ATTN_MIN_KEYS keys a split: a short cache (or a small model's
     // few KV heads) leaves the later splits empty rather than merging many
     // slivers; an empty split's work item returns at once, and the merge
     // counts and reads the `used` ones only.
-    int chunk = max((nk + n_split - 1) / n_split, ATTN_MIN_KEYS);
+    int chunk = max((nw + n_split - 1) / n_split, ATTN_MIN_KEYS);
     chunk = (chunk + TILE - 1) / TILE * TILE;
-    sp.used = (nk + chunk - 1) / chunk;
-    sp.p0 = split * chunk;
+    sp.used = (nw + chunk - 1) / chunk;
+    sp.p0 = lo + split * chunk;
     sp.p1 = min(nk, sp.p0 + chunk);
     const int seq = a.kv_per_batch ? b : 0;
     sp.head_base = ((int64_t)seq * a.HKV + kvh) * a.n_ctx;
@@ -239,10 +242,12 @@ __device__ inline void attn_prepare(const AttnArgs &a, int kvh, int b, const Att
     // Rounded as the cache keeps them, a wave per (key, K or V), a pair of
     // values a lane; query b's own token (pq) also stored at its slot.
     for (int pr = wave; pr < 2 * nn; pr += NWV) {
-        const int kk = pr >> 1, which = pr & 1, i = lane, key = sp.n_lo + kk;
+        const int kk = pr >> 1, which = pr & 1, key = sp.n_lo + kk;
         const bool own = key == pq;
         const int64_t slot = sp.head_base + key;
-        if (2 * i >= HD) continue;
+        // Values d, d + 1 a lane: d = 2 lane (+ 128 past head dimension 128).
+        for (int d = 2 * lane; d < HD; d += 128) {
+        const int i = d / 2;
         if constexpr (F16) {  // engine/src/cpu_backend.cpp:80: each value to the nearest f16
             const uint32_t pair = (uint32_t)f2h(kv_s[kk][which][2 * i]) | (uint32_t)f2h(kv_s[kk][which][2 * i + 1]) << 16;
             *(uint32_t *)(S.new16[kk][which] + 2 * i) = pair;
@@ -268,6 +273,7 @@ __device__ inline void attn_prepare(const AttnArgs &a, int kvh, int b, const Att
                 S.new_sc[kk][which][i / 16] = sh;
                 if (own) (which ? a.kv.vs : a.kv.ks)[slot * (HD / 32) + i / 16] = sh;
             }
+        }
         }
     }
     __syncthreads();
@@ -295,7 +301,7 @@ __device__ inline void attn_prepare(const AttnArgs &a, int kvh, int b, const Att
 // ---------------------------------------------------------------------------
 template <int HD, int G>
 struct SliceShape {
-    static constexpr int DPL = (HD == 128 && G <= 4) ? 16 : 8;  // dims a lane
+    static constexpr int DPL = (HD == 256 || (HD == 128 && G <= 4)) ? 16 : 8;  // dims a lane
     static constexpr int LPK = HD / DPL;                         // lanes a key: 8 or 16
     static constexpr int KPS = 64 / LPK;                         // keys a sweep: 8 or 4
     static constexpr int S = 16 / KPS;                           // sweeps a chunk (16 keys)

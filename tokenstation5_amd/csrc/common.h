@@ -215,6 +215,13 @@ __device__ inline int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(
 // this way are also laid out so that no 128-byte line holds data of two
 // different hand-offs. None of this needs buffer_wbl2 / buffer_inv, which
 // __threadfence() would emit.
+// The gated unit's value: act(g) * u with SiLU (engine/src/cpu_backend.cpp:260-261), or with
+// gelu the tanh form of GELU (Gemma 3, cpu_backend.cpp:71-73, :258-259).
+__device__ inline float glu_act(float g, float u, int gelu) {
+    if (gelu) return 0.5f * g * (1.0f + tanhf(0.7978845608f * (g + 0.044715f * g * g * g))) * u;
+    return g / (1.0f + expf(-g)) * u;
+}
+
 __device__ inline void st_dev(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ inline void st_dev(int *p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ inline float ld_dev(const float *p) {

@@ -63,6 +63,7 @@ struct GemmArgs {
     // records (mact_bytes(nrows) per token), row tiles then taken in pairs
     // (a 32-row chunk a workgroup; nrows a multiple of 256). Null: none.
     uint8_t *qout;
+    int gelu;  // G_GLU: GELU (tanh form) for SiLU
 };
 
 enum { G_STORE = 0, G_ADD = 1, G_GLU = 2 };
@@ -263,7 +264,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
                 const int64_t o = (int64_t)tok * a.ldy + r;
                 const float v = acc[0][g][i];
                 if (MODE == G_ADD) a.out[o] = a.y_in[o] + v;
-                else if (MODE == G_GLU) a.out[o] = v / (1.0f + expf(-v)) * acc[NW - 1][g][i];  // cpu_backend.cpp:260-261
+                else if (MODE == G_GLU) a.out[o] = glu_act(v, acc[NW - 1][g][i], a.gelu);
                 else a.out[o] = v;
             }
         }
@@ -522,7 +523,7 @@ __global__ __launch_bounds__(256) void k_gemm_small(GemmArgs a) {
         const int64_t o = (int64_t)tok * a.ldy + r;
         const float v = acc[0][i];
         if (MODE == G_ADD) a.out[o] = a.y_in[o] + v;
-        else if (MODE == G_GLU) a.out[o] = v / (1.0f + expf(-v)) * acc[NW - 1][i];  // cpu_backend.cpp:260-261
+        else if (MODE == G_GLU) a.out[o] = glu_act(v, acc[NW - 1][i], a.gelu);
         else a.out[o] = v;
     }
 }
@@ -961,7 +962,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_m(GemmArgs a) {
             const int64_t o = (int64_t)tok * a.ldy + row;
             const float v = acc[r][0][tt];
             if (MODE == G_ADD) a.out[o] = a.y_in[o] + v;
-            else if (MODE == G_GLU) a.out[o] = v / (1.0f + expf(-v)) * acc[r][NW - 1][tt];  // cpu_backend.cpp:260-261
+            else if (MODE == G_GLU) a.out[o] = glu_act(v, acc[r][NW - 1][tt], a.gelu);
             else a.out[o] = v;
         }
     }
@@ -1180,7 +1181,7 @@ __global__ __launch_bounds__(64 * GX_WAVES) void k_gemm_mx(GemmArgs a) {
             const int64_t o = (int64_t)tok * a.ldy + row;
             float y;
             if (MODE == G_ADD) y = a.y_in[o] + v[0];
-            else if (MODE == G_GLU) y = v[0] / (1.0f + expf(-v[0])) * v[NW - 1];  // cpu_backend.cpp:260-261
+            else if (MODE == G_GLU) y = glu_act(v[0], v[NW - 1], a.gelu);
             else y = v[0];
             a.out[o] = y;
             if (a.qout) ys[(tok * RT + r) * 16 + (ln & 15)] = y;
@@ -1450,6 +1451,8 @@ hipError_t launch_gemm_fused(const void *w, const void *w2, int64_t ne0, int64_t
     if (!gemm_fused_fits(T_Q4_K, ne0, M)) return hipErrorInvalidValue;
     if (qout && !gemm_fused_qout_fits(ne0, ne1, M)) return hipErrorInvalidValue;
     GemmArgs a{};
+    a.gelu = (mode & GLU_GELU) ? 1 : 0;
+    mode &= ~GLU_GELU;
     a.t = T_Q4_K, a.w = (const uint8_t *)w, a.w2 = (const uint8_t *)w2, a.nrows = (int)ne1;
     a.nb = (int)(ne0 / 256), a.n_in = (int)ne0, a.M = M, a.ks = 1, a.out = y, a.y_in = y_in, a.ldy = ldy;
     a.xin = x, a.xin_stride = xstride, a.norm_w = norm_w, a.eps = eps, a.qout = (uint8_t *)qout;
@@ -1510,13 +1513,13 @@ static hipError_t launch_gemm_m(const GemmArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Split-K: y[t][r] = (y_in +) sum over splits in order (GLU: silu(g) * u).
+// Split-K: y[t][r] = (y_in +) sum over splits in order (GLU: act(g) * u).
 // Four consecutive values a thread (rows of one token when nrows % 4 == 0,
 // else one value at a time), every split's partial requested before the
 // first is added; the sums run in split order.
 template <int MODE>
 __device__ inline void gemm_reduce_one(const float *__restrict__ part, int ks, int64_t n, int nrows, int64_t e,
-                                       float *y, const float *y_in, int64_t ldy) {
+                                       float *y, const float *y_in, int64_t ldy, int gelu) {
     float g = 0.f, u = 0.f;
     for (int k = 0; k < ks; k++) {
         g += part[(int64_t)k * 2 * n + e];
@@ -1525,18 +1528,18 @@ __device__ inline void gemm_reduce_one(const float *__restrict__ part, int ks, i
     const int tok = (int)(e / nrows), r = (int)(e % nrows);
     const int64_t o = (int64_t)tok * ldy + r;
     if (MODE == G_ADD) y[o] = y_in[o] + g;
-    else if (MODE == G_GLU) y[o] = g / (1.0f + expf(-g)) * u;
+    else if (MODE == G_GLU) y[o] = glu_act(g, u, gelu);
     else y[o] = g;
 }
 
 template <int MODE>
 __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ part, int ks, int M, int nrows, float *y,
-                                                     const float *y_in, int64_t ldy) {
+                                                     const float *y_in, int64_t ldy, int gelu) {
     const int64_t n = (int64_t)M * nrows;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     if (nrows % 4) {
         for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += stride)
-            gemm_reduce_one<MODE>(part, ks, n, nrows, e, y, y_in, ldy);
+            gemm_reduce_one<MODE>(part, ks, n, nrows, e, y, y_in, ldy, gelu);
         return;
     }
     constexpr int KC = 8;  // splits requested at once
@@ -1565,19 +1568,19 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float *__restrict__ p
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             if (MODE == G_ADD) o[j] = y_in[(int64_t)tok * ldy + r + j] + gv[j];
-            else if (MODE == G_GLU) o[j] = gv[j] / (1.0f + expf(-gv[j])) * uv[j];  // cpu_backend.cpp:260-261
+            else if (MODE == G_GLU) o[j] = glu_act(gv[j], uv[j], gelu);
             else o[j] = gv[j];
         }
     }
 }
 
 static hipError_t launch_gemm_reduce(const float *part, int ks, int M, int nrows, int mode, float *y, const float *y_in,
-                                     int64_t ldy, hipStream_t s) {
+                                     int64_t ldy, int gelu, hipStream_t s) {
     const int64_t n = (int64_t)M * nrows, per = nrows % 4 ? 1 : 4;
     const dim3 g((unsigned)std::min<int64_t>(4096, (n / per + 255) / 256)), b(256);
-    if (mode == G_ADD) hipLaunchKernelGGL(k_gemm_reduce<G_ADD>, g, b, 0, s, part, ks, M, nrows, y, y_in, ldy);
-    else if (mode == G_GLU) hipLaunchKernelGGL(k_gemm_reduce<G_GLU>, g, b, 0, s, part, ks, M, nrows, y, y_in, ldy);
-    else hipLaunchKernelGGL(k_gemm_reduce<G_STORE>, g, b, 0, s, part, ks, M, nrows, y, y_in, ldy);
+    if (mode == G_ADD) hipLaunchKernelGGL(k_gemm_reduce<G_ADD>, g, b, 0, s, part, ks, M, nrows, y, y_in, ldy, 0);
+    else if (mode == G_GLU) hipLaunchKernelGGL(k_gemm_reduce<G_GLU>, g, b, 0, s, part, ks, M, nrows, y, y_in, ldy, gelu);
+    else hipLaunchKernelGGL(k_gemm_reduce<G_STORE>, g, b, 0, s, part, ks, M, nrows, y, y_in, ldy, 0);
     return hipGetLastError();
 }
 
@@ -1667,14 +1670,17 @@ size_t gemm_scratch_bytes(int64_t rows, int M, int nb) {  // the bound for every
 
 hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, int64_t ne1, const void *act, int M,
                        int mode, float *y, const float *y_in, int64_t ldy, void *scratch, hipStream_t s) {
+    const int gelu = (mode & GLU_GELU) ? 1 : 0;
+    mode &= ~GLU_GELU;
     GemmArgs a{};
+    a.gelu = gelu;
     a.t = t, a.w = (const uint8_t *)w, a.w2 = (const uint8_t *)w2, a.nrows = (int)ne1;
     a.nb = (int)(ne0 / block_values(t)), a.n_in = (int)ne0, a.M = M, a.act = (const uint8_t *)act;
     if (gemm_act_form(t, ne0, M) == GA_HACT) {
         const int ks = wide_splits(ne1, M, (int)(ne0 / 256), g_gemm_cu, mode);
-        hipError_t e = launch_gemm_wide(w, w2, ne0, ne1, act, M, mode, y, y_in, ldy, scratch, ks, s);
+        hipError_t e = launch_gemm_wide(w, w2, ne0, ne1, act, M, mode | (gelu ? GLU_GELU : 0), y, y_in, ldy, scratch, ks, s);
         if (e != hipSuccess || ks == 1) return e;
-        return launch_gemm_reduce((const float *)scratch, ks, M, (int)ne1, mode, y, y_in, ldy, s);
+        return launch_gemm_reduce((const float *)scratch, ks, M, (int)ne1, mode, y, y_in, ldy, gelu, s);
     }
     a.act_stride = (int64_t)gemm_act_bytes(t, ne0, M), a.y_in = y_in, a.ldy = ldy;
     if (split_layout(t)) {  // Q8SM: (scale, min) pairs behind the quants, read as float2
@@ -1690,7 +1696,7 @@ hipError_t launch_gemm(uint32_t t, const void *w, const void *w2, int64_t ne0, i
                    : mode == G_GLU ? gemm_fmt<G_GLU>(a, grid, tn, s)
                                    : gemm_fmt<G_STORE>(a, grid, tn, s);
     if (e != hipSuccess || a.ks == 1) return e;
-    return launch_gemm_reduce((const float *)scratch, a.ks, M, (int)ne1, mode, y, y_in, ldy, s);
+    return launch_gemm_reduce((const float *)scratch, a.ks, M, (int)ne1, mode, y, y_in, ldy, gelu, s);
 }
 
 }  // namespace ts5hip

@@ -55,6 +55,7 @@ struct WideArgs {
     const float *y_in;      // W_ADD: residual [M][ldy] (may be out)
     int64_t ldy;
     int nrows, nb, n_in, M, ks;
+    int gelu;  // W_GLU: GELU (tanh form) for SiLU
 };
 
 enum { W_STORE = 0, W_ADD = 1, W_GLU = 2 };
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_wide(WideArgs a) {
                 } else {
                     const int64_t o2 = (int64_t)tok * a.ldy + r;
                     if (MODE == W_ADD) a.out[o2] = a.y_in[o2] + v;
-                    else if (MODE == W_GLU) a.out[o2] = v / (1.0f + expf(-v)) * (R.acc[1][g][i] * us);  // cpu_backend.cpp:260-261
+                    else if (MODE == W_GLU) a.out[o2] = glu_act(v, R.acc[1][g][i] * us, a.gelu);
                     else a.out[o2] = v;
                 }
             }
@@ -278,6 +279,8 @@ int wide_splits(int64_t rows, int M, int nb, int cus, int mode) {
 hipError_t launch_gemm_wide(const void *w, const void *w2, int64_t ne0, int64_t ne1, const void *act, int M, int mode,
                             float *y, const float *y_in, int64_t ldy, void *scratch, int ks, hipStream_t s) {
     WideArgs a{};
+    a.gelu = (mode & GLU_GELU) ? 1 : 0;
+    mode &= ~GLU_GELU;
     a.w = (const uint8_t *)w, a.w2 = (const uint8_t *)w2, a.act = (const uint8_t *)act;
     a.act_stride = (int64_t)hact_bytes(ne0), a.y_in = y_in, a.ldy = ldy;
     a.nrows = (int)ne1, a.nb = (int)(ne0 / 256), a.n_in = (int)ne0, a.M = M, a.ks = ks;

@@ -22,6 +22,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -213,9 +214,8 @@ bool parse(const char *path, GgufFile &g, std::string &err) {
 // Hyperparameters as engine/src/model.cpp:13-68 derives them.
 bool hparams_of(const GgufFile &g, ts5hip_hparams &hp, int &n_ctx_train, std::string &err) {
     const std::string arch = g.str("general.architecture");
-    if (arch != "llama" && arch != "mistral" && arch != "qwen2" && arch != "qwen3") {
-        err = arch == "gemma3" ? "gemma3 (sliding windows, GELU) is not supported by this backend"
-                               : "architecture '" + arch + "' is not supported";
+    if (arch != "llama" && arch != "mistral" && arch != "qwen2" && arch != "qwen3" && arch != "gemma3") {
+        err = "architecture '" + arch + "' is not supported";
         return false;
     }
     const std::string a = arch + ".";
@@ -236,13 +236,40 @@ bool hparams_of(const GgufFile &g, ts5hip_hparams &hp, int &n_ctx_train, std::st
     hp.rms_eps = (float)g.real(a + "attention.layer_norm_rms_epsilon", 1e-6);
     hp.rope_base = (float)g.real(a + "rope.freq_base", 10000.0);
     hp.rope_dims = (int)g.num(a + "rope.dimension_count", hp.head_dim);
-    hp.rope_neox = arch == "qwen2" || arch == "qwen3";
+    hp.rope_neox = arch == "qwen2" || arch == "qwen3" || arch == "gemma3";
     hp.rope_scale = 1.0f;
     if (!hp.n_embd || !hp.n_layer || !hp.n_ff || !hp.n_head) {
         err = "missing hyperparameters";
         return false;
     }
     hp.attn_scale = 1.0f / std::sqrt((float)hp.head_dim);
+    if (arch == "gemma3") {
+        // What the file does not say, as llama.cpp and the reference fix it:
+        // a window on five layers of six with RoPE base 10000 there, the
+        // scaled embedding, GELU, and the 27B's (62 layers) query scale.
+        hp.embd_scale = std::sqrt((float)hp.n_embd);
+        hp.gelu = 1;
+        hp.swa_window = (int)g.num(a + "attention.sliding_window", 0);
+        hp.swa_pattern = 6;
+        hp.rope_base_swa = 10000.f;
+        if (scaling == "linear") {
+            const double factor = g.real(a + "rope.scaling.factor", 1.0);
+            if (factor > 0) hp.rope_scale = (float)(1.0 / factor);
+        }
+        if (hp.n_layer == 62) hp.attn_scale = 1.0f / std::sqrt((float)(hp.n_embd / hp.n_head));
+        // Tests: a small window, so that a short check crosses it (TS5_SWA_WINDOW).
+        if (const char *e = std::getenv("TS5_SWA_WINDOW"))
+            if (std::atoi(e) > 0 && hp.swa_window > 0) hp.swa_window = std::atoi(e);
+        // Gemma 3 layers need their norms after attention and the FFN (model.cpp:114-116).
+        for (int l = 0; l < hp.n_layer; l++)
+            for (const char *r : {"post_attention_norm.weight", "post_ffw_norm.weight"}) {
+                const std::string n = "blk." + std::to_string(l) + "." + r;
+                if (!g.find(n)) {
+                    err = "missing tensor " + n;
+                    return false;
+                }
+            }
+    }
     const TensorInfo *emb = g.find("token_embd.weight");
     if (!emb) {
         err = "missing tensor token_embd.weight";

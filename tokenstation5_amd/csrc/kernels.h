@@ -17,8 +17,9 @@ struct KvLayer {
 // quant.hip
 hipError_t launch_dequant(uint32_t t, const void *w, int64_t ne0, int64_t rows, float *y, hipStream_t s);
 // x[t] = row ids[*pos + t] of the embedding (pos null: ids[t]).
+// scale > 0: every value times scale (Gemma 3's embedding scale).
 hipError_t launch_embed(uint32_t t, const void *w, int64_t ne0, int64_t n_rows, const int32_t *ids, const int32_t *pos,
-                        int ntok, float *x, hipStream_t s);
+                        int ntok, float *x, hipStream_t s, float scale = 0.f);
 // Split layouts (Q6_K, Q8_0): nblocks GGUF blocks in HBM -> bodies and f16 scales.
 hipError_t launch_repack(uint32_t t, int64_t nblocks, const void *gguf, void *body, void *scales, hipStream_t s);
 // nrows random-init rows of ne0 values (scales: the split layout's f16 array, else unused).
@@ -29,8 +30,10 @@ hipError_t launch_synth(uint32_t t, int64_t ne0, int64_t nrows, uint64_t seed, i
 
 // gemm.hip: Y[t] = W x_t for M tokens on the matrix cores; act: M records of
 // act_bytes(ne0) (launch_act_quant); mode 0 store, 1 add (y = y_in + ...),
-// 2 GLU (w2 = up: y = silu(W x) * (W2 x)); y [M][ldy]; scratch:
+// 2 GLU (w2 = up: y = silu(W x) * (W2 x)), 2 | GLU_GELU the same with GELU's
+// tanh form for SiLU (Gemma 3); y [M][ldy]; scratch:
 // gemm_scratch_bytes(ne1, M, blocks per row) bytes.
+constexpr int GLU_GELU = 0x10;
 void set_gemm_cu_count(int n);
 // gemm_wide.hip: the Q4_K prompt matmul on hact_* records (launch_gemm picks it).
 int wide_splits(int64_t rows, int M, int nb, int cus, int mode);
@@ -53,6 +56,9 @@ hipError_t launch_gemm_fused(const void *w, const void *w2, int64_t ne0, int64_t
 
 // act.hip
 hipError_t launch_rmsnorm(const float *x, const float *w, float eps, int n, int ntok, float *y, hipStream_t s);
+// x_t += rmsnorm(o_t) * w for ntok tokens (Gemma 3's norms after attention and the FFN); n <= 8192.
+hipError_t launch_norm_add(const float *o, int64_t ostride, const float *w, float eps, int n, int ntok, float *x,
+                           int64_t xstride, hipStream_t s);
 // The activation records launch_gemm reads for type t and ntok tokens
 // (gemm_act_form: Act, the matmul layout mact_* or the fp16 pair form hact_*),
 // gemm_act_bytes(t, n, ntok) per token.
@@ -68,11 +74,12 @@ hipError_t launch_act_quant(const float *x, int64_t xstride, const float *w, flo
 void set_cu_count(int n);
 hipError_t launch_matvec(uint32_t t, const void *w, int64_t ne0, int64_t ne1, const float *x, const float *norm_w,
                          float eps, float *y, int add, hipStream_t s);
-// y = silu(Wg x) * (Wu x).
+// y = silu(Wg x) * (Wu x); with gelu, GELU (tanh form) for SiLU.
 hipError_t launch_matvec_glu(uint32_t t, const void *wg, const void *wu, int64_t ne0, int64_t ne1, const float *x,
-                             const float *norm_w, float eps, float *y, hipStream_t s);
+                             const float *norm_w, float eps, float *y, hipStream_t s, int gelu = 0);
 // ntok tokens (x rows xstride apart, y rows ldy apart) one matvec launch each:
-// mode 0 store, 1 add, 2 gate/up + SiLU (w2 the up rows). F16 / F32 matrices' batches.
+// mode 0 store, 1 add, 2 gate/up + SiLU (w2 the up rows; 2 | GLU_GELU: GELU).
+// F16 / F32 matrices' batches.
 hipError_t launch_matvec_tokens(uint32_t t, const void *w, const void *w2, int64_t ne0, int64_t ne1, const float *x,
                                 int64_t xstride, const float *norm_w, float eps, int ntok, int mode, float *y,
                                 int64_t ldy, hipStream_t s);
@@ -130,6 +137,9 @@ struct AttnIO {
     // token (the next projection then reads them instead of quantizing).
     void *act_out;
     int64_t act_stride;
+    // > 0: a sliding layer's window (Gemma 3): each query sees only its last
+    // `win` keys, its own included (engine/src/cpu_backend.cpp:228-229).
+    int win;
 };
 hipError_t launch_attn(const AttnIO &io, hipStream_t s);
 // Whether launch_attn takes the batch's queries together on the matrix cores

@@ -17,6 +17,7 @@ struct MvTail {
     float *best_v;
     int *best_i, *counter;
     int32_t *out, *seq, *pos;
+    int gelu;
 };
 
 // The arguments every mode needs come first and one by one: 14 dwords the
@@ -33,7 +34,7 @@ __global__ __launch_bounds__(WAVES *WAVE) void k_mv(const void *w, const void *w
     a.eps = eps, a.y = y, a.y_in = tail.y_in;
     a.best_v = tail.best_v, a.best_i = tail.best_i, a.counter = tail.counter, a.out = tail.out, a.seq = tail.seq;
     a.pos = tail.pos;
-    a.nfirst = tail.nfirst, a.n1 = tail.n1;
+    a.nfirst = tail.nfirst, a.n1 = tail.n1, a.gelu = tail.gelu;
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[2 * WAVES];
     __shared__ int last;
@@ -139,7 +140,7 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
         const int64_t want = (int64_t)(MV_FIRST_SHARE * (double)ngroups / nfirst + 0.5) * nfirst;
         n1 = (int)std::min<int64_t>(std::max<int64_t>(want, nfirst), ngroups - ((int64_t)grid - nfirst));
     }
-    const MvTail tail{a.t, a.nb, nfirst, n1, a.y_in, a.best_v, a.best_i, a.counter, a.out, a.seq, a.pos};
+    const MvTail tail{a.t, a.nb, nfirst, n1, a.y_in, a.best_v, a.best_i, a.counter, a.out, a.seq, a.pos, a.gelu};
 #define TS5_MV_LAUNCH(RUNS, NORM)                                                                                 \
     hipLaunchKernelGGL((k_mv<F, R, WAVES, KS, MODE, RUNS, NORM>), g, b, lds, s, a.w, a.w2, a.x, a.norm_w, a.y,        \
                        (int)a.nrows, a.n_in, (int)grid, a.eps, tail)
@@ -225,9 +226,10 @@ hipError_t launch_matvec(uint32_t t, const void *w, int64_t ne0, int64_t ne1, co
 }
 
 hipError_t launch_matvec_glu(uint32_t t, const void *wg, const void *wu, int64_t ne0, int64_t ne1, const float *x,
-                             const float *norm_w, float eps, float *y, hipStream_t s) {
+                             const float *norm_w, float eps, float *y, hipStream_t s, int gelu) {
     MvArgs a = mv_args(t, wg, ne0, ne1, x, norm_w, eps, y);
     a.w2 = wu;
+    a.gelu = gelu ? 1 : 0;
     return mv_dispatch<MV_GLU>(a, s);
 }
 
@@ -239,8 +241,9 @@ hipError_t launch_matvec_tokens(uint32_t t, const void *w, const void *w2, int64
     for (int k = 0; k < ntok; k++) {
         const float *xk = x + (int64_t)k * xstride;
         float *yk = y + (int64_t)k * ldy;
-        const hipError_t e = mode == 2 ? launch_matvec_glu(t, w, w2, ne0, ne1, xk, norm_w, eps, yk, s)
-                                       : launch_matvec(t, w, ne0, ne1, xk, norm_w, eps, yk, mode == 1, s);
+        const int m = mode & ~GLU_GELU;
+        const hipError_t e = m == 2 ? launch_matvec_glu(t, w, w2, ne0, ne1, xk, norm_w, eps, yk, s, mode & GLU_GELU)
+                                    : launch_matvec(t, w, ne0, ne1, xk, norm_w, eps, yk, m == 1, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

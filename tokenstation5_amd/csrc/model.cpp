@@ -39,6 +39,7 @@ struct DevT {
 
 struct LayerDev {
     DevT attn_norm, ffn_norm, q_norm, k_norm;
+    DevT post_attn_norm, post_ffn_norm;  // Gemma 3: norms of the attention / FFN output
     DevT qkv;                    // [q; k; v] rows of one type
     DevT part[3];                // a q/k/v matrix whose type differs from qkv's
     bool in_qkv[3] = {false, false, false};
@@ -65,9 +66,11 @@ struct ts5hip_model {
     int8_t *k8 = nullptr, *v8 = nullptr;
     uint16_t *ks = nullptr, *vs = nullptr;
     float *rope_cs = nullptr;
+    float *rope_cs_swa = nullptr;  // the sliding layers' (rope_base_swa, no position scaling)
     bool rope_ready = false;
     // Activations and scratch.
     float *x = nullptr, *qkv = nullptr, *att = nullptr, *ffn = nullptr, *logits = nullptr, *part = nullptr;
+    float *otmp = nullptr;  // a projection's output before its post-norm (Gemma 3)
     int *counters = nullptr;  // HKV attention merges (CTR_STRIDE apart), then the head argmax's; zero between launches
     void *amax = nullptr;
     int32_t *seq = nullptr;    // [n_ctx + 1] token id at each position
@@ -90,6 +93,7 @@ struct ts5hip_model {
     // chunk's activations [CHUNK][...], its quantized activations, the
     // matmul's split-K partials, attention partials and merge counters.
     float *bx = nullptr, *bqkv = nullptr, *bq = nullptr, *batt = nullptr, *bffn = nullptr, *bpart = nullptr;
+    float *botmp = nullptr;
     void *bact = nullptr, *bgemm = nullptr;
     int *bcounters = nullptr;
     // Profile (TS5_PROFILE or TS5HIP_PROFILE, engine/src/vk_backend.cpp:347-358):
@@ -106,6 +110,14 @@ struct ts5hip_model {
     std::vector<void *> allocs;
 
     int qkv_rows() const { return (hp.n_head + 2 * hp.n_head_kv) * hp.head_dim; }
+    // A sliding layer (engine/src/model.h:41): the last swa_window keys only.
+    bool swa(int l) const {
+        return hp.swa_window > 0 && hp.swa_pattern > 0 && l % hp.swa_pattern < hp.swa_pattern - 1;
+    }
+    int win(int l) const { return swa(l) ? hp.swa_window : 0; }
+    const float *rope_of(int l) const { return swa(l) ? rope_cs_swa : rope_cs; }
+    // GELU for SiLU in the gate/up's mode (Gemma 3).
+    int glu_mode() const { return 2 | (hp.gelu ? GLU_GELU : 0); }
     int64_t kv_head_elems() const { return (int64_t)n_ctx * hp.head_dim; }
     bool kv_f16() const { return kv_type == KV_F16; }
     KvLayer kv_layer(int l) const {
@@ -370,6 +382,8 @@ int set_tensor(ts5hip_model *m, const char *name, uint32_t type, int64_t ne0, in
     if (r == "ffn_norm.weight") return set_vector(m, L.ffn_norm, type, ne0 * ne1, E, src, name);
     if (r == "attn_q_norm.weight") return set_vector(m, L.q_norm, type, ne0 * ne1, HD, src, name);
     if (r == "attn_k_norm.weight") return set_vector(m, L.k_norm, type, ne0 * ne1, HD, src, name);
+    if (r == "post_attention_norm.weight") return set_vector(m, L.post_attn_norm, type, ne0 * ne1, E, src, name);
+    if (r == "post_ffw_norm.weight") return set_vector(m, L.post_ffn_norm, type, ne0 * ne1, E, src, name);
     if (r == "attn_output.weight") return set_matrix(m, L.wo, type, ne0, ne1, H * HD, E, src, name);
     if (r == "ffn_gate.weight") return set_matrix(m, L.gate, type, ne0, ne1, E, F, src, name);
     if (r == "ffn_up.weight") return set_matrix(m, L.up, type, ne0, ne1, E, F, src, name);
@@ -430,12 +444,18 @@ int check_complete(ts5hip_model *m) {
         if (int rc = need(L.up, "ffn_up.weight", l)) return rc;
         if (int rc = need(L.down, "ffn_down.weight", l)) return rc;
         if (L.gate.type != L.up.type) return fail(m->ctx, TS5HIP_ERR_UNSUPPORTED, "gate and up of different types");
+        if (L.post_attn_norm.set != L.post_ffn_norm.set)  // both or neither (cpu_backend.cpp:103)
+            return fail(m->ctx, TS5HIP_ERR_STATE, "blk.%d: post_attention_norm and post_ffw_norm go together", l);
     }
     if (!m->rope_ready) {
+        const float *ff = m->freqs.empty() ? nullptr : m->freqs.data();
         std::vector<float> t;
-        rope_table_host(m->hp.rope_dims, m->n_ctx, m->hp.rope_base, m->hp.rope_scale,
-                        m->freqs.empty() ? nullptr : m->freqs.data(), t);
+        rope_table_host(m->hp.rope_dims, m->n_ctx, m->hp.rope_base, m->hp.rope_scale, ff, t);
         if (int rc = ts5hip_upload(m->ctx, m->rope_cs, t.data(), t.size() * 4)) return rc;
+        if (m->rope_cs_swa) {  // cpu_backend.cpp:208: the sliding layers' base, no scaling
+            rope_table_host(m->hp.rope_dims, m->n_ctx, m->hp.rope_base_swa, 1.0f, ff, t);
+            if (int rc = ts5hip_upload(m->ctx, m->rope_cs_swa, t.data(), t.size() * 4)) return rc;
+        }
         m->rope_ready = true;
     }
     return TS5HIP_OK;
@@ -453,7 +473,8 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
     const int QR = m->qkv_rows();
 #define TS5_STAMP(kernel, role) \
     if (int rc_ = prof_stamp(m, kernel, role)) return rc_
-    TS5_HIP(ctx, launch_embed(m->tok_embd.type, m->tok_embd.d, E, hp.n_vocab, m->seq, m->state, 1, m->x, s));
+    TS5_HIP(ctx, launch_embed(m->tok_embd.type, m->tok_embd.d, E, hp.n_vocab, m->seq, m->state, 1, m->x, s,
+                              hp.embd_scale));
     TS5_STAMP("embed_" + type_tag(m->tok_embd.type), "token_embd");
     for (int l = 0; l < hp.n_layer; l++) {
         const LayerDev &L = m->layers[l];
@@ -486,19 +507,32 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
         io.bias = m->has_bias[l] ? m->bias + (int64_t)l * QR : nullptr;
         io.q_norm = L.q_norm.set ? (const float *)L.q_norm.d : nullptr;
         io.k_norm = L.k_norm.set ? (const float *)L.k_norm.d : nullptr;
-        io.eps = hp.rms_eps, io.rope_cs = m->rope_cs, io.n_rot = hp.rope_dims, io.neox = hp.rope_neox;
+        io.eps = hp.rms_eps, io.rope_cs = m->rope_of(l), io.n_rot = hp.rope_dims, io.neox = hp.rope_neox;
         io.kv = m->kv_layer(l), io.kv_f16 = m->kv_f16(), io.kv_per_batch = 0, io.n_ctx = m->n_ctx;
         io.n_keys = m->state, io.B = 1, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = m->n_split, io.scale = hp.attn_scale;
-        io.part = m->part, io.counters = m->counters, io.out = m->att;
+        io.part = m->part, io.counters = m->counters, io.out = m->att, io.win = m->win(l);
         TS5_HIP(ctx, launch_attn(io, s));
         TS5_STAMP(m->kv_f16() ? "attention_f16" : "attention_q8", "decode");
-        TS5_HIP(ctx, launch_matvec(L.wo.type, L.wo.d, (int64_t)H * HD, E, m->att, nullptr, 0.f, m->x, 1, s));
+        // With Gemma 3's post-norms a projection's output is normalized before
+        // the residual add (cpu_backend.cpp:250-252, :263-265).
+        const bool post = L.post_attn_norm.set;
+        TS5_HIP(ctx, launch_matvec(L.wo.type, L.wo.d, (int64_t)H * HD, E, m->att, nullptr, 0.f, post ? m->otmp : m->x,
+                                   post ? 0 : 1, s));
         TS5_STAMP("matvec_" + type_tag(L.wo.type), "attn_output");
+        if (post) {
+            TS5_HIP(ctx, launch_norm_add(m->otmp, E, (const float *)L.post_attn_norm.d, hp.rms_eps, E, 1, m->x, E, s));
+            TS5_STAMP("norm_add", "post_attention_norm");
+        }
         TS5_HIP(ctx, launch_matvec_glu(L.gate.type, L.gate.d, L.up.d, E, F, m->x, (const float *)L.ffn_norm.d,
-                                       hp.rms_eps, m->ffn, s));
+                                       hp.rms_eps, m->ffn, s, hp.gelu));
         TS5_STAMP("matvec_glu_" + type_tag(L.gate.type), "ffn_gate+up");
-        TS5_HIP(ctx, launch_matvec(L.down.type, L.down.d, F, E, m->ffn, nullptr, 0.f, m->x, 1, s));
+        TS5_HIP(ctx, launch_matvec(L.down.type, L.down.d, F, E, m->ffn, nullptr, 0.f, post ? m->otmp : m->x,
+                                   post ? 0 : 1, s));
         TS5_STAMP("matvec_" + type_tag(L.down.type), "ffn_down");
+        if (post) {
+            TS5_HIP(ctx, launch_norm_add(m->otmp, E, (const float *)L.post_ffn_norm.d, hp.rms_eps, E, 1, m->x, E, s));
+            TS5_STAMP("norm_add", "post_ffw_norm");
+        }
     }
     if (head) {
         const DevT &out = m->output.set ? m->output : m->tok_embd;
@@ -631,7 +665,7 @@ int ensure_batch(ts5hip_model *m) {
     int rc = 0;
     if ((rc = alloc_t(m, CHUNK * E, &m->bx)) || (rc = alloc_t(m, CHUNK * QR, &m->bqkv)) ||
         (rc = alloc_t(m, CHUNK * AH, &m->bq)) || (rc = alloc_t(m, CHUNK * AH, &m->batt)) ||
-        (rc = alloc_t(m, CHUNK * F, &m->bffn)) ||
+        (rc = alloc_t(m, CHUNK * F, &m->bffn)) || (rc = alloc_t(m, CHUNK * E, &m->botmp)) ||
         (rc = alloc(m, CHUNK * std::max({act_bytes(wide), mact_bytes(wide), hact_bytes(wide)}), &m->bact)) ||
         (rc = alloc(m, std::max<size_t>(gemm, 256), &m->bgemm)) || (rc = alloc(m, part, (void **)&m->bpart)) ||
         (rc = alloc_t(m, (size_t)CHUNK * hp.n_head_kv * CTR_STRIDE, &m->bcounters)))
@@ -672,7 +706,8 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
     };
     TS5_HIP(ctx, launch_set_pos(m->state, p0, s));
     TS5_STAMP("set_pos", "");
-    TS5_HIP(ctx, launch_embed(m->tok_embd.type, m->tok_embd.d, E, hp.n_vocab, m->seq, m->state, nc, m->bx, s));
+    TS5_HIP(ctx, launch_embed(m->tok_embd.type, m->tok_embd.d, E, hp.n_vocab, m->seq, m->state, nc, m->bx, s,
+                              hp.embd_scale));
     TS5_STAMP("embed_" + type_tag(m->tok_embd.type), "token_embd");
     for (int l = 0; l < hp.n_layer; l++) {
         const LayerDev &L = m->layers[l];
@@ -705,16 +740,20 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
         // K/V append to the attention's work items; longer chunks round and
         // append first (k_rope_kv) and read the cache.
         const bool fused = nc <= ATTN_MAX_NEW;
+        const int win = m->win(l);  // a sliding layer's window, else 0
+        const bool post = L.post_attn_norm.set;
         // Up to 5 tokens with the multi-query attention: it also writes wo's
         // activation records, and wo runs on them (k_gemm_mw).
-        const bool wo_rec = fused && nc <= 5 && L.wo.type == T_Q4_K && AH % 256 == 0 &&
-                            attn_mq_fits(nc, H, HKV, HD, m->kv_f16(), 0);
+        const bool mq = !win && attn_mq_fits(nc, H, HKV, HD, m->kv_f16(), 0);
+        const bool wo_rec = fused && nc <= 5 && L.wo.type == T_Q4_K && AH % 256 == 0 && mq && !post;
         if (!fused) {
-            TS5_HIP(ctx, launch_rope_kv(m->bqkv, QR, bias, qn, kn, eps, m->rope_cs, hp.rope_dims, hp.rope_neox,
+            TS5_HIP(ctx, launch_rope_kv(m->bqkv, QR, bias, qn, kn, eps, m->rope_of(l), hp.rope_dims, hp.rope_neox,
                                         m->state, H, HKV, HD, m->n_ctx, nc, m->bq, m->kv_layer(l), m->kv_f16(), s));
             TS5_STAMP("rope_kv_append", "");
         }
-        if (nc > 16 && !m->kv_f16() && attn_prefill_supported(H, HKV, HD)) {  // prompt chunks on the matrix cores
+        // Prompt chunks on the matrix cores; a sliding layer's chunk (each
+        // query its own window) on the per-query kernel.
+        if (nc > 16 && !win && !m->kv_f16() && attn_prefill_supported(H, HKV, HD)) {
             TS5_HIP(ctx, launch_attn_prefill(m->bq, AH, m->kv_layer(l), m->n_ctx, H, HKV, HD, p0, nc, hp.attn_scale,
                                              m->bpart, m->batt, s));
             TS5_STAMP("attention_prompt", "");
@@ -722,14 +761,15 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
             AttnIO io{};
             if (fused) {
                 io.q = m->bqkv, io.q_stride = QR, io.rope = 1, io.append = 1;
-                io.bias = bias, io.q_norm = qn, io.k_norm = kn, io.eps = eps, io.rope_cs = m->rope_cs;
+                io.bias = bias, io.q_norm = qn, io.k_norm = kn, io.eps = eps, io.rope_cs = m->rope_of(l);
                 io.n_rot = hp.rope_dims, io.neox = hp.rope_neox;
             } else {
                 io.q = m->bq, io.q_stride = AH, io.rope = 0, io.append = 0;
             }
             io.kv = m->kv_layer(l), io.kv_f16 = m->kv_f16(), io.kv_per_batch = 0, io.n_ctx = m->n_ctx;
-            io.n_keys = m->state, io.B = nc, io.H = H, io.HKV = HKV, io.HD = HD, io.n_split = attn_mq_fits(nc, H, HKV, HD, io.kv_f16, 0) ? attn_mq_splits(HKV, ctx->n_cu) : attn_splits(nc, HKV, ctx->n_cu);
-            io.scale = hp.attn_scale, io.part = m->bpart, io.counters = m->bcounters, io.out = m->batt;
+            io.n_keys = m->state, io.B = nc, io.H = H, io.HKV = HKV, io.HD = HD;
+            io.n_split = mq ? attn_mq_splits(HKV, ctx->n_cu) : attn_splits(nc, HKV, ctx->n_cu);
+            io.scale = hp.attn_scale, io.part = m->bpart, io.counters = m->bcounters, io.out = m->batt, io.win = win;
             // A verify batch's attention also writes wo's activation records.
             if (wo_rec) io.act_out = m->bact, io.act_stride = (int64_t)gemm_act_bytes(L.wo.type, AH, nc);
             TS5_HIP(ctx, launch_attn(io, s));
@@ -738,26 +778,35 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
         if (wo_rec) {
             TS5_HIP(ctx, launch_gemm(L.wo.type, L.wo.d, nullptr, AH, E, m->bact, nc, 1, m->bx, m->bx, E, m->bgemm, s));
             TS5_STAMP("matmul_" + type_tag(L.wo.type), "attn_output");
-        } else if (int rc = proj(L.wo.type, L.wo.d, nullptr, AH, E, m->batt, AH, nullptr, nc, 1, m->bx, E,
-                                 "attn_output")) {
+        } else if (int rc = proj(L.wo.type, L.wo.d, nullptr, AH, E, m->batt, AH, nullptr, nc, post ? 0 : 1,
+                                 post ? m->botmp : m->bx, E, "attn_output")) {
             return rc;
+        }
+        if (post) {  // Gemma 3: x += rmsnorm(wo . att) (cpu_backend.cpp:250-252)
+            TS5_HIP(ctx, launch_norm_add(m->botmp, E, (const float *)L.post_attn_norm.d, eps, E, nc, m->bx, E, s));
+            TS5_STAMP("norm_add", "post_attention_norm");
         }
         // A verify batch's gate/up also writes the down projection's
         // activation records (no separate quantization launch between them).
-        const bool down_rec = L.gate.type == T_Q4_K && L.down.type == T_Q4_K && nc <= 5 &&
+        const bool down_rec = L.gate.type == T_Q4_K && L.down.type == T_Q4_K && nc <= 5 && !post &&
                               gemm_fused_qout_fits(E, F, nc) && !gemm_fused_fits(L.down.type, F, nc);
         if (down_rec) {
-            TS5_HIP(ctx, launch_gemm_fused(L.gate.d, L.up.d, E, F, m->bx, E, (const float *)L.ffn_norm.d, eps, nc, 2,
-                                           m->bffn, m->bffn, F, s, m->bact));
+            TS5_HIP(ctx, launch_gemm_fused(L.gate.d, L.up.d, E, F, m->bx, E, (const float *)L.ffn_norm.d, eps, nc,
+                                           m->glu_mode(), m->bffn, m->bffn, F, s, m->bact));
             TS5_STAMP("matmul_fused_" + type_tag(L.gate.type), "ffn_gate+up");
             TS5_HIP(ctx, launch_gemm(L.down.type, L.down.d, nullptr, F, E, m->bact, nc, 1, m->bx, m->bx, E, m->bgemm, s));
             TS5_STAMP("matmul_" + type_tag(L.down.type), "ffn_down");
         } else {
-            if (int rc = proj(L.gate.type, L.gate.d, L.up.d, E, F, m->bx, E, (const float *)L.ffn_norm.d, nc, 2,
-                              m->bffn, F, "ffn_gate+up"))
+            if (int rc = proj(L.gate.type, L.gate.d, L.up.d, E, F, m->bx, E, (const float *)L.ffn_norm.d, nc,
+                              m->glu_mode(), m->bffn, F, "ffn_gate+up"))
                 return rc;
-            if (int rc = proj(L.down.type, L.down.d, nullptr, F, E, m->bffn, F, nullptr, nc, 1, m->bx, E, "ffn_down"))
+            if (int rc = proj(L.down.type, L.down.d, nullptr, F, E, m->bffn, F, nullptr, nc, post ? 0 : 1,
+                              post ? m->botmp : m->bx, E, "ffn_down"))
                 return rc;
+            if (post) {  // cpu_backend.cpp:263-265
+                TS5_HIP(ctx, launch_norm_add(m->botmp, E, (const float *)L.post_ffn_norm.d, eps, E, nc, m->bx, E, s));
+                TS5_STAMP("norm_add", "post_ffw_norm");
+            }
         }
     }
     if (rows) {
@@ -909,6 +958,8 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
     if ((rc = alloc_t(m, kv_elems * kv_value_bytes, &m->k8)) || (rc = alloc_t(m, kv_elems * kv_value_bytes, &m->v8)) ||
         (kv_scales && ((rc = alloc_t(m, kv_scales, &m->ks)) || (rc = alloc_t(m, kv_scales, &m->vs)))) ||
         (rc = alloc_t(m, (size_t)n_ctx * hp->rope_dims, &m->rope_cs)) ||
+        (hp->swa_window > 0 && (rc = alloc_t(m, (size_t)n_ctx * hp->rope_dims, &m->rope_cs_swa))) ||
+        (rc = alloc_t(m, E, &m->otmp)) ||
         (rc = alloc_t(m, (size_t)hp->n_layer * m->qkv_rows(), &m->bias)) || (rc = alloc_t(m, E, &m->x)) ||
         (rc = alloc_t(m, m->qkv_rows(), &m->qkv)) || (rc = alloc_t(m, H * HD, &m->att)) ||
         (rc = alloc_t(m, F, &m->ffn)) || (rc = alloc_t(m, hp->n_vocab, &m->logits)) ||

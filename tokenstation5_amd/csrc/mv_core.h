@@ -493,6 +493,7 @@ struct MvArgs {
     // (dispatched first, one a CU) take groups [0, n1) in turn and the others
     // [n1, ngroups); else workgroup wg takes wg, wg + nwg, ...
     int nfirst, n1;
+    int gelu;  // MV_GLU: GELU (tanh form) for SiLU
 };
 
 template <class F, int R>
@@ -636,7 +637,7 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
             if (MODE == MV_ADD) {
                 st_dev(a.y + row, a.y_in[row] + v);
             } else if (MODE == MV_GLU) {
-                st_dev(a.y + row, v / (1.0f + expf(-v)) * u);  // engine/src/cpu_backend.cpp:260-261
+                st_dev(a.y + row, glu_act(v, u, a.gelu));
             } else {
                 st_dev(a.y + row, v);
                 if (MODE == MV_ARGMAX && (v > best_v || (v == best_v && row < best_i))) best_v = v, best_i = (int)row;

@@ -24,7 +24,8 @@ __global__ void k_dequant(uint32_t t, const uint8_t *__restrict__ w, int64_t ne0
 // Embedding lookup (engine/src/cpu_backend.cpp:124-134): x[t] = row
 // ids[p0 + t], p0 = *pos (0 when pos is null).
 __global__ void k_embed(uint32_t t, const uint8_t *__restrict__ w, int64_t ne0, int64_t n_rows,
-                        const int32_t *__restrict__ ids, const int32_t *__restrict__ pos, float *__restrict__ x) {
+                        const int32_t *__restrict__ ids, const int32_t *__restrict__ pos, float *__restrict__ x,
+                        float scale) {
     const int bv = block_values(t);
     const int nb = (int)(ne0 / bv);
     int64_t row = ids[(pos ? pos[0] : 0) + (int)blockIdx.x];
@@ -33,7 +34,9 @@ __global__ void k_embed(uint32_t t, const uint8_t *__restrict__ w, int64_t ne0, 
     // One value per thread (grid.y covers the row): every value's loads are
     // independent, so a token costs one memory round trip, not one per value.
     const int64_t i = (int64_t)blockIdx.y * blockDim.x + threadIdx.x;
-    if (i < ne0) out[i] = unpack_value(t, w, (int64_t)nb * n_rows, row, t == T_F32 || t == T_F16 ? (int)ne0 : nb, i);
+    if (i >= ne0) return;
+    const float v = unpack_value(t, w, (int64_t)nb * n_rows, row, t == T_F32 || t == T_F16 ? (int)ne0 : nb, i);
+    out[i] = scale > 0.f ? v * scale : v;  // Gemma 3's sqrt(n_embd) (engine/src/cpu_backend.cpp:132-133)
 }
 
 // ---------------------------------------------------------------------------
@@ -229,9 +232,9 @@ hipError_t launch_dequant(uint32_t t, const void *w, int64_t ne0, int64_t rows, 
 }
 
 hipError_t launch_embed(uint32_t t, const void *w, int64_t ne0, int64_t n_rows, const int32_t *ids, const int32_t *pos,
-                        int ntok, float *x, hipStream_t s) {
+                        int ntok, float *x, hipStream_t s, float scale) {
     hipLaunchKernelGGL(k_embed, dim3(ntok, (unsigned)((ne0 + 255) / 256)), dim3(256), 0, s, t, (const uint8_t *)w, ne0,
-                       n_rows, ids, pos, x);
+                       n_rows, ids, pos, x, scale);
     return hipGetLastError();
 }
 

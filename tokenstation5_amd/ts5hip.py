@@ -26,7 +26,9 @@ _vp, _i64, _i32, _u32, _u64, _f32 = C.c_void_p, C.c_int64, C.c_int, C.c_uint32, 
 class HParams(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("n_vocab", "n_embd", "n_layer", "n_ff", "n_head", "n_head_kv",
                                           "head_dim", "rope_dims", "rope_neox")] + \
-               [(n, C.c_float) for n in ("rms_eps", "rope_base", "attn_scale", "rope_scale")]
+               [(n, C.c_float) for n in ("rms_eps", "rope_base", "attn_scale", "rope_scale", "embd_scale",
+                                         "rope_base_swa")] + \
+               [(n, C.c_int32) for n in ("gelu", "swa_window", "swa_pattern")]
 
 
 class CheckResult(C.Structure):
@@ -364,12 +366,19 @@ class Sampler:
 
 def hparams(hp: dict) -> HParams:
     """HParams of a synth.py model dict (engine/src/model.cpp:13-68 derivations)."""
-    return HParams(n_vocab=hp["n_vocab"], n_embd=hp["n_embd"], n_layer=hp["n_layer"], n_ff=hp["n_ff"],
-                   n_head=hp["n_head"], n_head_kv=hp["n_head_kv"], head_dim=hp["head_dim"],
-                   rope_dims=hp.get("rope_dims", hp["head_dim"]),
-                   rope_neox=int(hp["arch"] in ("qwen2", "qwen3", "gemma3")),
-                   rms_eps=hp["rms_eps"], rope_base=hp["rope_base"],
-                   attn_scale=float(np.float32(1.0) / np.sqrt(np.float32(hp["head_dim"]))), rope_scale=1.0)
+    f32 = np.float32
+    h = HParams(n_vocab=hp["n_vocab"], n_embd=hp["n_embd"], n_layer=hp["n_layer"], n_ff=hp["n_ff"],
+                n_head=hp["n_head"], n_head_kv=hp["n_head_kv"], head_dim=hp["head_dim"],
+                rope_dims=hp.get("rope_dims", hp["head_dim"]),
+                rope_neox=int(hp["arch"] in ("qwen2", "qwen3", "gemma3")),
+                rms_eps=hp["rms_eps"], rope_base=hp["rope_base"],
+                attn_scale=float(f32(1.0) / np.sqrt(f32(hp["head_dim"]))), rope_scale=1.0)
+    if hp["arch"] == "gemma3":  # model.cpp:44-63
+        h.embd_scale = float(np.sqrt(f32(hp["n_embd"])))
+        h.gelu, h.swa_window, h.swa_pattern, h.rope_base_swa = 1, hp.get("swa_window", 0), 6, 10000.0
+        if hp["n_layer"] == 62:
+            h.attn_scale = float(f32(1.0) / np.sqrt(f32(hp["n_embd"] // hp["n_head"])))
+    return h
 
 
 class Model:

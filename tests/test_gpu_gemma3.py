@@ -8,8 +8,9 @@ make_golden.py from engine/src/cpu_backend.cpp; the oracle restates it bit for b
 schedule's logits at the reference's bars (engine/src/checks.cpp:152-159: max|diff| / max|ref|
 <= 5e-3 with an f16 cache, 2e-2 with q8) and its 64 greedy ids. Against the oracle: a 40-token
 prompt chunk (the matmuls and the per-query windowed attention), verify batches of 5 and 12,
-and single tokens after them. A GGUF file loads to the same logits, and the engine's
-self-drafting output equals plain greedy decoding."""
+and single tokens after them; the same at head dimension 128 (27B's attention shape) and at
+Gemma 3 1B's layer width over a 700-token prompt past its 512-key window. A GGUF file loads to
+the same logits, and the engine's self-drafting output equals plain greedy decoding."""
 import os
 
 import numpy as np
@@ -127,6 +128,38 @@ def test_greedy_64_q8(ctx, tensors):
         print(f"gemma3 q8 greedy: first difference at token {k}, oracle top-2 gap {gap:.2e} of the largest logit")
         assert gap < 2e-2, (k, gap)
         assert ids[k] in np.argsort(lg)[-2:], k
+    m.close()
+
+
+# Head dimension 128 with two query heads a KV head (Gemma 3 27B's attention
+# shape): decode on the LDS kernel with windows, the global layer's q8 prompt
+# chunks on the matrix cores and its verify batches on the multi-query kernel.
+HP128 = dict(HP, n_head=8, n_head_kv=4, head_dim=128)
+# Gemma 3 1B's layer (1152 wide: Q8_0 rows, not whole Q4_K super-blocks;
+# window 512), seven layers so that one is global, and a smaller vocabulary.
+HP1B = dict(HP, n_embd=1152, n_ff=6912, n_layer=7, swa_window=512, wtype=synth.Q8_0, embd_type=synth.Q8_0,
+            n_vocab=4096, centered=False)
+
+
+@pytest.mark.parametrize("hp,kv,n_prompt", [(HP128, ts5hip.KV_Q8, 40), (HP128, ts5hip.KV_F16, 40),
+                                            (HP1B, ts5hip.KV_Q8, 700)])
+def test_other_shapes_against_oracle(ctx, hp, kv, n_prompt):
+    tensors = synth.model_tensors(hp, 11)
+    n_ctx = n_prompt + 32
+    m = ts5hip.Model(ctx, hp, n_ctx, kv)
+    m.set_tensors(tensors)
+    ref = oracle.Model(hp, tensors, n_ctx, kv)
+    rng = np.random.default_rng(9)
+    prompt = rng.integers(0, hp["n_vocab"], n_prompt).astype(np.int32)
+    rows_within(m.forward(prompt, 0), ref.forward(prompt, 0), BAR[kv], "prompt")
+    pos = n_prompt
+    toks = rng.integers(0, hp["n_vocab"], 5).astype(np.int32)
+    rows_within(m.forward(toks, pos, all_logits=True), ref.forward(toks, pos, all_logits=True), BAR[kv], "verify")
+    pos += 5
+    for i in range(4):
+        t = rng.integers(0, hp["n_vocab"], 1).astype(np.int32)
+        rows_within(m.forward(t, pos), ref.forward(t, pos), BAR[kv], f"token {pos}")
+        pos += 1
     m.close()
 
 

@@ -281,3 +281,31 @@ def test_missing_tensor_is_reported(ctx):
     with pytest.raises(ts5hip.Ts5HipError) as e:
         m.forward(np.array([1], np.int32), 0)
     assert e.value.code == ts5hip.ERR_STATE and "blk.1.ffn_up" in str(e.value)
+
+
+@pytest.mark.parametrize("arch", ["qwen3", "qwen2"])
+@pytest.mark.parametrize("kv", [ts5hip.KV_F16, ts5hip.KV_Q8])
+def test_decode_past_one_slice(ctx, arch, kv):
+    """Single tokens whose keys span several split-K slices (130-301 keys:
+    slices before the new key hold none of the new keys), with qwen3's
+    per-head q/k norms and qwen2's neox RoPE, against the oracle."""
+    hp = dict(synth.TINY_LLAMA_C, arch=arch)
+    tensors = synth.model_tensors(hp, 11)
+    m = ts5hip.Model(ctx, hp, 400, kv)
+    m.set_tensors(tensors)
+    ref = oracle.Model(hp, tensors, 400, kv)
+    rng = np.random.default_rng(4)
+    prompt = rng.integers(0, hp["n_vocab"], 129).astype(np.int32)
+    check_rows(m.forward(prompt, 0), ref.forward(prompt, 0), 5e-3 if kv == ts5hip.KV_F16 else 2e-2)
+    pos = prompt.size
+    for step in range(3):
+        for i in range(4):
+            t = rng.integers(0, hp["n_vocab"], 1).astype(np.int32)
+            check_rows(m.forward(t, pos), ref.forward(t, pos), 5e-3 if kv == ts5hip.KV_F16 else 2e-2)
+            pos += 1
+        fill = rng.integers(0, hp["n_vocab"], 60).astype(np.int32)  # on to the next slice
+        m.forward(fill, pos, logits=False)
+        ref.forward(fill, pos, logits=False)
+        pos += fill.size
+    m.close()
+

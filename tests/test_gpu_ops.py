@@ -377,7 +377,8 @@ def q8_cache(rng, B, HKV, n_ctx, HD):
 @pytest.mark.parametrize("B,ctxlen,H,HKV,HD", [(1, 8192, 32, 8, 128), (4, 8192, 32, 8, 128), (16, 8192, 32, 8, 128),
                                                (1, 32768, 32, 8, 128), (4, 32768, 32, 8, 128),
                                                (16, 32768, 32, 8, 128), (1, 1000, 32, 8, 128),
-                                               (2, 33, 14, 2, 64), (3, 1, 32, 8, 128)])
+                                               (2, 33, 14, 2, 64), (3, 1, 32, 8, 128),
+                                               (1, 700, 4, 1, 256), (3, 1500, 8, 4, 256), (2, 4096, 16, 8, 256)])
 def test_attention_vs_oracle(ctx, B, ctxlen, H, HKV, HD):
     """cfg3: one query per sequence over its q8 cache, full context, scale 1/sqrt(HD);
     every cfg3 shape (B 1, 4, 16 x 8192, 32768 keys) with the default split count."""
@@ -401,7 +402,8 @@ def test_attention_vs_oracle(ctx, B, ctxlen, H, HKV, HD):
 @pytest.mark.parametrize("B,ctxlen,H,HKV,HD,n_split", [(1, 8192, 32, 8, 128, 0), (4, 8192, 32, 8, 128, 0),
                                                        (16, 8192, 32, 8, 128, 0), (1, 32768, 32, 8, 128, 0),
                                                        (4, 32768, 32, 8, 128, 0), (16, 32768, 32, 8, 128, 0),
-                                                       (2, 70, 14, 2, 64, 0), (1, 5000, 32, 8, 128, 64)])
+                                                       (2, 70, 14, 2, 64, 0), (1, 5000, 32, 8, 128, 64),
+                                                       (1, 700, 4, 1, 256, 0), (2, 3000, 8, 4, 256, 0)])
 def test_attention_f16_vs_oracle(ctx, B, ctxlen, H, HKV, HD, n_split):
     """cfg3's attention over an f16 cache (KvType::F16, the reference's
     default; each value the nearest half of N(0,1)), long contexts included."""

@@ -91,7 +91,10 @@ __device__ inline AttnSpan attn_span(const AttnArgs &a, int split, int kvh, int 
     const int seq = a.kv_per_batch ? b : 0;
     sp.head_base = ((int64_t)seq * a.HKV + kvh) * a.n_ctx;
     const int first = a.kv_per_batch ? sp.pq : a.n_keys[0];  // the batch's first new key
-    sp.n_lo = max(first, sp.p0), sp.n_hi = a.append ? min(sp.pq + 1, sp.p1) : sp.n_lo;
+    // A slice that ends before the first new key holds none: n_hi = n_lo, not
+    // below it (the preparation counts n_hi - n_lo new keys beside the query
+    // heads it normalizes).
+    sp.n_lo = max(first, sp.p0), sp.n_hi = a.append ? max(sp.n_lo, min(sp.pq + 1, sp.p1)) : sp.n_lo;
     sp.has_new = sp.n_lo < sp.n_hi;
     return sp;
 }

@@ -223,9 +223,10 @@ const float *ts5hip_logits_view(const ts5hip_model *m);
 /* Backend::n_ctx / kv_type (engine/src/backend.h:34-39). */
 int ts5hip_n_ctx(const ts5hip_model *m);
 int ts5hip_kv_type(const ts5hip_model *m);
-/* How single-token steps run once every tensor is set: 1 HIP graph replays, 0 direct kernel
- * launches (TS5HIP_GRAPHS=0 at model creation); < 0 an error. No counterpart in the
- * reference (its Vulkan backend has one path): for tests and profiles. */
+/* How single-token steps and verify batches (2-16 tokens, one graph per token count and
+ * logits rows, captured on first use) run once every tensor is set: 1 HIP graph replays, 0
+ * direct kernel launches (TS5HIP_GRAPHS=0 at model creation); < 0 an error. No counterpart in
+ * the reference (its Vulkan backend has one path): for tests and profiles. */
 int ts5hip_token_path(ts5hip_model *m);
 /* The k (1..64) largest logits of rows [row0, row0 + nrows) of the last forward, found on the
  * GPU where the rows stay, descending with ties by ascending id, into host arrays

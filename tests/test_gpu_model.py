@@ -309,3 +309,42 @@ def test_decode_past_one_slice(ctx, arch, kv):
         pos += fill.size
     m.close()
 
+
+def test_verify_graph_replays(ctx, token_path, monkeypatch):
+    """Verify batches (2-16 tokens) replay a graph captured per token count
+    and logits rows: a sequence of batches of repeated and new sizes, at
+    advancing positions, with all, last or no logits rows (the rows buffer
+    growing in between), each bit-identical to the same batch launched
+    directly, with single tokens and syncs between the replays."""
+    if token_path != "graphs":
+        pytest.skip("compares the graph replays with direct launches")
+    hp = dict(MODELS["tiny_llama_c"]["hparams"])
+    tensors = synth.model_tensors(hp, make_golden.MODEL_SEED)
+    g = ts5hip.Model(ctx, hp, 160, ts5hip.KV_Q8)
+    g.set_tensors(tensors)
+    monkeypatch.setenv("TS5HIP_GRAPHS", "0")
+    d = ts5hip.Model(ctx, hp, 160, ts5hip.KV_Q8)
+    d.set_tensors(tensors)
+    assert (g.token_path(), d.token_path()) == ("graphs", "direct")
+    rng = np.random.default_rng(21)
+    prompt = rng.integers(0, hp["n_vocab"], 20).astype(np.int32)
+    assert np.array_equal(g.forward(prompt, 0).view(np.uint32), d.forward(prompt, 0).view(np.uint32))
+    pos = prompt.size
+    for n, rows in [(5, "all"), (5, "all"), (3, "last"), (5, "none"), (12, "all"), (2, "last"), (5, "all"),
+                    (16, "all"), (5, "last"), (7, "none"), (16, "all")]:
+        toks = rng.integers(0, hp["n_vocab"], n).astype(np.int32)
+        kw = dict(logits=rows != "none", all_logits=rows == "all")
+        got, want = g.forward(toks, pos, **kw), d.forward(toks, pos, **kw)
+        if rows != "none":
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (n, rows, pos)
+        pos += n
+        t = rng.integers(0, hp["n_vocab"], 1).astype(np.int32)  # a token step between the batches
+        assert np.array_equal(g.forward(t, pos).view(np.uint32), d.forward(t, pos).view(np.uint32))
+        pos += 1
+    # Rejected drafts: a batch again at an earlier position overwrites its cache rows.
+    toks = rng.integers(0, hp["n_vocab"], 5).astype(np.int32)
+    assert np.array_equal(g.forward(toks, pos - 8, all_logits=True).view(np.uint32),
+                          d.forward(toks, pos - 8, all_logits=True).view(np.uint32))
+    g.close()
+    d.close()
+

@@ -88,6 +88,14 @@ struct ts5hip_model {
     int32_t *pinned_ids = nullptr;  // [n_ctx + 1]
     hipGraphExec_t graph[N_GRAPHS] = {nullptr, nullptr, nullptr};
     bool graphs_stale = true;
+    // Verify batches (2..ATTN_MAX_NEW tokens) captured once per token count
+    // and logits rows (none, the last, all), replayed like a token's graph.
+    struct BatchGraph {
+        int nc = 0, rows = 0;
+        const float *out = nullptr;  // the logits rows it writes (reallocated rows: captured again)
+        hipGraphExec_t exec = nullptr;
+    };
+    std::vector<BatchGraph> bgraphs;
     bool use_graphs = true;  // TS5HIP_GRAPHS=0: launch each token's kernels directly (profilers)
     // Several tokens per call (prompt chunks, speculative verification): the
     // chunk's activations [CHUNK][...], its quantized activations, the
@@ -552,9 +560,19 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
     return TS5HIP_OK;
 }
 
+void drop_batch_graphs(ts5hip_model *m) {
+    for (auto &g : m->bgraphs)
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    m->bgraphs.clear();
+}
+
 int build_graphs(ts5hip_model *m) {
     if (!m->graphs_stale) return TS5HIP_OK;
     if (int rc = check_complete(m)) return rc;
+    if (!m->bgraphs.empty()) {
+        TS5_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+        drop_batch_graphs(m);
+    }
     if (!m->use_graphs) {
         m->graphs_stale = false;
         return TS5HIP_OK;
@@ -678,7 +696,7 @@ int ensure_batch(ts5hip_model *m) {
 // layer: every projection a matmul over the chunk, attention a causal batch
 // over the cache. Logits (rows: 0, 1 = the last token's, nc = all) go to
 // `logits` ([rows][n_vocab]).
-int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
+int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits, bool set_pos = true) {
     ts5hip_ctx *ctx = m->ctx;
     const hipStream_t s = ctx->stream;
     const ts5hip_hparams &hp = m->hp;
@@ -704,8 +722,10 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
         TS5_STAMP("matmul_" + type_tag(t), role);
         return TS5HIP_OK;
     };
-    TS5_HIP(ctx, launch_set_pos(m->state, p0, s));
-    TS5_STAMP("set_pos", "");
+    if (set_pos) {  // a captured batch reads the position its caller stored
+        TS5_HIP(ctx, launch_set_pos(m->state, p0, s));
+        TS5_STAMP("set_pos", "");
+    }
     TS5_HIP(ctx, launch_embed(m->tok_embd.type, m->tok_embd.d, E, hp.n_vocab, m->seq, m->state, nc, m->bx, s,
                               hp.embd_scale));
     TS5_STAMP("embed_" + type_tag(m->tok_embd.type), "token_embd");
@@ -820,6 +840,43 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits) {
 }
 #undef TS5_STAMP
 
+// A verify batch of nc tokens at the position in state[0] (set by the
+// caller), logits rows 0, 1 (the last) or nc to dev_rows: its captured graph,
+// captured on first use.
+int launch_batch_graph(ts5hip_model *m, int nc, int rows) {
+    ts5hip_ctx *ctx = m->ctx;
+    ts5hip_model::BatchGraph *hit = nullptr;
+    for (auto &g : m->bgraphs)
+        if (g.nc == nc && g.rows == rows) hit = &g;
+    if (hit && rows && hit->out != m->dev_rows) {  // the rows were reallocated since the capture
+        TS5_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        (void)hipGraphExecDestroy(hit->exec);
+        hit->exec = nullptr;
+    }
+    if (!hit || !hit->exec) {
+        hipGraph_t graph = nullptr;
+        TS5_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        const int rc = enqueue_batch(m, nc, 0, rows, m->dev_rows, false);
+        const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+        if (rc) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return rc;
+        }
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamEndCapture");
+        hipGraphExec_t exec = nullptr;
+        const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (ei != hipSuccess) return hip_fail(ctx, ei, "hipGraphInstantiate");
+        if (!hit) {
+            m->bgraphs.emplace_back();
+            hit = &m->bgraphs.back();
+        }
+        hit->nc = nc, hit->rows = rows, hit->out = m->dev_rows, hit->exec = exec;
+    }
+    TS5_HIP(ctx, hipGraphLaunch(hit->exec, ctx->stream));
+    return TS5HIP_OK;
+}
+
 int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool want_logits, bool all) {
     ts5hip_ctx *ctx = m->ctx;
     if (!tokens || n <= 0 || pos0 < 0) return fail(ctx, TS5HIP_ERR_ARG, "bad tokens/n/pos0");
@@ -843,6 +900,10 @@ int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool wan
         if (int rc = launch_token(m, want_logits ? G_LOGITS : G_KV)) return rc;
         if (want_logits)
             TS5_HIP(ctx, hipMemcpyAsync(m->dev_rows, m->logits, row_bytes, hipMemcpyDeviceToDevice, s));
+    } else if (m->use_graphs && n <= ATTN_MAX_NEW) {
+        if (int rc = ensure_batch(m)) return rc;
+        if (int rc = launch_batch_graph(m, n, !want_logits ? 0 : all ? n : 1)) return rc;
+        TS5_HIP(ctx, launch_set_pos(m->state, pos0 + n, s));
     } else {
         if (int rc = ensure_batch(m)) return rc;
         for (int c0 = 0; c0 < n; c0 += CHUNK) {
@@ -993,6 +1054,7 @@ void ts5hip_model_destroy(ts5hip_model *m) {
     (void)hipStreamSynchronize(m->ctx->stream);
     for (auto &g : m->graph)
         if (g) (void)hipGraphExecDestroy(g);
+    drop_batch_graphs(m);
     for (void *p : m->allocs) (void)hipFree(p);
     free_rows(m);
     if (m->pinned_ids) (void)hipHostFree(m->pinned_ids);

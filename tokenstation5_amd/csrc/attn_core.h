@@ -8,6 +8,12 @@
 
 namespace ts5hip {
 constexpr int ATTN_MIN_KEYS = 128;  // the fewest keys a split takes
+// Up to this many keys one work item takes them all: merging slices costs
+// ~2.3 us (the partials' writes, the count, the merge's read), more than one
+// work item spends on 256 keys (decode at 129-256 keys: 8.8 against 9.7 us,
+// 32/8 heads of 128; past 256 the LDS kernel's second pass of keys costs
+// more than the merge: 12.0 against 9.8 us at 384).
+constexpr int ATTN_SINGLE_MAX = 256;
 constexpr int ATTN_DEPTH = 2;       // chunks of K and V in flight per wave (attn_slice; 3 and 4 measured slower)
 
 // x0*c - x1*s and x0*s + x1*c with separate roundings, as the reference's
@@ -83,7 +89,7 @@ __device__ inline AttnSpan attn_span(const AttnArgs &a, int split, int kvh, int 
     // few KV heads) leaves the later splits empty rather than merging many
     // slivers; an empty split's work item returns at once, and the merge
     // counts and reads the `used` ones only.
-    int chunk = max((nw + n_split - 1) / n_split, ATTN_MIN_KEYS);
+    int chunk = nw <= ATTN_SINGLE_MAX ? nw : max((nw + n_split - 1) / n_split, ATTN_MIN_KEYS);
     chunk = (chunk + TILE - 1) / TILE * TILE;
     sp.used = (nw + chunk - 1) / chunk;
     sp.p0 = lo + split * chunk;
@@ -739,7 +745,7 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
         mo = M, lo_ = L;
         return O;
     };
-    if (n_split == 1) {  // the only work item: the output directly
+    if (sp.used == 1) {  // the only split with keys: the output directly, as the merge would
         for (int j = tid; j < NOUT; j += NT) {
             float M, L;
             const float O = item_value(j, M, L);

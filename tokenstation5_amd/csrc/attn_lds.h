@@ -249,6 +249,20 @@ __device__ inline void attn_slice_lds(const AttnArgs &a, int split, int kvh, int
     }
     __syncthreads();
 
+    if (sp.used == 1) {  // the only split with keys (a short cache): the output directly, as the merge would
+        for (int q = tid; q < G * HD / 4; q += NT) {
+            float4 v = *(const float4 *)&S.o_s[0][4 * q];
+#pragma unroll
+            for (int w = 1; w < NW; w++) {
+                const float4 o = *(const float4 *)&S.o_s[w][4 * q];
+                v.x += o.x, v.y += o.y, v.z += o.z, v.w += o.w;
+            }
+            const float L = S.l_s[4 * q / HD];
+            const float4 r = L > 0.f ? make_float4(v.x / L, v.y / L, v.z / L, v.w / L) : make_float4(0.f, 0.f, 0.f, 0.f);
+            *(float4 *)(a.out + (int64_t)b * a.H * HD + (int64_t)kvh * G * HD + 4 * q) = r;
+        }
+        return;
+    }
     attn_publish<G, HD, NT>(
         attn_part_group<G, HD>(a, b, split, kvh, n_split),
         [&](int q) {

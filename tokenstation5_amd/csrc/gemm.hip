@@ -1591,14 +1591,9 @@ template <int FMT, int MODE>
 static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
     if constexpr (FMT == F_Q4K || (FMT == F_Q6K && MODE != G_GLU)) {
         // Q4_K up to 8 tokens and Q6_K up to 5 (the verify batch's head) on
-        // k_gemm_m; the rest on k_gemm_small. TS5HIP_GEMM_M=0 keeps every
-        // batch on k_gemm_small, for comparison.
-        static const bool use_m = [] {
-            const char *e = getenv("TS5HIP_GEMM_M");
-            return !(e && e[0] == '0');
-        }();
+        // k_gemm_m; the rest on k_gemm_small.
         if constexpr (FMT == F_Q4K && MODE != G_GLU)
-            if (use_m && a.M <= 5 && a.ks == 1) {
+            if (a.M <= 5 && a.ks == 1) {
                 const int tiles = (a.nrows + 15) / 16;
                 const size_t lds = (size_t)GX_WAVES * 2 * (16 * Q4K_BYTES + 5 * 1024) + GX_WAVES * 2 * 64 * 4;
                 const dim3 g((unsigned)std::min(tiles, g_gemm_m_cu)), blk(64 * GX_WAVES);
@@ -1607,7 +1602,7 @@ static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
                 return hipGetLastError();
             }
         if constexpr (FMT == F_Q6K && MODE == G_STORE)
-            if (use_m && a.M <= 5 && a.ks == 1 && gemm_mh_lds(a.M, a.nb) <= 160 * 1024) {
+            if (a.M <= 5 && a.ks == 1 && gemm_mh_lds(a.M, a.nb) <= 160 * 1024) {
                 const int tiles = (a.nrows + 15) / 16;
                 const dim3 g((unsigned)std::min((tiles + GX_WAVES - 1) / GX_WAVES, g_gemm_m_cu)), blk(64 * GX_WAVES);
                 const size_t lds = gemm_mh_lds(a.M, a.nb);
@@ -1615,7 +1610,7 @@ static hipError_t gemm_go(const GemmArgs &a, dim3 grid, int tn, hipStream_t s) {
                 else hipLaunchKernelGGL((k_gemm_mh<1>), g, blk, lds, s, a);
                 return hipGetLastError();
             }
-        if (use_m && gemm_m_fits<FMT, MODE>(a.M)) return launch_gemm_m<FMT, MODE>(a, s);
+        if (gemm_m_fits<FMT, MODE>(a.M)) return launch_gemm_m<FMT, MODE>(a, s);
     }
     if (a.M <= 16) {
         hipLaunchKernelGGL((k_gemm_small<FMT, MODE>), dim3((a.nrows + 15) / 16), dim3(256), 0, s, a);

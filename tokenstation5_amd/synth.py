@@ -132,6 +132,8 @@ TINY_DRAFT = dict(arch="qwen2", n_vocab=1000, n_embd=448, n_layer=2, n_ff=768, n
 # The same shapes with centred Q4_K weights (input-dependent argmax).
 TINY_LLAMA_C = dict(TINY_LLAMA, centered=True)
 TINY_DRAFT_C = dict(TINY_DRAFT, centered=True)
+# Qwen 3's layer: per-head q/k norms, neox RoPE, no biases.
+TINY_QWEN3 = dict(TINY_LLAMA_C, arch="qwen3", rope_base=1000000.0, rms_eps=1e-6)
 # Gemma 3's layer (engine/src/model.cpp:44-63): head_dim 256 as in its 1B-12B
 # models, per-head q/k norms, norms after attention and the FFN, GELU, a
 # scaled embedding, tied Q6_K head (one small block scale for every row, so

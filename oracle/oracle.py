@@ -184,6 +184,8 @@ def hparams(hp: dict) -> HParams:
         h.swa_window = hp.get("swa_window", 0)
         h.swa_pattern = 6
         h.rope_base_swa = 10000.0
+        if hp.get("rope_scaling_factor"):  # linear scaling (model.cpp:53-56)
+            h.rope_scale = float(np.float32(1.0 / hp["rope_scaling_factor"]))
         if hp["n_layer"] == 62:
             h.attn_scale = float(f32(1.0) / np.sqrt(f32(hp["n_embd"] // hp["n_head"])))
     return h

@@ -78,6 +78,9 @@ def model_kv(hp: dict, vocab_pieces: bool = True) -> dict:
     }
     if hp.get("swa_window"):
         kv[f"{a}.attention.sliding_window"] = hp["swa_window"]
+    if hp.get("rope_scaling_factor"):
+        kv[f"{a}.rope.scaling.type"] = "linear"
+        kv[f"{a}.rope.scaling.factor"] = float(hp["rope_scaling_factor"])
     if vocab_pieces:
         # Pieces that decode back to "<id>" (no merges, no end-of-generation).
         kv["tokenizer.ggml.model"] = "gpt2"

@@ -126,7 +126,8 @@ def check_schedule(R, path, n, kv, nv):
 
 
 MODELS = {"tiny_llama": synth.TINY_LLAMA, "tiny_draft": synth.TINY_DRAFT, "tiny_llama_c": synth.TINY_LLAMA_C,
-          "tiny_draft_c": synth.TINY_DRAFT_C, "tiny_gemma3": synth.TINY_GEMMA3, "tiny_qwen3": synth.TINY_QWEN3}
+          "tiny_draft_c": synth.TINY_DRAFT_C, "tiny_gemma3": synth.TINY_GEMMA3, "tiny_qwen3": synth.TINY_QWEN3,
+          "tiny_llama31": synth.TINY_LLAMA31}
 
 
 def golden_models(names=None):

@@ -53,7 +53,8 @@ def check_rows(got, want, tol=2e-2):
         assert d <= tol and cos > 0.999, (r, d, cos)
 
 
-@pytest.mark.parametrize("name", ["tiny_llama", "tiny_draft", "tiny_llama_c", "tiny_draft_c", "tiny_qwen3"])
+@pytest.mark.parametrize("name", ["tiny_llama", "tiny_draft", "tiny_llama_c", "tiny_draft_c", "tiny_qwen3",
+                                  "tiny_llama31"])
 def test_check_schedule_logits(ctx, name):
     """ts5 check's order (engine/src/checks.cpp:119-124): n-4 tokens in one
     call with every position's logits, then 4 single-token calls."""
@@ -71,7 +72,8 @@ def test_check_schedule_logits(ctx, name):
     print(f"{name}: top-1 agreement {top:.3f}")
 
 
-@pytest.mark.parametrize("name", ["tiny_llama", "tiny_draft", "tiny_llama_c", "tiny_draft_c", "tiny_qwen3"])
+@pytest.mark.parametrize("name", ["tiny_llama", "tiny_draft", "tiny_llama_c", "tiny_draft_c", "tiny_qwen3",
+                                  "tiny_llama31"])
 def test_check_schedule_logits_f16_cache(ctx, name):
     """The same schedule with an f16 cache against the reference's f16 logits,
     at the reference's bar for that cache (engine/src/checks.cpp:159: 5e-3 of
@@ -93,7 +95,9 @@ def test_check_schedule_logits_f16_cache(ctx, name):
                                          ("tiny_llama_c", ts5hip.KV_F16, "greedy_f16_ids"),
                                          ("tiny_draft_c", ts5hip.KV_F16, "greedy_f16_ids"),
                                          ("tiny_qwen3", ts5hip.KV_Q8, "greedy_q8_ids"),
-                                         ("tiny_qwen3", ts5hip.KV_F16, "greedy_f16_ids")])
+                                         ("tiny_qwen3", ts5hip.KV_F16, "greedy_f16_ids"),
+                                         ("tiny_llama31", ts5hip.KV_Q8, "greedy_q8_ids"),
+                                         ("tiny_llama31", ts5hip.KV_F16, "greedy_f16_ids")])
 def test_greedy_64_tokens_match_reference(ctx, name, kv, key):
     """100 % argmax agreement over the first 64 generated tokens, with the
     device-resident greedy loop (argmax feeding the next step), for q8 and

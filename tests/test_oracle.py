@@ -205,12 +205,12 @@ def _check_model(name):
 
 
 @pytest.mark.parametrize("name", ["tiny_llama", "tiny_draft", "tiny_llama_c", "tiny_draft_c", "tiny_gemma3",
-                                  "tiny_qwen3"])
+                                  "tiny_qwen3", "tiny_llama31"])
 def test_model_logits_match_reference(name):
     _check_model(name)
 
 
-@pytest.mark.parametrize("name", ["tiny_llama_c", "tiny_draft_c", "tiny_gemma3", "tiny_qwen3"])
+@pytest.mark.parametrize("name", ["tiny_llama_c", "tiny_draft_c", "tiny_gemma3", "tiny_qwen3", "tiny_llama31"])
 @pytest.mark.parametrize("kv,key", [(2, "greedy_q8_ids"), (1, "greedy_f16_ids")])
 def test_greedy_decode_matches_reference(name, kv, key):
     hp = dict(json.load(open(os.path.join(G, "models.json")))[name]["hparams"])

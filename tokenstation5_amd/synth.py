@@ -132,6 +132,9 @@ TINY_DRAFT = dict(arch="qwen2", n_vocab=1000, n_embd=448, n_layer=2, n_ff=768, n
 # The same shapes with centred Q4_K weights (input-dependent argmax).
 TINY_LLAMA_C = dict(TINY_LLAMA, centered=True)
 TINY_DRAFT_C = dict(TINY_DRAFT, centered=True)
+# Llama 3.1's RoPE: a rope_freqs.weight tensor of per-frequency divisors
+# (with base 10000, so that 12-72 positions turn the slow frequencies too).
+TINY_LLAMA31 = dict(TINY_LLAMA_C, rope_freqs=True, rope_base=10000.0)
 # Qwen 3's layer: per-head q/k norms, neox RoPE, no biases.
 TINY_QWEN3 = dict(TINY_LLAMA_C, arch="qwen3", rope_base=1000000.0, rms_eps=1e-6)
 # Gemma 3's layer (engine/src/model.cpp:44-63): head_dim 256 as in its 1B-12B
@@ -139,10 +142,11 @@ TINY_QWEN3 = dict(TINY_LLAMA_C, arch="qwen3", rope_base=1000000.0, rms_eps=1e-6)
 # scaled embedding, tied Q6_K head (one small block scale for every row, so
 # that no row outweighs the others and the layers, not the token's own
 # embedding, decide the next token); 7 layers so that layer 5 is global and
-# the others slide, over an 8-key window that short sequences already cross.
+# the others slide, over an 8-key window that short sequences already cross;
+# linear RoPE scaling by 8 on the global layer, as Gemma 3 4B-27B have it.
 TINY_GEMMA3 = dict(arch="gemma3", n_vocab=1000, n_embd=512, n_layer=7, n_ff=1536, n_head=4, n_head_kv=1,
                    head_dim=256, rope_base=1000000.0, rms_eps=1e-6, swa_window=8, wtype=Q4_K, head_type=None,
-                   embd_type=Q6_K, centered=True, embd_d=5e-6)
+                   embd_type=Q6_K, centered=True, embd_d=5e-6, rope_scaling_factor=8.0)
 
 
 def _extra_norms(hp: dict, p: str):
@@ -154,6 +158,15 @@ def _extra_norms(hp: dict, p: str):
     if hp["arch"] == "gemma3":
         yield p + "post_attention_norm.weight", hp["n_embd"]
         yield p + "post_ffw_norm.weight", hp["n_embd"]
+
+
+def rope_divisors(hp: dict) -> np.ndarray:
+    """RoPE divisors per frequency, as Llama 3.1's GGUFs store them in
+    rope_freqs.weight (1 for the fastest frequencies up to 8 for the
+    slowest): here a ramp over the whole range, so that a test model's
+    short sequences already feel every one."""
+    n = hp.get("rope_dims", hp["head_dim"]) // 2
+    return (1.0 + 7.0 * (np.arange(n) / (n - 1)) ** 2).astype(np.float32)
 
 
 def model_tensors(hp: dict, seed: int):
@@ -175,6 +188,9 @@ def model_tensors(hp: dict, seed: int):
         b[:, 208:210] = _half_bytes(np.full(b.shape[0], hp["embd_d"]))
     out["token_embd.weight"] = (t, ne0, ne1, emb)
     out["output_norm.weight"] = (F32, E, 1, norm_weight(E, seed, "output_norm.weight"))
+    if hp.get("rope_freqs"):
+        f = rope_divisors(hp)
+        out["rope_freqs.weight"] = (F32, f.size, 1, f.view(np.uint8).reshape(1, -1))
     if hp.get("head_type") is not None:
         mat("output.weight", hp["head_type"], E, V)
     for i in range(hp["n_layer"]):

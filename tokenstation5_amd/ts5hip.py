@@ -376,6 +376,8 @@ def hparams(hp: dict) -> HParams:
     if hp["arch"] == "gemma3":  # model.cpp:44-63
         h.embd_scale = float(np.sqrt(f32(hp["n_embd"])))
         h.gelu, h.swa_window, h.swa_pattern, h.rope_base_swa = 1, hp.get("swa_window", 0), 6, 10000.0
+        if hp.get("rope_scaling_factor"):  # linear scaling (model.cpp:53-56)
+            h.rope_scale = float(np.float32(1.0 / hp["rope_scaling_factor"]))
         if hp["n_layer"] == 62:
             h.attn_scale = float(f32(1.0) / np.sqrt(f32(hp["n_embd"] // hp["n_head"])))
     return h

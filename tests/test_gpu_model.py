@@ -316,6 +316,44 @@ def test_decode_past_one_slice(ctx, arch, kv):
     m.close()
 
 
+def q8_values(rng, n, w, spread):
+    """n x w values ~ N(0, spread^2) as the q8 cache keeps them (per 32
+    values sc = f16(amax / 127), q = rint(v / sc) clamped to +-127): stored
+    exactly by ts5hip_kv_write and by the oracle's cache."""
+    blocks = (rng.standard_normal((n * w // 32, 32)) * spread).astype(np.float32)
+    sc = (np.abs(blocks).max(1) / np.float32(127)).astype(np.float16).astype(np.float32)
+    q = np.clip(np.rint(blocks / sc[:, None]), -127, 127)
+    return (q * sc[:, None]).astype(np.float32).reshape(n, w)
+
+
+@pytest.mark.parametrize("arch", ["llama", "qwen3", "qwen2"])
+def test_decode_over_long_q8_cache(ctx, arch):
+    """Single tokens at positions past 8192 over a q8 cache (one query over a
+    cache the LDS kernel does not take: the matrix-core attention k_attn_m1,
+    with the token's RoPE, per-head norms or bias and q8 append). Both
+    caches first hold the same q8 values at the 8990 earlier positions
+    (ts5hip_kv_write on the GPU, the oracle's own cache array), then each
+    token against the oracle at the reference's q8 bar."""
+    hp = dict(synth.TINY_LLAMA_C, arch=arch)
+    tensors = synth.model_tensors(hp, 11)
+    n_ctx, p0 = 9000, 8990
+    m = ts5hip.Model(ctx, hp, n_ctx, ts5hip.KV_Q8)
+    m.set_tensors(tensors)
+    ref = oracle.Model(hp, tensors, n_ctx, ts5hip.KV_Q8)
+    rng = np.random.default_rng(6)
+    W = hp["n_head_kv"] * hp["head_dim"]
+    for layer in range(hp["n_layer"]):
+        for which in (0, 1):
+            vals = q8_values(rng, p0, W, 2.0)
+            m.kv_write(layer, which, 0, vals)
+            ref.kv(which, layer)[:p0] = vals
+            assert np.array_equal(m.kv(layer, which, p0 - 64, 64), vals[-64:])
+    for i in range(6):
+        t = rng.integers(0, hp["n_vocab"], 1).astype(np.int32)
+        check_rows(m.forward(t, p0 + i), ref.forward(t, p0 + i), 2e-2)
+    m.close()
+
+
 def test_verify_graph_replays(ctx, token_path, monkeypatch):
     """Verify batches (2-16 tokens) replay a graph captured per token count
     and logits rows: a sequence of batches of repeated and new sizes, at

@@ -510,6 +510,60 @@ __device__ inline void attn_merge(const AttnArgs &a, int b, int kvh, int n_split
     if (tid == 0) st_dev(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 0);  // ready for the next use
 }
 
+// The end of a work item: its (m, l, o) from its waves' (S.m_w, S.l_w,
+// S.o_w: [wave][head] with m in the natural-log domain), then the output
+// itself when it is the only split with keys, else its partial, the count,
+// and the merge by the last work item of the (query, KV head).
+template <int HD, int G, int NT, class Lds>
+__device__ inline void attn_item_out(const AttnArgs &a, const AttnSpan &sp, int split, int kvh, int b, int n_split,
+                                     Lds &S) {
+    constexpr int NW = NT / 64;
+    constexpr float LOG2E = 1.4426950408889634f;
+    const int tid = threadIdx.x;
+    constexpr int NOUT = G * HD;
+    auto item_value = [&](int j, float &mo, float &lo_) -> float {
+        const int g = j / HD, d = j % HD;
+        float M = S.m_w[0][g];
+#pragma unroll
+        for (int w = 1; w < NW; w++) M = fmaxf(M, S.m_w[w][g]);
+        float O = 0.f, L = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float wt = S.m_w[w][g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((S.m_w[w][g] - M) * LOG2E);
+            O += wt * S.o_w[w][g][d];
+            L += wt * S.l_w[w][g];
+        }
+        mo = M, lo_ = L;
+        return O;
+    };
+    if (sp.used == 1) {  // the only split with keys: the output directly, as the merge would
+        for (int j = tid; j < NOUT; j += NT) {
+            float M, L;
+            const float O = item_value(j, M, L);
+            a.out[(int64_t)b * a.H * HD + (int64_t)kvh * G * HD + j] = L > 0.f ? O / L : 0.f;
+        }
+        return;
+    }
+    attn_publish<G, HD, NT>(
+        attn_part_group<G, HD>(a, b, split, kvh, n_split),
+        [&](int q) {
+            float M, L, o[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] = item_value(4 * q + i, M, L);
+            return make_float4(o[0], o[1], o[2], o[3]);
+        },
+        [&](int g) {
+            float M, L;
+            item_value(g * HD, M, L);
+            return make_float2(M, L);
+        });
+    __syncthreads();
+    if (tid == 0) S.last = atomicAdd(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 1) == sp.used - 1;
+    __syncthreads();
+    if (!S.last) return;
+    attn_merge<G, HD, NT>(a, b, kvh, n_split, sp.used, S.wts, S.red, &S.o_w[0][0][0]);
+}
+
 template <int HD, int G, int NT, bool F16 = false>
 __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, int n_split,
                                   SliceLds<HD, G, NT> &S) {
@@ -728,49 +782,7 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
     }
     __syncthreads();
 
-    // The work item's (m, l, o) from its waves'.
-    constexpr int NOUT = G * HD;
-    auto item_value = [&](int j, float &mo, float &lo_) -> float {
-        const int g = j / HD, d = j % HD;
-        float M = S.m_w[0][g];
-#pragma unroll
-        for (int w = 1; w < NW; w++) M = fmaxf(M, S.m_w[w][g]);
-        float O = 0.f, L = 0.f;
-#pragma unroll
-        for (int w = 0; w < NW; w++) {
-            const float wt = S.m_w[w][g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((S.m_w[w][g] - M) * LOG2E);
-            O += wt * S.o_w[w][g][d];
-            L += wt * S.l_w[w][g];
-        }
-        mo = M, lo_ = L;
-        return O;
-    };
-    if (sp.used == 1) {  // the only split with keys: the output directly, as the merge would
-        for (int j = tid; j < NOUT; j += NT) {
-            float M, L;
-            const float O = item_value(j, M, L);
-            a.out[(int64_t)b * a.H * HD + (int64_t)kvh * G * HD + j] = L > 0.f ? O / L : 0.f;
-        }
-        return;
-    }
-    attn_publish<G, HD, NT>(
-        attn_part_group<G, HD>(a, b, split, kvh, n_split),
-        [&](int q) {
-            float M, L, o[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) o[i] = item_value(4 * q + i, M, L);
-            return make_float4(o[0], o[1], o[2], o[3]);
-        },
-        [&](int g) {
-            float M, L;
-            item_value(g * HD, M, L);
-            return make_float2(M, L);
-        });
-    __syncthreads();
-    if (tid == 0) S.last = atomicAdd(a.counters + (b * a.HKV + kvh) * CTR_STRIDE, 1) == sp.used - 1;
-    __syncthreads();
-    if (!S.last) return;
-    attn_merge<G, HD, NT>(a, b, kvh, n_split, sp.used, S.wts, S.red, &S.o_w[0][0][0]);
+    attn_item_out<HD, G, NT>(a, sp, split, kvh, b, n_split, S);
 }
 
 }  // namespace ts5hip

@@ -495,6 +495,8 @@ def main():
                     help="only the cfg2 decode and its JSON line (for rocprofv3 runs)")
     ap.add_argument("--draft-only", action="store_true",
                     help="only cfg5's draft model: a 2048-token prompt, then 32 greedy tokens (for rocprofv3 runs)")
+    ap.add_argument("--cfg3-only", action="store_true",
+                    help="only cfg3's attention configurations and their JSON (for rocprofv3 runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this backend runs ts5's token loop on one GPU (batch 1); "
@@ -512,6 +514,11 @@ def main():
         return
     if args.draft_only:
         draft_only()
+        return
+    if args.cfg3_only:
+        ctx = ts5hip.Context(0)
+        print(json.dumps({"cfg3_attention": cfg3_attention(ctx)}), flush=True)
+        ctx.close()
         return
     ctx = ts5hip.Context(0)
     log(f"device {ctx.arch}, {ctx.n_cu} CUs, {ctx.hbm / 2**30:.0f} GiB")

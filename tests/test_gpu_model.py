@@ -327,30 +327,35 @@ def q8_values(rng, n, w, spread):
 
 
 @pytest.mark.parametrize("arch", ["llama", "qwen3", "qwen2"])
-def test_decode_over_long_q8_cache(ctx, arch):
-    """Single tokens at positions past 8192 over a q8 cache (one query over a
-    cache the LDS kernel does not take: the matrix-core attention k_attn_m1,
-    with the token's RoPE, per-head norms or bias and q8 append). Both
-    caches first hold the same q8 values at the 8990 earlier positions
-    (ts5hip_kv_write on the GPU, the oracle's own cache array), then each
-    token against the oracle at the reference's q8 bar."""
+@pytest.mark.parametrize("kv", [ts5hip.KV_Q8, ts5hip.KV_F16])
+def test_decode_over_long_cache(ctx, arch, kv):
+    """Single tokens at positions past 8192 (one query over a cache the LDS
+    kernel does not take: the matrix-core attention k_attn_m1, with the
+    token's RoPE, per-head norms or bias and its K/V append, q8 or f16).
+    Both caches first hold the same values at the 8990 earlier positions, as
+    the cache keeps them (ts5hip_kv_write on the GPU, the oracle's own cache
+    array), then each token against the oracle at the reference's bars
+    (engine/src/checks.cpp:152-159)."""
     hp = dict(synth.TINY_LLAMA_C, arch=arch)
     tensors = synth.model_tensors(hp, 11)
     n_ctx, p0 = 9000, 8990
-    m = ts5hip.Model(ctx, hp, n_ctx, ts5hip.KV_Q8)
+    m = ts5hip.Model(ctx, hp, n_ctx, kv)
     m.set_tensors(tensors)
-    ref = oracle.Model(hp, tensors, n_ctx, ts5hip.KV_Q8)
+    ref = oracle.Model(hp, tensors, n_ctx, kv)
     rng = np.random.default_rng(6)
     W = hp["n_head_kv"] * hp["head_dim"]
     for layer in range(hp["n_layer"]):
         for which in (0, 1):
-            vals = q8_values(rng, p0, W, 2.0)
+            if kv == ts5hip.KV_Q8:
+                vals = q8_values(rng, p0, W, 2.0)
+            else:
+                vals = (rng.standard_normal((p0, W)) * 2.0).astype(np.float16).astype(np.float32)
             m.kv_write(layer, which, 0, vals)
             ref.kv(which, layer)[:p0] = vals
             assert np.array_equal(m.kv(layer, which, p0 - 64, 64), vals[-64:])
     for i in range(6):
         t = rng.integers(0, hp["n_vocab"], 1).astype(np.int32)
-        check_rows(m.forward(t, p0 + i), ref.forward(t, p0 + i), 2e-2)
+        check_rows(m.forward(t, p0 + i), ref.forward(t, p0 + i), 2e-2 if kv == ts5hip.KV_Q8 else 5e-3)
     m.close()
 
 

@@ -13,7 +13,7 @@
 //                 and the last workgroup per (query, KV head) merges the
 //                 splits (attn_merge.comp:18-47).
 //  k_attn_m1      the same for one query per cache at head dimension 128
-//                 over a q8 cache, its key loop on the matrix cores.
+//                 (q8 or f16), its key loop on the matrix cores.
 //  k_attn_mq,     the same for a batch of 2-16 consecutive queries on one q8
 //  k_attn_mq_merge cache (B x G <= 32 rows, head dimension 128): all the
 //                 batch's queries in each (key slice, KV head) work item, on
@@ -140,9 +140,9 @@ __global__ __launch_bounds__(ATTN_NT) void k_attn(const int8_t *k8, const uint16
     attn_slice<HD, G, ATTN_NT, F16>(a, blockIdx.x, blockIdx.y, blockIdx.z, n_split, S);
 }
 
-// One query per (key slice, KV head, query) over a q8 cache at head dimension
-// 128, the key loop on the matrix cores (attn_m1.h).
-template <int G>
+// One query per (key slice, KV head, query) over a q8 or f16 cache at head
+// dimension 128, the key loop on the matrix cores (attn_m1.h).
+template <int G, bool F16>
 __global__ __launch_bounds__(M1_NT) void k_attn_m1(const int8_t *k8, const uint16_t *ks, const int8_t *v8,
                                                    const uint16_t *vs, const int32_t *n_keys, int n_ctx, int HKV,
                                                    int flags, int n_split, AttnArgs tail) {
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(M1_NT) void k_attn_m1(const int8_t *k8, const uint1
                    const_cast<uint16_t *>(vs)};
     a.n_keys = n_keys, a.n_ctx = n_ctx, a.HKV = HKV;
     a.kv_per_batch = flags & 1, a.append = (flags >> 1) & 1, a.rope = (flags >> 2) & 1;
-    attn_m1<G>(a, blockIdx.x, blockIdx.y, blockIdx.z, n_split, S);
+    attn_m1<G, F16>(a, blockIdx.x, blockIdx.y, blockIdx.z, n_split, S);
 }
 
 // A batch of B consecutive queries on one q8 cache, B x G <= 32 rows of
@@ -280,17 +280,17 @@ hipError_t launch_rope_kv(const float *qkv, int64_t qkv_stride, const float *bia
 // One query over a cache of up to this many positions takes k_attn_lds
 // (4096 keys: 12.4 against 14.1 us a layer inside a decode token for k_attn;
 // the two meet near 8192). Past it, and for a batch of queries on caches of
-// their own, a q8 cache at head dimension 128 takes k_attn_m1 (B 16 x 32768
-// keys: 248 against 306 us for k_attn), any other cache k_attn.
+// their own, a cache at head dimension 128 takes k_attn_m1 (q8, B 16 x 32768
+// keys: 248 against 306 us for k_attn), any other k_attn.
 constexpr int LDS_MAX_CTX = 8192;
 
 template <int HD, bool F16>
 static hipError_t attn_launch(int G, dim3 grid, const AttnArgs &a, hipStream_t s) {
     const int flags = (a.kv_per_batch ? 1 : 0) | (a.append ? 2 : 0) | (a.rope ? 4 : 0);
     const bool lds = grid.z == 1 && a.n_ctx <= LDS_MAX_CTX;
-    // Past the LDS kernel, one query per cache on a q8 cache of head
-    // dimension 128 takes the matrix-core key loop.
-    const bool m1 = !lds && !F16 && HD == 128 && (a.kv_per_batch || grid.z == 1);
+    // Past the LDS kernel, one query per cache at head dimension 128 takes
+    // the matrix-core key loop.
+    const bool m1 = !lds && HD == 128 && (a.kv_per_batch || grid.z == 1);
     if constexpr (HD == 256) {  // Gemma 3's heads (G 1, 2 or 4): the per-wave kernel
         auto go = [&](auto gc) {
             constexpr int GG = decltype(gc)::value;
@@ -309,7 +309,7 @@ static hipError_t attn_launch(int G, dim3 grid, const AttnArgs &a, hipStream_t s
 #define TS5_ATTN(GG)                                                                                          \
     case GG:                                                                                                  \
         if (m1)                                                                                               \
-            hipLaunchKernelGGL((k_attn_m1<GG>), grid, dim3(M1_NT), 0, s, (const int8_t *)a.kv.k,              \
+            hipLaunchKernelGGL((k_attn_m1<GG, F16>), grid, dim3(M1_NT), 0, s, (const int8_t *)a.kv.k,         \
                                (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs,  \
                                a.n_keys, a.n_ctx, a.HKV, flags, (int)grid.x, a);                             \
         else if (lds)                                                                                         \

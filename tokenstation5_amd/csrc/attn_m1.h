@@ -1,5 +1,5 @@
 // Split-K decode attention of one query per (key slice, KV head, query) work
-// item on the matrix cores, for a q8 cache at head dimension 128: the work
+// item on the matrix cores, for a q8 or f16 cache at head dimension 128: the work
 // items of k_attn (attn_core.h; the same spans, preparation, partials and
 // merge, engine/src/cpu_backend.cpp:224-248 per query, attn_merge.comp:18-47)
 // with the key loop of the multi-query kernel (attn_mq.h) on one 16-row tile
@@ -10,17 +10,20 @@
 // conversions), which bounds it near 3.7 TB/s at 16 queries x 32768 keys.
 //
 // 8 waves; each takes 16 keys of every 128-key step of the slice:
-//   S^T (16 keys x 16 rows) = K . Q^T on v_mfma_f32_16x16x32_f16 per 32-value
-//   scale group, K as exact fp16 integers and each row as fp16 hi + lo planes
-//   of q * scale * 2^-e (e per row), then S += ks * R;
+//   S^T (16 keys x 16 rows) = K . Q^T on v_mfma_f32_16x16x32_f16, each row as
+//   fp16 hi + lo planes of q * scale * 2^-e (e per row); q8: per 32-value
+//   scale group, K as exact fp16 integers, then S += ks * R; f16: K as it is
+//   stored, one sum over the 128 dims;
 //   online softmax per row (the rows are the lanes' columns);
 //   O^T (128 dims x 16 rows) += V^T . (P o vs)^T on v_mfma_f32_16x16x16_f16,
-//   V as exact integers transposed through the wave's own LDS, 128 P o vs
-//   as fp16 hi + lo (the D layout of S^T is the B layout: P stays in
-//   registers; the factor 128 keeps its lo plane out of the f16 subnormals
-//   and leaves O at the end).
+//   V (q8: exact integers; f16: as stored) transposed through the wave's own
+//   LDS, 128 P o vs (vs = 1 for f16) as fp16 hi + lo (the D layout of S^T is
+//   the B layout: P stays in registers; the factor 128 keeps its lo plane
+//   out of the f16 subnormals and leaves O at the end).
 // The waves' (m, l, O) then go through attn_item_out like k_attn's.
 #pragma once
+#include <type_traits>
+
 #include "attn_mq.h"
 
 namespace ts5hip {
@@ -53,10 +56,11 @@ struct M1Lds {
     int last;
 };
 
-template <int G>
+template <int G, bool F16>
 __device__ inline void attn_m1(const AttnArgs &a, int split, int kvh, int b, int n_split, M1Lds<G> &S) {
     static_assert(G >= 1 && G <= 16, "the query heads fit one 16-row tile");
     constexpr int HD = MQ_HD;
+    constexpr int VB = F16 ? 2 : 1;  // bytes per cached value
     constexpr float LOG2E = 1.4426950408889634f;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rl = lane & 15, kq = lane >> 4;
@@ -67,30 +71,42 @@ __device__ inline void attn_m1(const AttnArgs &a, int split, int kvh, int b, int
     // The slice's K and V (and scales) as bounded buffers from key p0: past
     // p1 they read zeros and touch no memory.
     const int64_t base = sp.head_base + sp.p0;
-    const __amdgpu_buffer_rsrc_t rk = slice_rsrc(a.kv.k + base * HD, (uint32_t)nkeys * HD);
-    const __amdgpu_buffer_rsrc_t rv = slice_rsrc(a.kv.v + base * HD, (uint32_t)nkeys * HD);
+    const __amdgpu_buffer_rsrc_t rk = slice_rsrc(a.kv.k + base * HD * VB, (uint32_t)nkeys * HD * VB);
+    const __amdgpu_buffer_rsrc_t rv = slice_rsrc(a.kv.v + base * HD * VB, (uint32_t)nkeys * HD * VB);
     const __amdgpu_buffer_rsrc_t rks = slice_rsrc(a.kv.ks + base * 4, (uint32_t)nkeys * 8);
     const __amdgpu_buffer_rsrc_t rvs = slice_rsrc(a.kv.vs + base * 4, (uint32_t)nkeys * 8);
     // A step's loads for this wave's 16 keys kl .. kl + 15 (relative to p0):
     // K: key kl + rl, dims 32 c + 8 kq .. + 7 (the A operand of group c);
     // V: keys kl + 4 kq + i, dims 8 rl .. 8 rl + 7 (the lane's share of the
-    // transpose); the K and V scales of keys kl + 4 kq + i (the lane's S and
-    // P entries), all 4 groups.
+    // transpose); q8: the K and V scales of keys kl + 4 kq + i (the lane's S
+    // and P entries), all 4 groups.
+    using Piece = std::conditional_t<F16, u32x4, u32x2>;  // 8 values
     struct Step {
-        u32x2 k[4], v[4];
-        u32x4 ks[2], vs[2];
+        Piece k[4], v[4];
+        u32x4 ks[F16 ? 1 : 2], vs[F16 ? 1 : 2];
+    };
+    auto piece = [&](__amdgpu_buffer_rsrc_t r, uint32_t e) -> Piece {  // values e .. e + 7
+        if constexpr (F16) return __builtin_amdgcn_raw_buffer_load_b128(r, e * 2, 0, 0);
+        else return __builtin_amdgcn_raw_buffer_load_b64(r, e, 0, 0);
     };
     auto load = [&](Step &w, int st) {
         const uint32_t kl = (uint32_t)(st * M1_STEP + wave * 16);
 #pragma unroll
-        for (int c = 0; c < 4; c++) w.k[c] = __builtin_amdgcn_raw_buffer_load_b64(rk, (kl + rl) * HD + 32 * c + 8 * kq, 0, 0);
+        for (int c = 0; c < 4; c++) w.k[c] = piece(rk, (kl + rl) * HD + 32 * c + 8 * kq);
 #pragma unroll
-        for (int i = 0; i < 4; i++) w.v[i] = __builtin_amdgcn_raw_buffer_load_b64(rv, (kl + 4 * kq + i) * HD + 8 * rl, 0, 0);
+        for (int i = 0; i < 4; i++) w.v[i] = piece(rv, (kl + 4 * kq + i) * HD + 8 * rl);
+        if constexpr (!F16) {
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            w.ks[h] = __builtin_amdgcn_raw_buffer_load_b128(rks, (kl + 4 * kq) * 8 + 16 * h, 0, 0);
-            w.vs[h] = __builtin_amdgcn_raw_buffer_load_b128(rvs, (kl + 4 * kq) * 8 + 16 * h, 0, 0);
+            for (int h = 0; h < 2; h++) {
+                w.ks[h] = __builtin_amdgcn_raw_buffer_load_b128(rks, (kl + 4 * kq) * 8 + 16 * h, 0, 0);
+                w.vs[h] = __builtin_amdgcn_raw_buffer_load_b128(rvs, (kl + 4 * kq) * 8 + 16 * h, 0, 0);
+            }
         }
+    };
+    // The 8 values of a piece as the MFMA operand.
+    auto values = [&](const Piece &p) -> mq_h8 {
+        if constexpr (F16) return __builtin_bit_cast(mq_h8, p);
+        else return mq_i8x8(p[0], p[1]);
     };
     // The query's inputs are requested first, then the first three steps'
     // K and V (loads complete in order: the preparation then waits for its
@@ -101,7 +117,7 @@ __device__ inline void attn_m1(const AttnArgs &a, int split, int kvh, int b, int
     attn_preload<HD, G, M1_NT>(a, kvh, b, sp, pre);
     Step A, Bs, Cs;
     if (!sp.has_new) load(A, 0), load(Bs, 1), load(Cs, 2);
-    attn_prepare<HD, G, M1_NT, false>(a, kvh, b, sp, S, &pre);
+    attn_prepare<HD, G, M1_NT, F16>(a, kvh, b, sp, S, &pre);
     if (sp.has_new) {
         wait_stores();
         __syncthreads();
@@ -143,34 +159,46 @@ __device__ inline void attn_m1(const AttnArgs &a, int split, int kvh, int b, int
     uint32_t *vt = S.vt[wave];
     auto step = [&](const Step &w, int st) {
         const int kl = st * M1_STEP + wave * 16;
-        // Scales: halfword 4 i + c of the pair of u32x4 is key kl + 4 kq + i, group c.
+        // q8 scales: halfword 4 i + c of the pair of u32x4 is key kl + 4 kq + i, group c.
         float ksf[4][4], vsf[4][4];
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 const int hw = 4 * i + c;
-                ksf[i][c] = h2f((w.ks[hw >> 3][(hw >> 1) & 3] >> (16 * (hw & 1))) & 0xffff);
-                vsf[i][c] = h2f((w.vs[hw >> 3][(hw >> 1) & 3] >> (16 * (hw & 1))) & 0xffff);
+                ksf[i][c] = F16 ? 1.f : h2f((w.ks[hw >> 3][(hw >> 1) & 3] >> (16 * (hw & 1))) & 0xffff);
+                vsf[i][c] = F16 ? 1.f : h2f((w.vs[hw >> 3][(hw >> 1) & 3] >> (16 * (hw & 1))) & 0xffff);
             }
         // S^T: D[key 4 kq + i][row rl].
         float s[4];
+        if constexpr (F16) {  // one sum over the 128 dims
+            mq_f4 R = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const mq_h8 ka = mq_i8x8(w.k[c][0], w.k[c][1]);
-            mq_f4 R = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[c], mq_f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            R = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[c], R, 0, 0, 0);
+            for (int c = 0; c < 4; c++) {
+                const mq_h8 ka = values(w.k[c]);
+                R = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[c], R, 0, 0, 0);
+                R = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[c], R, 0, 0, 0);
+            }
 #pragma unroll
-            for (int i = 0; i < 4; i++) s[i] = c == 0 ? ksf[i][c] * R[i] : fmaf(ksf[i][c], R[i], s[i]);
+            for (int i = 0; i < 4; i++) s[i] = R[i];
+        } else {  // a sum per scale group, scaled
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const mq_h8 ka = values(w.k[c]);
+                mq_f4 R = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[c], mq_f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                R = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[c], R, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) s[i] = c == 0 ? ksf[i][c] * R[i] : fmaf(ksf[i][c], R[i], s[i]);
+            }
         }
         // V^T of the wave's 16 keys into its LDS: dim d = 8 rl + j, key quad
         // kq (keys 4 kq + i) as 4 f16 at dword MQ_VT d + 2 kq, each value the
-        // exact integer v8 (P carries the scale times 128, O the factor 128
-        // until the end).
+        // exact integer v8 or the f16 value (P carries the scale times 128, O
+        // the factor 128 until the end).
         {
             mq_h8 hv[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) hv[i] = mq_i8x8(w.v[i][0], w.v[i][1]);
+            for (int i = 0; i < 4; i++) hv[i] = values(w.v[i]);
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const mq_h4 col = {hv[0][j], hv[1][j], hv[2][j], hv[3][j]};

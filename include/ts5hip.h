@@ -257,8 +257,11 @@ int ts5hip_kv_write(ts5hip_model *m, int layer, int which, int pos0, int n, cons
  * (or TS5HIP_PROFILE) set when the model is made: GPU time of its forward calls; with the value 1
  * also GPU time per kernel and weight role ("matvec_q4_k ffn_down", "attention_q8 decode", ...),
  * most first, with share and launch count (the reference's per-dispatch timestamps,
- * engine/src/vk_backend.cpp:347-358, :737-749, :926-932): every launch then runs directly with an
- * event after it instead of a graph replay. A buffer too small is an error that keeps the profile. */
+ * engine/src/vk_backend.cpp:347-358, :737-749, :926-932). Graph replays (single tokens, verify
+ * batches) then carry an event node after each kernel and are read after every replay (a host
+ * wait per replay; each kernel's time includes its node's, a few us); with TS5HIP_GRAPHS=0 every
+ * launch runs directly with an event after it. A buffer too small is an error that keeps the
+ * profile. */
 int ts5hip_take_profile(ts5hip_model *m, char *buf, int len);
 
 /* ---- GGUF files, KV sizing (engine/src/backend.h:53-81, engine/src/model.cpp:13-138,

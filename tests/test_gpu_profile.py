@@ -5,11 +5,12 @@ as ts5's per-dispatch timestamps report it (engine/src/vk_backend.cpp:347-358,
 
 Bars: every launch of a decode token and of a prompt batch appears under its
 kernel and weight role with the exact launch count the token loop makes
-(n_layer per layer kernel and token, one head per token); the per-kernel
-times add up to no more than the forward calls' GPU time; the profiled run
-(direct launches) computes exactly what the graph replay computes; taking
-the profile empties it; a model made without TS5_PROFILE reports nothing."""
-import os
+(n_layer per layer kernel and token, one head per token), with the token's
+kernels replayed as a HIP graph (an event node after each) or launched
+directly; so does a verify batch (its own graph); the per-kernel times add
+up to no more than the forward calls' GPU time; the profiled run computes
+exactly what the unprofiled one computes; taking the profile empties it; a
+model made without TS5_PROFILE reports nothing."""
 import re
 
 import numpy as np
@@ -28,20 +29,15 @@ def ctx():
     c.close()
 
 
-def model(ctx, profile):
-    old = os.environ.get("TS5_PROFILE")
+def model(ctx, profile, monkeypatch, graphs="1"):
+    monkeypatch.setenv("TS5HIP_GRAPHS", graphs)
     if profile:
-        os.environ["TS5_PROFILE"] = profile
+        monkeypatch.setenv("TS5_PROFILE", profile)
     else:
-        os.environ.pop("TS5_PROFILE", None)
-    try:
-        m = ts5hip.Model(ctx, HP, 128)
-    finally:
-        if old is None:
-            os.environ.pop("TS5_PROFILE", None)
-        else:
-            os.environ["TS5_PROFILE"] = old
+        monkeypatch.delenv("TS5_PROFILE", raising=False)
+    m = ts5hip.Model(ctx, HP, 128)
     m.set_tensors(synth.model_tensors(HP, 21))
+    assert m.token_path() == ("graphs" if graphs == "1" else "direct")
     return m
 
 
@@ -56,16 +52,19 @@ def parse(text):
     return rows, float(calls.group(1)) if calls else None
 
 
-def test_profile_per_kernel(ctx):
+@pytest.mark.parametrize("graphs", ["1", "0"])
+def test_profile_per_kernel(ctx, monkeypatch, graphs):
     L = HP["n_layer"]
     prompt = np.arange(3, 40, dtype=np.int32)
-    plain = model(ctx, None)
+    plain = model(ctx, None, monkeypatch, graphs)
     want = plain.forward(prompt, 0)[0]
     want_ids = plain.generate_greedy(int(np.argmax(want)), prompt.size, 8)
+    batch = np.array([5, 9, 11, 13, 17], np.int32)
+    want_batch = plain.forward(batch, prompt.size + 8, all_logits=True)
     assert plain.take_profile() == ""
     plain.close()
 
-    m = model(ctx, "1")
+    m = model(ctx, "1", monkeypatch, graphs)
     got = m.forward(prompt, 0)[0]
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     pf, total = parse(m.take_profile())
@@ -84,6 +83,14 @@ def test_profile_per_kernel(ctx):
         assert pf[label][1] == 8 * L, (label, pf.get(label))
     assert pf["matvec_argmax_q6_k output"][1] == 8 and pf["embed_q4_k token_embd"][1] == 8
     assert all(v[0] > 0 for v in pf.values())
+    assert sum(v[0] for v in pf.values()) <= total * 1.01 + 0.05
+
+    got_batch = m.forward(batch, prompt.size + 8, all_logits=True)
+    assert np.array_equal(got_batch.view(np.uint32), want_batch.view(np.uint32))
+    pf, total = parse(m.take_profile())
+    att = [v[1] for k, v in pf.items() if k.startswith("attention")]
+    assert sum(att) == L, pf
+    assert any(k.endswith(" ffn_down") for k in pf) and all(v[0] > 0 for v in pf.values()), pf
     assert sum(v[0] for v in pf.values()) <= total * 1.01 + 0.05
     assert m.take_profile() == ""
     m.close()

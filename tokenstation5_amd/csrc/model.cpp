@@ -90,10 +90,20 @@ struct ts5hip_model {
     bool graphs_stale = true;
     // Verify batches (2..ATTN_MAX_NEW tokens) captured once per token count
     // and logits rows (none, the last, all), replayed like a token's graph.
+    // With the per-kernel profile, a graph's own events: [0] before its
+    // first kernel, [i] after kernel i (recorded as event nodes of the graph,
+    // timed at every replay), and what kernel i was.
+    struct GraphProf {
+        std::vector<hipEvent_t> ev;
+        std::vector<std::string> label;
+    };
+    GraphProf gprof[N_GRAPHS];
+    GraphProf *prof_cap = nullptr;  // the graph being captured
     struct BatchGraph {
         int nc = 0, rows = 0;
         const float *out = nullptr;  // the logits rows it writes (reallocated rows: captured again)
         hipGraphExec_t exec = nullptr;
+        GraphProf prof;
     };
     std::vector<BatchGraph> bgraphs;
     bool use_graphs = true;  // TS5HIP_GRAPHS=0: launch each token's kernels directly (profilers)
@@ -106,8 +116,9 @@ struct ts5hip_model {
     int *bcounters = nullptr;
     // Profile (TS5_PROFILE or TS5HIP_PROFILE, engine/src/vk_backend.cpp:347-358):
     // 1 = GPU time of every kernel launch, by kernel and weight role (an event
-    // after each launch; tokens launched directly, not replayed as graphs);
-    // another nonzero value = GPU time of whole forward calls only.
+    // after each launch; in a graph, an event node after each kernel, read
+    // after every replay); another nonzero value = GPU time of whole forward
+    // calls only.
     int profile = 0;
     double prof_ms = 0;
     int prof_calls = 0, prof_tokens = 0;
@@ -211,9 +222,50 @@ int prof_close(ts5hip_model *m) {
     return TS5HIP_OK;
 }
 
+// An event of the graph being captured (an event node), labelled.
+int prof_node(ts5hip_model *m, const std::string &label) {
+    ts5hip_ctx *ctx = m->ctx;
+    hipEvent_t e;
+    TS5_HIP(ctx, hipEventCreate(&e));
+    m->prof_cap->ev.push_back(e);
+    m->prof_cap->label.push_back(label);
+    TS5_HIP(ctx, hipEventRecordWithFlags(e, ctx->stream, hipEventRecordExternal));
+    return TS5HIP_OK;
+}
+
+void prof_clear(ts5hip_model::GraphProf &gp) {
+    for (hipEvent_t e : gp.ev) (void)hipEventDestroy(e);
+    gp.ev.clear();
+    gp.label.clear();
+}
+
+// Starts the events of a graph about to be captured (profile 1).
+int prof_capture(ts5hip_model *m, ts5hip_model::GraphProf *gp) {
+    if (m->profile != 1) return TS5HIP_OK;
+    prof_clear(*gp);
+    m->prof_cap = gp;
+    return prof_node(m, std::string());
+}
+
+// After a replay of a graph captured with events: waits for it and adds its
+// kernels' times.
+int prof_replayed(ts5hip_model *m, const ts5hip_model::GraphProf &gp) {
+    if (m->profile != 1 || gp.ev.size() < 2) return TS5HIP_OK;
+    ts5hip_ctx *ctx = m->ctx;
+    TS5_HIP(ctx, hipEventSynchronize(gp.ev.back()));
+    for (size_t i = 1; i < gp.ev.size(); i++) {
+        float ms = 0;
+        TS5_HIP(ctx, hipEventElapsedTime(&ms, gp.ev[i - 1], gp.ev[i]));
+        auto &e = m->prof_kernels[gp.label[i]];
+        e.first += ms, e.second++;
+    }
+    return TS5HIP_OK;
+}
+
 // The event after the launch just enqueued, labelled "kernel role".
 int prof_stamp(ts5hip_model *m, const std::string &kernel, const char *role) {
     if (m->profile != 1) return TS5HIP_OK;
+    if (m->prof_cap) return prof_node(m, role && *role ? kernel + " " + role : kernel);
     if (m->prof_used == 0)
         if (int rc = prof_start(m)) return rc;  // a launch outside a forward call: timed from here on
     if (int rc = prof_event(m, role && *role ? kernel + " " + role : kernel)) return rc;
@@ -561,8 +613,10 @@ int enqueue_token(ts5hip_model *m, bool head, int tail) {
 }
 
 void drop_batch_graphs(ts5hip_model *m) {
-    for (auto &g : m->bgraphs)
+    for (auto &g : m->bgraphs) {
         if (g.exec) (void)hipGraphExecDestroy(g.exec);
+        prof_clear(g.prof);
+    }
     m->bgraphs.clear();
 }
 
@@ -586,7 +640,9 @@ int build_graphs(ts5hip_model *m) {
         }
         hipGraph_t graph = nullptr;
         TS5_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-        const int rc = enqueue_token(m, g != G_KV, g == G_GREEDY ? 1 : 0);
+        int rc = prof_capture(m, &m->gprof[g]);
+        if (!rc) rc = enqueue_token(m, g != G_KV, g == G_GREEDY ? 1 : 0);
+        m->prof_cap = nullptr;
         const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
         if (rc) {
             if (graph) (void)hipGraphDestroy(graph);
@@ -605,7 +661,7 @@ int build_graphs(ts5hip_model *m) {
 int launch_token(ts5hip_model *m, int g) {
     if (!m->use_graphs) return enqueue_token(m, g != G_KV, g == G_GREEDY ? 1 : 0);
     TS5_HIP(m->ctx, hipGraphLaunch(m->graph[g], m->ctx->stream));
-    return TS5HIP_OK;
+    return prof_replayed(m, m->gprof[g]);
 }
 
 // Candidates per row of a GPU pick: top-k with k <= PICK_K - 1, plus one more
@@ -854,9 +910,16 @@ int launch_batch_graph(ts5hip_model *m, int nc, int rows) {
         hit->exec = nullptr;
     }
     if (!hit || !hit->exec) {
+        if (!hit) {
+            m->bgraphs.emplace_back();
+            hit = &m->bgraphs.back();
+            hit->nc = nc, hit->rows = rows;
+        }
         hipGraph_t graph = nullptr;
         TS5_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-        const int rc = enqueue_batch(m, nc, 0, rows, m->dev_rows, false);
+        int rc = prof_capture(m, &hit->prof);
+        if (!rc) rc = enqueue_batch(m, nc, 0, rows, m->dev_rows, false);
+        m->prof_cap = nullptr;
         const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
         if (rc) {
             if (graph) (void)hipGraphDestroy(graph);
@@ -867,14 +930,10 @@ int launch_batch_graph(ts5hip_model *m, int nc, int rows) {
         const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
         (void)hipGraphDestroy(graph);
         if (ei != hipSuccess) return hip_fail(ctx, ei, "hipGraphInstantiate");
-        if (!hit) {
-            m->bgraphs.emplace_back();
-            hit = &m->bgraphs.back();
-        }
-        hit->nc = nc, hit->rows = rows, hit->out = m->dev_rows, hit->exec = exec;
+        hit->out = m->dev_rows, hit->exec = exec;
     }
     TS5_HIP(ctx, hipGraphLaunch(hit->exec, ctx->stream));
-    return TS5HIP_OK;
+    return prof_replayed(m, hit->prof);
 }
 
 int run_tokens(ts5hip_model *m, const int32_t *tokens, int n, int pos0, bool want_logits, bool all) {
@@ -1011,7 +1070,7 @@ int ts5hip_model_create(ts5hip_ctx *ctx, const ts5hip_hparams *hp, int n_ctx, in
     m->profile = prof && *prof ? std::atoi(prof) : 0;
     const char *graphs = std::getenv("TS5HIP_GRAPHS");
     // Every kernel timed on its own: launched directly, not replayed as a graph.
-    m->use_graphs = !(graphs && std::strcmp(graphs, "0") == 0) && m->profile != 1;
+    m->use_graphs = !(graphs && std::strcmp(graphs, "0") == 0);
     const int64_t E = hp->n_embd, F = hp->n_ff, HD = hp->head_dim, H = hp->n_head, HKV = hp->n_head_kv;
     const int64_t kv_elems = (int64_t)hp->n_layer * HKV * n_ctx * HD;
     int rc = 0;
@@ -1059,6 +1118,7 @@ void ts5hip_model_destroy(ts5hip_model *m) {
     free_rows(m);
     if (m->pinned_ids) (void)hipHostFree(m->pinned_ids);
     for (hipEvent_t e : m->prof_ev) (void)hipEventDestroy(e);
+    for (auto &gp : m->gprof) prof_clear(gp);
     delete m;
 }
 

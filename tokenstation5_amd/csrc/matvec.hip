@@ -193,15 +193,23 @@ static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
     } else {
         switch (a.t) {
         case T_Q4_K:
-            if (MODE != MV_ARGMAX && a.nb >= MV_KS_MINNB)
+            if (MODE != MV_ARGMAX && a.nb >= MV_KS_MINNB) {
+                // Too few rows for a group a CU at 4 rows a wave (the draft's
+                // 896-row down: 56 groups): one row a wave, 4 times the groups
+                // (a draft token 0.843 -> 0.796 ms with the Q8_0 rule below).
+                if ((a.nrows + MV_KS_R * 4 - 1) / (MV_KS_R * 4) < g_n_cu)
+                    return mv_go<Q4K, 1, MV_KS_WAVES, MV_KS, MODE>(a, s);
                 return mv_go<Q4K, MV_KS_R, MV_KS_WAVES, MV_KS, MODE>(a, s);
+            }
             switch (mv_rows_per_wave(a.nrows)) {
             case 3: return mv_go<Q4K, 3, 4, 1, MODE>(a, s);
             case 2: return mv_go<Q4K, 2, 4, 1, MODE>(a, s);
             default: return mv_go<Q4K, 4, 4, 1, MODE>(a, s);
             }
         case T_Q6_K: return mv_go<Q6K, MV_Q6_R, 4, 1, MODE>(a, s);
-        case T_Q8_0: return mv_go<Q80, 4, 4, 1, MODE>(a, s);
+        case T_Q8_0:  // one row a wave where 4 leave CUs without a group (the draft's 896-1152 rows)
+            if (MODE != MV_ARGMAX && (a.nrows + 15) / 16 < g_n_cu) return mv_go<Q80, 1, 4, 1, MODE>(a, s);
+            return mv_go<Q80, 4, 4, 1, MODE>(a, s);
         case T_Q8SM: return mv_go<Q8M, 4, 4, 1, MODE>(a, s);
         case T_F16: return mv_go<F16W, 4, 4, 1, MODE>(a, s);
         case T_F32: return mv_go<F32W, 2, 4, 1, MODE>(a, s);

@@ -360,6 +360,27 @@ def draft_only(prompt_len: int = 2048, steps: int = 32):
     ctx.close()
 
 
+def kernel_profile(hp, prompt_len: int = PROMPT, steps: int = 32):
+    """take_profile with TS5_PROFILE=1 over cfg2's decode: GPU time per kernel
+    and weight role of `steps` greedy tokens after the prompt, from event nodes
+    in the token's graph (or, with TS5HIP_GRAPHS=0, events after its direct
+    launches)."""
+    os.environ["TS5_PROFILE"] = "1"
+    ctx = ts5hip.Context(0)
+    m = ts5hip.Model(ctx, hp, prompt_len + steps + 16)
+    for name, t, ne0, ne1 in synth.tensor_specs(hp):
+        m.synth_tensor(name, t, ne0, ne1, SEED)
+    prompt = np.random.default_rng(SEED).integers(0, hp["n_vocab"], prompt_len).astype(np.int32)
+    m.forward(prompt[:-1], 0, logits=False)
+    first = int(m.generate_greedy(int(prompt[-1]), prompt_len - 1, 1)[0])
+    m.take_profile()  # the prompt's and the first token's
+    m.generate_greedy(first, prompt_len, steps)
+    print(f"token path: {m.token_path()}")
+    print(m.take_profile(), flush=True)
+    m.close()
+    ctx.close()
+
+
 def roofline_only(hp):
     """The roofline kernel's launches alone, then one RMSNorm over 256 MiB
     (k_rmsnorm_reg: 16384 rows of 4096 values, each row held in registers
@@ -497,6 +518,8 @@ def main():
                     help="only cfg5's draft model: a 2048-token prompt, then 32 greedy tokens (for rocprofv3 runs)")
     ap.add_argument("--cfg3-only", action="store_true",
                     help="only cfg3's attention configurations and their JSON (for rocprofv3 runs)")
+    ap.add_argument("--kernel-profile", action="store_true",
+                    help="only take_profile (TS5_PROFILE=1) of 32 decode tokens: GPU time per kernel and role")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this backend runs ts5's token loop on one GPU (batch 1); "
@@ -514,6 +537,9 @@ def main():
         return
     if args.draft_only:
         draft_only()
+        return
+    if args.kernel_profile:
+        kernel_profile(hp, args.prompt)
         return
     if args.cfg3_only:
         ctx = ts5hip.Context(0)

@@ -73,8 +73,11 @@ __device__ inline void attn_m1(const AttnArgs &a, int split, int kvh, int b, int
     const int64_t base = sp.head_base + sp.p0;
     const __amdgpu_buffer_rsrc_t rk = slice_rsrc(a.kv.k + base * HD * VB, (uint32_t)nkeys * HD * VB);
     const __amdgpu_buffer_rsrc_t rv = slice_rsrc(a.kv.v + base * HD * VB, (uint32_t)nkeys * HD * VB);
-    const __amdgpu_buffer_rsrc_t rks = slice_rsrc(a.kv.ks + base * 4, (uint32_t)nkeys * 8);
-    const __amdgpu_buffer_rsrc_t rvs = slice_rsrc(a.kv.vs + base * 4, (uint32_t)nkeys * 8);
+    __amdgpu_buffer_rsrc_t rks = rk, rvs = rv;  // q8: the scales (an f16 cache has none)
+    if constexpr (!F16) {
+        rks = slice_rsrc(a.kv.ks + base * 4, (uint32_t)nkeys * 8);
+        rvs = slice_rsrc(a.kv.vs + base * 4, (uint32_t)nkeys * 8);
+    }
     // A step's loads for this wave's 16 keys kl .. kl + 15 (relative to p0):
     // K: key kl + rl, dims 32 c + 8 kq .. + 7 (the A operand of group c);
     // V: keys kl + 4 kq + i, dims 8 rl .. 8 rl + 7 (the lane's share of the

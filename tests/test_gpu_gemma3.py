@@ -8,8 +8,9 @@ make_golden.py from engine/src/cpu_backend.cpp; the oracle restates it bit for b
 schedule's logits at the reference's bars (engine/src/checks.cpp:152-159: max|diff| / max|ref|
 <= 5e-3 with an f16 cache, 2e-2 with q8) and its 64 greedy ids. Against the oracle: a 40-token
 prompt chunk (the matmuls and the per-query windowed attention), verify batches of 5 and 12,
-and single tokens after them; the same at head dimension 128 (27B's attention shape) and at
-Gemma 3 1B's layer width over a 700-token prompt past its 512-key window. A GGUF file loads to
+and single tokens after them; the same at head dimension 128 (27B's attention shape), also
+over a 9000-position cache, and at Gemma 3 1B's layer width over a 700-token prompt past its
+512-key window. A GGUF file loads to
 the same logits, and the engine's self-drafting output equals plain greedy decoding."""
 import os
 
@@ -160,6 +161,39 @@ def test_other_shapes_against_oracle(ctx, hp, kv, n_prompt):
         t = rng.integers(0, hp["n_vocab"], 1).astype(np.int32)
         rows_within(m.forward(t, pos), ref.forward(t, pos), BAR[kv], f"token {pos}")
         pos += 1
+    m.close()
+
+
+@pytest.mark.parametrize("kv", [ts5hip.KV_Q8, ts5hip.KV_F16])
+def test_decode_over_long_cache(ctx, kv):
+    """Single tokens at positions past 8192 at head dimension 128: the global
+    layer over all 8990 earlier positions on the matrix-core one-query
+    attention (k_attn_m1), the sliding layers over their last 8 keys. Both
+    caches first hold the same values as the cache keeps them
+    (ts5hip_kv_write; the oracle's own cache array), then each token against
+    the oracle at the reference's bars."""
+    hp = HP128
+    tensors = synth.model_tensors(hp, 13)
+    n_ctx, p0 = 9000, 8990
+    m = ts5hip.Model(ctx, hp, n_ctx, kv)
+    m.set_tensors(tensors)
+    ref = oracle.Model(hp, tensors, n_ctx, kv)
+    rng = np.random.default_rng(8)
+    W = hp["n_head_kv"] * hp["head_dim"]
+    for layer in range(hp["n_layer"]):
+        for which in (0, 1):
+            x = (rng.standard_normal((p0, W)) * 2.0).astype(np.float32)
+            if kv == ts5hip.KV_Q8:  # per 32 values sc = f16(amax / 127), q = rint(v / sc)
+                b = x.reshape(-1, 32)
+                sc = (np.abs(b).max(1) / np.float32(127)).astype(np.float16).astype(np.float32)
+                x = (np.clip(np.rint(b / sc[:, None]), -127, 127) * sc[:, None]).astype(np.float32).reshape(p0, W)
+            else:
+                x = x.astype(np.float16).astype(np.float32)
+            m.kv_write(layer, which, 0, x)
+            ref.kv(which, layer)[:p0] = x
+    for i in range(5):
+        t = rng.integers(0, hp["n_vocab"], 1).astype(np.int32)
+        rows_within(m.forward(t, p0 + i), ref.forward(t, p0 + i), BAR[kv], f"token {p0 + i}")
     m.close()
 
 

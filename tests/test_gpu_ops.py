@@ -399,6 +399,42 @@ def test_attention_vs_oracle(ctx, B, ctxlen, H, HKV, HD):
         assert rel_l2(got[b], want) <= REL_L2, (b, rel_l2(got[b], want))
 
 
+@pytest.mark.parametrize("kv", ["q8", "f16"])
+@pytest.mark.parametrize("H,HKV", [(8, 8), (16, 8), (40, 8), (28, 4), (64, 8)])
+def test_attention_matrix_core_one_query(ctx, kv, H, HKV):
+    """The matrix-core one-query kernel (k_attn_m1: queries on caches of their
+    own, head dimension 128) for every query-head group it takes (G 1, 2, 5,
+    7, 8; G 4 is cfg3's), q8 and f16, each sequence with its own key count
+    (a whole number of 128-key steps, a ragged tail, a short cache of 5
+    keys), against the oracle at 2e-5 relative L2."""
+    HD, ctxlen, B = 128, 1000, 3
+    n_keys = np.array([ctxlen, ctxlen - 37, 5], np.int32)
+    rng = np.random.default_rng(H * 3 + HKV)
+    if kv == "q8":
+        k8, ks, kd = q8_cache(rng, B, HKV, ctxlen, HD)
+        v8, vs, vd = q8_cache(rng, B, HKV, ctxlen, HD)
+    else:
+        kd = rng.standard_normal((B, HKV, ctxlen, HD), dtype=np.float32).astype(np.float16)
+        vd = rng.standard_normal((B, HKV, ctxlen, HD), dtype=np.float32).astype(np.float16)
+    q = rng.standard_normal((B, H * HD)).astype(np.float32)
+    scale = float(np.float32(1) / np.sqrt(np.float32(HD)))
+    out = ctx.alloc(q.nbytes)
+    nk = ctx.to_device(n_keys)
+    if kv == "q8":
+        ctx.attn_decode(ctx.to_device(q), B, H, HKV, HD, ctx.to_device(k8), ctx.to_device(ks), ctx.to_device(v8),
+                        ctx.to_device(vs), ctxlen, nk, 1, scale, out)
+    else:
+        ctx.attn_decode_f16(ctx.to_device(q), B, H, HKV, HD, ctx.to_device(kd), ctx.to_device(vd), ctxlen, nk, 1,
+                            scale, out)
+    got = out.download(np.float32, (B, H * HD))
+    for b in range(B):
+        n = int(n_keys[b])
+        kc = kd[b].astype(np.float32).transpose(1, 0, 2).reshape(ctxlen, HKV * HD)[:n]
+        vc = vd[b].astype(np.float32).transpose(1, 0, 2).reshape(ctxlen, HKV * HD)[:n]
+        want = oracle.attention(q[b], kc, vc, H, HKV, HD, n - 1, scale)
+        assert rel_l2(got[b], want) <= 2e-5, (b, rel_l2(got[b], want))
+
+
 @pytest.mark.parametrize("B,ctxlen,H,HKV,HD,n_split", [(1, 8192, 32, 8, 128, 0), (4, 8192, 32, 8, 128, 0),
                                                        (16, 8192, 32, 8, 128, 0), (1, 32768, 32, 8, 128, 0),
                                                        (4, 32768, 32, 8, 128, 0), (16, 32768, 32, 8, 128, 0),

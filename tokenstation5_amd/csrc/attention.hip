@@ -13,7 +13,7 @@
 //                 and the last workgroup per (query, KV head) merges the
 //                 splits (attn_merge.comp:18-47).
 //  k_attn_m1      the same for one query per cache at head dimension 128
-//                 (q8 or f16), its key loop on the matrix cores.
+//                 (q8 or f16), its key loop on the matrix cores (attn_m1.hip).
 //  k_attn_mq,     the same for a batch of 2-16 consecutive queries on one q8
 //  k_attn_mq_merge cache (B x G <= 32 rows, head dimension 128): all the
 //                 batch's queries in each (key slice, KV head) work item, on
@@ -25,7 +25,6 @@
 #include <mutex>
 
 #include "attn_lds.h"
-#include "attn_m1.h"
 #include "attn_mq.h"
 
 
@@ -138,21 +137,6 @@ __global__ __launch_bounds__(ATTN_NT) void k_attn(const int8_t *k8, const uint16
     a.n_keys = n_keys, a.n_ctx = n_ctx, a.HKV = HKV;
     a.kv_per_batch = flags & 1, a.append = (flags >> 1) & 1, a.rope = (flags >> 2) & 1;
     attn_slice<HD, G, ATTN_NT, F16>(a, blockIdx.x, blockIdx.y, blockIdx.z, n_split, S);
-}
-
-// One query per (key slice, KV head, query) over a q8 or f16 cache at head
-// dimension 128, the key loop on the matrix cores (attn_m1.h).
-template <int G, bool F16>
-__global__ __launch_bounds__(M1_NT) void k_attn_m1(const int8_t *k8, const uint16_t *ks, const int8_t *v8,
-                                                   const uint16_t *vs, const int32_t *n_keys, int n_ctx, int HKV,
-                                                   int flags, int n_split, AttnArgs tail) {
-    __shared__ M1Lds<G> S;
-    AttnArgs a = tail;
-    a.kv = KvLayer{const_cast<int8_t *>(k8), const_cast<uint16_t *>(ks), const_cast<int8_t *>(v8),
-                   const_cast<uint16_t *>(vs)};
-    a.n_keys = n_keys, a.n_ctx = n_ctx, a.HKV = HKV;
-    a.kv_per_batch = flags & 1, a.append = (flags >> 1) & 1, a.rope = (flags >> 2) & 1;
-    attn_m1<G, F16>(a, blockIdx.x, blockIdx.y, blockIdx.z, n_split, S);
 }
 
 // A batch of B consecutive queries on one q8 cache, B x G <= 32 rows of
@@ -308,11 +292,7 @@ static hipError_t attn_launch(int G, dim3 grid, const AttnArgs &a, hipStream_t s
     } else {
 #define TS5_ATTN(GG)                                                                                          \
     case GG:                                                                                                  \
-        if (m1)                                                                                               \
-            hipLaunchKernelGGL((k_attn_m1<GG, F16>), grid, dim3(M1_NT), 0, s, (const int8_t *)a.kv.k,         \
-                               (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs,  \
-                               a.n_keys, a.n_ctx, a.HKV, flags, (int)grid.x, a);                             \
-        else if (lds)                                                                                         \
+        if (lds)                                                                                              \
             hipLaunchKernelGGL((k_attn_lds<HD, GG, F16>), grid, dim3(ATTN_NT), 0, s, (const int8_t *)a.kv.k,  \
                                (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs,  \
                                a.n_keys, a.n_ctx, a.HKV, flags, (int)grid.x, a);                             \
@@ -321,6 +301,7 @@ static hipError_t attn_launch(int G, dim3 grid, const AttnArgs &a, hipStream_t s
                                (const uint16_t *)a.kv.ks, (const int8_t *)a.kv.v, (const uint16_t *)a.kv.vs,  \
                                a.n_keys, a.n_ctx, a.HKV, flags, (int)grid.x, a);                             \
         break;
+    if (m1) return launch_attn_m1(G, F16, grid, a, s);
     switch (G) {
         TS5_ATTN(1)
         TS5_ATTN(2)

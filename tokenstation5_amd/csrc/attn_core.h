@@ -785,4 +785,8 @@ __device__ inline void attn_slice(const AttnArgs &a, int split, int kvh, int b, 
     attn_item_out<HD, G, NT>(a, sp, split, kvh, b, n_split, S);
 }
 
+// The matrix-core one-query kernel (attn_m1.hip): G query heads a KV head,
+// a q8 or f16 cache at head dimension 128, grid (n_split, HKV, B).
+hipError_t launch_attn_m1(int G, bool f16, dim3 grid, const AttnArgs &a, hipStream_t s);
+
 }  // namespace ts5hip

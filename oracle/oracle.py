@@ -241,7 +241,7 @@ class Model:
         return np.ctypeslib.as_array(p, shape=(self.n_ctx, kvw))
 
 
-# --- the reference's own CPU code (built in the survey container only) -------------
+# --- the reference's own CPU code (built only where its sources are present) --------
 
 _ref = None
 

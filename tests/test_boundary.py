@@ -93,6 +93,7 @@ def test_synth_layouts_are_whole_blocks():
     for hp in (synth.LLAMA_8B, synth.DRAFT_0P5B, synth.TARGET_14B):
         wb = synth.weight_bytes(hp)
         assert wb["layer"] > 0 and wb["head"] > 0
-    # cfg2's per-token weight bytes (algorithmic) from the survey's figure.
+    # cfg2's per-token weight bytes (algorithmic): 32 Q4_K layers of 4096-wide
+    # rows (14336 for down) and the Q6_K head over a 128256-token vocabulary.
     wb = synth.weight_bytes(synth.LLAMA_8B)
     assert wb["layers"] == 3925868544 and wb["head"] == 430940160

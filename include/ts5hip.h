@@ -165,6 +165,11 @@ int ts5hip_attn_decode_noalloc(ts5hip_ctx *ctx, const float *q, int B, int n_hea
 int ts5hip_attn_prompt(ts5hip_ctx *ctx, const float *q, int nq, int n_head, int n_head_kv, int head_dim,
                        const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx, int pos0,
                        float scale, float *out);
+/* The same over an f16 cache (KvType::F16: k16 / v16 the halves, [n_head_kv][n_ctx][head_dim],
+ * no scales), the reference's attn_pf128 for f16 caches (engine/shaders/attn_pf128.comp over
+ * attn_pf.glsl; chosen at engine/src/vk_backend.cpp:954-975). */
+int ts5hip_attn_prompt_f16(ts5hip_ctx *ctx, const float *q, int nq, int n_head, int n_head_kv, int head_dim,
+                           const void *k16, const void *v16, int n_ctx, int pos0, float scale, float *out);
 /* Greedy token per row: the first maximum of each row of n logits (engine/src/engine.cpp:17). */
 int ts5hip_argmax(ts5hip_ctx *ctx, const float *x, int n, int rows, int32_t *out_dev);
 /* The k (<= 64) largest of n logits, descending, ties by ascending id (the candidate set

@@ -603,6 +603,29 @@ def test_attention_prompt_vs_oracle(ctx, nq, p0, n_ctx, H, HKV):
         assert rel_l2(got[t], want) <= 2e-5, (t, rel_l2(got[t], want))
 
 
+@pytest.mark.parametrize("nq,p0,n_ctx,H,HKV", [(64, 0, 64, 32, 8), (256, 3840, 4096, 32, 8), (100, 1000, 2048, 8, 2),
+                                             (37, 5, 64, 4, 1), (130, 300, 512, 16, 16), (17, 4079, 4096, 32, 8),
+                                             (1, 100, 200, 32, 8)])
+def test_attention_prompt_f16_vs_oracle(ctx, nq, p0, n_ctx, H, HKV):
+    """Prompt chunks over an f16 cache (each value the nearest half of N(0,1))
+    on the matrix cores, K and V as stored: one split and merged splits,
+    ragged query blocks, GQA groups 1-8, held to 2e-5 like the q8 path."""
+    HD = 128
+    rng = np.random.default_rng(nq + p0 + H + 7)
+    k = rng.standard_normal((HKV, n_ctx, HD), dtype=np.float32).astype(np.float16)
+    v = rng.standard_normal((HKV, n_ctx, HD), dtype=np.float32).astype(np.float16)
+    q = (rng.standard_normal((nq, H * HD)) * 3).astype(np.float32)
+    scale = float(np.float32(1) / np.sqrt(np.float32(HD)))
+    out = ctx.alloc(q.nbytes)
+    ctx.attn_prompt_f16(ctx.to_device(q), nq, H, HKV, HD, ctx.to_device(k), ctx.to_device(v), n_ctx, p0, scale, out)
+    got = out.download(np.float32, (nq, H * HD))
+    kc = k.astype(np.float32).transpose(1, 0, 2).reshape(n_ctx, HKV * HD)
+    vc = v.astype(np.float32).transpose(1, 0, 2).reshape(n_ctx, HKV * HD)
+    for t in range(nq):
+        want = oracle.attention(q[t], kc, vc, H, HKV, HD, p0 + t, scale)
+        assert rel_l2(got[t], want) <= 2e-5, (t, rel_l2(got[t], want))
+
+
 def test_attention_prompt_large_values_and_bad_shapes(ctx):
     """Queries of 1e6 (past fp16: each row is scaled by a power of two first), keys of
     1e3; then shapes the path does not take are refused, not guessed."""

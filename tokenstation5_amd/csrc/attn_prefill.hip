@@ -23,6 +23,12 @@
 //    fp16 hi + lo; Vh Ph + Vl Ph + Vh Pl.
 // Several key splits write (m, l, O) partials that a second kernel merges in
 // split order; one split writes O / l directly.
+//
+// An f16 cache (the reference's default KV type) takes the same kernel with
+// K and V as stored: DMA brings K straight into the fp16 tile layout (two
+// buffers, the next block's while this one is computed), V's raw block is
+// transposed into V^T, S needs no scale and the value product no lo plane of
+// V (Vh Ph + Vh Pl).
 #include <algorithm>
 
 #include "common.h"
@@ -49,8 +55,11 @@ constexpr int PF_KB = 64;     // keys per block
 constexpr int PF_ROWS = 128;  // query rows per workgroup
 constexpr float PF_LOG2E = 1.4426950408889634f;
 
+template <int HD, bool F16>
+struct PfLds;
+
 template <int HD>
-struct PfLds {
+struct PfLds<HD, false> {
     int8_t k8[PF_KB][HD];          // raw blocks (DMA)
     int8_t v8[PF_KB][HD];
     uint16_t ks[PF_KB][HD / 32];
@@ -61,9 +70,16 @@ struct PfLds {
     uint2 vl[HD][PF_KB / 4];       // V^T lo
 };
 
+template <int HD>
+struct PfLds<HD, true> {
+    uint4 k16[2][PF_KB][HD / 8];  // K as stored (DMA), unit u of key k at u ^ (k & 15); two blocks in turn
+    uint16_t v16[PF_KB][HD];      // raw V block (DMA)
+    uint2 vh[HD][PF_KB / 4];      // V^T, key quad q of row d at q ^ (d & 15)
+};
+
 // Raw block at key kb (keys past n_ctx read the last slot; they are masked).
 template <int HD>
-__device__ inline void pf_issue(const PfArgs &a, PfLds<HD> &L, int64_t slot0, int kb, int wave, int lane) {
+__device__ inline void pf_issue(const PfArgs &a, PfLds<HD, false> &L, int64_t slot0, int kb, int wave, int lane, int) {
     constexpr int PIECES = PF_KB * HD / 16;  // 16-byte pieces per plane
     constexpr int PER_WAVE = PIECES / 64 / 4;
 #pragma unroll
@@ -82,9 +98,55 @@ __device__ inline void pf_issue(const PfArgs &a, PfLds<HD> &L, int64_t slot0, in
     }
 }
 
+// An f16 block at key kb: K into k16[buf] (LDS piece p = 64 j + lane is
+// unit p % (HD / 8) ^ (key & 15) of key p / (HD / 8)), V raw into v16.
+template <int HD>
+__device__ inline void pf_issue(const PfArgs &a, PfLds<HD, true> &L, int64_t slot0, int kb, int wave, int lane,
+                                int buf) {
+    constexpr int UNITS = HD / 8;                     // 16-byte units of a key
+    constexpr int PER_WAVE = PF_KB * UNITS / 64 / 4;  // 1024-byte requests a wave, per plane
+    const int8_t *kbase = (const int8_t *)a.kv.k, *vbase = (const int8_t *)a.kv.v;
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; i++) {
+        const int j = wave * PER_WAVE + i, p = 64 * j + lane, key = p / UNITS, pos = p % UNITS;
+        const int64_t slot = slot0 + min(kb + key, a.n_ctx - 1);
+        dma16(kbase + slot * HD * 2 + 16 * (pos ^ (key & 15)), lds_addr(&L.k16[buf][0][0]) + 1024 * j);
+        dma16(vbase + slot * HD * 2 + 16 * pos, lds_addr(&L.v16[0][0]) + 1024 * j);
+    }
+}
+
+// Raw V -> V^T (keys at or past kend: V = 0); K is already in place.
+template <int HD>
+__device__ inline void pf_convert(PfLds<HD, true> &L, int kb, int kend) {
+    constexpr int DQ = HD / 4;  // d quads; thread = (4 consecutive d, 8 consecutive keys)
+    for (int w = threadIdx.x; w < DQ * (PF_KB / 8); w += 256) {
+        const int dq = w % DQ, k0 = 8 * (w / DQ), d0 = 4 * dq;
+        uint32_t hw[4][4];  // [d][key pair]
+#pragma unroll
+        for (int kk = 0; kk < 8; kk += 2) {
+            uint2 r[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int key = k0 + kk + e;
+                r[e] = kb + key < kend ? *(const uint2 *)&L.v16[key][d0] : make_uint2(0u, 0u);
+            }
+            hw[0][kk / 2] = (r[0].x & 0xffffu) | (r[1].x << 16);
+            hw[1][kk / 2] = (r[0].x >> 16) | (r[1].x & 0xffff0000u);
+            hw[2][kk / 2] = (r[0].y & 0xffffu) | (r[1].y << 16);
+            hw[3][kk / 2] = (r[0].y >> 16) | (r[1].y & 0xffff0000u);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int d = d0 + j, q0 = k0 / 4;
+            L.vh[d][q0 ^ (d & 15)] = make_uint2(hw[j][0], hw[j][1]);
+            L.vh[d][(q0 + 1) ^ (d & 15)] = make_uint2(hw[j][2], hw[j][3]);
+        }
+    }
+}
+
 // Raw -> K16, ksf, V^T hi/lo (keys at or past kend: V = 0).
 template <int HD>
-__device__ inline void pf_convert(PfLds<HD> &L, int kb, int kend) {
+__device__ inline void pf_convert(PfLds<HD, false> &L, int kb, int kend) {
     const int t = threadIdx.x;
     {  // K: thread t converts 8 * HD / 256 ... one key quarter of 32 values
         constexpr int PER_KEY = HD / 32;  // threads per key
@@ -145,10 +207,10 @@ __device__ inline void pf_convert(PfLds<HD> &L, int kb, int kend) {
     }
 }
 
-template <int HD, int G>
+template <int HD, int G, bool F16>
 __global__ __launch_bounds__(256, 2) void k_attn_pf(PfArgs a) {
     constexpr int NC = HD / 32, NDT = HD / 16, QB = PF_ROWS / G;
-    __shared__ PfLds<HD> L;
+    __shared__ PfLds<HD, F16> L;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, kq = lane >> 4, rl = lane & 15;
     const int h = blockIdx.y, t0 = blockIdx.x * QB, sp = blockIdx.z;
@@ -198,30 +260,48 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(PfArgs a) {
         for (int dt = 0; dt < NDT; dt++) O[qt][dt] = v4f{0.f, 0.f, 0.f, 0.f};
     }
 
-    pf_issue<HD>(a, L, slot0, kbeg, wave, lane);
-    for (int kb = kbeg; kb < kend; kb += PF_KB) {
+    pf_issue<HD>(a, L, slot0, kbeg, wave, lane, 0);
+    for (int kb = kbeg, nb = 0; kb < kend; kb += PF_KB, nb++) {
         wait_vm_n<0>();
         __syncthreads();  // the raw block is in; every wave is done with the last block's K16 / V^T
         pf_convert<HD>(L, kb, kend);
         __syncthreads();  // K16 / V^T ready; the raw buffers are free
-        if (kb + PF_KB < kend) pf_issue<HD>(a, L, slot0, kb + PF_KB, wave, lane);
+        if (kb + PF_KB < kend) pf_issue<HD>(a, L, slot0, kb + PF_KB, wave, lane, (nb + 1) & 1);
 
         // S^T tiles: keys kb + 16 kt + 4 kq + i, row columns.
         float S[4][2][4];
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
             const int key = 16 * kt + rl;
+            if constexpr (F16) {  // K as stored: one sum over the head dimension
+                v4f R[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-            for (int c = 0; c < NC; c++) {
-                const v8h A = __builtin_bit_cast(v8h, L.k16[key][(4 * c + kq) ^ (key & 15)]);
-                const float4 ks4 = *(const float4 *)&L.ksf[c][16 * kt + 4 * kq];
-                const float ksv[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
+                for (int c = 0; c < NC; c++) {
+                    const v8h A = __builtin_bit_cast(v8h, L.k16[nb & 1][key][(4 * c + kq) ^ (key & 15)]);
 #pragma unroll
-                for (int qt = 0; qt < 2; qt++) {
-                    v4f R = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, qh[qt][c], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    R = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, ql[qt][c], R, 0, 0, 0);
+                    for (int qt = 0; qt < 2; qt++) {
+                        R[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, qh[qt][c], R[qt], 0, 0, 0);
+                        R[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, ql[qt][c], R[qt], 0, 0, 0);
+                    }
+                }
 #pragma unroll
-                    for (int i = 0; i < 4; i++) S[kt][qt][i] = c == 0 ? ksv[i] * R[i] : fmaf(ksv[i], R[i], S[kt][qt][i]);
+                for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) S[kt][qt][i] = R[qt][i];
+            } else {
+#pragma unroll
+                for (int c = 0; c < NC; c++) {
+                    const v8h A = __builtin_bit_cast(v8h, L.k16[key][(4 * c + kq) ^ (key & 15)]);
+                    const float4 ks4 = *(const float4 *)&L.ksf[c][16 * kt + 4 * kq];
+                    const float ksv[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
+#pragma unroll
+                    for (int qt = 0; qt < 2; qt++) {
+                        v4f R = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, qh[qt][c], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        R = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, ql[qt][c], R, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            S[kt][qt][i] = c == 0 ? ksv[i] * R[i] : fmaf(ksv[i], R[i], S[kt][qt][i]);
+                    }
                 }
             }
         }
@@ -265,11 +345,13 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(PfArgs a) {
             for (int kt = 0; kt < 4; kt++) {
                 const int quad = 4 * kt + kq;
                 const v4h vh = __builtin_bit_cast(v4h, L.vh[d][quad ^ (d & 15)]);
-                const v4h vl = __builtin_bit_cast(v4h, L.vl[d][quad ^ (d & 15)]);
 #pragma unroll
                 for (int qt = 0; qt < 2; qt++) {
                     O[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, ph[kt][qt], O[qt][dt], 0, 0, 0);
-                    O[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vl, ph[kt][qt], O[qt][dt], 0, 0, 0);
+                    if constexpr (!F16) {
+                        const v4h vl = __builtin_bit_cast(v4h, L.vl[d][quad ^ (d & 15)]);
+                        O[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vl, ph[kt][qt], O[qt][dt], 0, 0, 0);
+                    }
                     O[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, pl[kt][qt], O[qt][dt], 0, 0, 0);
                 }
             }
@@ -354,8 +436,8 @@ size_t attn_prefill_partial_bytes(int nq, int H, int HD, int64_t max_keys) {
     return ns > 1 ? (size_t)nq * H * ns * (HD + 4) * sizeof(float) : 0;
 }
 
-hipError_t launch_attn_prefill(const float *q, int64_t q_stride, KvLayer kv, int n_ctx, int H, int HKV, int HD, int p0,
-                               int nq, float scale, float *part, float *out, hipStream_t s) {
+hipError_t launch_attn_prefill(const float *q, int64_t q_stride, KvLayer kv, int kv_f16, int n_ctx, int H, int HKV,
+                               int HD, int p0, int nq, float scale, float *part, float *out, hipStream_t s) {
     if (!attn_prefill_supported(H, HKV, HD) || nq < 1 || p0 < 0 || p0 + nq > n_ctx) return hipErrorInvalidValue;
     PfArgs a{};
     a.q = q, a.q_stride = q_stride, a.kv = kv, a.n_ctx = n_ctx, a.H = H, a.HKV = HKV, a.p0 = p0, a.nq = nq;
@@ -366,12 +448,17 @@ hipError_t launch_attn_prefill(const float *q, int64_t q_stride, KvLayer kv, int
     a.n_split = (int)((max_keys + a.split_keys - 1) / a.split_keys);
     const int G = H / HKV, QB = PF_ROWS / G;
     const dim3 grid((unsigned)((nq + QB - 1) / QB), (unsigned)HKV, (unsigned)a.n_split);
-    switch (G) {
-    case 1: hipLaunchKernelGGL((k_attn_pf<128, 1>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((k_attn_pf<128, 2>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((k_attn_pf<128, 4>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((k_attn_pf<128, 8>), grid, dim3(256), 0, s, a); break;
-    }
+    auto go = [&](auto fc) {
+        constexpr bool F = decltype(fc)::value;
+        switch (G) {
+        case 1: hipLaunchKernelGGL((k_attn_pf<128, 1, F>), grid, dim3(256), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((k_attn_pf<128, 2, F>), grid, dim3(256), 0, s, a); break;
+        case 4: hipLaunchKernelGGL((k_attn_pf<128, 4, F>), grid, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL((k_attn_pf<128, 8, F>), grid, dim3(256), 0, s, a); break;
+        }
+    };
+    if (kv_f16) go(std::true_type{});
+    else go(std::false_type{});
     if (a.n_split > 1) hipLaunchKernelGGL(k_attn_pf_merge<128>, dim3((unsigned)(nq * H)), dim3(128), 0, s, a);
     return hipGetLastError();
 }

@@ -416,19 +416,31 @@ int ts5hip_attn_decode_noalloc(ts5hip_ctx *ctx, const float *q, int B, int n_hea
                             scale, n_split, out, (float *)(base + NOALLOC_COUNTER_BYTES), (int *)base);
 }
 
-int ts5hip_attn_prompt(ts5hip_ctx *ctx, const float *q, int nq, int n_head, int n_head_kv, int head_dim,
-                       const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx, int pos0,
-                       float scale, float *out) {
-    if (!ctx || !q || !k8 || !ks || !v8 || !vs || !out) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
+static int attn_prompt_into(ts5hip_ctx *ctx, const float *q, int nq, int n_head, int n_head_kv, int head_dim,
+                            const void *k, const void *ks, const void *v, const void *vs, int kv_f16, int n_ctx,
+                            int pos0, float scale, float *out) {
+    if (!ctx || !q || !k || !v || !out || (!kv_f16 && (!ks || !vs))) return fail(ctx, TS5HIP_ERR_ARG, "null argument");
     if (!attn_prefill_supported(n_head, n_head_kv, head_dim))
         return fail(ctx, TS5HIP_ERR_UNSUPPORTED, "prompt attention for %d/%d heads of %d", n_head, n_head_kv, head_dim);
     if (nq <= 0 || pos0 < 0 || n_ctx <= 0 || (int64_t)pos0 + nq > n_ctx)
         return fail(ctx, TS5HIP_ERR_ARG, "%d queries at %d in a cache of %d", nq, pos0, n_ctx);
     if (int rc = ensure_scratch(ctx, attn_prefill_partial_bytes(nq, n_head, head_dim, (int64_t)pos0 + nq))) return rc;
-    const KvLayer kv{(int8_t *)k8, (uint16_t *)ks, (int8_t *)v8, (uint16_t *)vs};
-    TS5_HIP(ctx, launch_attn_prefill(q, (int64_t)n_head * head_dim, kv, n_ctx, n_head, n_head_kv, head_dim, pos0, nq,
-                                     scale, (float *)ctx->scratch, out, ctx->stream));
+    const KvLayer kv{(int8_t *)k, (uint16_t *)ks, (int8_t *)v, (uint16_t *)vs};
+    TS5_HIP(ctx, launch_attn_prefill(q, (int64_t)n_head * head_dim, kv, kv_f16, n_ctx, n_head, n_head_kv, head_dim,
+                                     pos0, nq, scale, (float *)ctx->scratch, out, ctx->stream));
     return TS5HIP_OK;
+}
+
+int ts5hip_attn_prompt(ts5hip_ctx *ctx, const float *q, int nq, int n_head, int n_head_kv, int head_dim,
+                       const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx, int pos0,
+                       float scale, float *out) {
+    return attn_prompt_into(ctx, q, nq, n_head, n_head_kv, head_dim, k8, ks, v8, vs, 0, n_ctx, pos0, scale, out);
+}
+
+int ts5hip_attn_prompt_f16(ts5hip_ctx *ctx, const float *q, int nq, int n_head, int n_head_kv, int head_dim,
+                           const void *k16, const void *v16, int n_ctx, int pos0, float scale, float *out) {
+    return attn_prompt_into(ctx, q, nq, n_head, n_head_kv, head_dim, k16, nullptr, v16, nullptr, 1, n_ctx, pos0, scale,
+                            out);
 }
 
 int ts5hip_argmax(ts5hip_ctx *ctx, const float *x, int n, int rows, int32_t *out_dev) {

@@ -158,12 +158,12 @@ constexpr size_t NOALLOC_COUNTER_BYTES = (size_t)4096 * CTR_STRIDE * 4;
 constexpr int NOALLOC_DEVICES = 64;
 hipError_t attn_noalloc_setup(int device, void **ptr, hipStream_t s);
 // attn_prefill.hip: causal attention of nq consecutive queries (positions p0..,
-// rows q [nq][q_stride]) over one q8 cache on the matrix cores; out [nq][H * HD];
-// part: attn_prefill_partial_bytes(nq, H, HD, p0 + nq) bytes.
+// rows q [nq][q_stride]) over one q8 or (kv_f16) f16 cache on the matrix cores;
+// out [nq][H * HD]; part: attn_prefill_partial_bytes(nq, H, HD, p0 + nq) bytes.
 bool attn_prefill_supported(int H, int HKV, int HD);
 size_t attn_prefill_partial_bytes(int nq, int H, int HD, int64_t max_keys);
-hipError_t launch_attn_prefill(const float *q, int64_t q_stride, KvLayer kv, int n_ctx, int H, int HKV, int HD, int p0,
-                               int nq, float scale, float *part, float *out, hipStream_t s);
+hipError_t launch_attn_prefill(const float *q, int64_t q_stride, KvLayer kv, int kv_f16, int n_ctx, int H, int HKV,
+                               int HD, int p0, int nq, float scale, float *part, float *out, hipStream_t s);
 hipError_t launch_kv_read(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, int kv_f16, float *out,
                           hipStream_t s);
 hipError_t launch_kv_write(KvLayer kv, int which, int HKV, int HD, int n_ctx, int pos0, int n, int kv_f16,

@@ -829,9 +829,9 @@ int enqueue_batch(ts5hip_model *m, int nc, int p0, int rows, float *logits, bool
         }
         // Prompt chunks on the matrix cores; a sliding layer's chunk (each
         // query its own window) on the per-query kernel.
-        if (nc > 16 && !win && !m->kv_f16() && attn_prefill_supported(H, HKV, HD)) {
-            TS5_HIP(ctx, launch_attn_prefill(m->bq, AH, m->kv_layer(l), m->n_ctx, H, HKV, HD, p0, nc, hp.attn_scale,
-                                             m->bpart, m->batt, s));
+        if (nc > 16 && !win && attn_prefill_supported(H, HKV, HD)) {
+            TS5_HIP(ctx, launch_attn_prefill(m->bq, AH, m->kv_layer(l), m->kv_f16(), m->n_ctx, H, HKV, HD, p0, nc,
+                                             hp.attn_scale, m->bpart, m->batt, s));
             TS5_STAMP("attention_prompt", "");
         } else {
             AttnIO io{};

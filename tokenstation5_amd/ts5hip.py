@@ -81,6 +81,7 @@ _SIGS = {
     "ts5hip_attn_decode_noalloc": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32,
                                           _f32, _i32, _vp]),
     "ts5hip_attn_prompt": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
+    "ts5hip_attn_prompt_f16": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _i32, _i32, _f32, _vp]),
     "ts5hip_argmax": (_i32, [_vp, _vp, _i32, _i32, _vp]),
     "ts5hip_topk": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp]),
     "ts5hip_sampler_new": (_vp, [_u64]),
@@ -342,6 +343,10 @@ class Context:
         self.check(lib().ts5hip_attn_prompt(self.h, _ptr(q), nq, H, HKV, HD, _ptr(k8), _ptr(ks), _ptr(v8), _ptr(vs),
                                             n_ctx, pos0, scale, _ptr(out)))
 
+
+    def attn_prompt_f16(self, q, nq, H, HKV, HD, k16, v16, n_ctx, pos0, scale, out):
+        self.check(lib().ts5hip_attn_prompt_f16(self.h, _ptr(q), nq, H, HKV, HD, _ptr(k16), _ptr(v16), n_ctx, pos0,
+                                                scale, _ptr(out)))
     def argmax(self, x, n, rows, out):
         self.check(lib().ts5hip_argmax(self.h, _ptr(x), n, rows, _ptr(out)))
 

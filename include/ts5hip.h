@@ -160,8 +160,8 @@ int ts5hip_attn_decode_noalloc(ts5hip_ctx *ctx, const float *q, int B, int n_hea
 /* Causal prompt attention on the matrix cores (attn_pf, engine/shaders/attn_pf.glsl with its
  * policy at engine/src/vk_backend.cpp:954-961; CPU engine/src/cpu_backend.cpp:222-248): nq
  * queries at positions pos0 .. pos0 + nq - 1 over one q8 cache (the layout above), query t
- * reading keys 0 .. pos0 + t. q: [nq][H HD]; out: [nq][H HD] fp32. head_dim 128 and
- * n_head / n_head_kv in {1, 2, 4, 8}; otherwise TS5HIP_ERR_UNSUPPORTED. */
+ * reading keys 0 .. pos0 + t. q: [nq][H HD]; out: [nq][H HD] fp32. head_dim 64 or 128 and
+ * n_head / n_head_kv at most 64; otherwise TS5HIP_ERR_UNSUPPORTED. */
 int ts5hip_attn_prompt(ts5hip_ctx *ctx, const float *q, int nq, int n_head, int n_head_kv, int head_dim,
                        const void *k8, const void *ks, const void *v8, const void *vs, int n_ctx, int pos0,
                        float scale, float *out);

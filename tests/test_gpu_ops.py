@@ -577,16 +577,22 @@ def test_attention_causal_batch(ctx):
         assert rel_l2(got[b], want) <= REL_L2
 
 
-@pytest.mark.parametrize("nq,p0,n_ctx,H,HKV", [(64, 0, 64, 32, 8), (256, 3840, 4096, 32, 8), (100, 1000, 2048, 8, 2),
-                                             (37, 5, 64, 4, 1), (130, 300, 512, 16, 16), (50, 200, 300, 16, 8),
-                                             (40, 700, 1000, 64, 8), (17, 4079, 4096, 32, 8),
-                                             (5, 4091, 4096, 32, 8), (16, 1000, 2048, 8, 2), (1, 100, 200, 32, 8)])
-def test_attention_prompt_vs_oracle(ctx, nq, p0, n_ctx, H, HKV):
+@pytest.mark.parametrize("nq,p0,n_ctx,H,HKV,HD", [(64, 0, 64, 32, 8, 128), (256, 3840, 4096, 32, 8, 128),
+                                                (100, 1000, 2048, 8, 2, 128), (37, 5, 64, 4, 1, 128),
+                                                (130, 300, 512, 16, 16, 128), (50, 200, 300, 16, 8, 128),
+                                                (40, 700, 1000, 64, 8, 128), (17, 4079, 4096, 32, 8, 128),
+                                                (5, 4091, 4096, 32, 8, 128), (16, 1000, 2048, 8, 2, 128),
+                                                (1, 100, 200, 32, 8, 128),
+                                                (256, 1792, 2048, 14, 2, 64), (60, 0, 60, 14, 2, 64),
+                                                (100, 400, 600, 12, 4, 64), (33, 90, 200, 48, 3, 64),
+                                                (256, 768, 1024, 40, 8, 128), (70, 10, 100, 28, 4, 128)])
+def test_attention_prompt_vs_oracle(ctx, nq, p0, n_ctx, H, HKV, HD):
     """Prompt chunks on the matrix cores: query t at p0 + t over keys 0..p0+t (one split
-    up to 256 keys, then up to 16 merged splits; ragged query blocks; GQA groups 1-8).
-    A few queries (5, 16, 1) take the same kernel. The path keeps ~22-bit
+    up to 256 keys, then up to 16 merged splits; ragged query blocks; GQA groups 1-8 at
+    head dimension 128, and groups that leave rows of the 128 idle: 7 and 3 and 16 at
+    head dimension 64 (the 0.5B draft's 14/2 heads), 5 and 7 at 128 (14B-class 40/8,
+    28/4)). A few queries (5, 16, 1) take the same kernel. The path keeps ~22-bit
     operands, so it is held to 2e-5, not the shared 1e-3."""
-    HD = 128
     rng = np.random.default_rng(nq + p0 + H)
     q8, sc, deq = q8_cache(rng, 1, HKV, n_ctx, HD)
     v8, vsc, vdeq = q8_cache(rng, 1, HKV, n_ctx, HD)
@@ -603,14 +609,16 @@ def test_attention_prompt_vs_oracle(ctx, nq, p0, n_ctx, H, HKV):
         assert rel_l2(got[t], want) <= 2e-5, (t, rel_l2(got[t], want))
 
 
-@pytest.mark.parametrize("nq,p0,n_ctx,H,HKV", [(64, 0, 64, 32, 8), (256, 3840, 4096, 32, 8), (100, 1000, 2048, 8, 2),
-                                             (37, 5, 64, 4, 1), (130, 300, 512, 16, 16), (17, 4079, 4096, 32, 8),
-                                             (1, 100, 200, 32, 8)])
-def test_attention_prompt_f16_vs_oracle(ctx, nq, p0, n_ctx, H, HKV):
+@pytest.mark.parametrize("nq,p0,n_ctx,H,HKV,HD", [(64, 0, 64, 32, 8, 128), (256, 3840, 4096, 32, 8, 128),
+                                                (100, 1000, 2048, 8, 2, 128), (37, 5, 64, 4, 1, 128),
+                                                (130, 300, 512, 16, 16, 128), (17, 4079, 4096, 32, 8, 128),
+                                                (1, 100, 200, 32, 8, 128), (256, 1792, 2048, 14, 2, 64),
+                                                (100, 400, 600, 12, 4, 64), (256, 768, 1024, 40, 8, 128)])
+def test_attention_prompt_f16_vs_oracle(ctx, nq, p0, n_ctx, H, HKV, HD):
     """Prompt chunks over an f16 cache (each value the nearest half of N(0,1))
     on the matrix cores, K and V as stored: one split and merged splits,
-    ragged query blocks, GQA groups 1-8, held to 2e-5 like the q8 path."""
-    HD = 128
+    ragged query blocks, GQA groups 1-8 at head dimension 128 and 7, 3, 5 with
+    idle rows, held to 2e-5 like the q8 path."""
     rng = np.random.default_rng(nq + p0 + H + 7)
     k = rng.standard_normal((HKV, n_ctx, HD), dtype=np.float32).astype(np.float16)
     v = rng.standard_normal((HKV, n_ctx, HD), dtype=np.float32).astype(np.float16)
@@ -645,8 +653,8 @@ def test_attention_prompt_large_values_and_bad_shapes(ctx):
     for t in range(nq):
         want = oracle.attention(q[t], kc, vc, H, HKV, HD, p0 + t, 0.088)
         assert rel_l2(got[t], want) <= 2e-5, t
-    with pytest.raises(ts5hip.Ts5HipError):
-        ctx.attn_prompt(ctx.to_device(q), nq, 14, 2, 64, ctx.to_device(q8), ctx.to_device(sc), ctx.to_device(v8),
+    with pytest.raises(ts5hip.Ts5HipError):  # head dimension 256 (Gemma 3) takes the per-query kernel
+        ctx.attn_prompt(ctx.to_device(q), nq, 4, 2, 256, ctx.to_device(q8), ctx.to_device(sc), ctx.to_device(v8),
                         ctx.to_device(vsc), n_ctx, p0, 0.088, out)
     with pytest.raises(ts5hip.Ts5HipError):
         ctx.attn_prompt(ctx.to_device(q), nq, H, HKV, HD, ctx.to_device(q8), ctx.to_device(sc), ctx.to_device(v8),

@@ -4,8 +4,8 @@
 // attn_pf.glsl with its policy in engine/src/vk_backend.cpp:954-961; the CPU
 // restatement engine/src/cpu_backend.cpp:224-248).
 //
-// Workgroup: one KV head, QB = 128 / G queries (128 query rows: query t,
-// group head j at row G t + j), one split of the keys (split_keys, a
+// Workgroup: one KV head, QB = floor(128 / G) queries (G QB of its 128 query
+// rows: query t, group head j at row G t + j), one split of the keys (split_keys, a
 // multiple of 64). Four waves, 32 query rows (two 16-row tiles) each. Keys go
 // in blocks of 64:
 //  * DMA brings the block's raw q8 keys and values (and their f16 scales) into
@@ -53,6 +53,9 @@ struct PfArgs {
 
 constexpr int PF_KB = 64;     // keys per block
 constexpr int PF_ROWS = 128;  // query rows per workgroup
+// The k16 tiles' swizzle: unit u of key k sits at u ^ (k & pf_ksw(HD)), a
+// permutation of the key's HD / 8 units.
+__host__ __device__ constexpr int pf_ksw(int hd) { return hd / 8 - 1 < 15 ? hd / 8 - 1 : 15; }
 constexpr float PF_LOG2E = 1.4426950408889634f;
 
 template <int HD, bool F16>
@@ -64,7 +67,7 @@ struct PfLds<HD, false> {
     int8_t v8[PF_KB][HD];
     uint16_t ks[PF_KB][HD / 32];
     uint16_t vs[PF_KB][HD / 32];
-    uint4 k16[PF_KB][HD / 8];      // k8 as fp16, unit u of key k at u ^ (k & 15)
+    uint4 k16[PF_KB][HD / 8];      // k8 as fp16, unit u of key k at u ^ (k & pf_ksw(HD))
     float ksf[HD / 32][PF_KB];     // K scales, [group][key]
     uint2 vh[HD][PF_KB / 4];       // V^T hi, key quad q of row d at q ^ (d & 15)
     uint2 vl[HD][PF_KB / 4];       // V^T lo
@@ -72,7 +75,7 @@ struct PfLds<HD, false> {
 
 template <int HD>
 struct PfLds<HD, true> {
-    uint4 k16[2][PF_KB][HD / 8];  // K as stored (DMA), unit u of key k at u ^ (k & 15); two blocks in turn
+    uint4 k16[2][PF_KB][HD / 8];  // K as stored (DMA), unit u of key k at u ^ (k & pf_ksw(HD)); two blocks in turn
     uint16_t v16[PF_KB][HD];      // raw V block (DMA)
     uint2 vh[HD][PF_KB / 4];      // V^T, key quad q of row d at q ^ (d & 15)
 };
@@ -89,17 +92,20 @@ __device__ inline void pf_issue(const PfArgs &a, PfLds<HD, false> &L, int64_t sl
         dma16(a.kv.k + slot * HD + 16 * piece, lds_addr(&L.k8[0][0]) + 1024 * j);
         dma16(a.kv.v + slot * HD + 16 * piece, lds_addr(&L.v8[0][0]) + 1024 * j);
     }
-    {  // scales: 64 keys x HD / 32 f16 = 128 dwords a plane; wave w: plane w / 2, dwords 64 (w % 2) + lane
-        static_assert(PF_KB * (HD / 32) / 2 == 128, "two dword DMAs per scale plane");
-        const int w = 64 * (wave & 1) + lane, key = w / (HD / 64);
-        const uint16_t *base = (wave >> 1) ? a.kv.vs : a.kv.ks;
-        const uint16_t *src = base + (slot0 + min(kb + key, a.n_ctx - 1)) * (HD / 32) + 2 * (w % (HD / 64));
-        dma4(src, lds_addr((wave >> 1) ? &L.vs[0][0] : &L.ks[0][0]) + 256 * (wave & 1));
+    {  // scales: 64 keys x HD / 32 f16 = DW dwords a plane, WPP waves a plane (dwords 64 (w % WPP) + lane)
+        constexpr int DW = PF_KB * (HD / 32) / 2, WPP = DW / 64;
+        static_assert(DW % 64 == 0 && 2 * WPP <= 4, "whole dword DMAs, both planes in four waves");
+        if (WPP == 2 || wave < 2 * WPP) {  // (four waves: every wave)
+            const int plane = wave / WPP, w = 64 * (wave % WPP) + lane, key = w / (HD / 64);
+            const uint16_t *base = plane ? a.kv.vs : a.kv.ks;
+            const uint16_t *src = base + (slot0 + min(kb + key, a.n_ctx - 1)) * (HD / 32) + 2 * (w % (HD / 64));
+            dma4(src, lds_addr(plane ? &L.vs[0][0] : &L.ks[0][0]) + 256 * (wave % WPP));
+        }
     }
 }
 
 // An f16 block at key kb: K into k16[buf] (LDS piece p = 64 j + lane is
-// unit p % (HD / 8) ^ (key & 15) of key p / (HD / 8)), V raw into v16.
+// unit p % (HD / 8) ^ (key & pf_ksw(HD)) of key p / (HD / 8)), V raw into v16.
 template <int HD>
 __device__ inline void pf_issue(const PfArgs &a, PfLds<HD, true> &L, int64_t slot0, int kb, int wave, int lane,
                                 int buf) {
@@ -110,7 +116,7 @@ __device__ inline void pf_issue(const PfArgs &a, PfLds<HD, true> &L, int64_t slo
     for (int i = 0; i < PER_WAVE; i++) {
         const int j = wave * PER_WAVE + i, p = 64 * j + lane, key = p / UNITS, pos = p % UNITS;
         const int64_t slot = slot0 + min(kb + key, a.n_ctx - 1);
-        dma16(kbase + slot * HD * 2 + 16 * (pos ^ (key & 15)), lds_addr(&L.k16[buf][0][0]) + 1024 * j);
+        dma16(kbase + slot * HD * 2 + 16 * (pos ^ (key & pf_ksw(HD))), lds_addr(&L.k16[buf][0][0]) + 1024 * j);
         dma16(vbase + slot * HD * 2 + 16 * pos, lds_addr(&L.v16[0][0]) + 1024 * j);
     }
 }
@@ -164,7 +170,8 @@ __device__ inline void pf_convert(PfLds<HD, false> &L, int kb, int kend) {
             }
 #pragma unroll
             for (int k = 0; k < 4; k++)
-                L.k16[key][(4 * part + k) ^ (key & 15)] = make_uint4(h[4 * k], h[4 * k + 1], h[4 * k + 2], h[4 * k + 3]);
+                L.k16[key][(4 * part + k) ^ (key & pf_ksw(HD))] =
+                    make_uint4(h[4 * k], h[4 * k + 1], h[4 * k + 2], h[4 * k + 3]);
         }
     }
     if (t < PF_KB * (HD / 32)) {
@@ -207,9 +214,13 @@ __device__ inline void pf_convert(PfLds<HD, false> &L, int kb, int kend) {
     }
 }
 
-template <int HD, int G, bool F16>
+// GT: the query group as a constant, or 0 to take it from the arguments;
+// rows past G QB (G not a power of two) are idle.
+template <int HD, int GT, bool F16>
 __global__ __launch_bounds__(256, 2) void k_attn_pf(PfArgs a) {
-    constexpr int NC = HD / 32, NDT = HD / 16, QB = PF_ROWS / G;
+    constexpr int NC = HD / 32, NDT = HD / 16, KSW = pf_ksw(HD);
+    const int G = GT ? GT : a.H / a.HKV, QB = PF_ROWS / G;
+    constexpr bool FULL = GT && PF_ROWS % GT == 0;  // every row a query's
     __shared__ PfLds<HD, F16> L;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, kq = lane >> 4, rl = lane & 15;
@@ -221,14 +232,15 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(PfArgs a) {
     const int64_t slot0 = (int64_t)h * a.n_ctx;
 
     // The lane's query rows (its MFMA columns): row 32 wave + 16 qt + rl.
-    int tq[2], pos[2], hh[2];
+    int pos[2];  // the rows' positions (the causal limit); their query and head again at the end
     float p2e[2];
     v8h qh[2][NC], ql[2][NC];
 #pragma unroll
     for (int qt = 0; qt < 2; qt++) {
         const int r = 32 * wave + 16 * qt + rl;
-        tq[qt] = t0 + r / G, hh[qt] = h * G + r % G, pos[qt] = a.p0 + tq[qt];
-        const float *qr = a.q + (int64_t)min(tq[qt], a.nq - 1) * a.q_stride + (int64_t)hh[qt] * HD + 8 * kq;
+        const int tq = t0 + r / G, hh = h * G + r % G;
+        pos[qt] = a.p0 + tq;
+        const float *qr = a.q + (int64_t)min(tq, a.nq - 1) * a.q_stride + (int64_t)hh * HD + 8 * kq;
         float v[NC][8], amax = 0.f;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
@@ -277,7 +289,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(PfArgs a) {
                 v4f R[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
                 for (int c = 0; c < NC; c++) {
-                    const v8h A = __builtin_bit_cast(v8h, L.k16[nb & 1][key][(4 * c + kq) ^ (key & 15)]);
+                    const v8h A = __builtin_bit_cast(v8h, L.k16[nb & 1][key][(4 * c + kq) ^ (key & KSW)]);
 #pragma unroll
                     for (int qt = 0; qt < 2; qt++) {
                         R[qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, qh[qt][c], R[qt], 0, 0, 0);
@@ -291,7 +303,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(PfArgs a) {
             } else {
 #pragma unroll
                 for (int c = 0; c < NC; c++) {
-                    const v8h A = __builtin_bit_cast(v8h, L.k16[key][(4 * c + kq) ^ (key & 15)]);
+                    const v8h A = __builtin_bit_cast(v8h, L.k16[key][(4 * c + kq) ^ (key & KSW)]);
                     const float4 ks4 = *(const float4 *)&L.ksf[c][16 * kt + 4 * kq];
                     const float ksv[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
 #pragma unroll
@@ -361,16 +373,17 @@ __global__ __launch_bounds__(256, 2) void k_attn_pf(PfArgs a) {
     // Rows of this lane's columns: O^T[d = 16 dt + 4 kq + i][row].
 #pragma unroll
     for (int qt = 0; qt < 2; qt++) {
-        if (tq[qt] >= a.nq) continue;
+        const int r = 32 * wave + 16 * qt + rl, tq = t0 + r / G, hh = h * G + r % G;
+        if (tq >= a.nq || (!FULL && r >= G * QB)) continue;
         if (a.n_split == 1) {
             const float inv = 1.0f / l[qt];
-            float *o = a.out + (int64_t)tq[qt] * a.H * HD + (int64_t)hh[qt] * HD;
+            float *o = a.out + (int64_t)tq * a.H * HD + (int64_t)hh * HD;
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++)
                 *(float4 *)(o + 16 * dt + 4 * kq) =
                     make_float4(O[qt][dt][0] * inv, O[qt][dt][1] * inv, O[qt][dt][2] * inv, O[qt][dt][3] * inv);
         } else {
-            float *p = a.part + (((int64_t)tq[qt] * a.H + hh[qt]) * a.n_split + sp) * (HD + 4);
+            float *p = a.part + (((int64_t)tq * a.H + hh) * a.n_split + sp) * (HD + 4);
             if (kq == 0) p[0] = m[qt], p[1] = l[qt];
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++)
@@ -417,7 +430,7 @@ __global__ __launch_bounds__(HD) void k_attn_pf_merge(PfArgs a) {
 bool attn_prefill_supported(int H, int HKV, int HD) {
     if (HKV <= 0 || H % HKV) return false;
     const int G = H / HKV;
-    return HD == 128 && (G == 1 || G == 2 || G == 4 || G == 8);
+    return (HD == 64 || HD == 128) && G <= 64;
 }
 
 // Keys per split: a multiple of 64, at least 256, at most 16 splits, and
@@ -448,13 +461,20 @@ hipError_t launch_attn_prefill(const float *q, int64_t q_stride, KvLayer kv, int
     a.n_split = (int)((max_keys + a.split_keys - 1) / a.split_keys);
     const int G = H / HKV, QB = PF_ROWS / G;
     const dim3 grid((unsigned)((nq + QB - 1) / QB), (unsigned)HKV, (unsigned)a.n_split);
+    if (HD == 64) {
+        if (kv_f16) hipLaunchKernelGGL((k_attn_pf<64, 0, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((k_attn_pf<64, 0, false>), grid, dim3(256), 0, s, a);
+        if (a.n_split > 1) hipLaunchKernelGGL(k_attn_pf_merge<64>, dim3((unsigned)(nq * H)), dim3(64), 0, s, a);
+        return hipGetLastError();
+    }
     auto go = [&](auto fc) {
         constexpr bool F = decltype(fc)::value;
         switch (G) {
         case 1: hipLaunchKernelGGL((k_attn_pf<128, 1, F>), grid, dim3(256), 0, s, a); break;
         case 2: hipLaunchKernelGGL((k_attn_pf<128, 2, F>), grid, dim3(256), 0, s, a); break;
         case 4: hipLaunchKernelGGL((k_attn_pf<128, 4, F>), grid, dim3(256), 0, s, a); break;
-        default: hipLaunchKernelGGL((k_attn_pf<128, 8, F>), grid, dim3(256), 0, s, a); break;
+        case 8: hipLaunchKernelGGL((k_attn_pf<128, 8, F>), grid, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL((k_attn_pf<128, 0, F>), grid, dim3(256), 0, s, a); break;
         }
     };
     if (kv_f16) go(std::true_type{});

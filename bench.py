@@ -516,6 +516,8 @@ def main():
                     help="only the cfg2 decode and its JSON line (for rocprofv3 runs)")
     ap.add_argument("--draft-only", action="store_true",
                     help="only cfg5's draft model: a 2048-token prompt, then 32 greedy tokens (for rocprofv3 runs)")
+    ap.add_argument("--target-only", action="store_true",
+                    help="only cfg5's 48x5120 target: a 2048-token prompt, then greedy decode (for rocprofv3 runs)")
     ap.add_argument("--cfg3-only", action="store_true",
                     help="only cfg3's attention configurations and their JSON (for rocprofv3 runs)")
     ap.add_argument("--kernel-profile", action="store_true",
@@ -540,6 +542,13 @@ def main():
         return
     if args.kernel_profile:
         kernel_profile(hp, args.prompt)
+        return
+    if args.target_only:
+        ctx = ts5hip.Context(0)
+        steps = min(args.steps, 64)
+        ms, _, extra = decode_bench(ctx, dict(synth.TARGET_14B), steps, args.warmup, 2048)
+        print(json.dumps({"target_48x5120_tok_s": round(steps / ms * 1e3, 1), **extra}), flush=True)
+        ctx.close()
         return
     if args.cfg3_only:
         ctx = ts5hip.Context(0)

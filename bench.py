@@ -328,8 +328,22 @@ def cfg5_speculation(ctx, gen: int = 512, prompt_len: int = 2048):
         verify = timed(ctx, lambda i: fwd(m, 5), 10, 2, busy=False)
         dstep = timed(ctx, lambda i: fwd(draft, 1), 10, 2, busy=False)
         (ids0, st0, dt0), (ids4, st4, dt4) = runs[0], runs[4]
+        same = bool(np.array_equal(ids0, ids4))
+        div = None
+        if not same:
+            # Where drafting changed the greedy output, and how close the
+            # undrafted run's top two logits were there (the verify batches
+            # write the cache through the batch kernels, whose float sums
+            # run in another order than the single-step kernels').
+            d = next((i for i in range(min(len(ids0), len(ids4))) if ids0[i] != ids4[i]), min(len(ids0), len(ids4)))
+            if d < min(len(ids0), len(ids4)):
+                lg = m.forward(prompt, 0, logits=d == 0)  # its last row predicts ids0[0]
+                for i in range(d):  # ids0[i] at prompt_len + i predicts ids0[i + 1]
+                    lg = m.forward(np.array([ids0[i]], np.int32), prompt_len + i, logits=i == d - 1)
+                row = np.sort(np.asarray(lg[0], np.float64))
+                div = dict(at=int(d), top2_gap_rel=float((row[-1] - row[-2]) / abs(row[-1])))
         res[tag] = dict(tok_s_draft0=round(gen / dt0, 1), tok_s_draft4=round(gen / dt4, 1),
-                        same_output=bool(np.array_equal(ids0, ids4)), distinct_ids=int(np.unique(ids0).size),
+                        same_output=same, first_divergence=div, distinct_ids=int(np.unique(ids0).size),
                         drafted=int(st4[3]), accepted=int(st4[4]), **sources[4],
                         step_ms=round(step / 1e3, 3), verify5_ms=round(verify / 1e3, 3),
                         verify5_over_step=round(verify / step, 3), draft_ms_per_token=round(dstep / 1e3, 3))

@@ -1,13 +1,14 @@
-// Prompt attention over the q8 KV cache on the matrix cores: causal flash
-// attention for a batch of consecutive queries (positions p0 .. p0 + nq - 1)
-// against keys 0 .. p0 + t (the reference's attn_pf path, engine/shaders/
-// attn_pf.glsl with its policy in engine/src/vk_backend.cpp:954-961; the CPU
-// restatement engine/src/cpu_backend.cpp:224-248).
+// Prompt attention over the q8 (or f16) KV cache on the matrix cores: causal
+// flash attention for a batch of consecutive queries (positions p0 .. p0 +
+// nq - 1) against keys 0 .. p0 + t (the reference's attn_pf path,
+// engine/shaders/attn_pf.glsl, attn_pf_q8.comp and attn_pf128.comp, with its
+// policy in engine/src/vk_backend.cpp:954-975; the CPU restatement
+// engine/src/cpu_backend.cpp:224-248). Head dimension 64 or 128.
 //
 // Workgroup: one KV head, QB = floor(128 / G) queries (G QB of its 128 query
-// rows: query t, group head j at row G t + j), one split of the keys (split_keys, a
-// multiple of 64). Four waves, 32 query rows (two 16-row tiles) each. Keys go
-// in blocks of 64:
+// rows: query t, group head j at row G t + j), one split of the keys
+// (split_keys, a multiple of 64). Four waves, 32 query rows (two 16-row
+// tiles) each. Keys go in blocks of 64:
 //  * DMA brings the block's raw q8 keys and values (and their f16 scales) into
 //    LDS while the previous block is computed; all 256 threads then convert
 //    them: K to exact fp16 integers (k8), V to exact fp16 hi + lo planes of

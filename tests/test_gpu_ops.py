@@ -146,6 +146,9 @@ def run_matvec(ctx, t, W, ne0, rows, x, accumulate=None, norm=None, eps=1e-5):
     (synth.Q4_K, 4864, 896),      # the draft's ffn_down (19 blocks per row)
     (synth.Q4_K, 4352, 37),       # 17 blocks: split 9 + 8 across waves, ragged rows
     (synth.Q4_K, 256, 37),        # one block, ragged rows
+    (synth.Q4_K, 5120, 7168),     # 20 blocks a row (the 14B-class QKV): row-packed steps of 4 blocks
+    (synth.Q4_K, 3072, 1000),     # 12 blocks, row-packed, rows past the last group's
+    (synth.Q4_K, 5120, 37),       # row-packed, fewer rows than one group of 16
     (synth.Q6_K, 4096, 4096),
     (synth.Q6_K, 512, 1000),
     (synth.Q8_0, 896, 896),       # the draft's 896-wide matrices
@@ -193,7 +196,7 @@ def test_matvec_precision(ctx, t, ne0, rows, centered):
         assert rel_l2(got5[k], want[k]) <= 2e-6, (k, rel_l2(got5[k], want[k]))
 
 
-@pytest.mark.parametrize("ne0,rows", [(1024, 256), (14336, 200)])
+@pytest.mark.parametrize("ne0,rows", [(1024, 256), (14336, 200), (5120, 300)])
 def test_matvec_accumulate_and_scales(ctx, ne0, rows):
     """Input magnitudes from 1e-6 to 1e7 (the activation scale is per 32
     values), and accumulation into an existing fp32 vector (y += W x), for
@@ -310,7 +313,8 @@ def test_q6k_small_batch_matmul(ctx, M, ne0, rows, mode):
         assert rel_l2(got[k], want[k]) <= 2e-6, (k, rel_l2(got[k], want[k]))
 
 
-@pytest.mark.parametrize("t,ne0,rows", [(synth.Q4_K, 4096, 14336), (synth.Q8_0, 896, 4864), (synth.Q4_K, 512, 64)])
+@pytest.mark.parametrize("t,ne0,rows", [(synth.Q4_K, 4096, 14336), (synth.Q8_0, 896, 4864), (synth.Q4_K, 512, 64),
+                                        (synth.Q4_K, 5120, 13824), (synth.Q4_K, 3072, 1001)])
 def test_glu_vs_oracle(ctx, t, ne0, rows):
     Wg = synth.tensor(t, ne0, rows, 6, "gate")
     Wu = synth.tensor(t, ne0, rows, 6, "up")

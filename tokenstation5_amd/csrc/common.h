@@ -259,6 +259,14 @@ __device__ inline float wave_sum_dpp(float v) {
     v = dpp_add<0x143, 0xC, false>(v);  // row_bcast:31 into rows 2 and 3
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+// The sum over each 16-lane row of the wave, in every lane of the row (the
+// first four steps of wave_sum_dpp).
+__device__ inline float row_sum_dpp(float v) {
+    v = dpp_add<0xB1, 0xF, true>(v);
+    v = dpp_add<0x4E, 0xF, true>(v);
+    v = dpp_add<0x141, 0xF, true>(v);
+    return dpp_add<0x140, 0xF, true>(v);
+}
 // Max over the wave by the same DPP steps (disabled rows keep their own value).
 template <int CTRL, int ROW_MASK, bool BOUND>
 __device__ inline float dpp_max(float x) {

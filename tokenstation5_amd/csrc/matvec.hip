@@ -9,17 +9,6 @@
 
 namespace ts5hip {
 
-// The arguments only some modes need, passed after the others.
-struct MvTail {
-    uint32_t t;
-    int nb, nfirst, n1;
-    const float *y_in;
-    float *best_v;
-    int *best_i, *counter;
-    int32_t *out, *seq, *pos;
-    int gelu;
-};
-
 // The arguments every mode needs come first and one by one: 14 dwords the
 // command processor preloads into SGPRs at wave launch (the matvec file builds
 // with -amdgpu-kernarg-preload-count=16; two of the 16 user SGPRs hold the
@@ -109,10 +98,11 @@ void set_cu_count(int n) { g_n_cu = n > 0 ? n : 256; }
 // head's argmax.
 static size_t mv_max_grid() { return (size_t)MV_WG_PER_CU * g_n_cu; }
 
-template <class F, int R, int WAVES, int KS, int MODE>
+template <class F, int R, int WAVES, int KS, int MODE, int BR = 0>
 static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
     if (a.nrows > INT32_MAX) return hipErrorInvalidValue;  // the kernel takes a 32-bit row count
-    const int64_t rpg = (int64_t)R * (WAVES / KS);
+    constexpr int BPI = WAVE / F::LPB, LR = BR ? BPI / BR : 1;  // rows a row-packed slot spans
+    const int64_t rpg = (int64_t)R * LR * (WAVES / KS);
     const int64_t ngroups = (a.nrows + rpg - 1) / rpg;
     const int64_t cap = (int64_t)mv_max_grid();
     const int64_t per = (ngroups + cap - 1) / cap;  // groups per workgroup
@@ -141,15 +131,23 @@ static hipError_t mv_go(const MvArgs &a, hipStream_t s) {
         n1 = (int)std::min<int64_t>(std::max<int64_t>(want, nfirst), ngroups - ((int64_t)grid - nfirst));
     }
     const MvTail tail{a.t, a.nb, nfirst, n1, a.y_in, a.best_v, a.best_i, a.counter, a.out, a.seq, a.pos, a.gelu};
+    if constexpr (BR != 0) {  // row-packed steps (matvec_packed.hip)
+        static_assert(std::is_same_v<F, Q4K> && R == 1 && WAVES == 4 && KS == 1 && BR == 4, "the packed kernels built");
+        const int runs = nr <= nt ? 1 : nr <= 2 * nt ? 2 : nr <= 4 * nt && !norm ? 4 : 0;
+        return launch_mv_packed(MODE, runs, norm && runs > 0 && runs <= 2, g, b, lds, s, a.w, a.w2, a.x, a.norm_w,
+                                a.y, (int)a.nrows, a.n_in, (int)grid, a.eps, tail);
+    }
 #define TS5_MV_LAUNCH(RUNS, NORM)                                                                                 \
     hipLaunchKernelGGL((k_mv<F, R, WAVES, KS, MODE, RUNS, NORM>), g, b, lds, s, a.w, a.w2, a.x, a.norm_w, a.y,        \
                        (int)a.nrows, a.n_in, (int)grid, a.eps, tail)
-    if (nr <= nt && norm) TS5_MV_LAUNCH(1, true);
-    else if (nr <= nt) TS5_MV_LAUNCH(1, false);
-    else if (nr <= 2 * nt && norm) TS5_MV_LAUNCH(2, true);
-    else if (nr <= 2 * nt) TS5_MV_LAUNCH(2, false);
-    else if (nr <= 4 * nt && !norm) TS5_MV_LAUNCH(4, false);
-    else TS5_MV_LAUNCH(0, false);
+    if constexpr (BR == 0) {
+        if (nr <= nt && norm) TS5_MV_LAUNCH(1, true);
+        else if (nr <= nt) TS5_MV_LAUNCH(1, false);
+        else if (nr <= 2 * nt && norm) TS5_MV_LAUNCH(2, true);
+        else if (nr <= 2 * nt) TS5_MV_LAUNCH(2, false);
+        else if (nr <= 4 * nt && !norm) TS5_MV_LAUNCH(4, false);
+        else TS5_MV_LAUNCH(0, false);
+    }
 #undef TS5_MV_LAUNCH
     return hipGetLastError();
 }
@@ -181,6 +179,11 @@ static int mv_rows_per_wave(int64_t nrows) {
 
 template <int MODE>
 static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
+    // Q4_K rows of 4n blocks short of a whole 16-block step (3072 and 5120
+    // wide: 12 and 20 blocks) on row-packed steps of 4 blocks, every lane busy.
+    const bool packed = a.t == T_Q4_K && MODE != MV_ARGMAX && a.nb % 16 != 0 && a.nb % 4 == 0 && a.nb < 32;
+    if constexpr (MODE != MV_ARGMAX)
+        if (packed) return mv_go<Q4K, 1, 4, 1, MODE, 4>(a, s);
     if constexpr (MODE == MV_GLU) {
         switch (a.t) {
         case T_Q4_K: return mv_go<Q4K, MV_GLU_R, MV_GLU_WAVES, 1, MODE>(a, s);

@@ -496,6 +496,24 @@ struct MvArgs {
     int gelu;  // MV_GLU: GELU (tanh form) for SiLU
 };
 
+// The arguments only some modes need, passed after the others.
+struct MvTail {
+    uint32_t t;
+    int nb, nfirst, n1;
+    const float *y_in;
+    float *best_v;
+    int *best_i, *counter;
+    int32_t *out, *seq, *pos;
+    int gelu;
+};
+
+// The row-packed matvec kernels (mv_run's BR = 4: Q4_K, one row a slot, 4
+// waves), in matvec_packed.hip: mode MV_STORE / MV_ADD / MV_GLU, the
+// prologue's runs per thread (0: two-pass), norm fused.
+hipError_t launch_mv_packed(int mode, int runs, bool norm, dim3 g, dim3 b, size_t lds, hipStream_t s, const void *w,
+                            const void *w2, const float *x, const float *norm_w, float *y, int nrows, int n_in,
+                            int nwg, float eps, const MvTail &tail);
+
 template <class F, int R>
 __device__ inline void load_rows(const WPtr &w, int64_t row0, int64_t nrows, int nb, int b, int bmax, int sub,
                                  typename F::W (&wf)[R]) {
@@ -523,17 +541,25 @@ __device__ inline void best_pick_wave(float &v, int &i) {
 // runs after the first weight loads are issued and before the activation is
 // built. lds: act_bytes(a.n_in) bytes; red: NT/64 floats. MV_ARGMAX returns
 // this workgroup's best (value, row) in best_v / best_i (every thread).
-template <class F, int R, int WAVES, int KS, int MODE, int RUNS, bool NORM, class Hook>
+// BR (0: a step sweeps BPI blocks of each of the wave's R rows) = 4: a step
+// sweeps 4 blocks of 4 times as many rows, each 16-lane row of the wave on
+// its own matrix row, so rows whose block count is a multiple of 4 but not
+// of BPI (5120 wide: 20 Q4_K blocks) fill every step instead of leaving most
+// of their last one empty; one split, no pick.
+template <class F, int R, int WAVES, int KS, int MODE, int RUNS, bool NORM, int BR = 0, class Hook>
 __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, float *red, Hook before_act,
                               float &best_v, int &best_i) {
     static_assert(WAVES % KS == 0, "splits of whole row waves");
     constexpr int NT = WAVES * WAVE, BPI = WAVE / F::LPB, NW = MODE == MV_GLU ? 2 : 1, RW = WAVES / KS;
+    constexpr int BS = BR ? BR : BPI, LR = BPI / BS;  // blocks of a row a step; rows a slot's lanes span
+    static_assert(BR == 0 || (BR * F::LPB == 16 && KS == 1 && MODE != MV_ARGMAX && R <= 16),
+                  "row-packed steps: 16-lane rows, one split, no pick");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, bsub = lane / F::LPB, sub = lane % F::LPB;
     const int rw = wave % RW, ks = wave / RW;
-    const int64_t rpg = (int64_t)R * RW;
+    const int64_t rpg = (int64_t)R * LR * RW;
     const int64_t ngroups = (a.nrows + rpg - 1) / rpg;
     const int nbk = KS == 1 ? a.nb : (a.nb + KS - 1) / KS;
-    const int spg = (nbk + BPI - 1) / BPI;  // steps per row group
+    const int spg = (nbk + BS - 1) / BS;  // steps per row group
     const int kb0 = ks * nbk, kb1 = min(a.nb, kb0 + nbk);
     const int64_t nblocks = (int64_t)a.nb * a.nrows;
     const WPtr w1 = wptr(a.t, a.w, nblocks), w2 = wptr(a.t, MODE == MV_GLU ? a.w2 : a.w, nblocks);
@@ -561,9 +587,21 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
     typename F::W cur[NW][R], nxt[NW][R];
     // The weights of step `i` of group `gi` into `buf`.
     auto issue = [&](int64_t gi, int i, typename F::W (&buf)[NW][R]) {
-        const int64_t row0 = gi * rpg + (int64_t)rw * R;
-        load_rows<F, R>(w1, row0, a.nrows, a.nb, kb0 + i * BPI + bsub, kb1 - 1, sub, buf[0]);
-        if (MODE == MV_GLU) load_rows<F, R>(w2, row0, a.nrows, a.nb, kb0 + i * BPI + bsub, kb1 - 1, sub, buf[NW - 1]);
+        if constexpr (BR == 0) {
+            const int64_t row0 = gi * rpg + (int64_t)rw * R;
+            load_rows<F, R>(w1, row0, a.nrows, a.nb, kb0 + i * BPI + bsub, kb1 - 1, sub, buf[0]);
+            if (MODE == MV_GLU) load_rows<F, R>(w2, row0, a.nrows, a.nb, kb0 + i * BPI + bsub, kb1 - 1, sub, buf[NW - 1]);
+        } else {  // slot r: row row0 + r LR + lrow (clamped), block kb0 + i BS + lblk (clamped)
+            const int lrow = bsub / BS, lblk = bsub % BS;
+            const int64_t row0 = gi * rpg + (int64_t)rw * R * LR + lrow;
+            const int bb = min(kb0 + i * BS + lblk, kb1 - 1);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int64_t row = min(row0 + (int64_t)r * LR, a.nrows - 1);
+                buf[0][r] = F::load_w(w1, row, a.nb, bb, sub);
+                if (MODE == MV_GLU) buf[NW - 1][r] = F::load_w(w2, row, a.nb, bb, sub);
+            }
+        }
     };
     // Unconditional (rows are clamped; every workgroup has gbeg < gend), so no
     // branch makes the compiler's waits for the activation cover these.
@@ -593,7 +631,9 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
         // Branch-free: lanes past the split's end compute on its last block
         // (loaded clamped) and add nothing, so no path skips the arithmetic
         // whose waits the compiler must then assume still open.
-        const int b = kb0 + it * BPI + bsub;
+        int b;
+        if constexpr (BR == 0) b = kb0 + it * BPI + bsub;
+        else b = kb0 + it * BS + bsub % BS;
         const bool valid = b < kb1;
         const typename F::X xf = F::load_x(x, min(b, kb1 - 1), sub);
 #pragma unroll
@@ -604,10 +644,17 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
                 acc[k][r] += valid ? d : 0.f;
             }
         if (it != spg - 1) return;
+        if constexpr (BR == 0) {
 #pragma unroll
-        for (int k = 0; k < NW; k++)
+            for (int k = 0; k < NW; k++)
 #pragma unroll
-            for (int r = 0; r < R; r++) acc[k][r] = wave_sum_dpp(acc[k][r]);
+                for (int r = 0; r < R; r++) acc[k][r] = wave_sum_dpp(acc[k][r]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < NW; k++)
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[k][r] = row_sum_dpp(acc[k][r]);
+        }
         if constexpr (KS > 1) {
             if (lane == 0)
 #pragma unroll
@@ -626,6 +673,25 @@ __device__ inline void mv_run(const MvArgs &a, int wg, int nwg, uint8_t *lds, fl
                         acc[k][r] = v;
                     }
             par ^= 1;
+        }
+        if constexpr (BR != 0) {  // slot r: lane r of each 16-lane row, row row0 + r LR + that row's index
+            const int wl = lane & 15;
+            const int64_t row0 = g * rpg + (int64_t)rw * R * LR + bsub / BS;
+            if (wl < R && row0 + (int64_t)wl * LR < a.nrows) {
+                float v = acc[0][0], u = acc[NW - 1][0];
+#pragma unroll
+                for (int r = 1; r < R; r++)
+                    if (wl == r) v = acc[0][r], u = acc[NW - 1][r];
+                const int64_t row = row0 + (int64_t)wl * LR;
+                if (MODE == MV_ADD) st_dev(a.y + row, a.y_in[row] + v);
+                else if (MODE == MV_GLU) st_dev(a.y + row, glu_act(v, u, a.gelu));
+                else st_dev(a.y + row, v);
+            }
+#pragma unroll
+            for (int k = 0; k < NW; k++)
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[k][r] = 0.f;
+            return;
         }
         const int64_t row0 = g * rpg + (int64_t)rw * R;
         if (ks == 0 && lane < R && row0 + lane < a.nrows) {

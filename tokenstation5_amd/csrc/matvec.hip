@@ -198,9 +198,13 @@ static hipError_t mv_dispatch(const MvArgs &a, hipStream_t s) {
         case T_Q4_K:
             if (MODE != MV_ARGMAX && a.nb >= MV_KS_MINNB) {
                 // Too few rows for a group a CU at 4 rows a wave (the draft's
-                // 896-row down: 56 groups): one row a wave, 4 times the groups
-                // (a draft token 0.843 -> 0.796 ms with the Q8_0 rule below).
-                if ((a.nrows + MV_KS_R * 4 - 1) / (MV_KS_R * 4) < g_n_cu)
+                // 896-row down: 56 groups), or a count that leaves CUs with one
+                // group and others two (the 48x5120 target's 5120-row down: 320
+                // groups): one row a wave, 4 times the groups (a draft token
+                // 0.843 -> 0.796 ms with the Q8_0 rule below; the target's
+                // token 289 -> 310 tok/s).
+                const int64_t g4 = (a.nrows + MV_KS_R * 4 - 1) / (MV_KS_R * 4);
+                if (g4 < g_n_cu || (g4 < 2 * g_n_cu && g4 % g_n_cu != 0))
                     return mv_go<Q4K, 1, MV_KS_WAVES, MV_KS, MODE>(a, s);
                 return mv_go<Q4K, MV_KS_R, MV_KS_WAVES, MV_KS, MODE>(a, s);
             }

@@ -196,11 +196,12 @@ def test_matvec_precision(ctx, t, ne0, rows, centered):
         assert rel_l2(got5[k], want[k]) <= 2e-6, (k, rel_l2(got5[k], want[k]))
 
 
-@pytest.mark.parametrize("ne0,rows", [(1024, 256), (14336, 200), (5120, 300)])
+@pytest.mark.parametrize("ne0,rows", [(1024, 256), (14336, 200), (5120, 300), (5120, 5120)])
 def test_matvec_accumulate_and_scales(ctx, ne0, rows):
     """Input magnitudes from 1e-6 to 1e7 (the activation scale is per 32
     values), and accumulation into an existing fp32 vector (y += W x), for
-    rows of one step and rows whose blocks the workgroup's waves split."""
+    rows of one step (1024 wide: 4 blocks, row-packed), rows whose blocks
+    the workgroup's waves split, and 5120-wide rows on row-packed steps."""
     W = synth.tensor(synth.Q4_K, ne0, rows, 3, f"acc{ne0}")
     rng = np.random.default_rng(4)
     for scale in (1e-6, 1.0, 1e7):

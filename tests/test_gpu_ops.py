@@ -253,7 +253,7 @@ def test_head_argmax(ctx, t, ne0, rows):
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 6, 8, 9, 16])
 @pytest.mark.parametrize("ne0,rows,mode", [(4096, 1000, "store"), (14336, 528, "add"), (512, 37, "glu"),
                                            (4096, 9000, "add"), (4096, 4100, "glu"), (14336, 4200, "add"),
-                                           (4096, 6144, "store")])
+                                           (4096, 6144, "store"), (5120, 7168, "store"), (5120, 5120, "add")])
 def test_q4k_small_batch_matmul(ctx, M, ne0, rows, mode):
     """The Q4_K matmul of 1-16 tokens (k_gemm_m up to 8, k_gemm_small past
     it; up to 5 tokens over inputs up to 4096 wide, k_gemm_mx): every token's
@@ -261,9 +261,9 @@ def test_q4k_small_batch_matmul(ctx, M, ne0, rows, mode):
     accumulating into a residual, fused gate/up + SiLU), with row counts that
     leave partial 16-row tiles; 9000 and 4100 rows give k_gemm_mx 4 and 2
     row tiles a workgroup, some of them past the last row, and 6144 rows
-    (the 8B's QKV) 2 tiles of one matrix, each wave's 4 items all in flight;
-    14336-wide inputs take k_gemm_mw (4200 rows: 263 tiles over 256
-    workgroups)."""
+    (the 8B's QKV) 2 tiles of one matrix; inputs past 4096 wide (5120: the
+    14B-class QKV and wo; 14336) take k_gemm_mw over quantized records
+    (4200 rows: 263 tiles over 256 workgroups)."""
     rng = np.random.default_rng(M * 100 + rows)
     W = synth.tensor(synth.Q4_K, ne0, rows, 21, f"sb{ne0}", centered=True)
     x = rng.standard_normal((M, ne0)).astype(np.float32)
